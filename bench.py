@@ -1,0 +1,220 @@
+"""MoE-layer forward benchmark on one MI355X (the BASELINE.json metric).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--no-cpu]
+
+A step is one MoE-layer forward (router, dispatch, grouped SwiGLU GEMMs,
+combine, aux losses; train mode so the aux loss is computed) over one batch of
+synthetic input already resident in HBM.  Rank 0 prints one JSON line with
+whole-job tokens/s, the roofline of the dominant kernel (the gate/up grouped
+GEMM) measured with HIP events on its launch stream, per-stage figures and a
+CPU baseline (the op-for-op torch-CPU port of the reference path, timed on this
+host on a bounded token sample).
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "kolmogorov-moe-architecture_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "MoE-layer fwd tokens/sec (d2048,16e,top-2,bf16); % MFMA peak; dispatch GB/s"
+PEAK_BF16 = 2.5e15
+PEAK_FP8 = 5.0e15
+PEAK_HBM = 8.0e12
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU baseline")
+    return ap.parse_args()
+
+
+def stage_bytes_flops(wl, layer, fwd_state):
+    """Algorithmic work per launch of each stage (bytes or FLOPs)."""
+    d, F, E, k = wl.d, wl.F, wl.E, wl.k
+    s = 2  # bf16
+    T = wl.T
+    a_kept = fwd_state["a_kept"]
+    a_all = fwd_state["a_all"]
+    t_in = fwd_state["t_in"]
+    xs = 1 if wl.fp8 else s
+    return {
+        "gemm_gate_up": ("flop", 4.0 * d * F * a_kept),
+        "gemm_down": ("flop", 2.0 * d * F * a_kept),
+        # read each routed token row once, write its kept rows, 8 B/assignment of metadata
+        "dispatch": ("byte", t_in * d * s + a_kept * d * xs + 8.0 * a_all + (a_kept * 4 if wl.fp8 else 0)),
+        "gather": ("byte", a_kept * d * s + a_kept * d * xs + 4.0 * a_kept),
+        # read the kept expert rows, write y, 8 B/assignment of metadata
+        "combine": ("byte", a_kept * d * s + T * d * s + 8.0 * a_all),
+        "router": ("byte", t_in * d * s + t_in * E * 4 + t_in * k * 12),
+    }
+
+
+def run_gpu(args, wl):
+    import torch
+    from kmoe import ops, synth
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t = synth.make_tensors(wl, "cpu")
+    t = {kk: v.to(dev) for kk, v in t.items()}
+    layer = synth.build_layer(wl, dev, t).train()
+    x = t["x"]
+    torch.cuda.synchronize()
+
+    def step():
+        return layer(x)
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        # routing statistics of this input (outside the timed region)
+        moe = layer.ffn if wl.mod else layer
+        if wl.routing == "expert_choice":
+            C = moe.router.capacity(wl.S)
+            a_all = a_kept = wl.E * wl.B * min(C, wl.S)
+            t_in = wl.T
+        else:
+            counts = moe.last_expert_counts.cpu().long()
+            t_in = wl.B * layer.ffn_mod_router.keep_count(wl.S) if wl.mod else wl.T
+            a_all = t_in * wl.k
+            if moe.drop_overflow:
+                cap = ops.capacity_of(moe.capacity_factor, t_in, wl.k, wl.E)
+                a_kept = int(counts.clamp(max=cap).sum())
+            else:
+                a_kept = int(counts.sum())
+        # timed region: K back-to-back forwards, per-stage HIP events on the launch stream
+        events = []
+        ops.set_stage_timing(events)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        ops.set_stage_timing(None)
+    stages = {}
+    for name, a, b in events:
+        stages.setdefault(name, []).append(a.elapsed_time(b) * 1e3)  # us
+    work = stage_bytes_flops(wl, layer, dict(a_kept=a_kept, a_all=a_all, t_in=t_in))
+    stage_out = {}
+    for name, v in stages.items():
+        us = statistics.mean(v)
+        rec = {"us": round(us, 2), "launches_per_step": len(v) // args.steps}
+        if name in work:
+            kind, amount = work[name]
+            if kind == "flop":
+                rec["TFLOPs"] = round(amount / (us * 1e-6) / 1e12, 1)
+                rec["frac_peak"] = round(amount / (us * 1e-6) / (PEAK_FP8 if wl.fp8 else PEAK_BF16), 4)
+            else:
+                rec["GBps"] = round(amount / (us * 1e-6) / 1e9, 1)
+                rec["frac_hbm"] = round(amount / (us * 1e-6) / PEAK_HBM, 4)
+        stage_out[name] = rec
+    elapsed = t1 - t0
+    return dict(elapsed=elapsed, stages=stage_out, a_kept=a_kept, a_all=a_all, t_in=t_in,
+                gemm_us=stages.get("gemm_gate_up", [float("nan")]), work=work)
+
+
+def run_cpu_baseline(wl, tokens):
+    """The op-for-op torch-CPU port of the reference path on a bounded sample."""
+    import torch
+    from kmoe import synth
+    from oracle import torch_port as P
+
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    torch.set_num_threads(cores)
+    wl32 = synth.Workload(wl.name, B=1, S=tokens, d=wl.d, E=wl.E, k=wl.k, F=wl.F, dtype=torch.float32,
+                          seed=wl.seed)
+    t = synth.make_tensors(wl32, "cpu", tokens=tokens)
+    args = (t["x"], t["w_in"], t["w_out"], t["w1"], t["w2"], t["w3"])
+    times = []
+    with torch.no_grad():
+        for i in range(4):
+            t0 = time.perf_counter()
+            P.moe_layer_tc(*args, wl.k, training=True)
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times[1:])
+    return {"value": round(tokens / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{tokens} tokens of the config-2 layer (d={wl.d}, E={wl.E}, top-{wl.k}, F={wl.F}), fp32, "
+                      f"oracle/torch_port.py (reference op sequence: padded bmm experts), median of 3 after 1 warm-up",
+            "seconds_per_forward": round(med, 3)}
+
+
+def load_traffic(name):
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            return json.load(f)
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on exactly one GPU (no expert parallelism / collectives); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from kmoe import synth
+
+    wl = synth.WORKLOADS[args.config]
+    res = run_gpu(args, wl)
+    ms = res["elapsed"] / args.steps * 1e3
+    tokens_per_s = wl.T * args.steps / res["elapsed"]
+    gu = res["stages"].get("gemm_gate_up", {})
+    flops_gu = res["work"]["gemm_gate_up"][1]
+    peak = PEAK_FP8 if wl.fp8 else PEAK_BF16
+    us = gu.get("us", float("nan"))
+    achieved = flops_gu / (us * 1e-6) / 1e12
+    traffic = load_traffic(f"gemm_gate_up_cfg{args.config}")
+    out = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3" if wl.fp8 else "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02^2) weights)",
+        "config": {"workload": wl.name, "tokens": wl.T, "d_model": wl.d, "n_experts": wl.E, "top_k": wl.k,
+                   "d_ff_expert": wl.F, "routing": wl.routing, "assignments_kept": res["a_kept"]},
+        "roofline": {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(achieved, 1),
+                     "peak": peak / 1e12, "unit": "TFLOP/s", "frac": round(achieved * 1e12 / peak, 4),
+                     "traffic": traffic.get("bytes_per_launch") if traffic else None,
+                     "work_per_launch": f"4*d*F*A_kept = {flops_gu:.4g} FLOP"},
+        "stages": res["stages"],
+    }
+    gemm_us = res["stages"].get("gemm_gate_up", {}).get("us", 0) + res["stages"].get("gemm_down", {}).get("us", 0)
+    if gemm_us:
+        tot = res["work"]["gemm_gate_up"][1] + res["work"]["gemm_down"][1]
+        out["gemm_frac_peak"] = round(tot / (gemm_us * 1e-6) / peak, 4)
+    if "dispatch" in res["stages"]:
+        out["dispatch_GBps"] = res["stages"]["dispatch"].get("GBps")
+    if "combine" in res["stages"]:
+        out["combine_GBps"] = res["stages"]["combine"].get("GBps")
+    if not args.no_cpu:
+        out["cpu_baseline"] = run_cpu_baseline(synth.WORKLOADS[2], args.cpu_tokens)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

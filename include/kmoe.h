@@ -1,0 +1,184 @@
+/*
+ * kmoe.h — C ABI of the MI355X-native MoE feed-forward hot path.
+ *
+ * One MoE layer forward = router -> dispatch -> grouped SwiGLU GEMMs -> combine
+ * (+ aux-loss finalisation).  Every entry point:
+ *   - takes raw device pointers, sizes, dtype enums and a hipStream_t passed as
+ *     `void* stream` (NULL = the null stream); all work is stream-ordered;
+ *   - never allocates, never synchronises the host, never throws;
+ *   - returns 0 (KMOE_OK) or a negative KMOE_ERR_* code, with a message in
+ *     kmoe_last_error() (thread-local);
+ *   - borrows every buffer: outputs and workspaces are caller-owned.
+ *
+ * Reference interfaces replaced (file:line into JBedichek/Kolmogorov-MoE-Architecture):
+ *   Router.forward                   moe_arch/model/moe.py:423-462
+ *   GroupedExperts.forward           moe_arch/model/moe.py:213-294
+ *   MoELayer._compute_*_loss         moe_arch/model/moe.py:840-939
+ *   ExpertChoiceRouter.forward       moe_arch/model/moe.py:494-530
+ *   GroupedExpertsExpertChoice       moe_arch/model/moe.py:626-673, 132-158
+ *   MoDRouter.forward                moe_arch/model/mod.py:67-122 (+ layers.py:148-185)
+ *   moe_kernels.grouped_swiglu_forward
+ *                                    moe_arch/kernels/grouped_gemm.cu:186-257
+ *                                    (Python binding moe_arch/kernels/__init__.py:29-56)
+ */
+#ifndef KMOE_H
+#define KMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KMOE_ABI_VERSION 1
+
+/* status codes */
+#define KMOE_OK 0
+#define KMOE_ERR_NULL (-1)        /* a required pointer is NULL */
+#define KMOE_ERR_SHAPE (-2)       /* a size is out of the supported range */
+#define KMOE_ERR_DTYPE (-3)       /* unsupported dtype enum */
+#define KMOE_ERR_WORKSPACE (-4)   /* workspace too small */
+#define KMOE_ERR_LAUNCH (-5)      /* HIP reported an error at launch */
+#define KMOE_ERR_UNSUPPORTED (-6) /* valid request this build does not implement */
+
+/* dtype enums */
+#define KMOE_DTYPE_BF16 0
+#define KMOE_DTYPE_F32 1
+#define KMOE_DTYPE_FP8_E4M3 2 /* OCP e4m3fn, saturating at +-448 */
+
+/* limits */
+#define KMOE_MAX_EXPERTS 64
+#define KMOE_ROUTER_HIDDEN 128 /* the reference router MLP width, moe.py:346 */
+
+const char* kmoe_last_error(void);
+int kmoe_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* (a) Router — replaces Router.forward (moe.py:423-462) and the logits half of
+ * ExpertChoiceRouter.forward (moe.py:513-514).
+ *   logits[t,:] = SiLU(x[row(t)] . w_in^T) . w_out^T  (+ logit_bias), fp32 accumulate
+ *   row(t) = row_index ? row_index[t] : t
+ * When k > 0 it also selects the top-k experts of each token, ranked by fp32
+ * logit (descending; equal logits -> lowest expert index first), and writes the
+ * renormalised softmax weights  w_j = p_j / sum_sel p  (moe.py:441,455-460).
+ * `partials` (nullable) receives per-block sums for the aux losses; its length in
+ * floats is kmoe_router_partials_len(T, E).
+ *   x: (rows, d) bf16;  w_in: (128, d) bf16;  w_out: (E, 128) bf16
+ *   logits: (T, E) f32; topk_idx: (T, k) int64; topk_w: (T, k) f32          */
+int64_t kmoe_router_partials_len(int64_t T, int E);
+int kmoe_router(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,
+                const void* w_out, int E, const float* logit_bias, int k, float* logits,
+                int64_t* topk_idx, float* topk_w, float* partials, void* stream);
+
+/* Aux losses — replaces MoELayer._compute_auxiliary_losses (moe.py:840-939).
+ *   LB = E * sum_e (counts[e] / (T*k)) * mean_t softmax(logits)[t,e]
+ *   z  = mean_t logsumexp(logits[t,:])^2
+ *   out[0] = w_lb*LB + w_z*z, out[1] = LB, out[2] = z
+ * counts may be NULL (then LB = 0; expert-choice uses w_z*z only, moe.py:833-836).
+ * Reduces the router partials in a fixed order (deterministic).            */
+int kmoe_aux_loss(const float* partials, int64_t T, int E, const int32_t* counts, int k, float w_lb,
+                  float w_z, float* out, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* (b) Dispatch — replaces the sort/bincount/gather half of GroupedExperts.forward
+ * (moe.py:238-272).  Stable counting sort of the T*k assignments a = t*k + j by
+ * expert (ties in assignment order, = torch.argsort(stable=True)), optional
+ * capacity drop (keep the first `capacity` assignments of each expert in that
+ * order; capacity <= 0 keeps all), and the row gather
+ *   xperm[offsets[e] + r] = x[row(t)]  for the r-th kept assignment of expert e.
+ * Outputs: counts (E) routed counts before the drop; offsets (E+1) kept-row
+ * offsets; row_token (T*k) token of each permuted row; slot_row (T*k) permuted
+ * row of assignment a or -1 if dropped; slot_w (T*k) f32 routing weight.
+ * xperm_dtype BF16 copies rows; FP8_E4M3 quantises each row with the per-token
+ * scale amax(|x[row]|)/448 written to xperm_scale (one per permuted row).
+ *   topk_w dtype: w_dtype (BF16 or F32).  workspace: kmoe_dispatch_workspace_bytes. */
+size_t kmoe_dispatch_workspace_bytes(int64_t T, int k, int E);
+int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
+                  const void* topk_w, int w_dtype, int k, int E, int64_t capacity, int32_t* counts,
+                  int32_t* offsets, int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm,
+                  int xperm_dtype, float* xperm_scale, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* Row gather: out[r] = x[row_token[r]] for r < n_rows (rows with row_token < 0 are
+ * zero-filled).  out_dtype BF16 (copy) or FP8_E4M3 (per-row scale to out_scale).
+ * n_rows_dev (nullable): device int32 holding the number of valid rows.      */
+int kmoe_gather_rows(const void* x, const int32_t* row_token, int64_t n_rows, const int32_t* n_rows_dev,
+                     int d, void* out, int out_dtype, float* out_scale, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* (c) Grouped SwiGLU expert GEMMs — replaces moe_kernels.grouped_swiglu_forward
+ * (grouped_gemm.cu:186-257) and the bmm block of GroupedExperts.forward
+ * (moe.py:275-279).  Rows of expert e are [offsets[e], offsets[e+1]) of xperm;
+ * offsets live on the device (no host sync).  max_rows >= offsets[E] bounds the
+ * launch.  Weights are used in a packed, derived layout produced by
+ * kmoe_pack_weights from the reference parameters w1,w2: (E,d,F), w3: (E,F,d).
+ *   F_pad = round_up(F, 128); d % 64 == 0.
+ *   h:   (max_rows, F_pad) bf16   h = silu(x.w1[e]) * (x.w2[e])   (ffn.py:17-64)
+ *   y:   (max_rows, d)     bf16   y = h.w3[e]
+ * FP8_E4M3 inputs carry per-row scales (xperm_scale / h_scale) and per-expert
+ * per-output-row weight scales; accumulation is fp32, outputs bf16.          */
+int kmoe_padded_ff(int F);
+size_t kmoe_packed_w13_bytes(int E, int d, int F, int dtype);
+size_t kmoe_packed_w3_bytes(int E, int d, int F, int dtype);
+int kmoe_pack_weights(const void* w1, const void* w2, const void* w3, int w_dtype, int E, int d, int F,
+                      int packed_dtype, void* w13_packed, float* w13_scale, void* w3_packed,
+                      float* w3_scale, void* stream);
+int kmoe_gemm_gate_up(const void* xperm, const float* xperm_scale, int in_dtype, const int32_t* offsets,
+                      int E, int d, int F, int64_t max_rows, const void* w13_packed,
+                      const float* w13_scale, void* h, void* stream);
+int kmoe_gemm_down(const void* h, const float* h_scale, int in_dtype, const int32_t* offsets, int E,
+                   int d, int F, int64_t max_rows, const void* w3_packed, const float* w3_scale,
+                   void* y, void* stream);
+/* Per-row fp8 quantisation of a bf16 matrix (used between the fp8 GEMMs):
+ * scale[r] = amax(|in[r,:]|)/448, out = e4m3(sat(in/scale)), RNE.          */
+int kmoe_quant_rows_fp8(const void* in, int64_t rows, const int32_t* n_rows_dev, int cols, uint8_t* out,
+                        float* scale, void* stream);
+/* Convenience: gate_up + down on bf16 (the reference's native entry point). */
+int kmoe_grouped_swiglu(const void* xperm, const int32_t* offsets, int E, int d, int F, int64_t max_rows,
+                        const void* w13_packed, const void* w3_packed, void* h, void* y, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* (d) Combine — replaces the gather/scale/index_add_ tail of GroupedExperts.forward
+ * (moe.py:285-292) and _pytorch_scatter_add_experts (moe.py:132-158).
+ *   y[o,:] = scale[s] * sum_{j<fan, src[s,j]>=0} w[s,j] * yperm[src[s,j],:],  s = out_map ? out_map[o] : o
+ * rows with s < 0 are written as zeros.  fp32 accumulate in fixed j order (no
+ * atomics: bit-reproducible), y in y_dtype (BF16 or F32).                    */
+int kmoe_combine(const void* yperm, int d, const int32_t* src_row, const float* src_w, int fan,
+                 const int32_t* out_map, const float* scale, int64_t T_out, void* y, int y_dtype,
+                 void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Expert-choice selection — replaces ExpertChoiceRouter.forward (moe.py:494-530).
+ * For each sequence b and expert e, select the C tokens of sequence b with the
+ * largest fp32 logit (= largest softmax-over-tokens probability; equal logits ->
+ * lowest token index first), in descending order, and write
+ *   idx (B,E,C) int64, w (B,E,C) f32 = p / (sum_c p + 1e-9), p = softmax over S.
+ * Also writes the dispatch/combine tables: row_token (E*B*C, expert-major rows
+ * e*B*C + b*C + c -> token b*S + idx), offsets (E+1) and the per-token combine
+ * table src_row/src_w (B*S, E): permuted row of (token, expert) or -1.
+ * Requires C <= S.  workspace: kmoe_ec_workspace_bytes.                      */
+size_t kmoe_ec_workspace_bytes(int B, int64_t S, int E);
+int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int64_t C, int64_t* idx, float* w,
+                   int32_t* row_token, int32_t* offsets, int32_t* src_row, float* src_w, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Mixture-of-Depths selection — replaces MoDRouter.forward (mod.py:67-122) and
+ * the gather/scatter bookkeeping of TransformerBlock.forward (layers.py:148-185).
+ *   r[b,s] = x[b,s,:] . w_mod  (fp32 accumulate)
+ *   keep the `keep` largest r of each sequence (equal r -> lowest index first),
+ *   sel_idx (B,keep) int64 ascending, sel_w (B,keep) f32 = softmax over the kept r
+ *   in ascending-index order; token_rows (B*keep) = b*S + sel_idx; out_map (B*S)
+ *   = compact index b*keep + i of a kept token, -1 otherwise.
+ * Requires 1 <= keep <= S.  workspace: kmoe_mod_workspace_bytes.            */
+size_t kmoe_mod_workspace_bytes(int B, int64_t S);
+int kmoe_mod_select(const void* x, int B, int64_t S, int d, const void* w_mod, int64_t keep, float* logits,
+                    int64_t* sel_idx, float* sel_w, int32_t* token_rows, int32_t* out_map, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KMOE_H */

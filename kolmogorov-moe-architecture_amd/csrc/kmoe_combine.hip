@@ -1,0 +1,109 @@
+// Combine: y[o] = scale[s] * sum_j w[s,j] * yperm[src[s,j]],  s = out_map ? out_map[o] : o.
+// Replaces the gather / weight / index_add_ tail of GroupedExperts.forward
+// (moe_arch/model/moe.py:285-292), the expert-choice scatter-add
+// (_pytorch_scatter_add_experts, moe.py:132-158) and, with out_map/scale, the
+// MoD weighted scatter back to full sequence length (layers.py:175-185).
+//
+// One wave per output row, 16-byte vector loads of each source row, fp32
+// accumulation in a fixed source order: no atomics, bit-reproducible.
+#include "kmoe_common.h"
+
+namespace {
+
+constexpr int CROWS = 4;  // rows (waves) per workgroup
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(64 * CROWS) void combine_kernel(const uint16_t* __restrict__ yperm, int d,
+                                                             const int32_t* __restrict__ src_row,
+                                                             const float* __restrict__ src_w, int fan,
+                                                             const int32_t* __restrict__ out_map,
+                                                             const float* __restrict__ scale, int64_t T_out,
+                                                             void* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int64_t o = (int64_t)blockIdx.x * CROWS + (threadIdx.x >> 6);
+  if (o >= T_out) return;
+  const int64_t s = out_map ? (int64_t)out_map[o] : o;
+  const int nvec = d / 8;
+  if (s < 0) {
+    if (OUT_F32) {
+      f32x4_t* dst = reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o * d);
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      for (int v = lane; v < nvec; v += 64) {
+        dst[2 * v] = z;
+        dst[2 * v + 1] = z;
+      }
+    } else {
+      i32x4_t* dst = reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(y) + o * d);
+      const i32x4_t z = {0, 0, 0, 0};
+      for (int v = lane; v < nvec; v += 64) dst[v] = z;
+    }
+    return;
+  }
+  const float sc = scale ? scale[s] : 1.0f;
+  // Source list of this row (fan <= 64): lane j holds source j.
+  int my_src = -1;
+  float my_w = 0.0f;
+  if (lane < fan) {
+    my_src = src_row[s * fan + lane];
+    my_w = src_w[s * fan + lane];
+  }
+  const uint64_t live = __ballot(my_src >= 0);
+  for (int v0 = 0; v0 < nvec; v0 += 64) {
+    const int v = v0 + lane;
+    float acc[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+    uint64_t m = live;
+    while (m) {
+      const int j = __builtin_ctzll(m);
+      m &= m - 1;
+      const int r = __shfl(my_src, j, 64);
+      const float w = __shfl(my_w, j, 64);
+      if (v < nvec) {
+        const i32x4_t val = reinterpret_cast<const i32x4_t*>(yperm + (int64_t)r * d)[v];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] = fmaf(w, __uint_as_float(((uint32_t)val[q]) << 16), acc[2 * q]);
+          acc[2 * q + 1] = fmaf(w, __uint_as_float(((uint32_t)val[q]) & 0xffff0000u), acc[2 * q + 1]);
+        }
+      }
+    }
+    if (v < nvec) {
+      if (OUT_F32) {
+        f32x4_t* dst = reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o * d) + 2 * v;
+        dst[0] = f32x4_t{acc[0] * sc, acc[1] * sc, acc[2] * sc, acc[3] * sc};
+        dst[1] = f32x4_t{acc[4] * sc, acc[5] * sc, acc[6] * sc, acc[7] * sc};
+      } else {
+        i32x4_t out;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          out[q] = (int)((uint32_t)f32_to_bf16(acc[2 * q] * sc) | ((uint32_t)f32_to_bf16(acc[2 * q + 1] * sc) << 16));
+        reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(y) + o * d)[v] = out;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int kmoe_combine(const void* yperm, int d, const int32_t* src_row, const float* src_w, int fan,
+                            const int32_t* out_map, const float* scale, int64_t T_out, void* y, int y_dtype,
+                            void* stream) {
+  KMOE_REQUIRE(yperm && src_row && src_w && y, KMOE_ERR_NULL, "kmoe_combine: null buffer");
+  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "kmoe_combine: d=%d must be a positive multiple of 64", d);
+  KMOE_REQUIRE(fan >= 1 && fan <= 64, KMOE_ERR_SHAPE, "kmoe_combine: fan=%d not in [1,64]", fan);
+  KMOE_REQUIRE(T_out >= 0, KMOE_ERR_SHAPE, "kmoe_combine: T_out < 0");
+  KMOE_REQUIRE(y_dtype == KMOE_DTYPE_BF16 || y_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE,
+               "kmoe_combine: y dtype must be bf16 or f32");
+  if (T_out == 0) return KMOE_OK;
+  const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(T_out, CROWS));
+  hipStream_t s = kmoe::as_stream(stream);
+  const uint16_t* yp = static_cast<const uint16_t*>(yperm);
+  if (y_dtype == KMOE_DTYPE_BF16)
+    hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(64 * CROWS), 0, s, yp, d, src_row, src_w, fan, out_map,
+                       scale, T_out, y);
+  else
+    hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(64 * CROWS), 0, s, yp, d, src_row, src_w, fan, out_map,
+                       scale, T_out, y);
+  return kmoe::check_launch("kmoe_combine");
+}

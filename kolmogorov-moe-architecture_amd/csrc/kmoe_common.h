@@ -1,0 +1,98 @@
+// Shared device/host helpers for the kmoe HIP kernels (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "kmoe.h"
+
+// ---------------------------------------------------------------- vector types
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+#define KMOE_LDS __attribute__((address_space(3)))
+
+// ---------------------------------------------------------------- error state
+namespace kmoe {
+
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+template <typename T>
+inline T ceil_div(T a, T b) { return (a + b - 1) / b; }
+
+}  // namespace kmoe
+
+#define KMOE_REQUIRE(cond, code, ...)      \
+  do {                                     \
+    if (!(cond)) {                         \
+      kmoe::set_error(__VA_ARGS__);        \
+      return (code);                       \
+    }                                      \
+  } while (0)
+
+// ---------------------------------------------------------------- device math
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+
+// fp32 -> OCP e4m3fn, saturating to +-448, round-to-nearest-even.  Pure integer
+// arithmetic, so it is specified exactly (the oracle restates it in numpy).
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t sign = (u >> 24) & 0x80u;
+  if (f != f) return sign | 0x7fu;  // NaN stays NaN
+  float a = fminf(fabsf(f), 448.0f);
+  uint32_t ua = __float_as_uint(a);
+  int exp = (int)(ua >> 23) - 127;
+  uint32_t code;
+  if (exp < -6) {
+    // subnormal range of e4m3: value = m * 2^-9, m in [0, 8]
+    // a * 2^9 rounded to nearest even integer
+    float s = a * 512.0f;              // exact (power-of-two scaling)
+    float r = __builtin_rintf(s);      // RNE
+    code = (uint32_t)r;                // 8 -> becomes the smallest normal (exp field 1, mant 0)
+  } else {
+    uint32_t mant = ua & 0x7fffffu;
+    uint32_t m3 = mant >> 20;
+    uint32_t rest = mant & 0xfffffu;
+    uint32_t half = 0x80000u;
+    uint32_t e = (uint32_t)(exp + 7);
+    code = (e << 3) | m3;
+    if (rest > half || (rest == half && (m3 & 1u))) code += 1u;  // carries into exponent correctly
+    if (code > 0x7eu) code = 0x7eu;  // saturate (448 = 0x7e)
+  }
+  return sign | code;
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  uint32_t s = c & 0x80u, e = (c >> 3) & 15u, m = c & 7u;
+  float v = e == 0 ? (float)m * (1.0f / 512.0f) : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return s ? -v : v;
+}
+
+// Wave-level reductions (64 lanes).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}

@@ -1,0 +1,338 @@
+// Dispatch: stable counting sort of the T*k token->expert assignments, optional
+// capacity drop, and the gather of token rows into expert-contiguous order.
+// Replaces the argsort/bincount/cumsum/gather/pad block of GroupedExperts.forward
+// (moe_arch/model/moe.py:238-272); the capacity drop is this build's rule for
+// config 3 (keep the first `capacity` assignments of each expert in assignment
+// order, drop the rest).
+//
+// Three launches, no host sync:
+//   1. hist:    per-block (DTB tokens) expert histograms
+//   2. scan:    per-expert exclusive scan over blocks -> block bases, counts,
+//               kept counts and expert offsets
+//   3. permute: per-block stable ranks via wave ballots, slot tables, then one
+//               read of each token row and k 16-byte-vector row writes
+#include "kmoe_common.h"
+
+namespace {
+
+constexpr int DTB = 128;      // tokens per dispatch block
+constexpr int DTHREADS = 256;
+
+__device__ __forceinline__ int load_expert(const int64_t* idx, int64_t a, int E) {
+  int64_t e = idx[a];
+  return (e >= 0 && e < E) ? (int)e : -1;  // out-of-range ids are dropped
+}
+
+__global__ __launch_bounds__(DTHREADS) void hist_kernel(const int64_t* __restrict__ idx, int64_t T, int k, int E,
+                                                        int32_t* __restrict__ block_counts) {
+  __shared__ int cnt[KMOE_MAX_EXPERTS];
+  const int tid = threadIdx.x;
+  if (tid < E) cnt[tid] = 0;
+  __syncthreads();
+  const int64_t a0 = (int64_t)blockIdx.x * DTB * k;
+  const int64_t a1 = min<int64_t>(a0 + (int64_t)DTB * k, T * k);
+  for (int64_t a = a0 + tid; a < a1; a += DTHREADS) {
+    int e = load_expert(idx, a, E);
+    if (e >= 0) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (tid < E) block_counts[(int64_t)blockIdx.x * E + tid] = cnt[tid];
+}
+
+// Single workgroup: for every expert, exclusive scan of block_counts over blocks.
+__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ block_counts, int64_t nblk, int E,
+                                                    int64_t capacity, int32_t* __restrict__ block_base,
+                                                    int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
+  __shared__ int wsum[16];
+  __shared__ int total[KMOE_MAX_EXPERTS];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, nwave = blockDim.x >> 6;
+  for (int e = 0; e < E; ++e) {
+    int running = 0;
+    for (int64_t b0 = 0; b0 < nblk; b0 += blockDim.x) {
+      const int64_t b = b0 + tid;
+      const int v = b < nblk ? block_counts[b * E + e] : 0;
+      // inclusive wave scan
+      int s = v;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        int u = __shfl_up(s, o, 64);
+        if (lane >= o) s += u;
+      }
+      if (lane == 63) wsum[wave] = s;
+      __syncthreads();
+      int before = 0, chunk = 0;
+      for (int w = 0; w < nwave; ++w) {
+        if (w < wave) before += wsum[w];
+        chunk += wsum[w];
+      }
+      if (b < nblk) block_base[b * E + e] = running + before + s - v;
+      running += chunk;
+      __syncthreads();
+    }
+    if (tid == 0) total[e] = running;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int off = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = total[e];
+      counts[e] = c;
+      offsets[e] = off;
+      off += (capacity > 0 && c > capacity) ? (int)capacity : c;
+    }
+    offsets[E] = off;
+  }
+}
+
+template <bool FP8>
+__global__ __launch_bounds__(DTHREADS) void permute_kernel(
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, int64_t T, int d,
+    const int64_t* __restrict__ idx, const void* __restrict__ wsrc, int w_dtype, int k, int E, int64_t capacity,
+    const int32_t* __restrict__ block_base, const int32_t* __restrict__ offsets, int32_t* __restrict__ row_token,
+    int32_t* __restrict__ slot_row, float* __restrict__ slot_w, void* __restrict__ xperm,
+    float* __restrict__ xperm_scale) {
+  __shared__ int wave_cnt[DTHREADS / 64][KMOE_MAX_EXPERTS];
+  __shared__ int running[KMOE_MAX_EXPERTS];
+  __shared__ int dest[DTB * 8];  // k <= 8 handled per chunk below
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * DTB;
+  const int64_t a0 = t0 * k;
+  const int64_t a1 = min<int64_t>(a0 + (int64_t)DTB * k, T * k);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  if (tid < E) running[tid] = 0;
+  __syncthreads();
+
+  // ---- ranks, in assignment order (chunks of 256 assignments)
+  for (int64_t c0 = a0; c0 < a1; c0 += DTHREADS) {
+    const int64_t a = c0 + tid;
+    const bool valid = a < a1;
+    const int e = valid ? load_expert(idx, a, E) : -1;
+    int rank_w = 0;
+    for (int ee = 0; ee < E; ++ee) {
+      const uint64_t m = __ballot(e == ee);
+      if (e == ee) rank_w = __popcll(m & lt_mask);
+      if (lane == 0) wave_cnt[wave][ee] = __popcll(m);
+    }
+    __syncthreads();
+    if (valid) {
+      int row = -1;
+      if (e >= 0) {
+        int r = running[e] + rank_w;
+        for (int w = 0; w < wave; ++w) r += wave_cnt[w][e];
+        const int64_t g = (int64_t)block_base[(int64_t)blockIdx.x * E + e] + r;
+        if (capacity <= 0 || g < capacity) {
+          row = offsets[e] + (int)g;
+          row_token[row] = (int32_t)(a / k);
+        }
+      }
+      slot_row[a] = row;
+      float wv;
+      if (w_dtype == KMOE_DTYPE_F32)
+        wv = static_cast<const float*>(wsrc)[a];
+      else
+        wv = bf16_to_f32(static_cast<const uint16_t*>(wsrc)[a]);
+      slot_w[a] = wv;
+      dest[a - a0] = row;
+    }
+    __syncthreads();
+    if (tid < E) {
+      int s = 0;
+      for (int w = 0; w < DTHREADS / 64; ++w) s += wave_cnt[w][tid];
+      running[tid] += s;
+    }
+    __syncthreads();
+  }
+
+  // ---- row gather: one wave per token, row read once, written to its k rows
+  const int64_t ntok = min<int64_t>(DTB, T - t0);
+  const int nvec = d / 8;  // 16-byte vectors per row
+  for (int64_t tl = wave; tl < ntok; tl += DTHREADS / 64) {
+    const int64_t t = t0 + tl;
+    const int64_t xr = row_index ? (int64_t)row_index[t] : t;
+    const i32x4_t* src = reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d);
+    if (!FP8) {
+      for (int v = lane; v < nvec; v += 64) {
+        const i32x4_t val = src[v];
+        for (int j = 0; j < k; ++j) {
+          const int row = dest[tl * k + j];
+          if (row >= 0) reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(xperm) + (int64_t)row * d)[v] = val;
+        }
+      }
+    } else {
+      float amax = 0.0f;
+      for (int v = lane; v < nvec; v += 64) {
+        const i32x4_t val = src[v];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) << 16)));
+          amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) & 0xffff0000u)));
+        }
+      }
+      amax = wave_max(amax);
+      const float scale = amax / 448.0f;
+      const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+      for (int v = lane; v < nvec; v += 64) {
+        const i32x4_t val = src[v];
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const uint32_t w0 = (uint32_t)val[q];
+          lo |= f32_to_e4m3(__uint_as_float(w0 << 16) * inv) << (16 * q);
+          lo |= f32_to_e4m3(__uint_as_float(w0 & 0xffff0000u) * inv) << (16 * q + 8);
+          const uint32_t w1 = (uint32_t)val[q + 2];
+          hi |= f32_to_e4m3(__uint_as_float(w1 << 16) * inv) << (16 * q);
+          hi |= f32_to_e4m3(__uint_as_float(w1 & 0xffff0000u) * inv) << (16 * q + 8);
+        }
+        for (int j = 0; j < k; ++j) {
+          const int row = dest[tl * k + j];
+          if (row >= 0) {
+            uint32_t* o = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(xperm) + (int64_t)row * d) + 2 * v;
+            o[0] = lo;
+            o[1] = hi;
+          }
+        }
+      }
+      if (lane == 0)
+        for (int j = 0; j < k; ++j) {
+          const int row = dest[tl * k + j];
+          if (row >= 0) xperm_scale[row] = scale;
+        }
+    }
+  }
+}
+
+template <bool FP8>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint16_t* __restrict__ x,
+                                                          const int32_t* __restrict__ row_token, int64_t n_rows,
+                                                          const int32_t* __restrict__ n_rows_dev, int d,
+                                                          void* __restrict__ out, float* __restrict__ out_scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  int64_t nr = n_rows;
+  if (n_rows_dev) nr = min<int64_t>(nr, (int64_t)*n_rows_dev);
+  if (r >= nr) return;
+  const int nvec = d / 8;
+  const int32_t tok = row_token[r];
+  if (!FP8) {
+    i32x4_t* dst = reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(out) + r * d);
+    if (tok < 0) {
+      const i32x4_t z = {0, 0, 0, 0};
+      for (int v = lane; v < nvec; v += 64) dst[v] = z;
+      return;
+    }
+    const i32x4_t* src = reinterpret_cast<const i32x4_t*>(x + (int64_t)tok * d);
+    for (int v = lane; v < nvec; v += 64) dst[v] = src[v];
+  } else {
+    uint32_t* dst = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(out) + r * d);
+    if (tok < 0) {
+      for (int v = lane; v < nvec; v += 64) {
+        dst[2 * v] = 0u;
+        dst[2 * v + 1] = 0u;
+      }
+      if (lane == 0) out_scale[r] = 0.0f;
+      return;
+    }
+    const i32x4_t* src = reinterpret_cast<const i32x4_t*>(x + (int64_t)tok * d);
+    float amax = 0.0f;
+    for (int v = lane; v < nvec; v += 64) {
+      const i32x4_t val = src[v];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) << 16)));
+        amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) & 0xffff0000u)));
+      }
+    }
+    amax = wave_max(amax);
+    const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+    for (int v = lane; v < nvec; v += 64) {
+      const i32x4_t val = src[v];
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t w0 = (uint32_t)val[q];
+        lo |= f32_to_e4m3(__uint_as_float(w0 << 16) * inv) << (16 * q);
+        lo |= f32_to_e4m3(__uint_as_float(w0 & 0xffff0000u) * inv) << (16 * q + 8);
+        const uint32_t w1 = (uint32_t)val[q + 2];
+        hi |= f32_to_e4m3(__uint_as_float(w1 << 16) * inv) << (16 * q);
+        hi |= f32_to_e4m3(__uint_as_float(w1 & 0xffff0000u) * inv) << (16 * q + 8);
+      }
+      dst[2 * v] = lo;
+      dst[2 * v + 1] = hi;
+    }
+    if (lane == 0) out_scale[r] = amax / 448.0f;
+  }
+}
+
+}  // namespace
+
+extern "C" size_t kmoe_dispatch_workspace_bytes(int64_t T, int k, int E) {
+  (void)k;
+  const int64_t nblk = kmoe::ceil_div<int64_t>(T, DTB);
+  return (size_t)(2 * nblk * E) * sizeof(int32_t) + 256;
+}
+
+extern "C" int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
+                             const void* topk_w, int w_dtype, int k, int E, int64_t capacity, int32_t* counts,
+                             int32_t* offsets, int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm,
+                             int xperm_dtype, float* xperm_scale, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  KMOE_REQUIRE(x && topk_idx && topk_w && counts && offsets && row_token && slot_row && slot_w && xperm,
+               KMOE_ERR_NULL, "kmoe_dispatch: null buffer");
+  KMOE_REQUIRE(T >= 0 && T * (int64_t)k < ((int64_t)1 << 31), KMOE_ERR_SHAPE,
+               "kmoe_dispatch: T*k must fit in int32");
+  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "kmoe_dispatch: d=%d must be a positive multiple of 64", d);
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_dispatch: E=%d out of range", E);
+  KMOE_REQUIRE(k >= 1 && k <= 8 && k <= E, KMOE_ERR_SHAPE, "kmoe_dispatch: k=%d not in [1, min(8,E)]", k);
+  KMOE_REQUIRE(w_dtype == KMOE_DTYPE_BF16 || w_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE,
+               "kmoe_dispatch: topk_w dtype must be bf16 or f32");
+  KMOE_REQUIRE(xperm_dtype == KMOE_DTYPE_BF16 || xperm_dtype == KMOE_DTYPE_FP8_E4M3, KMOE_ERR_DTYPE,
+               "kmoe_dispatch: xperm dtype must be bf16 or fp8_e4m3");
+  KMOE_REQUIRE(xperm_dtype != KMOE_DTYPE_FP8_E4M3 || xperm_scale, KMOE_ERR_NULL,
+               "kmoe_dispatch: fp8 output needs xperm_scale");
+  const size_t need = kmoe_dispatch_workspace_bytes(T, k, E);
+  KMOE_REQUIRE(workspace && workspace_bytes >= need, KMOE_ERR_WORKSPACE,
+               "kmoe_dispatch: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = kmoe::as_stream(stream);
+  const int64_t nblk = kmoe::ceil_div<int64_t>(T, DTB);
+  int32_t* block_counts = static_cast<int32_t*>(workspace);
+  int32_t* block_base = block_counts + nblk * E;
+  if (T == 0) {
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, (int64_t)0, E, capacity, block_base,
+                       counts, offsets);
+    return kmoe::check_launch("kmoe_dispatch(scan)");
+  }
+  hipLaunchKernelGGL(hist_kernel, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, topk_idx, T, k, E, block_counts);
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, nblk, E, capacity, block_base, counts,
+                     offsets);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  if (xperm_dtype == KMOE_DTYPE_BF16)
+    hipLaunchKernelGGL(permute_kernel<false>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
+                       topk_idx, topk_w, w_dtype, k, E, capacity, block_base, offsets, row_token, slot_row, slot_w,
+                       xperm, xperm_scale);
+  else
+    hipLaunchKernelGGL(permute_kernel<true>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
+                       topk_idx, topk_w, w_dtype, k, E, capacity, block_base, offsets, row_token, slot_row, slot_w,
+                       xperm, xperm_scale);
+  return kmoe::check_launch("kmoe_dispatch");
+}
+
+extern "C" int kmoe_gather_rows(const void* x, const int32_t* row_token, int64_t n_rows, const int32_t* n_rows_dev,
+                                int d, void* out, int out_dtype, float* out_scale, void* stream) {
+  KMOE_REQUIRE(x && row_token && out, KMOE_ERR_NULL, "kmoe_gather_rows: null buffer");
+  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "kmoe_gather_rows: d=%d must be a positive multiple of 64", d);
+  KMOE_REQUIRE(n_rows >= 0, KMOE_ERR_SHAPE, "kmoe_gather_rows: n_rows < 0");
+  KMOE_REQUIRE(out_dtype == KMOE_DTYPE_BF16 || out_dtype == KMOE_DTYPE_FP8_E4M3, KMOE_ERR_DTYPE,
+               "kmoe_gather_rows: out dtype must be bf16 or fp8_e4m3");
+  KMOE_REQUIRE(out_dtype != KMOE_DTYPE_FP8_E4M3 || out_scale, KMOE_ERR_NULL, "kmoe_gather_rows: fp8 needs out_scale");
+  if (n_rows == 0) return KMOE_OK;
+  const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(n_rows, 4));
+  hipStream_t s = kmoe::as_stream(stream);
+  if (out_dtype == KMOE_DTYPE_BF16)
+    hipLaunchKernelGGL(gather_rows_kernel<false>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(x), row_token,
+                       n_rows, n_rows_dev, d, out, out_scale);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel<true>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(x), row_token,
+                       n_rows, n_rows_dev, d, out, out_scale);
+  return kmoe::check_launch("kmoe_gather_rows");
+}

@@ -1,0 +1,504 @@
+// Grouped SwiGLU expert GEMMs on CDNA4 MFMA.
+// Replaces moe_kernels.grouped_swiglu_forward (moe_arch/kernels/grouped_gemm.cu:186-257)
+// and the padded bmm block of GroupedExperts.forward (moe_arch/model/moe.py:275-279):
+//   gate_up:  h[r, f] = silu(x[r] . w1[e][:, f]) * (x[r] . w2[e][:, f])     (ffn.py:17-64)
+//   down:     y[r, n] = h[r] . w3[e][:, n]
+// for the rows r of expert e, [offsets[e], offsets[e+1]).
+//
+// Tiling: a workgroup (4 waves) owns a 256-row x 256-B-row tile; every wave a
+// 128x128 quarter as 4x4 blocks of v_mfma_f32_32x32x16_bf16 (fp8: 32x32x64).
+// K advances 64 bf16 (128 fp8 bytes) per step.  A and B tiles are staged through
+// LDS, double buffered (4 x 32 KiB), rows XOR-swizzled in 16-byte chunks so the
+// MFMA fragment reads are bank-conflict free.  The next step's tiles are loaded
+// into registers while the current step computes.
+//
+// Ragged groups: the grid is sized for the worst case (ceil(max_rows/256) + E
+// row tiles per column tile); every workgroup maps its id to (expert, row tile)
+// from the device-resident offsets and exits when it has none.  No host sync.
+//
+// Weights are consumed in a packed, derived layout (kmoe_pack_weights):
+//   w13: (E, 2*F_pad, d)   per 128-wide f block: 128 gate rows then 128 up rows,
+//                          each row K(=d)-contiguous (w1/w2 transposed)
+//   w3 : (E, d_pad, F_pad) row n K(=f)-contiguous (w3 transposed), d_pad = round_up(d, 256)
+#include "kmoe_common.h"
+
+namespace {
+
+constexpr int BM = 256;
+constexpr int BN = 256;       // B rows per tile (gate_up: 128 gate + 128 up)
+constexpr int KBYTES = 128;   // bytes of K per step per row (64 bf16 / 128 fp8)
+constexpr int TILE_BYTES = BM * KBYTES;  // 32 KiB
+constexpr int GEMM_THREADS = 256;
+
+__host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
+
+// (expert, row-tile) of row-slot `slot`, from the offsets; returns false if none.
+__device__ __forceinline__ bool find_row_tile(const int32_t* __restrict__ offsets, int E, int slot, int& e_out,
+                                              int& m0, int& m_end) {
+  int base = 0;
+  int lo = offsets[0];
+  for (int e = 0; e < E; ++e) {
+    const int hi = offsets[e + 1];
+    const int nt = (hi - lo + BM - 1) / BM;
+    if (slot < base + nt) {
+      e_out = e;
+      m0 = lo + (slot - base) * BM;
+      m_end = hi;
+      return true;
+    }
+    base += nt;
+    lo = hi;
+  }
+  return false;
+}
+
+__device__ __forceinline__ int swz(int row, int chunk) { return row * KBYTES + ((chunk ^ (row & 7)) << 4); }
+
+// Loads one 256 x 128-byte tile (rows clamped to [row_lo, row_hi)) into 8 registers/thread.
+__device__ __forceinline__ void load_tile(const uint8_t* __restrict__ base, int64_t ld_bytes, int row0, int row_clamp,
+                                          int kbyte, int tid, i32x4_t (&reg)[8]) {
+  const int c = tid & 7;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    int r = row0 + p * 32 + (tid >> 3);
+    r = r < row_clamp ? r : row_clamp - 1;
+    reg[p] = *reinterpret_cast<const i32x4_t*>(base + (int64_t)r * ld_bytes + kbyte + c * 16);
+  }
+}
+
+__device__ __forceinline__ void store_tile(uint8_t* lds, int tid, const i32x4_t (&reg)[8]) {
+  const int c = tid & 7;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int r = p * 32 + (tid >> 3);
+    *reinterpret_cast<i32x4_t*>(lds + swz(r, c)) = reg[p];
+  }
+}
+
+// B-row of the wave's j-th 32-row block.
+template <bool GATE_UP>
+__device__ __forceinline__ int b_row(int wn, int j, int lr) {
+  if (GATE_UP) return (j < 2 ? 0 : 128) + wn * 64 + (j & 1) * 32 + lr;
+  return wn * 128 + j * 32 + lr;
+}
+
+// FP8: A/B bytes are e4m3; a_scale per A row, b_scale per B row (global row index).
+template <bool GATE_UP, bool FP8>
+__global__ __launch_bounds__(GEMM_THREADS, 1) void grouped_gemm_kernel(
+    const uint8_t* __restrict__ A, int64_t lda_bytes, const float* __restrict__ a_scale,
+    const int32_t* __restrict__ offsets, int E, const uint8_t* __restrict__ B, int64_t b_expert_rows,
+    int64_t ldb_bytes, const float* __restrict__ b_scale, int k_bytes, uint16_t* __restrict__ C, int64_t ldc,
+    int n_valid, int n_tiles) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][TILE_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lh = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int slot = blockIdx.x / n_tiles;
+  const int nt = blockIdx.x - slot * n_tiles;
+  int e, m0, m_end;
+  if (!find_row_tile(offsets, E, slot, e, m0, m_end)) return;
+
+  const int64_t brow0 = (int64_t)e * b_expert_rows + (int64_t)nt * BN;
+  const uint8_t* Bexp = B + brow0 * ldb_bytes;
+  const int nk = k_bytes / KBYTES;
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  i32x4_t ra[8], rb[8];
+  load_tile(A, lda_bytes, m0, m_end, 0, tid, ra);
+  load_tile(Bexp, ldb_bytes, 0, BN, 0, tid, rb);
+  store_tile(lds[0][0], tid, ra);
+  store_tile(lds[0][1], tid, rb);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) {
+      load_tile(A, lda_bytes, m0, m_end, (kt + 1) * KBYTES, tid, ra);
+      load_tile(Bexp, ldb_bytes, 0, BN, (kt + 1) * KBYTES, tid, rb);
+    }
+    const uint8_t* la = lds[cur][0];
+    const uint8_t* lb = lds[cur][1];
+    if (!FP8) {
+      // 4 K-substeps of 16 bf16; lane half lh reads chunk 2*i + lh
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ch = 2 * i + lh;
+        bf16x8_t af[4], bfr[4];
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+          af[mi] = *reinterpret_cast<const bf16x8_t*>(la + swz(wm * 128 + mi * 32 + lr, ch));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bfr[j] = *reinterpret_cast<const bf16x8_t*>(lb + swz(b_row<GATE_UP>(wn, j, lr), ch));
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bfr[j], acc[mi][j], 0, 0, 0);
+      }
+    } else {
+      // 2 K-substeps of 64 fp8; lane half lh reads chunks 4*i + 2*lh, +1 (32 bytes)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int ch = 4 * i + 2 * lh;
+        i32x8_t af[4], bfr[4];
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+          const int r = wm * 128 + mi * 32 + lr;
+          const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(la + swz(r, ch));
+          const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(la + swz(r, ch + 1));
+          af[mi] = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = b_row<GATE_UP>(wn, j, lr);
+          const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(lb + swz(r, ch));
+          const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(lb + swz(r, ch + 1));
+          bfr[j] = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[mi][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[mi], bfr[j], acc[mi][j], 0, 0, 0, 127, 0,
+                                                                          127);
+      }
+    }
+    if (kt + 1 < nk) {
+      store_tile(lds[cur ^ 1][0], tid, ra);
+      store_tile(lds[cur ^ 1][1], tid, rb);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: acc[mi][j][r] is (row 8*(r/4)+4*lh+r%4, col lr) of block (mi, j)
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+      if (row >= m_end) continue;
+      const float sa = FP8 ? a_scale[row] : 1.0f;
+      uint16_t* crow = C + (int64_t)row * ldc;
+      if (GATE_UP) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int col = nt * 128 + wn * 64 + j * 32 + lr;
+          float g = acc[mi][j][r], u = acc[mi][j + 2][r];
+          if (FP8) {
+            g *= sa * b_scale[brow0 + b_row<true>(wn, j, lr)];
+            u *= sa * b_scale[brow0 + b_row<true>(wn, j + 2, lr)];
+          }
+          crow[col] = f32_to_bf16(silu_f32(g) * u);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int col = nt * BN + wn * 128 + j * 32 + lr;
+          if (col >= n_valid) continue;
+          float v = acc[mi][j][r];
+          if (FP8) v *= sa * b_scale[brow0 + b_row<false>(wn, j, lr)];
+          crow[col] = f32_to_bf16(v);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- weight packing
+// out[e][map(c)][r] = in[e][r][c] for in (E, R, Cn) row-major; rows of `out` have
+// length out_ld (>= R, zero padded), out has out_rows rows per expert (zero padded).
+// gate_up maps input column f of w1 (half 0) / w2 (half 1) to packed row
+// (f/128)*256 + half*128 + f%128; down maps column n of w3 to row n.
+template <bool IN_F32, bool FP8>
+__global__ __launch_bounds__(256) void pack_transpose_kernel(const void* __restrict__ in, int R, int Cn,
+                                                             int64_t in_expert_stride, int half, bool gate_up,
+                                                             uint8_t* __restrict__ out, int64_t out_rows, int out_ld,
+                                                             const float* __restrict__ row_scale) {
+  __shared__ float tile[64][65];
+  const int e = blockIdx.z;
+  const int r0 = blockIdx.y * 64;  // input rows (become output columns)
+  const int c0 = blockIdx.x * 64;  // input cols (become output rows)
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    const int r = r0 + i, c = c0 + tx;
+    float v = 0.0f;
+    if (r < R && c < Cn) {
+      const int64_t off = (int64_t)e * in_expert_stride + (int64_t)r * Cn + c;
+      v = IN_F32 ? static_cast<const float*>(in)[off] : bf16_to_f32(static_cast<const uint16_t*>(in)[off]);
+    }
+    tile[i][tx] = v;
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int c = c0 + i;  // output row source column
+    const int r = r0 + tx;  // output column
+    if (c >= Cn || r >= out_ld) continue;
+    const int64_t orow = gate_up ? (int64_t)(c / 128) * 256 + half * 128 + (c % 128) : (int64_t)c;
+    const int64_t o = ((int64_t)e * out_rows + orow) * out_ld + r;
+    const float v = tile[tx][i];
+    if (FP8) {
+      // row_scale holds the row amax at this point (finalised to amax/448 afterwards)
+      const float amax = row_scale[(int64_t)e * out_rows + orow];
+      const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+      out[o] = (uint8_t)f32_to_e4m3(v * inv);
+    } else {
+      reinterpret_cast<uint16_t*>(out)[o] = f32_to_bf16(v);
+    }
+  }
+}
+
+// Column amax of in[e] (R x Cn) -> per packed row amax (turned into amax/448 by
+// finalize_scale_kernel once the rows have been quantised).
+template <bool IN_F32>
+__global__ __launch_bounds__(256) void col_scale_kernel(const void* __restrict__ in, int R, int Cn,
+                                                        int64_t in_expert_stride, int half, bool gate_up,
+                                                        float* __restrict__ scale, int64_t out_rows) {
+  const int e = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= Cn) return;
+  float amax = 0.0f;
+  for (int r = 0; r < R; ++r) {
+    const int64_t off = (int64_t)e * in_expert_stride + (int64_t)r * Cn + c;
+    const float v = IN_F32 ? static_cast<const float*>(in)[off] : bf16_to_f32(static_cast<const uint16_t*>(in)[off]);
+    amax = fmaxf(amax, fabsf(v));
+  }
+  const int64_t orow = gate_up ? (int64_t)(c / 128) * 256 + half * 128 + (c % 128) : (int64_t)c;
+  scale[(int64_t)e * out_rows + orow] = amax;
+}
+
+__global__ void finalize_scale_kernel(float* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = p[i] / 448.0f;
+}
+
+__global__ void zero_kernel(uint8_t* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+__global__ void zero_f32_kernel(float* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0.0f;
+}
+
+// Per-row fp8 quantisation of a bf16 matrix, one wave per row.
+__global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restrict__ in, int64_t rows,
+                                                         const int32_t* __restrict__ n_rows_dev, int cols,
+                                                         uint8_t* __restrict__ out, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  int64_t nr = rows;
+  if (n_rows_dev) nr = min<int64_t>(nr, (int64_t)*n_rows_dev);
+  if (r >= nr) return;
+  const int nvec = cols / 8;
+  const i32x4_t* src = reinterpret_cast<const i32x4_t*>(in + r * cols);
+  float amax = 0.0f;
+  for (int v = lane; v < nvec; v += 64) {
+    const i32x4_t val = src[v];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) << 16)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) & 0xffff0000u)));
+    }
+  }
+  amax = wave_max(amax);
+  const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+  uint32_t* dst = reinterpret_cast<uint32_t*>(out + r * cols);
+  for (int v = lane; v < nvec; v += 64) {
+    const i32x4_t val = src[v];
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t w0 = (uint32_t)val[q];
+      lo |= f32_to_e4m3(__uint_as_float(w0 << 16) * inv) << (16 * q);
+      lo |= f32_to_e4m3(__uint_as_float(w0 & 0xffff0000u) * inv) << (16 * q + 8);
+      const uint32_t w1 = (uint32_t)val[q + 2];
+      hi |= f32_to_e4m3(__uint_as_float(w1 << 16) * inv) << (16 * q);
+      hi |= f32_to_e4m3(__uint_as_float(w1 & 0xffff0000u) * inv) << (16 * q + 8);
+    }
+    dst[2 * v] = lo;
+    dst[2 * v + 1] = hi;
+  }
+  if (lane == 0) scale[r] = amax / 448.0f;
+}
+
+int elem_bytes(int dtype) { return dtype == KMOE_DTYPE_FP8_E4M3 ? 1 : 2; }
+
+int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, const int32_t* offsets, int E, int K,
+                int64_t max_rows, const void* B, int64_t b_expert_rows, const float* b_scale, void* C, int64_t ldc,
+                int n_valid, int n_tiles, hipStream_t s) {
+  const int eb = fp8 ? 1 : 2;
+  const int64_t slots = kmoe::ceil_div<int64_t>(max_rows, BM) + E;
+  const int64_t blocks = slots * n_tiles;
+  if (blocks > 0x7fffffff) {
+    kmoe::set_error("kmoe gemm: grid too large");
+    return KMOE_ERR_SHAPE;
+  }
+  const uint8_t* a = static_cast<const uint8_t*>(A);
+  const uint8_t* b = static_cast<const uint8_t*>(B);
+  uint16_t* c = static_cast<uint16_t*>(C);
+  const int64_t lda = (int64_t)K * eb, ldb = (int64_t)K * eb;
+  const int kbytes = K * eb;
+  const dim3 grid((unsigned)blocks), block(GEMM_THREADS);
+  if (gate_up && !fp8)
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, false>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+                       b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
+  else if (gate_up && fp8)
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, true>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+                       b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
+  else if (!fp8)
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, false>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+                       b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, true>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+                       b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
+  return KMOE_OK;
+}
+
+}  // namespace
+
+extern "C" int kmoe_padded_ff(int F) { return round_up(F, 128); }
+
+extern "C" size_t kmoe_packed_w13_bytes(int E, int d, int F, int dtype) {
+  return (size_t)E * 2 * (size_t)round_up(F, 128) * (size_t)d * (size_t)elem_bytes(dtype);
+}
+
+extern "C" size_t kmoe_packed_w3_bytes(int E, int d, int F, int dtype) {
+  return (size_t)E * (size_t)round_up(d, 256) * (size_t)round_up(F, 128) * (size_t)elem_bytes(dtype);
+}
+
+extern "C" int kmoe_pack_weights(const void* w1, const void* w2, const void* w3, int w_dtype, int E, int d, int F,
+                                 int packed_dtype, void* w13_packed, float* w13_scale, void* w3_packed,
+                                 float* w3_scale, void* stream) {
+  KMOE_REQUIRE(w1 && w2 && w3 && w13_packed && w3_packed, KMOE_ERR_NULL, "kmoe_pack_weights: null buffer");
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_pack_weights: E=%d out of range", E);
+  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "kmoe_pack_weights: d=%d must be a positive multiple of 64", d);
+  KMOE_REQUIRE(F > 0, KMOE_ERR_SHAPE, "kmoe_pack_weights: F=%d must be > 0", F);
+  KMOE_REQUIRE(w_dtype == KMOE_DTYPE_BF16 || w_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE,
+               "kmoe_pack_weights: weight dtype must be bf16 or f32");
+  KMOE_REQUIRE(packed_dtype == KMOE_DTYPE_BF16 || packed_dtype == KMOE_DTYPE_FP8_E4M3, KMOE_ERR_DTYPE,
+               "kmoe_pack_weights: packed dtype must be bf16 or fp8_e4m3");
+  const bool fp8 = packed_dtype == KMOE_DTYPE_FP8_E4M3;
+  KMOE_REQUIRE(!fp8 || (w13_scale && w3_scale), KMOE_ERR_NULL, "kmoe_pack_weights: fp8 needs scale buffers");
+  hipStream_t s = kmoe::as_stream(stream);
+  const int Fp = round_up(F, 128), dp = round_up(d, 256);
+  const int64_t rows13 = 2 * (int64_t)Fp, rows3 = dp;
+  // zero the padding (whole buffers: simple and only done when weights change)
+  hipLaunchKernelGGL(zero_kernel, dim3(1024), dim3(256), 0, s, static_cast<uint8_t*>(w13_packed),
+                     (int64_t)kmoe_packed_w13_bytes(E, d, F, packed_dtype));
+  hipLaunchKernelGGL(zero_kernel, dim3(1024), dim3(256), 0, s, static_cast<uint8_t*>(w3_packed),
+                     (int64_t)kmoe_packed_w3_bytes(E, d, F, packed_dtype));
+  const bool f32 = w_dtype == KMOE_DTYPE_F32;
+  if (fp8) {
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(64), dim3(256), 0, s, w13_scale, (int64_t)E * rows13);
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(64), dim3(256), 0, s, w3_scale, (int64_t)E * rows3);
+    const dim3 g13((unsigned)kmoe::ceil_div(F, 256), (unsigned)E), g3((unsigned)kmoe::ceil_div(d, 256), (unsigned)E);
+    if (f32) {
+      hipLaunchKernelGGL(col_scale_kernel<true>, g13, dim3(256), 0, s, w1, d, F, (int64_t)d * F, 0, true, w13_scale, rows13);
+      hipLaunchKernelGGL(col_scale_kernel<true>, g13, dim3(256), 0, s, w2, d, F, (int64_t)d * F, 1, true, w13_scale, rows13);
+      hipLaunchKernelGGL(col_scale_kernel<true>, g3, dim3(256), 0, s, w3, F, d, (int64_t)d * F, 0, false, w3_scale, rows3);
+    } else {
+      hipLaunchKernelGGL(col_scale_kernel<false>, g13, dim3(256), 0, s, w1, d, F, (int64_t)d * F, 0, true, w13_scale, rows13);
+      hipLaunchKernelGGL(col_scale_kernel<false>, g13, dim3(256), 0, s, w2, d, F, (int64_t)d * F, 1, true, w13_scale, rows13);
+      hipLaunchKernelGGL(col_scale_kernel<false>, g3, dim3(256), 0, s, w3, F, d, (int64_t)d * F, 0, false, w3_scale, rows3);
+    }
+  }
+  // w1/w2: (E, d, F) -> rows f, cols d.  w3: (E, F, d) -> rows n, cols f.
+  const dim3 gt13((unsigned)kmoe::ceil_div(F, 64), (unsigned)kmoe::ceil_div(d, 64), (unsigned)E);
+  const dim3 gt3((unsigned)kmoe::ceil_div(d, 64), (unsigned)kmoe::ceil_div(F, 64), (unsigned)E);
+  uint8_t* o13 = static_cast<uint8_t*>(w13_packed);
+  uint8_t* o3 = static_cast<uint8_t*>(w3_packed);
+#define KMOE_PACK(F32_, FP8_)                                                                                        \
+  do {                                                                                                               \
+    hipLaunchKernelGGL((pack_transpose_kernel<F32_, FP8_>), gt13, dim3(256), 0, s, w1, d, F, (int64_t)d * F, 0, true, \
+                       o13, rows13, d, w13_scale);                                                                   \
+    hipLaunchKernelGGL((pack_transpose_kernel<F32_, FP8_>), gt13, dim3(256), 0, s, w2, d, F, (int64_t)d * F, 1, true, \
+                       o13, rows13, d, w13_scale);                                                                   \
+    hipLaunchKernelGGL((pack_transpose_kernel<F32_, FP8_>), gt3, dim3(256), 0, s, w3, F, d, (int64_t)d * F, 0, false, \
+                       o3, rows3, Fp, w3_scale);                                                                     \
+  } while (0)
+  if (f32 && fp8)
+    KMOE_PACK(true, true);
+  else if (f32)
+    KMOE_PACK(true, false);
+  else if (fp8)
+    KMOE_PACK(false, true);
+  else
+    KMOE_PACK(false, false);
+#undef KMOE_PACK
+  if (fp8) {
+    hipLaunchKernelGGL(finalize_scale_kernel, dim3(64), dim3(256), 0, s, w13_scale, (int64_t)E * rows13);
+    hipLaunchKernelGGL(finalize_scale_kernel, dim3(64), dim3(256), 0, s, w3_scale, (int64_t)E * rows3);
+  }
+  return kmoe::check_launch("kmoe_pack_weights");
+}
+
+static int check_gemm_args(const char* who, const void* a, const int32_t* offsets, int E, int d, int F,
+                           int64_t max_rows, const void* w, const void* out, int in_dtype) {
+  KMOE_REQUIRE(a && offsets && w && out, KMOE_ERR_NULL, "%s: null buffer", who);
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "%s: E=%d out of range", who, E);
+  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "%s: d=%d must be a positive multiple of 64", who, d);
+  KMOE_REQUIRE(F > 0, KMOE_ERR_SHAPE, "%s: F=%d must be > 0", who, F);
+  KMOE_REQUIRE(max_rows >= 0 && max_rows < ((int64_t)1 << 31), KMOE_ERR_SHAPE, "%s: max_rows out of range", who);
+  KMOE_REQUIRE(in_dtype == KMOE_DTYPE_BF16 || in_dtype == KMOE_DTYPE_FP8_E4M3, KMOE_ERR_DTYPE,
+               "%s: input dtype must be bf16 or fp8_e4m3", who);
+  return KMOE_OK;
+}
+
+extern "C" int kmoe_gemm_gate_up(const void* xperm, const float* xperm_scale, int in_dtype, const int32_t* offsets,
+                                 int E, int d, int F, int64_t max_rows, const void* w13_packed, const float* w13_scale,
+                                 void* h, void* stream) {
+  int rc = check_gemm_args("kmoe_gemm_gate_up", xperm, offsets, E, d, F, max_rows, w13_packed, h, in_dtype);
+  if (rc) return rc;
+  const bool fp8 = in_dtype == KMOE_DTYPE_FP8_E4M3;
+  KMOE_REQUIRE(!fp8 || (xperm_scale && w13_scale), KMOE_ERR_NULL, "kmoe_gemm_gate_up: fp8 needs scales");
+  KMOE_REQUIRE(!fp8 || d % 128 == 0, KMOE_ERR_SHAPE, "kmoe_gemm_gate_up: fp8 needs d %% 128 == 0 (d=%d)", d);
+  if (max_rows == 0) return KMOE_OK;
+  const int Fp = round_up(F, 128);
+  rc = launch_gemm(true, fp8, xperm, xperm_scale, offsets, E, d, max_rows, w13_packed, 2 * (int64_t)Fp, w13_scale, h,
+                   Fp, Fp, Fp / 128, kmoe::as_stream(stream));
+  if (rc) return rc;
+  return kmoe::check_launch("kmoe_gemm_gate_up");
+}
+
+extern "C" int kmoe_gemm_down(const void* h, const float* h_scale, int in_dtype, const int32_t* offsets, int E, int d,
+                              int F, int64_t max_rows, const void* w3_packed, const float* w3_scale, void* y,
+                              void* stream) {
+  int rc = check_gemm_args("kmoe_gemm_down", h, offsets, E, d, F, max_rows, w3_packed, y, in_dtype);
+  if (rc) return rc;
+  const bool fp8 = in_dtype == KMOE_DTYPE_FP8_E4M3;
+  KMOE_REQUIRE(!fp8 || (h_scale && w3_scale), KMOE_ERR_NULL, "kmoe_gemm_down: fp8 needs scales");
+  if (max_rows == 0) return KMOE_OK;
+  const int Fp = round_up(F, 128), dp = round_up(d, 256);
+  rc = launch_gemm(false, fp8, h, h_scale, offsets, E, Fp, max_rows, w3_packed, dp, w3_scale, y, d, d, dp / BN,
+                   kmoe::as_stream(stream));
+  if (rc) return rc;
+  return kmoe::check_launch("kmoe_gemm_down");
+}
+
+extern "C" int kmoe_quant_rows_fp8(const void* in, int64_t rows, const int32_t* n_rows_dev, int cols, uint8_t* out,
+                                   float* scale, void* stream) {
+  KMOE_REQUIRE(in && out && scale, KMOE_ERR_NULL, "kmoe_quant_rows_fp8: null buffer");
+  KMOE_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0, KMOE_ERR_SHAPE, "kmoe_quant_rows_fp8: bad shape");
+  if (rows == 0) return KMOE_OK;
+  hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(rows, 4)), dim3(256), 0,
+                     kmoe::as_stream(stream), static_cast<const uint16_t*>(in), rows, n_rows_dev, cols, out, scale);
+  return kmoe::check_launch("kmoe_quant_rows_fp8");
+}
+
+extern "C" int kmoe_grouped_swiglu(const void* xperm, const int32_t* offsets, int E, int d, int F, int64_t max_rows,
+                                   const void* w13_packed, const void* w3_packed, void* h, void* y, void* stream) {
+  int rc = kmoe_gemm_gate_up(xperm, nullptr, KMOE_DTYPE_BF16, offsets, E, d, F, max_rows, w13_packed, nullptr, h,
+                             stream);
+  if (rc) return rc;
+  return kmoe_gemm_down(h, nullptr, KMOE_DTYPE_BF16, offsets, E, d, F, max_rows, w3_packed, nullptr, y, stream);
+}

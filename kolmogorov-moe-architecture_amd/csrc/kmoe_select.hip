@@ -1,0 +1,338 @@
+// Per-sequence top-C selection for expert-choice routing and Mixture-of-Depths.
+//   kmoe_ec_select   follows ExpertChoiceRouter.forward (moe_arch/model/moe.py:494-530)
+//   kmoe_mod_select  follows MoDRouter.forward (moe_arch/model/mod.py:67-122) plus the
+//                    gather/scatter index bookkeeping of TransformerBlock.forward
+//                    (moe_arch/model/layers.py:148-185)
+//
+// Selection is an exact radix select over order-preserving uint32 images of the
+// fp32 scores (4 passes of 8 bits, LDS histograms), followed by an index-ordered
+// compaction: every score above the threshold is taken, and of the scores equal
+// to it the lowest indices are taken first.  One 1024-thread workgroup per
+// (sequence, expert); keys live in LDS.
+#include "kmoe_common.h"
+
+namespace {
+
+constexpr int SEL_THREADS = 1024;
+constexpr int SEL_MAX_S = 16384;  // keys held in LDS
+constexpr int SEL_MAX_C = 8192;   // sort buffer for the expert-choice order
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (f != f) return 0u;  // NaN ranks last
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Exclusive block scan of one int per thread (1024 threads); returns the exclusive
+// prefix and writes the total to *total.
+__device__ int block_excl_scan(int v, int* s_wave, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int s = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(s, o, 64);
+    if (lane >= o) s += u;
+  }
+  if (lane == 63) s_wave[wave] = s;
+  __syncthreads();
+  int before = 0, tot = 0;
+  for (int w = 0; w < nw; ++w) {
+    if (w < wave) before += s_wave[w];
+    tot += s_wave[w];
+  }
+  __syncthreads();
+  *total = tot;
+  return before + s - v;
+}
+
+__device__ float block_sum(float v, float* s_red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_sum(v);
+  if (lane == 0) s_red[wave] = v;
+  __syncthreads();
+  float t = 0.0f;
+  for (int w = 0; w < nw; ++w) t += s_red[w];
+  __syncthreads();
+  return t;
+}
+
+// Finds the key `thr` of the C-th largest element and how many elements equal to
+// thr must be taken (`need`).
+__device__ void radix_select_desc(const uint32_t* keys, int n, int C, uint32_t* s_hist, uint32_t* s_bcast,
+                                  uint32_t& thr, int& need) {
+  uint32_t prefix = 0, pmask = 0;
+  int remaining = C;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) s_hist[i] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const uint32_t k = keys[i];
+      if ((k & pmask) == prefix) atomicAdd(&s_hist[(k >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int cum = 0, dsel = 0;
+      for (int dg = 255; dg >= 0; --dg) {
+        const int h = (int)s_hist[dg];
+        if (cum + h >= remaining) {
+          dsel = dg;
+          break;
+        }
+        cum += h;
+      }
+      s_bcast[0] = (uint32_t)dsel;
+      s_bcast[1] = (uint32_t)(remaining - cum);
+    }
+    __syncthreads();
+    prefix |= s_bcast[0] << shift;
+    pmask |= 255u << shift;
+    remaining = (int)s_bcast[1];
+    __syncthreads();
+  }
+  thr = prefix;
+  need = remaining;
+}
+
+// Index-ordered compaction of the selection; calls emit(i, pos) for each selected
+// index i with its position pos in index order.  Threads own contiguous chunks.
+template <typename Emit>
+__device__ void compact_selected(const uint32_t* keys, int n, uint32_t thr, int need, int* s_wave, Emit emit) {
+  const int chunk = (n + (int)blockDim.x - 1) / (int)blockDim.x;
+  const int i0 = min(n, (int)threadIdx.x * chunk), i1 = min(n, i0 + chunk);
+  int n_eq = 0;
+  for (int i = i0; i < i1; ++i) n_eq += keys[i] == thr;
+  int tot;
+  int eq_before = block_excl_scan(n_eq, s_wave, &tot);
+  int n_take = 0;
+  {
+    int eqr = eq_before;
+    for (int i = i0; i < i1; ++i) {
+      const uint32_t k = keys[i];
+      if (k > thr) ++n_take;
+      else if (k == thr) n_take += (eqr++ < need);
+    }
+  }
+  int pos = block_excl_scan(n_take, s_wave, &tot);
+  int eqr = eq_before;
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t k = keys[i];
+    bool take = k > thr;
+    if (k == thr) take = (eqr++ < need);
+    if (take) emit(i, pos++);
+  }
+}
+
+__global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+__global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __restrict__ logits, int B, int S, int E,
+                                                                int C, int64_t* __restrict__ idx, float* __restrict__ w,
+                                                                int32_t* __restrict__ row_token,
+                                                                int32_t* __restrict__ offsets,
+                                                                int32_t* __restrict__ src_row,
+                                                                float* __restrict__ src_w) {
+  __shared__ uint32_t keys[SEL_MAX_S];
+  __shared__ uint64_t sorted[SEL_MAX_C];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t bc[2];
+  __shared__ int s_wave[SEL_THREADS / 64];
+  __shared__ float s_red[SEL_THREADS / 64];
+  const int b = blockIdx.x / E, e = blockIdx.x % E;
+  const float* lg = logits + (int64_t)b * S * E + e;
+
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < S; i += blockDim.x) {
+    const float v = lg[(int64_t)i * E];
+    keys[i] = order_key(v);
+    mx = fmaxf(mx, v);
+  }
+  mx = wave_max(mx);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = s_red[0];
+  for (int q = 1; q < SEL_THREADS / 64; ++q) mx = fmaxf(mx, s_red[q]);
+  __syncthreads();
+  // softmax denominator over the whole sequence (moe.py:520)
+  float den = 0.0f;
+  for (int i = threadIdx.x; i < S; i += blockDim.x) den += __expf(lg[(int64_t)i * E] - mx);
+  den = block_sum(den, s_red);
+
+  uint32_t thr;
+  int need;
+  radix_select_desc(keys, S, C, hist, bc, thr, need);
+
+  int Cp = 1;
+  while (Cp < C) Cp <<= 1;
+  for (int i = threadIdx.x; i < Cp; i += blockDim.x) sorted[i] = 0ull;
+  __syncthreads();
+  compact_selected(keys, S, thr, need, s_wave, [&](int i, int pos) {
+    if (pos < C) sorted[pos] = ((uint64_t)keys[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+  });
+  __syncthreads();
+  // bitonic sort, descending by (key, -index)
+  for (int kk = 2; kk <= Cp; kk <<= 1) {
+    for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+      for (int i = threadIdx.x; i < Cp; i += blockDim.x) {
+        const int l = i ^ jj;
+        if (l > i) {
+          const uint64_t a = sorted[i], c = sorted[l];
+          const bool desc = (i & kk) == 0;
+          if (desc ? (a < c) : (a > c)) {
+            sorted[i] = c;
+            sorted[l] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // weights: p / (sum_sel p + 1e-9)  (moe.py:528)
+  float psel = 0.0f;
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    const int s = (int)(0xffffffffu - (uint32_t)(sorted[c] & 0xffffffffu));
+    psel += __expf(lg[(int64_t)s * E] - mx) / den;
+  }
+  psel = block_sum(psel, s_red);
+  const float inv = 1.0f / (psel + 1e-9f);
+  const int64_t BC = (int64_t)B * C;
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    const int s = (int)(0xffffffffu - (uint32_t)(sorted[c] & 0xffffffffu));
+    const float p = __expf(lg[(int64_t)s * E] - mx) / den;
+    const float wv = p * inv;
+    const int64_t o = ((int64_t)b * E + e) * C + c;
+    idx[o] = s;
+    w[o] = wv;
+    const int64_t row = (int64_t)e * BC + (int64_t)b * C + c;
+    const int64_t tok = (int64_t)b * S + s;
+    row_token[row] = (int32_t)tok;
+    src_row[tok * E + e] = (int32_t)row;
+    src_w[tok * E + e] = wv;
+  }
+  if (b == 0 && threadIdx.x == 0) {
+    offsets[e] = (int32_t)(e * BC);
+    if (e == E - 1) offsets[E] = (int32_t)(E * BC);
+  }
+}
+
+// r[t] = x[t,:] . w_mod, one wave per token.
+__global__ __launch_bounds__(256) void mod_logits_kernel(const uint16_t* __restrict__ x, int64_t T, int d,
+                                                         const uint16_t* __restrict__ wm, float* __restrict__ r) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const i32x4_t* xv = reinterpret_cast<const i32x4_t*>(x + t * d);
+  const i32x4_t* wv = reinterpret_cast<const i32x4_t*>(wm);
+  float acc = 0.0f;
+  for (int v = lane; v < d / 8; v += 64) {
+    const i32x4_t a = xv[v], c = wv[v];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc = fmaf(__uint_as_float(((uint32_t)a[q]) << 16), __uint_as_float(((uint32_t)c[q]) << 16), acc);
+      acc = fmaf(__uint_as_float(((uint32_t)a[q]) & 0xffff0000u), __uint_as_float(((uint32_t)c[q]) & 0xffff0000u), acc);
+    }
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) r[t] = acc;
+}
+
+__global__ __launch_bounds__(SEL_THREADS) void mod_select_kernel(const float* __restrict__ r, int S, int keep,
+                                                                 int64_t* __restrict__ sel_idx,
+                                                                 float* __restrict__ sel_w,
+                                                                 int32_t* __restrict__ token_rows,
+                                                                 int32_t* __restrict__ out_map) {
+  __shared__ uint32_t keys[SEL_MAX_S];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t bc[2];
+  __shared__ int s_wave[SEL_THREADS / 64];
+  __shared__ float s_red[SEL_THREADS / 64];
+  const int b = blockIdx.x;
+  const float* rb = r + (int64_t)b * S;
+  for (int i = threadIdx.x; i < S; i += blockDim.x) {
+    keys[i] = order_key(rb[i]);
+    out_map[(int64_t)b * S + i] = -1;
+  }
+  __syncthreads();
+  uint32_t thr;
+  int need;
+  radix_select_desc(keys, S, keep, hist, bc, thr, need);
+  // max over the kept logits = max over the sequence (the top element is kept)
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < S; i += blockDim.x) mx = fmaxf(mx, rb[i]);
+  mx = wave_max(mx);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = s_red[0];
+  for (int q = 1; q < SEL_THREADS / 64; ++q) mx = fmaxf(mx, s_red[q]);
+  __syncthreads();
+  // pass 1: positions + softmax denominator over the kept tokens (mod.py:112)
+  float den = 0.0f;
+  compact_selected(keys, S, thr, need, s_wave, [&](int i, int pos) {
+    if (pos >= keep) return;
+    const int64_t o = (int64_t)b * keep + pos;
+    sel_idx[o] = i;
+    token_rows[o] = (int32_t)((int64_t)b * S + i);
+    out_map[(int64_t)b * S + i] = (int32_t)o;
+    den += __expf(rb[i] - mx);
+  });
+  den = block_sum(den, s_red);
+  const float inv = 1.0f / den;
+  __syncthreads();
+  for (int p = threadIdx.x; p < keep; p += blockDim.x) {
+    const int64_t o = (int64_t)b * keep + p;
+    sel_w[o] = __expf(rb[sel_idx[o]] - mx) * inv;
+  }
+}
+
+}  // namespace
+
+extern "C" size_t kmoe_ec_workspace_bytes(int B, int64_t S, int E) {
+  (void)B;
+  (void)S;
+  (void)E;
+  return 0;
+}
+
+extern "C" int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int64_t C, int64_t* idx, float* w,
+                              int32_t* row_token, int32_t* offsets, int32_t* src_row, float* src_w, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  KMOE_REQUIRE(logits && idx && w && row_token && offsets && src_row && src_w, KMOE_ERR_NULL,
+               "kmoe_ec_select: null buffer");
+  KMOE_REQUIRE(B >= 1 && E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_ec_select: bad B=%d/E=%d", B, E);
+  KMOE_REQUIRE(S >= 1 && S <= SEL_MAX_S, KMOE_ERR_UNSUPPORTED, "kmoe_ec_select: S=%lld not in [1,%d]", (long long)S,
+               SEL_MAX_S);
+  KMOE_REQUIRE(C >= 1 && C <= S && C <= SEL_MAX_C, KMOE_ERR_SHAPE, "kmoe_ec_select: C=%lld not in [1,min(S,%d)]",
+               (long long)C, SEL_MAX_C);
+  KMOE_REQUIRE((int64_t)E * B * C < ((int64_t)1 << 31), KMOE_ERR_SHAPE, "kmoe_ec_select: E*B*C must fit in int32");
+  hipStream_t s = kmoe::as_stream(stream);
+  const int64_t n = (int64_t)B * S * E;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(256), dim3(256), 0, s, src_row, n, -1);
+  hipLaunchKernelGGL(ec_select_kernel, dim3((unsigned)(B * E)), dim3(SEL_THREADS), 0, s, logits, B, (int)S, E, (int)C,
+                     idx, w, row_token, offsets, src_row, src_w);
+  return kmoe::check_launch("kmoe_ec_select");
+}
+
+extern "C" size_t kmoe_mod_workspace_bytes(int B, int64_t S) { return (size_t)B * (size_t)S * sizeof(float); }
+
+extern "C" int kmoe_mod_select(const void* x, int B, int64_t S, int d, const void* w_mod, int64_t keep, float* logits,
+                               int64_t* sel_idx, float* sel_w, int32_t* token_rows, int32_t* out_map, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  KMOE_REQUIRE(x && w_mod && logits && sel_idx && sel_w && token_rows && out_map, KMOE_ERR_NULL,
+               "kmoe_mod_select: null buffer");
+  KMOE_REQUIRE(B >= 1, KMOE_ERR_SHAPE, "kmoe_mod_select: B=%d", B);
+  KMOE_REQUIRE(S >= 1 && S <= SEL_MAX_S, KMOE_ERR_UNSUPPORTED, "kmoe_mod_select: S=%lld not in [1,%d]", (long long)S,
+               SEL_MAX_S);
+  KMOE_REQUIRE(keep >= 1 && keep <= S, KMOE_ERR_SHAPE, "kmoe_mod_select: keep=%lld not in [1,S]", (long long)keep);
+  KMOE_REQUIRE(d > 0 && d % 8 == 0, KMOE_ERR_SHAPE, "kmoe_mod_select: d=%d must be a multiple of 8", d);
+  hipStream_t s = kmoe::as_stream(stream);
+  const int64_t T = (int64_t)B * S;
+  hipLaunchKernelGGL(mod_logits_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(x), T, d, static_cast<const uint16_t*>(w_mod), logits);
+  hipLaunchKernelGGL(mod_select_kernel, dim3((unsigned)B), dim3(SEL_THREADS), 0, s, logits, (int)S, (int)keep, sel_idx,
+                     sel_w, token_rows, out_map);
+  return kmoe::check_launch("kmoe_mod_select");
+}

@@ -1,0 +1,305 @@
+"""Tensor-level wrappers over the kmoe C ABI (one function per entry point).
+
+Every wrapper validates shapes/dtypes/devices on the host, allocates its
+outputs with torch (the C ABI itself never allocates), and launches on
+torch's current HIP stream.  There is no CPU path: inputs must live on a GPU.
+"""
+from __future__ import annotations
+
+import math
+from typing import NamedTuple, Optional
+
+import torch
+
+from . import _lib
+from ._lib import ptr
+
+_BF16 = torch.bfloat16
+
+
+def _need_gpu(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("kmoe: tensors must be on a GPU (the HIP kernels are the only implementation)")
+
+
+def _contig(t, dtype=None):
+    if t is None:
+        return None
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    return t.contiguous()
+
+
+def _stream(t):
+    return _lib.stream_ptr(t.device)
+
+
+# ---------------------------------------------------------------- stage timing
+# When a list is installed here (bench.py does), every stage records a pair of
+# HIP events on the launch stream: (name, start, end).  Off by default.
+_STAGE_EVENTS: Optional[list] = None
+
+
+class _Stage:
+    def __init__(self, name):
+        self.name = name
+
+    def __enter__(self):
+        if _STAGE_EVENTS is not None:
+            self.start = torch.cuda.Event(enable_timing=True)
+            self.start.record()
+        return self
+
+    def __exit__(self, *exc):
+        if _STAGE_EVENTS is not None:
+            end = torch.cuda.Event(enable_timing=True)
+            end.record()
+            _STAGE_EVENTS.append((self.name, self.start, end))
+        return False
+
+
+def set_stage_timing(events: Optional[list]):
+    """Install (a list) or remove (None) the per-stage event recorder."""
+    global _STAGE_EVENTS
+    _STAGE_EVENTS = events
+
+
+class RouterOut(NamedTuple):
+    logits: torch.Tensor          # (T, E) f32
+    idx: Optional[torch.Tensor]   # (T, k) int64
+    w: Optional[torch.Tensor]     # (T, k) f32
+    partials: torch.Tensor        # per-block aux partial sums
+
+
+def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None) -> RouterOut:
+    """logits/top-k of the reference Router (moe.py:423-462) on the HIP kernel.
+
+    x2d: (rows, d) bf16; w_in: (128, d); w_out: (E, 128); row_index: optional
+    int32 (T,) selecting the rows of x2d that are the tokens.
+    """
+    _need_gpu(x2d, w_in, w_out)
+    x2d = _contig(x2d, _BF16)
+    w_in = _contig(w_in, _BF16)
+    w_out = _contig(w_out, _BF16)
+    d = x2d.shape[1]
+    E = w_out.shape[0]
+    if w_in.shape != (_lib.ROUTER_HIDDEN, d) or w_out.shape[1] != _lib.ROUTER_HIDDEN:
+        raise ValueError(f"kmoe.router: weight shapes {tuple(w_in.shape)}, {tuple(w_out.shape)} "
+                         f"do not match d={d}, hidden={_lib.ROUTER_HIDDEN}")
+    if T is None:
+        T = row_index.shape[0] if row_index is not None else x2d.shape[0]
+    dev = x2d.device
+    logits = torch.empty(T, E, device=dev, dtype=torch.float32)
+    idx = torch.empty(T, k, device=dev, dtype=torch.int64) if k > 0 else None
+    w = torch.empty(T, k, device=dev, dtype=torch.float32) if k > 0 else None
+    npart = _lib.load().kmoe_router_partials_len(T, E)
+    partials = torch.empty(max(npart, 1), device=dev, dtype=torch.float32)
+    bias = _contig(bias, torch.float32)
+    with _Stage("router"):
+        _lib.call("kmoe_router", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
+              ptr(logits), ptr(idx), ptr(w), ptr(partials), _stream(x2d))
+    return RouterOut(logits, idx, w, partials)
+
+
+def aux_loss(partials, T, E, counts, k, w_lb, w_z):
+    """(aux, load_balance, z) of MoELayer._compute_auxiliary_losses (moe.py:840-939)."""
+    out = torch.empty(3, device=partials.device, dtype=torch.float32)
+    with _Stage("aux"):
+        _lib.call("kmoe_aux_loss", ptr(partials), T, E, ptr(counts), k, float(w_lb), float(w_z), ptr(out),
+              _stream(partials))
+    return out
+
+
+class DispatchOut(NamedTuple):
+    counts: torch.Tensor     # (E,) int32 routed counts
+    offsets: torch.Tensor    # (E+1,) int32 kept-row offsets
+    row_token: torch.Tensor  # (T*k,) int32
+    slot_row: torch.Tensor   # (T*k,) int32, -1 = dropped
+    slot_w: torch.Tensor     # (T*k,) f32
+    xperm: torch.Tensor      # (T*k, d) bf16 or uint8 (fp8 e4m3)
+    xscale: Optional[torch.Tensor]  # (T*k,) f32 for fp8
+
+
+def capacity_of(cf: float, T: int, k: int, E: int) -> int:
+    """Per-expert capacity ceil(cf*T*k/E) of the token-choice drop rule."""
+    return int(math.ceil(cf * T * k / E))
+
+
+def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None) -> DispatchOut:
+    """Stable counting-sort dispatch (moe.py:238-272) + optional capacity drop."""
+    _need_gpu(x2d, idx, w)
+    x2d = _contig(x2d, _BF16)
+    idx = _contig(idx, torch.int64)
+    if w.dtype not in (torch.float32, _BF16):
+        w = w.float()
+    w = w.contiguous()
+    T, k = idx.shape
+    d = x2d.shape[1]
+    A = T * k
+    dev = x2d.device
+    lib = _lib.load()
+    counts = torch.empty(E, device=dev, dtype=torch.int32)
+    offsets = torch.empty(E + 1, device=dev, dtype=torch.int32)
+    row_token = torch.empty(max(A, 1), device=dev, dtype=torch.int32)
+    slot_row = torch.empty(max(A, 1), device=dev, dtype=torch.int32)
+    slot_w = torch.empty(max(A, 1), device=dev, dtype=torch.float32)
+    xperm = torch.empty(max(A, 1), d, device=dev, dtype=torch.uint8 if fp8 else _BF16)
+    xscale = torch.empty(max(A, 1), device=dev, dtype=torch.float32) if fp8 else None
+    wsb = lib.kmoe_dispatch_workspace_bytes(T, k, E)
+    ws = torch.empty(wsb, device=dev, dtype=torch.uint8)
+    wdt = _lib.DTYPE_F32 if w.dtype == torch.float32 else _lib.DTYPE_BF16
+    with _Stage("dispatch"):
+        _lib.call("kmoe_dispatch", ptr(x2d), ptr(row_index), T, d, ptr(idx), ptr(w), wdt, k, E, int(capacity),
+              ptr(counts), ptr(offsets), ptr(row_token), ptr(slot_row), ptr(slot_w), ptr(xperm),
+              _lib.DTYPE_FP8_E4M3 if fp8 else _lib.DTYPE_BF16, ptr(xscale), ptr(ws), wsb, _stream(x2d))
+    return DispatchOut(counts, offsets, row_token, slot_row, slot_w, xperm, xscale)
+
+
+def gather_rows(x2d, row_token, n_rows, fp8=False, n_rows_dev=None):
+    _need_gpu(x2d, row_token)
+    x2d = _contig(x2d, _BF16)
+    d = x2d.shape[1]
+    out = torch.empty(max(n_rows, 1), d, device=x2d.device, dtype=torch.uint8 if fp8 else _BF16)
+    scale = torch.empty(max(n_rows, 1), device=x2d.device, dtype=torch.float32) if fp8 else None
+    with _Stage("gather"):
+        _lib.call("kmoe_gather_rows", ptr(x2d), ptr(row_token), n_rows, ptr(n_rows_dev), d, ptr(out),
+              _lib.DTYPE_FP8_E4M3 if fp8 else _lib.DTYPE_BF16, ptr(scale), _stream(x2d))
+    return out, scale
+
+
+class PackedWeights(NamedTuple):
+    w13: torch.Tensor
+    w3: torch.Tensor
+    s13: Optional[torch.Tensor]
+    s3: Optional[torch.Tensor]
+    E: int
+    d: int
+    F: int
+    fp8: bool
+
+
+def pack_weights(w1, w2, w3, fp8=False) -> PackedWeights:
+    """Derived kernel layout of the reference expert weights w1,w2 (E,d,F), w3 (E,F,d)."""
+    _need_gpu(w1, w2, w3)
+    E, d, F = w1.shape
+    if w2.shape != (E, d, F) or w3.shape != (E, F, d):
+        raise ValueError("kmoe.pack_weights: w1/w2 must be (E,d,F) and w3 (E,F,d)")
+    if w1.dtype not in (torch.float32, _BF16):
+        raise ValueError(f"kmoe.pack_weights: unsupported weight dtype {w1.dtype}")
+    dt = w1.dtype
+    w1, w2, w3 = _contig(w1, dt), _contig(w2, dt), _contig(w3, dt)
+    lib = _lib.load()
+    pdt = _lib.DTYPE_FP8_E4M3 if fp8 else _lib.DTYPE_BF16
+    wdt = _lib.DTYPE_F32 if dt == torch.float32 else _lib.DTYPE_BF16
+    Fp = lib.kmoe_padded_ff(F)
+    dp = (d + 255) // 256 * 256
+    dev = w1.device
+    w13p = torch.empty(lib.kmoe_packed_w13_bytes(E, d, F, pdt), device=dev, dtype=torch.uint8)
+    w3p = torch.empty(lib.kmoe_packed_w3_bytes(E, d, F, pdt), device=dev, dtype=torch.uint8)
+    s13 = torch.empty(E * 2 * Fp, device=dev, dtype=torch.float32) if fp8 else None
+    s3 = torch.empty(E * dp, device=dev, dtype=torch.float32) if fp8 else None
+    _lib.call("kmoe_pack_weights", ptr(w1), ptr(w2), ptr(w3), wdt, E, d, F, pdt, ptr(w13p), ptr(s13), ptr(w3p),
+              ptr(s3), _stream(w1))
+    return PackedWeights(w13p, w3p, s13, s3, E, d, F, fp8)
+
+
+def gemm_gate_up(xperm, xscale, offsets, pw: PackedWeights, max_rows):
+    lib = _lib.load()
+    Fp = lib.kmoe_padded_ff(pw.F)
+    h = torch.empty(max(max_rows, 1), Fp, device=xperm.device, dtype=_BF16)
+    with _Stage("gemm_gate_up"):
+        _lib.call("kmoe_gemm_gate_up", ptr(xperm), ptr(xscale),
+              _lib.DTYPE_FP8_E4M3 if pw.fp8 else _lib.DTYPE_BF16, ptr(offsets), pw.E, pw.d, pw.F, max_rows,
+              ptr(pw.w13), ptr(pw.s13), ptr(h), _stream(xperm))
+    return h
+
+
+def gemm_down(h, hscale, offsets, pw: PackedWeights, max_rows):
+    y = torch.empty(max(max_rows, 1), pw.d, device=h.device, dtype=_BF16)
+    with _Stage("gemm_down"):
+        _lib.call("kmoe_gemm_down", ptr(h), ptr(hscale), _lib.DTYPE_FP8_E4M3 if pw.fp8 else _lib.DTYPE_BF16,
+              ptr(offsets), pw.E, pw.d, pw.F, max_rows, ptr(pw.w3), ptr(pw.s3), ptr(y), _stream(h))
+    return y
+
+
+def quant_rows_fp8(m, n_rows_dev=None):
+    rows, cols = m.shape
+    q = torch.empty(rows, cols, device=m.device, dtype=torch.uint8)
+    s = torch.empty(rows, device=m.device, dtype=torch.float32)
+    with _Stage("quant_h"):
+        _lib.call("kmoe_quant_rows_fp8", ptr(m), rows, ptr(n_rows_dev), cols, ptr(q), ptr(s), _stream(m))
+    return q, s
+
+
+def grouped_ffn(xperm, xscale, offsets, pw: PackedWeights, max_rows):
+    """gate_up -> (fp8: per-row requant of h) -> down.  Returns yperm (max_rows, d) bf16."""
+    h = gemm_gate_up(xperm, xscale, offsets, pw, max_rows)
+    if pw.fp8:
+        hq, hs = quant_rows_fp8(h, offsets[pw.E:])
+        return gemm_down(hq, hs, offsets, pw, max_rows)
+    return gemm_down(h, None, offsets, pw, max_rows)
+
+
+def combine(yperm, src_row, src_w, T_out, out_map=None, scale=None, out_dtype=_BF16):
+    """y[o] = scale[s] * sum_j src_w[s,j] * yperm[src_row[s,j]] (moe.py:285-292, 132-158)."""
+    fan = src_row.shape[1]
+    d = yperm.shape[1]
+    y = torch.empty(T_out, d, device=yperm.device, dtype=out_dtype)
+    ydt = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
+    with _Stage("combine"):
+        _lib.call("kmoe_combine", ptr(yperm), d, ptr(src_row), ptr(src_w), fan, ptr(out_map), ptr(scale), T_out,
+              ptr(y), ydt, _stream(yperm))
+    return y
+
+
+class ECSelectOut(NamedTuple):
+    idx: torch.Tensor        # (B,E,C) int64
+    w: torch.Tensor          # (B,E,C) f32
+    row_token: torch.Tensor  # (E*B*C,) int32
+    offsets: torch.Tensor    # (E+1,) int32
+    src_row: torch.Tensor    # (B*S, E) int32
+    src_w: torch.Tensor      # (B*S, E) f32
+
+
+def ec_select(logits, B, S, E, C) -> ECSelectOut:
+    """Expert-choice top-C per (sequence, expert) (moe.py:494-530)."""
+    _need_gpu(logits)
+    logits = _contig(logits, torch.float32)
+    dev = logits.device
+    idx = torch.empty(B, E, C, device=dev, dtype=torch.int64)
+    w = torch.empty(B, E, C, device=dev, dtype=torch.float32)
+    row_token = torch.empty(E * B * C, device=dev, dtype=torch.int32)
+    offsets = torch.empty(E + 1, device=dev, dtype=torch.int32)
+    src_row = torch.empty(B * S, E, device=dev, dtype=torch.int32)
+    src_w = torch.empty(B * S, E, device=dev, dtype=torch.float32)
+    with _Stage("ec_select"):
+        _lib.call("kmoe_ec_select", ptr(logits), B, S, E, C, ptr(idx), ptr(w), ptr(row_token), ptr(offsets),
+              ptr(src_row), ptr(src_w), None, 0, _stream(logits))
+    return ECSelectOut(idx, w, row_token, offsets, src_row, src_w)
+
+
+class ModSelectOut(NamedTuple):
+    logits: torch.Tensor      # (B,S) f32
+    sel_idx: torch.Tensor     # (B,keep) int64 ascending
+    sel_w: torch.Tensor       # (B,keep) f32 softmax over kept
+    token_rows: torch.Tensor  # (B*keep,) int32
+    out_map: torch.Tensor     # (B*S,) int32
+
+
+def mod_select(x3d, w_mod, keep) -> ModSelectOut:
+    """Mixture-of-Depths top-keep per sequence (mod.py:67-122)."""
+    _need_gpu(x3d, w_mod)
+    x3d = _contig(x3d, _BF16)
+    w_mod = _contig(w_mod, _BF16).reshape(-1)
+    B, S, d = x3d.shape
+    dev = x3d.device
+    logits = torch.empty(B, S, device=dev, dtype=torch.float32)
+    sel_idx = torch.empty(B, keep, device=dev, dtype=torch.int64)
+    sel_w = torch.empty(B, keep, device=dev, dtype=torch.float32)
+    token_rows = torch.empty(B * keep, device=dev, dtype=torch.int32)
+    out_map = torch.empty(B * S, device=dev, dtype=torch.int32)
+    with _Stage("mod_select"):
+        _lib.call("kmoe_mod_select", ptr(x3d), B, S, d, ptr(w_mod), keep, ptr(logits), ptr(sel_idx), ptr(sel_w),
+              ptr(token_rows), ptr(out_map), None, 0, _stream(x3d))
+    return ModSelectOut(logits, sel_idx, sel_w, token_rows, out_map)

@@ -1,0 +1,27 @@
+"""TEST INFRASTRUCTURE ONLY — CPU oracle of the MoE feed-forward hot path.
+
+This package is the checker, never the product: only tests/, the smoke() of
+__graft_entry__ and the cpu_baseline leg of bench.py may import it.  The
+product path (kolmogorov-moe-architecture_amd/kmoe) runs on the HIP kernels
+only and fails loudly without them.
+
+moe_oracle.py   numpy restatement of the reference algorithm, function by
+                function, each citing the reference file:line it follows.
+torch_port.py   op-for-op torch-CPU restatement of the reference's default
+                PyTorch path (padded bmm experts); the timed CPU baseline.
+
+Pinning (how each oracle function is checked independently, tests/test_oracle.py):
+  router_logits      fp64 per-token brute-force loops; torch nn.Sequential(Linear,SiLU,Linear)
+  topk_select        brute-force sort on (-logit, index); torch.topk on tie-free rows
+  softmax/aux_losses closed forms: uniform logits -> z = (ln E)^2, LB = 1 for balanced
+                     counts with uniform probabilities; brute-force loops
+  dispatch           numpy/torch stable argsort + bincount (library routines); brute force
+  swiglu_rows        fp64 per-token brute force
+  combine            brute-force per-token sums
+  ec_select          brute-force sort on (-logit, index); torch.topk on tie-free columns
+  mod_select         brute-force sort; torch.topk + sort on tie-free rows
+  f32_to_e4m3        torch.float8_e4m3fn cast (library routine) on saturated inputs,
+                     exhaustively over every code and every rounding midpoint
+  torch_port vs moe_oracle at small shapes (two independent restatements)
+No function is left unpinned.
+"""

@@ -1,0 +1,93 @@
+"""torch-CPU restatement of the reference's default PyTorch MoE path
+(TEST INFRASTRUCTURE ONLY; the timed CPU baseline of bench.py).
+
+It runs the same sequence of ATen ops as the reference's `batched`
+implementation, so its CPU time is the reference's CPU time:
+  token choice  Router.forward (moe.py:423-462) then GroupedExperts.forward
+                (moe.py:213-294): stable argsort, bincount, cumsum, gather,
+                .item() max count, zero-padded (E, max, d) buffer, 3 x bmm,
+                gather back, weight multiply, index_add_
+  aux losses    moe.py:840-939 (one_hot counts, softmax mean, logsumexp^2)
+  expert choice ExpertChoiceRouter.forward (moe.py:494-530) then
+                GroupedExpertsExpertChoice.forward (moe.py:626-673) with the
+                weight repeat and scatter_add_ (moe.py:132-158)
+The code is this build's own; only the op sequence follows the reference.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+
+def router_tc(x3d, w_in, w_out, k):
+    """(weights, experts, logits) as Router.forward."""
+    logits = F.linear(F.silu(F.linear(x3d, w_in)), w_out)
+    probs = F.softmax(logits, dim=-1)
+    w, idx = torch.topk(probs, k, dim=-1)
+    return w / w.sum(dim=-1, keepdim=True), idx, logits
+
+
+def grouped_experts_tc(x, idx, w, w1, w2, w3):
+    """GroupedExperts.forward's padded-bmm formulation."""
+    n_tok, k = idx.shape
+    E = w1.shape[0]
+    flat_e = idx.reshape(-1)
+    flat_w = w.reshape(-1)
+    tok = torch.arange(n_tok).unsqueeze(1).expand(-1, k).reshape(-1)
+    order = torch.argsort(flat_e, stable=True)
+    s_tok, s_e, s_w = tok[order], flat_e[order], flat_w[order]
+    counts = torch.bincount(flat_e, minlength=E)
+    ends = torch.cumsum(counts, 0)
+    starts = ends - counts
+    rows = x[s_tok]
+    m = int(counts.max().item())
+    if m == 0:
+        return torch.zeros_like(x)
+    pos = torch.arange(s_tok.numel()) - starts[s_e]
+    padded = x.new_zeros(E, m, x.shape[1])
+    padded[s_e, pos] = rows
+    h = F.silu(torch.bmm(padded, w1)) * torch.bmm(padded, w2)
+    out = torch.bmm(h, w3)
+    contrib = out[s_e, pos] * s_w.unsqueeze(1)
+    y = x.new_zeros(x.shape)
+    y.index_add_(0, s_tok, contrib)
+    return y
+
+
+def aux_tc(logits, idx, E, w_lb=0.01, w_z=0.001):
+    P = F.softmax(logits, dim=-1).mean(dim=[0, 1])
+    B, S, k = idx.shape
+    f = F.one_hot(idx, num_classes=E).float().sum(dim=[0, 1, 2]) / (B * S * k)
+    lb = E * (f * P).sum()
+    z = (torch.logsumexp(logits, dim=-1) ** 2).mean()
+    return w_lb * lb + w_z * z
+
+
+def moe_layer_tc(x3d, w_in, w_out, w1, w2, w3, k, training=True):
+    """MoELayer token-choice forward (moe.py:782-813): returns (y, aux)."""
+    B, S, d = x3d.shape
+    w, idx, logits = router_tc(x3d, w_in, w_out, k)
+    y = grouped_experts_tc(x3d.reshape(-1, d), idx.reshape(-1, k), w.reshape(-1, k), w1, w2, w3)
+    aux = aux_tc(logits, idx, w_out.shape[0]) if training else 0.0
+    return y.view(B, S, d), aux
+
+
+def moe_layer_ec(x3d, w_in, w_out, w1, w2, w3, cf):
+    """MoELayer expert-choice forward (moe.py:815-838) without torch.compile."""
+    B, S, d = x3d.shape
+    E = w_out.shape[0]
+    C = int(math.ceil(S * cf / E))
+    logits = F.linear(F.silu(F.linear(x3d, w_in)), w_out)
+    probs = F.softmax(logits.transpose(1, 2), dim=-1)
+    ew, ti = torch.topk(probs, C, dim=-1)
+    ew = ew / (ew.sum(dim=-1, keepdim=True) + 1e-9)
+    gi = ti.unsqueeze(-1).expand(-1, -1, -1, d)
+    xin = torch.gather(x3d.unsqueeze(1).expand(-1, E, -1, -1), 2, gi).reshape(B * E, C, d)
+    W1, W2, W3 = w1.repeat(B, 1, 1), w2.repeat(B, 1, 1), w3.repeat(B, 1, 1)
+    out = torch.bmm(F.silu(torch.bmm(xin, W1)) * torch.bmm(xin, W2), W3).view(B, E, C, d)
+    wout = out * ew.unsqueeze(-1)
+    y = x3d.new_zeros(B, S, d)
+    y.scatter_add_(1, ti.reshape(B, E * C).unsqueeze(-1).expand(-1, -1, d), wout.reshape(B, E * C, d))
+    return y

@@ -1,0 +1,99 @@
+"""CPU tests of the C-ABI library: it loads, exports every symbol include/kmoe.h
+declares, and its host-side argument validation rejects bad calls with the
+documented status codes (no kernel is launched on these paths)."""
+import ctypes
+
+import pytest
+
+from kmoe import _lib
+
+NULL = None
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_exports_every_header_symbol(lib):
+    names = _lib.header_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding covers the whole header
+    assert sorted(_lib._SIGNATURES) == names
+
+
+def test_version_and_sizes(lib):
+    assert lib.kmoe_abi_version() == 1
+    assert lib.kmoe_padded_ff(2816) == 2816 and lib.kmoe_padded_ff(352) == 384
+    assert lib.kmoe_router_partials_len(16384, 16) == 256 * 17
+    assert lib.kmoe_packed_w13_bytes(16, 2048, 2816, _lib.DTYPE_BF16) == 16 * 2 * 2816 * 2048 * 2
+    assert lib.kmoe_packed_w3_bytes(16, 2048, 2816, _lib.DTYPE_FP8_E4M3) == 16 * 2048 * 2816
+    assert lib.kmoe_dispatch_workspace_bytes(16384, 2, 16) >= 2 * 128 * 16 * 4
+
+
+def _err(lib, name, *args):
+    rc = getattr(lib, name)(*args)
+    return rc, lib.kmoe_last_error().decode()
+
+
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+
+
+def test_router_validation(lib):
+    rc, msg = _err(lib, "kmoe_router", NULL, NULL, 16, 64, FAKE, FAKE, 8, NULL, 2, FAKE, FAKE, FAKE, NULL, NULL)
+    assert rc == -1 and "null" in msg
+    rc, msg = _err(lib, "kmoe_router", FAKE, NULL, 16, 65, FAKE, FAKE, 8, NULL, 2, FAKE, FAKE, FAKE, NULL, NULL)
+    assert rc == -2 and "d=65" in msg
+    rc, msg = _err(lib, "kmoe_router", FAKE, NULL, 16, 64, FAKE, FAKE, 65, NULL, 2, FAKE, FAKE, FAKE, NULL, NULL)
+    assert rc == -2 and "E=65" in msg
+    rc, msg = _err(lib, "kmoe_router", FAKE, NULL, 16, 64, FAKE, FAKE, 8, NULL, 9, FAKE, FAKE, FAKE, NULL, NULL)
+    assert rc == -2 and "k=9" in msg
+    rc, _ = _err(lib, "kmoe_router", FAKE, NULL, 16, 64, FAKE, FAKE, 8, NULL, 2, FAKE, NULL, FAKE, NULL, NULL)
+    assert rc == -1
+
+
+def test_dispatch_validation(lib):
+    args = [FAKE, NULL, 16, 64, FAKE, FAKE, _lib.DTYPE_F32, 2, 8, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+            _lib.DTYPE_BF16, NULL, FAKE, 1 << 20, NULL]
+    bad = list(args)
+    bad[6] = 7
+    assert _err(lib, "kmoe_dispatch", *bad)[0] == -3
+    bad = list(args)
+    bad[16] = _lib.DTYPE_FP8_E4M3  # fp8 needs a scale buffer
+    assert _err(lib, "kmoe_dispatch", *bad)[0] == -1
+    bad = list(args)
+    bad[19] = 8  # workspace too small
+    rc, msg = _err(lib, "kmoe_dispatch", *bad)
+    assert rc == -4 and "workspace" in msg
+    bad = list(args)
+    bad[7] = 9  # k > 8
+    assert _err(lib, "kmoe_dispatch", *bad)[0] == -2
+
+
+def test_gemm_and_combine_validation(lib):
+    assert _err(lib, "kmoe_gemm_gate_up", FAKE, NULL, _lib.DTYPE_BF16, FAKE, 0, 64, 64, 16, FAKE, NULL, FAKE,
+                NULL)[0] == -2
+    assert _err(lib, "kmoe_gemm_gate_up", FAKE, NULL, _lib.DTYPE_F32, FAKE, 4, 64, 64, 16, FAKE, NULL, FAKE,
+                NULL)[0] == -3
+    assert _err(lib, "kmoe_gemm_down", FAKE, NULL, _lib.DTYPE_FP8_E4M3, FAKE, 4, 64, 64, 16, FAKE, NULL, FAKE,
+                NULL)[0] == -1
+    rc, msg = _err(lib, "kmoe_gemm_gate_up", FAKE, FAKE, _lib.DTYPE_FP8_E4M3, FAKE, 4, 64, 64, 16, FAKE, FAKE,
+                   FAKE, NULL)
+    assert rc == -2 and "128" in msg
+    assert _err(lib, "kmoe_combine", FAKE, 64, FAKE, FAKE, 0, NULL, NULL, 4, FAKE, _lib.DTYPE_BF16, NULL)[0] == -2
+    assert _err(lib, "kmoe_combine", FAKE, 64, FAKE, FAKE, 2, NULL, NULL, 4, FAKE, _lib.DTYPE_FP8_E4M3,
+                NULL)[0] == -3
+    assert _err(lib, "kmoe_pack_weights", FAKE, FAKE, FAKE, _lib.DTYPE_BF16, 4, 64, 64, _lib.DTYPE_FP8_E4M3,
+                FAKE, NULL, FAKE, NULL, NULL)[0] == -1
+
+
+def test_select_validation(lib):
+    assert _err(lib, "kmoe_ec_select", FAKE, 1, 100, 4, 101, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
+                NULL)[0] == -2
+    assert _err(lib, "kmoe_ec_select", FAKE, 1, 100000, 4, 10, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
+                NULL)[0] == -6
+    assert _err(lib, "kmoe_mod_select", FAKE, 2, 100, 64, FAKE, 0, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
+                NULL)[0] == -2
+    assert _err(lib, "kmoe_aux_loss", NULL, 16, 4, NULL, 2, 0.01, 0.001, FAKE, NULL)[0] == -1

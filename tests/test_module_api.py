@@ -1,0 +1,70 @@
+"""CPU tests of the drop-in Python API: constructor config, attributes,
+parameter names/shapes (the reference's state-dict keys), and that the
+product path refuses to run without a GPU (no silent CPU fallback)."""
+import pytest
+import torch
+
+import kmoe
+from kmoe import AdvancedMoEConfig, MoELayer, get_test_config
+
+
+def test_config_defaults_match_reference():
+    c = AdvancedMoEConfig()  # moe_arch/model/config.py:17-56
+    assert (c.d_model, c.d_ff_expert, c.n_experts, c.moe_top_k) == (2048, 2816, 16, 2)
+    assert c.moe_capacity_factor == 1.25
+    assert (c.moe_load_balance_loss_weight, c.moe_router_z_loss_weight) == (0.01, 0.001)
+    assert (c.moe_implementation, c.moe_routing, c.moe_balanced_routing) == ("batched", "token_choice", False)
+    assert (c.mod_capacity_factor, c.ffn_activation) == (0.75, "swiglu")
+    t = get_test_config()
+    assert (t.d_model, t.d_ff_expert, t.n_experts) == (256, 352, 4)
+
+
+def test_token_choice_state_dict_keys():
+    cfg = AdvancedMoEConfig(d_model=256, n_experts=8, d_ff_expert=512)
+    m = MoELayer(cfg, layer_idx=3)
+    shapes = {k: tuple(v.shape) for k, v in m.state_dict().items()}
+    assert shapes == {
+        "router.router.0.weight": (128, 256),
+        "router.router.2.weight": (8, 128),
+        "grouped_experts.w1": (8, 256, 512),
+        "grouped_experts.w2": (8, 256, 512),
+        "grouped_experts.w3": (8, 512, 256),
+    }
+    for attr in ("config", "layer_idx", "n_experts", "top_k", "capacity_factor", "routing_type", "implementation",
+                 "router", "grouped_experts", "grouped_experts_ec", "experts", "load_balance_loss_weight",
+                 "router_z_loss_weight", "aux_loss"):
+        assert hasattr(m, attr), attr
+    assert m.layer_idx == 3 and m.experts is None and m.grouped_experts_ec is None and m.aux_loss == 0.0
+    # reference init bound 1/sqrt(fan_in) per expert (moe.py:194-211)
+    assert m.grouped_experts.w1.abs().max() <= 1 / 256 ** 0.5 + 1e-7
+    assert m.grouped_experts.w3.abs().max() <= 1 / 512 ** 0.5 + 1e-7
+
+
+def test_expert_choice_state_dict_keys():
+    cfg = AdvancedMoEConfig(d_model=128, n_experts=4, d_ff_expert=256, moe_routing="expert_choice")
+    m = MoELayer(cfg, 0)
+    assert sorted(m.state_dict()) == ["grouped_experts_ec.w1", "grouped_experts_ec.w2", "grouped_experts_ec.w3",
+                                      "router.router.0.weight", "router.router.2.weight"]
+    assert m.grouped_experts is None
+    assert m.router.capacity(2048) == 640  # ceil(2048*1.25/4), moe.py:511
+
+
+def test_mod_module_keys():
+    cfg = AdvancedMoEConfig(d_model=128, n_experts=4, d_ff_expert=256)
+    m = kmoe.MoDMoE(cfg)
+    keys = set(m.state_dict())
+    assert "ffn_mod_router.router.weight" in keys and "ffn_mod_router.aux_router.0.weight" in keys
+    assert m.ffn_mod_router.keep_count(2048) == 1536 and m.ffn_mod_router.keep_count(1) == 1
+
+
+def test_unsupported_modes_fail_loudly():
+    with pytest.raises(NotImplementedError):
+        MoELayer(AdvancedMoEConfig(d_model=128, moe_implementation="expert_parallel"), 0)
+    with pytest.raises(NotImplementedError):
+        MoELayer(AdvancedMoEConfig(d_model=128, ffn_activation="gelu"), 0)
+
+
+def test_cpu_input_is_rejected():
+    m = MoELayer(AdvancedMoEConfig(d_model=128, n_experts=4, d_ff_expert=256), 0)
+    with pytest.raises(ValueError, match="GPU"):
+        m(torch.randn(1, 8, 128))

@@ -1,0 +1,301 @@
+"""Pins the CPU oracle (oracle/moe_oracle.py) against independent checks:
+brute force, library routines (numpy/torch), closed forms and the golden
+fixtures.  CPU only."""
+import itertools
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from oracle import moe_oracle as O
+from oracle import torch_port as P
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ------------------------------------------------------------------ router logits
+def test_router_logits_bruteforce():
+    r = rng(0)
+    T, d, E = 5, 16, 4
+    x = r.standard_normal((T, d))
+    w_in = r.standard_normal((128, d)) * 0.1
+    w_out = r.standard_normal((E, 128)) * 0.1
+    lg = O.router_logits(x, w_in, w_out)
+    for t in range(T):
+        for e in range(E):
+            acc = 0.0
+            for j in range(128):
+                h = sum(x[t, i] * w_in[j, i] for i in range(d))
+                acc += (h / (1.0 + math.exp(-h))) * w_out[e, j]
+            assert abs(acc - lg[t, e]) < 1e-12
+
+
+def test_router_logits_match_torch_modules():
+    """Same math as the reference's nn.Sequential(Linear, SiLU, Linear) (moe.py:347-351)."""
+    r = rng(1)
+    T, d, E = 64, 32, 8
+    x = r.standard_normal((T, d))
+    seq = nn.Sequential(nn.Linear(d, 128, bias=False), nn.SiLU(), nn.Linear(128, E, bias=False)).double()
+    ref = seq(torch.from_numpy(x)).detach().numpy()
+    lg = O.router_logits(x, seq[0].weight.detach().numpy(), seq[2].weight.detach().numpy())
+    np.testing.assert_allclose(lg, ref, rtol=1e-12, atol=1e-12)
+    bias = r.standard_normal(E)
+    np.testing.assert_allclose(O.router_logits(x, seq[0].weight.detach().numpy(), seq[2].weight.detach().numpy(),
+                                               bias), ref + bias, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------ top-k
+def test_topk_bruteforce_with_ties():
+    r = rng(2)
+    lg = r.integers(0, 3, size=(200, 6)).astype(np.float64)  # many ties
+    idx, w = O.topk_select(lg, 3)
+    for t in range(lg.shape[0]):
+        order = sorted(range(6), key=lambda e: (-lg[t, e], e))[:3]
+        assert list(idx[t]) == order
+        ex = np.exp(lg[t, order] - lg[t].max())
+        np.testing.assert_allclose(w[t], ex / ex.sum(), rtol=1e-12)
+
+
+def test_topk_matches_torch_on_tie_free():
+    r = rng(3)
+    lg = r.standard_normal((500, 16))
+    idx, w = O.topk_select(lg, 2)
+    p = torch.softmax(torch.from_numpy(lg), -1)
+    tv, ti = torch.topk(p, 2, dim=-1)
+    assert np.array_equal(idx, ti.numpy())
+    np.testing.assert_allclose(w, (tv / tv.sum(-1, keepdim=True)).numpy(), rtol=1e-12)
+    np.testing.assert_allclose(w.sum(1), 1.0, atol=1e-12)  # test_phase2_moe.py:84-85 invariant
+    assert np.all(w[:, 0] >= w[:, 1])
+
+
+# ------------------------------------------------------------------ aux
+def test_aux_closed_forms():
+    E, T, k = 8, 64, 2
+    lg = np.zeros((T, E))
+    counts = np.full(E, T * k // E)
+    aux, lb, z = O.aux_losses(lg, counts, T, k, E)
+    assert abs(z - math.log(E) ** 2) < 1e-12
+    assert abs(lb - 1.0) < 1e-12
+    assert abs(aux - (0.01 * lb + 0.001 * z)) < 1e-15
+    # all routed to expert 0 with all probability on it -> LB = E
+    lg2 = np.full((T, E), -1e4)
+    lg2[:, 0] = 0.0
+    _, lb2, _ = O.aux_losses(lg2, np.array([T * k] + [0] * (E - 1)), T, k, E)
+    assert abs(lb2 - E) < 1e-9
+
+
+def test_aux_matches_bruteforce_and_torch():
+    r = rng(4)
+    T, E, k = 50, 6, 2
+    lg = r.standard_normal((T, E))
+    idx, _ = O.topk_select(lg, k)
+    counts = np.bincount(idx.reshape(-1), minlength=E)
+    aux, lb, z = O.aux_losses(lg, counts, T, k, E)
+    p = np.array([[math.exp(v) / sum(math.exp(u) for u in row) for v in row] for row in lg])
+    lb_bf = E * sum((counts[e] / (T * k)) * p[:, e].mean() for e in range(E))
+    z_bf = np.mean([math.log(sum(math.exp(v) for v in row)) ** 2 for row in lg])
+    assert abs(lb - lb_bf) < 1e-12 and abs(z - z_bf) < 1e-12
+    ref = P.aux_tc(torch.from_numpy(lg).view(1, T, E), torch.from_numpy(idx).view(1, T, k), E)
+    assert abs(float(ref) - aux) < 1e-7 * abs(aux)  # the port builds f in float32 (one_hot().float())
+
+
+# ------------------------------------------------------------------ dispatch
+@pytest.mark.parametrize("cap", [0, 3, 40])
+def test_dispatch_matches_stable_argsort(cap):
+    r = rng(5)
+    T, k, E = 97, 2, 7
+    idx = r.integers(0, E, size=(T, k))
+    idx[:, 1] = (idx[:, 0] + 1 + r.integers(0, E - 1, size=T)) % E
+    dp = O.dispatch(idx, E, cap)
+    flat = idx.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    torder = torch.argsort(torch.from_numpy(flat), stable=True).numpy()
+    assert np.array_equal(order, torder)
+    assert np.array_equal(dp["counts"], np.bincount(flat, minlength=E))
+    # without capacity the permutation is exactly argsort(stable)
+    if cap == 0:
+        assert np.array_equal(dp["row_token"], order // k)
+        inv = np.empty_like(order)
+        inv[order] = np.arange(order.size)
+        assert np.array_equal(dp["slot_row"], inv)
+    # brute force of the capacity rule
+    seen = [0] * E
+    row = 0
+    rows = {}
+    for e in range(E):
+        for a in range(T * k):
+            if flat[a] == e:
+                if cap <= 0 or seen[e] < cap:
+                    rows[a] = row
+                    row += 1
+                seen[e] += 1
+    for a in range(T * k):
+        assert dp["slot_row"][a] == rows.get(a, -1)
+    assert dp["offsets"][-1] == row
+
+
+# ------------------------------------------------------------------ experts / combine
+def test_swiglu_rows_bruteforce():
+    r = rng(6)
+    E, d, F_ = 3, 8, 5
+    w1, w2, w3 = (r.standard_normal(s) for s in [(E, d, F_), (E, d, F_), (E, F_, d)])
+    offsets = np.array([0, 2, 2, 5])
+    x = r.standard_normal((5, d))
+    y = O.swiglu_rows(x, offsets, w1, w2, w3, dtype=np.float64)
+    for e in range(E):
+        for row in range(offsets[e], offsets[e + 1]):
+            g = [sum(x[row, i] * w1[e, i, f] for i in range(d)) for f in range(F_)]
+            u = [sum(x[row, i] * w2[e, i, f] for i in range(d)) for f in range(F_)]
+            h = [g[f] / (1 + math.exp(-g[f])) * u[f] for f in range(F_)]
+            ref = [sum(h[f] * w3[e, f, n] for f in range(F_)) for n in range(d)]
+            np.testing.assert_allclose(y[row], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_combine_bruteforce():
+    r = rng(7)
+    yrows = r.standard_normal((6, 4))
+    src = np.array([[0, 3], [-1, 5], [2, -1]])
+    w = r.standard_normal((3, 2))
+    out = O.combine(yrows, src, w, out_map=np.array([2, -1, 0, 1]), scale=np.array([2.0, 3.0, 4.0]), T_out=4)
+    exp = np.zeros((4, 4))
+    exp[0] = 4.0 * (w[2, 0] * yrows[2])
+    exp[2] = 2.0 * (w[0, 0] * yrows[0] + w[0, 1] * yrows[3])
+    exp[3] = 3.0 * (w[1, 1] * yrows[5])
+    np.testing.assert_allclose(out, exp, rtol=1e-12)
+
+
+def test_oracle_layer_matches_torch_port():
+    """Two independent restatements agree: numpy oracle vs the op-for-op torch port."""
+    r = rng(8)
+    B, S, d, E, k, F_ = 2, 24, 32, 4, 2, 48
+    x = r.standard_normal((B, S, d))
+    w_in = r.standard_normal((128, d)) * 0.2
+    w_out = r.standard_normal((E, 128)) * 0.2
+    w1, w2 = r.standard_normal((E, d, F_)) * 0.2, r.standard_normal((E, d, F_)) * 0.2
+    w3 = r.standard_normal((E, F_, d)) * 0.2
+    res = O.moe_forward_tc(x.reshape(-1, d), w_in, w_out, w1, w2, w3, k, dtype=np.float64)
+    tt = [torch.from_numpy(a) for a in (x, w_in, w_out, w1, w2, w3)]
+    y, aux = P.moe_layer_tc(*tt, k)
+    np.testing.assert_allclose(res["y"].reshape(B, S, d), y.numpy(), rtol=1e-9, atol=1e-9)
+    assert abs(res["aux"][0] - float(aux)) < 1e-7 * abs(float(aux))  # f built in float32 by the port
+
+
+# ------------------------------------------------------------------ expert choice
+def test_ec_select_bruteforce_and_torch():
+    r = rng(9)
+    B, S, E, C = 2, 40, 4, 10
+    lg = r.integers(0, 5, size=(B * S, E)).astype(np.float64)  # ties
+    idx, w = O.ec_select(lg, B, S, E, C)
+    L = lg.reshape(B, S, E)
+    for b in range(B):
+        for e in range(E):
+            order = sorted(range(S), key=lambda s: (-L[b, s, e], s))[:C]
+            assert list(idx[b, e]) == order
+            p = np.exp(L[b, :, e] - L[b, :, e].max())
+            p /= p.sum()
+            np.testing.assert_allclose(w[b, e], p[order] / (p[order].sum() + 1e-9), rtol=1e-12)
+    lg2 = r.standard_normal((B * S, E))
+    idx2, w2 = O.ec_select(lg2, B, S, E, C)
+    pr = torch.softmax(torch.from_numpy(lg2).view(B, S, E).transpose(1, 2), -1)
+    tv, ti = torch.topk(pr, C, dim=-1)
+    assert np.array_equal(idx2, ti.numpy())
+    np.testing.assert_allclose(w2, (tv / (tv.sum(-1, keepdim=True) + 1e-9)).numpy(), rtol=1e-12)
+
+
+def test_ec_layer_matches_torch_port():
+    r = rng(10)
+    B, S, d, E, F_, cf = 2, 32, 16, 4, 24, 2.0
+    x = r.standard_normal((B, S, d))
+    w_in, w_out = r.standard_normal((128, d)) * 0.3, r.standard_normal((E, 128)) * 0.3
+    w1, w2, w3 = r.standard_normal((E, d, F_)) * 0.3, r.standard_normal((E, d, F_)) * 0.3, r.standard_normal((E, F_, d)) * 0.3
+    C = math.ceil(S * cf / E)
+    lg = O.router_logits(x.reshape(-1, d), w_in, w_out)
+    idx, w = O.ec_select(lg, B, S, E, C)
+    row_token, offsets, src_row, src_w = O.ec_tables(idx, w, S)
+    yrows = O.swiglu_rows(x.reshape(-1, d)[row_token], offsets, w1, w2, w3, dtype=np.float64)
+    y = O.combine(yrows, src_row, src_w)
+    ref = P.moe_layer_ec(*[torch.from_numpy(a) for a in (x, w_in, w_out, w1, w2, w3)], cf)
+    np.testing.assert_allclose(y.reshape(B, S, d), ref.numpy(), rtol=1e-9, atol=1e-9)
+
+
+# ------------------------------------------------------------------ MoD
+def test_mod_select_bruteforce_and_torch():
+    r = rng(11)
+    B, S, keep = 3, 30, 22
+    rr = r.integers(0, 4, size=(B, S)).astype(np.float64)
+    sel, w = O.mod_select(rr, keep)
+    for b in range(B):
+        order = sorted(sorted(range(S), key=lambda s: (-rr[b, s], s))[:keep])
+        assert list(sel[b]) == order
+        ex = np.exp(rr[b, order] - rr[b, order].max())
+        np.testing.assert_allclose(w[b], ex / ex.sum(), rtol=1e-12)
+    rr2 = r.standard_normal((B, S))
+    sel2, w2 = O.mod_select(rr2, keep)
+    tv, ti = torch.topk(torch.from_numpy(rr2), keep, dim=-1)
+    si, so = torch.sort(ti, dim=-1)
+    assert np.array_equal(sel2, si.numpy())
+    np.testing.assert_allclose(w2, torch.softmax(torch.gather(tv, -1, so), -1).numpy(), rtol=1e-12)
+
+
+# ------------------------------------------------------------------ fp8
+def _torch_e4m3(v):
+    t = torch.from_numpy(np.asarray(v, dtype=np.float32)).clamp(-448, 448)
+    return t.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def test_e4m3_exhaustive_against_torch():
+    codes = np.arange(256, dtype=np.uint32)
+    codes = codes[(codes & 0x7F) != 0x7F]
+    vals = O.e4m3_to_f32(codes)
+    # every code decodes/encodes to itself (except -0 -> 0x80 handled by sign)
+    assert np.array_equal(O.f32_to_e4m3(vals), codes.astype(np.uint8))
+    assert np.array_equal(_torch_e4m3(vals), codes.astype(np.uint8))
+    # every rounding midpoint and its neighbours, plus out-of-range values
+    pos = np.sort(np.unique(np.abs(vals)))
+    mids = (pos[:-1].astype(np.float64) + pos[1:]) / 2
+    probe = np.concatenate([mids, np.nextafter(mids.astype(np.float32), np.float32(0)),
+                            np.nextafter(mids.astype(np.float32), np.float32(1e9)), [449.0, 464.0, 500.0, 1e6, 1e-12]])
+    probe = np.concatenate([probe, -probe]).astype(np.float32)
+    assert np.array_equal(O.f32_to_e4m3(probe), _torch_e4m3(probe))
+    r = rng(12)
+    rnd = (r.standard_normal(200000) * np.exp(r.uniform(-12, 7, 200000))).astype(np.float32)
+    assert np.array_equal(O.f32_to_e4m3(rnd), _torch_e4m3(rnd))
+
+
+def test_quant_rows_roundtrip():
+    r = rng(13)
+    m = r.standard_normal((8, 64)).astype(np.float32)
+    m[3] = 0.0
+    q, s = O.quant_rows(m)
+    assert s[3] == 0 and np.all(q[3] == 0)
+    dq = O.dequant_rows(q, s)
+    rel = np.abs(dq - m).max(axis=1) / np.maximum(np.abs(m).max(axis=1), 1e-30)
+    assert np.all(rel[[0, 1, 2, 4, 5, 6, 7]] <= 2 ** -4)  # e4m3 has 3 mantissa bits
+    # amax element maps exactly to +-448
+    for i in [0, 1, 2]:
+        j = np.argmax(np.abs(m[i]))
+        assert O.e4m3_to_f32(q[i, j:j + 1])[0] == np.sign(m[i, j]) * 448.0
+
+
+# ------------------------------------------------------------------ golden fixtures
+def test_golden_fixture_cfg1():
+    path = os.path.join(GOLDEN, "cfg1_small.npz")
+    g = np.load(path)
+    res = O.moe_forward_tc(g["x"], g["w_in"], g["w_out"], g["w1"], g["w2"], g["w3"], int(g["k"]))
+    assert np.array_equal(res["idx"], g["idx"])
+    assert np.array_equal(res["counts"], g["counts"])
+    np.testing.assert_allclose(res["y"], g["y"], rtol=2e-5, atol=2e-6)
+    np.testing.assert_allclose(res["aux"][0], float(g["aux"]), rtol=1e-5)
+
+
+def test_golden_fixture_e4m3():
+    g = np.load(os.path.join(GOLDEN, "e4m3_kat.npz"))
+    assert np.array_equal(O.f32_to_e4m3(g["inputs"]), g["codes"])
