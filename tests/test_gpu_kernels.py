@@ -226,9 +226,12 @@ def test_grouped_swiglu_fp8(dev):
     qx, sx = O.quant_rows(npf(xb))
     faithful = O.swiglu_rows_fp8(qx, sx, offsets, O.quant_weight_cols(W1), O.quant_weight_cols(W2),
                                  O.quant_weight_cols(W3))
-    assert relL2(npf(y[:A]), faithful) <= 1e-2
+    # bar: the fp32 fake-quant reference (e4m3 casts, per-token / per-row scales)
+    assert relL2(npf(y[:A]), faithful) <= 3e-2
+    assert relL2(npf(y[:A]), faithful) <= 1e-2  # measured well inside the bar
+    # e4m3 (3 mantissa bits) on Gaussian data costs ~6-7% against unquantised fp32
     ref = O.swiglu_rows(npf(xb), offsets, W1, W2, W3)
-    assert relL2(npf(y[:A]), ref) <= 3e-2
+    assert relL2(npf(y[:A]), ref) <= 1e-1
 
 
 # ------------------------------------------------------------------ combine
@@ -243,8 +246,10 @@ def test_combine_parity(dev):
     y = ops.combine(yperm.to(dev), src.to(dev), w.to(dev), T + 100, out_map=out_map.to(dev), scale=scale.to(dev))
     ref = O.combine(npf(yperm), src.numpy(), w.numpy(), out_map=out_map.numpy(), scale=scale.numpy(), T_out=T + 100)
     got = npf(y)
-    ulp = np.abs(ref) * 2.0 ** -8 + 1e-30
-    assert np.all(np.abs(got - ref) <= ulp * 1.01)
+    # one bf16 rounding of the result plus fp32 accumulation error of the terms
+    mag = O.combine(np.abs(npf(yperm)), src.numpy(), np.abs(w.numpy()), out_map=out_map.numpy(),
+                    scale=scale.numpy(), T_out=T + 100)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + mag * 2.0 ** -22)
     yf = ops.combine(yperm.to(dev), src.to(dev), w.to(dev), T + 100, out_map=out_map.to(dev), scale=scale.to(dev),
                      out_dtype=torch.float32)
     np.testing.assert_allclose(npf(yf), ref, rtol=1e-5, atol=1e-6)
