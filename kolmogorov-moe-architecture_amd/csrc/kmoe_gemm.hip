@@ -5,16 +5,21 @@
 //   down:     y[r, n] = h[r] . w3[e][:, n]
 // for the rows r of expert e, [offsets[e], offsets[e+1]).
 //
-// Tiling: a workgroup (4 waves) owns a 256-row x 256-B-row tile; every wave a
-// 128x128 quarter as 4x4 blocks of v_mfma_f32_32x32x16_bf16 (fp8: 32x32x64).
-// K advances 64 bf16 (128 fp8 bytes) per step.  A and B tiles are staged through
-// LDS, double buffered (4 x 32 KiB), rows XOR-swizzled in 16-byte chunks so the
-// MFMA fragment reads are bank-conflict free.  The next step's tiles are loaded
-// into registers while the current step computes.
+// Tiling: a workgroup of 8 waves (2 per SIMD) owns a 256-row x 256-B-row tile;
+// waves form 2 (rows) x 4 (B rows) and each computes 128 x 64 as 4x2 blocks of
+// v_mfma_f32_32x32x16_bf16 (fp8: v_mfma_scale_f32_32x32x64_f8f6f4).  K advances 64
+// bf16 (128 fp8 bytes) per step.  A and B tiles go global -> LDS directly
+// (global_load_lds_dwordx4, no register staging), double buffered (4 x 32 KiB), with
+// 16-byte chunks XOR-swizzled by (row/2)%8 so that the 16 lanes of each LDS read
+// pass hit distinct banks.  Operand fragments are double buffered in registers.
+// The output tile is staged through LDS and written with 16-byte row stores.
 //
-// Ragged groups: the grid is sized for the worst case (ceil(max_rows/256) + E
-// row tiles per column tile); every workgroup maps its id to (expert, row tile)
-// from the device-resident offsets and exits when it has none.  No host sync.
+// Ragged groups: every row tile ("slot") of every expert is enumerated from the
+// device-resident offsets; the grid is sized for the worst case
+// (ceil(max_rows/256) + E slots) and workgroups without a tile exit.  No host sync.
+// Tile order is XCD-aware: workgroups are dispatched round-robin over the 8 XCDs,
+// so consecutive ids of one XCD are given 32-tile super-blocks of 4 slots x 8
+// column tiles, which then share their A and B K-slices in that XCD's L2.
 //
 // Weights are consumed in a packed, derived layout (kmoe_pack_weights):
 //   w13: (E, 2*F_pad, d)   per 128-wide f block: 128 gate rows then 128 up rows,
@@ -28,7 +33,12 @@ constexpr int BM = 256;
 constexpr int BN = 256;       // B rows per tile (gate_up: 128 gate + 128 up)
 constexpr int KBYTES = 128;   // bytes of K per step per row (64 bf16 / 128 fp8)
 constexpr int TILE_BYTES = BM * KBYTES;  // 32 KiB
-constexpr int GEMM_THREADS = 256;
+constexpr int GEMM_THREADS = 512;
+constexpr int NXCD = 8;
+constexpr int SB_TILES = 32;  // tiles per XCD super-block (4 slots x 8 column tiles)
+// output staging: 256 rows x up to 256 bf16 columns, rows padded by 16 bytes
+constexpr int OUT_STRIDE_MAX = 256 * 2 + 16;
+constexpr int LDS_BYTES = (4 * TILE_BYTES > BM * OUT_STRIDE_MAX) ? 4 * TILE_BYTES : BM * OUT_STRIDE_MAX;
 
 __host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 
@@ -52,34 +62,59 @@ __device__ __forceinline__ bool find_row_tile(const int32_t* __restrict__ offset
   return false;
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * KBYTES + ((chunk ^ (row & 7)) << 4); }
+// Workgroup id -> (slot, column tile), XCD-aware (see the file comment).
+__device__ __forceinline__ void map_tile(int L, int n_tiles, int& slot, int& nt) {
+  const int xcd = L % NXCD, i = L / NXCD;
+  const int t = ((i / SB_TILES) * NXCD + xcd) * SB_TILES + (i % SB_TILES);
+  const int per_group = 4 * n_tiles;
+  const int g = t / per_group, r = t - g * per_group;
+  nt = r >> 2;
+  slot = g * 4 + (r & 3);
+}
 
-// Loads one 256 x 128-byte tile (rows clamped to [row_lo, row_hi)) into 8 registers/thread.
-__device__ __forceinline__ void load_tile(const uint8_t* __restrict__ base, int64_t ld_bytes, int row0, int row_clamp,
-                                          int kbyte, int tid, i32x4_t (&reg)[8]) {
-  const int c = tid & 7;
-#pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    int r = row0 + p * 32 + (tid >> 3);
-    r = r < row_clamp ? r : row_clamp - 1;
-    reg[p] = *reinterpret_cast<const i32x4_t*>(base + (int64_t)r * ld_bytes + kbyte + c * 16);
+// Byte offset of 16-byte chunk `chunk` of tile row `row` in an LDS tile.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * KBYTES + ((chunk ^ ((row >> 1) & 7)) << 4); }
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <bool FP8>
+struct Frag;
+template <>
+struct Frag<false> {
+  bf16x8_t v;
+};
+template <>
+struct Frag<true> {
+  i32x8_t v;
+};
+
+// One MFMA operand fragment of K-substep `i` (bf16: 16 of K, chunk 2i+lh; fp8: 64
+// of K, chunks 4i+2lh and 4i+2lh+1) for LDS tile row `r`.
+template <bool FP8>
+__device__ __forceinline__ void read_frag(const uint8_t* l, int r, int i, int lh, Frag<FP8>& f) {
+  if constexpr (!FP8) {
+    f.v = *reinterpret_cast<const bf16x8_t*>(l + swz(r, 2 * i + lh));
+  } else {
+    const int ch = 4 * i + 2 * lh;
+    const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(l + swz(r, ch));
+    const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(l + swz(r, ch + 1));
+    f.v = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
 }
 
-__device__ __forceinline__ void store_tile(uint8_t* lds, int tid, const i32x4_t (&reg)[8]) {
-  const int c = tid & 7;
-#pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const int r = p * 32 + (tid >> 3);
-    *reinterpret_cast<i32x4_t*>(lds + swz(r, c)) = reg[p];
-  }
+template <bool FP8>
+__device__ __forceinline__ void mfma(f32x16_t& acc, const Frag<FP8>& a, const Frag<FP8>& b) {
+  if constexpr (!FP8)
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v, b.v, acc, 0, 0, 0);
+  else
+    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a.v, b.v, acc, 0, 0, 0, 127, 0, 127);
 }
 
-// B-row of the wave's j-th 32-row block.
+// B-tile row of the wave's j-th 32-row block (wn in 0..3, j in 0..1).
 template <bool GATE_UP>
 __device__ __forceinline__ int b_row(int wn, int j, int lr) {
-  if (GATE_UP) return (j < 2 ? 0 : 128) + wn * 64 + (j & 1) * 32 + lr;
-  return wn * 128 + j * 32 + lr;
+  if (GATE_UP) return (j == 0 ? 0 : 128) + wn * 32 + lr;  // gate block, up block
+  return wn * 64 + j * 32 + lr;
 }
 
 // FP8: A/B bytes are e4m3; a_scale per A row, b_scale per B row (global row index).
@@ -89,128 +124,147 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) void grouped_gemm_kernel(
     const int32_t* __restrict__ offsets, int E, const uint8_t* __restrict__ B, int64_t b_expert_rows,
     int64_t ldb_bytes, const float* __restrict__ b_scale, int k_bytes, uint16_t* __restrict__ C, int64_t ldc,
     int n_valid, int n_tiles) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][TILE_BYTES];
-
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+  constexpr int NSUB = FP8 ? 2 : 4;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, lh = lane >> 5;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
 
-  const int slot = blockIdx.x / n_tiles;
-  const int nt = blockIdx.x - slot * n_tiles;
+  int slot, nt;
+  map_tile(blockIdx.x, n_tiles, slot, nt);
   int e, m0, m_end;
   if (!find_row_tile(offsets, E, slot, e, m0, m_end)) return;
 
   const int64_t brow0 = (int64_t)e * b_expert_rows + (int64_t)nt * BN;
-  const uint8_t* Bexp = B + brow0 * ldb_bytes;
+  const uint8_t* ag = A;
+  const uint8_t* bg = B + brow0 * ldb_bytes;
   const int nk = k_bytes / KBYTES;
+  // LDS: [A0 | B0 | A1 | B1], 32 KiB each
+  auto la_buf = [&](int b) { return lds + b * 2 * TILE_BYTES; };
+  auto lb_buf = [&](int b) { return lds + b * 2 * TILE_BYTES + TILE_BYTES; };
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  i32x4_t ra[8], rb[8];
-  load_tile(A, lda_bytes, m0, m_end, 0, tid, ra);
-  load_tile(Bexp, ldb_bytes, 0, BN, 0, tid, rb);
-  store_tile(lds[0][0], tid, ra);
-  store_tile(lds[0][1], tid, rb);
-  __syncthreads();
+  // Direct-to-LDS tile loads: a 256-row x 128-byte tile is 32 wave instructions of
+  // 1 KiB; wave w issues A and B blocks [4w, 4w+4).  Block q fills tile rows
+  // [8q, 8q+8): lane l lands at byte 16*l of the block (row 8q + l/8, physical
+  // chunk l%8) and so fetches logical chunk (l%8)^((row/2)%8) -- the swizzle swz()
+  // reads back.  A rows past the expert's last row are clamped to it (never stored).
+  const int rsub = lane >> 3, pc = lane & 7;
+  uint32_t a_off[4], b_off[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int tr = (wave * 4 + q) * 8 + rsub;
+    int ra = m0 + tr;
+    ra = ra < m_end ? ra : m_end - 1;
+    const uint32_t chunk = (uint32_t)(pc ^ ((tr >> 1) & 7)) << 4;
+    a_off[q] = (uint32_t)ra * (uint32_t)lda_bytes + chunk;
+    b_off[q] = (uint32_t)tr * (uint32_t)ldb_bytes + chunk;
+  }
+  auto issue = [&](uint8_t* adst, uint8_t* bdst) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      __builtin_amdgcn_global_load_lds(ag + a_off[q], (KMOE_LDS void*)(adst + (wave * 4 + q) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      __builtin_amdgcn_global_load_lds(bg + b_off[q], (KMOE_LDS void*)(bdst + (wave * 4 + q) * 1024), 16, 0, 0);
+  };
+  // bf16: fragments double buffered across substeps; fp8 (8-register fragments):
+  // single buffered to stay within 256 registers at 2 waves per SIMD.
+  constexpr int NBUF = FP8 ? 1 : 2;
+  Frag<FP8> fa[NBUF][4], fb[NBUF][2];
+  auto rd = [&](const uint8_t* la, const uint8_t* lb, int i, Frag<FP8> (&a)[4], Frag<FP8> (&b)[2]) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) read_frag<FP8>(la, wm * 128 + mi * 32 + lr, i, lh, a[mi]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) read_frag<FP8>(lb, b_row<GATE_UP>(wn, j, lr), i, lh, b[j]);
+  };
 
+  issue(la_buf(0), lb_buf(0));
+  wait_vmem();
+  __syncthreads();
+  rd(la_buf(0), lb_buf(0), 0, fa[0], fb[0]);
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) {
-      load_tile(A, lda_bytes, m0, m_end, (kt + 1) * KBYTES, tid, ra);
-      load_tile(Bexp, ldb_bytes, 0, BN, (kt + 1) * KBYTES, tid, rb);
+    const bool more = kt + 1 < nk;
+    if (more) {
+      ag += KBYTES;
+      bg += KBYTES;
+      issue(la_buf(cur ^ 1), lb_buf(cur ^ 1));
     }
-    const uint8_t* la = lds[cur][0];
-    const uint8_t* lb = lds[cur][1];
-    if (!FP8) {
-      // 4 K-substeps of 16 bf16; lane half lh reads chunk 2*i + lh
+    const uint8_t* la = la_buf(cur);
+    const uint8_t* lb = lb_buf(cur);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ch = 2 * i + lh;
-        bf16x8_t af[4], bfr[4];
+    for (int i = 0; i < NSUB; ++i) {
+      const int cb = i % NBUF;
+      if (NBUF == 2 && i + 1 < NSUB) rd(la, lb, i + 1, fa[(i + 1) % NBUF], fb[(i + 1) % NBUF]);
+      if (NBUF == 1 && i > 0) rd(la, lb, i, fa[0], fb[0]);
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-          af[mi] = *reinterpret_cast<const bf16x8_t*>(la + swz(wm * 128 + mi * 32 + lr, ch));
+      for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bfr[j] = *reinterpret_cast<const bf16x8_t*>(lb + swz(b_row<GATE_UP>(wn, j, lr), ch));
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bfr[j], acc[mi][j], 0, 0, 0);
-      }
-    } else {
-      // 2 K-substeps of 64 fp8; lane half lh reads chunks 4*i + 2*lh, +1 (32 bytes)
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int ch = 4 * i + 2 * lh;
-        i32x8_t af[4], bfr[4];
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-          const int r = wm * 128 + mi * 32 + lr;
-          const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(la + swz(r, ch));
-          const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(la + swz(r, ch + 1));
-          af[mi] = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = b_row<GATE_UP>(wn, j, lr);
-          const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(lb + swz(r, ch));
-          const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(lb + swz(r, ch + 1));
-          bfr[j] = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[mi][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[mi], bfr[j], acc[mi][j], 0, 0, 0, 127, 0,
-                                                                          127);
-      }
+        for (int j = 0; j < 2; ++j) mfma<FP8>(acc[mi][j], fa[cb][mi], fb[cb][j]);
     }
-    if (kt + 1 < nk) {
-      store_tile(lds[cur ^ 1][0], tid, ra);
-      store_tile(lds[cur ^ 1][1], tid, rb);
+    if (more) {
+      wait_vmem();
+      __syncthreads();
+      rd(la_buf(cur ^ 1), lb_buf(cur ^ 1), 0, fa[0], fb[0]);
     }
-    __syncthreads();
   }
 
-  // ---- epilogue: acc[mi][j][r] is (row 8*(r/4)+4*lh+r%4, col lr) of block (mi, j)
+  // ---- epilogue.  acc[mi][j][r] is (row 8*(r/4)+4*lh+r%4, col lr) of block (mi, j).
+  // Results go to an LDS tile (rows padded by 16 bytes; even lanes store the bf16
+  // pair of lanes lr, lr+1), then out with 16-byte stores along rows.
+  constexpr int NC = GATE_UP ? 128 : 256;   // output columns of the tile
+  constexpr int OSTR = NC * 2 + 16;          // LDS row stride (bytes)
+  __syncthreads();
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-      if (row >= m_end) continue;
-      const float sa = FP8 ? a_scale[row] : 1.0f;
-      uint16_t* crow = C + (int64_t)row * ldc;
-      if (GATE_UP) {
+      const int trow = wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+      const int grow = m0 + trow;
+      const float sa = (FP8 && grow < m_end) ? a_scale[grow] : 1.0f;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int col = nt * 128 + wn * 64 + j * 32 + lr;
-          float g = acc[mi][j][r], u = acc[mi][j + 2][r];
+      for (int jo = 0; jo < (GATE_UP ? 1 : 2); ++jo) {
+        float v;
+        int col;
+        if (GATE_UP) {
+          float g = acc[mi][0][r], u = acc[mi][1][r];
           if (FP8) {
-            g *= sa * b_scale[brow0 + b_row<true>(wn, j, lr)];
-            u *= sa * b_scale[brow0 + b_row<true>(wn, j + 2, lr)];
+            g *= sa * b_scale[brow0 + b_row<true>(wn, 0, lr)];
+            u *= sa * b_scale[brow0 + b_row<true>(wn, 1, lr)];
           }
-          crow[col] = f32_to_bf16(silu_f32(g) * u);
+          v = silu_f32(g) * u;
+          col = wn * 32 + lr;
+        } else {
+          v = acc[mi][jo][r];
+          if (FP8) v *= sa * b_scale[brow0 + b_row<false>(wn, jo, lr)];
+          col = wn * 64 + jo * 32 + lr;
         }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int col = nt * BN + wn * 128 + j * 32 + lr;
-          if (col >= n_valid) continue;
-          float v = acc[mi][j][r];
-          if (FP8) v *= sa * b_scale[brow0 + b_row<false>(wn, j, lr)];
-          crow[col] = f32_to_bf16(v);
-        }
+        const uint32_t bits = f32_to_bf16(v);
+        const uint32_t nb = (uint32_t)__shfl_xor((int)bits, 1, 64);
+        if ((lr & 1) == 0) *reinterpret_cast<uint32_t*>(lds + trow * OSTR + col * 2) = bits | (nb << 16);
       }
     }
+  }
+  __syncthreads();
+  constexpr int CPR = NC * 2 / 16;  // 16-byte chunks per row
+  const int col0 = nt * NC;
+  for (int c = tid; c < BM * CPR; c += GEMM_THREADS) {
+    const int trow = c / CPR, ch = c % CPR;
+    const int grow = m0 + trow;
+    const int gcol = col0 + ch * 8;
+    if (grow < m_end && gcol < n_valid)
+      *reinterpret_cast<i32x4_t*>(C + (int64_t)grow * ldc + gcol) =
+          *reinterpret_cast<const i32x4_t*>(lds + trow * OSTR + ch * 16);
   }
 }
 
@@ -338,7 +392,9 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
                 int n_valid, int n_tiles, hipStream_t s) {
   const int eb = fp8 ? 1 : 2;
   const int64_t slots = kmoe::ceil_div<int64_t>(max_rows, BM) + E;
-  const int64_t blocks = slots * n_tiles;
+  // whole 4-slot groups, whole XCD super-blocks (map_tile covers [0, blocks))
+  const int64_t blocks = kmoe::ceil_div<int64_t>(kmoe::ceil_div<int64_t>(slots, 4) * 4 * n_tiles,
+                                                 (int64_t)NXCD * SB_TILES) * NXCD * SB_TILES;
   if (blocks > 0x7fffffff) {
     kmoe::set_error("kmoe gemm: grid too large");
     return KMOE_ERR_SHAPE;
