@@ -48,36 +48,70 @@ __global__ __launch_bounds__(64 * CROWS) void combine_kernel(const uint16_t* __r
     my_w = src_w[s * fan + lane];
   }
   const uint64_t live = __ballot(my_src >= 0);
-  for (int v0 = 0; v0 < nvec; v0 += 64) {
-    const int v = v0 + lane;
-    float acc[8];
+  // Row vectors in groups of 4 x 64 (one per lane per group); sources in pairs, so
+  // up to 8 16-byte loads are in flight per lane.  Accumulation order is the
+  // source order, as written.
+  for (int v0 = 0; v0 < nvec; v0 += 256) {
+    float acc[4][8];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[u][q] = 0.0f;
     uint64_t m = live;
     while (m) {
-      const int j = __builtin_ctzll(m);
+      const int j0 = __builtin_ctzll(m);
       m &= m - 1;
-      const int r = __shfl(my_src, j, 64);
-      const float w = __shfl(my_w, j, 64);
-      if (v < nvec) {
-        const i32x4_t val = reinterpret_cast<const i32x4_t*>(yperm + (int64_t)r * d)[v];
+      int j1 = -1;
+      if (m) {
+        j1 = __builtin_ctzll(m);
+        m &= m - 1;
+      }
+      const int r0 = __shfl(my_src, j0, 64);
+      const float w0 = __shfl(my_w, j0, 64);
+      const int r1 = __shfl(my_src, j1 < 0 ? j0 : j1, 64);
+      const float w1 = __shfl(my_w, j1 < 0 ? j0 : j1, 64);
+      i32x4_t a[4], b[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          acc[2 * q] = fmaf(w, __uint_as_float(((uint32_t)val[q]) << 16), acc[2 * q]);
-          acc[2 * q + 1] = fmaf(w, __uint_as_float(((uint32_t)val[q]) & 0xffff0000u), acc[2 * q + 1]);
+      for (int u = 0; u < 4; ++u) {
+        const int v = v0 + u * 64 + lane;
+        if (v < nvec) {
+          a[u] = reinterpret_cast<const i32x4_t*>(yperm + (int64_t)r0 * d)[v];
+          if (j1 >= 0) b[u] = reinterpret_cast<const i32x4_t*>(yperm + (int64_t)r1 * d)[v];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int v = v0 + u * 64 + lane;
+        if (v < nvec) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[u][2 * q] = fmaf(w0, __uint_as_float(((uint32_t)a[u][q]) << 16), acc[u][2 * q]);
+            acc[u][2 * q + 1] = fmaf(w0, __uint_as_float(((uint32_t)a[u][q]) & 0xffff0000u), acc[u][2 * q + 1]);
+          }
+          if (j1 >= 0) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              acc[u][2 * q] = fmaf(w1, __uint_as_float(((uint32_t)b[u][q]) << 16), acc[u][2 * q]);
+              acc[u][2 * q + 1] = fmaf(w1, __uint_as_float(((uint32_t)b[u][q]) & 0xffff0000u), acc[u][2 * q + 1]);
+            }
+          }
         }
       }
     }
-    if (v < nvec) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int v = v0 + u * 64 + lane;
+      if (v >= nvec) continue;
       if (OUT_F32) {
         f32x4_t* dst = reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o * d) + 2 * v;
-        dst[0] = f32x4_t{acc[0] * sc, acc[1] * sc, acc[2] * sc, acc[3] * sc};
-        dst[1] = f32x4_t{acc[4] * sc, acc[5] * sc, acc[6] * sc, acc[7] * sc};
+        dst[0] = f32x4_t{acc[u][0] * sc, acc[u][1] * sc, acc[u][2] * sc, acc[u][3] * sc};
+        dst[1] = f32x4_t{acc[u][4] * sc, acc[u][5] * sc, acc[u][6] * sc, acc[u][7] * sc};
       } else {
         i32x4_t out;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          out[q] = (int)((uint32_t)f32_to_bf16(acc[2 * q] * sc) | ((uint32_t)f32_to_bf16(acc[2 * q + 1] * sc) << 16));
+          out[q] = (int)((uint32_t)f32_to_bf16(acc[u][2 * q] * sc) |
+                         ((uint32_t)f32_to_bf16(acc[u][2 * q + 1] * sc) << 16));
         reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(y) + o * d)[v] = out;
       }
     }

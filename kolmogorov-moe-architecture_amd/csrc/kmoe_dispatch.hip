@@ -15,7 +15,7 @@
 
 namespace {
 
-constexpr int DTB = 128;      // tokens per dispatch block
+constexpr int DTB = 64;       // tokens per dispatch block
 constexpr int DTHREADS = 256;
 
 __device__ __forceinline__ int load_expert(const int64_t* idx, int64_t a, int E) {
@@ -39,41 +39,31 @@ __global__ __launch_bounds__(DTHREADS) void hist_kernel(const int64_t* __restric
   if (tid < E) block_counts[(int64_t)blockIdx.x * E + tid] = cnt[tid];
 }
 
-// Single workgroup: for every expert, exclusive scan of block_counts over blocks.
+// Single workgroup of 16 waves: wave w scans experts w, w+16, ... over the blocks
+// (64 blocks per shuffle scan), then thread 0 lays out the expert offsets.
 __global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ block_counts, int64_t nblk, int E,
                                                     int64_t capacity, int32_t* __restrict__ block_base,
                                                     int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
-  __shared__ int wsum[16];
   __shared__ int total[KMOE_MAX_EXPERTS];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6, nwave = blockDim.x >> 6;
-  for (int e = 0; e < E; ++e) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+  for (int e = wave; e < E; e += nwave) {
     int running = 0;
-    for (int64_t b0 = 0; b0 < nblk; b0 += blockDim.x) {
-      const int64_t b = b0 + tid;
+    for (int64_t b0 = 0; b0 < nblk; b0 += 64) {
+      const int64_t b = b0 + lane;
       const int v = b < nblk ? block_counts[b * E + e] : 0;
-      // inclusive wave scan
       int s = v;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
-        int u = __shfl_up(s, o, 64);
+        const int u = __shfl_up(s, o, 64);
         if (lane >= o) s += u;
       }
-      if (lane == 63) wsum[wave] = s;
-      __syncthreads();
-      int before = 0, chunk = 0;
-      for (int w = 0; w < nwave; ++w) {
-        if (w < wave) before += wsum[w];
-        chunk += wsum[w];
-      }
-      if (b < nblk) block_base[b * E + e] = running + before + s - v;
-      running += chunk;
-      __syncthreads();
+      if (b < nblk) block_base[b * E + e] = running + s - v;
+      running += __shfl(s, 63, 64);
     }
-    if (tid == 0) total[e] = running;
+    if (lane == 0) total[e] = running;
   }
   __syncthreads();
-  if (tid == 0) {
+  if (threadIdx.x == 0) {
     int off = 0;
     for (int e = 0; e < E; ++e) {
       const int c = total[e];
@@ -94,7 +84,7 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
     float* __restrict__ xperm_scale) {
   __shared__ int wave_cnt[DTHREADS / 64][KMOE_MAX_EXPERTS];
   __shared__ int running[KMOE_MAX_EXPERTS];
-  __shared__ int dest[DTB * 8];  // k <= 8 handled per chunk below
+  __shared__ int dest[DTB * 8];  // k <= 8
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = (int64_t)blockIdx.x * DTB;
   const int64_t a0 = t0 * k;
@@ -144,22 +134,42 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
     __syncthreads();
   }
 
-  // ---- row gather: one wave per token, row read once, written to its k rows
+  // ---- row gather: every 16-byte chunk of the block's token rows is read once
+  // and written to the token's k permuted rows; 4 chunks in flight per thread.
   const int64_t ntok = min<int64_t>(DTB, T - t0);
   const int nvec = d / 8;  // 16-byte vectors per row
-  for (int64_t tl = wave; tl < ntok; tl += DTHREADS / 64) {
-    const int64_t t = t0 + tl;
-    const int64_t xr = row_index ? (int64_t)row_index[t] : t;
-    const i32x4_t* src = reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d);
-    if (!FP8) {
-      for (int v = lane; v < nvec; v += 64) {
-        const i32x4_t val = src[v];
-        for (int j = 0; j < k; ++j) {
-          const int row = dest[tl * k + j];
-          if (row >= 0) reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(xperm) + (int64_t)row * d)[v] = val;
+  if (!FP8) {
+    const int64_t total = ntok * nvec;
+    for (int64_t c0 = tid; c0 < total; c0 += 4 * DTHREADS) {
+      i32x4_t val[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t c = c0 + (int64_t)u * DTHREADS;
+        if (c < total) {
+          const int64_t tl = c / nvec, v = c - tl * nvec;
+          const int64_t t = t0 + tl;
+          const int64_t xr = row_index ? (int64_t)row_index[t] : t;
+          val[u] = reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d)[v];
         }
       }
-    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t c = c0 + (int64_t)u * DTHREADS;
+        if (c < total) {
+          const int64_t tl = c / nvec, v = c - tl * nvec;
+          for (int j = 0; j < k; ++j) {
+            const int row = dest[tl * k + j];
+            if (row >= 0) reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(xperm) + (int64_t)row * d)[v] = val[u];
+          }
+        }
+      }
+    }
+  } else {
+    // fp8: one wave per token (the per-token amax needs the whole row)
+    for (int64_t tl = wave; tl < ntok; tl += DTHREADS / 64) {
+      const int64_t t = t0 + tl;
+      const int64_t xr = row_index ? (int64_t)row_index[t] : t;
+      const i32x4_t* src = reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d);
       float amax = 0.0f;
       for (int v = lane; v < nvec; v += 64) {
         const i32x4_t val = src[v];

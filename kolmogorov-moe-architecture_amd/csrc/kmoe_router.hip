@@ -2,99 +2,147 @@
 // Follows Router.forward (moe_arch/model/moe.py:423-462) and the loss inputs of
 // MoELayer._compute_load_balance_loss / _compute_router_z_loss (moe.py:872-939).
 //
-// Layout: one workgroup = 2 waves = 64 tokens.  Each wave owns 32 tokens and all
-// 128 hidden units: 4 accumulator blocks of v_mfma_f32_32x32x16_bf16.  Operands are
-// read straight from global memory (x rows and w_in rows are both K-contiguous);
-// within every 64-wide K block lane half h holds elements [32h, 32h+32) of its row,
-// a consistent K permutation for A and B that lets each lane issue 64-byte loads.
-// The hidden activations go through LDS (fp32) for the 128->E layer, which runs on
-// the vector ALUs in fp32; softmax/top-k then run one token per lane.
+// Layout: one workgroup = 4 waves = 64 tokens.  The d -> 128 layer runs on
+// v_mfma_f32_32x32x16_bf16 (each wave: 32 tokens x 64 hidden units) over a 4-stage
+// K pipeline: x rows and w_in rows go global -> LDS directly (global_load_lds), so
+// three K-steps of loads are in flight while one is computed.  The hidden
+// activations go through LDS (fp32) for the 128 -> E layer, computed on the vector
+// ALUs in fp32; softmax/top-k then run one token per thread.
 #include "kmoe_common.h"
 
 namespace {
 
-constexpr int RT_TOK = 64;       // tokens per workgroup
+constexpr int RT_TOK = 64;        // tokens per workgroup
+constexpr int RT_THREADS = 256;   // 4 waves: 2 (token halves) x 2 (hidden halves)
 constexpr int RT_HID = KMOE_ROUTER_HIDDEN;
 constexpr int HSTR = RT_HID + 1;  // padded LDS row stride (floats) of the hidden tile
+constexpr int RT_STAGES = 4;      // K pipeline depth (3 K-steps of loads in flight)
+constexpr int RT_XT = RT_TOK * 128;   // x tile of one K-step: 64 rows x 128 bytes (64 bf16)
+constexpr int RT_WT = RT_HID * 128;   // w_in tile of one K-step: 128 rows x 128 bytes
+constexpr int RT_STAGE = RT_XT + RT_WT;
+constexpr int RT_LOADS = 6;       // direct-to-LDS instructions per wave and K-step (2 x + 4 w_in)
+
+// Byte offset of 16-byte chunk `chunk` of row `row` in a 128-byte-row tile; the
+// XOR by (row/2)%8 spreads the 16 lanes of each LDS read pass over distinct banks.
+__device__ __forceinline__ int rswz(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 template <int NE>
-__global__ __launch_bounds__(128) void router_kernel(const uint16_t* __restrict__ x,
-                                                     const int32_t* __restrict__ row_index, int64_t T,
-                                                     int d, const uint16_t* __restrict__ w_in,
-                                                     const uint16_t* __restrict__ w_out, int E,
-                                                     const float* __restrict__ bias, int k,
-                                                     float* __restrict__ logits, int64_t* __restrict__ topk_idx,
-                                                     float* __restrict__ topk_w, float* __restrict__ partials) {
-  __shared__ float hs[2][32 * HSTR];     // SiLU(hidden) per wave, fp32
-  __shared__ float wo[NE * RT_HID];      // w_out as fp32
-  __shared__ float lg[2][32][NE + 1];    // logits per wave
-  __shared__ float pe[RT_TOK][NE + 1];   // softmax probabilities (aux partials)
-  __shared__ float lse2[RT_TOK];
+__global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __restrict__ x,
+                                                            const int32_t* __restrict__ row_index, int64_t T, int d,
+                                                            const uint16_t* __restrict__ w_in,
+                                                            const uint16_t* __restrict__ w_out, int E,
+                                                            const float* __restrict__ bias, int k,
+                                                            float* __restrict__ logits, int64_t* __restrict__ topk_idx,
+                                                            float* __restrict__ topk_w, float* __restrict__ partials) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[RT_STAGES * RT_STAGE];
+  __shared__ float wo[NE * RT_HID];  // w_out as fp32
+  // after the K loop smem holds: hs[64][HSTR], lg[64][NE+1], pe[64][NE+1], lse2[64]
+  float* hs = reinterpret_cast<float*>(smem);
+  float* lg = hs + RT_TOK * HSTR;
+  float* pe = lg + RT_TOK * (NE + 1);
+  float* lse2 = pe + RT_TOK * (NE + 1);
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int lr = lane & 31;
-  const int lh = lane >> 5;
-  const int64_t tok0 = (int64_t)blockIdx.x * RT_TOK + wave * 32;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int64_t tok0 = (int64_t)blockIdx.x * RT_TOK;
 
-  for (int i = tid; i < NE * RT_HID; i += blockDim.x) {
-    int e = i / RT_HID;
+  for (int i = tid; i < NE * RT_HID; i += RT_THREADS) {
+    const int e = i / RT_HID;
     wo[i] = e < E ? bf16_to_f32(w_out[i]) : 0.0f;
   }
 
-  // ---- layer 1 on MFMA: 32 tokens x 128 hidden, K = d
-  int64_t t_a = tok0 + lr;
-  if (t_a >= T) t_a = T - 1;
-  const int64_t xrow = row_index ? (int64_t)row_index[t_a] : t_a;
-  const uint16_t* ap = x + xrow * (int64_t)d + 32 * lh;
-  const uint16_t* bp[4];
+  // ---- per-lane sources of the direct-to-LDS loads (block q fills tile rows
+  // [8q, 8q+8), lane l lands at byte 16*l of the block: row 8q + l/8, physical
+  // chunk l%8, holding logical chunk (l%8) ^ ((row/2)%8))
+  const int rsub = lane >> 3, pc = lane & 7;
+  const uint8_t* xsrc[2];
+  uint32_t wsrc[4];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) bp[nb] = w_in + (int64_t)(nb * 32 + lr) * d + 32 * lh;
-
-  f32x16_t acc[4];
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
-
-  for (int k0 = 0; k0 < d; k0 += 64) {
-    bf16x8_t a[4], b[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const bf16x8_t*>(ap + k0 + 8 * i);
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) b[nb][i] = *reinterpret_cast<const bf16x8_t*>(bp[nb] + k0 + 8 * i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[nb][i], acc[nb], 0, 0, 0);
+  for (int q = 0; q < 2; ++q) {
+    const int tr = (wave * 2 + q) * 8 + rsub;
+    int64_t t = tok0 + tr;
+    t = t < T ? t : T - 1;
+    const int64_t xr = row_index ? (int64_t)row_index[t] : t;
+    xsrc[q] = reinterpret_cast<const uint8_t*>(x) + xr * (int64_t)d * 2 + ((pc ^ ((tr >> 1) & 7)) << 4);
   }
-
-  // SiLU, then to LDS: acc[nb][r] holds hidden nb*32+lr of token 8*(r/4)+4*lh+(r%4)
-  float* h = hs[wave];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
+  for (int q = 0; q < 4; ++q) {
+    const int tr = (wave * 4 + q) * 8 + rsub;
+    wsrc[q] = (uint32_t)tr * (uint32_t)d * 2u + ((pc ^ ((tr >> 1) & 7)) << 4);
+  }
+  const uint8_t* wbase = reinterpret_cast<const uint8_t*>(w_in);
+  auto issue = [&](int kt) {
+    uint8_t* st = smem + (kt % RT_STAGES) * RT_STAGE;
+    const int kb = kt * 128;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      __builtin_amdgcn_global_load_lds(xsrc[q] + kb, (KMOE_LDS void*)(st + (wave * 2 + q) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      __builtin_amdgcn_global_load_lds(wbase + wsrc[q] + kb, (KMOE_LDS void*)(st + RT_XT + (wave * 4 + q) * 1024), 16,
+                                       0, 0);
+  };
+
+  // ---- layer 1 on MFMA: wave (wm, wn) computes 32 tokens x 64 hidden
+  f32x16_t acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+  const int nk = d / 64;
+  for (int s = 0; s < RT_STAGES - 1 && s < nk; ++s) issue(s);
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + RT_STAGES - 2 < nk)
+      wait_vmcnt<(RT_STAGES - 2) * RT_LOADS>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
+    if (kt + RT_STAGES - 1 < nk) issue(kt + RT_STAGES - 1);
+    const uint8_t* xt = smem + (kt % RT_STAGES) * RT_STAGE;
+    const uint8_t* wt = xt + RT_XT;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ch = 2 * i + lh;
+      const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(xt + rswz(wm * 32 + lr, ch));
+      const bf16x8_t b0 = *reinterpret_cast<const bf16x8_t*>(wt + rswz(wn * 64 + lr, ch));
+      const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(wt + rswz(wn * 64 + 32 + lr, ch));
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b0, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b1, acc[1], 0, 0, 0);
+    }
+  }
+  __syncthreads();  // stage buffers are reused below
+
+  // SiLU, then to LDS: acc[j][r] is hidden wn*64+j*32+lr of token wm*32+8*(r/4)+4*lh+r%4
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      int m = 8 * (r >> 2) + 4 * lh + (r & 3);
-      h[m * HSTR + nb * 32 + lr] = silu_f32(acc[nb][r]);
+      const int m = wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+      hs[m * HSTR + wn * 64 + j * 32 + lr] = silu_f32(acc[j][r]);
     }
   __syncthreads();
 
-  // ---- layer 2 (fp32 FMA): lane (lr, lh) computes experts e = 2q + lh of token lr
+  // ---- layer 2 (fp32 FMA): thread (token t>>2, part t&3) computes experts part+4q
   {
-    float l2[NE / 2];
+    const int tl = tid >> 2, part = tid & 3;
+    float l2[NE / 4];
 #pragma unroll
-    for (int q = 0; q < NE / 2; ++q) l2[q] = 0.0f;
-    const float* hrow = h + lr * HSTR;
+    for (int q = 0; q < NE / 4; ++q) l2[q] = 0.0f;
+    const float* hrow = hs + tl * HSTR;
 #pragma unroll 4
     for (int j = 0; j < RT_HID; j += 4) {
-      float h0 = hrow[j], h1 = hrow[j + 1], h2 = hrow[j + 2], h3 = hrow[j + 3];
+      const float h0 = hrow[j], h1 = hrow[j + 1], h2 = hrow[j + 2], h3 = hrow[j + 3];
 #pragma unroll
-      for (int q = 0; q < NE / 2; ++q) {
-        const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(&wo[(2 * q + lh) * RT_HID + j]);
+      for (int q = 0; q < NE / 4; ++q) {
+        const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(&wo[(part + 4 * q) * RT_HID + j]);
         l2[q] = fmaf(h0, wv[0], l2[q]);
         l2[q] = fmaf(h1, wv[1], l2[q]);
         l2[q] = fmaf(h2, wv[2], l2[q]);
@@ -102,18 +150,18 @@ __global__ __launch_bounds__(128) void router_kernel(const uint16_t* __restrict_
       }
     }
 #pragma unroll
-    for (int q = 0; q < NE / 2; ++q) {
-      int e = 2 * q + lh;
-      if (e < E) lg[wave][lr][e] = l2[q] + (bias ? bias[e] : 0.0f);
+    for (int q = 0; q < NE / 4; ++q) {
+      const int e = part + 4 * q;
+      if (e < E) lg[tl * (NE + 1) + e] = l2[q] + (bias ? bias[e] : 0.0f);
     }
   }
   __syncthreads();
 
-  // ---- softmax, top-k, outputs: one token per lane (lanes 0..31 of each wave)
-  if (lh == 0) {
-    const int64_t t = tok0 + lr;
-    const float* L = lg[wave][lr];
-    const int tl = wave * 32 + lr;
+  // ---- softmax, top-k, outputs: one token per thread (threads 0..63)
+  if (tid < RT_TOK) {
+    const int64_t t = tok0 + tid;
+    const float* L = lg + tid * (NE + 1);
+    float* P = pe + tid * (NE + 1);
     if (t < T) {
       float mx = L[0];
       for (int e = 1; e < E; ++e) mx = fmaxf(mx, L[e]);
@@ -124,9 +172,9 @@ __global__ __launch_bounds__(128) void router_kernel(const uint16_t* __restrict_
       float* lout = logits + t * E;
       for (int e = 0; e < E; ++e) {
         lout[e] = L[e];
-        pe[tl][e] = __expf(L[e] - mx) * inv_s;
+        P[e] = __expf(L[e] - mx) * inv_s;
       }
-      lse2[tl] = lse * lse;
+      lse2[tid] = lse * lse;
       if (k > 0) {
         // Two identical selection passes (sum of the selected exps, then the
         // outputs) keep everything in registers.
@@ -157,8 +205,8 @@ __global__ __launch_bounds__(128) void router_kernel(const uint16_t* __restrict_
         }
       }
     } else {
-      for (int e = 0; e < E; ++e) pe[tl][e] = 0.0f;
-      lse2[tl] = 0.0f;
+      for (int e = 0; e < E; ++e) P[e] = 0.0f;
+      lse2[tid] = 0.0f;
     }
   }
   __syncthreads();
@@ -168,7 +216,7 @@ __global__ __launch_bounds__(128) void router_kernel(const uint16_t* __restrict_
     float* pb = partials + (int64_t)blockIdx.x * (E + 1);
     if (tid < E) {
       float s = 0.0f;
-      for (int i = 0; i < RT_TOK; ++i) s += pe[i][tid];
+      for (int i = 0; i < RT_TOK; ++i) s += pe[i * (NE + 1) + tid];
       pb[tid] = s;
     } else if (tid == E) {
       float s = 0.0f;
@@ -178,18 +226,22 @@ __global__ __launch_bounds__(128) void router_kernel(const uint16_t* __restrict_
   }
 }
 
-__global__ void aux_loss_kernel(const float* __restrict__ partials, int64_t nblk, int64_t T, int E,
-                                const int32_t* __restrict__ counts, int k, float w_lb, float w_z,
-                                float* __restrict__ out) {
+// One workgroup, 4 waves: wave w reduces partial columns w, w+4, ...; lane l sums
+// blocks l, l+64, ... and the wave then sums its lanes with a fixed shuffle tree, so
+// the result is bit-reproducible.
+__global__ __launch_bounds__(256) void aux_loss_kernel(const float* __restrict__ partials, int64_t nblk, int64_t T,
+                                                       int E, const int32_t* __restrict__ counts, int k, float w_lb,
+                                                       float w_z, float* __restrict__ out) {
   __shared__ float col[KMOE_MAX_EXPERTS + 1];
-  const int tid = threadIdx.x;
-  if (tid <= E) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int c = wave; c <= E; c += 4) {
     float s = 0.0f;
-    for (int64_t b = 0; b < nblk; ++b) s += partials[b * (E + 1) + tid];
-    col[tid] = s;
+    for (int64_t b = lane; b < nblk; b += 64) s += partials[b * (E + 1) + c];
+    s = wave_sum(s);
+    if (lane == 0) col[c] = s;
   }
   __syncthreads();
-  if (tid == 0) {
+  if (threadIdx.x == 0) {
     const float invT = 1.0f / (float)T;
     float lb = 0.0f;
     if (counts) {
@@ -228,7 +280,7 @@ extern "C" int kmoe_router(const void* x, const int32_t* row_index, int64_t T, i
   const uint16_t* wi = static_cast<const uint16_t*>(w_in);
   const uint16_t* wo = static_cast<const uint16_t*>(w_out);
 #define KMOE_ROUTER_LAUNCH(NE_)                                                                          \
-  hipLaunchKernelGGL(router_kernel<NE_>, grid, dim3(128), 0, s, xp, row_index, T, d, wi, wo, E, logit_bias, k, \
+  hipLaunchKernelGGL(router_kernel<NE_>, grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, wo, E, logit_bias, k, \
                      logits, topk_idx, topk_w, partials)
   if (E <= 8)
     KMOE_ROUTER_LAUNCH(8);
@@ -249,7 +301,7 @@ extern "C" int kmoe_aux_loss(const float* partials, int64_t T, int E, const int3
   KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_aux_loss: E=%d out of range", E);
   KMOE_REQUIRE(!counts || k >= 1, KMOE_ERR_SHAPE, "kmoe_aux_loss: k must be >= 1 with counts");
   const int64_t nblk = kmoe::ceil_div<int64_t>(T, RT_TOK);
-  hipLaunchKernelGGL(aux_loss_kernel, dim3(1), dim3(128), 0, kmoe::as_stream(stream), partials, nblk, T, E,
+  hipLaunchKernelGGL(aux_loss_kernel, dim3(1), dim3(256), 0, kmoe::as_stream(stream), partials, nblk, T, E,
                      counts, k, w_lb, w_z, out);
   return kmoe::check_launch("kmoe_aux_loss");
 }
