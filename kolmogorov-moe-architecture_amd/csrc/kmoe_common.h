@@ -85,6 +85,23 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
   return s ? -v : v;
 }
 
+// Workgroup barrier without a memory fence.  __syncthreads() also waits for every
+// outstanding global load (vmcnt(0)), which would drain in-flight prefetches of
+// direct-to-LDS pipelines; callers wait explicitly for what they need (vmcnt(N)
+// for their own tile loads, lgkmcnt(0) after LDS writes) before calling this.
+__device__ __forceinline__ void barrier_nofence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 // Wave-level reductions (64 lanes).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

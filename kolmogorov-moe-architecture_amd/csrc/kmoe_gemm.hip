@@ -25,20 +25,50 @@
 //   w13: (E, 2*F_pad, d)   per 128-wide f block: 128 gate rows then 128 up rows,
 //                          each row K(=d)-contiguous (w1/w2 transposed)
 //   w3 : (E, d_pad, F_pad) row n K(=f)-contiguous (w3 transposed), d_pad = round_up(d, 256)
+// Every packed row is followed by WPAD bytes of padding: with power-of-two row
+// strides the 256 rows of a tile K-slice would all map to the same memory
+// channels; the pad spreads them (measured: +20% on the gate/up GEMM).
 #include "kmoe_common.h"
 
 namespace {
 
 constexpr int BM = 256;
 constexpr int BN = 256;       // B rows per tile (gate_up: 128 gate + 128 up)
-constexpr int KBYTES = 128;   // bytes of K per step per row (64 bf16 / 128 fp8)
-constexpr int TILE_BYTES = BM * KBYTES;  // 32 KiB
 constexpr int GEMM_THREADS = 512;
+constexpr int WPAD = 128;     // bytes of padding after every packed weight row
 constexpr int NXCD = 8;
 constexpr int SB_TILES = 32;  // tiles per XCD super-block (4 slots x 8 column tiles)
 // output staging: 256 rows x up to 256 bf16 columns, rows padded by 16 bytes
 constexpr int OUT_STRIDE_MAX = 256 * 2 + 16;
-constexpr int LDS_BYTES = (4 * TILE_BYTES > BM * OUT_STRIDE_MAX) ? 4 * TILE_BYTES : BM * OUT_STRIDE_MAX;
+
+// K pipeline configuration: KB bytes of K per row per step (128 = 64 bf16, 64 = 32
+// bf16), NST LDS stages (NST-1 steps of loads in flight).
+template <int KB, int NST>
+struct Pipe {
+  static constexpr int TB = BM * KB;                       // bytes of one A or B stage tile
+  static constexpr int CPR = KB / 16;                      // 16-byte chunks per row
+  static constexpr int RPB = 1024 / KB;                    // rows per 1 KiB load block
+  static constexpr int RS = (KB == 128) ? 1 : 2;           // swizzle row shift (256/KB = 2^RS)
+  static constexpr int BLK_PER_WAVE = (BM / RPB) / 8;      // load blocks per wave per tile
+  static constexpr int LOADS = 2 * BLK_PER_WAVE;           // A + B load instructions per wave per step
+  static constexpr int LDS = (NST * 2 * TB > BM * OUT_STRIDE_MAX) ? NST * 2 * TB : BM * OUT_STRIDE_MAX;
+  // Byte offset of 16-byte chunk `chunk` of row `row`: XOR by (row >> RS) spreads
+  // the 16 lanes of each LDS read pass (16 consecutive rows) over distinct banks.
+  __device__ static __forceinline__ int swz(int row, int chunk) {
+    return row * KB + ((chunk ^ ((row >> RS) & (CPR - 1))) << 4);
+  }
+};
+
+// K-pipeline configuration of the shipped kernels (bytes of K per step, stages).
+#ifndef KMOE_GEMM_KB
+#define KMOE_GEMM_KB 128
+#endif
+#ifndef KMOE_GEMM_NST
+#define KMOE_GEMM_NST 2
+#endif
+// Static LDS of the kernel (a dependent array size would keep the host-side
+// launch stub from being emitted).
+constexpr int GEMM_LDS = Pipe<KMOE_GEMM_KB, KMOE_GEMM_NST>::LDS;
 
 __host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 
@@ -72,11 +102,6 @@ __device__ __forceinline__ void map_tile(int L, int n_tiles, int& slot, int& nt)
   slot = g * 4 + (r & 3);
 }
 
-// Byte offset of 16-byte chunk `chunk` of tile row `row` in an LDS tile.
-__device__ __forceinline__ int swz(int row, int chunk) { return row * KBYTES + ((chunk ^ ((row >> 1) & 7)) << 4); }
-
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
 template <bool FP8>
 struct Frag;
 template <>
@@ -90,14 +115,14 @@ struct Frag<true> {
 
 // One MFMA operand fragment of K-substep `i` (bf16: 16 of K, chunk 2i+lh; fp8: 64
 // of K, chunks 4i+2lh and 4i+2lh+1) for LDS tile row `r`.
-template <bool FP8>
+template <class P, bool FP8>
 __device__ __forceinline__ void read_frag(const uint8_t* l, int r, int i, int lh, Frag<FP8>& f) {
   if constexpr (!FP8) {
-    f.v = *reinterpret_cast<const bf16x8_t*>(l + swz(r, 2 * i + lh));
+    f.v = *reinterpret_cast<const bf16x8_t*>(l + P::swz(r, 2 * i + lh));
   } else {
     const int ch = 4 * i + 2 * lh;
-    const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(l + swz(r, ch));
-    const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(l + swz(r, ch + 1));
+    const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(l + P::swz(r, ch));
+    const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(l + P::swz(r, ch + 1));
     f.v = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
 }
@@ -118,14 +143,16 @@ __device__ __forceinline__ int b_row(int wn, int j, int lr) {
 }
 
 // FP8: A/B bytes are e4m3; a_scale per A row, b_scale per B row (global row index).
-template <bool GATE_UP, bool FP8>
+template <bool GATE_UP, bool FP8, int KB, int NST>
 __global__ __launch_bounds__(GEMM_THREADS, 1) void grouped_gemm_kernel(
     const uint8_t* __restrict__ A, int64_t lda_bytes, const float* __restrict__ a_scale,
     const int32_t* __restrict__ offsets, int E, const uint8_t* __restrict__ B, int64_t b_expert_rows,
     int64_t ldb_bytes, const float* __restrict__ b_scale, int k_bytes, uint16_t* __restrict__ C, int64_t ldc,
     int n_valid, int n_tiles) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
-  constexpr int NSUB = FP8 ? 2 : 4;
+  using P = Pipe<KB, NST>;
+  static_assert(P::LDS <= GEMM_LDS, "LDS budget of this pipeline configuration");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[GEMM_LDS];
+  constexpr int NSUB = FP8 ? KB / 64 : KB / 32;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -138,12 +165,11 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) void grouped_gemm_kernel(
   if (!find_row_tile(offsets, E, slot, e, m0, m_end)) return;
 
   const int64_t brow0 = (int64_t)e * b_expert_rows + (int64_t)nt * BN;
-  const uint8_t* ag = A;
-  const uint8_t* bg = B + brow0 * ldb_bytes;
-  const int nk = k_bytes / KBYTES;
-  // LDS: [A0 | B0 | A1 | B1], 32 KiB each
-  auto la_buf = [&](int b) { return lds + b * 2 * TILE_BYTES; };
-  auto lb_buf = [&](int b) { return lds + b * 2 * TILE_BYTES + TILE_BYTES; };
+  const uint8_t* bexp = B + brow0 * ldb_bytes;
+  const int nk = k_bytes / KB;
+  // LDS stage s: [A tile | B tile]
+  auto la_buf = [&](int st) { return lds + st * 2 * P::TB; };
+  auto lb_buf = [&](int st) { return lds + st * 2 * P::TB + P::TB; };
 
   f32x16_t acc[4][2];
 #pragma unroll
@@ -153,55 +179,60 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) void grouped_gemm_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // Direct-to-LDS tile loads: a 256-row x 128-byte tile is 32 wave instructions of
-  // 1 KiB; wave w issues A and B blocks [4w, 4w+4).  Block q fills tile rows
-  // [8q, 8q+8): lane l lands at byte 16*l of the block (row 8q + l/8, physical
-  // chunk l%8) and so fetches logical chunk (l%8)^((row/2)%8) -- the swizzle swz()
-  // reads back.  A rows past the expert's last row are clamped to it (never stored).
-  const int rsub = lane >> 3, pc = lane & 7;
-  uint32_t a_off[4], b_off[4];
+  // Direct-to-LDS tile loads: a 256-row tile is 256*KB/1024 blocks of 1 KiB; wave w
+  // issues A and B blocks [w*BPW, (w+1)*BPW).  Block q fills tile rows [q*RPB,
+  // (q+1)*RPB): lane l lands at byte 16*l of the block (row q*RPB + l/CPR, physical
+  // chunk l%CPR) and so fetches the logical chunk that swz() maps there.  A rows
+  // past the expert's last row are clamped to it (their results are never stored).
+  constexpr int BPW = P::BLK_PER_WAVE;
+  const int rsub = lane / P::CPR, pc = lane % P::CPR;
+  static_assert(BPW <= 4, "load blocks per wave");
+  uint32_t a_off[4], b_off[4];  // fixed size: a dependent array size drops the host launch stub
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int tr = (wave * 4 + q) * 8 + rsub;
+  for (int q = 0; q < BPW; ++q) {
+    const int tr = (wave * BPW + q) * P::RPB + rsub;
     int ra = m0 + tr;
     ra = ra < m_end ? ra : m_end - 1;
-    const uint32_t chunk = (uint32_t)(pc ^ ((tr >> 1) & 7)) << 4;
+    const uint32_t chunk = (uint32_t)(pc ^ ((tr >> P::RS) & (P::CPR - 1))) << 4;
     a_off[q] = (uint32_t)ra * (uint32_t)lda_bytes + chunk;
     b_off[q] = (uint32_t)tr * (uint32_t)ldb_bytes + chunk;
   }
-  auto issue = [&](uint8_t* adst, uint8_t* bdst) {
+  auto issue = [&](int kt) {
+    uint8_t* adst = la_buf(kt % NST);
+    uint8_t* bdst = lb_buf(kt % NST);
+    const uint8_t* ag = A + (int64_t)kt * KB;
+    const uint8_t* bg = bexp + (int64_t)kt * KB;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      __builtin_amdgcn_global_load_lds(ag + a_off[q], (KMOE_LDS void*)(adst + (wave * 4 + q) * 1024), 16, 0, 0);
+    for (int q = 0; q < BPW; ++q)
+      __builtin_amdgcn_global_load_lds(ag + a_off[q], (KMOE_LDS void*)(adst + (wave * BPW + q) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      __builtin_amdgcn_global_load_lds(bg + b_off[q], (KMOE_LDS void*)(bdst + (wave * 4 + q) * 1024), 16, 0, 0);
+    for (int q = 0; q < BPW; ++q)
+      __builtin_amdgcn_global_load_lds(bg + b_off[q], (KMOE_LDS void*)(bdst + (wave * BPW + q) * 1024), 16, 0, 0);
   };
   // bf16: fragments double buffered across substeps; fp8 (8-register fragments):
   // single buffered to stay within 256 registers at 2 waves per SIMD.
-  constexpr int NBUF = FP8 ? 1 : 2;
+  constexpr int NBUF = (FP8 || NSUB == 1) ? 1 : 2;
   Frag<FP8> fa[NBUF][4], fb[NBUF][2];
   auto rd = [&](const uint8_t* la, const uint8_t* lb, int i, Frag<FP8> (&a)[4], Frag<FP8> (&b)[2]) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) read_frag<FP8>(la, wm * 128 + mi * 32 + lr, i, lh, a[mi]);
+    for (int mi = 0; mi < 4; ++mi) read_frag<P, FP8>(la, wm * 128 + mi * 32 + lr, i, lh, a[mi]);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) read_frag<FP8>(lb, b_row<GATE_UP>(wn, j, lr), i, lh, b[j]);
+    for (int j = 0; j < 2; ++j) read_frag<P, FP8>(lb, b_row<GATE_UP>(wn, j, lr), i, lh, b[j]);
   };
 
-  issue(la_buf(0), lb_buf(0));
-  wait_vmem();
-  __syncthreads();
-  rd(la_buf(0), lb_buf(0), 0, fa[0], fb[0]);
+  // NST-stage pipeline: stage kt is waited for (own loads by vmcnt, everyone's by the
+  // barrier), then the loads of step kt+NST-1 go into the buffer freed by step kt-1.
+  for (int st = 0; st < NST - 1 && st < nk; ++st) issue(st);
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      ag += KBYTES;
-      bg += KBYTES;
-      issue(la_buf(cur ^ 1), lb_buf(cur ^ 1));
-    }
-    const uint8_t* la = la_buf(cur);
-    const uint8_t* lb = lb_buf(cur);
+    if (kt + NST - 2 < nk)
+      wait_vmcnt<(NST - 2) * P::LOADS>();
+    else
+      wait_vmcnt<0>();
+    barrier_nofence();
+    if (kt + NST - 1 < nk) issue(kt + NST - 1);
+    const uint8_t* la = la_buf(kt % NST);
+    const uint8_t* lb = lb_buf(kt % NST);
+    rd(la, lb, 0, fa[0], fb[0]);
 #pragma unroll
     for (int i = 0; i < NSUB; ++i) {
       const int cb = i % NBUF;
@@ -211,11 +242,6 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) void grouped_gemm_kernel(
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int j = 0; j < 2; ++j) mfma<FP8>(acc[mi][j], fa[cb][mi], fb[cb][j]);
-    }
-    if (more) {
-      wait_vmem();
-      __syncthreads();
-      rd(la_buf(cur ^ 1), lb_buf(cur ^ 1), 0, fa[0], fb[0]);
     }
   }
 
@@ -399,23 +425,29 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
     kmoe::set_error("kmoe gemm: grid too large");
     return KMOE_ERR_SHAPE;
   }
+  const int kbytes = K * eb;
+  if (kbytes % KMOE_GEMM_KB != 0) {
+    kmoe::set_error("kmoe gemm: K bytes %d not a multiple of %d", kbytes, KMOE_GEMM_KB);
+    return KMOE_ERR_SHAPE;
+  }
   const uint8_t* a = static_cast<const uint8_t*>(A);
   const uint8_t* b = static_cast<const uint8_t*>(B);
   uint16_t* c = static_cast<uint16_t*>(C);
-  const int64_t lda = (int64_t)K * eb, ldb = (int64_t)K * eb;
-  const int kbytes = K * eb;
-  const dim3 grid((unsigned)blocks), block(GEMM_THREADS);
+  const int64_t lda = kbytes, ldb = kbytes + WPAD;
+  const dim3 grid((unsigned)blocks);
+  constexpr int KB = KMOE_GEMM_KB, NST = KMOE_GEMM_NST;
+  const dim3 block(GEMM_THREADS);
   if (gate_up && !fp8)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, false>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, false, KB, NST>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
                        b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
   else if (gate_up && fp8)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, true>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, true, KB, NST>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
                        b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
   else if (!fp8)
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, false>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, false, KB, NST>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
                        b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, true>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, true, KB, NST>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
                        b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
   return KMOE_OK;
 }
@@ -425,11 +457,11 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
 extern "C" int kmoe_padded_ff(int F) { return round_up(F, 128); }
 
 extern "C" size_t kmoe_packed_w13_bytes(int E, int d, int F, int dtype) {
-  return (size_t)E * 2 * (size_t)round_up(F, 128) * (size_t)d * (size_t)elem_bytes(dtype);
+  return (size_t)E * 2 * (size_t)round_up(F, 128) * ((size_t)d * (size_t)elem_bytes(dtype) + WPAD);
 }
 
 extern "C" size_t kmoe_packed_w3_bytes(int E, int d, int F, int dtype) {
-  return (size_t)E * (size_t)round_up(d, 256) * (size_t)round_up(F, 128) * (size_t)elem_bytes(dtype);
+  return (size_t)E * (size_t)round_up(d, 256) * ((size_t)round_up(F, 128) * (size_t)elem_bytes(dtype) + WPAD);
 }
 
 extern "C" int kmoe_pack_weights(const void* w1, const void* w2, const void* w3, int w_dtype, int E, int d, int F,
@@ -469,6 +501,8 @@ extern "C" int kmoe_pack_weights(const void* w1, const void* w2, const void* w3,
     }
   }
   // w1/w2: (E, d, F) -> rows f, cols d.  w3: (E, F, d) -> rows n, cols f.
+  const int eb = elem_bytes(packed_dtype);
+  const int ld13 = d + WPAD / eb, ld3 = Fp + WPAD / eb;  // packed row strides in elements
   const dim3 gt13((unsigned)kmoe::ceil_div(F, 64), (unsigned)kmoe::ceil_div(d, 64), (unsigned)E);
   const dim3 gt3((unsigned)kmoe::ceil_div(d, 64), (unsigned)kmoe::ceil_div(F, 64), (unsigned)E);
   uint8_t* o13 = static_cast<uint8_t*>(w13_packed);
@@ -476,11 +510,11 @@ extern "C" int kmoe_pack_weights(const void* w1, const void* w2, const void* w3,
 #define KMOE_PACK(F32_, FP8_)                                                                                        \
   do {                                                                                                               \
     hipLaunchKernelGGL((pack_transpose_kernel<F32_, FP8_>), gt13, dim3(256), 0, s, w1, d, F, (int64_t)d * F, 0, true, \
-                       o13, rows13, d, w13_scale);                                                                   \
+                       o13, rows13, ld13, w13_scale);                                                                   \
     hipLaunchKernelGGL((pack_transpose_kernel<F32_, FP8_>), gt13, dim3(256), 0, s, w2, d, F, (int64_t)d * F, 1, true, \
-                       o13, rows13, d, w13_scale);                                                                   \
+                       o13, rows13, ld13, w13_scale);                                                                   \
     hipLaunchKernelGGL((pack_transpose_kernel<F32_, FP8_>), gt3, dim3(256), 0, s, w3, F, d, (int64_t)d * F, 0, false, \
-                       o3, rows3, Fp, w3_scale);                                                                     \
+                       o3, rows3, ld3, w3_scale);                                                                     \
   } while (0)
   if (f32 && fp8)
     KMOE_PACK(true, true);

@@ -26,11 +26,6 @@ constexpr int RT_LOADS = 6;       // direct-to-LDS instructions per wave and K-s
 // XOR by (row/2)%8 spreads the 16 lanes of each LDS read pass over distinct banks.
 __device__ __forceinline__ int rswz(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 template <int NE>
 __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __restrict__ x,
                                                             const int32_t* __restrict__ row_index, int64_t T, int d,
@@ -104,7 +99,7 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
       wait_vmcnt<(RT_STAGES - 2) * RT_LOADS>();
     else
       wait_vmcnt<0>();
-    __syncthreads();
+    barrier_nofence();
     if (kt + RT_STAGES - 1 < nk) issue(kt + RT_STAGES - 1);
     const uint8_t* xt = smem + (kt % RT_STAGES) * RT_STAGE;
     const uint8_t* wt = xt + RT_XT;

@@ -28,8 +28,9 @@ def test_version_and_sizes(lib):
     assert lib.kmoe_abi_version() == 1
     assert lib.kmoe_padded_ff(2816) == 2816 and lib.kmoe_padded_ff(352) == 384
     assert lib.kmoe_router_partials_len(16384, 16) == 256 * 17
-    assert lib.kmoe_packed_w13_bytes(16, 2048, 2816, _lib.DTYPE_BF16) == 16 * 2 * 2816 * 2048 * 2
-    assert lib.kmoe_packed_w3_bytes(16, 2048, 2816, _lib.DTYPE_FP8_E4M3) == 16 * 2048 * 2816
+    # packed rows carry 128 bytes of padding after the K-contiguous data
+    assert lib.kmoe_packed_w13_bytes(16, 2048, 2816, _lib.DTYPE_BF16) == 16 * 2 * 2816 * (2048 * 2 + 128)
+    assert lib.kmoe_packed_w3_bytes(16, 2048, 2816, _lib.DTYPE_FP8_E4M3) == 16 * 2048 * (2816 + 128)
     assert lib.kmoe_dispatch_workspace_bytes(16384, 2, 16) >= 2 * 128 * 16 * 4
 
 
