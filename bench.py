@@ -37,6 +37,8 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU baseline")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only run a plain 512 MiB device copy (the reference for PMC byte-counter scaling)")
     return ap.parse_args()
 
 
@@ -171,6 +173,15 @@ def main():
     from kmoe import synth
 
     wl = synth.WORKLOADS[args.config]
+    if args.calib_copy:
+        # reference kernel for PMC byte-counter scaling: reads and writes exactly 512 MiB per launch
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.add(src, 1, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": 512 << 20, "launches": 3}))
+        return
     res = run_gpu(args, wl)
     ms = res["elapsed"] / args.steps * 1e3
     tokens_per_s = wl.T * args.steps / res["elapsed"]
