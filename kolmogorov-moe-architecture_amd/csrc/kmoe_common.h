@@ -9,6 +9,8 @@
 
 // ---------------------------------------------------------------- vector types
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
@@ -49,6 +51,9 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 }
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+// SiLU with a hardware reciprocal (1 ulp) instead of an IEEE divide: for values
+// that are rounded to bf16 right after.
+__device__ __forceinline__ float silu_fast_f32(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // fp32 -> OCP e4m3fn, saturating to +-448, round-to-nearest-even.  Pure integer
 // arithmetic, so it is specified exactly (the oracle restates it in numpy).

@@ -5,14 +5,20 @@
 //   down:     y[r, n] = h[r] . w3[e][:, n]
 // for the rows r of expert e, [offsets[e], offsets[e+1]).
 //
-// Tiling: a workgroup of 8 waves (2 per SIMD) owns a 256-row x 256-B-row tile;
-// waves form 2 (rows) x 4 (B rows) and each computes 128 x 64 as 4x2 blocks of
-// v_mfma_f32_32x32x16_bf16 (fp8: v_mfma_scale_f32_32x32x64_f8f6f4).  K advances 64
-// bf16 (128 fp8 bytes) per step.  A and B tiles go global -> LDS directly
-// (global_load_lds_dwordx4, no register staging), double buffered (4 x 32 KiB), with
-// 16-byte chunks XOR-swizzled by (row/2)%8 so that the 16 lanes of each LDS read
-// pass hit distinct banks.  Operand fragments are double buffered in registers.
-// The output tile is staged through LDS and written with 16-byte row stores.
+// Tiling: a workgroup of 4 waves (one per SIMD) owns a 256-row x 256-B-row tile;
+// waves form 2 (rows) x 2 (B rows) and each computes 128 x 128 as 4x4 blocks of
+// v_mfma_f32_32x32x16_bf16 (fp8: v_mfma_scale_f32_32x32x64_f8f6f4), 256 fp32
+// accumulators per lane.  A 128x128 wave tile reads 0.5 KiB of LDS per MFMA, the
+// least a 4-wave workgroup of this tile allows.  K advances 64 bf16 (128 fp8
+// bytes) per pipeline step through 2 LDS stages of 2 x 32 KiB.  Tile data is
+// loaded into registers with buffer loads (the K offset is a scalar operand) one
+// step ahead and written to the stage not being read, 16-byte chunks XOR-swizzled
+// so that both the 1 KiB block writes and the 16 lanes of each fragment read pass
+// are bank-conflict free.  Fragment reads, LDS writes and loads are interleaved
+// with the MFMAs by scheduling groups; fragments are double buffered in registers;
+// one barrier per step, in its last substep.
+// The output tile is staged through LDS (bf16 pairs formed across lanes with DPP)
+// and written with 16-byte row stores.
 //
 // Ragged groups: every row tile ("slot") of every expert is enumerated from the
 // device-resident offsets; the grid is sized for the worst case
@@ -28,47 +34,33 @@
 // Every packed row is followed by WPAD bytes of padding: with power-of-two row
 // strides the 256 rows of a tile K-slice would all map to the same memory
 // channels; the pad spreads them (measured: +20% on the gate/up GEMM).
+#include <type_traits>
+
 #include "kmoe_common.h"
 
 namespace {
 
 constexpr int BM = 256;
 constexpr int BN = 256;       // B rows per tile (gate_up: 128 gate + 128 up)
-constexpr int GEMM_THREADS = 512;
+constexpr int GEMM_THREADS = 256;
 constexpr int WPAD = 128;     // bytes of padding after every packed weight row
 constexpr int NXCD = 8;
 constexpr int SB_TILES = 32;  // tiles per XCD super-block (4 slots x 8 column tiles)
+constexpr int KB = 128;       // K bytes per row per pipeline step (64 bf16 / 128 fp8)
+constexpr int TB = BM * KB;   // bytes of one A or B stage tile (32 KiB)
+constexpr int NST = 2;        // LDS stages: one read while the next is written
+constexpr int CPR = KB / 16;  // 16-byte chunks per tile row
+constexpr int RPB = 1024 / KB;                        // tile rows per 1 KiB load block
+constexpr int BLK_PER_WAVE = (BM * KB / 1024) / 4;    // load blocks per wave per operand per step
 // output staging: 256 rows x up to 256 bf16 columns, rows padded by 16 bytes
 constexpr int OUT_STRIDE_MAX = 256 * 2 + 16;
+constexpr int GEMM_LDS = (NST * 2 * TB > BM * OUT_STRIDE_MAX) ? NST * 2 * TB : BM * OUT_STRIDE_MAX;
+static_assert(GEMM_LDS <= 160 * 1024, "LDS budget");
 
-// K pipeline configuration: KB bytes of K per row per step (128 = 64 bf16, 64 = 32
-// bf16), NST LDS stages (NST-1 steps of loads in flight).
-template <int KB, int NST>
-struct Pipe {
-  static constexpr int TB = BM * KB;                       // bytes of one A or B stage tile
-  static constexpr int CPR = KB / 16;                      // 16-byte chunks per row
-  static constexpr int RPB = 1024 / KB;                    // rows per 1 KiB load block
-  static constexpr int RS = (KB == 128) ? 1 : 2;           // swizzle row shift (256/KB = 2^RS)
-  static constexpr int BLK_PER_WAVE = (BM / RPB) / 8;      // load blocks per wave per tile
-  static constexpr int LOADS = 2 * BLK_PER_WAVE;           // A + B load instructions per wave per step
-  static constexpr int LDS = (NST * 2 * TB > BM * OUT_STRIDE_MAX) ? NST * 2 * TB : BM * OUT_STRIDE_MAX;
-  // Byte offset of 16-byte chunk `chunk` of row `row`: XOR by (row >> RS) spreads
-  // the 16 lanes of each LDS read pass (16 consecutive rows) over distinct banks.
-  __device__ static __forceinline__ int swz(int row, int chunk) {
-    return row * KB + ((chunk ^ ((row >> RS) & (CPR - 1))) << 4);
-  }
-};
-
-// K-pipeline configuration of the shipped kernels (bytes of K per step, stages).
-#ifndef KMOE_GEMM_KB
-#define KMOE_GEMM_KB 128
-#endif
-#ifndef KMOE_GEMM_NST
-#define KMOE_GEMM_NST 2
-#endif
-// Static LDS of the kernel (a dependent array size would keep the host-side
-// launch stub from being emitted).
-constexpr int GEMM_LDS = Pipe<KMOE_GEMM_KB, KMOE_GEMM_NST>::LDS;
+// Byte offset of 16-byte chunk `chunk` of tile row `row`.  A 128-byte row puts rows
+// r and r+2 on the same banks; XOR-ing the chunk by (row/2)%8 gives the 16 lanes of
+// an LDS read pass (16 consecutive rows, one chunk) 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * KB + ((chunk ^ ((row >> 1) & (CPR - 1))) << 4); }
 
 __host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 
@@ -115,14 +107,14 @@ struct Frag<true> {
 
 // One MFMA operand fragment of K-substep `i` (bf16: 16 of K, chunk 2i+lh; fp8: 64
 // of K, chunks 4i+2lh and 4i+2lh+1) for LDS tile row `r`.
-template <class P, bool FP8>
+template <bool FP8>
 __device__ __forceinline__ void read_frag(const uint8_t* l, int r, int i, int lh, Frag<FP8>& f) {
   if constexpr (!FP8) {
-    f.v = *reinterpret_cast<const bf16x8_t*>(l + P::swz(r, 2 * i + lh));
+    f.v = *reinterpret_cast<const bf16x8_t*>(l + swz(r, 2 * i + lh));
   } else {
     const int ch = 4 * i + 2 * lh;
-    const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(l + P::swz(r, ch));
-    const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(l + P::swz(r, ch + 1));
+    const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(l + swz(r, ch));
+    const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(l + swz(r, ch + 1));
     f.v = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
 }
@@ -135,29 +127,57 @@ __device__ __forceinline__ void mfma(f32x16_t& acc, const Frag<FP8>& a, const Fr
     acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a.v, b.v, acc, 0, 0, 0, 127, 0, 127);
 }
 
-// B-tile row of the wave's j-th 32-row block (wn in 0..3, j in 0..1).
+// B-tile row of the wave's j-th 32-row block (wn in 0..1, j in 0..3).  gate_up:
+// blocks 0,1 are gate rows and 2,3 the up rows of the same 64 f columns.
 template <bool GATE_UP>
 __device__ __forceinline__ int b_row(int wn, int j, int lr) {
-  if (GATE_UP) return (j == 0 ? 0 : 128) + wn * 32 + lr;  // gate block, up block
-  return wn * 64 + j * 32 + lr;
+  if (GATE_UP) return (j >> 1) * 128 + wn * 64 + (j & 1) * 32 + lr;
+  return wn * 128 + j * 32 + lr;
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [I0, N).
+template <int I0, int N, class Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+  if constexpr (I0 < N) {
+    f(std::integral_constant<int, I0>{});
+    static_for<I0 + 1, N>(f);
+  }
+}
+
+// Scheduling groups for a 16-MFMA substep: after each MFMA, an even share of the
+// substep's NDS LDS operations and NVM memory operations.
+template <int NDS, int NVM, int G = 0>
+__device__ __forceinline__ void sched_spread() {
+  if constexpr (G < 16) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    constexpr int d = (NDS * (G + 1)) / 16 - (NDS * G) / 16;
+    constexpr int v = (NVM * (G + 1)) / 16 - (NVM * G) / 16;
+    if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x080, d, 0);  // DS
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x010, v, 0);  // VMEM
+    sched_spread<NDS, NVM, G + 1>();
+  }
+}
+
+// Raw buffer resource over [base, base + 4 GiB): loads address it with a 32-bit
+// per-lane offset plus a wave-uniform (SGPR) offset, so advancing K costs no VALU.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
 
 // FP8: A/B bytes are e4m3; a_scale per A row, b_scale per B row (global row index).
-template <bool GATE_UP, bool FP8, int KB, int NST>
-__global__ __launch_bounds__(GEMM_THREADS, 1) void grouped_gemm_kernel(
+template <bool GATE_UP, bool FP8>
+__global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_kernel(
     const uint8_t* __restrict__ A, int64_t lda_bytes, const float* __restrict__ a_scale,
     const int32_t* __restrict__ offsets, int E, const uint8_t* __restrict__ B, int64_t b_expert_rows,
     int64_t ldb_bytes, const float* __restrict__ b_scale, int k_bytes, uint16_t* __restrict__ C, int64_t ldc,
     int n_valid, int n_tiles) {
-  using P = Pipe<KB, NST>;
-  static_assert(P::LDS <= GEMM_LDS, "LDS budget of this pipeline configuration");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[GEMM_LDS];
-  constexpr int NSUB = FP8 ? KB / 64 : KB / 32;
+  constexpr int NSUB = FP8 ? KB / 64 : KB / 32;  // MFMA K-substeps per pipeline step
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, lh = lane >> 5;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave >> 1, wn = wave & 1;
 
   int slot, nt;
   map_tile(blockIdx.x, n_tiles, slot, nt);
@@ -165,127 +185,184 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) void grouped_gemm_kernel(
   if (!find_row_tile(offsets, E, slot, e, m0, m_end)) return;
 
   const int64_t brow0 = (int64_t)e * b_expert_rows + (int64_t)nt * BN;
-  const uint8_t* bexp = B + brow0 * ldb_bytes;
+  const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(A + (int64_t)m0 * lda_bytes);
+  const __amdgpu_buffer_rsrc_t brsrc = make_rsrc(B + brow0 * ldb_bytes);
   const int nk = k_bytes / KB;
   // LDS stage s: [A tile | B tile]
-  auto la_buf = [&](int st) { return lds + st * 2 * P::TB; };
-  auto lb_buf = [&](int st) { return lds + st * 2 * P::TB + P::TB; };
+  auto la_buf = [&](int st) { return lds + st * 2 * TB; };
+  auto lb_buf = [&](int st) { return lds + st * 2 * TB + TB; };
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // Direct-to-LDS tile loads: a 256-row tile is 256*KB/1024 blocks of 1 KiB; wave w
-  // issues A and B blocks [w*BPW, (w+1)*BPW).  Block q fills tile rows [q*RPB,
-  // (q+1)*RPB): lane l lands at byte 16*l of the block (row q*RPB + l/CPR, physical
-  // chunk l%CPR) and so fetches the logical chunk that swz() maps there.  A rows
-  // past the expert's last row are clamped to it (their results are never stored).
-  constexpr int BPW = P::BLK_PER_WAVE;
-  const int rsub = lane / P::CPR, pc = lane % P::CPR;
-  static_assert(BPW <= 4, "load blocks per wave");
-  uint32_t a_off[4], b_off[4];  // fixed size: a dependent array size drops the host launch stub
+  // Tile loads: a 256-row stage tile is 32 blocks of 1 KiB (8 rows of 128 B); wave w
+  // loads A and B blocks [8w, 8w+8) into registers and writes them to LDS.  Lane l
+  // of block q covers bytes [16l, 16l+16) of the block (tile row 8q + l/8, physical
+  // chunk l%8) and so loads the logical chunk that swz() maps there: the LDS write of
+  // a block is one contiguous, conflict-free 1 KiB.  A rows past the expert's last
+  // row are clamped to it (their results are never stored).
+  const int rsub = lane / CPR, pc = lane % CPR;
+  uint32_t a_off[BLK_PER_WAVE], b_off[BLK_PER_WAVE];
+  const int a_last = m_end - 1 - m0;
 #pragma unroll
-  for (int q = 0; q < BPW; ++q) {
-    const int tr = (wave * BPW + q) * P::RPB + rsub;
-    int ra = m0 + tr;
-    ra = ra < m_end ? ra : m_end - 1;
-    const uint32_t chunk = (uint32_t)(pc ^ ((tr >> P::RS) & (P::CPR - 1))) << 4;
+  for (int q = 0; q < BLK_PER_WAVE; ++q) {
+    const int tr = (wave * BLK_PER_WAVE + q) * RPB + rsub;
+    const int ra = tr < a_last ? tr : a_last;
+    const uint32_t chunk = (uint32_t)(pc ^ ((tr >> 1) & (CPR - 1))) << 4;
     a_off[q] = (uint32_t)ra * (uint32_t)lda_bytes + chunk;
     b_off[q] = (uint32_t)tr * (uint32_t)ldb_bytes + chunk;
   }
-  auto issue = [&](int kt) {
-    uint8_t* adst = la_buf(kt % NST);
-    uint8_t* bdst = lb_buf(kt % NST);
-    const uint8_t* ag = A + (int64_t)kt * KB;
-    const uint8_t* bg = bexp + (int64_t)kt * KB;
+  i32x4_t stg[2 * BLK_PER_WAVE];  // one step of this wave's tile data (A blocks, then B blocks)
+  // global -> registers: half 0 = A blocks, half 1 = B blocks of K-step kt (clamped)
+  auto load_half = [&](int kt, int half) {
+    const int ks = kt < nk ? kt : nk - 1;
 #pragma unroll
-    for (int q = 0; q < BPW; ++q)
-      __builtin_amdgcn_global_load_lds(ag + a_off[q], (KMOE_LDS void*)(adst + (wave * BPW + q) * 1024), 16, 0, 0);
-#pragma unroll
-    for (int q = 0; q < BPW; ++q)
-      __builtin_amdgcn_global_load_lds(bg + b_off[q], (KMOE_LDS void*)(bdst + (wave * BPW + q) * 1024), 16, 0, 0);
+    for (int q = 0; q < BLK_PER_WAVE; ++q) {
+      if (half == 0)
+        stg[q] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, a_off[q], ks * KB, 0);
+      else
+        stg[BLK_PER_WAVE + q] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, b_off[q], ks * KB, 0);
+    }
   };
-  // bf16: fragments double buffered across substeps; fp8 (8-register fragments):
-  // single buffered to stay within 256 registers at 2 waves per SIMD.
-  constexpr int NBUF = (FP8 || NSUB == 1) ? 1 : 2;
-  Frag<FP8> fa[NBUF][4], fb[NBUF][2];
-  auto rd = [&](const uint8_t* la, const uint8_t* lb, int i, Frag<FP8> (&a)[4], Frag<FP8> (&b)[2]) {
+  // registers -> LDS stage st
+  auto write_half = [&](int st, int half) {
+    uint8_t* dst = (half == 0 ? la_buf(st) : lb_buf(st)) + wave * BLK_PER_WAVE * 1024 + lane * 16;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) read_frag<P, FP8>(la, wm * 128 + mi * 32 + lr, i, lh, a[mi]);
+    for (int q = 0; q < BLK_PER_WAVE; ++q)
+      *reinterpret_cast<i32x4_t*>(dst + q * 1024) = stg[half * BLK_PER_WAVE + q];
+  };
+  Frag<FP8> fa[2][4], fb[2][4];
+  auto rd = [&](int st, int i, Frag<FP8> (&a)[4], Frag<FP8> (&b)[4]) {
+    const uint8_t* la = la_buf(st);
+    const uint8_t* lb = lb_buf(st);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) read_frag<P, FP8>(lb, b_row<GATE_UP>(wn, j, lr), i, lh, b[j]);
+    for (int mi = 0; mi < 4; ++mi) read_frag<FP8>(la, wm * 128 + mi * 32 + lr, i, lh, a[mi]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) read_frag<FP8>(lb, b_row<GATE_UP>(wn, j, lr), i, lh, b[j]);
+  };
+  auto mma = [&](const Frag<FP8> (&a)[4], const Frag<FP8> (&b)[4]) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mfma<FP8>(acc[mi][j], a[mi], b[j]);
   };
 
-  // NST-stage pipeline: stage kt is waited for (own loads by vmcnt, everyone's by the
-  // barrier), then the loads of step kt+NST-1 go into the buffer freed by step kt-1.
-  for (int st = 0; st < NST - 1 && st < nk; ++st) issue(st);
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + NST - 2 < nk)
-      wait_vmcnt<(NST - 2) * P::LOADS>();
-    else
-      wait_vmcnt<0>();
-    barrier_nofence();
-    if (kt + NST - 1 < nk) issue(kt + NST - 1);
-    const uint8_t* la = la_buf(kt % NST);
-    const uint8_t* lb = lb_buf(kt % NST);
-    rd(la, lb, 0, fa[0], fb[0]);
-#pragma unroll
-    for (int i = 0; i < NSUB; ++i) {
-      const int cb = i % NBUF;
-      if (NBUF == 2 && i + 1 < NSUB) rd(la, lb, i + 1, fa[(i + 1) % NBUF], fb[(i + 1) % NBUF]);
-      if (NBUF == 1 && i > 0) rd(la, lb, i, fa[0], fb[0]);
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) mfma<FP8>(acc[mi][j], fa[cb][mi], fb[cb][j]);
-    }
-  }
+  // Pipeline.  Step kt computes LDS stage kt%2 while the registers hold step kt+1's
+  // tile data.  bf16 (4 substeps): substeps 0 and 1 write that data (A, then B)
+  // into stage (kt+1)%2, which every wave stopped reading at step kt-1's barrier;
+  // substeps 1 and 2 then load step kt+2 into the freed registers, so a load has
+  // three substeps to land before it is written.  The last substep waits for this
+  // wave's LDS writes and reads, then one barrier publishes stage kt+1, whose first
+  // fragments are read under the last substep's MFMAs.  fp8 (2 substeps) does the
+  // writes and loads in substep 0.  Register dependencies give the vmcnt waits.
+  // The scheduling groups interleave one LDS or memory operation per MFMA.
+  constexpr int RD = FP8 ? 16 : 8;  // LDS reads of a substep's fragments
+  constexpr int SUB_WA = 0, SUB_WB = NSUB == 4 ? 1 : 0, SUB_LA = NSUB == 4 ? 1 : 0, SUB_LB = NSUB == 4 ? 2 : 0;
+  load_half(0, 0);
+  load_half(0, 1);
+  write_half(0, 0);
+  write_half(0, 1);
+  load_half(1, 0);
+  load_half(1, 1);
+  wait_lgkmcnt0();
+  barrier_nofence();
+  rd(0, 0, fa[0], fb[0]);
+
+  auto step = [&](int kt, auto last_tag) {
+    constexpr bool LAST = decltype(last_tag)::value;
+    const int cur = kt & 1, nxt = cur ^ 1;
+    static_for<0, NSUB>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr int bi = i & 1;
+      constexpr bool WA = !LAST && i == SUB_WA, WB = !LAST && i == SUB_WB;
+      constexpr bool LA = !LAST && i == SUB_LA, LB = !LAST && i == SUB_LB;
+      constexpr bool RDN = i + 1 < NSUB || !LAST;
+      // next substep's fragments first: they are on the MFMA critical path
+      if constexpr (i + 1 < NSUB) {
+        rd(cur, i + 1, fa[bi ^ 1], fb[bi ^ 1]);
+      } else if constexpr (!LAST) {
+        wait_lgkmcnt0();
+        barrier_nofence();
+        rd(nxt, 0, fa[bi ^ 1], fb[bi ^ 1]);
+      }
+      if constexpr (WA) write_half(nxt, 0);
+      if constexpr (WB) write_half(nxt, 1);
+      if constexpr (LA) load_half(kt + 2, 0);
+      if constexpr (LB) load_half(kt + 2, 1);
+      mma(fa[bi], fb[bi]);
+      constexpr int n_ds = (WA ? BLK_PER_WAVE : 0) + (WB ? BLK_PER_WAVE : 0) + (RDN ? RD : 0);
+      constexpr int n_vm = (LA ? BLK_PER_WAVE : 0) + (LB ? BLK_PER_WAVE : 0);
+      sched_spread<n_ds, n_vm>();
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  for (int kt = 0; kt + 1 < nk; ++kt) step(kt, std::false_type{});
+  step(nk - 1, std::true_type{});
 
   // ---- epilogue.  acc[mi][j][r] is (row 8*(r/4)+4*lh+r%4, col lr) of block (mi, j).
-  // Results go to an LDS tile (rows padded by 16 bytes; even lanes store the bf16
-  // pair of lanes lr, lr+1), then out with 16-byte stores along rows.
+  // Results go to an LDS tile (rows padded by 16 bytes) as bf16 pairs, then out with
+  // 16-byte stores along rows.  Pairs are formed across neighbouring lanes with DPP
+  // (VALU, no LDS round trip): for the rows of r = 2p and 2p+1, an even lane packs
+  // its own and its right neighbour's value of row 2p, an odd lane its left
+  // neighbour's and its own of row 2p+1, so every lane writes 4 bytes, unmasked.
   constexpr int NC = GATE_UP ? 128 : 256;   // output columns of the tile
+  constexpr int NJ = GATE_UP ? 2 : 4;       // output column blocks per wave
   constexpr int OSTR = NC * 2 + 16;          // LDS row stride (bytes)
+  const bool odd = lr & 1;
   __syncthreads();
+  // lane's write address for p = 0 of block (0, 0): even lanes row 4lh col lr,
+  // odd lanes row 4lh+1 col lr-1
+  uint8_t* const wbase = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR + (wn * (NC / 2) + lr - (odd ? 1 : 0)) * 2;
+  auto result = [&](int mi, int r, int jo) -> float {
+    if (GATE_UP) {
+      float g = acc[mi][jo][r], u = acc[mi][jo + 2][r];
+      if (FP8) {
+        const int grow = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        const float sa = grow < m_end ? a_scale[grow] : 1.0f;
+        g *= sa * b_scale[brow0 + b_row<true>(wn, jo, lr)];
+        u *= sa * b_scale[brow0 + b_row<true>(wn, jo + 2, lr)];
+      }
+      return silu_fast_f32(g) * u;
+    } else {
+      float v = acc[mi][jo][r];
+      if (FP8) {
+        const int grow = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        const float sa = grow < m_end ? a_scale[grow] : 1.0f;
+        v *= sa * b_scale[brow0 + b_row<false>(wn, jo, lr)];
+      }
+      return v;
+    }
+  };
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int trow = wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-      const int grow = m0 + trow;
-      const float sa = (FP8 && grow < m_end) ? a_scale[grow] : 1.0f;
+    for (int p = 0; p < 8; ++p) {
+      const int r0 = 2 * p, r1 = 2 * p + 1;
 #pragma unroll
-      for (int jo = 0; jo < (GATE_UP ? 1 : 2); ++jo) {
-        float v;
-        int col;
-        if (GATE_UP) {
-          float g = acc[mi][0][r], u = acc[mi][1][r];
-          if (FP8) {
-            g *= sa * b_scale[brow0 + b_row<true>(wn, 0, lr)];
-            u *= sa * b_scale[brow0 + b_row<true>(wn, 1, lr)];
-          }
-          v = silu_f32(g) * u;
-          col = wn * 32 + lr;
-        } else {
-          v = acc[mi][jo][r];
-          if (FP8) v *= sa * b_scale[brow0 + b_row<false>(wn, jo, lr)];
-          col = wn * 64 + jo * 32 + lr;
-        }
-        const uint32_t bits = f32_to_bf16(v);
-        const uint32_t nb = (uint32_t)__shfl_xor((int)bits, 1, 64);
-        if ((lr & 1) == 0) *reinterpret_cast<uint32_t*>(lds + trow * OSTR + col * 2) = bits | (nb << 16);
+      for (int jo = 0; jo < NJ; ++jo) {
+        const float a = result(mi, r0, jo), b = result(mi, r1, jo);
+        // row_shl:1 -> value of lane+1, row_shr:1 -> value of lane-1 (within 16 lanes)
+        const float a_next = __builtin_bit_cast(
+            float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, a), 0x101, 0xf, 0xf, false));
+        const float b_prev = __builtin_bit_cast(
+            float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, b), 0x111, 0xf, 0xf, false));
+        const float lo = odd ? b_prev : a, hi = odd ? b : a_next;
+        const uint32_t packed = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+        // row of r0 is mi*32 + 8*(p/2) + 2*(p%2) (+1 for odd lanes via wbase)
+        *reinterpret_cast<uint32_t*>(wbase + (mi * 32 + 8 * (p >> 1) + 2 * (p & 1)) * OSTR + jo * 64) = packed;
       }
     }
   }
   __syncthreads();
-  constexpr int CPR = NC * 2 / 16;  // 16-byte chunks per row
+  constexpr int OCPR = NC * 2 / 16;  // 16-byte chunks per output row
   const int col0 = nt * NC;
-  for (int c = tid; c < BM * CPR; c += GEMM_THREADS) {
-    const int trow = c / CPR, ch = c % CPR;
+  for (int c = tid; c < BM * OCPR; c += GEMM_THREADS) {
+    const int trow = c / OCPR, ch = c % OCPR;
     const int grow = m0 + trow;
     const int gcol = col0 + ch * 8;
     if (grow < m_end && gcol < n_valid)
@@ -426,28 +503,32 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
     return KMOE_ERR_SHAPE;
   }
   const int kbytes = K * eb;
-  if (kbytes % KMOE_GEMM_KB != 0) {
-    kmoe::set_error("kmoe gemm: K bytes %d not a multiple of %d", kbytes, KMOE_GEMM_KB);
+  if (kbytes % KB != 0) {
+    kmoe::set_error("kmoe gemm: K bytes %d not a multiple of %d", kbytes, KB);
     return KMOE_ERR_SHAPE;
   }
   const uint8_t* a = static_cast<const uint8_t*>(A);
   const uint8_t* b = static_cast<const uint8_t*>(B);
   uint16_t* c = static_cast<uint16_t*>(C);
   const int64_t lda = kbytes, ldb = kbytes + WPAD;
+  // tile loads address a 2 GiB buffer window from the tile's first A / B row
+  if ((int64_t)(BM + 1) * ldb >= ((int64_t)1 << 31)) {
+    kmoe::set_error("kmoe gemm: K bytes %d too large", kbytes);
+    return KMOE_ERR_SHAPE;
+  }
   const dim3 grid((unsigned)blocks);
-  constexpr int KB = KMOE_GEMM_KB, NST = KMOE_GEMM_NST;
   const dim3 block(GEMM_THREADS);
   if (gate_up && !fp8)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, false, KB, NST>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, false>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
                        b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
   else if (gate_up && fp8)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, true, KB, NST>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, true>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
                        b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
   else if (!fp8)
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, false, KB, NST>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, false>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
                        b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, true, KB, NST>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, true>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
                        b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
   return KMOE_OK;
 }
