@@ -54,8 +54,11 @@ def stage_bytes_flops(wl, layer, fwd_state):
     return {
         "gemm_gate_up": ("flop", 4.0 * d * F * a_kept),
         "gemm_down": ("flop", 2.0 * d * F * a_kept),
-        # read each routed token row once, write its kept rows, 8 B/assignment of metadata
-        "dispatch": ("byte", t_in * d * s + a_kept * d * xs + 8.0 * a_all + (a_kept * 4 if wl.fp8 else 0)),
+        # fp8: read each routed token row once, write its kept quantised rows + scales;
+        # bf16: tables only (the gate/up GEMM gathers the rows): read ids twice (8 B) and
+        # weights (4 B), write row_token / slot_row / slot_w (12 B) per assignment
+        "dispatch": ("byte", t_in * d * s + a_kept * d * xs + 8.0 * a_all + a_kept * 4 if wl.fp8
+                     else 28.0 * a_all),
         "gather": ("byte", a_kept * d * s + a_kept * d * xs + 4.0 * a_kept),
         # read the kept expert rows, write y, 8 B/assignment of metadata
         "combine": ("byte", a_kept * d * s + T * d * s + 8.0 * a_all),

@@ -92,6 +92,8 @@ int kmoe_aux_loss(const float* partials, int64_t T, int E, const int32_t* counts
  * row of assignment a or -1 if dropped; slot_w (T*k) f32 routing weight.
  * xperm_dtype BF16 copies rows; FP8_E4M3 quantises each row with the per-token
  * scale amax(|x[row]|)/448 written to xperm_scale (one per permuted row).
+ * xperm may be NULL with BF16: only the tables are written (for
+ * kmoe_gemm_gate_up_rows, which gathers the rows itself).
  *   topk_w dtype: w_dtype (BF16 or F32).  workspace: kmoe_dispatch_workspace_bytes. */
 size_t kmoe_dispatch_workspace_bytes(int64_t T, int k, int E);
 int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
@@ -127,6 +129,15 @@ int kmoe_pack_weights(const void* w1, const void* w2, const void* w3, int w_dtyp
 int kmoe_gemm_gate_up(const void* xperm, const float* xperm_scale, int in_dtype, const int32_t* offsets,
                       int E, int d, int F, int64_t max_rows, const void* w13_packed,
                       const float* w13_scale, void* h, void* stream);
+/* gate_up with the dispatch gather fused into its A loads: replaces the gather
+ * all_inputs = x[sorted_token_idx] + the first two bmm of GroupedExperts.forward
+ * (moe.py:255-277).  Permuted row r is x[row_index ? row_index[row_token[r]] :
+ * row_token[r]] (x: n_x_rows x d bf16; row_token from kmoe_dispatch, which then
+ * need not write xperm).  bf16 only; same result as kmoe_gemm_gate_up on the
+ * gathered rows, bit for bit.                                                 */
+int kmoe_gemm_gate_up_rows(const void* x, const int32_t* row_index, int64_t n_x_rows, const int32_t* row_token,
+                           const int32_t* offsets, int E, int d, int F, int64_t max_rows, const void* w13_packed,
+                           void* h, void* stream);
 int kmoe_gemm_down(const void* h, const float* h_scale, int in_dtype, const int32_t* offsets, int E,
                    int d, int F, int64_t max_rows, const void* w3_packed, const float* w3_scale,
                    void* y, void* stream);

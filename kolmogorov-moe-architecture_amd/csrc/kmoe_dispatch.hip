@@ -139,6 +139,7 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
   const int64_t ntok = min<int64_t>(DTB, T - t0);
   const int nvec = d / 8;  // 16-byte vectors per row
   if (!FP8) {
+    if (xperm == nullptr) return;  // tables only: the GEMM gathers the rows
     const int64_t total = ntok * nvec;
     for (int64_t c0 = tid; c0 < total; c0 += 4 * DTHREADS) {
       i32x4_t val[4];
@@ -287,7 +288,8 @@ extern "C" int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T,
                              int32_t* offsets, int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm,
                              int xperm_dtype, float* xperm_scale, void* workspace, size_t workspace_bytes,
                              void* stream) {
-  KMOE_REQUIRE(x && topk_idx && topk_w && counts && offsets && row_token && slot_row && slot_w && xperm,
+  KMOE_REQUIRE(x && topk_idx && topk_w && counts && offsets && row_token && slot_row && slot_w &&
+                   (xperm || xperm_dtype == KMOE_DTYPE_BF16),
                KMOE_ERR_NULL, "kmoe_dispatch: null buffer");
   KMOE_REQUIRE(T >= 0 && T * (int64_t)k < ((int64_t)1 << 31), KMOE_ERR_SHAPE,
                "kmoe_dispatch: T*k must fit in int32");

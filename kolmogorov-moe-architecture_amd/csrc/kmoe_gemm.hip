@@ -165,12 +165,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
 }
 
 // FP8: A/B bytes are e4m3; a_scale per A row, b_scale per B row (global row index).
-template <bool GATE_UP, bool FP8>
+// GATHER: A is the unpermuted activation matrix and permuted row r is its row
+// row_index[row_token[r]] (row_token[r] without row_index): the dispatch gather is
+// fused into the A loads.
+template <bool GATE_UP, bool FP8, bool GATHER>
 __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_kernel(
     const uint8_t* __restrict__ A, int64_t lda_bytes, const float* __restrict__ a_scale,
+    const int32_t* __restrict__ row_token, const int32_t* __restrict__ row_index,
     const int32_t* __restrict__ offsets, int E, const uint8_t* __restrict__ B, int64_t b_expert_rows,
     int64_t ldb_bytes, const float* __restrict__ b_scale, int k_bytes, uint16_t* __restrict__ C, int64_t ldc,
     int n_valid, int n_tiles) {
+  static_assert(!(GATHER && FP8), "the fp8 path reads rows quantised by the dispatch");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[GEMM_LDS];
   constexpr int NSUB = FP8 ? KB / 64 : KB / 32;  // MFMA K-substeps per pipeline step
   const int tid = threadIdx.x;
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   if (!find_row_tile(offsets, E, slot, e, m0, m_end)) return;
 
   const int64_t brow0 = (int64_t)e * b_expert_rows + (int64_t)nt * BN;
-  const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(A + (int64_t)m0 * lda_bytes);
+  const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(GATHER ? A : A + (int64_t)m0 * lda_bytes);
   const __amdgpu_buffer_rsrc_t brsrc = make_rsrc(B + brow0 * ldb_bytes);
   const int nk = k_bytes / KB;
   // LDS stage s: [A tile | B tile]
@@ -212,7 +217,11 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
   for (int q = 0; q < BLK_PER_WAVE; ++q) {
     const int tr = (wave * BLK_PER_WAVE + q) * RPB + rsub;
-    const int ra = tr < a_last ? tr : a_last;
+    int ra = tr < a_last ? tr : a_last;
+    if constexpr (GATHER) {
+      const int tok = row_token[m0 + ra];
+      ra = row_index ? row_index[tok] : tok;
+    }
     const uint32_t chunk = (uint32_t)(pc ^ ((tr >> 1) & (CPR - 1))) << 4;
     a_off[q] = (uint32_t)ra * (uint32_t)lda_bytes + chunk;
     b_off[q] = (uint32_t)tr * (uint32_t)ldb_bytes + chunk;
@@ -490,9 +499,12 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
 
 int elem_bytes(int dtype) { return dtype == KMOE_DTYPE_FP8_E4M3 ? 1 : 2; }
 
-int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, const int32_t* offsets, int E, int K,
-                int64_t max_rows, const void* B, int64_t b_expert_rows, const float* b_scale, void* C, int64_t ldc,
-                int n_valid, int n_tiles, hipStream_t s) {
+// A rows: the permuted rows (row_token == nullptr) or gathered rows of the
+// activation matrix A (n_a_rows rows) through row_token / row_index.
+int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, const int32_t* row_token,
+                const int32_t* row_index, int64_t n_a_rows, const int32_t* offsets, int E, int K, int64_t max_rows,
+                const void* B, int64_t b_expert_rows, const float* b_scale, void* C, int64_t ldc, int n_valid,
+                int n_tiles, hipStream_t s) {
   const int eb = fp8 ? 1 : 2;
   const int64_t slots = kmoe::ceil_div<int64_t>(max_rows, BM) + E;
   // whole 4-slot groups, whole XCD super-blocks (map_tile covers [0, blocks))
@@ -511,25 +523,28 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
   const uint8_t* b = static_cast<const uint8_t*>(B);
   uint16_t* c = static_cast<uint16_t*>(C);
   const int64_t lda = kbytes, ldb = kbytes + WPAD;
-  // tile loads address a 2 GiB buffer window from the tile's first A / B row
-  if ((int64_t)(BM + 1) * ldb >= ((int64_t)1 << 31)) {
-    kmoe::set_error("kmoe gemm: K bytes %d too large", kbytes);
+  // tile loads address a 2 GiB buffer window from the tile's first A / B row (from
+  // the first row of A when gathering)
+  if ((int64_t)(BM + 1) * ldb >= ((int64_t)1 << 31) || (row_token && (n_a_rows + 1) * lda >= ((int64_t)1 << 31))) {
+    kmoe::set_error("kmoe gemm: operand too large for 32-bit tile offsets (K bytes %d)", kbytes);
     return KMOE_ERR_SHAPE;
   }
   const dim3 grid((unsigned)blocks);
   const dim3 block(GEMM_THREADS);
-  if (gate_up && !fp8)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, false>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
-                       b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
+#define KMOE_LAUNCH_GEMM(GU, F8, GA)                                                                       \
+  hipLaunchKernelGGL((grouped_gemm_kernel<GU, F8, GA>), grid, block, 0, s, a, lda, a_scale, row_token, row_index, \
+                     offsets, E, b, b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles)
+  if (row_token)
+    KMOE_LAUNCH_GEMM(true, false, true);
+  else if (gate_up && !fp8)
+    KMOE_LAUNCH_GEMM(true, false, false);
   else if (gate_up && fp8)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, true>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
-                       b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
+    KMOE_LAUNCH_GEMM(true, true, false);
   else if (!fp8)
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, false>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
-                       b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
+    KMOE_LAUNCH_GEMM(false, false, false);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, true>), grid, block, 0, s, a, lda, a_scale, offsets, E, b,
-                       b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles);
+    KMOE_LAUNCH_GEMM(false, true, false);
+#undef KMOE_LAUNCH_GEMM
   return KMOE_OK;
 }
 
@@ -635,10 +650,26 @@ extern "C" int kmoe_gemm_gate_up(const void* xperm, const float* xperm_scale, in
   KMOE_REQUIRE(!fp8 || d % 128 == 0, KMOE_ERR_SHAPE, "kmoe_gemm_gate_up: fp8 needs d %% 128 == 0 (d=%d)", d);
   if (max_rows == 0) return KMOE_OK;
   const int Fp = round_up(F, 128);
-  rc = launch_gemm(true, fp8, xperm, xperm_scale, offsets, E, d, max_rows, w13_packed, 2 * (int64_t)Fp, w13_scale, h,
-                   Fp, Fp, Fp / 128, kmoe::as_stream(stream));
+  rc = launch_gemm(true, fp8, xperm, xperm_scale, nullptr, nullptr, 0, offsets, E, d, max_rows, w13_packed,
+                   2 * (int64_t)Fp, w13_scale, h, Fp, Fp, Fp / 128, kmoe::as_stream(stream));
   if (rc) return rc;
   return kmoe::check_launch("kmoe_gemm_gate_up");
+}
+
+extern "C" int kmoe_gemm_gate_up_rows(const void* x, const int32_t* row_index, int64_t n_x_rows,
+                                      const int32_t* row_token, const int32_t* offsets, int E, int d, int F,
+                                      int64_t max_rows, const void* w13_packed, void* h, void* stream) {
+  int rc = check_gemm_args("kmoe_gemm_gate_up_rows", x, offsets, E, d, F, max_rows, w13_packed, h, KMOE_DTYPE_BF16);
+  if (rc) return rc;
+  KMOE_REQUIRE(row_token, KMOE_ERR_NULL, "kmoe_gemm_gate_up_rows: null row_token");
+  KMOE_REQUIRE(n_x_rows >= 1, KMOE_ERR_SHAPE, "kmoe_gemm_gate_up_rows: n_x_rows=%lld must be >= 1",
+               (long long)n_x_rows);
+  if (max_rows == 0) return KMOE_OK;
+  const int Fp = round_up(F, 128);
+  rc = launch_gemm(true, false, x, nullptr, row_token, row_index, n_x_rows, offsets, E, d, max_rows, w13_packed,
+                   2 * (int64_t)Fp, nullptr, h, Fp, Fp, Fp / 128, kmoe::as_stream(stream));
+  if (rc) return rc;
+  return kmoe::check_launch("kmoe_gemm_gate_up_rows");
 }
 
 extern "C" int kmoe_gemm_down(const void* h, const float* h_scale, int in_dtype, const int32_t* offsets, int E, int d,
@@ -650,8 +681,8 @@ extern "C" int kmoe_gemm_down(const void* h, const float* h_scale, int in_dtype,
   KMOE_REQUIRE(!fp8 || (h_scale && w3_scale), KMOE_ERR_NULL, "kmoe_gemm_down: fp8 needs scales");
   if (max_rows == 0) return KMOE_OK;
   const int Fp = round_up(F, 128), dp = round_up(d, 256);
-  rc = launch_gemm(false, fp8, h, h_scale, offsets, E, Fp, max_rows, w3_packed, dp, w3_scale, y, d, d, dp / BN,
-                   kmoe::as_stream(stream));
+  rc = launch_gemm(false, fp8, h, h_scale, nullptr, nullptr, 0, offsets, E, Fp, max_rows, w3_packed, dp, w3_scale, y,
+                   d, d, dp / BN, kmoe::as_stream(stream));
   if (rc) return rc;
   return kmoe::check_launch("kmoe_gemm_down");
 }

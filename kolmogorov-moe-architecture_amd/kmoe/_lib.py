@@ -43,6 +43,7 @@ _SIGNATURES = {
     "kmoe_packed_w3_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "kmoe_pack_weights": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_gemm_gate_up": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp]),
+    "kmoe_gemm_gate_up_rows": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp]),
     "kmoe_gemm_down": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp]),
     "kmoe_quant_rows_fp8": (_i32, [_vp, _i64, _vp, _i32, _vp, _vp, _vp]),
     "kmoe_grouped_swiglu": (_i32, [_vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp]),

@@ -176,9 +176,16 @@ class GroupedExperts(_PackedExperts):
         E = self.n_experts
         pw = self.packed()
         T, k = expert_indices.shape
-        disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=self.capacity, fp8=pw.fp8,
-                            row_index=row_index)
-        yperm = ops.grouped_ffn(disp.xperm, disp.xscale, disp.offsets, pw, T * k)
+        if pw.fp8:
+            disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=self.capacity, fp8=True,
+                                row_index=row_index)
+            yperm = ops.grouped_ffn(disp.xperm, disp.xscale, disp.offsets, pw, T * k)
+        else:
+            # bf16: the gate/up GEMM gathers the token rows itself (no permuted copy of x)
+            disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=self.capacity,
+                                row_index=row_index, materialize=False)
+            h = ops.gemm_gate_up_rows(x2d, row_index, disp.row_token, disp.offsets, pw, T * k)
+            yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k),
                         T if T_out is None else T_out, out_map=out_map, scale=scale, out_dtype=out_dtype)
         return y, disp

@@ -126,8 +126,13 @@ def capacity_of(cf: float, T: int, k: int, E: int) -> int:
     return int(math.ceil(cf * T * k / E))
 
 
-def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None) -> DispatchOut:
-    """Stable counting-sort dispatch (moe.py:238-272) + optional capacity drop."""
+def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None, materialize=True) -> DispatchOut:
+    """Stable counting-sort dispatch (moe.py:238-272) + optional capacity drop.
+
+    materialize=False (bf16 only) writes the routing tables but not the permuted
+    rows: gemm_gate_up_rows gathers them itself (xperm is then None)."""
+    if not materialize and fp8:
+        raise ValueError("kmoe.dispatch: the fp8 path needs the quantised permuted rows (materialize=True)")
     _need_gpu(x2d, idx, w)
     x2d = _contig(x2d, _BF16)
     idx = _contig(idx, torch.int64)
@@ -144,7 +149,7 @@ def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None) -> DispatchO
     row_token = torch.empty(max(A, 1), device=dev, dtype=torch.int32)
     slot_row = torch.empty(max(A, 1), device=dev, dtype=torch.int32)
     slot_w = torch.empty(max(A, 1), device=dev, dtype=torch.float32)
-    xperm = torch.empty(max(A, 1), d, device=dev, dtype=torch.uint8 if fp8 else _BF16)
+    xperm = torch.empty(max(A, 1), d, device=dev, dtype=torch.uint8 if fp8 else _BF16) if materialize else None
     xscale = torch.empty(max(A, 1), device=dev, dtype=torch.float32) if fp8 else None
     wsb = lib.kmoe_dispatch_workspace_bytes(T, k, E)
     ws = torch.empty(wsb, device=dev, dtype=torch.uint8)
@@ -212,6 +217,22 @@ def gemm_gate_up(xperm, xscale, offsets, pw: PackedWeights, max_rows):
         _lib.call("kmoe_gemm_gate_up", ptr(xperm), ptr(xscale),
               _lib.DTYPE_FP8_E4M3 if pw.fp8 else _lib.DTYPE_BF16, ptr(offsets), pw.E, pw.d, pw.F, max_rows,
               ptr(pw.w13), ptr(pw.s13), ptr(h), _stream(xperm))
+    return h
+
+
+def gemm_gate_up_rows(x2d, row_index, row_token, offsets, pw: PackedWeights, max_rows):
+    """gate_up GEMM whose A rows are x2d[row_index[row_token[r]]] (x2d[row_token[r]]
+    without row_index): the dispatch gather fused into the GEMM's loads (bf16)."""
+    if pw.fp8:
+        raise ValueError("kmoe.gemm_gate_up_rows: bf16 weights only (fp8 reads quantised permuted rows)")
+    _need_gpu(x2d, row_token, offsets)
+    x2d = _contig(x2d, _BF16)
+    lib = _lib.load()
+    Fp = lib.kmoe_padded_ff(pw.F)
+    h = torch.empty(max(max_rows, 1), Fp, device=x2d.device, dtype=_BF16)
+    with _Stage("gemm_gate_up"):
+        _lib.call("kmoe_gemm_gate_up_rows", ptr(x2d), ptr(row_index), x2d.shape[0], ptr(row_token), ptr(offsets),
+                  pw.E, pw.d, pw.F, max_rows, ptr(pw.w13), ptr(h), _stream(x2d))
     return h
 
 

@@ -191,6 +191,40 @@ def test_grouped_swiglu_bf16(dev, d, F, counts):
             assert relL2(npf(y[lo:hi]), ref[lo:hi]) <= 1e-2
 
 
+@pytest.mark.parametrize("with_row_index,cap", [(False, 0), (True, 0), (False, 300)])
+def test_gate_up_gather_fused(dev, with_row_index, cap):
+    """The gate/up GEMM that gathers its rows (x[row_index[row_token[r]]]) equals
+    the one on the materialised permuted rows bit for bit, and the table-only
+    dispatch writes the same tables as the materialising one."""
+    T, k, E, d, F = 3000, 2, 8, 512, 768
+    n_x = T + 321 if with_row_index else T
+    (x,) = gen(30, (n_x, d))
+    idx, w = _routing(T, k, E, 31, True)
+    rows = (torch.randperm(n_x, generator=torch.Generator().manual_seed(3))[:T].to(torch.int32).to(dev)
+            if with_row_index else None)
+    xb = bf16(x).to(dev)
+    w1, w2, w3 = _experts(E, d, F, 32)
+    pw = ops.pack_weights(bf16(w1).to(dev), bf16(w2).to(dev), bf16(w3).to(dev))
+    full = ops.dispatch(xb, idx.to(dev), w.to(dev), E, capacity=cap, row_index=rows)
+    tab = ops.dispatch(xb, idx.to(dev), w.to(dev), E, capacity=cap, row_index=rows, materialize=False)
+    assert tab.xperm is None
+    A_kept = int(full.offsets[-1])
+    for name in ("counts", "offsets", "slot_row", "slot_w"):
+        assert torch.equal(getattr(full, name), getattr(tab, name)), name
+    assert torch.equal(full.row_token[:A_kept], tab.row_token[:A_kept])
+    h_ref = ops.gemm_gate_up(full.xperm, None, full.offsets, pw, T * k)
+    h = ops.gemm_gate_up_rows(xb, rows, tab.row_token, tab.offsets, pw, T * k)
+    torch.cuda.synchronize()
+    assert torch.equal(h[:A_kept], h_ref[:A_kept])
+    # and against the oracle on the gathered rows
+    src = npf(xb)[rows.cpu().numpy()] if with_row_index else npf(xb)
+    xg = src[tab.row_token[:A_kept].cpu().numpy()]
+    off = tab.offsets.cpu().numpy().astype(np.int64)
+    g = np.concatenate([xg[off[e]:off[e + 1]] @ npf(bf16(w1))[e] for e in range(E)])
+    u = np.concatenate([xg[off[e]:off[e + 1]] @ npf(bf16(w2))[e] for e in range(E)])
+    assert relL2(npf(h[:A_kept, :F]), O.silu(g) * u) <= 1e-2
+
+
 def test_grouped_swiglu_f32_weights_and_kernels_api(dev):
     """fp32 parameters are packed directly; the reference's native-extension
     signature (kernels/__init__.py:105) runs on the same GEMMs."""
