@@ -144,16 +144,17 @@ __device__ __forceinline__ void static_for(Fn&& f) {
   }
 }
 
-// Scheduling groups for a 16-MFMA substep: after each MFMA, an even share of the
-// substep's NDS LDS operations and NVM memory operations.
+// Scheduling groups for a 16-MFMA substep: LDS operations front-loaded, one
+// after each of the first NDS MFMAs (two each when NDS > 16), memory operations
+// spread evenly over all 16.
 template <int NDS, int NVM, int G = 0>
 __device__ __forceinline__ void sched_spread() {
   if constexpr (G < 16) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    constexpr int d = (NDS * (G + 1)) / 16 - (NDS * G) / 16;
+    constexpr int dd = NDS <= 16 ? (G < NDS ? 1 : 0) : (NDS * (G + 1) + 15) / 16 - (NDS * G + 15) / 16;
     constexpr int v = (NVM * (G + 1)) / 16 - (NVM * G) / 16;
-    if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x080, d, 0);  // DS
-    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x010, v, 0);  // VMEM
+    if constexpr (dd > 0) __builtin_amdgcn_sched_group_barrier(0x080, dd, 0);  // DS
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x010, v, 0);   // VMEM
     sched_spread<NDS, NVM, G + 1>();
   }
 }
@@ -226,24 +227,20 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
     a_off[q] = (uint32_t)ra * (uint32_t)lda_bytes + chunk;
     b_off[q] = (uint32_t)tr * (uint32_t)ldb_bytes + chunk;
   }
-  i32x4_t stg[2 * BLK_PER_WAVE];  // one step of this wave's tile data (A blocks, then B blocks)
-  // global -> registers: half 0 = A blocks, half 1 = B blocks of K-step kt (clamped)
-  auto load_half = [&](int kt, int half) {
+  i32x4_t stg[2 * BLK_PER_WAVE];  // one step of this wave's tile data: A blocks 0-7, B blocks 8-15
+  // block q: global -> registers (K-step kt, clamped to the last step)
+  auto load_block = [&](int q, int kt) {
     const int ks = kt < nk ? kt : nk - 1;
-#pragma unroll
-    for (int q = 0; q < BLK_PER_WAVE; ++q) {
-      if (half == 0)
-        stg[q] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, a_off[q], ks * KB, 0);
-      else
-        stg[BLK_PER_WAVE + q] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, b_off[q], ks * KB, 0);
-    }
+    if (q < BLK_PER_WAVE)
+      stg[q] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, a_off[q], ks * KB, 0);
+    else
+      stg[q] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, b_off[q - BLK_PER_WAVE], ks * KB, 0);
   };
-  // registers -> LDS stage st
-  auto write_half = [&](int st, int half) {
-    uint8_t* dst = (half == 0 ? la_buf(st) : lb_buf(st)) + wave * BLK_PER_WAVE * 1024 + lane * 16;
-#pragma unroll
-    for (int q = 0; q < BLK_PER_WAVE; ++q)
-      *reinterpret_cast<i32x4_t*>(dst + q * 1024) = stg[half * BLK_PER_WAVE + q];
+  // block q: registers -> LDS stage st
+  auto write_block = [&](int q, int st) {
+    uint8_t* dst = (q < BLK_PER_WAVE ? la_buf(st) + q * 1024 : lb_buf(st) + (q - BLK_PER_WAVE) * 1024) +
+                   wave * BLK_PER_WAVE * 1024 + lane * 16;
+    *reinterpret_cast<i32x4_t*>(dst) = stg[q];
   };
   Frag<FP8> fa[2][4], fb[2][4];
   auto rd = [&](int st, int i, Frag<FP8> (&a)[4], Frag<FP8> (&b)[4]) {
@@ -262,22 +259,20 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   };
 
   // Pipeline.  Step kt computes LDS stage kt%2 while the registers hold step kt+1's
-  // tile data.  bf16 (4 substeps): substeps 0 and 1 write that data (A, then B)
-  // into stage (kt+1)%2, which every wave stopped reading at step kt-1's barrier;
-  // substeps 1 and 2 then load step kt+2 into the freed registers, so a load has
-  // three substeps to land before it is written.  The last substep waits for this
-  // wave's LDS writes and reads, then one barrier publishes stage kt+1, whose first
-  // fragments are read under the last substep's MFMAs.  fp8 (2 substeps) does the
-  // writes and loads in substep 0.  Register dependencies give the vmcnt waits.
-  // The scheduling groups interleave one LDS or memory operation per MFMA.
+  // tile data.  Those 16 blocks are written into stage (kt+1)%2 (which every wave
+  // stopped reading at step kt-1's barrier) over the first substeps, each block
+  // reloaded with step kt+2's data right after its write, so a load has a whole
+  // step to land and the LDS write traffic is spread evenly (bf16: 6/5/5 blocks in
+  // substeps 0-2; fp8: all in substep 0).  The last substep waits for this wave's
+  // LDS writes and reads, then one barrier publishes stage kt+1, whose first
+  // fragments are read under the last substep's MFMAs.  Register dependencies give
+  // the vmcnt waits; the scheduling groups interleave the LDS and memory
+  // operations with the MFMAs, fragment reads first.
   constexpr int RD = FP8 ? 16 : 8;  // LDS reads of a substep's fragments
-  constexpr int SUB_WA = 0, SUB_WB = NSUB == 4 ? 1 : 0, SUB_LA = NSUB == 4 ? 1 : 0, SUB_LB = NSUB == 4 ? 2 : 0;
-  load_half(0, 0);
-  load_half(0, 1);
-  write_half(0, 0);
-  write_half(0, 1);
-  load_half(1, 0);
-  load_half(1, 1);
+  constexpr int NBLK = 2 * BLK_PER_WAVE;
+  for (int q = 0; q < NBLK; ++q) load_block(q, 0);
+  for (int q = 0; q < NBLK; ++q) write_block(q, 0);
+  for (int q = 0; q < NBLK; ++q) load_block(q, 1);
   wait_lgkmcnt0();
   barrier_nofence();
   rd(0, 0, fa[0], fb[0]);
@@ -288,8 +283,10 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
     static_for<0, NSUB>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr int bi = i & 1;
-      constexpr bool WA = !LAST && i == SUB_WA, WB = !LAST && i == SUB_WB;
-      constexpr bool LA = !LAST && i == SUB_LA, LB = !LAST && i == SUB_LB;
+      // blocks [q0, q1) are written and reloaded in this substep
+      constexpr int q0 = NSUB == 4 ? (i == 0 ? 0 : i == 1 ? 6 : i == 2 ? 11 : NBLK) : (i == 0 ? 0 : NBLK);
+      constexpr int q1 = NSUB == 4 ? (i == 0 ? 6 : i == 1 ? 11 : NBLK) : NBLK;
+      constexpr int nq = LAST ? 0 : q1 - q0;
       constexpr bool RDN = i + 1 < NSUB || !LAST;
       // next substep's fragments first: they are on the MFMA critical path
       if constexpr (i + 1 < NSUB) {
@@ -299,14 +296,12 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
         barrier_nofence();
         rd(nxt, 0, fa[bi ^ 1], fb[bi ^ 1]);
       }
-      if constexpr (WA) write_half(nxt, 0);
-      if constexpr (WB) write_half(nxt, 1);
-      if constexpr (LA) load_half(kt + 2, 0);
-      if constexpr (LB) load_half(kt + 2, 1);
+      if constexpr (nq > 0) {
+        static_for<q0, q1>([&](auto qc) { write_block(decltype(qc)::value, nxt); });
+        static_for<q0, q1>([&](auto qc) { load_block(decltype(qc)::value, kt + 2); });
+      }
       mma(fa[bi], fb[bi]);
-      constexpr int n_ds = (WA ? BLK_PER_WAVE : 0) + (WB ? BLK_PER_WAVE : 0) + (RDN ? RD : 0);
-      constexpr int n_vm = (LA ? BLK_PER_WAVE : 0) + (LB ? BLK_PER_WAVE : 0);
-      sched_spread<n_ds, n_vm>();
+      sched_spread<(RDN ? RD : 0) + nq, nq>();
       __builtin_amdgcn_sched_barrier(0);
     });
   };
