@@ -1,6 +1,9 @@
-// Library-wide state of the kmoe C ABI: the thread-local error message and the
-// launch-status check every entry point ends with.
+// Library-wide state of the kmoe C ABI: the thread-local error message, the
+// launch-status check every entry point ends with, and the per-device CU count
+// that sizes persistent grids.
 #include <stdarg.h>
+
+#include <atomic>
 
 #include "kmoe_common.h"
 
@@ -24,6 +27,18 @@ int check_launch(const char* what) {
     return KMOE_ERR_LAUNCH;
   }
   return KMOE_OK;
+}
+
+int cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  cached[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 }  // namespace kmoe

@@ -23,6 +23,8 @@ namespace kmoe {
 
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
+// compute units of the current device (cached per device): the grid of persistent kernels
+int cu_count();
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -65,21 +65,28 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * KB + ((chu
 __host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 
 // (expert, row-tile) of row-slot `slot`, from the offsets; returns false if none.
+// One vector load gives lane e the row range of expert e (E <= 64); the walk over
+// the experts then reads the per-lane tile counts with readlane, so the lookup
+// costs one memory round trip instead of one per expert.
 __device__ __forceinline__ bool find_row_tile(const int32_t* __restrict__ offsets, int E, int slot, int& e_out,
                                               int& m0, int& m_end) {
+  const int lane = threadIdx.x & 63;
+  int lo = 0, hi = 0;
+  if (lane < E) {
+    lo = offsets[lane];
+    hi = offsets[lane + 1];
+  }
+  const int nt = (hi - lo + BM - 1) / BM;
   int base = 0;
-  int lo = offsets[0];
   for (int e = 0; e < E; ++e) {
-    const int hi = offsets[e + 1];
-    const int nt = (hi - lo + BM - 1) / BM;
-    if (slot < base + nt) {
+    const int n = __builtin_amdgcn_readlane(nt, e);
+    if (slot < base + n) {
       e_out = e;
-      m0 = lo + (slot - base) * BM;
-      m_end = hi;
+      m0 = __builtin_amdgcn_readlane(lo, e) + (slot - base) * BM;
+      m_end = __builtin_amdgcn_readlane(hi, e);
       return true;
     }
-    base += nt;
-    lo = hi;
+    base += n;
   }
   return false;
 }
@@ -215,16 +222,26 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   const int rsub = lane / CPR, pc = lane % CPR;
   uint32_t a_off[BLK_PER_WAVE], b_off[BLK_PER_WAVE];
   const int a_last = m_end - 1 - m0;
+  int ra[BLK_PER_WAVE];
 #pragma unroll
   for (int q = 0; q < BLK_PER_WAVE; ++q) {
     const int tr = (wave * BLK_PER_WAVE + q) * RPB + rsub;
-    int ra = tr < a_last ? tr : a_last;
-    if constexpr (GATHER) {
-      const int tok = row_token[m0 + ra];
-      ra = row_index ? row_index[tok] : tok;
+    ra[q] = tr < a_last ? tr : a_last;
+  }
+  if constexpr (GATHER) {
+    // batched: all row_token loads, then all row_index loads (two round trips)
+#pragma unroll
+    for (int q = 0; q < BLK_PER_WAVE; ++q) ra[q] = row_token[m0 + ra[q]];
+    if (row_index) {
+#pragma unroll
+      for (int q = 0; q < BLK_PER_WAVE; ++q) ra[q] = row_index[ra[q]];
     }
+  }
+#pragma unroll
+  for (int q = 0; q < BLK_PER_WAVE; ++q) {
+    const int tr = (wave * BLK_PER_WAVE + q) * RPB + rsub;
     const uint32_t chunk = (uint32_t)(pc ^ ((tr >> 1) & (CPR - 1))) << 4;
-    a_off[q] = (uint32_t)ra * (uint32_t)lda_bytes + chunk;
+    a_off[q] = (uint32_t)ra[q] * (uint32_t)lda_bytes + chunk;
     b_off[q] = (uint32_t)tr * (uint32_t)ldb_bytes + chunk;
   }
   i32x4_t stg[2 * BLK_PER_WAVE];  // one step of this wave's tile data: A blocks 0-7, B blocks 8-15
