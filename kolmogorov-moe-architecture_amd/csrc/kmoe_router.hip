@@ -3,11 +3,14 @@
 // MoELayer._compute_load_balance_loss / _compute_router_z_loss (moe.py:872-939).
 //
 // Layout: one workgroup = 4 waves = 64 tokens.  The d -> 128 layer runs on
-// v_mfma_f32_32x32x16_bf16 (each wave: 32 tokens x 64 hidden units) over a 4-stage
-// K pipeline: x rows and w_in rows go global -> LDS directly (global_load_lds), so
-// three K-steps of loads are in flight while one is computed.  The hidden
+// v_mfma_f32_32x32x16_bf16 (each wave: 32 tokens x 64 hidden units) over a K
+// pipeline of as many stages as fit in LDS (K-steps of 128 or 256 bytes per row):
+// x rows and w_in rows go global -> LDS directly (global_load_lds), so all but one
+// stage are in flight while one is computed.  The hidden
 // activations go through LDS (fp32) for the 128 -> E layer, computed on the vector
-// ALUs in fp32; softmax/top-k then run one token per thread.
+// ALUs in fp32; softmax/top-k then run one token per thread with the token's logits
+// in registers, and the logits, aux partials and outputs leave through coalesced,
+// all-thread copies and wave reductions.
 #include "kmoe_common.h"
 
 namespace {
@@ -16,17 +19,28 @@ constexpr int RT_TOK = 64;        // tokens per workgroup
 constexpr int RT_THREADS = 256;   // 4 waves: 2 (token halves) x 2 (hidden halves)
 constexpr int RT_HID = KMOE_ROUTER_HIDDEN;
 constexpr int HSTR = RT_HID + 1;  // padded LDS row stride (floats) of the hidden tile
-constexpr int RT_STAGES = 4;      // K pipeline depth (3 K-steps of loads in flight)
-constexpr int RT_XT = RT_TOK * 128;   // x tile of one K-step: 64 rows x 128 bytes (64 bf16)
-constexpr int RT_WT = RT_HID * 128;   // w_in tile of one K-step: 128 rows x 128 bytes
-constexpr int RT_STAGE = RT_XT + RT_WT;
-constexpr int RT_LOADS = 6;       // direct-to-LDS instructions per wave and K-step (2 x + 4 w_in)
+// One K-step covers RKB bytes of every row (RKB = 128 or 256: 64 or 128 bf16).
+template <int RKB>
+struct RtGeom {
+  static constexpr int XT = RT_TOK * RKB;      // x tile of one K-step (64 rows)
+  static constexpr int WT = RT_HID * RKB;      // w_in tile of one K-step (128 rows)
+  static constexpr int STAGE = XT + WT;
+  static constexpr int RPB = 1024 / RKB;       // rows per 1 KiB load block
+  static constexpr int CPR = RKB / 16;         // 16-byte chunks per row
+  static constexpr int XBLK = RT_TOK / RPB / 4;  // x load blocks per wave per K-step
+  static constexpr int WBLK = RT_HID / RPB / 4;  // w_in load blocks per wave per K-step
+  static constexpr int LOADS = XBLK + WBLK;    // direct-to-LDS instructions per wave per K-step
+  // Byte offset of 16-byte chunk `chunk` of row `row`: the XOR spreads the 16 lanes
+  // of each LDS read pass (16 consecutive rows, one chunk) over distinct banks.
+  __device__ static __forceinline__ int swz(int row, int chunk) {
+    return row * RKB + ((chunk ^ (RKB == 128 ? ((row >> 1) & 7) : (row & 15))) << 4);
+  }
+};
+// K pipeline depth: as many stages as fit beside w_out (NE padded rows of 132 fp32)
+template <int NE, int RKB>
+constexpr int rt_stages() { return (160 * 1024 - NE * (RT_HID + 4) * 4) / RtGeom<RKB>::STAGE; }
 
-// Byte offset of 16-byte chunk `chunk` of row `row` in a 128-byte-row tile; the
-// XOR by (row/2)%8 spreads the 16 lanes of each LDS read pass over distinct banks.
-__device__ __forceinline__ int rswz(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
-
-template <int NE>
+template <int NE, int RKB>
 __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __restrict__ x,
                                                             const int32_t* __restrict__ row_index, int64_t T, int d,
                                                             const uint16_t* __restrict__ w_in,
@@ -34,13 +48,19 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
                                                             const float* __restrict__ bias, int k,
                                                             float* __restrict__ logits, int64_t* __restrict__ topk_idx,
                                                             float* __restrict__ topk_w, float* __restrict__ partials) {
+  using G = RtGeom<RKB>;
+  constexpr int RT_STAGES = rt_stages<NE, RKB>();
+  constexpr int RT_STAGE = G::STAGE;
+  static_assert(RT_STAGES >= 2, "K pipeline");
+  constexpr int WOS = RT_HID + 4;  // padded w_out row (floats): the 4 lanes of a token hit distinct banks
+  constexpr int LGS = NE + 4;      // logits / probabilities row stride (floats), 16-byte aligned rows
   __shared__ __attribute__((aligned(1024))) uint8_t smem[RT_STAGES * RT_STAGE];
-  __shared__ float wo[NE * RT_HID];  // w_out as fp32
-  // after the K loop smem holds: hs[64][HSTR], lg[64][NE+1], pe[64][NE+1], lse2[64]
+  __shared__ __attribute__((aligned(16))) float wo[NE * WOS];  // w_out as fp32
+  // after the K loop smem holds: hs[64][HSTR], lg[64][LGS], pe[64][LGS], lse2[64]
   float* hs = reinterpret_cast<float*>(smem);
-  float* lg = hs + RT_TOK * HSTR;
-  float* pe = lg + RT_TOK * (NE + 1);
-  float* lse2 = pe + RT_TOK * (NE + 1);
+  float* lg = hs + RT_TOK * HSTR;  // 64 * 129 floats = 33024 bytes: lg rows stay 16-byte aligned
+  float* pe = lg + RT_TOK * LGS;
+  float* lse2 = pe + RT_TOK * LGS;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -50,67 +70,78 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   const int64_t tok0 = (int64_t)blockIdx.x * RT_TOK;
 
   for (int i = tid; i < NE * RT_HID; i += RT_THREADS) {
-    const int e = i / RT_HID;
-    wo[i] = e < E ? bf16_to_f32(w_out[i]) : 0.0f;
+    const int e = i / RT_HID, j = i % RT_HID;
+    wo[e * WOS + j] = e < E ? bf16_to_f32(w_out[i]) : 0.0f;
   }
 
   // ---- per-lane sources of the direct-to-LDS loads (block q fills tile rows
-  // [8q, 8q+8), lane l lands at byte 16*l of the block: row 8q + l/8, physical
-  // chunk l%8, holding logical chunk (l%8) ^ ((row/2)%8))
-  const int rsub = lane >> 3, pc = lane & 7;
-  const uint8_t* xsrc[2];
-  uint32_t wsrc[4];
+  // [RPB q, RPB q + RPB), lane l lands at byte 16*l of the block: row RPB q + l/CPR,
+  // physical chunk l%CPR, holding the logical chunk that swz() maps there)
+  const int rsub = lane / G::CPR, pc = lane % G::CPR;
+  auto chunk_of = [&](int tr) { return (G::swz(tr, pc) - tr * RKB); };
+  // fixed sizes (the largest geometry): a template-dependent local array size keeps
+  // hipcc from emitting the kernel's host launch stub
+  static_assert(G::XBLK <= 4 && G::WBLK <= 8, "load blocks per wave");
+  const uint8_t* xsrc[4];
+  uint32_t wsrc[8];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int tr = (wave * 2 + q) * 8 + rsub;
+  for (int q = 0; q < G::XBLK; ++q) {
+    const int tr = (wave * G::XBLK + q) * G::RPB + rsub;
     int64_t t = tok0 + tr;
     t = t < T ? t : T - 1;
     const int64_t xr = row_index ? (int64_t)row_index[t] : t;
-    xsrc[q] = reinterpret_cast<const uint8_t*>(x) + xr * (int64_t)d * 2 + ((pc ^ ((tr >> 1) & 7)) << 4);
+    xsrc[q] = reinterpret_cast<const uint8_t*>(x) + xr * (int64_t)d * 2 + chunk_of(tr);
   }
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int tr = (wave * 4 + q) * 8 + rsub;
-    wsrc[q] = (uint32_t)tr * (uint32_t)d * 2u + ((pc ^ ((tr >> 1) & 7)) << 4);
+  for (int q = 0; q < G::WBLK; ++q) {
+    const int tr = (wave * G::WBLK + q) * G::RPB + rsub;
+    wsrc[q] = (uint32_t)tr * (uint32_t)d * 2u + (uint32_t)chunk_of(tr);
   }
   const uint8_t* wbase = reinterpret_cast<const uint8_t*>(w_in);
   auto issue = [&](int kt) {
     uint8_t* st = smem + (kt % RT_STAGES) * RT_STAGE;
-    const int kb = kt * 128;
+    const int kb = kt * RKB;
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-      __builtin_amdgcn_global_load_lds(xsrc[q] + kb, (KMOE_LDS void*)(st + (wave * 2 + q) * 1024), 16, 0, 0);
+    for (int q = 0; q < G::XBLK; ++q)
+      __builtin_amdgcn_global_load_lds(xsrc[q] + kb, (KMOE_LDS void*)(st + (wave * G::XBLK + q) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      __builtin_amdgcn_global_load_lds(wbase + wsrc[q] + kb, (KMOE_LDS void*)(st + RT_XT + (wave * 4 + q) * 1024), 16,
-                                       0, 0);
+    for (int q = 0; q < G::WBLK; ++q)
+      __builtin_amdgcn_global_load_lds(wbase + wsrc[q] + kb,
+                                       (KMOE_LDS void*)(st + G::XT + (wave * G::WBLK + q) * 1024), 16, 0, 0);
   };
 
-  // ---- layer 1 on MFMA: wave (wm, wn) computes 32 tokens x 64 hidden
+  // ---- layer 1 on MFMA: wave (wm, wn) computes 32 tokens x 64 hidden; the next
+  // substep's fragments are read before the current substep's MFMAs
   f32x16_t acc[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
-  const int nk = d / 64;
+  const int nk = d * 2 / RKB;
   for (int s = 0; s < RT_STAGES - 1 && s < nk; ++s) issue(s);
+  constexpr int NSUB = RKB / 32;  // MFMA K-substeps per K-step
   for (int kt = 0; kt < nk; ++kt) {
     if (kt + RT_STAGES - 2 < nk)
-      wait_vmcnt<(RT_STAGES - 2) * RT_LOADS>();
+      wait_vmcnt<(RT_STAGES - 2) * G::LOADS>();
     else
       wait_vmcnt<0>();
     barrier_nofence();
     if (kt + RT_STAGES - 1 < nk) issue(kt + RT_STAGES - 1);
     const uint8_t* xt = smem + (kt % RT_STAGES) * RT_STAGE;
-    const uint8_t* wt = xt + RT_XT;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    const uint8_t* wt = xt + G::XT;
+    bf16x8_t a[2], b0[2], b1[2];
+    auto rdf = [&](int i, int buf) {
       const int ch = 2 * i + lh;
-      const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(xt + rswz(wm * 32 + lr, ch));
-      const bf16x8_t b0 = *reinterpret_cast<const bf16x8_t*>(wt + rswz(wn * 64 + lr, ch));
-      const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(wt + rswz(wn * 64 + 32 + lr, ch));
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b0, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b1, acc[1], 0, 0, 0);
+      a[buf] = *reinterpret_cast<const bf16x8_t*>(xt + G::swz(wm * 32 + lr, ch));
+      b0[buf] = *reinterpret_cast<const bf16x8_t*>(wt + G::swz(wn * 64 + lr, ch));
+      b1[buf] = *reinterpret_cast<const bf16x8_t*>(wt + G::swz(wn * 64 + 32 + lr, ch));
+    };
+    rdf(0, 0);
+#pragma unroll
+    for (int i = 0; i < NSUB; ++i) {
+      if (i + 1 < NSUB) rdf(i + 1, (i + 1) & 1);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i & 1], b0[i & 1], acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i & 1], b1[i & 1], acc[1], 0, 0, 0);
     }
   }
   __syncthreads();  // stage buffers are reused below
@@ -137,7 +168,7 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
       const float h0 = hrow[j], h1 = hrow[j + 1], h2 = hrow[j + 2], h3 = hrow[j + 3];
 #pragma unroll
       for (int q = 0; q < NE / 4; ++q) {
-        const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(&wo[(part + 4 * q) * RT_HID + j]);
+        const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(&wo[(part + 4 * q) * WOS + j]);
         l2[q] = fmaf(h0, wv[0], l2[q]);
         l2[q] = fmaf(h1, wv[1], l2[q]);
         l2[q] = fmaf(h2, wv[2], l2[q]);
@@ -147,76 +178,92 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
 #pragma unroll
     for (int q = 0; q < NE / 4; ++q) {
       const int e = part + 4 * q;
-      if (e < E) lg[tl * (NE + 1) + e] = l2[q] + (bias ? bias[e] : 0.0f);
+      lg[tl * LGS + e] = e < E ? l2[q] + (bias ? bias[e] : 0.0f) : 0.0f;
     }
   }
   __syncthreads();
 
-  // ---- softmax, top-k, outputs: one token per thread (threads 0..63)
+  // ---- softmax, top-k, outputs: one token per thread (threads 0..63), the token's
+  // logits in registers
+  const int64_t ntok = T - tok0 < RT_TOK ? T - tok0 : RT_TOK;
   if (tid < RT_TOK) {
     const int64_t t = tok0 + tid;
-    const float* L = lg + tid * (NE + 1);
-    float* P = pe + tid * (NE + 1);
+    float L[NE];
+#pragma unroll
+    for (int q = 0; q < NE / 4; ++q) {
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(lg + tid * LGS + 4 * q);
+      L[4 * q] = v[0];
+      L[4 * q + 1] = v[1];
+      L[4 * q + 2] = v[2];
+      L[4 * q + 3] = v[3];
+    }
+    float* P = pe + tid * LGS;
     if (t < T) {
       float mx = L[0];
-      for (int e = 1; e < E; ++e) mx = fmaxf(mx, L[e]);
+#pragma unroll
+      for (int e = 1; e < NE; ++e)
+        if (e < E) mx = fmaxf(mx, L[e]);
       float s = 0.0f;
-      for (int e = 0; e < E; ++e) s += __expf(L[e] - mx);
+      float ex[NE];
+#pragma unroll
+      for (int e = 0; e < NE; ++e) {
+        ex[e] = e < E ? __expf(L[e] - mx) : 0.0f;
+        s += ex[e];
+      }
       const float inv_s = 1.0f / s;
       const float lse = mx + __logf(s);
-      float* lout = logits + t * E;
-      for (int e = 0; e < E; ++e) {
-        lout[e] = L[e];
-        P[e] = __expf(L[e] - mx) * inv_s;
-      }
+#pragma unroll
+      for (int q = 0; q < NE / 4; ++q)
+        *reinterpret_cast<f32x4_t*>(P + 4 * q) =
+            f32x4_t{ex[4 * q] * inv_s, ex[4 * q + 1] * inv_s, ex[4 * q + 2] * inv_s, ex[4 * q + 3] * inv_s};
       lse2[tid] = lse * lse;
       if (k > 0) {
-        // Two identical selection passes (sum of the selected exps, then the
-        // outputs) keep everything in registers.
+        // k selections over the registers; strict '>' keeps the lower index on ties
+        uint64_t taken = 0;
+        int sel[8];
+        float sev[8];
         float ssum = 0.0f;
-        float inv = 0.0f;
-        for (int pass = 0; pass < 2; ++pass) {
-          uint64_t taken = 0;
-          for (int j = 0; j < k; ++j) {
-            int bi = -1;
-            float bv = 0.0f;
-            for (int e = 0; e < E; ++e) {
-              if ((taken >> e) & 1ull) continue;
-              if (bi < 0 || L[e] > bv) {  // strict: equal logits keep the lower index
-                bi = e;
-                bv = L[e];
-              }
-            }
-            taken |= 1ull << bi;
-            const float ev = __expf(bv - mx);
-            if (pass == 0) {
-              ssum += ev;
-            } else {
-              topk_idx[t * k + j] = bi;
-              topk_w[t * k + j] = ev * inv;
+        for (int j = 0; j < k; ++j) {
+          int bi = -1;
+          float bv = 0.0f;
+#pragma unroll
+          for (int e = 0; e < NE; ++e) {
+            const bool ok = e < E && !((taken >> e) & 1ull);
+            if (ok && (bi < 0 || L[e] > bv)) {
+              bi = e;
+              bv = L[e];
             }
           }
-          inv = 1.0f / ssum;
+          taken |= 1ull << bi;
+          sel[j] = bi;
+          sev[j] = __expf(bv - mx);
+          ssum += sev[j];
+        }
+        const float inv = 1.0f / ssum;
+        for (int j = 0; j < k; ++j) {
+          topk_idx[t * k + j] = sel[j];
+          topk_w[t * k + j] = sev[j] * inv;
         }
       }
     } else {
-      for (int e = 0; e < E; ++e) P[e] = 0.0f;
+#pragma unroll
+      for (int q = 0; q < NE / 4; ++q) *reinterpret_cast<f32x4_t*>(P + 4 * q) = f32x4_t{0.f, 0.f, 0.f, 0.f};
       lse2[tid] = 0.0f;
     }
   }
   __syncthreads();
 
-  // ---- per-block aux partials, summed over tokens in a fixed order
+  // ---- logits out: the block's ntok x E floats are contiguous; coalesced copy
+  for (int i = tid; i < ntok * E; i += RT_THREADS) logits[tok0 * E + i] = lg[(i / E) * LGS + i % E];
+
+  // ---- per-block aux partials: column c of the block's 64 tokens (c < E: the
+  // probabilities, c == E: lse^2) summed by one wave with a fixed shuffle tree
   if (partials) {
     float* pb = partials + (int64_t)blockIdx.x * (E + 1);
-    if (tid < E) {
-      float s = 0.0f;
-      for (int i = 0; i < RT_TOK; ++i) s += pe[i * (NE + 1) + tid];
-      pb[tid] = s;
-    } else if (tid == E) {
-      float s = 0.0f;
-      for (int i = 0; i < RT_TOK; ++i) s += lse2[i];
-      pb[E] = s;
+    for (int c = wave; c <= E; c += RT_THREADS / 64) {
+      const float v = c < E ? pe[lane * LGS + c] : lse2[lane];
+      const float sum = wave_sum(v);
+      if (lane == 0) pb[c] = sum;
     }
   }
 }
@@ -274,9 +321,17 @@ extern "C" int kmoe_router(const void* x, const int32_t* row_index, int64_t T, i
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wi = static_cast<const uint16_t*>(w_in);
   const uint16_t* wo = static_cast<const uint16_t*>(w_out);
-#define KMOE_ROUTER_LAUNCH(NE_)                                                                          \
-  hipLaunchKernelGGL(router_kernel<NE_>, grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, wo, E, logit_bias, k, \
-                     logits, topk_idx, topk_w, partials)
+  // wide K-steps (256 bytes of every row, half the barriers) when d allows and at
+  // least three stages fit; 128-byte steps otherwise
+#define KMOE_ROUTER_LAUNCH(NE_)                                                                                  \
+  do {                                                                                                           \
+    if (d % 128 == 0 && rt_stages<NE_, 256>() >= 3)                                                              \
+      hipLaunchKernelGGL((router_kernel<NE_, 256>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, wo, E, \
+                         logit_bias, k, logits, topk_idx, topk_w, partials);                                       \
+    else                                                                                                         \
+      hipLaunchKernelGGL((router_kernel<NE_, 128>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, wo, E, \
+                         logit_bias, k, logits, topk_idx, topk_w, partials);                                       \
+  } while (0)
   if (E <= 8)
     KMOE_ROUTER_LAUNCH(8);
   else if (E <= 16)
