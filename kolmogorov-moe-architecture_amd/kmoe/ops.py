@@ -44,25 +44,31 @@ _STAGE_EVENTS: Optional[list] = None
 class _Stage:
     def __init__(self, name):
         self.name = name
+        self.on = _STAGE_EVENTS is not None and (_STAGE_ONLY is None or name in _STAGE_ONLY)
 
     def __enter__(self):
-        if _STAGE_EVENTS is not None:
+        if self.on:
             self.start = torch.cuda.Event(enable_timing=True)
             self.start.record()
         return self
 
     def __exit__(self, *exc):
-        if _STAGE_EVENTS is not None:
+        if self.on:
             end = torch.cuda.Event(enable_timing=True)
             end.record()
             _STAGE_EVENTS.append((self.name, self.start, end))
         return False
 
 
-def set_stage_timing(events: Optional[list]):
-    """Install (a list) or remove (None) the per-stage event recorder."""
-    global _STAGE_EVENTS
+_STAGE_ONLY: Optional[set] = None
+
+
+def set_stage_timing(events: Optional[list], only: Optional[set] = None):
+    """Install (a list) or remove (None) the per-stage event recorder; `only`
+    restricts it to the named stages."""
+    global _STAGE_EVENTS, _STAGE_ONLY
     _STAGE_EVENTS = events
+    _STAGE_ONLY = set(only) if only is not None else None
 
 
 class RouterOut(NamedTuple):
