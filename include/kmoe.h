@@ -93,7 +93,8 @@ int kmoe_aux_loss(const float* partials, int64_t T, int E, const int32_t* counts
  * xperm_dtype BF16 copies rows; FP8_E4M3 quantises each row with the per-token
  * scale amax(|x[row]|)/448 written to xperm_scale (one per permuted row).
  * xperm may be NULL with BF16: only the tables are written (for
- * kmoe_gemm_gate_up_rows, which gathers the rows itself).
+ * kmoe_gemm_gate_up_rows, which gathers the rows itself).  FP8_E4M3 rows need
+ * d <= 8192 (a row is quantised from registers; KMOE_ERR_UNSUPPORTED beyond).
  *   topk_w dtype: w_dtype (BF16 or F32).  workspace: kmoe_dispatch_workspace_bytes. */
 size_t kmoe_dispatch_workspace_bytes(int64_t T, int k, int E);
 int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
@@ -103,7 +104,8 @@ int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T, int d, con
                   void* stream);
 
 /* Row gather: out[r] = x[row_token[r]] for r < n_rows (rows with row_token < 0 are
- * zero-filled).  out_dtype BF16 (copy) or FP8_E4M3 (per-row scale to out_scale).
+ * zero-filled).  out_dtype BF16 (copy) or FP8_E4M3 (per-row scale to out_scale;
+ * d <= 8192).
  * n_rows_dev (nullable): device int32 holding the number of valid rows.      */
 int kmoe_gather_rows(const void* x, const int32_t* row_token, int64_t n_rows, const int32_t* n_rows_dev,
                      int d, void* out, int out_dtype, float* out_scale, void* stream);
@@ -142,7 +144,7 @@ int kmoe_gemm_down(const void* h, const float* h_scale, int in_dtype, const int3
                    int d, int F, int64_t max_rows, const void* w3_packed, const float* w3_scale,
                    void* y, void* stream);
 /* Per-row fp8 quantisation of a bf16 matrix (used between the fp8 GEMMs):
- * scale[r] = amax(|in[r,:]|)/448, out = e4m3(sat(in/scale)), RNE.          */
+ * scale[r] = amax(|in[r,:]|)/448, out = e4m3(sat(in/scale)), RNE; cols <= 8192. */
 int kmoe_quant_rows_fp8(const void* in, int64_t rows, const int32_t* n_rows_dev, int cols, uint8_t* out,
                         float* scale, void* stream);
 /* Convenience: gate_up + down on bf16 (the reference's native entry point). */

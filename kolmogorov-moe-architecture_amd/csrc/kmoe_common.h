@@ -120,3 +120,43 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+
+// ---------------------------------------------------------------- fp8 rows
+// One wave quantises one bf16 row of `nvec` 16-byte vectors to e4m3 with the
+// per-row scale amax/448: the row is read once into registers (lane l holds
+// vectors l, l+64, ...; up to ROW_REGS per lane, i.e. rows of up to 8192 bf16),
+// its amax reduced across the wave, then quantised from the registers.
+constexpr int ROW_REGS = 16;
+struct RowRegs {
+  i32x4_t v[ROW_REGS];
+};
+__device__ __forceinline__ float bf16_pair_absmax(uint32_t w) {
+  return fmaxf(fabsf(__uint_as_float(w << 16)), fabsf(__uint_as_float(w & 0xffff0000u)));
+}
+__device__ __forceinline__ float load_row_amax(const i32x4_t* __restrict__ src, int nvec, int lane, RowRegs& r) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < ROW_REGS; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+      r.v[i] = src[v];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) amax = fmaxf(amax, bf16_pair_absmax((uint32_t)r.v[i][q]));
+    }
+  }
+  return wave_max(amax);
+}
+// e4m3 bytes of one 16-byte bf16 vector (8 values) as two 32-bit words
+__device__ __forceinline__ void quant_vec_e4m3(const i32x4_t& val, float inv, uint32_t& lo, uint32_t& hi) {
+  lo = 0;
+  hi = 0;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const uint32_t w0 = (uint32_t)val[q];
+    lo |= f32_to_e4m3(__uint_as_float(w0 << 16) * inv) << (16 * q);
+    lo |= f32_to_e4m3(__uint_as_float(w0 & 0xffff0000u) * inv) << (16 * q + 8);
+    const uint32_t w1 = (uint32_t)val[q + 2];
+    hi |= f32_to_e4m3(__uint_as_float(w1 << 16) * inv) << (16 * q);
+    hi |= f32_to_e4m3(__uint_as_float(w1 & 0xffff0000u) * inv) << (16 * q + 8);
+  }
+}

@@ -75,13 +75,12 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ 
   }
 }
 
-template <bool FP8>
+// Tables of a block of DTB tokens, then (xperm != nullptr: the bf16 copy) the rows.
 __global__ __launch_bounds__(DTHREADS) void permute_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, int64_t T, int d,
     const int64_t* __restrict__ idx, const void* __restrict__ wsrc, int w_dtype, int k, int E, int64_t capacity,
     const int32_t* __restrict__ block_base, const int32_t* __restrict__ offsets, int32_t* __restrict__ row_token,
-    int32_t* __restrict__ slot_row, float* __restrict__ slot_w, void* __restrict__ xperm,
-    float* __restrict__ xperm_scale) {
+    int32_t* __restrict__ slot_row, float* __restrict__ slot_w, uint16_t* __restrict__ xperm) {
   __shared__ int wave_cnt[DTHREADS / 64][KMOE_MAX_EXPERTS];
   __shared__ int running[KMOE_MAX_EXPERTS];
   __shared__ int dest[DTB * 8];  // k <= 8
@@ -134,82 +133,75 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
     __syncthreads();
   }
 
-  // ---- row gather: every 16-byte chunk of the block's token rows is read once
-  // and written to the token's k permuted rows; 4 chunks in flight per thread.
+  // ---- row gather (bf16 copy): every 16-byte chunk of the block's token rows is
+  // read once and written to the token's k permuted rows; 4 chunks in flight per
+  // thread.  Without xperm only the tables are written.
+  if (xperm == nullptr) return;
   const int64_t ntok = min<int64_t>(DTB, T - t0);
   const int nvec = d / 8;  // 16-byte vectors per row
-  if (!FP8) {
-    if (xperm == nullptr) return;  // tables only: the GEMM gathers the rows
-    const int64_t total = ntok * nvec;
-    for (int64_t c0 = tid; c0 < total; c0 += 4 * DTHREADS) {
-      i32x4_t val[4];
+  const int64_t total = ntok * nvec;
+  for (int64_t c0 = tid; c0 < total; c0 += 4 * DTHREADS) {
+    i32x4_t val[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t c = c0 + (int64_t)u * DTHREADS;
-        if (c < total) {
-          const int64_t tl = c / nvec, v = c - tl * nvec;
-          const int64_t t = t0 + tl;
-          const int64_t xr = row_index ? (int64_t)row_index[t] : t;
-          val[u] = reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d)[v];
-        }
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = c0 + (int64_t)u * DTHREADS;
+      if (c < total) {
+        const int64_t tl = c / nvec, v = c - tl * nvec;
+        const int64_t t = t0 + tl;
+        const int64_t xr = row_index ? (int64_t)row_index[t] : t;
+        val[u] = reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d)[v];
       }
+    }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t c = c0 + (int64_t)u * DTHREADS;
-        if (c < total) {
-          const int64_t tl = c / nvec, v = c - tl * nvec;
-          for (int j = 0; j < k; ++j) {
-            const int row = dest[tl * k + j];
-            if (row >= 0) reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(xperm) + (int64_t)row * d)[v] = val[u];
-          }
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = c0 + (int64_t)u * DTHREADS;
+      if (c < total) {
+        const int64_t tl = c / nvec, v = c - tl * nvec;
+        for (int j = 0; j < k; ++j) {
+          const int row = dest[tl * k + j];
+          if (row >= 0) reinterpret_cast<i32x4_t*>(xperm + (int64_t)row * d)[v] = val[u];
         }
       }
     }
-  } else {
-    // fp8: one wave per token (the per-token amax needs the whole row)
-    for (int64_t tl = wave; tl < ntok; tl += DTHREADS / 64) {
-      const int64_t t = t0 + tl;
-      const int64_t xr = row_index ? (int64_t)row_index[t] : t;
-      const i32x4_t* src = reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d);
-      float amax = 0.0f;
-      for (int v = lane; v < nvec; v += 64) {
-        const i32x4_t val = src[v];
+  }
+}
+
+// fp8 rows of the dispatch: one wave per token quantises the token's row once
+// (register-resident, per-token scale amax/448) and writes it to the token's kept
+// permuted rows (slot_row of its k assignments), with their scales.
+__global__ __launch_bounds__(256) void quant_scatter_kernel(const uint16_t* __restrict__ x,
+                                                            const int32_t* __restrict__ row_index, int64_t T,
+                                                            int d, int k, const int32_t* __restrict__ slot_row,
+                                                            uint8_t* __restrict__ xperm,
+                                                            float* __restrict__ xperm_scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  int rows[8];
+  bool any = false;
+  for (int j = 0; j < k; ++j) {
+    rows[j] = slot_row[t * k + j];
+    any |= rows[j] >= 0;
+  }
+  if (!any) return;  // every assignment of the token was dropped
+  const int nvec = d / 8;
+  const int64_t xr = row_index ? (int64_t)row_index[t] : t;
+  RowRegs r;
+  const float amax = load_row_amax(reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d), nvec, lane, r);
+  const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+  uint32_t q[2 * ROW_REGS];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) << 16)));
-          amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) & 0xffff0000u)));
-        }
-      }
-      amax = wave_max(amax);
-      const float scale = amax / 448.0f;
-      const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
-      for (int v = lane; v < nvec; v += 64) {
-        const i32x4_t val = src[v];
-        uint32_t lo = 0, hi = 0;
+  for (int i = 0; i < ROW_REGS; ++i)
+    if (lane + 64 * i < nvec) quant_vec_e4m3(r.v[i], inv, q[2 * i], q[2 * i + 1]);
+  for (int j = 0; j < k; ++j) {
+    if (rows[j] < 0) continue;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(xperm + (int64_t)rows[j] * d);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const uint32_t w0 = (uint32_t)val[q];
-          lo |= f32_to_e4m3(__uint_as_float(w0 << 16) * inv) << (16 * q);
-          lo |= f32_to_e4m3(__uint_as_float(w0 & 0xffff0000u) * inv) << (16 * q + 8);
-          const uint32_t w1 = (uint32_t)val[q + 2];
-          hi |= f32_to_e4m3(__uint_as_float(w1 << 16) * inv) << (16 * q);
-          hi |= f32_to_e4m3(__uint_as_float(w1 & 0xffff0000u) * inv) << (16 * q + 8);
-        }
-        for (int j = 0; j < k; ++j) {
-          const int row = dest[tl * k + j];
-          if (row >= 0) {
-            uint32_t* o = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(xperm) + (int64_t)row * d) + 2 * v;
-            o[0] = lo;
-            o[1] = hi;
-          }
-        }
-      }
-      if (lane == 0)
-        for (int j = 0; j < k; ++j) {
-          const int row = dest[tl * k + j];
-          if (row >= 0) xperm_scale[row] = scale;
-        }
+    for (int i = 0; i < ROW_REGS; ++i) {
+      const int v = lane + 64 * i;
+      if (v < nvec) *reinterpret_cast<uint2*>(dst + 2 * v) = make_uint2(q[2 * i], q[2 * i + 1]);
     }
+    if (lane == 0) xperm_scale[rows[j]] = amax / 448.0f;
   }
 }
 
@@ -245,31 +237,17 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const uint16_t* __rest
       return;
     }
     const i32x4_t* src = reinterpret_cast<const i32x4_t*>(x + (int64_t)tok * d);
-    float amax = 0.0f;
-    for (int v = lane; v < nvec; v += 64) {
-      const i32x4_t val = src[v];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) << 16)));
-        amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) & 0xffff0000u)));
-      }
-    }
-    amax = wave_max(amax);
+    RowRegs rr;  // d <= 64 * 8 * ROW_REGS (checked on the host)
+    const float amax = load_row_amax(src, nvec, lane, rr);
     const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
-    for (int v = lane; v < nvec; v += 64) {
-      const i32x4_t val = src[v];
-      uint32_t lo = 0, hi = 0;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const uint32_t w0 = (uint32_t)val[q];
-        lo |= f32_to_e4m3(__uint_as_float(w0 << 16) * inv) << (16 * q);
-        lo |= f32_to_e4m3(__uint_as_float(w0 & 0xffff0000u) * inv) << (16 * q + 8);
-        const uint32_t w1 = (uint32_t)val[q + 2];
-        hi |= f32_to_e4m3(__uint_as_float(w1 << 16) * inv) << (16 * q);
-        hi |= f32_to_e4m3(__uint_as_float(w1 & 0xffff0000u) * inv) << (16 * q + 8);
+    for (int i = 0; i < ROW_REGS; ++i) {
+      const int v = lane + 64 * i;
+      if (v < nvec) {
+        uint32_t lo, hi;
+        quant_vec_e4m3(rr.v[i], inv, lo, hi);
+        *reinterpret_cast<uint2*>(dst + 2 * v) = make_uint2(lo, hi);
       }
-      dst[2 * v] = lo;
-      dst[2 * v + 1] = hi;
     }
     if (lane == 0) out_scale[r] = amax / 448.0f;
   }
@@ -302,6 +280,8 @@ extern "C" int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T,
                "kmoe_dispatch: xperm dtype must be bf16 or fp8_e4m3");
   KMOE_REQUIRE(xperm_dtype != KMOE_DTYPE_FP8_E4M3 || xperm_scale, KMOE_ERR_NULL,
                "kmoe_dispatch: fp8 output needs xperm_scale");
+  KMOE_REQUIRE(xperm_dtype != KMOE_DTYPE_FP8_E4M3 || d <= 64 * 8 * ROW_REGS, KMOE_ERR_UNSUPPORTED,
+               "kmoe_dispatch: fp8 rows need d <= %d (d=%d)", 64 * 8 * ROW_REGS, d);
   const size_t need = kmoe_dispatch_workspace_bytes(T, k, E);
   KMOE_REQUIRE(workspace && workspace_bytes >= need, KMOE_ERR_WORKSPACE,
                "kmoe_dispatch: workspace %zu < %zu bytes", workspace_bytes, need);
@@ -318,14 +298,13 @@ extern "C" int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T,
   hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, nblk, E, capacity, block_base, counts,
                      offsets);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
-  if (xperm_dtype == KMOE_DTYPE_BF16)
-    hipLaunchKernelGGL(permute_kernel<false>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
-                       topk_idx, topk_w, w_dtype, k, E, capacity, block_base, offsets, row_token, slot_row, slot_w,
-                       xperm, xperm_scale);
-  else
-    hipLaunchKernelGGL(permute_kernel<true>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
-                       topk_idx, topk_w, w_dtype, k, E, capacity, block_base, offsets, row_token, slot_row, slot_w,
-                       xperm, xperm_scale);
+  const bool fp8 = xperm_dtype == KMOE_DTYPE_FP8_E4M3;
+  hipLaunchKernelGGL(permute_kernel, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d, topk_idx,
+                     topk_w, w_dtype, k, E, capacity, block_base, offsets, row_token, slot_row, slot_w,
+                     fp8 ? nullptr : static_cast<uint16_t*>(xperm));
+  if (fp8)
+    hipLaunchKernelGGL(quant_scatter_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0, s, xp,
+                       row_index, T, d, k, slot_row, static_cast<uint8_t*>(xperm), xperm_scale);
   return kmoe::check_launch("kmoe_dispatch");
 }
 
@@ -337,6 +316,8 @@ extern "C" int kmoe_gather_rows(const void* x, const int32_t* row_token, int64_t
   KMOE_REQUIRE(out_dtype == KMOE_DTYPE_BF16 || out_dtype == KMOE_DTYPE_FP8_E4M3, KMOE_ERR_DTYPE,
                "kmoe_gather_rows: out dtype must be bf16 or fp8_e4m3");
   KMOE_REQUIRE(out_dtype != KMOE_DTYPE_FP8_E4M3 || out_scale, KMOE_ERR_NULL, "kmoe_gather_rows: fp8 needs out_scale");
+  KMOE_REQUIRE(out_dtype != KMOE_DTYPE_FP8_E4M3 || d <= 64 * 8 * ROW_REGS, KMOE_ERR_UNSUPPORTED,
+               "kmoe_gather_rows: fp8 rows need d <= %d (d=%d)", 64 * 8 * ROW_REGS, d);
   if (n_rows == 0) return KMOE_OK;
   const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(n_rows, 4));
   hipStream_t s = kmoe::as_stream(stream);

@@ -477,34 +477,19 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
   int64_t nr = rows;
   if (n_rows_dev) nr = min<int64_t>(nr, (int64_t)*n_rows_dev);
   if (r >= nr) return;
-  const int nvec = cols / 8;
-  const i32x4_t* src = reinterpret_cast<const i32x4_t*>(in + r * cols);
-  float amax = 0.0f;
-  for (int v = lane; v < nvec; v += 64) {
-    const i32x4_t val = src[v];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) << 16)));
-      amax = fmaxf(amax, fabsf(__uint_as_float(((uint32_t)val[q]) & 0xffff0000u)));
-    }
-  }
-  amax = wave_max(amax);
+  const int nvec = cols / 8;  // <= 64 * ROW_REGS (checked on the host)
+  RowRegs rr;
+  const float amax = load_row_amax(reinterpret_cast<const i32x4_t*>(in + r * cols), nvec, lane, rr);
   const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
   uint32_t* dst = reinterpret_cast<uint32_t*>(out + r * cols);
-  for (int v = lane; v < nvec; v += 64) {
-    const i32x4_t val = src[v];
-    uint32_t lo = 0, hi = 0;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint32_t w0 = (uint32_t)val[q];
-      lo |= f32_to_e4m3(__uint_as_float(w0 << 16) * inv) << (16 * q);
-      lo |= f32_to_e4m3(__uint_as_float(w0 & 0xffff0000u) * inv) << (16 * q + 8);
-      const uint32_t w1 = (uint32_t)val[q + 2];
-      hi |= f32_to_e4m3(__uint_as_float(w1 << 16) * inv) << (16 * q);
-      hi |= f32_to_e4m3(__uint_as_float(w1 & 0xffff0000u) * inv) << (16 * q + 8);
+  for (int i = 0; i < ROW_REGS; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+      uint32_t lo, hi;
+      quant_vec_e4m3(rr.v[i], inv, lo, hi);
+      *reinterpret_cast<uint2*>(dst + 2 * v) = make_uint2(lo, hi);
     }
-    dst[2 * v] = lo;
-    dst[2 * v + 1] = hi;
   }
   if (lane == 0) scale[r] = amax / 448.0f;
 }
@@ -703,6 +688,8 @@ extern "C" int kmoe_quant_rows_fp8(const void* in, int64_t rows, const int32_t* 
                                    float* scale, void* stream) {
   KMOE_REQUIRE(in && out && scale, KMOE_ERR_NULL, "kmoe_quant_rows_fp8: null buffer");
   KMOE_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0, KMOE_ERR_SHAPE, "kmoe_quant_rows_fp8: bad shape");
+  KMOE_REQUIRE(cols <= 64 * 8 * ROW_REGS, KMOE_ERR_UNSUPPORTED, "kmoe_quant_rows_fp8: cols=%d > %d", cols,
+               64 * 8 * ROW_REGS);
   if (rows == 0) return KMOE_OK;
   hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(rows, 4)), dim3(256), 0,
                      kmoe::as_stream(stream), static_cast<const uint16_t*>(in), rows, n_rows_dev, cols, out, scale);
