@@ -146,17 +146,29 @@ __device__ __forceinline__ float load_row_amax(const i32x4_t* __restrict__ src, 
   }
   return wave_max(amax);
 }
+// Four values to e4m3 bytes (a in byte 0) with the rule of f32_to_e4m3, on the
+// hardware converter: |x| > 448 (and +-inf) is clamped to +-448 first, so the
+// converter only sees finite values in range, where its round-to-nearest-even
+// equals the integer rule above on every fp32 bit pattern (checked exhaustively
+// on gfx950); NaN keeps its sign as sign | 0x7f (the converter writes 0xff).
+__device__ __forceinline__ float sat448(float f) { return fabsf(f) > 448.0f ? copysignf(448.0f, f) : f; }
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  int r = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), sat448(b), 0, false);
+  r = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(c), sat448(d), r, true);
+  uint32_t u = (uint32_t)r;
+  if (a != a || b != b || c != c || d != d) {
+    const float v[4] = {a, b, c, d};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (v[i] != v[i]) u = (u & ~(0xffu << (8 * i))) | ((((__float_as_uint(v[i]) >> 24) & 0x80u) | 0x7fu) << (8 * i));
+  }
+  return u;
+}
 // e4m3 bytes of one 16-byte bf16 vector (8 values) as two 32-bit words
 __device__ __forceinline__ void quant_vec_e4m3(const i32x4_t& val, float inv, uint32_t& lo, uint32_t& hi) {
-  lo = 0;
-  hi = 0;
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const uint32_t w0 = (uint32_t)val[q];
-    lo |= f32_to_e4m3(__uint_as_float(w0 << 16) * inv) << (16 * q);
-    lo |= f32_to_e4m3(__uint_as_float(w0 & 0xffff0000u) * inv) << (16 * q + 8);
-    const uint32_t w1 = (uint32_t)val[q + 2];
-    hi |= f32_to_e4m3(__uint_as_float(w1 << 16) * inv) << (16 * q);
-    hi |= f32_to_e4m3(__uint_as_float(w1 & 0xffff0000u) * inv) << (16 * q + 8);
-  }
+  const uint32_t w0 = (uint32_t)val[0], w1 = (uint32_t)val[1], w2 = (uint32_t)val[2], w3 = (uint32_t)val[3];
+  lo = e4m3x4(__uint_as_float(w0 << 16) * inv, __uint_as_float(w0 & 0xffff0000u) * inv,
+              __uint_as_float(w1 << 16) * inv, __uint_as_float(w1 & 0xffff0000u) * inv);
+  hi = e4m3x4(__uint_as_float(w2 << 16) * inv, __uint_as_float(w2 & 0xffff0000u) * inv,
+              __uint_as_float(w3 << 16) * inv, __uint_as_float(w3 & 0xffff0000u) * inv);
 }
