@@ -17,10 +17,17 @@ constexpr int SEL_THREADS = 1024;
 constexpr int SEL_MAX_S = 16384;  // keys held in LDS
 constexpr int SEL_MAX_C = 8192;   // sort buffer for the expert-choice order
 
+// Order-preserving uint32 image of a float: a > b  <=>  key(a) > key(b), and
+// a == b  <=>  key(a) == key(b); -0.0 and +0.0 compare equal, so they get one key
+// (they then tie, and the lower index wins, as for any equal scores).
 __device__ __forceinline__ uint32_t order_key(float f) {
-  uint32_t u = __float_as_uint(f);
   if (f != f) return 0u;  // NaN ranks last
+  const uint32_t u = f == 0.0f ? 0u : __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t k) {  // inverse of order_key (non-NaN keys)
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
 // Exclusive block scan of one int per thread (1024 threads); returns the exclusive
@@ -57,31 +64,50 @@ __device__ float block_sum(float v, float* s_red) {
 }
 
 // Finds the key `thr` of the C-th largest element and how many elements equal to
-// thr must be taken (`need`).
+// thr must be taken (`need`).  s_hist holds 256 bins per wave of the block.
 __device__ void radix_select_desc(const uint32_t* keys, int n, int C, uint32_t* s_hist, uint32_t* s_bcast,
                                   uint32_t& thr, int& need) {
+  __shared__ int s_scan[4];
   uint32_t prefix = 0, pmask = 0;
   int remaining = C;
+  const int nw = blockDim.x >> 6;  // one private 256-bin histogram per wave (no hot-bin contention)
+  uint32_t* wh = s_hist + 256 * (threadIdx.x >> 6);
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) s_hist[i] = 0;
+    for (int i = threadIdx.x; i < 256 * nw; i += blockDim.x) s_hist[i] = 0;
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
       const uint32_t k = keys[i];
-      if ((k & pmask) == prefix) atomicAdd(&s_hist[(k >> shift) & 255u], 1u);
+      if ((k & pmask) == prefix) atomicAdd(&wh[(k >> shift) & 255u], 1u);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int cum = 0, dsel = 0;
-      for (int dg = 255; dg >= 0; --dg) {
-        const int h = (int)s_hist[dg];
-        if (cum + h >= remaining) {
-          dsel = dg;
-          break;
-        }
-        cum += h;
+    // per-digit totals into the first histogram (fixed order: deterministic)
+    for (int dg = threadIdx.x; dg < 256; dg += blockDim.x) {
+      uint32_t tsum = 0;
+      for (int q = 0; q < nw; ++q) tsum += s_hist[256 * q + dg];
+      s_hist[dg] = tsum;
+    }
+    __syncthreads();
+    // bucket choice in parallel: thread t < 256 takes digit 255 - t (descending), an
+    // inclusive scan over t gives the count at or above each digit, and the one
+    // thread whose range crosses `remaining` publishes the digit
+    {
+      const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+      const int h = t < 256 ? (int)s_hist[255 - t] : 0;
+      int incl = h;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
       }
-      s_bcast[0] = (uint32_t)dsel;
-      s_bcast[1] = (uint32_t)(remaining - cum);
+      if (lane == 63 && w < 4) s_scan[w] = incl;
+      __syncthreads();
+      if (t < 256) {
+        for (int q = 0; q < w; ++q) incl += s_scan[q];
+        if (incl >= remaining && incl - h < remaining) {
+          s_bcast[0] = (uint32_t)(255 - t);
+          s_bcast[1] = (uint32_t)(remaining - (incl - h));
+        }
+      }
     }
     __syncthreads();
     prefix |= s_bcast[0] << shift;
@@ -134,7 +160,7 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
                                                                 float* __restrict__ src_w) {
   __shared__ uint32_t keys[SEL_MAX_S];
   __shared__ uint64_t sorted[SEL_MAX_C];
-  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist[256 * (SEL_THREADS / 64)];
   __shared__ uint32_t bc[2];
   __shared__ int s_wave[SEL_THREADS / 64];
   __shared__ float s_red[SEL_THREADS / 64];
@@ -155,7 +181,7 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
   __syncthreads();
   // softmax denominator over the whole sequence (moe.py:520)
   float den = 0.0f;
-  for (int i = threadIdx.x; i < S; i += blockDim.x) den += __expf(lg[(int64_t)i * E] - mx);
+  for (int i = threadIdx.x; i < S; i += blockDim.x) den += __expf(key_value(keys[i]) - mx);
   den = block_sum(den, s_red);
 
   uint32_t thr;
@@ -170,35 +196,78 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
     if (pos < C) sorted[pos] = ((uint64_t)keys[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
   });
   __syncthreads();
-  // bitonic sort, descending by (key, -index)
-  for (int kk = 2; kk <= Cp; kk <<= 1) {
-    for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-      for (int i = threadIdx.x; i < Cp; i += blockDim.x) {
-        const int l = i ^ jj;
-        if (l > i) {
-          const uint64_t a = sorted[i], c = sorted[l];
-          const bool desc = (i & kk) == 0;
-          if (desc ? (a < c) : (a > c)) {
-            sorted[i] = c;
-            sorted[l] = a;
+  // bitonic sort, descending by (key, -index).  Element i lives in thread i % 1024,
+  // register slot i / 1024 (Cp <= 8192: up to 8 per thread): strides < 64 are
+  // exchanged with wave shuffles, strides >= 1024 inside the thread, and only the
+  // strides 64..512 go through LDS.
+  {
+    constexpr int MAXPER = SEL_MAX_C / SEL_THREADS;
+    const int t = threadIdx.x;
+    const int per = Cp > SEL_THREADS ? Cp / SEL_THREADS : 1;
+    uint64_t v[MAXPER];
+#pragma unroll
+    for (int h = 0; h < MAXPER; ++h) v[h] = (h < per) ? sorted[t + h * SEL_THREADS] : 0ull;
+    __syncthreads();
+    // element i of the pair (i, partner) keeps the larger value in a descending block
+    // when it is the lower index, else the smaller
+    auto pick = [](uint64_t x, uint64_t y, int i, int partner, int kk) -> uint64_t {
+      const bool keep_max = (((i & kk) == 0) == (i < partner));
+      return keep_max ? (x > y ? x : y) : (x < y ? x : y);
+    };
+    for (int kk = 2; kk <= Cp; kk <<= 1) {
+      for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+        if (jj >= SEL_THREADS) {  // partner in the same thread, slot h ^ (jj / 1024)
+          const int hs = jj / SEL_THREADS;
+          uint64_t nv[MAXPER];
+#pragma unroll
+          for (int h = 0; h < MAXPER; ++h) {
+            const int i = t + h * SEL_THREADS;
+            nv[h] = h < per ? pick(v[h], v[h ^ hs], i, i ^ jj, kk) : v[h];
           }
+#pragma unroll
+          for (int h = 0; h < MAXPER; ++h) v[h] = nv[h];
+        } else if (jj < 64) {
+#pragma unroll
+          for (int h = 0; h < MAXPER; ++h) {
+            if (h >= per) continue;
+            const int i = t + h * SEL_THREADS;
+            const uint32_t lo = (uint32_t)v[h], hi = (uint32_t)(v[h] >> 32);
+            const uint64_t y = ((uint64_t)(uint32_t)__shfl_xor((int)hi, jj, 64) << 32) |
+                               (uint64_t)(uint32_t)__shfl_xor((int)lo, jj, 64);
+            v[h] = pick(v[h], y, i, i ^ jj, kk);
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < MAXPER; ++h)
+            if (h < per) sorted[t + h * SEL_THREADS] = v[h];
+          __syncthreads();
+#pragma unroll
+          for (int h = 0; h < MAXPER; ++h) {
+            if (h >= per) continue;
+            const int i = t + h * SEL_THREADS;
+            v[h] = pick(v[h], sorted[i ^ jj], i, i ^ jj, kk);
+          }
+          __syncthreads();
         }
       }
-      __syncthreads();
     }
+#pragma unroll
+    for (int h = 0; h < MAXPER; ++h)
+      if (h < per) sorted[t + h * SEL_THREADS] = v[h];
+    __syncthreads();
   }
   // weights: p / (sum_sel p + 1e-9)  (moe.py:528)
   float psel = 0.0f;
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
     const int s = (int)(0xffffffffu - (uint32_t)(sorted[c] & 0xffffffffu));
-    psel += __expf(lg[(int64_t)s * E] - mx) / den;
+    psel += __expf(key_value(keys[s]) - mx) / den;
   }
   psel = block_sum(psel, s_red);
   const float inv = 1.0f / (psel + 1e-9f);
   const int64_t BC = (int64_t)B * C;
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
     const int s = (int)(0xffffffffu - (uint32_t)(sorted[c] & 0xffffffffu));
-    const float p = __expf(lg[(int64_t)s * E] - mx) / den;
+    const float p = __expf(key_value(keys[s]) - mx) / den;
     const float wv = p * inv;
     const int64_t o = ((int64_t)b * E + e) * C + c;
     idx[o] = s;
@@ -242,7 +311,7 @@ __global__ __launch_bounds__(SEL_THREADS) void mod_select_kernel(const float* __
                                                                  int32_t* __restrict__ token_rows,
                                                                  int32_t* __restrict__ out_map) {
   __shared__ uint32_t keys[SEL_MAX_S];
-  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist[256 * (SEL_THREADS / 64)];
   __shared__ uint32_t bc[2];
   __shared__ int s_wave[SEL_THREADS / 64];
   __shared__ float s_red[SEL_THREADS / 64];

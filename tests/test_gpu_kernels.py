@@ -301,7 +301,8 @@ def test_combine_is_deterministic(dev):
 
 
 # ------------------------------------------------------------------ expert choice / MoD selection
-@pytest.mark.parametrize("B,S,E,C,ties", [(1, 16384, 16, 2048, False), (2, 300, 4, 75, True), (3, 64, 8, 64, False)])
+@pytest.mark.parametrize("B,S,E,C,ties", [(1, 16384, 16, 2048, False), (2, 300, 4, 75, True), (3, 64, 8, 64, False),
+                                         (1, 12000, 4, 5000, True)])
 def test_ec_select_parity(dev, B, S, E, C, ties):
     g = torch.Generator().manual_seed(40)
     lg = torch.randn(B * S, E, generator=g) * 0.2
