@@ -64,41 +64,69 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * KB + ((chu
 
 __host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 
-// (expert, row-tile) of row-slot `slot`, from the offsets; returns false if none.
-// One vector load gives lane e the row range of expert e (E <= 64); the walk over
-// the experts then reads the per-lane tile counts with readlane, so the lookup
-// costs one memory round trip instead of one per expert.
-__device__ __forceinline__ bool find_row_tile(const int32_t* __restrict__ offsets, int E, int slot, int& e_out,
-                                              int& m0, int& m_end) {
+// Row slots.  Lane e of a wave holds the row range [lo, hi) of expert e (E <= 64)
+// and its number of 256-row slots; slots are numbered expert by expert.
+struct SlotTable {
+  int lo, hi, ns;  // this lane's expert
+  int n_slots;     // all experts (wave-uniform)
+};
+__device__ __forceinline__ SlotTable load_slots(const int32_t* __restrict__ offsets, int E) {
   const int lane = threadIdx.x & 63;
-  int lo = 0, hi = 0;
+  SlotTable t;
+  t.lo = 0;
+  t.hi = 0;
   if (lane < E) {
-    lo = offsets[lane];
-    hi = offsets[lane + 1];
+    t.lo = offsets[lane];
+    t.hi = offsets[lane + 1];
   }
-  const int nt = (hi - lo + BM - 1) / BM;
+  t.ns = (t.hi - t.lo + BM - 1) / BM;
+  int n = t.ns;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) n += __shfl_xor(n, o, 64);
+  t.n_slots = __builtin_amdgcn_readfirstlane(n);
+  return t;
+}
+// (expert, first row, row end) of slot `slot` < n_slots: a readlane walk over the
+// experts' slot counts.
+__device__ __forceinline__ void find_slot(const SlotTable& t, int E, int slot, int& e_out, int& m0, int& m_end) {
   int base = 0;
+  e_out = 0;
+  m0 = 0;
+  m_end = 0;
   for (int e = 0; e < E; ++e) {
-    const int n = __builtin_amdgcn_readlane(nt, e);
+    const int n = __builtin_amdgcn_readlane(t.ns, e);
     if (slot < base + n) {
       e_out = e;
-      m0 = __builtin_amdgcn_readlane(lo, e) + (slot - base) * BM;
-      m_end = __builtin_amdgcn_readlane(hi, e);
-      return true;
+      m0 = __builtin_amdgcn_readlane(t.lo, e) + (slot - base) * BM;
+      m_end = __builtin_amdgcn_readlane(t.hi, e);
+      return;
     }
     base += n;
   }
-  return false;
 }
 
-// Workgroup id -> (slot, column tile), XCD-aware (see the file comment).
-__device__ __forceinline__ void map_tile(int L, int n_tiles, int& slot, int& nt) {
+// Dense tile order: slots in groups of 4, each group enumerated column tile by
+// column tile (4 consecutive tiles share a column tile, so 32 consecutive tiles are
+// 8 column tiles x 4 slots); the last, partial group likewise with its slots.
+__device__ __forceinline__ void dense_tile(int t, int n_slots, int n_tiles, int& slot, int& nt) {
+  const int full = (n_slots >> 2) * 4 * n_tiles;
+  if (t < full) {
+    const int g = t / (4 * n_tiles), r = t - g * 4 * n_tiles;
+    nt = r >> 2;
+    slot = g * 4 + (r & 3);
+  } else {
+    const int rem = n_slots & 3, u = t - full;
+    nt = u / rem;
+    slot = (n_slots & ~3) + (u - nt * rem);
+  }
+}
+
+// Workgroup id L < n (n a multiple of 256) -> dense tile, XCD-aware: workgroups are
+// dispatched round-robin over the 8 XCDs, so the consecutive ids one XCD receives
+// are given 32-tile super-blocks, which share A and B K-slices in that XCD's L2.
+__device__ __forceinline__ int xcd_tile(int L) {
   const int xcd = L % NXCD, i = L / NXCD;
-  const int t = ((i / SB_TILES) * NXCD + xcd) * SB_TILES + (i % SB_TILES);
-  const int per_group = 4 * n_tiles;
-  const int g = t / per_group, r = t - g * per_group;
-  nt = r >> 2;
-  slot = g * 4 + (r & 3);
+  return ((i / SB_TILES) * NXCD + xcd) * SB_TILES + (i % SB_TILES);
 }
 
 template <bool FP8>
@@ -134,12 +162,30 @@ __device__ __forceinline__ void mfma(f32x16_t& acc, const Frag<FP8>& a, const Fr
     acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a.v, b.v, acc, 0, 0, 0, 127, 0, 127);
 }
 
-// B-tile row of the wave's j-th 32-row block (wn in 0..1, j in 0..3).  gate_up:
-// blocks 0,1 are gate rows and 2,3 the up rows of the same 64 f columns.
-template <bool GATE_UP>
-__device__ __forceinline__ int b_row(int wn, int j, int lr) {
-  if (GATE_UP) return (j >> 1) * 128 + wn * 64 + (j & 1) * 32 + lr;
-  return wn * 128 + j * 32 + lr;
+// B-tile geometry of a tile whose waves hold WNB 32-row B blocks each (WNB = 4: the
+// full 256 B rows; 2 and 1: the narrow tiles of the split tail, a half or a
+// quarter `q` of a full tile's output columns).  LDS B row of block j of wave
+// column wn:  down: 32 WNB wn + 32 j + lr;  gate_up: the first WNB/2 blocks are
+// gate rows and the rest the up rows of the same f columns.
+template <bool GATE_UP, int WNB>
+__device__ __forceinline__ int b_lds_row(int wn, int j, int lr) {
+  if constexpr (GATE_UP) {
+    constexpr int H = WNB / 2;
+    return (j / H) * (32 * WNB) + wn * (16 * WNB) + (j % H) * 32 + lr;
+  } else {
+    return wn * (32 * WNB) + j * 32 + lr;
+  }
+}
+// Row of the 256-row packed B tile that LDS B row `lrow` holds (identity for WNB = 4).
+// gate_up packs 128 gate rows then 128 up rows per full tile.
+template <bool GATE_UP, int WNB>
+__device__ __forceinline__ int b_packed_row(int lrow, int q) {
+  if constexpr (GATE_UP) {
+    constexpr int HR = 32 * WNB;  // gate (or up) rows of the tile
+    return (lrow / HR) * 128 + q * HR + lrow % HR;
+  } else {
+    return q * (64 * WNB) + lrow;
+  }
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [I0, N).
@@ -151,18 +197,18 @@ __device__ __forceinline__ void static_for(Fn&& f) {
   }
 }
 
-// Scheduling groups for a 16-MFMA substep: LDS operations front-loaded, one
-// after each of the first NDS MFMAs (two each when NDS > 16), memory operations
-// spread evenly over all 16.
-template <int NDS, int NVM, int G = 0>
+// Scheduling groups for an NM-MFMA substep: LDS operations front-loaded, one after
+// each of the first NDS MFMAs (spread evenly when NDS > NM), memory operations
+// spread evenly over all NM.
+template <int NM, int NDS, int NVM, int G = 0>
 __device__ __forceinline__ void sched_spread() {
-  if constexpr (G < 16) {
+  if constexpr (G < NM) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    constexpr int dd = NDS <= 16 ? (G < NDS ? 1 : 0) : (NDS * (G + 1) + 15) / 16 - (NDS * G + 15) / 16;
-    constexpr int v = (NVM * (G + 1)) / 16 - (NVM * G) / 16;
+    constexpr int dd = NDS <= NM ? (G < NDS ? 1 : 0) : (NDS * (G + 1) + NM - 1) / NM - (NDS * G + NM - 1) / NM;
+    constexpr int v = (NVM * (G + 1)) / NM - (NVM * G) / NM;
     if constexpr (dd > 0) __builtin_amdgcn_sched_group_barrier(0x080, dd, 0);  // DS
     if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x010, v, 0);   // VMEM
-    sched_spread<NDS, NVM, G + 1>();
+    sched_spread<NM, NDS, NVM, G + 1>();
   }
 }
 
@@ -172,124 +218,142 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
 
+struct GemmArgs {
+  const uint8_t* A;
+  int64_t lda_bytes;
+  const float* a_scale;
+  const int32_t* row_token;
+  const int32_t* row_index;
+  const uint8_t* B;
+  int64_t b_expert_rows;
+  int64_t ldb_bytes;
+  const float* b_scale;
+  int k_bytes;
+  uint16_t* C;
+  int64_t ldc;
+  int n_valid;
+};
+
+// One output tile: rows [m0, min(m0 + 256, m_end)) of expert e against B rows of
+// full column tile nt (narrow part q when WNB < 4).
 // FP8: A/B bytes are e4m3; a_scale per A row, b_scale per B row (global row index).
 // GATHER: A is the unpermuted activation matrix and permuted row r is its row
 // row_index[row_token[r]] (row_token[r] without row_index): the dispatch gather is
 // fused into the A loads.
-template <bool GATE_UP, bool FP8, bool GATHER>
-__global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_kernel(
-    const uint8_t* __restrict__ A, int64_t lda_bytes, const float* __restrict__ a_scale,
-    const int32_t* __restrict__ row_token, const int32_t* __restrict__ row_index,
-    const int32_t* __restrict__ offsets, int E, const uint8_t* __restrict__ B, int64_t b_expert_rows,
-    int64_t ldb_bytes, const float* __restrict__ b_scale, int k_bytes, uint16_t* __restrict__ C, int64_t ldc,
-    int n_valid, int n_tiles) {
-  static_assert(!(GATHER && FP8), "the fp8 path reads rows quantised by the dispatch");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[GEMM_LDS];
+template <bool GATE_UP, bool FP8, bool GATHER, int WNB>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e, int m0, int m_end, int nt,
+                                          int q) {
+  static_assert(WNB == 4 || WNB == 2 || (WNB == 1 && !GATE_UP), "tile width");
   constexpr int NSUB = FP8 ? KB / 64 : KB / 32;  // MFMA K-substeps per pipeline step
+  constexpr int BNT = 64 * WNB;                  // B rows of the tile
+  constexpr int TBB = BNT * KB;                  // bytes of one B stage tile
+  constexpr int BLK_B = BNT * KB / 1024 / 4;     // B load blocks per wave per step
+  constexpr int NBLK = BLK_PER_WAVE + BLK_B;     // load blocks per wave per step
+  constexpr int NM = 4 * WNB;                    // MFMAs per substep
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, lh = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
 
-  int slot, nt;
-  map_tile(blockIdx.x, n_tiles, slot, nt);
-  int e, m0, m_end;
-  if (!find_row_tile(offsets, E, slot, e, m0, m_end)) return;
-
-  const int64_t brow0 = (int64_t)e * b_expert_rows + (int64_t)nt * BN;
-  const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(GATHER ? A : A + (int64_t)m0 * lda_bytes);
-  const __amdgpu_buffer_rsrc_t brsrc = make_rsrc(B + brow0 * ldb_bytes);
-  const int nk = k_bytes / KB;
+  const int64_t brow0 = (int64_t)e * g.b_expert_rows + (int64_t)nt * BN;  // full packed tile
+  const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(GATHER ? g.A : g.A + (int64_t)m0 * g.lda_bytes);
+  const __amdgpu_buffer_rsrc_t brsrc = make_rsrc(g.B + brow0 * g.ldb_bytes);
+  const int nk = g.k_bytes / KB;
   // LDS stage s: [A tile | B tile]
-  auto la_buf = [&](int st) { return lds + st * 2 * TB; };
-  auto lb_buf = [&](int st) { return lds + st * 2 * TB + TB; };
+  auto la_buf = [&](int st) { return lds + st * (TB + TBB); };
+  auto lb_buf = [&](int st) { return lds + st * (TB + TBB) + TB; };
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[4][WNB];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < WNB; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // Tile loads: a 256-row stage tile is 32 blocks of 1 KiB (8 rows of 128 B); wave w
-  // loads A and B blocks [8w, 8w+8) into registers and writes them to LDS.  Lane l
-  // of block q covers bytes [16l, 16l+16) of the block (tile row 8q + l/8, physical
-  // chunk l%8) and so loads the logical chunk that swz() maps there: the LDS write of
-  // a block is one contiguous, conflict-free 1 KiB.  A rows past the expert's last
-  // row are clamped to it (their results are never stored).
+  // Tile loads: a stage tile is a set of 1 KiB blocks (8 rows of 128 B); wave w loads
+  // A blocks [8w, 8w+8) and B blocks [BLK_B w, BLK_B w + BLK_B) into registers and
+  // writes them to LDS.  Lane l of a block covers bytes [16l, 16l+16) of it (tile row
+  // 8q + l/8, physical chunk l%8) and so loads the logical chunk that swz() maps
+  // there: the LDS write of a block is one contiguous, conflict-free 1 KiB.  A rows
+  // past the expert's last row are clamped to it (their results are never stored).
   const int rsub = lane / CPR, pc = lane % CPR;
-  uint32_t a_off[BLK_PER_WAVE], b_off[BLK_PER_WAVE];
+  uint32_t a_off[BLK_PER_WAVE], b_off[8];
   const int a_last = m_end - 1 - m0;
   int ra[BLK_PER_WAVE];
 #pragma unroll
-  for (int q = 0; q < BLK_PER_WAVE; ++q) {
-    const int tr = (wave * BLK_PER_WAVE + q) * RPB + rsub;
-    ra[q] = tr < a_last ? tr : a_last;
+  for (int qa = 0; qa < BLK_PER_WAVE; ++qa) {
+    const int tr = (wave * BLK_PER_WAVE + qa) * RPB + rsub;
+    ra[qa] = tr < a_last ? tr : a_last;
   }
   if constexpr (GATHER) {
     // batched: all row_token loads, then all row_index loads (two round trips)
 #pragma unroll
-    for (int q = 0; q < BLK_PER_WAVE; ++q) ra[q] = row_token[m0 + ra[q]];
-    if (row_index) {
+    for (int qa = 0; qa < BLK_PER_WAVE; ++qa) ra[qa] = g.row_token[m0 + ra[qa]];
+    if (g.row_index) {
 #pragma unroll
-      for (int q = 0; q < BLK_PER_WAVE; ++q) ra[q] = row_index[ra[q]];
+      for (int qa = 0; qa < BLK_PER_WAVE; ++qa) ra[qa] = g.row_index[ra[qa]];
     }
   }
 #pragma unroll
-  for (int q = 0; q < BLK_PER_WAVE; ++q) {
-    const int tr = (wave * BLK_PER_WAVE + q) * RPB + rsub;
+  for (int qa = 0; qa < BLK_PER_WAVE; ++qa) {
+    const int tr = (wave * BLK_PER_WAVE + qa) * RPB + rsub;
     const uint32_t chunk = (uint32_t)(pc ^ ((tr >> 1) & (CPR - 1))) << 4;
-    a_off[q] = (uint32_t)ra[q] * (uint32_t)lda_bytes + chunk;
-    b_off[q] = (uint32_t)tr * (uint32_t)ldb_bytes + chunk;
+    a_off[qa] = (uint32_t)ra[qa] * (uint32_t)g.lda_bytes + chunk;
   }
-  i32x4_t stg[2 * BLK_PER_WAVE];  // one step of this wave's tile data: A blocks 0-7, B blocks 8-15
-  // block q: global -> registers (K-step kt, clamped to the last step)
-  auto load_block = [&](int q, int kt) {
+#pragma unroll
+  for (int qb = 0; qb < BLK_B; ++qb) {
+    const int tr = (wave * BLK_B + qb) * RPB + rsub;
+    const uint32_t chunk = (uint32_t)(pc ^ ((tr >> 1) & (CPR - 1))) << 4;
+    b_off[qb] = (uint32_t)b_packed_row<GATE_UP, WNB>(tr, q) * (uint32_t)g.ldb_bytes + chunk;
+  }
+  i32x4_t stg[16];  // one step of this wave's tile data: A blocks, then B blocks
+  // block qq: global -> registers (K-step kt, clamped to the last step)
+  auto load_block = [&](int qq, int kt) {
     const int ks = kt < nk ? kt : nk - 1;
-    if (q < BLK_PER_WAVE)
-      stg[q] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, a_off[q], ks * KB, 0);
+    if (qq < BLK_PER_WAVE)
+      stg[qq] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, a_off[qq], ks * KB, 0);
     else
-      stg[q] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, b_off[q - BLK_PER_WAVE], ks * KB, 0);
+      stg[qq] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, b_off[qq - BLK_PER_WAVE], ks * KB, 0);
   };
-  // block q: registers -> LDS stage st
-  auto write_block = [&](int q, int st) {
-    uint8_t* dst = (q < BLK_PER_WAVE ? la_buf(st) + q * 1024 : lb_buf(st) + (q - BLK_PER_WAVE) * 1024) +
-                   wave * BLK_PER_WAVE * 1024 + lane * 16;
-    *reinterpret_cast<i32x4_t*>(dst) = stg[q];
+  // block qq: registers -> LDS stage st
+  auto write_block = [&](int qq, int st) {
+    uint8_t* dst = qq < BLK_PER_WAVE ? la_buf(st) + (wave * BLK_PER_WAVE + qq) * 1024
+                                     : lb_buf(st) + (wave * BLK_B + qq - BLK_PER_WAVE) * 1024;
+    *reinterpret_cast<i32x4_t*>(dst + lane * 16) = stg[qq];
   };
-  Frag<FP8> fa[2][4], fb[2][4];
-  auto rd = [&](int st, int i, Frag<FP8> (&a)[4], Frag<FP8> (&b)[4]) {
+  Frag<FP8> fa[2][4], fb[2][WNB];
+  auto rd = [&](int st, int i, Frag<FP8> (&a)[4], Frag<FP8> (&b)[WNB]) {
     const uint8_t* la = la_buf(st);
     const uint8_t* lb = lb_buf(st);
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) read_frag<FP8>(la, wm * 128 + mi * 32 + lr, i, lh, a[mi]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) read_frag<FP8>(lb, b_row<GATE_UP>(wn, j, lr), i, lh, b[j]);
+    for (int j = 0; j < WNB; ++j) read_frag<FP8>(lb, b_lds_row<GATE_UP, WNB>(wn, j, lr), i, lh, b[j]);
   };
-  auto mma = [&](const Frag<FP8> (&a)[4], const Frag<FP8> (&b)[4]) {
+  auto mma = [&](const Frag<FP8> (&a)[4], const Frag<FP8> (&b)[WNB]) {
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) mfma<FP8>(acc[mi][j], a[mi], b[j]);
+      for (int j = 0; j < WNB; ++j) mfma<FP8>(acc[mi][j], a[mi], b[j]);
   };
 
   // Pipeline.  Step kt computes LDS stage kt%2 while the registers hold step kt+1's
-  // tile data.  Those 16 blocks are written into stage (kt+1)%2 (which every wave
+  // tile data.  Those blocks are written into stage (kt+1)%2 (which every wave
   // stopped reading at step kt-1's barrier) over the first substeps, each block
   // reloaded with step kt+2's data right after its write, so a load has a whole
-  // step to land and the LDS write traffic is spread evenly (bf16: 6/5/5 blocks in
-  // substeps 0-2; fp8: all in substep 0).  The last substep waits for this wave's
-  // LDS writes and reads, then one barrier publishes stage kt+1, whose first
-  // fragments are read under the last substep's MFMAs.  Register dependencies give
-  // the vmcnt waits; the scheduling groups interleave the LDS and memory
-  // operations with the MFMAs, fragment reads first.
-  constexpr int RD = FP8 ? 16 : 8;  // LDS reads of a substep's fragments
-  constexpr int NBLK = 2 * BLK_PER_WAVE;
-  for (int q = 0; q < NBLK; ++q) load_block(q, 0);
-  for (int q = 0; q < NBLK; ++q) write_block(q, 0);
-  for (int q = 0; q < NBLK; ++q) load_block(q, 1);
+  // step to land and the LDS write traffic is spread evenly (bf16: about 6/5/5
+  // sixteenths of the blocks in substeps 0-2; fp8: all in substep 0).  The last
+  // substep waits for this wave's LDS writes and reads, then one barrier publishes
+  // stage kt+1, whose first fragments are read under the last substep's MFMAs.
+  // Register dependencies give the vmcnt waits; the scheduling groups interleave the
+  // LDS and memory operations with the MFMAs, fragment reads first.
+  constexpr int RD = (FP8 ? 2 : 1) * (4 + WNB);  // LDS reads of a substep's fragments
+  constexpr int C1 = (NBLK * 6 + 8) / 16, C2 = (NBLK * 11 + 8) / 16;
+  for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 0);
+  for (int qq = 0; qq < NBLK; ++qq) write_block(qq, 0);
+  for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 1);
   wait_lgkmcnt0();
   barrier_nofence();
   rd(0, 0, fa[0], fb[0]);
@@ -301,8 +365,8 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
       constexpr int i = decltype(ic)::value;
       constexpr int bi = i & 1;
       // blocks [q0, q1) are written and reloaded in this substep
-      constexpr int q0 = NSUB == 4 ? (i == 0 ? 0 : i == 1 ? 6 : i == 2 ? 11 : NBLK) : (i == 0 ? 0 : NBLK);
-      constexpr int q1 = NSUB == 4 ? (i == 0 ? 6 : i == 1 ? 11 : NBLK) : NBLK;
+      constexpr int q0 = NSUB == 4 ? (i == 0 ? 0 : i == 1 ? C1 : i == 2 ? C2 : NBLK) : (i == 0 ? 0 : NBLK);
+      constexpr int q1 = NSUB == 4 ? (i == 0 ? C1 : i == 1 ? C2 : NBLK) : NBLK;
       constexpr int nq = LAST ? 0 : q1 - q0;
       constexpr bool RDN = i + 1 < NSUB || !LAST;
       // next substep's fragments first: they are on the MFMA critical path
@@ -318,7 +382,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
         static_for<q0, q1>([&](auto qc) { load_block(decltype(qc)::value, kt + 2); });
       }
       mma(fa[bi], fb[bi]);
-      sched_spread<(RDN ? RD : 0) + nq, nq>();
+      sched_spread<NM, (RDN ? RD : 0) + nq, nq>();
       __builtin_amdgcn_sched_barrier(0);
     });
   };
@@ -331,30 +395,31 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   // (VALU, no LDS round trip): for the rows of r = 2p and 2p+1, an even lane packs
   // its own and its right neighbour's value of row 2p, an odd lane its left
   // neighbour's and its own of row 2p+1, so every lane writes 4 bytes, unmasked.
-  constexpr int NC = GATE_UP ? 128 : 256;   // output columns of the tile
-  constexpr int NJ = GATE_UP ? 2 : 4;       // output column blocks per wave
-  constexpr int OSTR = NC * 2 + 16;          // LDS row stride (bytes)
+  constexpr int NC = GATE_UP ? 32 * WNB : 64 * WNB;  // output columns of the tile
+  constexpr int NJ = GATE_UP ? WNB / 2 : WNB;        // output column blocks per wave
+  constexpr int OSTR = NC * 2 + 16;                  // LDS row stride (bytes)
   const bool odd = lr & 1;
   __syncthreads();
   // lane's write address for p = 0 of block (0, 0): even lanes row 4lh col lr,
   // odd lanes row 4lh+1 col lr-1
   uint8_t* const wbase = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR + (wn * (NC / 2) + lr - (odd ? 1 : 0)) * 2;
+  auto bscale = [&](int j) { return g.b_scale[brow0 + b_packed_row<GATE_UP, WNB>(b_lds_row<GATE_UP, WNB>(wn, j, lr), q)]; };
   auto result = [&](int mi, int r, int jo) -> float {
     if (GATE_UP) {
-      float g = acc[mi][jo][r], u = acc[mi][jo + 2][r];
+      float gg = acc[mi][jo][r], u = acc[mi][jo + WNB / 2][r];
       if (FP8) {
         const int grow = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        const float sa = grow < m_end ? a_scale[grow] : 1.0f;
-        g *= sa * b_scale[brow0 + b_row<true>(wn, jo, lr)];
-        u *= sa * b_scale[brow0 + b_row<true>(wn, jo + 2, lr)];
+        const float sa = grow < m_end ? g.a_scale[grow] : 1.0f;
+        gg *= sa * bscale(jo);
+        u *= sa * bscale(jo + WNB / 2);
       }
-      return silu_fast_f32(g) * u;
+      return silu_fast_f32(gg) * u;
     } else {
       float v = acc[mi][jo][r];
       if (FP8) {
         const int grow = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        const float sa = grow < m_end ? a_scale[grow] : 1.0f;
-        v *= sa * b_scale[brow0 + b_row<false>(wn, jo, lr)];
+        const float sa = grow < m_end ? g.a_scale[grow] : 1.0f;
+        v *= sa * bscale(jo);
       }
       return v;
     }
@@ -381,15 +446,62 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   }
   __syncthreads();
   constexpr int OCPR = NC * 2 / 16;  // 16-byte chunks per output row
-  const int col0 = nt * NC;
+  const int col0 = (GATE_UP ? nt * 128 : nt * 256) + q * NC;
   for (int c = tid; c < BM * OCPR; c += GEMM_THREADS) {
     const int trow = c / OCPR, ch = c % OCPR;
     const int grow = m0 + trow;
     const int gcol = col0 + ch * 8;
-    if (grow < m_end && gcol < n_valid)
-      *reinterpret_cast<i32x4_t*>(C + (int64_t)grow * ldc + gcol) =
+    if (grow < m_end && gcol < g.n_valid)
+      *reinterpret_cast<i32x4_t*>(g.C + (int64_t)grow * g.ldc + gcol) =
           *reinterpret_cast<const i32x4_t*>(lds + trow * OSTR + ch * 16);
   }
+}
+
+// Work of workgroup blockIdx.x.  The tiles (slot, column tile) are numbered densely
+// (dense_tile); with n_cu workgroups resident at a time, the first R = N/n_cu full
+// rounds take one tile per workgroup in the XCD-aware order.  The N - R n_cu tiles
+// left would occupy few compute units for a whole tile time, so when they fit
+// (split > 1: at most n_cu / split of them) each is split into `split` narrow tiles
+// of 1/split of its columns (the full K), which all run at once.  A narrow tile
+// computes every output element with the same MFMA sequence as the full tile, so
+// the results are identical.  split = 1 keeps the tail tiles whole.
+template <bool GATE_UP, bool FP8, bool GATHER>
+__global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_kernel(
+    GemmArgs g, const int32_t* __restrict__ offsets, int E, int n_tiles, int n_cu, int allow_split) {
+  static_assert(!(GATHER && FP8), "the fp8 path reads rows quantised by the dispatch");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[GEMM_LDS];
+  const SlotTable st = load_slots(offsets, E);
+  const int n_all = st.n_slots * n_tiles;
+  const int rounds = n_all / n_cu, base = rounds * n_cu, n_rest = n_all - base;
+  int split = 1;
+  if (allow_split && n_rest > 0) {
+    if (!GATE_UP && 4 * n_rest <= n_cu)
+      split = 4;
+    else if (2 * n_rest <= n_cu)
+      split = 2;
+  }
+  const int L = blockIdx.x;
+  int t, q = 0;
+  if (L < base) {
+    t = (base % (NXCD * SB_TILES)) == 0 ? xcd_tile(L) : L;
+  } else if (split == 1) {
+    if (L >= n_all) return;
+    t = L;
+  } else {
+    const int u = L - base;
+    if (u >= n_rest * split) return;
+    t = base + u / split;
+    q = u % split;
+  }
+  int slot, nt, e, m0, m_end;
+  dense_tile(t, st.n_slots, n_tiles, slot, nt);
+  find_slot(st, E, slot, e, m0, m_end);
+  if (L < base || split == 1)
+    gemm_tile<GATE_UP, FP8, GATHER, 4>(g, lds, e, m0, m_end, nt, 0);
+  else if (split == 2)
+    gemm_tile<GATE_UP, FP8, GATHER, 2>(g, lds, e, m0, m_end, nt, q);
+  else if constexpr (!GATE_UP)
+    gemm_tile<GATE_UP, FP8, GATHER, 1>(g, lds, e, m0, m_end, nt, q);
 }
 
 // ---------------------------------------------------------------- weight packing
@@ -504,9 +616,10 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
                 int n_tiles, hipStream_t s) {
   const int eb = fp8 ? 1 : 2;
   const int64_t slots = kmoe::ceil_div<int64_t>(max_rows, BM) + E;
-  // whole 4-slot groups, whole XCD super-blocks (map_tile covers [0, blocks))
-  const int64_t blocks = kmoe::ceil_div<int64_t>(kmoe::ceil_div<int64_t>(slots, 4) * 4 * n_tiles,
-                                                 (int64_t)NXCD * SB_TILES) * NXCD * SB_TILES;
+  // every tile of the worst-case slot count, plus one narrow tile per resident
+  // workgroup for the split tail
+  const int n_cu = kmoe::cu_count();
+  const int64_t blocks = slots * n_tiles + n_cu;
   if (blocks > 0x7fffffff) {
     kmoe::set_error("kmoe gemm: grid too large");
     return KMOE_ERR_SHAPE;
@@ -516,21 +629,33 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
     kmoe::set_error("kmoe gemm: K bytes %d not a multiple of %d", kbytes, KB);
     return KMOE_ERR_SHAPE;
   }
-  const uint8_t* a = static_cast<const uint8_t*>(A);
-  const uint8_t* b = static_cast<const uint8_t*>(B);
-  uint16_t* c = static_cast<uint16_t*>(C);
-  const int64_t lda = kbytes, ldb = kbytes + WPAD;
+  GemmArgs g;
+  g.A = static_cast<const uint8_t*>(A);
+  g.lda_bytes = kbytes;
+  g.a_scale = a_scale;
+  g.row_token = row_token;
+  g.row_index = row_index;
+  g.B = static_cast<const uint8_t*>(B);
+  g.b_expert_rows = b_expert_rows;
+  g.ldb_bytes = kbytes + WPAD;
+  g.b_scale = b_scale;
+  g.k_bytes = kbytes;
+  g.C = static_cast<uint16_t*>(C);
+  g.ldc = ldc;
+  g.n_valid = n_valid;
   // tile loads address a 2 GiB buffer window from the tile's first A / B row (from
   // the first row of A when gathering)
-  if ((int64_t)(BM + 1) * ldb >= ((int64_t)1 << 31) || (row_token && (n_a_rows + 1) * lda >= ((int64_t)1 << 31))) {
+  if ((int64_t)(BM + 1) * g.ldb_bytes >= ((int64_t)1 << 31) ||
+      (row_token && (n_a_rows + 1) * g.lda_bytes >= ((int64_t)1 << 31))) {
     kmoe::set_error("kmoe gemm: operand too large for 32-bit tile offsets (K bytes %d)", kbytes);
     return KMOE_ERR_SHAPE;
   }
   const dim3 grid((unsigned)blocks);
   const dim3 block(GEMM_THREADS);
-#define KMOE_LAUNCH_GEMM(GU, F8, GA)                                                                       \
-  hipLaunchKernelGGL((grouped_gemm_kernel<GU, F8, GA>), grid, block, 0, s, a, lda, a_scale, row_token, row_index, \
-                     offsets, E, b, b_expert_rows, ldb, b_scale, kbytes, c, ldc, n_valid, n_tiles)
+  const int allow_split = 1;
+#define KMOE_LAUNCH_GEMM(GU, F8, GA)                                                                         \
+  hipLaunchKernelGGL((grouped_gemm_kernel<GU, F8, GA>), grid, block, 0, s, g, offsets, E, n_tiles, n_cu, \
+                     allow_split)
   if (row_token)
     KMOE_LAUNCH_GEMM(true, false, true);
   else if (gate_up && !fp8)
