@@ -98,9 +98,16 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
     wsrc[q] = (uint32_t)tr * (uint32_t)d * 2u + (uint32_t)chunk_of(tr);
   }
   const uint8_t* wbase = reinterpret_cast<const uint8_t*>(w_in);
+  // Workgroups walk K from different starting steps (blockIdx.x mod the step count):
+  // with every workgroup at the same K offset of 4 KiB-strided rows at once, the
+  // loads concentrate on a few memory channels (measured: 22% slower cold-cache).
+  // The sum order over K then depends on the workgroup, deterministically.
+  const int nk_all = d * 2 / RKB;
+  const int k_rot = (int)(blockIdx.x % (unsigned)nk_all);
   auto issue = [&](int kt) {
     uint8_t* st = smem + (kt % RT_STAGES) * RT_STAGE;
-    const int kb = kt * RKB;
+    const int kr = kt + k_rot;
+    const int kb = (kr < nk_all ? kr : kr - nk_all) * RKB;
 #pragma unroll
     for (int q = 0; q < G::XBLK; ++q)
       __builtin_amdgcn_global_load_lds(xsrc[q] + kb, (KMOE_LDS void*)(st + (wave * G::XBLK + q) * 1024), 16, 0, 0);
