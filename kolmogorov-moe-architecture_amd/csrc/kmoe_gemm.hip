@@ -54,7 +54,9 @@ constexpr int RPB = 1024 / KB;                        // tile rows per 1 KiB loa
 constexpr int BLK_PER_WAVE = (BM * KB / 1024) / 4;    // load blocks per wave per operand per step
 // output staging: 256 rows x up to 256 bf16 columns, rows padded by 16 bytes
 constexpr int OUT_STRIDE_MAX = 256 * 2 + 16;
-constexpr int GEMM_LDS = (NST * 2 * TB > BM * OUT_STRIDE_MAX) ? NST * 2 * TB : BM * OUT_STRIDE_MAX;
+constexpr int SCALE_LDS = (NST * 2 * TB > BM * OUT_STRIDE_MAX) ? NST * 2 * TB : BM * OUT_STRIDE_MAX;
+// fp8: the tile's A-row and B-row scales (256 floats each) after the stages / output staging
+constexpr int GEMM_LDS = SCALE_LDS + 2 * BM * 4;
 static_assert(GEMM_LDS <= 160 * 1024, "LDS budget");
 
 // Byte offset of 16-byte chunk `chunk` of tile row `row`.  A 128-byte row puts rows
@@ -271,6 +273,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
     for (int j = 0; j < WNB; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  // fp8 scales of the tile's A rows (thread = row) and B rows (thread = LDS B row),
+  // loaded now and put in LDS for the epilogue (rows past the expert's end: 0)
+  float sa_v = 0.0f, sb_v = 0.0f;
+  if constexpr (FP8) {
+    const int row = m0 + tid;
+    if (row < m_end) sa_v = g.a_scale[row];
+    if (tid < BNT) sb_v = g.b_scale[brow0 + b_packed_row<GATE_UP, WNB>(tid, q)];
+  }
 
   // Tile loads: a stage tile is a set of 1 KiB blocks (8 rows of 128 B); wave w loads
   // A blocks [8w, 8w+8) and B blocks [BLK_B w, BLK_B w + BLK_B) into registers and
@@ -399,17 +409,22 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   constexpr int NJ = GATE_UP ? WNB / 2 : WNB;        // output column blocks per wave
   constexpr int OSTR = NC * 2 + 16;                  // LDS row stride (bytes)
   const bool odd = lr & 1;
+  float* const sa_l = reinterpret_cast<float*>(lds + SCALE_LDS);
+  float* const sb_l = sa_l + BM;
+  if constexpr (FP8) {
+    sa_l[tid] = sa_v;
+    if (tid < BNT) sb_l[tid] = sb_v;
+  }
   __syncthreads();
   // lane's write address for p = 0 of block (0, 0): even lanes row 4lh col lr,
   // odd lanes row 4lh+1 col lr-1
   uint8_t* const wbase = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR + (wn * (NC / 2) + lr - (odd ? 1 : 0)) * 2;
-  auto bscale = [&](int j) { return g.b_scale[brow0 + b_packed_row<GATE_UP, WNB>(b_lds_row<GATE_UP, WNB>(wn, j, lr), q)]; };
+  auto bscale = [&](int j) { return sb_l[b_lds_row<GATE_UP, WNB>(wn, j, lr)]; };
   auto result = [&](int mi, int r, int jo) -> float {
     if (GATE_UP) {
       float gg = acc[mi][jo][r], u = acc[mi][jo + WNB / 2][r];
       if (FP8) {
-        const int grow = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        const float sa = grow < m_end ? g.a_scale[grow] : 1.0f;
+        const float sa = sa_l[wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
         gg *= sa * bscale(jo);
         u *= sa * bscale(jo + WNB / 2);
       }
@@ -417,8 +432,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
     } else {
       float v = acc[mi][jo][r];
       if (FP8) {
-        const int grow = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        const float sa = grow < m_end ? g.a_scale[grow] : 1.0f;
+        const float sa = sa_l[wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
         v *= sa * bscale(jo);
       }
       return v;
