@@ -5,10 +5,11 @@
 // config 3 (keep the first `capacity` assignments of each expert in assignment
 // order, drop the rest).
 //
-// Three launches, no host sync:
+// Two or three launches, no host sync:
 //   1. hist:    per-block (DTB tokens) expert histograms
 //   2. scan:    per-expert exclusive scan over blocks -> block bases, counts,
-//               kept counts and expert offsets
+//               kept counts and expert offsets (up to FUSED_SCAN_MAX_BLOCKS blocks
+//               each permute block computes its own share of this instead)
 //   3. permute: per-block stable ranks via wave ballots, slot tables, then one
 //               read of each token row and k 16-byte-vector row writes
 #include "kmoe_common.h"
@@ -76,20 +77,82 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ 
 }
 
 // Tables of a block of DTB tokens, then (xperm != nullptr: the bf16 copy) the rows.
+// FUSED_SCAN: the block computes its own per-expert base (sum of the counts of the
+// blocks before it), the totals and the expert offsets from all block counts (block
+// 0 also writes counts and offsets), instead of reading them from the scan kernel:
+// one launch less, for up to FUSED_SCAN_MAX_BLOCKS blocks.
+constexpr int FUSED_SCAN_MAX_BLOCKS = 1024;
+template <bool FUSED_SCAN>
 __global__ __launch_bounds__(DTHREADS) void permute_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, int64_t T, int d,
     const int64_t* __restrict__ idx, const void* __restrict__ wsrc, int w_dtype, int k, int E, int64_t capacity,
-    const int32_t* __restrict__ block_base, const int32_t* __restrict__ offsets, int32_t* __restrict__ row_token,
+    const int32_t* __restrict__ block_counts, int64_t nblk, const int32_t* __restrict__ block_base,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ row_token,
     int32_t* __restrict__ slot_row, float* __restrict__ slot_w, uint16_t* __restrict__ xperm) {
   __shared__ int wave_cnt[DTHREADS / 64][KMOE_MAX_EXPERTS];
   __shared__ int running[KMOE_MAX_EXPERTS];
   __shared__ int dest[DTB * 8];  // k <= 8
+  __shared__ int base_l[KMOE_MAX_EXPERTS];
+  __shared__ int off_l[KMOE_MAX_EXPERTS + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = (int64_t)blockIdx.x * DTB;
   const int64_t a0 = t0 * k;
   const int64_t a1 = min<int64_t>(a0 + (int64_t)DTB * k, T * k);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   if (tid < E) running[tid] = 0;
+  if constexpr (FUSED_SCAN) {
+    // thread (j, e) of an ep x (DTHREADS/ep) grid sums blocks j, j + DTHREADS/ep, ...
+    __shared__ int red_pre[DTHREADS], red_tot[DTHREADS];
+    int ep = 1;
+    while (ep < E) ep <<= 1;
+    const int e = tid & (ep - 1), j = tid / ep, ng = DTHREADS / ep;
+    int pre = 0, tot = 0;
+    if (e < E) {
+      for (int64_t b = j; b < nblk; b += ng) {
+        const int v = block_counts[b * E + e];
+        tot += v;
+        if (b < (int64_t)blockIdx.x) pre += v;
+      }
+    }
+    red_pre[tid] = pre;
+    red_tot[tid] = tot;
+    __syncthreads();
+    if (wave == 0) {
+      // lane e: sums over the groups, then the exclusive scan of the kept counts
+      int p = 0, c = 0;
+      if (lane < E) {
+        for (int jj = 0; jj < ng; ++jj) {
+          p += red_pre[jj * ep + lane];
+          c += red_tot[jj * ep + lane];
+        }
+      }
+      const int kept = (capacity > 0 && c > capacity) ? (int)capacity : c;
+      int incl = kept;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
+      }
+      if (lane < E) {
+        base_l[lane] = p;
+        off_l[lane] = incl - kept;
+        if (blockIdx.x == 0) {
+          counts[lane] = c;
+          offsets[lane] = incl - kept;
+        }
+      }
+      const int all = __shfl(incl, E - 1, 64);
+      if (lane == 0) {
+        off_l[E] = all;
+        if (blockIdx.x == 0) offsets[E] = all;
+      }
+    }
+  } else {
+    if (tid < E) {
+      base_l[tid] = block_base[(int64_t)blockIdx.x * E + tid];
+      off_l[tid] = offsets[tid];
+    }
+  }
   __syncthreads();
 
   // ---- ranks, in assignment order (chunks of 256 assignments)
@@ -109,9 +172,9 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
       if (e >= 0) {
         int r = running[e] + rank_w;
         for (int w = 0; w < wave; ++w) r += wave_cnt[w][e];
-        const int64_t g = (int64_t)block_base[(int64_t)blockIdx.x * E + e] + r;
+        const int64_t g = (int64_t)base_l[e] + r;
         if (capacity <= 0 || g < capacity) {
-          row = offsets[e] + (int)g;
+          row = off_l[e] + (int)g;
           row_token[row] = (int32_t)(a / k);
         }
       }
@@ -295,13 +358,20 @@ extern "C" int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T,
     return kmoe::check_launch("kmoe_dispatch(scan)");
   }
   hipLaunchKernelGGL(hist_kernel, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, topk_idx, T, k, E, block_counts);
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, nblk, E, capacity, block_base, counts,
-                     offsets);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const bool fp8 = xperm_dtype == KMOE_DTYPE_FP8_E4M3;
-  hipLaunchKernelGGL(permute_kernel, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d, topk_idx,
-                     topk_w, w_dtype, k, E, capacity, block_base, offsets, row_token, slot_row, slot_w,
-                     fp8 ? nullptr : static_cast<uint16_t*>(xperm));
+  uint16_t* xo = fp8 ? nullptr : static_cast<uint16_t*>(xperm);
+  if (nblk <= FUSED_SCAN_MAX_BLOCKS) {
+    hipLaunchKernelGGL(permute_kernel<true>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
+                       topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, block_base, counts, offsets,
+                       row_token, slot_row, slot_w, xo);
+  } else {
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, nblk, E, capacity, block_base, counts,
+                       offsets);
+    hipLaunchKernelGGL(permute_kernel<false>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
+                       topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, block_base, counts, offsets,
+                       row_token, slot_row, slot_w, xo);
+  }
   if (fp8)
     hipLaunchKernelGGL(quant_scatter_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0, s, xp,
                        row_index, T, d, k, slot_row, static_cast<uint8_t*>(xperm), xperm_scale);
