@@ -165,14 +165,17 @@ int kmoe_combine(const void* yperm, int d, const int32_t* src_row, const float* 
 /* Expert-choice selection — replaces ExpertChoiceRouter.forward (moe.py:494-530).
  * For each sequence b and expert e, select the C tokens of sequence b with the
  * largest fp32 logit (= largest softmax-over-tokens probability; equal logits ->
- * lowest token index first), in descending order, and write
+ * lowest token index first) and write
  *   idx (B,E,C) int64, w (B,E,C) f32 = p / (sum_c p + 1e-9), p = softmax over S.
+ * order 1: the C slots in descending order (the reference's topk order, equal
+ * logits lowest index first); order 0: in ascending token order (the same tokens
+ * and weights; what a layer forward needs, without the sort).
  * Also writes the dispatch/combine tables: row_token (E*B*C, expert-major rows
  * e*B*C + b*C + c -> token b*S + idx), offsets (E+1) and the per-token combine
  * table src_row/src_w (B*S, E): permuted row of (token, expert) or -1.
  * Requires C <= S.  workspace: kmoe_ec_workspace_bytes.                      */
 size_t kmoe_ec_workspace_bytes(int B, int64_t S, int E);
-int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int64_t C, int64_t* idx, float* w,
+int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int64_t C, int order, int64_t* idx, float* w,
                    int32_t* row_token, int32_t* offsets, int32_t* src_row, float* src_w, void* workspace,
                    size_t workspace_bytes, void* stream);
 

@@ -153,7 +153,8 @@ __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
 }
 
 __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __restrict__ logits, int B, int S, int E,
-                                                                int C, int64_t* __restrict__ idx, float* __restrict__ w,
+                                                                int C, int order, int64_t* __restrict__ idx,
+                                                                float* __restrict__ w,
                                                                 int32_t* __restrict__ row_token,
                                                                 int32_t* __restrict__ offsets,
                                                                 int32_t* __restrict__ src_row,
@@ -196,6 +197,15 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
     if (pos < C) sorted[pos] = ((uint64_t)keys[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
   });
   __syncthreads();
+  // sum of the selected probabilities, over the selection in token order (the same
+  // sum whichever output order is asked for)
+  float psel = 0.0f;
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    const int s = (int)(0xffffffffu - (uint32_t)(sorted[c] & 0xffffffffu));
+    psel += __expf(key_value(keys[s]) - mx) / den;
+  }
+  psel = block_sum(psel, s_red);
+  if (order == 1) {
   // bitonic sort, descending by (key, -index).  Element i lives in thread i % 1024,
   // register slot i / 1024 (Cp <= 8192: up to 8 per thread): strides < 64 are
   // exchanged with wave shuffles, strides >= 1024 inside the thread, and only the
@@ -256,13 +266,8 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
       if (h < per) sorted[t + h * SEL_THREADS] = v[h];
     __syncthreads();
   }
-  // weights: p / (sum_sel p + 1e-9)  (moe.py:528)
-  float psel = 0.0f;
-  for (int c = threadIdx.x; c < C; c += blockDim.x) {
-    const int s = (int)(0xffffffffu - (uint32_t)(sorted[c] & 0xffffffffu));
-    psel += __expf(key_value(keys[s]) - mx) / den;
   }
-  psel = block_sum(psel, s_red);
+  // weights: p / (sum_sel p + 1e-9)  (moe.py:528)
   const float inv = 1.0f / (psel + 1e-9f);
   const int64_t BC = (int64_t)B * C;
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
@@ -362,9 +367,9 @@ extern "C" size_t kmoe_ec_workspace_bytes(int B, int64_t S, int E) {
   return 0;
 }
 
-extern "C" int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int64_t C, int64_t* idx, float* w,
-                              int32_t* row_token, int32_t* offsets, int32_t* src_row, float* src_w, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+extern "C" int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int64_t C, int order, int64_t* idx,
+                              float* w, int32_t* row_token, int32_t* offsets, int32_t* src_row, float* src_w,
+                              void* workspace, size_t workspace_bytes, void* stream) {
   (void)workspace;
   (void)workspace_bytes;
   KMOE_REQUIRE(logits && idx && w && row_token && offsets && src_row && src_w, KMOE_ERR_NULL,
@@ -375,11 +380,12 @@ extern "C" int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int6
   KMOE_REQUIRE(C >= 1 && C <= S && C <= SEL_MAX_C, KMOE_ERR_SHAPE, "kmoe_ec_select: C=%lld not in [1,min(S,%d)]",
                (long long)C, SEL_MAX_C);
   KMOE_REQUIRE((int64_t)E * B * C < ((int64_t)1 << 31), KMOE_ERR_SHAPE, "kmoe_ec_select: E*B*C must fit in int32");
+  KMOE_REQUIRE(order == 0 || order == 1, KMOE_ERR_SHAPE, "kmoe_ec_select: order=%d not 0 or 1", order);
   hipStream_t s = kmoe::as_stream(stream);
   const int64_t n = (int64_t)B * S * E;
   hipLaunchKernelGGL(fill_i32_kernel, dim3(256), dim3(256), 0, s, src_row, n, -1);
   hipLaunchKernelGGL(ec_select_kernel, dim3((unsigned)(B * E)), dim3(SEL_THREADS), 0, s, logits, B, (int)S, E, (int)C,
-                     idx, w, row_token, offsets, src_row, src_w);
+                     order, idx, w, row_token, offsets, src_row, src_w);
   return kmoe::check_launch("kmoe_ec_select");
 }
 

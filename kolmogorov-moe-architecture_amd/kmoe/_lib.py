@@ -49,7 +49,7 @@ _SIGNATURES = {
     "kmoe_grouped_swiglu": (_i32, [_vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_combine": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _i32, _vp]),
     "kmoe_ec_workspace_bytes": (_sz, [_i32, _i64, _i32]),
-    "kmoe_ec_select": (_i32, [_vp, _i32, _i64, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "kmoe_ec_select": (_i32, [_vp, _i32, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "kmoe_mod_workspace_bytes": (_sz, [_i32, _i64]),
     "kmoe_mod_select": (_i32, [_vp, _i32, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
 }

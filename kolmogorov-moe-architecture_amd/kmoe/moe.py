@@ -122,12 +122,12 @@ class ExpertChoiceRouter(_RouterMLP):
     def capacity(self, seq_len: int) -> int:
         return int(math.ceil(seq_len * self.capacity_factor / self.n_experts))  # moe.py:511
 
-    def route(self, hidden_states: torch.Tensor):
+    def route(self, hidden_states: torch.Tensor, descending: bool = True):
         B, S, d = hidden_states.shape
         C = min(self.capacity(S), S)
         w_in, w_out = self._kernel_weights()
         r = ops.router(hidden_states.reshape(B * S, d), w_in, w_out, 0)
-        sel = ops.ec_select(r.logits, B, S, self.n_experts, C)
+        sel = ops.ec_select(r.logits, B, S, self.n_experts, C, descending=descending)
         return r, sel, C
 
     def forward(self, hidden_states: torch.Tensor):
@@ -310,7 +310,9 @@ class MoELayer(nn.Module):
     def _forward_expert_choice(self, hidden_states: torch.Tensor) -> torch.Tensor:
         B, S, d = hidden_states.shape
         x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
-        r, sel, C = self.router.route(x)
+        # the layer output does not depend on the order of an expert's C slots: take
+        # them in token order (no sort)
+        r, sel, C = self.router.route(x, descending=False)
         y = self.grouped_experts_ec.run(x.reshape(B * S, d), sel, B, S, C, out_dtype=self._out_dtype(hidden_states))
         if self.training and self.router_z_loss_weight > 0:
             out = ops.aux_loss(r.partials, B * S, self.n_experts, None, 1, 0.0, self.router_z_loss_weight)

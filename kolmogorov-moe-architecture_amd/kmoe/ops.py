@@ -289,8 +289,11 @@ class ECSelectOut(NamedTuple):
     src_w: torch.Tensor      # (B*S, E) f32
 
 
-def ec_select(logits, B, S, E, C) -> ECSelectOut:
-    """Expert-choice top-C per (sequence, expert) (moe.py:494-530)."""
+def ec_select(logits, B, S, E, C, descending=True) -> ECSelectOut:
+    """Expert-choice top-C per (sequence, expert) (moe.py:494-530).
+
+    descending=True gives the reference's topk order; False the same selection in
+    ascending token order (no sort: enough for a layer forward)."""
     _need_gpu(logits)
     logits = _contig(logits, torch.float32)
     dev = logits.device
@@ -301,7 +304,8 @@ def ec_select(logits, B, S, E, C) -> ECSelectOut:
     src_row = torch.empty(B * S, E, device=dev, dtype=torch.int32)
     src_w = torch.empty(B * S, E, device=dev, dtype=torch.float32)
     with _Stage("ec_select"):
-        _lib.call("kmoe_ec_select", ptr(logits), B, S, E, C, ptr(idx), ptr(w), ptr(row_token), ptr(offsets),
+        _lib.call("kmoe_ec_select", ptr(logits), B, S, E, C, 1 if descending else 0, ptr(idx), ptr(w),
+              ptr(row_token), ptr(offsets),
               ptr(src_row), ptr(src_w), None, 0, _stream(logits))
     return ECSelectOut(idx, w, row_token, offsets, src_row, src_w)
 

@@ -91,9 +91,9 @@ def test_gemm_and_combine_validation(lib):
 
 
 def test_select_validation(lib):
-    assert _err(lib, "kmoe_ec_select", FAKE, 1, 100, 4, 101, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
+    assert _err(lib, "kmoe_ec_select", FAKE, 1, 100, 4, 101, 1, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
                 NULL)[0] == -2
-    assert _err(lib, "kmoe_ec_select", FAKE, 1, 100000, 4, 10, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
+    assert _err(lib, "kmoe_ec_select", FAKE, 1, 100000, 4, 10, 1, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
                 NULL)[0] == -6
     assert _err(lib, "kmoe_mod_select", FAKE, 2, 100, 64, FAKE, 0, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
                 NULL)[0] == -2

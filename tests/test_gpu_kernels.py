@@ -318,6 +318,30 @@ def test_ec_select_parity(dev, B, S, E, C, ties):
     assert np.array_equal(out.src_row.cpu().numpy(), src_row)
 
 
+@pytest.mark.parametrize("B,S,E,C,ties", [(1, 16384, 16, 2048, False), (2, 300, 4, 75, True), (1, 12000, 4, 5000, True)])
+def test_ec_select_token_order(dev, B, S, E, C, ties):
+    """order 0 (the layer forward's): the descending selection with each expert's
+    slots in ascending token order; weights bit-identical per (token, expert)."""
+    g = torch.Generator().manual_seed(42)
+    lg = torch.randn(B * S, E, generator=g) * 0.2
+    if ties:
+        lg = torch.round(lg * 8) / 8
+    desc = ops.ec_select(lg.to(dev), B, S, E, C)
+    asc = ops.ec_select(lg.to(dev), B, S, E, C, descending=False)
+    di, dw = desc.idx.cpu().numpy(), desc.w.cpu().numpy()
+    ai, aw = asc.idx.cpu().numpy(), asc.w.cpu().numpy()
+    order = np.argsort(di, axis=-1, kind="stable")
+    assert np.array_equal(ai, np.take_along_axis(di, order, axis=-1))
+    assert np.array_equal(aw, np.take_along_axis(dw, order, axis=-1))  # bit-identical
+    row_token, offsets, src_row, src_w = O.ec_tables(ai, aw, S)
+    assert np.array_equal(asc.row_token.cpu().numpy(), row_token)
+    assert np.array_equal(asc.offsets.cpu().numpy(), offsets)
+    assert np.array_equal(asc.src_row.cpu().numpy(), src_row)
+    sel = src_row >= 0
+    assert np.array_equal(asc.src_w.cpu().numpy()[sel], desc.src_w.cpu().numpy()[sel])
+    assert np.array_equal(asc.src_w.cpu().numpy()[sel], src_w[sel].astype(np.float32))
+
+
 @pytest.mark.parametrize("B,S,keep,ties", [(4, 2048, 1536, False), (2, 100, 75, True), (1, 7, 1, False)])
 def test_mod_select_parity(dev, B, S, keep, ties):
     d = 256
