@@ -121,8 +121,9 @@ __device__ void radix_select_desc(const uint32_t* keys, int n, int C, uint32_t* 
 
 // Index-ordered compaction of the selection; calls emit(i, pos) for each selected
 // index i with its position pos in index order.  Threads own contiguous chunks.
-template <typename Emit>
-__device__ void compact_selected(const uint32_t* keys, int n, uint32_t thr, int need, int* s_wave, Emit emit) {
+template <typename Emit, typename Skip>
+__device__ void compact_selected(const uint32_t* keys, int n, uint32_t thr, int need, int* s_wave, Emit emit,
+                                 Skip skip) {
   const int chunk = (n + (int)blockDim.x - 1) / (int)blockDim.x;
   const int i0 = min(n, (int)threadIdx.x * chunk), i1 = min(n, i0 + chunk);
   int n_eq = 0;
@@ -144,12 +145,11 @@ __device__ void compact_selected(const uint32_t* keys, int n, uint32_t thr, int 
     const uint32_t k = keys[i];
     bool take = k > thr;
     if (k == thr) take = (eqr++ < need);
-    if (take) emit(i, pos++);
+    if (take)
+      emit(i, pos++);
+    else
+      skip(i);
   }
-}
-
-__global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = v;
 }
 
 __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __restrict__ logits, int B, int S, int E,
@@ -168,11 +168,22 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
   const int b = blockIdx.x / E, e = blockIdx.x % E;
   const float* lg = logits + (int64_t)b * S * E + e;
 
+  // the sequence's column of logits: all of a thread's (strided) loads in flight at once
+  constexpr int PER = SEL_MAX_S / SEL_THREADS;
+  float v[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = threadIdx.x + u * SEL_THREADS;
+    v[u] = i < S ? lg[(int64_t)i * E] : 0.0f;
+  }
   float mx = -INFINITY;
-  for (int i = threadIdx.x; i < S; i += blockDim.x) {
-    const float v = lg[(int64_t)i * E];
-    keys[i] = order_key(v);
-    mx = fmaxf(mx, v);
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = threadIdx.x + u * SEL_THREADS;
+    if (i < S) {
+      keys[i] = order_key(v[u]);
+      mx = fmaxf(mx, v[u]);
+    }
   }
   mx = wave_max(mx);
   if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
@@ -182,7 +193,9 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
   __syncthreads();
   // softmax denominator over the whole sequence (moe.py:520)
   float den = 0.0f;
-  for (int i = threadIdx.x; i < S; i += blockDim.x) den += __expf(key_value(keys[i]) - mx);
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (threadIdx.x + u * SEL_THREADS < S) den += __expf(v[u] - mx);
   den = block_sum(den, s_red);
 
   uint32_t thr;
@@ -193,9 +206,15 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
   while (Cp < C) Cp <<= 1;
   for (int i = threadIdx.x; i < Cp; i += blockDim.x) sorted[i] = 0ull;
   __syncthreads();
-  compact_selected(keys, S, thr, need, s_wave, [&](int i, int pos) {
-    if (pos < C) sorted[pos] = ((uint64_t)keys[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-  });
+  // selected: into the sort buffer in token order; not selected: no row in the
+  // combine table (the selected ones get theirs with the weights below)
+  int32_t* const src_row_b = src_row + (int64_t)b * S * E + e;
+  compact_selected(
+      keys, S, thr, need, s_wave,
+      [&](int i, int pos) {
+        if (pos < C) sorted[pos] = ((uint64_t)keys[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+      },
+      [&](int i) { src_row_b[(int64_t)i * E] = -1; });
   __syncthreads();
   // sum of the selected probabilities, over the selection in token order (the same
   // sum whichever output order is asked for)
@@ -322,10 +341,7 @@ __global__ __launch_bounds__(SEL_THREADS) void mod_select_kernel(const float* __
   __shared__ float s_red[SEL_THREADS / 64];
   const int b = blockIdx.x;
   const float* rb = r + (int64_t)b * S;
-  for (int i = threadIdx.x; i < S; i += blockDim.x) {
-    keys[i] = order_key(rb[i]);
-    out_map[(int64_t)b * S + i] = -1;
-  }
+  for (int i = threadIdx.x; i < S; i += blockDim.x) keys[i] = order_key(rb[i]);
   __syncthreads();
   uint32_t thr;
   int need;
@@ -348,7 +364,7 @@ __global__ __launch_bounds__(SEL_THREADS) void mod_select_kernel(const float* __
     token_rows[o] = (int32_t)((int64_t)b * S + i);
     out_map[(int64_t)b * S + i] = (int32_t)o;
     den += __expf(rb[i] - mx);
-  });
+  }, [&](int i) { out_map[(int64_t)b * S + i] = -1; });
   den = block_sum(den, s_red);
   const float inv = 1.0f / den;
   __syncthreads();
@@ -382,8 +398,6 @@ extern "C" int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int6
   KMOE_REQUIRE((int64_t)E * B * C < ((int64_t)1 << 31), KMOE_ERR_SHAPE, "kmoe_ec_select: E*B*C must fit in int32");
   KMOE_REQUIRE(order == 0 || order == 1, KMOE_ERR_SHAPE, "kmoe_ec_select: order=%d not 0 or 1", order);
   hipStream_t s = kmoe::as_stream(stream);
-  const int64_t n = (int64_t)B * S * E;
-  hipLaunchKernelGGL(fill_i32_kernel, dim3(256), dim3(256), 0, s, src_row, n, -1);
   hipLaunchKernelGGL(ec_select_kernel, dim3((unsigned)(B * E)), dim3(SEL_THREADS), 0, s, logits, B, (int)S, E, (int)C,
                      order, idx, w, row_token, offsets, src_row, src_w);
   return kmoe::check_launch("kmoe_ec_select");
