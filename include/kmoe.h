@@ -162,6 +162,20 @@ int kmoe_combine(const void* yperm, int d, const int32_t* src_row, const float* 
                  void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Capacity-balanced top-k — replaces Router._balanced_topk_assignment
+ * (moe.py:353-421), taken by Router.forward when moe_balanced_routing is set
+ * (moe.py:443-451).  From fp32 logits (T,E) (kmoe_router with k = 0):
+ * k rounds, cap = max(T*k/E, 1); in round r an expert is full when the picks of
+ * rounds < r reached cap, and each token takes its best expert (logit descending,
+ * equal logits -> lowest index) that it has not picked and is not full, else its
+ * best expert not picked yet.  idx (T,k) int64 in pick order; w (T,k) f32 = the
+ * picks' softmax probabilities / (their sum + 1e-9).
+ * workspace: kmoe_balanced_workspace_bytes (per-round counts; no zeroing needed). */
+size_t kmoe_balanced_workspace_bytes(int E, int k);
+int kmoe_balanced_topk(const float* logits, int64_t T, int E, int k, int64_t* idx, float* w, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Expert-choice selection — replaces ExpertChoiceRouter.forward (moe.py:494-530).
  * For each sequence b and expert e, select the C tokens of sequence b with the
  * largest fp32 logit (= largest softmax-over-tokens probability; equal logits ->

@@ -48,6 +48,8 @@ _SIGNATURES = {
     "kmoe_quant_rows_fp8": (_i32, [_vp, _i64, _vp, _i32, _vp, _vp, _vp]),
     "kmoe_grouped_swiglu": (_i32, [_vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_combine": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _i32, _vp]),
+    "kmoe_balanced_workspace_bytes": (_sz, [_i32, _i32]),
+    "kmoe_balanced_topk": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "kmoe_ec_workspace_bytes": (_sz, [_i32, _i64, _i32]),
     "kmoe_ec_select": (_i32, [_vp, _i32, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "kmoe_mod_workspace_bytes": (_sz, [_i32, _i64]),

@@ -91,15 +91,19 @@ class Router(_RouterMLP):
 
     def route(self, x2d: torch.Tensor, row_index: Optional[torch.Tensor] = None,
               T: Optional[int] = None) -> ops.RouterOut:
-        """Kernel-level routing of flattened tokens: fp32 logits, int64 idx, f32 weights."""
-        if self.balanced_routing:
-            raise NotImplementedError("kmoe: moe_balanced_routing (moe.py:353-421) is not implemented")
+        """Kernel-level routing of flattened tokens: fp32 logits, int64 idx, f32 weights.
+        With moe_balanced_routing the picks are the capacity-balanced assignment
+        (moe.py:443-451) over all the tokens of the call."""
         w_in, w_out = self._kernel_weights()
         bias = None
         if self.logit_bias is not None:
             if self.logit_bias.device != x2d.device:
                 self.logit_bias = self.logit_bias.to(x2d.device)
             bias = self.logit_bias
+        if self.balanced_routing:
+            r = ops.router(x2d, w_in, w_out, 0, bias=bias, row_index=row_index, T=T)
+            idx, w = ops.balanced_topk(r.logits, self.top_k)
+            return ops.RouterOut(r.logits, idx, w, r.partials)
         return ops.router(x2d, w_in, w_out, self.top_k, bias=bias, row_index=row_index, T=T)
 
     def forward(self, hidden_states: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:

@@ -108,6 +108,23 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None) -> RouterOut:
     return RouterOut(logits, idx, w, partials)
 
 
+def balanced_topk(logits, k):
+    """Capacity-balanced top-k of Router._balanced_topk_assignment (moe.py:353-421)
+    from fp32 logits (T, E): returns (idx (T,k) int64, w (T,k) f32)."""
+    _need_gpu(logits)
+    logits = _contig(logits, torch.float32)
+    T, E = logits.shape
+    dev = logits.device
+    idx = torch.empty(T, k, device=dev, dtype=torch.int64)
+    w = torch.empty(T, k, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    wsb = lib.kmoe_balanced_workspace_bytes(E, k)
+    ws = torch.empty(max(wsb, 4), device=dev, dtype=torch.uint8)
+    with _Stage("router"):
+        _lib.call("kmoe_balanced_topk", ptr(logits), T, E, k, ptr(idx), ptr(w), ptr(ws), wsb, _stream(logits))
+    return idx, w
+
+
 def aux_loss(partials, T, E, counts, k, w_lb, w_z):
     """(aux, load_balance, z) of MoELayer._compute_auxiliary_losses (moe.py:840-939)."""
     out = torch.empty(3, device=partials.device, dtype=torch.float32)

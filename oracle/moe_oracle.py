@@ -54,6 +54,39 @@ def topk_select(logits, k):
     return order.astype(np.int64), ex / ex.sum(axis=1, keepdims=True)
 
 
+def balanced_topk(logits, k):
+    """Capacity-balanced greedy assignment (Router._balanced_topk_assignment,
+    moe.py:353-421), in k rounds over all tokens at once.
+
+    cap = max(T*k // E, 1).  Round r: experts whose count after rounds < r has
+    reached cap are masked for every token, as are the token's own earlier picks;
+    each token takes its best remaining expert (fp32 logit descending, equal logits
+    -> lowest expert index, the rule of topk_select; softmax is monotone, so this
+    is the argmax of the probabilities); a token with every remaining expert
+    masked takes its best expert not picked yet, ignoring capacity (moe.py:402-407).
+    Counts then add the round's picks (moe.py:414).  Weights: the picks'
+    probabilities / (their sum + 1e-9) (moe.py:411,420)."""
+    lg = np.asarray(logits, dtype=np.float64)
+    T, E = lg.shape
+    cap = max((T * k) // E, 1)
+    p = softmax(lg)
+    counts = np.zeros(E, dtype=np.int64)
+    taken = np.zeros((T, E), dtype=bool)
+    idx = np.zeros((T, k), dtype=np.int64)
+    wraw = np.zeros((T, k), dtype=np.float64)
+    for r in range(k):
+        masked = np.where(taken | (counts >= cap)[None, :], -np.inf, lg)
+        best = np.argmax(masked, axis=1)  # first maximum: lowest index
+        none = np.isneginf(masked.max(axis=1))
+        if none.any():
+            best[none] = np.argmax(np.where(taken[none], -np.inf, lg[none]), axis=1)
+        idx[:, r] = best
+        wraw[:, r] = p[np.arange(T), best]
+        counts += np.bincount(best, minlength=E)
+        taken[np.arange(T), best] = True
+    return idx, wraw / (wraw.sum(axis=1, keepdims=True) + 1e-9)
+
+
 def aux_losses(logits, counts, T, k, E, w_lb=0.01, w_z=0.001):
     """Load-balance and z losses (moe.py:840-939).
 

@@ -29,6 +29,30 @@ def router_tc(x3d, w_in, w_out, k):
     return w / w.sum(dim=-1, keepdim=True), idx, logits
 
 
+def balanced_topk_tc(probs, k):
+    """Router._balanced_topk_assignment's op sequence (moe.py:353-421) on (T, E)
+    probabilities: per round, capacity-masked max, fallback to the unmasked
+    max, gather of the original probability, count update, own-pick masking."""
+    T, E = probs.shape
+    cap = max((T * k) // E, 1)
+    sel = torch.zeros(T, k, dtype=torch.long)
+    wts = torch.zeros(T, k, dtype=probs.dtype)
+    work = probs.clone()
+    counts = torch.zeros(E, dtype=torch.long)
+    for r in range(k):
+        m = work.clone()
+        m[:, counts >= cap] = float("-inf")
+        best_p, best = m.max(dim=-1)
+        reset = best_p == float("-inf")
+        if reset.any():
+            best[reset] = work[reset].argmax(dim=-1)
+        sel[:, r] = best
+        wts[:, r] = probs.gather(1, best.unsqueeze(-1)).squeeze(-1)
+        counts.scatter_add_(0, best, torch.ones_like(best))
+        work.scatter_(1, best.unsqueeze(-1), float("-inf"))
+    return wts / (wts.sum(dim=-1, keepdim=True) + 1e-9), sel
+
+
 def grouped_experts_tc(x, idx, w, w1, w2, w3):
     """GroupedExperts.forward's padded-bmm formulation."""
     n_tok, k = idx.shape

@@ -98,3 +98,5 @@ def test_select_validation(lib):
     assert _err(lib, "kmoe_mod_select", FAKE, 2, 100, 64, FAKE, 0, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
                 NULL)[0] == -2
     assert _err(lib, "kmoe_aux_loss", NULL, 16, 4, NULL, 2, 0.01, 0.001, FAKE, NULL)[0] == -1
+    assert _err(lib, "kmoe_balanced_topk", FAKE, 100, 4, 5, FAKE, FAKE, FAKE, 1024, NULL)[0] == -2  # k > E
+    assert _err(lib, "kmoe_balanced_topk", FAKE, 100, 4, 2, FAKE, FAKE, FAKE, 4, NULL)[0] == -4  # workspace

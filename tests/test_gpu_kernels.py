@@ -93,6 +93,24 @@ def test_aux_loss_parity(dev):
     np.testing.assert_allclose(npf(z_only), [0.001 * z, 0.0, z], rtol=2e-5)
 
 
+# ------------------------------------------------------------------ balanced top-k
+@pytest.mark.parametrize("T,E,k,mode", [(16384, 16, 2, "skew"), (3000, 8, 3, "ties"), (4096, 64, 8, "skew"),
+                                        (8, 4, 3, "fallback"), (1, 5, 2, "plain"), (700, 6, 6, "ties")])
+def test_balanced_topk_parity(dev, T, E, k, mode):
+    g = torch.Generator().manual_seed(60 + T)
+    lg = torch.randn(T, E, generator=g)
+    if mode == "skew":
+        lg = lg + 2.0 * torch.linspace(1, 0, E)  # popular early experts: capacity bites
+    elif mode == "ties":
+        lg = torch.round(lg * 2) / 2
+    elif mode == "fallback":
+        lg = torch.tensor([[3.0, 2.0, 1.0, 0.0]] * 6 + [[1.0, 0.0, 3.0, 2.0]] * 2)  # last round: 2 tokens all-full
+    idx, w = ops.balanced_topk(lg.to(dev), k)
+    ri, rw = O.balanced_topk(lg.numpy(), k)
+    assert np.array_equal(idx.cpu().numpy(), ri)
+    np.testing.assert_allclose(npf(w), rw, rtol=2e-6, atol=1e-7)
+
+
 # ------------------------------------------------------------------ dispatch
 def _routing(T, k, E, seed, skew=False):
     g = torch.Generator().manual_seed(seed)

@@ -90,6 +90,35 @@ def test_cfg1_small_full_parity(dev, cfg_cache):
     assert aux2 == 0.0 and torch.equal(y2, y)
 
 
+def test_balanced_routing_layer(dev):
+    """moe_balanced_routing=True (moe.py:443-451): config 1 dimensions with a logit
+    skew so that capacity bites; routing bit-exact from the kernel's fp32 logits,
+    output against the oracle experts."""
+    wl = synth.WORKLOADS[1]
+    t = synth.make_tensors(wl, "cpu")
+    cfg = wl.config()
+    cfg.moe_balanced_routing = True
+    from kmoe.moe import MoELayer
+    layer = synth.load_into(MoELayer(cfg, 0).to(device=dev, dtype=wl.dtype), {k: v.to(dev) for k, v in t.items()})
+    with torch.no_grad():
+        layer.router.router[2].weight[:2] += 0.05  # experts 0 and 1 preferred by most tokens
+        x = t["x"].to(dev)
+        y = layer(x)
+        r = layer.router.route(x.reshape(wl.T, wl.d).to(torch.bfloat16))
+    lg = f(r.logits)
+    idx, w = O.balanced_topk(lg, wl.k)
+    assert np.array_equal(r.idx.cpu().numpy(), idx)
+    counts = np.bincount(idx.reshape(-1), minlength=wl.E)
+    assert np.array_equal(layer.last_expert_counts.cpu().numpy(), counts)
+    plain, _ = O.topk_select(lg, wl.k)
+    assert not np.array_equal(plain, idx)  # the capacity rule changed some picks
+    bf = lambda a: f(a.to(torch.bfloat16))
+    W = (bf(t["w1"]), bf(t["w2"]), bf(t["w3"]))
+    tokens = list(range(wl.T))
+    ref = token_outputs(bf(t["x"]).reshape(wl.T, wl.d), idx, w, np.ones_like(idx, dtype=bool), W, tokens)
+    assert relL2(f(y).reshape(wl.T, wl.d), ref) <= 1e-2
+
+
 def test_cfg2_full_size(dev, cfg_cache):
     wl, t, layer = setup(cfg_cache, 2, dev)
     x = t["x"].to(dev)

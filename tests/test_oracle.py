@@ -76,6 +76,89 @@ def test_topk_matches_torch_on_tie_free():
     assert np.all(w[:, 0] >= w[:, 1])
 
 
+# ------------------------------------------------------------------ balanced top-k
+@pytest.mark.parametrize("T,E,k,skew", [(500, 16, 2, 0.0), (300, 8, 3, 2.0), (64, 4, 4, 3.0), (37, 5, 2, 1.0)])
+def test_balanced_matches_torch_port(T, E, k, skew):
+    """Logit-ranked restatement vs the reference's probability-masked op sequence
+    (tie-free data): same experts, same weights."""
+    r = rng(50 + T)
+    lg = r.standard_normal((T, E)) + skew * np.linspace(1, 0, E)[None, :]  # skew: early experts popular
+    idx, w = O.balanced_topk(lg, k)
+    wt, it = P.balanced_topk_tc(torch.softmax(torch.from_numpy(lg), -1), k)
+    assert np.array_equal(idx, it.numpy())
+    np.testing.assert_allclose(w, wt.numpy(), rtol=1e-12)
+    assert np.all(np.sort(idx, axis=1)[:, 1:] != np.sort(idx, axis=1)[:, :-1])  # distinct per token
+
+
+def test_balanced_capacity_closed_form():
+    """All tokens rank the experts 0 > 1 > 2 > 3.  Round 0: everyone takes expert
+    0 (capacity is only checked between rounds), so its count (T) exceeds
+    cap = T*k/E and it is masked afterwards; round 1: everyone takes expert 1;
+    round 2 (k=3): experts 0 and 1 are full (T > cap = 3T/4), so everyone takes 2."""
+    T, E = 40, 4
+    lg = np.tile(np.array([3.0, 2.0, 1.0, 0.0]), (T, 1))
+    idx, w = O.balanced_topk(lg, 3)
+    assert np.all(idx == np.array([0, 1, 2]))
+    p = np.exp(lg[0] - 3.0) / np.exp(lg[0] - 3.0).sum()
+    np.testing.assert_allclose(w[0], p[:3] / (p[:3].sum() + 1e-9), rtol=1e-12)
+    # capacity bites: 30 of the 40 tokens prefer expert 3 first; cap = T*2/4 = 20
+    lg2 = lg.copy()
+    lg2[:30, 3] = 5.0  # 30 tokens take expert 3 in round 0 -> 3 is full for round 1
+    idx2, _ = O.balanced_topk(lg2, 2)
+    assert np.all(idx2[:30, 0] == 3) and np.all(idx2[30:, 0] == 0)
+    assert np.all(idx2[:30, 1] == 0) and np.all(idx2[30:, 1] == 1)  # expert 0 (10 picks) is not full
+
+
+def test_balanced_fallback_when_all_full():
+    """A token whose remaining experts are all full takes its best expert not
+    picked yet, ignoring capacity (moe.py:402-407)."""
+    # T=8, E=4, k=3, cap=6.  Tokens 2-7 rank 0 > 1 > 2 > 3, tokens 0-1 rank 2 > 3 > 0 > 1.
+    # Round 0: six take expert 0 (full), two take 2.  Round 1: six take 1 (0 is full:
+    # full too), two take 3.  Round 2: tokens 0-1 have only 0 and 1 left, both full:
+    # they fall back to the better of the two (0); the others take 2.
+    lg = np.tile(np.array([3.0, 2.0, 1.0, 0.0]), (8, 1))
+    lg[:2] = [1.0, 0.0, 3.0, 2.0]
+    idx, w = O.balanced_topk(lg, 3)
+    assert np.all(idx[:2] == np.array([2, 3, 0])) and np.all(idx[2:] == np.array([0, 1, 2]))
+    wt, it = P.balanced_topk_tc(torch.softmax(torch.from_numpy(lg), -1), 3)
+    assert np.array_equal(idx, it.numpy())
+    np.testing.assert_allclose(w, wt.numpy(), rtol=1e-12)
+    lg3 = np.tile(np.array([2.0, 1.0, 0.0]), (12, 1))  # E=3, k=3, cap=12: round 2 has expert 2 free
+    idx3, w3 = O.balanced_topk(lg3, 3)
+    assert np.all(idx3 == np.array([0, 1, 2]))
+    lg4 = np.tile(np.array([2.0, 1.0, 0.0]), (12, 1))
+    lg4[:, 2] = [3.0] * 12  # everyone takes 2 first (count 12 = cap: full), then 0 (full), then 1 (fallback-free)
+    idx4, _ = O.balanced_topk(lg4, 3)
+    assert np.all(idx4 == np.array([2, 0, 1]))
+    wt, it = P.balanced_topk_tc(torch.softmax(torch.from_numpy(lg4), -1), 3)
+    assert np.array_equal(idx4, it.numpy())
+
+
+def test_balanced_bruteforce_with_ties():
+    """Integer logits (many ties): a per-token, per-round loop with the
+    lowest-index rule."""
+    r = rng(9)
+    T, E, k = 120, 6, 3
+    lg = r.integers(0, 3, size=(T, E)).astype(np.float64)
+    idx, _ = O.balanced_topk(lg, k)
+    cap = max(T * k // E, 1)
+    counts = [0] * E
+    chosen = [[] for _ in range(T)]
+    for rr in range(k):
+        full = [counts[e] >= cap for e in range(E)]
+        picks = []
+        for t in range(T):
+            cand = [e for e in range(E) if e not in chosen[t] and not full[e]]
+            if not cand:
+                cand = [e for e in range(E) if e not in chosen[t]]
+            best = min(cand, key=lambda e: (-lg[t, e], e))
+            picks.append(best)
+        for t, b in enumerate(picks):
+            chosen[t].append(b)
+            counts[b] += 1
+    assert np.array_equal(idx, np.array(chosen))
+
+
 # ------------------------------------------------------------------ aux
 def test_aux_closed_forms():
     E, T, k = 8, 64, 2
