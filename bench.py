@@ -112,6 +112,22 @@ def run_gpu(args, wl):
             step()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
+        # the materialising dispatch (tables + the row copy; what the fp8 path and
+        # the C-ABI's xperm output use), outside the timed region, on this routing
+        rows_us = None
+        if not wl.fp8 and wl.routing != "expert_choice" and not wl.mod:
+            r0 = moe.router.route(x.reshape(wl.T, wl.d))
+            cap = ops.capacity_of(moe.capacity_factor, wl.T, wl.k, wl.E) if moe.drop_overflow else 0
+            for _ in range(3):
+                ops.dispatch(x.reshape(wl.T, wl.d), r0.idx, r0.w, wl.E, capacity=cap)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                ops.dispatch(x.reshape(wl.T, wl.d), r0.idx, r0.w, wl.E, capacity=cap)
+            e1.record()
+            torch.cuda.synchronize()
+            rows_us = e0.elapsed_time(e1) / 10 * 1e3
         # per-stage breakdown in a separate pass: an event pair around every stage
         # (their host-side cost would distort the timed region of small configs)
         events = []
@@ -140,7 +156,7 @@ def run_gpu(args, wl):
         stage_out[name] = rec
     elapsed = t1 - t0
     return dict(elapsed=elapsed, stages=stage_out, a_kept=a_kept, a_all=a_all, t_in=t_in,
-                gemm_us=statistics.mean(gu_timed) if gu_timed else float("nan"), work=work)
+                gemm_us=statistics.mean(gu_timed) if gu_timed else float("nan"), work=work, rows_us=rows_us)
 
 
 def run_cpu_baseline(wl, tokens):
@@ -232,6 +248,14 @@ def main():
         out["gemm_frac_peak"] = round(tot / (gemm_us * 1e-6) / peak, 4)
     if "dispatch" in res["stages"]:
         out["dispatch_GBps"] = res["stages"]["dispatch"].get("GBps")
+    if res.get("rows_us"):
+        # SURVEY definition of the dispatch bytes: read x once, write the kept
+        # permuted rows, 8 B of metadata per assignment
+        b = wl.T * wl.d * 2 + res["a_kept"] * wl.d * 2 + 8.0 * res["a_all"]
+        out["dispatch_rows"] = {"us": round(res["rows_us"], 2), "GBps": round(b / (res["rows_us"] * 1e-6) / 1e9, 1),
+                                "frac_hbm": round(b / (res["rows_us"] * 1e-6) / PEAK_HBM, 4),
+                                "note": "materialising dispatch (tables + row copy), timed separately; the bf16 "
+                                        "layer gathers rows inside the gate/up GEMM instead"}
     if "combine" in res["stages"]:
         out["combine_GBps"] = res["stages"]["combine"].get("GBps")
     if not args.no_cpu:

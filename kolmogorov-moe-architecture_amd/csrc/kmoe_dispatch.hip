@@ -197,29 +197,30 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
   }
 
   // ---- row gather (bf16 copy): every 16-byte chunk of the block's token rows is
-  // read once and written to the token's k permuted rows; 4 chunks in flight per
-  // thread.  Without xperm only the tables are written.
+  // read once and written to the token's k permuted rows; CP_UNR chunks in flight
+  // per thread (64 KiB per block).  Without xperm only the tables are written.
   if (xperm == nullptr) return;
-  const int64_t ntok = min<int64_t>(DTB, T - t0);
+  constexpr int CP_UNR = 16;
+  const int ntok = (int)min<int64_t>(DTB, T - t0);
   const int nvec = d / 8;  // 16-byte vectors per row
-  const int64_t total = ntok * nvec;
-  for (int64_t c0 = tid; c0 < total; c0 += 4 * DTHREADS) {
-    i32x4_t val[4];
+  const int total = ntok * nvec;
+  for (int c0 = tid; c0 < total; c0 += CP_UNR * DTHREADS) {
+    i32x4_t val[CP_UNR];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t c = c0 + (int64_t)u * DTHREADS;
+    for (int u = 0; u < CP_UNR; ++u) {
+      const int c = c0 + u * DTHREADS;
       if (c < total) {
-        const int64_t tl = c / nvec, v = c - tl * nvec;
+        const int tl = c / nvec, v = c - tl * nvec;
         const int64_t t = t0 + tl;
         const int64_t xr = row_index ? (int64_t)row_index[t] : t;
         val[u] = reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d)[v];
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t c = c0 + (int64_t)u * DTHREADS;
+    for (int u = 0; u < CP_UNR; ++u) {
+      const int c = c0 + u * DTHREADS;
       if (c < total) {
-        const int64_t tl = c / nvec, v = c - tl * nvec;
+        const int tl = c / nvec, v = c - tl * nvec;
         for (int j = 0; j < k; ++j) {
           const int row = dest[tl * k + j];
           if (row >= 0) reinterpret_cast<i32x4_t*>(xperm + (int64_t)row * d)[v] = val[u];
