@@ -199,18 +199,26 @@ __device__ __forceinline__ void static_for(Fn&& f) {
   }
 }
 
-// Scheduling groups for an NM-MFMA substep: LDS operations front-loaded, one after
-// each of the first NDS MFMAs (spread evenly when NDS > NM), memory operations
-// spread evenly over all NM.
-template <int NM, int NDS, int NVM, int G = 0>
+// Scheduling groups for an NM-MFMA substep: the NRD fragment reads two after each
+// of the first MFMAs (they feed the next substep), then the NWR LDS block writes and
+// NVM memory loads spread evenly over the MFMAs from W0 = min(4, NM/2) on, so the
+// writes do not queue in the LDS FIFO in front of the reads.  In-order issue means a
+// DS instruction stalled on a full FIFO also holds back the MFMAs behind it: with
+// reads and writes all front-loaded the K-loop took 8.6% (gate/up) and 5% (down)
+// more cycles per step.
+template <int NM, int NRD, int NWR, int NVM, int G = 0>
 __device__ __forceinline__ void sched_spread() {
   if constexpr (G < NM) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    constexpr int dd = NDS <= NM ? (G < NDS ? 1 : 0) : (NDS * (G + 1) + NM - 1) / NM - (NDS * G + NM - 1) / NM;
-    constexpr int v = (NVM * (G + 1)) / NM - (NVM * G) / NM;
-    if constexpr (dd > 0) __builtin_amdgcn_sched_group_barrier(0x080, dd, 0);  // DS
-    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x010, v, 0);   // VMEM
-    sched_spread<NM, NDS, NVM, G + 1>();
+    constexpr int W0 = NM / 2 < 4 ? NM / 2 : 4;
+    constexpr int span = NM - W0, gw = G - W0;
+    constexpr int r = 2 * G < NRD ? (NRD - 2 * G < 2 ? NRD - 2 * G : 2) : 0;
+    constexpr int w = G < W0 ? 0 : (NWR * (gw + 1)) / span - (NWR * gw) / span;
+    constexpr int v = G < W0 ? 0 : (NVM * (gw + 1)) / span - (NVM * gw) / span;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);  // DS read
+    if constexpr (w > 0) __builtin_amdgcn_sched_group_barrier(0x200, w, 0);  // DS write
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x020, v, 0);  // VMEM read
+    sched_spread<NM, NRD, NWR, NVM, G + 1>();
   }
 }
 
@@ -392,7 +400,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
         static_for<q0, q1>([&](auto qc) { load_block(decltype(qc)::value, kt + 2); });
       }
       mma(fa[bi], fb[bi]);
-      sched_spread<NM, (RDN ? RD : 0) + nq, nq>();
+      sched_spread<NM, (RDN ? RD : 0), nq, nq>();
       __builtin_amdgcn_sched_barrier(0);
     });
   };
