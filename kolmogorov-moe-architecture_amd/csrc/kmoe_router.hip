@@ -69,11 +69,6 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   const int wm = wave & 1, wn = wave >> 1;
   const int64_t tok0 = (int64_t)blockIdx.x * RT_TOK;
 
-  for (int i = tid; i < NE * RT_HID; i += RT_THREADS) {
-    const int e = i / RT_HID, j = i % RT_HID;
-    wo[e * WOS + j] = e < E ? bf16_to_f32(w_out[i]) : 0.0f;
-  }
-
   // ---- per-lane sources of the direct-to-LDS loads (block q fills tile rows
   // [RPB q, RPB q + RPB), lane l lands at byte 16*l of the block: row RPB q + l/CPR,
   // physical chunk l%CPR, holding the logical chunk that swz() maps there)
@@ -126,6 +121,13 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
     for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
   const int nk = d * 2 / RKB;
   for (int s = 0; s < RT_STAGES - 1 && s < nk; ++s) issue(s);
+  // w_out (needed only by layer 2) is staged while the first K-steps are in flight:
+  // loading it before them put its global round trip in front of every x load
+  // (2.9 -> 0.6 us before the first K-step)
+  for (int i = tid; i < NE * RT_HID; i += RT_THREADS) {
+    const int e = i / RT_HID, j = i % RT_HID;
+    wo[e * WOS + j] = e < E ? bf16_to_f32(w_out[i]) : 0.0f;
+  }
   constexpr int NSUB = RKB / 32;  // MFMA K-substeps per K-step
   for (int kt = 0; kt < nk; ++kt) {
     if (kt + RT_STAGES - 2 < nk)

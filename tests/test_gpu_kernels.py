@@ -307,6 +307,32 @@ def test_combine_parity(dev):
     np.testing.assert_allclose(npf(yf), ref, rtol=1e-5, atol=1e-6)
 
 
+def test_combine_top2_path_matches_generic(dev):
+    """fan 2, d 2048, bf16 out runs a two-source kernel; it must equal the generic
+    kernel bit for bit (the generic one is reached with a third, always-dropped source),
+    and the oracle to the combine bar.  Dropped sources, out_map and scale included."""
+    T, d, R = 3000, 2048, 6000
+    g = torch.Generator().manual_seed(32)
+    yperm = bf16(torch.randn(R, d, generator=g))
+    src = torch.randint(-1, R, (T, 2), generator=g).to(torch.int32)
+    w = torch.rand(T, 2, generator=g)
+    out_map = torch.randint(-1, T, (T + 50,), generator=g).to(torch.int32)
+    scale = torch.rand(T, generator=g)
+    src3 = torch.cat([src, torch.full((T, 1), -1, dtype=torch.int32)], 1)
+    w3 = torch.cat([w, torch.rand(T, 1, generator=g)], 1)
+    for om, sc in ((None, None), (out_map, scale)):
+        a = ops.combine(yperm.to(dev), src.to(dev), w.to(dev), T if om is None else T + 50,
+                        out_map=None if om is None else om.to(dev), scale=None if sc is None else sc.to(dev))
+        b = ops.combine(yperm.to(dev), src3.to(dev), w3.to(dev), T if om is None else T + 50,
+                        out_map=None if om is None else om.to(dev), scale=None if sc is None else sc.to(dev))
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+        ref = O.combine(npf(yperm), src.numpy(), w.numpy(), out_map=None if om is None else om.numpy(),
+                        scale=None if sc is None else sc.numpy(), T_out=T if om is None else T + 50)
+        mag = O.combine(np.abs(npf(yperm)), src.numpy(), w.numpy(), out_map=None if om is None else om.numpy(),
+                        scale=None if sc is None else sc.numpy(), T_out=T if om is None else T + 50)
+        assert np.all(np.abs(npf(a) - ref) <= np.abs(ref) * 2.0 ** -8 + mag * 2.0 ** -22)
+
+
 def test_combine_is_deterministic(dev):
     T, fan, d, R = 4096, 16, 512, 20000
     g = torch.Generator().manual_seed(31)
