@@ -207,6 +207,99 @@ int kmoe_mod_select(const void* x, int B, int64_t S, int d, const void* w_mod, i
                     int64_t* sel_idx, float* sel_w, int32_t* token_rows, int32_t* out_map, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* ======================================================================== */
+/* Backward pass of the token-choice MoE layer (bf16).  Replaces the autograd
+ * backward of Router.forward, GroupedExperts.forward and the aux losses
+ * (moe.py:423-462, 213-294, 840-939; SwiGLU ffn.py:17-64) and the gradient the
+ * reference's native path never produced (grouped_swiglu_with_grad,
+ * moe_arch/kernels/__init__.py:167-244).  The forward saves what these need:
+ * kmoe_router_train (pre-activation of the router's hidden layer) and
+ * kmoe_gemm_gate_up_rows_gu (pre-activation gate and up values).            */
+
+/* kmoe_router with the pre-activation hidden layer a = x[row(t)] . w_in^T saved
+ * to hidden_pre (T, 128) f32 (nullable: then identical to kmoe_router).     */
+int kmoe_router_train(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,
+                      const void* w_out, int E, const float* logit_bias, int k, float* logits,
+                      int64_t* topk_idx, float* topk_w, float* partials, float* hidden_pre, void* stream);
+
+/* kmoe_gemm_gate_up_rows that also writes g and u (bf16) to gu (max_rows,
+ * 2*F_pad) in the packed column order: per 128-column block of f, the 128 gate
+ * values then the 128 up values.                                            */
+int kmoe_gemm_gate_up_rows_gu(const void* x, const int32_t* row_index, int64_t n_x_rows,
+                              const int32_t* row_token, const int32_t* offsets, int E, int d, int F,
+                              int64_t max_rows, const void* w13_packed, void* h, void* gu, void* stream);
+
+/* Combine backward (moe.py:285-292 reversed): for every kept slot r = slot_row[t,j]
+ *   dyperm[r] = slot_w[t,j] * dy[t]            (bf16)
+ *   dw[t,j]   = dy[t] . yperm[r]               (f32, fixed order; 0 if dropped)
+ * yperm: the forward's expert output rows (max_rows, d) bf16.              */
+int kmoe_combine_bwd(const void* dy, const void* yperm, const int32_t* slot_row, const float* slot_w, int k,
+                     int d, int64_t T, void* dyperm, float* dw, void* stream);
+
+/* Backward packed weight layouts (derived caches, like kmoe_pack_weights):
+ *   w3n : (E, round_up(F,256), d)       rows of w3 (E,F,d), K = d contiguous
+ *   w13t: (E, round_up(d,256), 2*F_pad) rows i of w1/w2 (E,d,F), gate and up
+ *         columns interleaved per 128 like the gu order.  WPAD bytes after rows. */
+size_t kmoe_packed_w3n_bytes(int E, int d, int F);
+size_t kmoe_packed_w13t_bytes(int E, int d, int F);
+int kmoe_pack_weights_bwd(const void* w1, const void* w2, const void* w3, int w_dtype, int E, int d, int F,
+                          void* w3n_packed, void* w13t_packed, void* stream);
+
+/* Grouped GEMM over the routed rows: c[r, n] = a[r, :] . b_e[n, :] for the rows r of
+ * expert e ([offsets[e], offsets[e+1])), K-contiguous a (rows, K) bf16 and packed
+ * b (E, b_expert_rows, K + 64) bf16; columns n < n_valid stored, row stride ldc.
+ * dh = dyperm . w3^T: b = w3n, K = d, N = F;  dx = dgu . w13t^T: b = w13t,
+ * K = 2*F_pad, N = d.                                                        */
+int kmoe_gemm_grouped(const void* a, const int32_t* offsets, int E, int K, int64_t max_rows, const void* b_packed,
+                      int64_t b_expert_rows, int N, void* c, int64_t ldc, int n_valid, void* stream);
+
+/* SwiGLU backward on the packed order: s = sigmoid(g),
+ *   dg = dh * u * s * (1 + g (1 - s)),  du = dh * g * s
+ * dh (rows, F_pad), gu / dgu (rows, 2*F_pad) bf16; rows < *n_rows_dev if given. */
+int kmoe_swiglu_bwd(const void* dh, const void* gu, int64_t rows, const int32_t* n_rows_dev, int F, void* dgu,
+                    void* stream);
+
+/* Segmented transpose into the weight-gradient operand layout: expert e's rows
+ * become columns [koff_e, koff_e + n_e) of dst (dst_rows, k_total), koff_e =
+ * sum_{e'<e} round_up(n_e', 64), zero padded.  Row r reads src row
+ * row_index[row_token[r]] / row_token[r] / r.  k_total: kmoe_wgrad_k_total.   */
+int64_t kmoe_wgrad_k_total(int64_t n_rows, int E);
+int kmoe_seg_transpose(const void* src, int64_t ld_src, const int32_t* row_token, const int32_t* row_index,
+                       const int32_t* offsets, int E, int cols, int dst_rows, void* dst, int64_t k_total,
+                       void* stream);
+
+/* Weight gradients: c_e[m, n] = sum over expert e's rows r of at[m, r] * bt[n, r]
+ * (at (M, k_total), bt (N, k_total) from kmoe_seg_transpose; N a multiple of 256).
+ * c: (E, M, ldc) bf16, columns < n_valid.  With c2 (dW1/dW2 split of the packed
+ * order): columns of 256-column tile nt go to c (first 128) and c2 (last 128) at
+ * column nt*128.  dW3 = h^T dyperm: at = h^T, bt = dyperm^T;  dW1, dW2 = x^T [dg|du]:
+ * at = x^T (gathered), bt = dgu^T, c = dW1, c2 = dW2.                          */
+int kmoe_gemm_wgrad(const void* at, const void* bt, int64_t k_total, const int32_t* offsets, int E, int M, int N,
+                    void* c, void* c2, int64_t ldc, int n_valid, void* stream);
+
+/* Router logit gradient (f32, (T,E)): the top-k renormalisation's softmax-over-
+ * the-selected backward, dl[i_j] += w_j (dw_j - sum_l w_l dw_l), plus the aux
+ * losses scaled by *grad_aux (nullable = 0):
+ *   dl += g (w_lb E/T p (f - p.f) + w_z 2/T lse p),  f_e = counts[e] / (T k).   */
+int kmoe_router_dlogits(const float* logits, int64_t T, int E, const int64_t* topk_idx, const float* topk_w,
+                        const float* dw, int k, const int32_t* counts, const float* grad_aux, float w_lb, float w_z,
+                        float* dlogits, void* stream);
+
+/* Router MLP backward: da = (dl . w_out) * silu'(a) -> (T, 128) bf16 and
+ * dw_out = dl^T silu(a) -> (E, 128) (bf16 or f32), reduced in a fixed order.
+ * hidden_pre: a from kmoe_router_train.  workspace: kmoe_router_bwd_workspace_bytes.
+ * dw_in = da^T x and dx += da . w_in follow with kmoe_gemm_wgrad / kmoe_gemm_grouped
+ * (w_in^T packed by kmoe_pack_w_in_t).                                       */
+size_t kmoe_router_bwd_workspace_bytes(int64_t T, int E);
+int kmoe_router_mlp_bwd(const float* dlogits, const float* hidden_pre, int64_t T, int E, const void* w_out,
+                        void* da, void* dw_out, int dw_dtype, void* workspace, size_t workspace_bytes,
+                        void* stream);
+size_t kmoe_packed_w_in_t_bytes(int d);
+int kmoe_pack_w_in_t(const void* w_in, int w_dtype, int d, void* out, void* stream);
+
+/* y = a + b, n bf16 elements (n % 8 == 0), fp32 add, one rounding. */
+int kmoe_add_bf16(const void* a, const void* b, int64_t n, void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

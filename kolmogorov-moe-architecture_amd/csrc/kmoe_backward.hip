@@ -1,0 +1,473 @@
+// Backward pass of the token-choice MoE layer: the memory-bound kernels around the
+// grouped GEMMs (which run in kmoe_gemm.hip).  Gradients of the reference forward
+//   logits = SiLU(x w_in^T) w_out^T,  p = softmax(logits),  (v, i) = topk(p, k),
+//   w = v / sum(v)                                             (moe.py:423-462)
+//   y[t] = sum_j w[t,j] * FFN_{i[t,j]}(x[t]),  FFN(x) = (silu(x w1) * (x w2)) w3
+//                                                              (moe.py:213-294, ffn.py:17-64)
+//   aux = w_lb * E * sum_e f_e P_e + w_z * mean_t lse_t^2      (moe.py:840-939)
+// with f_e = counts[e] / (T k) a constant (one-hot of the selections) and
+// P_e = mean_t p[t,e].
+#include "kmoe_common.h"
+
+namespace {
+
+// dyperm[r] = w[t,j] * dy[t] (bf16) for the kept slot r = slot_row[t,j];
+// dw[t,j] = dy[t] . yperm[r] (fp32, lane-ordered fma then a fixed shuffle tree: the
+// result is bit-reproducible; 0 for a dropped slot).  One wave per token.
+__global__ __launch_bounds__(256) void combine_bwd_kernel(const uint16_t* __restrict__ dy,
+                                                          const uint16_t* __restrict__ yperm,
+                                                          const int32_t* __restrict__ slot_row,
+                                                          const float* __restrict__ slot_w, int k, int d, int64_t T,
+                                                          uint16_t* __restrict__ dyperm, float* __restrict__ dw) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int nvec = d / 8;
+  const i32x4_t* dyr = reinterpret_cast<const i32x4_t*>(dy + t * d);
+  for (int j = 0; j < k; ++j) {
+    const int r = slot_row[t * k + j];
+    const float w = slot_w[t * k + j];
+    if (r < 0) {
+      if (lane == 0) dw[t * k + j] = 0.0f;
+      continue;
+    }
+    const i32x4_t* yr = reinterpret_cast<const i32x4_t*>(yperm + (int64_t)r * d);
+    i32x4_t* out = reinterpret_cast<i32x4_t*>(dyperm + (int64_t)r * d);
+    float dot = 0.0f;
+    for (int v = lane; v < nvec; v += 64) {
+      const i32x4_t a = dyr[v], b = yr[v];
+      i32x4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a0 = __uint_as_float(((uint32_t)a[q]) << 16), a1 = __uint_as_float(((uint32_t)a[q]) & 0xffff0000u);
+        const float b0 = __uint_as_float(((uint32_t)b[q]) << 16), b1 = __uint_as_float(((uint32_t)b[q]) & 0xffff0000u);
+        dot = fmaf(a0, b0, dot);
+        dot = fmaf(a1, b1, dot);
+        o[q] = (int)((uint32_t)f32_to_bf16(w * a0) | ((uint32_t)f32_to_bf16(w * a1) << 16));
+      }
+      out[v] = o;
+    }
+    dot = wave_sum(dot);
+    if (lane == 0) dw[t * k + j] = dot;
+  }
+}
+
+// SwiGLU backward on the packed column order (per 128-column block: 128 gate then 128
+// up columns): for h = silu(g) * u,
+//   dg = dh * u * s * (1 + g (1 - s)),  du = dh * silu(g),  s = sigmoid(g).
+// dh (rows, Fp), gu / dgu (rows, 2 Fp); rows < n_rows_dev[0] when given.
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t* __restrict__ dh,
+                                                         const uint16_t* __restrict__ gu, int64_t rows,
+                                                         const int32_t* __restrict__ n_rows_dev, int Fp,
+                                                         uint16_t* __restrict__ dgu) {
+  int64_t nr = rows;
+  if (n_rows_dev) nr = min<int64_t>(nr, (int64_t)*n_rows_dev);
+  const int cpr = Fp / 8;  // 8-column chunks of a dh row
+  const int64_t total = nr * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / cpr;
+    const int f = (int)(i - r * cpr) * 8;
+    const int gc = (f >> 7) * 256 + (f & 127);  // gate column of f in the packed order
+    const i32x4_t hv = *reinterpret_cast<const i32x4_t*>(dh + r * Fp + f);
+    const i32x4_t gv = *reinterpret_cast<const i32x4_t*>(gu + r * 2 * Fp + gc);
+    const i32x4_t uv = *reinterpret_cast<const i32x4_t*>(gu + r * 2 * Fp + gc + 128);
+    i32x4_t dgo, duo;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t og = 0, ou = 0;
+#pragma unroll
+      for (int hlf = 0; hlf < 2; ++hlf) {
+        const int sh = hlf * 16;
+        const float hh = bf16_to_f32((uint16_t)((uint32_t)hv[q] >> sh));
+        const float g = bf16_to_f32((uint16_t)((uint32_t)gv[q] >> sh));
+        const float u = bf16_to_f32((uint16_t)((uint32_t)uv[q] >> sh));
+        const float s = 1.0f / (1.0f + __expf(-g));
+        const float dg = hh * u * s * (1.0f + g * (1.0f - s));
+        const float du = hh * g * s;
+        og |= (uint32_t)f32_to_bf16(dg) << sh;
+        ou |= (uint32_t)f32_to_bf16(du) << sh;
+      }
+      dgo[q] = (int)og;
+      duo[q] = (int)ou;
+    }
+    *reinterpret_cast<i32x4_t*>(dgu + r * 2 * Fp + gc) = dgo;
+    *reinterpret_cast<i32x4_t*>(dgu + r * 2 * Fp + gc + 128) = duo;
+  }
+}
+
+// Segmented transpose for the weight gradients: expert e's rows [off_e, off_e + n_e)
+// of src (rows, cols; row r read from src row rt[r], rt = row_index[row_token[r]],
+// row_token[r] or r) become columns [koff_e, koff_e + n_e) of dst (dst_rows, k_total),
+// koff_e = sum_{e' < e} round_up(n_e', 64); columns [n_e, round_up(n_e, 64)) of the
+// segment, columns past the last segment and rows [cols, dst_rows) are zero.
+// One 64 x 64 tile per workgroup, through LDS.
+constexpr int TT = 64;
+__global__ __launch_bounds__(256) void seg_transpose_kernel(const uint16_t* __restrict__ src, int64_t ld_src,
+                                                            const int32_t* __restrict__ row_token,
+                                                            const int32_t* __restrict__ row_index,
+                                                            const int32_t* __restrict__ offsets, int E, int cols,
+                                                            uint16_t* __restrict__ dst, int64_t k_total) {
+  __shared__ uint16_t tile[TT][TT + 2];
+  __shared__ int seg[3];  // first source row of the tile, rows valid in the tile
+  const int tid = threadIdx.x;
+  const int64_t kk0 = (int64_t)blockIdx.x * TT;
+  const int c0 = blockIdx.y * TT;
+  if (tid < 64) {
+    const int lane = tid;
+    int lo = 0, n = 0;
+    if (lane < E) {
+      lo = offsets[lane];
+      n = offsets[lane + 1] - lo;
+    }
+    const int pad = (n + TT - 1) / TT * TT;
+    int incl = pad;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += u;
+    }
+    const int koff = incl - pad;
+    const bool mine = lane < E && kk0 >= koff && kk0 < koff + pad;
+    const uint64_t m = __ballot(mine);
+    if (lane == 0) {
+      seg[0] = 0;
+      seg[1] = 0;
+    }
+    if (m) {
+      const int e = __builtin_ctzll(m);
+      if (lane == e) {
+        seg[0] = lo + (int)(kk0 - koff);
+        seg[1] = min(TT, n - (int)(kk0 - koff));
+      }
+    }
+  }
+  __syncthreads();
+  const int r0 = seg[0], nvalid = seg[1];
+  // load: 64 source rows x 64 columns = 512 chunks of 8 columns
+  for (int c = tid; c < TT * (TT / 8); c += 256) {
+    const int i = c / (TT / 8), q = c % (TT / 8);
+    i32x4_t v = {0, 0, 0, 0};
+    const int col = c0 + q * 8;
+    if (i < nvalid && col < cols) {
+      int64_t r = r0 + i;
+      if (row_token) r = row_token[r];
+      if (row_index) r = row_index[r];
+      if (col + 8 <= cols) {
+        v = *reinterpret_cast<const i32x4_t*>(src + r * ld_src + col);
+      } else {
+        uint16_t tmp[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) tmp[u] = col + u < cols ? src[r * ld_src + col + u] : (uint16_t)0;
+        v = *reinterpret_cast<const i32x4_t*>(tmp);
+      }
+    }
+    const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
+    uint16_t* tr = &tile[i][q * 8];
+    tr[0] = (uint16_t)w0;
+    tr[1] = (uint16_t)(w0 >> 16);
+    tr[2] = (uint16_t)w1;
+    tr[3] = (uint16_t)(w1 >> 16);
+    tr[4] = (uint16_t)w2;
+    tr[5] = (uint16_t)(w2 >> 16);
+    tr[6] = (uint16_t)w3;
+    tr[7] = (uint16_t)(w3 >> 16);
+  }
+  __syncthreads();
+  // store: 64 destination rows (source columns) x 64 k positions
+  for (int c = tid; c < TT * (TT / 8); c += 256) {
+    const int rr = c / (TT / 8), q = c % (TT / 8);
+    uint32_t w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      w[u] = (uint32_t)tile[q * 8 + 2 * u][rr] | ((uint32_t)tile[q * 8 + 2 * u + 1][rr] << 16);
+    *reinterpret_cast<i32x4_t*>(dst + (int64_t)(c0 + rr) * k_total + kk0 + q * 8) =
+        i32x4_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+  }
+}
+
+// Router logit gradient, one thread per token (E <= 64):
+//   top-k renormalisation (w_j = p_j / sum_sel p = softmax over the selected logits):
+//     dl[i_j] += w_j (dw_j - sum_l w_l dw_l)
+//   aux (scaled by the upstream gradient g of the aux loss):
+//     dl += g * (w_lb E / T * p (f - p.f) + w_z 2/T * lse * p),  f_e = counts[e] / (T k)
+template <int NE>
+__global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __restrict__ logits, int64_t T, int E,
+                                                             const int64_t* __restrict__ topk_idx,
+                                                             const float* __restrict__ topk_w,
+                                                             const float* __restrict__ dw, int k,
+                                                             const int32_t* __restrict__ counts,
+                                                             const float* __restrict__ grad_aux, float w_lb,
+                                                             float w_z, float* __restrict__ dl) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  float L[NE], g[NE];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    L[e] = e < E ? logits[t * E + e] : -INFINITY;
+    mx = fmaxf(mx, L[e]);
+    g[e] = 0.0f;
+  }
+  const float ga = grad_aux ? grad_aux[0] : 0.0f;
+  if (ga != 0.0f) {
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      L[e] = e < E ? __expf(L[e] - mx) : 0.0f;
+      s += L[e];
+    }
+    const float inv = 1.0f / s, lse = mx + __logf(s);
+    const float invTk = 1.0f / ((float)T * (float)k);
+    float pf = 0.0f;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      L[e] *= inv;  // p
+      if (counts && e < E) pf += L[e] * ((float)counts[e] * invTk);
+    }
+    const float clb = w_lb * (float)E / (float)T, cz = w_z * 2.0f / (float)T * lse;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      if (e < E) {
+        const float fe = counts ? (float)counts[e] * invTk : 0.0f;
+        g[e] = ga * (clb * L[e] * (fe - pf) + cz * L[e]);
+      }
+    }
+  }
+  float c = 0.0f;
+  for (int j = 0; j < k; ++j) c += topk_w[t * k + j] * dw[t * k + j];
+  for (int j = 0; j < k; ++j) {
+    const int e = (int)topk_idx[t * k + j];
+    const float v = topk_w[t * k + j] * (dw[t * k + j] - c);
+#pragma unroll
+    for (int q = 0; q < NE; ++q)
+      if (q == e) g[q] += v;
+  }
+#pragma unroll
+  for (int e = 0; e < NE; ++e)
+    if (e < E) dl[t * E + e] = g[e];
+}
+
+// Router MLP backward over a block of 64 tokens (256 threads, 4 per token):
+//   s = silu(a), ds = dl w_out, da = ds * silu'(a)      -> da (T, 128) bf16
+//   partial[b][e][j] = sum_{t in block} dl[t,e] s[t,j]  -> reduced by router_reduce_kernel
+// a (T, 128) f32 is the saved pre-activation of the d -> 128 layer.
+constexpr int RB_TOK = 64;
+constexpr int RH = KMOE_ROUTER_HIDDEN;
+template <int NE>
+__global__ __launch_bounds__(256) void router_mlp_bwd_kernel(const float* __restrict__ dl,
+                                                             const float* __restrict__ a, int64_t T, int E,
+                                                             const uint16_t* __restrict__ w_out,
+                                                             uint16_t* __restrict__ da,
+                                                             float* __restrict__ partial) {
+  __shared__ float wo[NE][RH];
+  __shared__ float s_l[RB_TOK][RH + 1];
+  __shared__ float dl_l[RB_TOK][NE];
+  const int tid = threadIdx.x;
+  const int64_t t0 = (int64_t)blockIdx.x * RB_TOK;
+  for (int i = tid; i < NE * RH; i += 256) wo[i / RH][i % RH] = i / RH < E ? bf16_to_f32(w_out[i]) : 0.0f;
+  for (int i = tid; i < RB_TOK * NE; i += 256) {
+    const int tl = i / NE, e = i % NE;
+    dl_l[tl][e] = (t0 + tl < T && e < E) ? dl[(t0 + tl) * E + e] : 0.0f;
+  }
+  __syncthreads();
+  const int tl = tid >> 2, part = tid & 3;
+  const int64_t t = t0 + tl;
+  for (int jj = 0; jj < RH / 4; ++jj) {
+    const int j = part + 4 * jj;
+    const float av = t < T ? a[t * RH + j] : 0.0f;
+    const float sg = 1.0f / (1.0f + __expf(-av));
+    const float s = av * sg;
+    float ds = 0.0f;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) ds = fmaf(dl_l[tl][e], wo[e][j], ds);
+    s_l[tl][j] = t < T ? s : 0.0f;
+    if (t < T) da[t * RH + j] = f32_to_bf16(ds * sg * (1.0f + av * (1.0f - sg)));
+  }
+  __syncthreads();
+  // partial dW_out of the block: thread handles (e, j) pairs tid, tid + 256, ...
+  for (int i = tid; i < NE * RH; i += 256) {
+    const int e = i / RH, j = i % RH;
+    float acc = 0.0f;
+    for (int q = 0; q < RB_TOK; ++q) acc = fmaf(dl_l[q][e], s_l[q][j], acc);
+    if (e < E) partial[(int64_t)blockIdx.x * E * RH + e * RH + j] = acc;
+  }
+}
+
+// out[i] = sum_b partial[b][i] in block order (fixed, bit-reproducible); bf16 or f32 out.
+__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ partial, int64_t nblk,
+                                                              int64_t n, void* __restrict__ out, bool out_f32) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.0f;
+  for (int64_t b = 0; b < nblk; ++b) s += partial[b * n + i];
+  if (out_f32)
+    static_cast<float*>(out)[i] = s;
+  else
+    static_cast<uint16_t*>(out)[i] = f32_to_bf16(s);
+}
+
+// w_in (128, d) -> packed rows of w_in^T: (round_up(d, 256), 128 + 64) bf16, row i =
+// w_in[:, i] (the B operand of dx_router = da . w_in), zero padded.
+__global__ __launch_bounds__(256) void pack_w_in_t_kernel(const void* __restrict__ w_in, bool in_f32, int d,
+                                                          uint16_t* __restrict__ out, int64_t rows, int ld) {
+  const int64_t n = rows * ld;
+  for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < n; o += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = o / ld;
+    const int j = (int)(o - i * ld);
+    uint16_t v = 0;
+    if (i < d && j < RH) {
+      const int64_t src = (int64_t)j * d + i;
+      v = in_f32 ? f32_to_bf16(static_cast<const float*>(w_in)[src]) : static_cast<const uint16_t*>(w_in)[src];
+    }
+    out[o] = v;
+  }
+}
+
+// y = a + b (bf16, fp32 add, one rounding)
+__global__ __launch_bounds__(256) void add_bf16_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+                                                       int64_t n8, uint16_t* __restrict__ y) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
+    const i32x4_t u = reinterpret_cast<const i32x4_t*>(a)[i], v = reinterpret_cast<const i32x4_t*>(b)[i];
+    i32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float lo = __uint_as_float(((uint32_t)u[q]) << 16) + __uint_as_float(((uint32_t)v[q]) << 16);
+      const float hi =
+          __uint_as_float(((uint32_t)u[q]) & 0xffff0000u) + __uint_as_float(((uint32_t)v[q]) & 0xffff0000u);
+      o[q] = (int)((uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16));
+    }
+    reinterpret_cast<i32x4_t*>(y)[i] = o;
+  }
+}
+
+unsigned grid_for(int64_t n, int per_block) {
+  const int64_t b = kmoe::ceil_div<int64_t>(n, per_block);
+  return (unsigned)(b < 65536 ? (b > 0 ? b : 1) : 65536);
+}
+
+}  // namespace
+
+extern "C" int kmoe_combine_bwd(const void* dy, const void* yperm, const int32_t* slot_row, const float* slot_w, int k,
+                                int d, int64_t T, void* dyperm, float* dw, void* stream) {
+  KMOE_REQUIRE(dy && yperm && slot_row && slot_w && dyperm && dw, KMOE_ERR_NULL, "kmoe_combine_bwd: null buffer");
+  KMOE_REQUIRE(k >= 1 && k <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_combine_bwd: k=%d", k);
+  KMOE_REQUIRE(d > 0 && d % 8 == 0, KMOE_ERR_SHAPE, "kmoe_combine_bwd: d=%d must be a multiple of 8", d);
+  KMOE_REQUIRE(T >= 0, KMOE_ERR_SHAPE, "kmoe_combine_bwd: T < 0");
+  if (T == 0) return KMOE_OK;
+  hipLaunchKernelGGL(combine_bwd_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0,
+                     kmoe::as_stream(stream), static_cast<const uint16_t*>(dy), static_cast<const uint16_t*>(yperm),
+                     slot_row, slot_w, k, d, T, static_cast<uint16_t*>(dyperm), dw);
+  return kmoe::check_launch("kmoe_combine_bwd");
+}
+
+extern "C" int kmoe_swiglu_bwd(const void* dh, const void* gu, int64_t rows, const int32_t* n_rows_dev, int F,
+                               void* dgu, void* stream) {
+  KMOE_REQUIRE(dh && gu && dgu, KMOE_ERR_NULL, "kmoe_swiglu_bwd: null buffer");
+  KMOE_REQUIRE(rows >= 0 && F > 0, KMOE_ERR_SHAPE, "kmoe_swiglu_bwd: bad shape");
+  if (rows == 0) return KMOE_OK;
+  const int Fp = (F + 127) / 128 * 128;
+  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(grid_for(rows * (Fp / 8), 256)), dim3(256), 0, kmoe::as_stream(stream),
+                     static_cast<const uint16_t*>(dh), static_cast<const uint16_t*>(gu), rows, n_rows_dev, Fp,
+                     static_cast<uint16_t*>(dgu));
+  return kmoe::check_launch("kmoe_swiglu_bwd");
+}
+
+extern "C" int kmoe_seg_transpose(const void* src, int64_t ld_src, const int32_t* row_token, const int32_t* row_index,
+                                  const int32_t* offsets, int E, int cols, int dst_rows, void* dst, int64_t k_total,
+                                  void* stream) {
+  KMOE_REQUIRE(src && offsets && dst, KMOE_ERR_NULL, "kmoe_seg_transpose: null buffer");
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_seg_transpose: E=%d", E);
+  KMOE_REQUIRE(cols > 0 && dst_rows >= cols && dst_rows % TT == 0, KMOE_ERR_SHAPE,
+               "kmoe_seg_transpose: cols=%d, dst_rows=%d (a multiple of %d >= cols)", cols, dst_rows, TT);
+  KMOE_REQUIRE(k_total > 0 && k_total % TT == 0, KMOE_ERR_SHAPE, "kmoe_seg_transpose: k_total=%lld",
+               (long long)k_total);
+  KMOE_REQUIRE(ld_src >= cols && ld_src % 8 == 0, KMOE_ERR_SHAPE, "kmoe_seg_transpose: ld_src=%lld",
+               (long long)ld_src);
+  KMOE_REQUIRE(!row_index || row_token, KMOE_ERR_NULL, "kmoe_seg_transpose: row_index needs row_token");
+  const dim3 grid((unsigned)(k_total / TT), (unsigned)(dst_rows / TT));
+  hipLaunchKernelGGL(seg_transpose_kernel, grid, dim3(256), 0, kmoe::as_stream(stream),
+                     static_cast<const uint16_t*>(src), ld_src, row_token, row_index, offsets, E, cols,
+                     static_cast<uint16_t*>(dst), k_total);
+  return kmoe::check_launch("kmoe_seg_transpose");
+}
+
+extern "C" int kmoe_router_dlogits(const float* logits, int64_t T, int E, const int64_t* topk_idx, const float* topk_w,
+                                   const float* dw, int k, const int32_t* counts, const float* grad_aux, float w_lb,
+                                   float w_z, float* dlogits, void* stream) {
+  KMOE_REQUIRE(logits && topk_idx && topk_w && dw && dlogits, KMOE_ERR_NULL, "kmoe_router_dlogits: null buffer");
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS && k >= 1 && k <= E, KMOE_ERR_SHAPE, "kmoe_router_dlogits: E=%d k=%d",
+               E, k);
+  if (T == 0) return KMOE_OK;
+  const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(T, 256));
+  hipStream_t s = kmoe::as_stream(stream);
+#define KMOE_DL(NE_) \
+  hipLaunchKernelGGL(router_dlogits_kernel<NE_>, grid, dim3(256), 0, s, logits, T, E, topk_idx, topk_w, dw, k, counts, \
+                     grad_aux, w_lb, w_z, dlogits)
+  if (E <= 8)
+    KMOE_DL(8);
+  else if (E <= 16)
+    KMOE_DL(16);
+  else if (E <= 32)
+    KMOE_DL(32);
+  else
+    KMOE_DL(64);
+#undef KMOE_DL
+  return kmoe::check_launch("kmoe_router_dlogits");
+}
+
+extern "C" size_t kmoe_router_bwd_workspace_bytes(int64_t T, int E) {
+  return (size_t)kmoe::ceil_div<int64_t>(T, RB_TOK) * (size_t)E * RH * sizeof(float);
+}
+
+extern "C" int kmoe_router_mlp_bwd(const float* dlogits, const float* hidden_pre, int64_t T, int E, const void* w_out,
+                                   void* da, void* dw_out, int dw_dtype, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  KMOE_REQUIRE(dlogits && hidden_pre && w_out && da && dw_out && workspace, KMOE_ERR_NULL,
+               "kmoe_router_mlp_bwd: null buffer");
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_router_mlp_bwd: E=%d", E);
+  KMOE_REQUIRE(dw_dtype == KMOE_DTYPE_BF16 || dw_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE,
+               "kmoe_router_mlp_bwd: dw_out dtype");
+  KMOE_REQUIRE(workspace_bytes >= kmoe_router_bwd_workspace_bytes(T, E), KMOE_ERR_WORKSPACE,
+               "kmoe_router_mlp_bwd: workspace %zu < %zu", workspace_bytes, kmoe_router_bwd_workspace_bytes(T, E));
+  if (T == 0) return KMOE_OK;
+  const int64_t nblk = kmoe::ceil_div<int64_t>(T, RB_TOK);
+  hipStream_t s = kmoe::as_stream(stream);
+  float* part = static_cast<float*>(workspace);
+#define KMOE_MB(NE_)                                                                                        \
+  hipLaunchKernelGGL(router_mlp_bwd_kernel<NE_>, dim3((unsigned)nblk), dim3(256), 0, s, dlogits, hidden_pre, T, E, \
+                     static_cast<const uint16_t*>(w_out), static_cast<uint16_t*>(da), part)
+  if (E <= 8)
+    KMOE_MB(8);
+  else if (E <= 16)
+    KMOE_MB(16);
+  else if (E <= 32)
+    KMOE_MB(32);
+  else
+    KMOE_MB(64);
+#undef KMOE_MB
+  const int64_t n = (int64_t)E * RH;
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(n, 256)), dim3(256), 0, s, part,
+                     nblk, n, dw_out, dw_dtype == KMOE_DTYPE_F32);
+  return kmoe::check_launch("kmoe_router_mlp_bwd");
+}
+
+extern "C" size_t kmoe_packed_w_in_t_bytes(int d) { return (size_t)((d + 255) / 256 * 256) * (RH + 64) * 2; }
+
+extern "C" int kmoe_pack_w_in_t(const void* w_in, int w_dtype, int d, void* out, void* stream) {
+  KMOE_REQUIRE(w_in && out, KMOE_ERR_NULL, "kmoe_pack_w_in_t: null buffer");
+  KMOE_REQUIRE(d > 0, KMOE_ERR_SHAPE, "kmoe_pack_w_in_t: d=%d", d);
+  KMOE_REQUIRE(w_dtype == KMOE_DTYPE_BF16 || w_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE, "kmoe_pack_w_in_t: dtype");
+  const int64_t rows = (d + 255) / 256 * 256;
+  hipLaunchKernelGGL(pack_w_in_t_kernel, dim3(grid_for(rows * (RH + 64), 256)), dim3(256), 0, kmoe::as_stream(stream),
+                     w_in, w_dtype == KMOE_DTYPE_F32, d, static_cast<uint16_t*>(out), rows, RH + 64);
+  return kmoe::check_launch("kmoe_pack_w_in_t");
+}
+
+extern "C" int kmoe_add_bf16(const void* a, const void* b, int64_t n, void* y, void* stream) {
+  KMOE_REQUIRE(a && b && y, KMOE_ERR_NULL, "kmoe_add_bf16: null buffer");
+  KMOE_REQUIRE(n >= 0 && n % 8 == 0, KMOE_ERR_SHAPE, "kmoe_add_bf16: n=%lld must be a multiple of 8", (long long)n);
+  if (n == 0) return KMOE_OK;
+  hipLaunchKernelGGL(add_bf16_kernel, dim3(grid_for(n / 8, 256)), dim3(256), 0, kmoe::as_stream(stream),
+                     static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), n / 8, static_cast<uint16_t*>(y));
+  return kmoe::check_launch("kmoe_add_bf16");
+}

@@ -242,6 +242,13 @@ struct GemmArgs {
   uint16_t* C;
   int64_t ldc;
   int n_valid;
+  // plain (non gate/up) tiles: when set, output columns [128, 256) of a full tile go
+  // to C2 and columns [0, 128) to C, both at column nt*128 (the gate and up halves
+  // of a w13-ordered tile: the dw1 / dw2 split of the weight gradient)
+  uint16_t* C2;
+  // gate/up tiles: when set, the pre-activation gate and up values are also written
+  // (bf16) in the packed column order, row stride 2*ldc: the backward's saved g, u
+  uint16_t* gu_out;
 };
 
 // One output tile: rows [m0, min(m0 + 256, m_end)) of expert e against B rows of
@@ -469,13 +476,59 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   __syncthreads();
   constexpr int OCPR = NC * 2 / 16;  // 16-byte chunks per output row
   const int col0 = (GATE_UP ? nt * 128 : nt * 256) + q * NC;
+  const bool split_c = !GATE_UP && g.C2 != nullptr;
   for (int c = tid; c < BM * OCPR; c += GEMM_THREADS) {
     const int trow = c / OCPR, ch = c % OCPR;
     const int grow = m0 + trow;
-    const int gcol = col0 + ch * 8;
+    uint16_t* dst = g.C;
+    int gcol = col0 + ch * 8;
+    if (split_c) {
+      const int cf = q * NC + ch * 8;  // column within the full tile
+      dst = cf < 128 ? g.C : g.C2;
+      gcol = nt * 128 + (cf & 127);
+    }
     if (grow < m_end && gcol < g.n_valid)
-      *reinterpret_cast<i32x4_t*>(g.C + (int64_t)grow * g.ldc + gcol) =
+      *reinterpret_cast<i32x4_t*>(dst + (int64_t)grow * g.ldc + gcol) =
           *reinterpret_cast<const i32x4_t*>(lds + trow * OSTR + ch * 16);
+  }
+
+  // training forward: the pre-activation gate and up values of the tile, bf16, in the
+  // packed column order (row stride 2*ldc), for the SwiGLU backward
+  if constexpr (GATE_UP && !FP8) {
+    if (g.gu_out != nullptr) {
+      constexpr int NC2 = 64 * WNB;
+      constexpr int OSTR2 = NC2 * 2 + 16;
+      __syncthreads();
+      uint8_t* const wb2 = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR2 + (lr - (odd ? 1 : 0)) * 2;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+#pragma unroll
+          for (int j = 0; j < WNB; ++j) {
+            const float a = acc[mi][j][2 * p], b = acc[mi][j][2 * p + 1];
+            const float a_next = __builtin_bit_cast(
+                float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, a), 0x101, 0xf, 0xf, false));
+            const float b_prev = __builtin_bit_cast(
+                float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, b), 0x111, 0xf, 0xf, false));
+            const float lo = odd ? b_prev : a, hi = odd ? b : a_next;
+            const uint32_t packed = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+            const int col = b_lds_row<true, WNB>(wn, j, 0);
+            *reinterpret_cast<uint32_t*>(wb2 + (mi * 32 + 8 * (p >> 1) + 2 * (p & 1)) * OSTR2 + col * 2) = packed;
+          }
+        }
+      }
+      __syncthreads();
+      constexpr int OCPR2 = NC2 * 2 / 16;
+      for (int c = tid; c < BM * OCPR2; c += GEMM_THREADS) {
+        const int trow = c / OCPR2, ch = c % OCPR2;
+        const int grow = m0 + trow;
+        const int gcol = nt * 256 + b_packed_row<true, WNB>(ch * 8, q);
+        if (grow < m_end)
+          *reinterpret_cast<i32x4_t*>(g.gu_out + (int64_t)grow * 2 * g.ldc + gcol) =
+              *reinterpret_cast<const i32x4_t*>(lds + trow * OSTR2 + ch * 16);
+      }
+    }
   }
 }
 
@@ -524,6 +577,65 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
     gemm_tile<GATE_UP, FP8, GATHER, 2>(g, lds, e, m0, m_end, nt, q);
   else if constexpr (!GATE_UP)
     gemm_tile<GATE_UP, FP8, GATHER, 1>(g, lds, e, m0, m_end, nt, q);
+}
+
+// ---------------------------------------------------------------- weight gradients
+// Row segments are transposed and padded per expert: expert e's rows occupy columns
+// [koff_e, koff_e + kpad_e) of the K axis, kpad_e = counts[e] rounded up to the
+// K-step (64), zero filled.  koff_e of expert e from the offsets (lane-parallel).
+constexpr int WG_KALIGN = KB / 2;  // bf16 elements per K-step
+__device__ __forceinline__ void wgrad_segment(const int32_t* __restrict__ offsets, int E, int e, int& koff, int& kpad) {
+  const int lane = threadIdx.x & 63;
+  int c = 0;
+  if (lane < E) c = round_up(offsets[lane + 1] - offsets[lane], WG_KALIGN);
+  int pre = lane < e ? c : 0;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) pre += __shfl_xor(pre, o, 64);
+  koff = __builtin_amdgcn_readfirstlane(pre);
+  kpad = __builtin_amdgcn_readlane(c, e);
+}
+
+// C_e[m, n] = sum over expert e's rows r of At[m, r] * Bt[n, r] for every expert (the
+// weight gradients dW = X_e^T dY_e of the grouped GEMMs, contraction over a ragged
+// number of rows).  Workgroup -> (expert, row tile, column tile); the tile itself is
+// gemm_tile on the expert's K range (At rows are the output rows, Bt rows the output
+// columns, both K-contiguous).  An expert without rows writes a zero tile.
+__global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void wgrad_kernel(
+    GemmArgs g, const int32_t* __restrict__ offsets, int E, int M, int n_mt, int n_nt, int64_t c_expert_stride) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[GEMM_LDS];
+  const int n_all = E * n_mt * n_nt;
+  const int L = blockIdx.x;
+  if (L >= n_all) return;
+  const int t = (n_all % (NXCD * SB_TILES)) == 0 ? xcd_tile(L) : L;
+  const int per_e = n_mt * n_nt;
+  const int e = t / per_e, rem = t - e * per_e;
+  const int mt = rem / n_nt, nt = rem - mt * n_nt;
+  int koff, kpad;
+  wgrad_segment(offsets, E, e, koff, kpad);
+  GemmArgs ge = g;
+  ge.C = g.C + (int64_t)e * c_expert_stride;
+  ge.C2 = g.C2 ? g.C2 + (int64_t)e * c_expert_stride : nullptr;
+  const int m0 = mt * BM;
+  if (kpad == 0) {
+    // no rows: a zero gradient tile
+    for (int c = threadIdx.x; c < BM * 32; c += GEMM_THREADS) {
+      const int trow = c / 32, ch = c % 32;
+      const int grow = m0 + trow;
+      uint16_t* dst = ge.C;
+      int gcol = nt * 256 + ch * 8;
+      if (ge.C2) {
+        dst = ch < 16 ? ge.C : ge.C2;
+        gcol = nt * 128 + (ch & 15) * 8;
+      }
+      if (grow < M && gcol < g.n_valid)
+        *reinterpret_cast<i32x4_t*>(dst + (int64_t)grow * g.ldc + gcol) = i32x4_t{0, 0, 0, 0};
+    }
+    return;
+  }
+  ge.A = g.A + (int64_t)koff * 2;
+  ge.B = g.B + (int64_t)koff * 2;
+  ge.k_bytes = kpad * 2;
+  gemm_tile<false, false, false, 4>(ge, lds, 0, m0, M, nt, 0);
 }
 
 // ---------------------------------------------------------------- weight packing
@@ -635,7 +747,7 @@ int elem_bytes(int dtype) { return dtype == KMOE_DTYPE_FP8_E4M3 ? 1 : 2; }
 int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, const int32_t* row_token,
                 const int32_t* row_index, int64_t n_a_rows, const int32_t* offsets, int E, int K, int64_t max_rows,
                 const void* B, int64_t b_expert_rows, const float* b_scale, void* C, int64_t ldc, int n_valid,
-                int n_tiles, hipStream_t s) {
+                int n_tiles, hipStream_t s, void* C2 = nullptr, void* gu_out = nullptr) {
   const int eb = fp8 ? 1 : 2;
   const int64_t slots = kmoe::ceil_div<int64_t>(max_rows, BM) + E;
   // every tile of the worst-case slot count, plus one narrow tile per resident
@@ -665,6 +777,8 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
   g.C = static_cast<uint16_t*>(C);
   g.ldc = ldc;
   g.n_valid = n_valid;
+  g.C2 = static_cast<uint16_t*>(C2);
+  g.gu_out = static_cast<uint16_t*>(gu_out);
   // tile loads address a 2 GiB buffer window from the tile's first A / B row (from
   // the first row of A when gathering)
   if ((int64_t)(BM + 1) * g.ldb_bytes >= ((int64_t)1 << 31) ||
@@ -849,4 +963,134 @@ extern "C" int kmoe_grouped_swiglu(const void* xperm, const int32_t* offsets, in
                              stream);
   if (rc) return rc;
   return kmoe_gemm_down(h, nullptr, KMOE_DTYPE_BF16, offsets, E, d, F, max_rows, w3_packed, nullptr, y, stream);
+}
+
+// ---------------------------------------------------------------- backward pass
+
+extern "C" int kmoe_gemm_gate_up_rows_gu(const void* x, const int32_t* row_index, int64_t n_x_rows,
+                                         const int32_t* row_token, const int32_t* offsets, int E, int d, int F,
+                                         int64_t max_rows, const void* w13_packed, void* h, void* gu, void* stream) {
+  int rc = check_gemm_args("kmoe_gemm_gate_up_rows_gu", x, offsets, E, d, F, max_rows, w13_packed, h,
+                           KMOE_DTYPE_BF16);
+  if (rc) return rc;
+  KMOE_REQUIRE(row_token && gu, KMOE_ERR_NULL, "kmoe_gemm_gate_up_rows_gu: null row_token / gu");
+  KMOE_REQUIRE(n_x_rows >= 1, KMOE_ERR_SHAPE, "kmoe_gemm_gate_up_rows_gu: n_x_rows=%lld must be >= 1",
+               (long long)n_x_rows);
+  if (max_rows == 0) return KMOE_OK;
+  const int Fp = round_up(F, 128);
+  rc = launch_gemm(true, false, x, nullptr, row_token, row_index, n_x_rows, offsets, E, d, max_rows, w13_packed,
+                   2 * (int64_t)Fp, nullptr, h, Fp, Fp, Fp / 128, kmoe::as_stream(stream), nullptr, gu);
+  if (rc) return rc;
+  return kmoe::check_launch("kmoe_gemm_gate_up_rows_gu");
+}
+
+namespace {
+// Backward packed layouts (rows K-contiguous, WPAD bytes after every row, zero padded):
+//   w3n : (E, round_up(F, 256), d)        row f = w3[e][f][:]            (dh = dY . w3^T, K = d)
+//   w13t: (E, round_up(d, 256), 2*F_pad)  row i = w1[e][i][:], w2[e][i][:] interleaved per 128
+//                                          columns like w13's rows        (dX = [dg|du] . w13, K = 2*F_pad)
+__global__ __launch_bounds__(256) void pack_rows_kernel(const void* __restrict__ w1, const void* __restrict__ w2,
+                                                        const void* __restrict__ w3, bool in_f32, int E, int d,
+                                                        int F, bool w13t, uint16_t* __restrict__ out,
+                                                        int64_t out_rows, int out_ld) {
+  const int e = blockIdx.z;
+  const int64_t row = blockIdx.y;
+  auto ld = [&](const void* p, int64_t off) {
+    return in_f32 ? f32_to_bf16(static_cast<const float*>(p)[off]) : static_cast<const uint16_t*>(p)[off];
+  };
+  for (int c = blockIdx.x * 256 + threadIdx.x; c < out_ld; c += gridDim.x * 256) {
+    uint16_t v = 0;
+    if (w13t) {
+      const int Fp = round_up(F, 128);
+      if (row < d && c < 2 * Fp) {
+        const int half = (c >> 7) & 1, f = (c >> 8) * 128 + (c & 127);
+        if (f < F) v = ld(half ? w2 : w1, ((int64_t)e * d + row) * F + f);
+      }
+    } else if (row < F && c < d) {
+      v = ld(w3, ((int64_t)e * F + row) * d + c);
+    }
+    out[((int64_t)e * out_rows + row) * out_ld + c] = v;
+  }
+}
+}  // namespace
+
+extern "C" size_t kmoe_packed_w3n_bytes(int E, int d, int F) {
+  return (size_t)E * (size_t)round_up(F, 256) * ((size_t)d * 2 + WPAD);
+}
+
+extern "C" size_t kmoe_packed_w13t_bytes(int E, int d, int F) {
+  return (size_t)E * (size_t)round_up(d, 256) * ((size_t)2 * round_up(F, 128) * 2 + WPAD);
+}
+
+extern "C" int kmoe_pack_weights_bwd(const void* w1, const void* w2, const void* w3, int w_dtype, int E, int d, int F,
+                                     void* w3n_packed, void* w13t_packed, void* stream) {
+  KMOE_REQUIRE(w1 && w2 && w3 && w3n_packed && w13t_packed, KMOE_ERR_NULL, "kmoe_pack_weights_bwd: null buffer");
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_pack_weights_bwd: E=%d out of range", E);
+  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "kmoe_pack_weights_bwd: d=%d must be a positive multiple of 64", d);
+  KMOE_REQUIRE(F > 0, KMOE_ERR_SHAPE, "kmoe_pack_weights_bwd: F=%d must be > 0", F);
+  KMOE_REQUIRE(w_dtype == KMOE_DTYPE_BF16 || w_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE,
+               "kmoe_pack_weights_bwd: weight dtype must be bf16 or f32");
+  hipStream_t s = kmoe::as_stream(stream);
+  const bool f32 = w_dtype == KMOE_DTYPE_F32;
+  const int Fp = round_up(F, 128);
+  const int64_t r3 = round_up(F, 256), r13 = round_up(d, 256);
+  const int ld3 = d + WPAD / 2, ld13 = 2 * Fp + WPAD / 2;
+  hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)kmoe::ceil_div(ld3, 256), (unsigned)r3, (unsigned)E), dim3(256), 0,
+                     s, w1, w2, w3, f32, E, d, F, false, static_cast<uint16_t*>(w3n_packed), r3, ld3);
+  hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)kmoe::ceil_div(ld13, 256), (unsigned)r13, (unsigned)E), dim3(256),
+                     0, s, w1, w2, w3, f32, E, d, F, true, static_cast<uint16_t*>(w13t_packed), r13, ld13);
+  return kmoe::check_launch("kmoe_pack_weights_bwd");
+}
+
+extern "C" int kmoe_gemm_grouped(const void* a, const int32_t* offsets, int E, int K, int64_t max_rows,
+                                 const void* b_packed, int64_t b_expert_rows, int N, void* c, int64_t ldc, int n_valid,
+                                 void* stream) {
+  KMOE_REQUIRE(a && offsets && b_packed && c, KMOE_ERR_NULL, "kmoe_gemm_grouped: null buffer");
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_gemm_grouped: E=%d out of range", E);
+  KMOE_REQUIRE(K > 0 && K % 64 == 0, KMOE_ERR_SHAPE, "kmoe_gemm_grouped: K=%d must be a positive multiple of 64", K);
+  KMOE_REQUIRE(N > 0 && b_expert_rows >= round_up(N, BN) && b_expert_rows % BN == 0, KMOE_ERR_SHAPE,
+               "kmoe_gemm_grouped: b_expert_rows=%lld must be a multiple of %d covering N=%d",
+               (long long)b_expert_rows, BN, N);
+  KMOE_REQUIRE(n_valid > 0 && n_valid <= ldc, KMOE_ERR_SHAPE, "kmoe_gemm_grouped: n_valid=%d, ldc=%lld", n_valid,
+               (long long)ldc);
+  KMOE_REQUIRE(max_rows >= 0 && max_rows < ((int64_t)1 << 31), KMOE_ERR_SHAPE, "kmoe_gemm_grouped: max_rows");
+  if (max_rows == 0) return KMOE_OK;
+  const int rc = launch_gemm(false, false, a, nullptr, nullptr, nullptr, 0, offsets, E, K, max_rows, b_packed,
+                             b_expert_rows, nullptr, c, ldc, n_valid, (int)(round_up(N, BN) / BN),
+                             kmoe::as_stream(stream));
+  if (rc) return rc;
+  return kmoe::check_launch("kmoe_gemm_grouped");
+}
+
+extern "C" int64_t kmoe_wgrad_k_total(int64_t n_rows, int E) {
+  return kmoe::ceil_div<int64_t>(n_rows, WG_KALIGN) * WG_KALIGN + (int64_t)E * WG_KALIGN;
+}
+
+extern "C" int kmoe_gemm_wgrad(const void* at, const void* bt, int64_t k_total, const int32_t* offsets, int E, int M,
+                               int N, void* c, void* c2, int64_t ldc, int n_valid, void* stream) {
+  KMOE_REQUIRE(at && bt && offsets && c, KMOE_ERR_NULL, "kmoe_gemm_wgrad: null buffer");
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_gemm_wgrad: E=%d out of range", E);
+  KMOE_REQUIRE(M > 0 && N > 0 && N % BN == 0, KMOE_ERR_SHAPE, "kmoe_gemm_wgrad: M=%d, N=%d (N a multiple of %d)", M,
+               N, BN);
+  KMOE_REQUIRE(k_total > 0 && k_total % WG_KALIGN == 0, KMOE_ERR_SHAPE,
+               "kmoe_gemm_wgrad: k_total=%lld must be a positive multiple of %d", (long long)k_total, WG_KALIGN);
+  KMOE_REQUIRE(n_valid > 0 && n_valid <= ldc, KMOE_ERR_SHAPE, "kmoe_gemm_wgrad: n_valid=%d, ldc=%lld", n_valid,
+               (long long)ldc);
+  KMOE_REQUIRE((int64_t)(BM + 1) * k_total * 2 < ((int64_t)1 << 31), KMOE_ERR_SHAPE,
+               "kmoe_gemm_wgrad: k_total=%lld too large for 32-bit tile offsets", (long long)k_total);
+  GemmArgs g{};
+  g.A = static_cast<const uint8_t*>(at);
+  g.lda_bytes = k_total * 2;
+  g.B = static_cast<const uint8_t*>(bt);
+  g.b_expert_rows = 0;
+  g.ldb_bytes = k_total * 2;
+  g.C = static_cast<uint16_t*>(c);
+  g.C2 = static_cast<uint16_t*>(c2);
+  g.ldc = ldc;
+  g.n_valid = n_valid;
+  const int n_mt = kmoe::ceil_div(M, BM), n_nt = N / BN;
+  const int64_t blocks = (int64_t)E * n_mt * n_nt;
+  hipLaunchKernelGGL(wgrad_kernel, dim3((unsigned)blocks), dim3(GEMM_THREADS), 0, kmoe::as_stream(stream), g, offsets,
+                     E, M, n_mt, n_nt, (int64_t)M * ldc);
+  return kmoe::check_launch("kmoe_gemm_wgrad");
 }

@@ -47,7 +47,8 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ w_out, int E,
                                                             const float* __restrict__ bias, int k,
                                                             float* __restrict__ logits, int64_t* __restrict__ topk_idx,
-                                                            float* __restrict__ topk_w, float* __restrict__ partials) {
+                                                            float* __restrict__ topk_w, float* __restrict__ partials,
+                                                            float* __restrict__ hidden_pre) {
   using G = RtGeom<RKB>;
   constexpr int RT_STAGES = rt_stages<NE, RKB>();
   constexpr int RT_STAGE = G::STAGE;
@@ -156,12 +157,14 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   __syncthreads();  // stage buffers are reused below
 
   // SiLU, then to LDS: acc[j][r] is hidden wn*64+j*32+lr of token wm*32+8*(r/4)+4*lh+r%4
+  // (training: the pre-activation is also kept for the backward)
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int m = wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
       hs[m * HSTR + wn * 64 + j * 32 + lr] = silu_f32(acc[j][r]);
+      if (hidden_pre && tok0 + m < T) hidden_pre[(tok0 + m) * RT_HID + wn * 64 + j * 32 + lr] = acc[j][r];
     }
   __syncthreads();
 
@@ -313,9 +316,9 @@ extern "C" int64_t kmoe_router_partials_len(int64_t T, int E) {
   return kmoe::ceil_div<int64_t>(T, RT_TOK) * (int64_t)(E + 1);
 }
 
-extern "C" int kmoe_router(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,
-                           const void* w_out, int E, const float* logit_bias, int k, float* logits,
-                           int64_t* topk_idx, float* topk_w, float* partials, void* stream) {
+extern "C" int kmoe_router_train(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,
+                                 const void* w_out, int E, const float* logit_bias, int k, float* logits,
+                                 int64_t* topk_idx, float* topk_w, float* partials, float* hidden_pre, void* stream) {
   KMOE_REQUIRE(x && w_in && w_out && logits, KMOE_ERR_NULL, "kmoe_router: null x/w_in/w_out/logits");
   KMOE_REQUIRE(T >= 0 && T <= (int64_t)1 << 31, KMOE_ERR_SHAPE, "kmoe_router: T=%lld out of range",
                (long long)T);
@@ -336,10 +339,10 @@ extern "C" int kmoe_router(const void* x, const int32_t* row_index, int64_t T, i
   do {                                                                                                           \
     if (d % 128 == 0 && rt_stages<NE_, 256>() >= 3)                                                              \
       hipLaunchKernelGGL((router_kernel<NE_, 256>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, wo, E, \
-                         logit_bias, k, logits, topk_idx, topk_w, partials);                                       \
+                         logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre);                                       \
     else                                                                                                         \
       hipLaunchKernelGGL((router_kernel<NE_, 128>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, wo, E, \
-                         logit_bias, k, logits, topk_idx, topk_w, partials);                                       \
+                         logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre);                                       \
   } while (0)
   if (E <= 8)
     KMOE_ROUTER_LAUNCH(8);
@@ -351,6 +354,13 @@ extern "C" int kmoe_router(const void* x, const int32_t* row_index, int64_t T, i
     KMOE_ROUTER_LAUNCH(64);
 #undef KMOE_ROUTER_LAUNCH
   return kmoe::check_launch("kmoe_router");
+}
+
+extern "C" int kmoe_router(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,
+                           const void* w_out, int E, const float* logit_bias, int k, float* logits,
+                           int64_t* topk_idx, float* topk_w, float* partials, void* stream) {
+  return kmoe_router_train(x, row_index, T, d, w_in, w_out, E, logit_bias, k, logits, topk_idx, topk_w, partials,
+                           nullptr, stream);
 }
 
 extern "C" int kmoe_aux_loss(const float* partials, int64_t T, int E, const int32_t* counts, int k, float w_lb,

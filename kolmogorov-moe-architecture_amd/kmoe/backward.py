@@ -1,0 +1,177 @@
+"""Backward pass of the token-choice MoE layer on the HIP kernels.
+
+Gradients of MoELayer.forward's token-choice path (moe.py:759-838): the router
+MLP and top-k renormalisation (moe.py:423-462), the grouped SwiGLU experts and
+combine (moe.py:213-294, ffn.py:17-64) and the load-balance / z losses
+(moe.py:840-939).  The reference gets these from autograd through its eager ops;
+its native grouped kernel has no backward at all (moe_arch/kernels/__init__.py:
+167-244 is unused, sparse_moe.py:362-368).
+
+Data flow (A = routed rows, grouped by expert):
+  dy --combine_bwd--> dyperm (A,d), dw (T,k)
+  dh  = dyperm . w3^T            grouped GEMM (packed w3n)
+  dgu = swiglu_bwd(dh, g, u)     g, u saved by the forward's gate/up GEMM
+  dxp = dgu . [w1|w2]^T          grouped GEMM (packed w13t)
+  dx  = sum_j dxp[slot(t,j)] + da . w_in        (combine with unit weights, add)
+  dW3 = h^T dyperm, dW1|dW2 = x^T dgu           per-expert GEMMs over transposed row segments
+  dlogits = topk-renorm backward(dw) + aux backward;  da, dW_out (router MLP);  dW_in = da^T x
+"""
+from __future__ import annotations
+
+from typing import NamedTuple, Optional
+
+import torch
+
+from . import _lib, ops
+from ._lib import ptr
+
+_BF16 = torch.bfloat16
+
+
+def _ru(a: int, b: int) -> int:
+    return (a + b - 1) // b * b
+
+
+class BwdWeights(NamedTuple):
+    w3n: torch.Tensor    # (E, round_up(F,256), d) packed rows of w3
+    w13t: torch.Tensor   # (E, round_up(d,256), 2*F_pad) packed rows of w1|w2
+    w_in_t: torch.Tensor  # (round_up(d,256), 128) packed rows of w_in^T
+
+
+def pack_bwd_weights(w1, w2, w3, w_in) -> BwdWeights:
+    E, d, F = w1.shape
+    dt = w1.dtype
+    if dt not in (torch.float32, _BF16):
+        raise ValueError(f"kmoe backward: unsupported weight dtype {dt}")
+    w1, w2, w3 = (w.detach().contiguous() for w in (w1, w2, w3))
+    w_in = w_in.detach().to(dt).contiguous()
+    lib = _lib.load()
+    wdt = _lib.DTYPE_F32 if dt == torch.float32 else _lib.DTYPE_BF16
+    dev = w1.device
+    w3n = torch.empty(lib.kmoe_packed_w3n_bytes(E, d, F), device=dev, dtype=torch.uint8)
+    w13t = torch.empty(lib.kmoe_packed_w13t_bytes(E, d, F), device=dev, dtype=torch.uint8)
+    wit = torch.empty(lib.kmoe_packed_w_in_t_bytes(d), device=dev, dtype=torch.uint8)
+    s = ops._stream(w1)
+    _lib.call("kmoe_pack_weights_bwd", ptr(w1), ptr(w2), ptr(w3), wdt, E, d, F, ptr(w3n), ptr(w13t), s)
+    _lib.call("kmoe_pack_w_in_t", ptr(w_in), wdt, d, ptr(wit), s)
+    return BwdWeights(w3n, w13t, wit)
+
+
+class Saved(NamedTuple):
+    """What the training forward keeps for the backward."""
+    x2d: torch.Tensor        # (T, d) bf16 layer input
+    logits: torch.Tensor     # (T, E) f32
+    idx: torch.Tensor        # (T, k) int64
+    w: torch.Tensor          # (T, k) f32
+    hidden: torch.Tensor     # (T, 128) f32 router pre-activation
+    disp: ops.DispatchOut    # routing tables
+    h: torch.Tensor          # (A, F_pad) bf16
+    gu: torch.Tensor         # (A, 2 F_pad) bf16 pre-activation gate / up
+    yperm: torch.Tensor      # (A, d) bf16 expert outputs
+
+
+class Grads(NamedTuple):
+    dx: torch.Tensor
+    dw_in: torch.Tensor
+    dw_out: torch.Tensor
+    dw1: torch.Tensor
+    dw2: torch.Tensor
+    dw3: torch.Tensor
+
+
+def _stage(name):
+    return ops._Stage(name)
+
+
+def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], w_out: torch.Tensor,
+                 bw: BwdWeights, E: int, F: int, w_lb: float, w_z: float, need_weights: bool = True) -> Grads:
+    """All gradients of one token-choice MoE layer forward (bf16 compute)."""
+    lib = _lib.load()
+    x2d = sv.x2d
+    T, d = x2d.shape
+    k = sv.idx.shape[1]
+    A = T * k
+    Fp = _ru(F, 128)
+    dev = x2d.device
+    s = ops._stream(x2d)
+    disp = sv.disp
+    dy = dy.reshape(T, d).to(_BF16).contiguous()
+
+    # ---- combine backward: dyperm, dw
+    dyperm = torch.empty(max(A, 1), d, device=dev, dtype=_BF16)
+    dw = torch.empty(T, k, device=dev, dtype=torch.float32)
+    with _stage("bwd_combine"):
+        _lib.call("kmoe_combine_bwd", ptr(dy), ptr(sv.yperm), ptr(disp.slot_row), ptr(disp.slot_w), k, d, T,
+                  ptr(dyperm), ptr(dw), s)
+    # ---- dh = dyperm . w3^T (fused nothing: plain grouped GEMM), SwiGLU backward
+    dh = torch.empty(max(A, 1), Fp, device=dev, dtype=_BF16)
+    with _stage("bwd_gemm_dh"):
+        _lib.call("kmoe_gemm_grouped", ptr(dyperm), ptr(disp.offsets), E, d, A, ptr(bw.w3n), _ru(F, 256), Fp,
+                  ptr(dh), Fp, Fp, s)
+    dgu = torch.empty(max(A, 1), 2 * Fp, device=dev, dtype=_BF16)
+    with _stage("bwd_swiglu"):
+        _lib.call("kmoe_swiglu_bwd", ptr(dh), ptr(sv.gu), A, ptr(disp.offsets[E:]), F, ptr(dgu), s)
+    # ---- dxperm = dgu . [w1|w2]^T, then back to tokens (unit weights)
+    dxp = torch.empty(max(A, 1), d, device=dev, dtype=_BF16)
+    with _stage("bwd_gemm_dx"):
+        _lib.call("kmoe_gemm_grouped", ptr(dgu), ptr(disp.offsets), E, 2 * Fp, A, ptr(bw.w13t), _ru(d, 256), d,
+                  ptr(dxp), d, d, s)
+    ones = torch.ones(T, k, device=dev, dtype=torch.float32)
+    dx_e = ops.combine(dxp, disp.slot_row.view(T, k), ones, T)
+
+    # ---- router: logit gradient, MLP backward, dx contribution, dW_in
+    dl = torch.empty(T, E, device=dev, dtype=torch.float32)
+    ga = None if grad_aux is None else grad_aux.reshape(1).to(torch.float32).contiguous()
+    with _stage("bwd_router"):
+        _lib.call("kmoe_router_dlogits", ptr(sv.logits), T, E, ptr(sv.idx), ptr(sv.w), ptr(dw), k,
+                  ptr(disp.counts), ptr(ga), float(w_lb), float(w_z), ptr(dl), s)
+        da = torch.empty(T, _lib.ROUTER_HIDDEN, device=dev, dtype=_BF16)
+        wdt = w_out.dtype
+        dw_out = torch.empty(E, _lib.ROUTER_HIDDEN, device=dev, dtype=wdt)
+        wsb = lib.kmoe_router_bwd_workspace_bytes(T, E)
+        ws = torch.empty(max(wsb, 4), device=dev, dtype=torch.uint8)
+        w_out_b = w_out.detach().to(_BF16).contiguous()
+        _lib.call("kmoe_router_mlp_bwd", ptr(dl), ptr(sv.hidden), T, E, ptr(w_out_b), ptr(da), ptr(dw_out),
+                  _lib.DTYPE_F32 if wdt == torch.float32 else _lib.DTYPE_BF16, ptr(ws), wsb, s)
+        one_seg = torch.tensor([0, T], device=dev, dtype=torch.int32)
+        dx_r = torch.empty(T, d, device=dev, dtype=_BF16)
+        _lib.call("kmoe_gemm_grouped", ptr(da), ptr(one_seg), 1, _lib.ROUTER_HIDDEN, T, ptr(bw.w_in_t), _ru(d, 256),
+                  d, ptr(dx_r), d, d, s)
+    dx = torch.empty(T, d, device=dev, dtype=_BF16)
+    _lib.call("kmoe_add_bf16", ptr(dx_e), ptr(dx_r), T * d, ptr(dx), s)
+    if not need_weights:
+        return Grads(dx, None, dw_out, None, None, None)
+
+    # ---- weight gradients over transposed row segments
+    with _stage("bwd_wgrad"):
+        kt1 = lib.kmoe_wgrad_k_total(T, 1)
+        daT = torch.empty(_lib.ROUTER_HIDDEN, kt1, device=dev, dtype=_BF16)
+        _lib.call("kmoe_seg_transpose", ptr(da), _lib.ROUTER_HIDDEN, None, None, ptr(one_seg), 1, _lib.ROUTER_HIDDEN,
+                  _lib.ROUTER_HIDDEN, ptr(daT), kt1, s)
+        dpad = _ru(d, 256)
+        xT1 = torch.empty(dpad, kt1, device=dev, dtype=_BF16)
+        _lib.call("kmoe_seg_transpose", ptr(x2d), d, None, None, ptr(one_seg), 1, d, dpad, ptr(xT1), kt1, s)
+        dw_in = torch.empty(_lib.ROUTER_HIDDEN, d, device=dev, dtype=_BF16)
+        _lib.call("kmoe_gemm_wgrad", ptr(daT), ptr(xT1), kt1, ptr(one_seg), 1, _lib.ROUTER_HIDDEN, dpad, ptr(dw_in),
+                  None, d, d, s)
+        del daT, xT1
+
+        kt = lib.kmoe_wgrad_k_total(A, E)
+        dw3 = torch.empty(E, F, d, device=dev, dtype=_BF16)
+        hT = torch.empty(Fp, kt, device=dev, dtype=_BF16)
+        _lib.call("kmoe_seg_transpose", ptr(sv.h), Fp, None, None, ptr(disp.offsets), E, Fp, Fp, ptr(hT), kt, s)
+        dyT = torch.empty(dpad, kt, device=dev, dtype=_BF16)
+        _lib.call("kmoe_seg_transpose", ptr(dyperm), d, None, None, ptr(disp.offsets), E, d, dpad, ptr(dyT), kt, s)
+        _lib.call("kmoe_gemm_wgrad", ptr(hT), ptr(dyT), kt, ptr(disp.offsets), E, F, dpad, ptr(dw3), None, d, d, s)
+        del hT, dyT
+        dw1 = torch.empty(E, d, F, device=dev, dtype=_BF16)
+        dw2 = torch.empty(E, d, F, device=dev, dtype=_BF16)
+        xT = torch.empty(d, kt, device=dev, dtype=_BF16)
+        _lib.call("kmoe_seg_transpose", ptr(x2d), d, ptr(disp.row_token), None, ptr(disp.offsets), E, d, d, ptr(xT),
+                  kt, s)
+        dguT = torch.empty(2 * Fp, kt, device=dev, dtype=_BF16)
+        _lib.call("kmoe_seg_transpose", ptr(dgu), 2 * Fp, None, None, ptr(disp.offsets), E, 2 * Fp, 2 * Fp, ptr(dguT),
+                  kt, s)
+        _lib.call("kmoe_gemm_wgrad", ptr(xT), ptr(dguT), kt, ptr(disp.offsets), E, d, 2 * Fp, ptr(dw1), ptr(dw2), F,
+                  F, s)
+    return Grads(dx, dw_in, dw_out, dw1, dw2, dw3)

@@ -11,7 +11,10 @@ return contracts as moe_arch/model/moe.py:
 Numerics: the router accumulates in fp32 and ranks experts by fp32 logit
 (equal logits -> lowest expert index); expert GEMMs run bf16 (or fp8 e4m3)
 MFMA with fp32 accumulation; the combine accumulates in fp32 in a fixed order.
-Only the forward pass is implemented: backward raises.
+Backward: the token-choice bf16 layer (MoELayer with top-k routing, optional
+capacity drop) trains through the HIP backward kernels (kmoe.backward); the
+other paths (expert choice, fp8, balanced routing, MoD, GroupedExperts called
+directly) are forward-only and raise in backward.
 """
 from __future__ import annotations
 
@@ -21,6 +24,7 @@ from typing import Optional, Tuple
 import torch
 import torch.nn as nn
 
+from . import backward as _bwd
 from . import ops
 from .config import AdvancedMoEConfig
 
@@ -90,7 +94,7 @@ class Router(_RouterMLP):
         self.logit_bias = None if bias is None else torch.tensor(list(bias), dtype=torch.float32)
 
     def route(self, x2d: torch.Tensor, row_index: Optional[torch.Tensor] = None,
-              T: Optional[int] = None) -> ops.RouterOut:
+              T: Optional[int] = None, save_hidden: bool = False) -> ops.RouterOut:
         """Kernel-level routing of flattened tokens: fp32 logits, int64 idx, f32 weights.
         With moe_balanced_routing the picks are the capacity-balanced assignment
         (moe.py:443-451) over all the tokens of the call."""
@@ -101,10 +105,12 @@ class Router(_RouterMLP):
                 self.logit_bias = self.logit_bias.to(x2d.device)
             bias = self.logit_bias
         if self.balanced_routing:
+            if save_hidden:
+                raise NotImplementedError("kmoe: backward through balanced routing is not implemented")
             r = ops.router(x2d, w_in, w_out, 0, bias=bias, row_index=row_index, T=T)
             idx, w = ops.balanced_topk(r.logits, self.top_k)
             return ops.RouterOut(r.logits, idx, w, r.partials)
-        return ops.router(x2d, w_in, w_out, self.top_k, bias=bias, row_index=row_index, T=T)
+        return ops.router(x2d, w_in, w_out, self.top_k, bias=bias, row_index=row_index, T=T, save_hidden=save_hidden)
 
     def forward(self, hidden_states: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         B, S, d = hidden_states.shape
@@ -234,6 +240,41 @@ class GroupedExpertsExpertChoice(_PackedExperts):
         return _forward_only(y.view(B, S, d).to(x.dtype), x, self.w1, self.w2, self.w3, expert_weights)
 
 
+class _MoETrainFn(torch.autograd.Function):
+    """Token-choice MoE layer whose backward runs on the HIP backward kernels.
+
+    Inputs are the layer input and the parameters (so autograd routes their
+    gradients); outputs are y and the aux loss (a 0-dim tensor, 0 in eval)."""
+
+    @staticmethod
+    def forward(ctx, x, w_in, w_out, w1, w2, w3, layer):
+        B, S, d = x.shape
+        T = B * S
+        x2d = x.reshape(T, d).to(torch.bfloat16).contiguous()
+        y2d, aux, sv = layer._train_forward(x2d, T, layer._out_dtype(x))
+        ctx.layer = layer
+        ctx.sv = sv
+        ctx.meta = (B, S, d, x.dtype, aux is not None)
+        aux_t = aux if aux is not None else torch.zeros((), device=x.device, dtype=torch.float32)
+        return y2d.view(B, S, d).to(x.dtype), aux_t
+
+    @staticmethod
+    def backward(ctx, dy, daux):
+        B, S, d, x_dtype, has_aux = ctx.meta
+        layer = ctx.layer
+        ge = layer.grouped_experts
+        w_in, w_out = layer.router.router[0].weight, layer.router.router[2].weight
+        need_w = any(ctx.needs_input_grad[1:6])
+        g = _bwd.moe_backward(ctx.sv, dy, daux if has_aux else None, w_out, layer._bwd_weights(), layer.n_experts,
+                              ge.d_ff, layer.load_balance_loss_weight, layer.router_z_loss_weight, need_weights=need_w)
+        ctx.sv = None
+        dx = g.dx.view(B, S, d).to(x_dtype)
+        if not need_w:
+            return dx, None, None, None, None, None, None
+        return (dx, g.dw_in.to(w_in.dtype), g.dw_out.to(w_out.dtype), g.dw1.to(ge.w1.dtype), g.dw2.to(ge.w2.dtype),
+                g.dw3.to(ge.w3.dtype), None)
+
+
 class MoELayer(nn.Module):
     """MoE feed-forward layer (moe.py:676-950) on the HIP kernels."""
 
@@ -282,8 +323,54 @@ class MoELayer(nn.Module):
     def _out_dtype(self, x):
         return torch.float32 if x.dtype == torch.float32 else torch.bfloat16
 
+    def _trainable(self, x) -> bool:
+        """Whether this forward records a backward through the HIP kernels."""
+        if not torch.is_grad_enabled():
+            return False
+        if not (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        ge = self.grouped_experts
+        return not (ge.use_fp8 or self.router.balanced_routing)
+
+    def _bwd_weights(self) -> _bwd.BwdWeights:
+        """Backward packed weights, rebuilt only when a parameter changed."""
+        ge = self.grouped_experts
+        w_in = self.router.router[0].weight
+        key = tuple((w.data_ptr(), w._version) for w in (ge.w1, ge.w2, ge.w3, w_in))
+        cache = getattr(self, "_bwd_cache", None)
+        if cache is None or cache[0] != key:
+            with torch.no_grad():
+                cache = (key, _bwd.pack_bwd_weights(ge.w1, ge.w2, ge.w3, w_in))
+            self._bwd_cache = cache
+        return cache[1]
+
+    def _train_forward(self, x2d, T, out_dtype):
+        """Token-choice forward keeping what the backward needs: (y, aux or None, Saved)."""
+        r = self.router.route(x2d, T=T, save_hidden=True)
+        ge = self.grouped_experts
+        k, E = self.top_k, self.n_experts
+        cap = ops.capacity_of(self.capacity_factor, T, k, E) if self.drop_overflow else 0
+        pw = ge.packed()
+        disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=False)
+        h, gu = ops.gemm_gate_up_rows(x2d, None, disp.row_token, disp.offsets, pw, T * k, save_gu=True)
+        yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
+        y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T, out_dtype=out_dtype)
+        self.last_expert_counts = disp.counts
+        aux = None
+        if self.training:
+            aux = ops.aux_loss(r.partials, T, E, disp.counts, k, self.load_balance_loss_weight,
+                               self.router_z_loss_weight)[0]
+        sv = _bwd.Saved(x2d, r.logits, r.idx, r.w, r.hidden, disp, h, gu, yperm)
+        return y, aux, sv
+
     def _forward_token_choice(self, hidden_states: torch.Tensor) -> torch.Tensor:
         B, S, d = hidden_states.shape
+        if self._trainable(hidden_states):
+            ge = self.grouped_experts
+            y, aux = _MoETrainFn.apply(hidden_states, self.router.router[0].weight, self.router.router[2].weight,
+                                       ge.w1, ge.w2, ge.w3, self)
+            self.aux_loss = aux if self.training else 0.0
+            return y
         x2d = hidden_states.reshape(B * S, d)
         y, r, disp = self.forward_rows(x2d, T=B * S, out_dtype=self._out_dtype(hidden_states))
         self._set_token_choice_aux(r, disp, B * S)

@@ -76,9 +76,10 @@ class RouterOut(NamedTuple):
     idx: Optional[torch.Tensor]   # (T, k) int64
     w: Optional[torch.Tensor]     # (T, k) f32
     partials: torch.Tensor        # per-block aux partial sums
+    hidden: Optional[torch.Tensor] = None  # (T, 128) f32 pre-activation (training router)
 
 
-def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None) -> RouterOut:
+def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=False) -> RouterOut:
     """logits/top-k of the reference Router (moe.py:423-462) on the HIP kernel.
 
     x2d: (rows, d) bf16; w_in: (128, d); w_out: (E, 128); row_index: optional
@@ -102,10 +103,11 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None) -> RouterOut:
     npart = _lib.load().kmoe_router_partials_len(T, E)
     partials = torch.empty(max(npart, 1), device=dev, dtype=torch.float32)
     bias = _contig(bias, torch.float32)
+    hidden = torch.empty(T, _lib.ROUTER_HIDDEN, device=dev, dtype=torch.float32) if save_hidden else None
     with _Stage("router"):
-        _lib.call("kmoe_router", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
-              ptr(logits), ptr(idx), ptr(w), ptr(partials), _stream(x2d))
-    return RouterOut(logits, idx, w, partials)
+        _lib.call("kmoe_router_train", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
+                  ptr(logits), ptr(idx), ptr(w), ptr(partials), ptr(hidden), _stream(x2d))
+    return RouterOut(logits, idx, w, partials, hidden)
 
 
 def balanced_topk(logits, k):
@@ -243,9 +245,11 @@ def gemm_gate_up(xperm, xscale, offsets, pw: PackedWeights, max_rows):
     return h
 
 
-def gemm_gate_up_rows(x2d, row_index, row_token, offsets, pw: PackedWeights, max_rows):
+def gemm_gate_up_rows(x2d, row_index, row_token, offsets, pw: PackedWeights, max_rows, save_gu=False):
     """gate_up GEMM whose A rows are x2d[row_index[row_token[r]]] (x2d[row_token[r]]
-    without row_index): the dispatch gather fused into the GEMM's loads (bf16)."""
+    without row_index): the dispatch gather fused into the GEMM's loads (bf16).
+    save_gu (training) also returns the pre-activation gate/up values (max_rows,
+    2*F_pad) in the packed order: returns (h, gu)."""
     if pw.fp8:
         raise ValueError("kmoe.gemm_gate_up_rows: bf16 weights only (fp8 reads quantised permuted rows)")
     _need_gpu(x2d, row_token, offsets)
@@ -253,6 +257,12 @@ def gemm_gate_up_rows(x2d, row_index, row_token, offsets, pw: PackedWeights, max
     lib = _lib.load()
     Fp = lib.kmoe_padded_ff(pw.F)
     h = torch.empty(max(max_rows, 1), Fp, device=x2d.device, dtype=_BF16)
+    if save_gu:
+        gu = torch.empty(max(max_rows, 1), 2 * Fp, device=x2d.device, dtype=_BF16)
+        with _Stage("gemm_gate_up"):
+            _lib.call("kmoe_gemm_gate_up_rows_gu", ptr(x2d), ptr(row_index), x2d.shape[0], ptr(row_token),
+                      ptr(offsets), pw.E, pw.d, pw.F, max_rows, ptr(pw.w13), ptr(h), ptr(gu), _stream(x2d))
+        return h, gu
     with _Stage("gemm_gate_up"):
         _lib.call("kmoe_gemm_gate_up_rows", ptr(x2d), ptr(row_index), x2d.shape[0], ptr(row_token), ptr(offsets),
                   pw.E, pw.d, pw.F, max_rows, ptr(pw.w13), ptr(h), _stream(x2d))

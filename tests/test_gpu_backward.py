@@ -1,0 +1,184 @@
+"""Backward pass of the token-choice MoE layer on the HIP kernels vs autograd of
+an fp64 CPU restatement of the reference forward (moe.py:423-462 router,
+moe.py:213-294 experts + combine, moe.py:840-939 aux losses; SwiGLU ffn.py:17-64),
+fed the kernel's own routing (the selection is pinned bit-exactly by the forward
+tests) and the bf16 values of the inputs and parameters.
+
+Tolerance: rel-L2 <= 1e-2 for dx and the expert weight gradients, 2e-2 for the
+router weight gradients (bf16 intermediates: the permuted dy rows, dh, dg/du, the
+saved g/u and the router's da are rounded to bf16 once each).
+"""
+import numpy as np
+import pytest
+import torch
+
+import kmoe  # noqa: F401
+from kmoe import synth
+from kmoe.config import AdvancedMoEConfig
+from kmoe.moe import MoELayer
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _ref_loss(x, w_in, w_out, w1, w2, w3, idx, dy, E, k, cap, w_lb, w_z, bias, train):
+    """fp64 restatement of the reference forward + the loss sum(y * dy) (+ aux)."""
+    T = x.shape[0]
+    a = x @ w_in.T
+    logits = torch.nn.functional.silu(a) @ w_out.T
+    if bias is not None:
+        logits = logits + bias
+    p = torch.softmax(logits, -1)
+    v = p.gather(1, idx)
+    w = v / v.sum(1, keepdim=True)
+    y = torch.zeros_like(x)
+    flat = idx.reshape(-1)
+    for e in range(E):
+        a_idx = torch.nonzero(flat == e).reshape(-1)  # assignment order = token order
+        if cap > 0:
+            a_idx = a_idx[:cap]
+        if a_idx.numel() == 0:
+            continue
+        t, j = a_idx // k, a_idx % k
+        rows = x[t]
+        h = torch.nn.functional.silu(rows @ w1[e]) * (rows @ w2[e])
+        y = y.index_add(0, t, w[t, j, None] * (h @ w3[e]))
+    loss = (y * dy).sum()
+    if train:
+        counts = torch.bincount(flat, minlength=E).double()
+        lb = E * ((counts / (T * k)) * p.mean(0)).sum()
+        z = (torch.logsumexp(logits, -1) ** 2).mean()
+        loss = loss + w_lb * lb + w_z * z
+    return loss
+
+
+def _rel(a, b):
+    a = a.double().cpu()
+    b = b.double().cpu()
+    return float((a - b).norm() / max(b.norm(), 1e-30))
+
+
+def _run(dev, B, S, d, E, k, F, seed, drop_cf=None, train=True, zipf=False, empty_expert=None, dy_zero=False):
+    cfg = AdvancedMoEConfig(d_model=d, n_experts=E, moe_top_k=k, d_ff_expert=F,
+                            moe_capacity_factor=drop_cf or 1.25, moe_drop_overflow=drop_cf is not None,
+                            moe_router_bias=synth.zipf_bias(E, seed).tolist() if zipf else None)
+    layer = MoELayer(cfg, 0).to(dev, torch.bfloat16)
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        layer.router.router[0].weight.copy_(torch.randn(128, d, generator=g) * 0.05)
+        layer.router.router[2].weight.copy_(torch.randn(E, 128, generator=g) * 0.05)
+        if empty_expert is not None:
+            # a large negative logit bias keeps expert `empty_expert` out of every top-k
+            b = torch.zeros(E)
+            b[empty_expert] = -1e4
+            layer.router.logit_bias = b.to(dev)
+        for w in (layer.grouped_experts.w1, layer.grouped_experts.w2, layer.grouped_experts.w3):
+            w.copy_(torch.randn(w.shape, generator=g) * 0.05)
+    layer.train(train)
+    x = (torch.randn(B, S, d, generator=g)).to(torch.bfloat16).to(dev).requires_grad_(True)
+    dy = torch.randn(B, S, d, generator=g).to(torch.bfloat16)
+    if dy_zero:
+        dy.zero_()
+    y = layer(x)
+    loss = (y.float() * dy.to(dev).float()).sum()
+    if train:
+        loss = loss + layer.aux_loss
+    loss.backward()
+    torch.cuda.synchronize()
+    # the kernel's routing (deterministic: same call as the forward's)
+    with torch.no_grad():
+        r = layer.router.route(x.detach().reshape(B * S, d))
+    idx = r.idx.cpu()
+    f64 = lambda t: t.detach().double().cpu().clone().requires_grad_(True)
+    ge = layer.grouped_experts
+    params = [f64(layer.router.router[0].weight), f64(layer.router.router[2].weight), f64(ge.w1), f64(ge.w2),
+              f64(ge.w3)]
+    xr = f64(x.reshape(B * S, d))
+    cap = int(np.ceil(drop_cf * B * S * k / E)) if drop_cf is not None else 0
+    bias = None if layer.router.logit_bias is None else layer.router.logit_bias.double().cpu()
+    ref = _ref_loss(xr, *params, idx, dy.reshape(B * S, d).double(), E, k, cap,
+                    layer.load_balance_loss_weight, layer.router_z_loss_weight, bias, train)
+    ref.backward()
+    got = [x.grad.reshape(B * S, d), layer.router.router[0].weight.grad, layer.router.router[2].weight.grad,
+           ge.w1.grad, ge.w2.grad, ge.w3.grad]
+    want = [xr.grad] + [p.grad for p in params]
+    names = ["dx", "dw_in", "dw_out", "dw1", "dw2", "dw3"]
+    errs = {n: _rel(a, b) for n, a, b in zip(names, got, want)}
+    for t in got:
+        assert torch.isfinite(t.float()).all()
+    return errs, layer, idx
+
+
+def _check(errs):
+    print("rel-L2:", {n: f"{e:.2e}" for n, e in errs.items()})
+    for n, e in errs.items():
+        tol = 2e-2 if n in ("dw_in", "dw_out") else 1e-2
+        assert e <= tol, (n, e, errs)
+
+
+@pytest.mark.parametrize("B,S,d,E,k,F", [(2, 256, 256, 8, 2, 512), (1, 640, 384, 4, 2, 320),
+                                         (2, 512, 512, 16, 2, 768)])
+def test_backward_parity(dev, B, S, d, E, k, F):
+    errs, _, _ = _run(dev, B, S, d, E, k, F, seed=100 + F)
+    _check(errs)
+
+
+def test_backward_capacity_drop(dev):
+    """Capacity drop (cf 1.0, Zipf bias): dropped slots contribute no gradient."""
+    errs, layer, idx = _run(dev, 2, 256, 256, 8, 2, 512, seed=7, drop_cf=1.0, zipf=True)
+    counts = np.bincount(idx.numpy().reshape(-1), minlength=8)
+    assert counts.max() > int(np.ceil(1.0 * 512 * 2 / 8)), "the test needs an overflowing expert"
+    _check(errs)
+
+
+def test_backward_empty_expert(dev):
+    """An expert that receives no rows gets exactly zero weight gradients."""
+    errs, layer, idx = _run(dev, 1, 512, 256, 8, 2, 256, seed=9, empty_expert=3)
+    assert not (idx.numpy() == 3).any()
+    ge = layer.grouped_experts
+    for w in (ge.w1, ge.w2, ge.w3):
+        assert torch.count_nonzero(w.grad[3]) == 0
+    _check(errs)
+
+
+def test_backward_eval_mode_no_aux(dev):
+    """Eval mode: aux_loss is 0.0 and the gradients come from y alone."""
+    errs, layer, _ = _run(dev, 2, 256, 256, 8, 2, 512, seed=11, train=False)
+    assert layer.aux_loss == 0.0
+    _check(errs)
+
+
+def test_backward_aux_only(dev):
+    """Loss = aux alone: the router gradients come only from the load-balance and z
+    losses (softmax backward of mean_t p and of lse^2); the experts get exact zeros."""
+    errs, layer, _ = _run(dev, 2, 256, 256, 8, 2, 512, seed=13, dy_zero=True)
+    ge = layer.grouped_experts
+    for w in (ge.w1, ge.w2, ge.w3):
+        assert torch.count_nonzero(w.grad) == 0
+    assert torch.count_nonzero(layer.router.router[0].weight.grad) > 0
+    errs.pop("dw1"), errs.pop("dw2"), errs.pop("dw3")
+    _check(errs)
+
+
+def test_backward_deterministic(dev):
+    """Two backward passes over the same inputs give bit-identical gradients."""
+    cfg = AdvancedMoEConfig(d_model=512, n_experts=8, moe_top_k=2, d_ff_expert=512)
+    layer = MoELayer(cfg, 0).to(dev, torch.bfloat16).train()
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 512, 512, generator=g).to(torch.bfloat16).to(dev)
+    dy = torch.randn(2, 512, 512, generator=g).to(torch.bfloat16).to(dev)
+    grads = []
+    for _ in range(2):
+        layer.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_(True)
+        y = layer(xx)
+        ((y.float() * dy.float()).sum() + layer.aux_loss).backward()
+        grads.append([xx.grad.clone()] + [p.grad.clone() for p in layer.parameters()])
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
