@@ -1,6 +1,6 @@
 """MoE-layer forward benchmark on one MI355X (the BASELINE.json metric).
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--no-cpu] [--no-train]
 
 A step is one MoE-layer forward (router, dispatch, grouped SwiGLU GEMMs,
 combine, aux losses; train mode so the aux loss is computed) over one batch of
@@ -9,7 +9,9 @@ whole-job tokens/s (timed with nothing but the forwards on the stream, plus a HI
 event pair around the gate/up grouped GEMM on every EVENT_EVERY-th forward: the
 roofline of that dominant kernel), per-stage figures from a separate pass
 and a CPU baseline (the op-for-op torch-CPU port of the reference path, timed on this
-host on a bounded token sample).
+host on a bounded token sample).  Token-choice bf16 configs also report a
+"training" object: the training forward + backward step on the HIP kernels,
+timed in its own pass after the forward metric's timed region.
 """
 import argparse
 import json
@@ -38,6 +40,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-train", action="store_true", help="skip the training-step (backward) pass")
     ap.add_argument("--stage-steps", type=int, default=20, help="forwards of the per-stage timing pass")
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
@@ -159,9 +162,80 @@ def run_gpu(args, wl):
                 rec["frac_hbm"] = round(amount / (us * 1e-6) / PEAK_HBM, 4)
         stage_out[name] = rec
     elapsed = t1 - t0
+    training = None
+    if not (wl.fp8 or wl.mod or wl.routing == "expert_choice") and not args.no_train:
+        training = run_training(args, wl, layer, x)
     return dict(elapsed=elapsed, stages=stage_out, a_kept=a_kept, a_all=a_all, t_in=t_in,
                 gemm_us=statistics.mean(gu_timed) if gu_timed else float("nan"), gemm_samples=len(gu_timed),
-                work=work, rows_us=rows_us)
+                work=work, rows_us=rows_us, training=training)
+
+
+def run_training(args, wl, layer, x):
+    """One training step of the layer (the forward that keeps what the backward needs,
+    then the backward on the HIP kernels), timed outside the forward metric's region:
+    K steps between synchronisations, then a per-stage pass with an event pair around
+    every stage (us per step, summed over the stage's launches)."""
+    import torch
+    from kmoe import backward as BW, ops
+
+    T, d, F, k = wl.T, wl.d, wl.F, wl.k
+    x2d = x.reshape(T, d)
+    dev = x2d.device
+    g = torch.Generator().manual_seed(wl.seed + 100)
+    dy = torch.randn(T, d, generator=g).to(torch.bfloat16).to(dev)
+    ga = torch.ones((), device=dev, dtype=torch.float32)
+    w_out = layer.router.router[2].weight
+    bw = layer._bwd_weights()
+
+    def train_step():
+        _, _, sv = layer._train_forward(x2d, T, torch.bfloat16)
+        return BW.moe_backward(sv, dy, ga, w_out, bw, wl.E, F, layer.load_balance_loss_weight,
+                               layer.router_z_loss_weight)
+
+    steps = max(1, args.steps // 5)
+    with torch.no_grad():
+        for _ in range(3):
+            train_step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            train_step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        events = []
+        ops.set_stage_timing(events)
+        for _ in range(steps):
+            train_step()
+        torch.cuda.synchronize()
+        ops.set_stage_timing(None)
+    per = {}
+    for name, a, b in events:
+        per[name] = per.get(name, 0.0) + a.elapsed_time(b) * 1e3 / steps
+    a_kept = int(layer.last_expert_counts.clamp(
+        max=ops.capacity_of(layer.capacity_factor, T, k, wl.E) if layer.drop_overflow else 1 << 30).sum().item())
+    dF = 2.0 * d * F * a_kept
+    gemm = {"bwd_gemm_dh": dF, "bwd_gemm_dx": 2 * dF, "bwd_wgrad_w3": dF, "bwd_wgrad_w13": 2 * dF,
+            "bwd_wgrad_router": 2.0 * T * 128 * d, "gemm_gate_up": 2 * dF, "gemm_down": dF}
+    stages = {}
+    for name, us in per.items():
+        rec = {"us": round(us, 2)}
+        if name in gemm:
+            rec["TFLOPs"] = round(gemm[name] / (us * 1e-6) / 1e12, 1)
+            rec["frac_peak"] = round(gemm[name] / (us * 1e-6) / PEAK_BF16, 4)
+        stages[name] = rec
+    bwd_names = [n for n in per if n.startswith("bwd_")]
+    bwd_gemm = [n for n in ("bwd_gemm_dh", "bwd_gemm_dx", "bwd_wgrad_w3", "bwd_wgrad_w13") if n in per]
+    g_us = sum(per[n] for n in bwd_gemm)
+    g_fl = sum(gemm[n] for n in bwd_gemm)
+    step_s = (t1 - t0) / steps
+    return {"step_ms": round(step_s * 1e3, 3), "tokens_per_s": round(T / step_s, 1),
+            "backward_us": round(sum(per[n] for n in bwd_names), 1),
+            "bwd_expert_gemm_TFLOPs": round(g_fl / (g_us * 1e-6) / 1e12, 1) if g_us else None,
+            "bwd_expert_gemm_frac_peak": round(g_fl / (g_us * 1e-6) / PEAK_BF16, 4) if g_us else None,
+            "work": "backward expert GEMMs 12*d*F*A_kept FLOP (dh 2, dX 4, dW3 2, dW1|dW2 4)",
+            "stages": stages, "steps": steps,
+            "note": "forward keeping g/u and the router pre-activation + backward (dy ~ N(0,1) bf16, aux grad 1); "
+                    "outside the forward metric's timed region"}
 
 
 def run_cpu_baseline(wl, tokens):
@@ -263,6 +337,8 @@ def main():
                                         "layer gathers rows inside the gate/up GEMM instead"}
     if "combine" in res["stages"]:
         out["combine_GBps"] = res["stages"]["combine"].get("GBps")
+    if res.get("training"):
+        out["training"] = res["training"]
     if not args.no_cpu:
         out["cpu_baseline"] = run_cpu_baseline(synth.WORKLOADS[2], args.cpu_tokens)
     else:

@@ -270,12 +270,16 @@ int kmoe_seg_transpose(const void* src, int64_t ld_src, const int32_t* row_token
 
 /* Weight gradients: c_e[m, n] = sum over expert e's rows r of at[m, r] * bt[n, r]
  * (at (M, k_total), bt (N, k_total) from kmoe_seg_transpose; N a multiple of 256).
- * c: (E, M, ldc) bf16, columns < n_valid.  With c2 (dW1/dW2 split of the packed
- * order): columns of 256-column tile nt go to c (first 128) and c2 (last 128) at
- * column nt*128.  dW3 = h^T dyperm: at = h^T, bt = dyperm^T;  dW1, dW2 = x^T [dg|du]:
- * at = x^T (gathered), bt = dgu^T, c = dW1, c2 = dW2.                          */
+ * c: (E, M, ldc) bf16 (c_dtype BF16) or f32 (F32: the raw fp32 sums, e.g. split-K
+ * partials over row segments), columns < n_valid.  With c2 (bf16 only; dW1/dW2 split
+ * of the packed order): columns of 256-column tile nt go to c (first 128) and c2
+ * (last 128) at column nt*128.  dW3 = h^T dyperm: at = h^T, bt = dyperm^T;
+ * dW1, dW2 = x^T [dg|du]: at = x^T (gathered), bt = dgu^T, c = dW1, c2 = dW2.   */
 int kmoe_gemm_wgrad(const void* at, const void* bt, int64_t k_total, const int32_t* offsets, int E, int M, int N,
-                    void* c, void* c2, int64_t ldc, int n_valid, void* stream);
+                    void* c, void* c2, int c_dtype, int64_t ldc, int n_valid, void* stream);
+
+/* out[i] = sum_p partial[p][i] (p = 0 .. n_parts-1 in order, fp32), bf16 or f32 out. */
+int kmoe_reduce_f32(const float* partial, int64_t n_parts, int64_t n, void* out, int out_dtype, void* stream);
 
 /* Router logit gradient (f32, (T,E)): the top-k renormalisation's softmax-over-
  * the-selected backward, dl[i_j] += w_j (dw_j - sum_l w_l dw_l), plus the aux
@@ -297,8 +301,6 @@ int kmoe_router_mlp_bwd(const float* dlogits, const float* hidden_pre, int64_t T
 size_t kmoe_packed_w_in_t_bytes(int d);
 int kmoe_pack_w_in_t(const void* w_in, int w_dtype, int d, void* out, void* stream);
 
-/* y = a + b, n bf16 elements (n % 8 == 0), fp32 add, one rounding. */
-int kmoe_add_bf16(const void* a, const void* b, int64_t n, void* y, void* stream);
 
 #ifdef __cplusplus
 }

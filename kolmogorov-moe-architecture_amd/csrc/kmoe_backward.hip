@@ -323,23 +323,6 @@ __global__ __launch_bounds__(256) void pack_w_in_t_kernel(const void* __restrict
   }
 }
 
-// y = a + b (bf16, fp32 add, one rounding)
-__global__ __launch_bounds__(256) void add_bf16_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
-                                                       int64_t n8, uint16_t* __restrict__ y) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
-    const i32x4_t u = reinterpret_cast<const i32x4_t*>(a)[i], v = reinterpret_cast<const i32x4_t*>(b)[i];
-    i32x4_t o;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float lo = __uint_as_float(((uint32_t)u[q]) << 16) + __uint_as_float(((uint32_t)v[q]) << 16);
-      const float hi =
-          __uint_as_float(((uint32_t)u[q]) & 0xffff0000u) + __uint_as_float(((uint32_t)v[q]) & 0xffff0000u);
-      o[q] = (int)((uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16));
-    }
-    reinterpret_cast<i32x4_t*>(y)[i] = o;
-  }
-}
-
 unsigned grid_for(int64_t n, int per_block) {
   const int64_t b = kmoe::ceil_div<int64_t>(n, per_block);
   return (unsigned)(b < 65536 ? (b > 0 ? b : 1) : 65536);
@@ -463,11 +446,14 @@ extern "C" int kmoe_pack_w_in_t(const void* w_in, int w_dtype, int d, void* out,
   return kmoe::check_launch("kmoe_pack_w_in_t");
 }
 
-extern "C" int kmoe_add_bf16(const void* a, const void* b, int64_t n, void* y, void* stream) {
-  KMOE_REQUIRE(a && b && y, KMOE_ERR_NULL, "kmoe_add_bf16: null buffer");
-  KMOE_REQUIRE(n >= 0 && n % 8 == 0, KMOE_ERR_SHAPE, "kmoe_add_bf16: n=%lld must be a multiple of 8", (long long)n);
+
+extern "C" int kmoe_reduce_f32(const float* partial, int64_t n_parts, int64_t n, void* out, int out_dtype,
+                               void* stream) {
+  KMOE_REQUIRE(partial && out, KMOE_ERR_NULL, "kmoe_reduce_f32: null buffer");
+  KMOE_REQUIRE(n_parts >= 1 && n >= 0, KMOE_ERR_SHAPE, "kmoe_reduce_f32: bad shape");
+  KMOE_REQUIRE(out_dtype == KMOE_DTYPE_BF16 || out_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE, "kmoe_reduce_f32: dtype");
   if (n == 0) return KMOE_OK;
-  hipLaunchKernelGGL(add_bf16_kernel, dim3(grid_for(n / 8, 256)), dim3(256), 0, kmoe::as_stream(stream),
-                     static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), n / 8, static_cast<uint16_t*>(y));
-  return kmoe::check_launch("kmoe_add_bf16");
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(n, 256)), dim3(256), 0,
+                     kmoe::as_stream(stream), partial, n_parts, n, out, out_dtype == KMOE_DTYPE_F32);
+  return kmoe::check_launch("kmoe_reduce_f32");
 }

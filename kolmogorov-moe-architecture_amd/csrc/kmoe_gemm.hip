@@ -249,6 +249,9 @@ struct GemmArgs {
   // gate/up tiles: when set, the pre-activation gate and up values are also written
   // (bf16) in the packed column order, row stride 2*ldc: the backward's saved g, u
   uint16_t* gu_out;
+  // plain tiles: when set, the fp32 accumulators are stored here (row stride ldc)
+  // instead of bf16 to C (split-K partial sums)
+  float* Cf;
 };
 
 // One output tile: rows [m0, min(m0 + 256, m_end)) of expert e against B rows of
@@ -420,6 +423,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   // (VALU, no LDS round trip): for the rows of r = 2p and 2p+1, an even lane packs
   // its own and its right neighbour's value of row 2p, an odd lane its left
   // neighbour's and its own of row 2p+1, so every lane writes 4 bytes, unmasked.
+  if constexpr (!GATE_UP && !FP8) {
+    if (g.Cf != nullptr) {
+      // fp32 out straight from the accumulators: for each (block, r) the 32 lanes of a
+      // half-wave store 32 consecutive columns (128 bytes) of one row
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int j = 0; j < WNB; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            const int col = nt * 256 + q * (64 * WNB) + b_lds_row<false, WNB>(wn, j, lr);
+            if (row < m_end && col < g.n_valid) g.Cf[(int64_t)row * g.ldc + col] = acc[mi][j][r];
+          }
+      return;
+    }
+  }
   constexpr int NC = GATE_UP ? 32 * WNB : 64 * WNB;  // output columns of the tile
   constexpr int NJ = GATE_UP ? WNB / 2 : WNB;        // output column blocks per wave
   constexpr int OSTR = NC * 2 + 16;                  // LDS row stride (bytes)
@@ -613,9 +633,17 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   int koff, kpad;
   wgrad_segment(offsets, E, e, koff, kpad);
   GemmArgs ge = g;
-  ge.C = g.C + (int64_t)e * c_expert_stride;
+  ge.C = g.C ? g.C + (int64_t)e * c_expert_stride : nullptr;
   ge.C2 = g.C2 ? g.C2 + (int64_t)e * c_expert_stride : nullptr;
+  ge.Cf = g.Cf ? g.Cf + (int64_t)e * c_expert_stride : nullptr;
   const int m0 = mt * BM;
+  if (kpad == 0 && ge.Cf) {
+    for (int c = threadIdx.x; c < BM * 256; c += GEMM_THREADS) {
+      const int grow = m0 + c / 256, gcol = nt * 256 + c % 256;
+      if (grow < M && gcol < g.n_valid) ge.Cf[(int64_t)grow * g.ldc + gcol] = 0.0f;
+    }
+    return;
+  }
   if (kpad == 0) {
     // no rows: a zero gradient tile
     for (int c = threadIdx.x; c < BM * 32; c += GEMM_THREADS) {
@@ -763,7 +791,7 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
     kmoe::set_error("kmoe gemm: K bytes %d not a multiple of %d", kbytes, KB);
     return KMOE_ERR_SHAPE;
   }
-  GemmArgs g;
+  GemmArgs g{};  // value-initialised: every optional output (C2, gu_out, Cf) starts null
   g.A = static_cast<const uint8_t*>(A);
   g.lda_bytes = kbytes;
   g.a_scale = a_scale;
@@ -779,6 +807,7 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
   g.n_valid = n_valid;
   g.C2 = static_cast<uint16_t*>(C2);
   g.gu_out = static_cast<uint16_t*>(gu_out);
+  g.Cf = nullptr;
   // tile loads address a 2 GiB buffer window from the tile's first A / B row (from
   // the first row of A when gathering)
   if ((int64_t)(BM + 1) * g.ldb_bytes >= ((int64_t)1 << 31) ||
@@ -1067,8 +1096,10 @@ extern "C" int64_t kmoe_wgrad_k_total(int64_t n_rows, int E) {
 }
 
 extern "C" int kmoe_gemm_wgrad(const void* at, const void* bt, int64_t k_total, const int32_t* offsets, int E, int M,
-                               int N, void* c, void* c2, int64_t ldc, int n_valid, void* stream) {
+                               int N, void* c, void* c2, int c_dtype, int64_t ldc, int n_valid, void* stream) {
   KMOE_REQUIRE(at && bt && offsets && c, KMOE_ERR_NULL, "kmoe_gemm_wgrad: null buffer");
+  KMOE_REQUIRE(c_dtype == KMOE_DTYPE_BF16 || (c_dtype == KMOE_DTYPE_F32 && c2 == nullptr), KMOE_ERR_DTYPE,
+               "kmoe_gemm_wgrad: c dtype must be bf16, or f32 without c2");
   KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_gemm_wgrad: E=%d out of range", E);
   KMOE_REQUIRE(M > 0 && N > 0 && N % BN == 0, KMOE_ERR_SHAPE, "kmoe_gemm_wgrad: M=%d, N=%d (N a multiple of %d)", M,
                N, BN);
@@ -1084,8 +1115,10 @@ extern "C" int kmoe_gemm_wgrad(const void* at, const void* bt, int64_t k_total, 
   g.B = static_cast<const uint8_t*>(bt);
   g.b_expert_rows = 0;
   g.ldb_bytes = k_total * 2;
-  g.C = static_cast<uint16_t*>(c);
+  const bool f32 = c_dtype == KMOE_DTYPE_F32;
+  g.C = f32 ? nullptr : static_cast<uint16_t*>(c);
   g.C2 = static_cast<uint16_t*>(c2);
+  g.Cf = f32 ? static_cast<float*>(c) : nullptr;
   g.ldc = ldc;
   g.n_valid = n_valid;
   const int n_mt = kmoe::ceil_div(M, BM), n_nt = N / BN;

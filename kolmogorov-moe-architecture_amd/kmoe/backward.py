@@ -12,7 +12,7 @@ Data flow (A = routed rows, grouped by expert):
   dh  = dyperm . w3^T            grouped GEMM (packed w3n)
   dgu = swiglu_bwd(dh, g, u)     g, u saved by the forward's gate/up GEMM
   dxp = dgu . [w1|w2]^T          grouped GEMM (packed w13t)
-  dx  = sum_j dxp[slot(t,j)] + da . w_in        (combine with unit weights, add)
+  dx  = sum_j dxp[slot(t,j)] + (da . w_in)[t]   (one unit-weight gather of both)
   dW3 = h^T dyperm, dW1|dW2 = x^T dgu           per-expert GEMMs over transposed row segments
   dlogits = topk-renorm backward(dw) + aux backward;  da, dW_out (router MLP);  dW_in = da^T x
 """
@@ -26,6 +26,7 @@ from . import _lib, ops
 from ._lib import ptr
 
 _BF16 = torch.bfloat16
+WG_SPLIT = 512  # token rows per split-K segment of the router's weight gradient
 
 
 def _ru(a: int, b: int) -> int:
@@ -111,13 +112,12 @@ def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], 
     dgu = torch.empty(max(A, 1), 2 * Fp, device=dev, dtype=_BF16)
     with _stage("bwd_swiglu"):
         _lib.call("kmoe_swiglu_bwd", ptr(dh), ptr(sv.gu), A, ptr(disp.offsets[E:]), F, ptr(dgu), s)
-    # ---- dxperm = dgu . [w1|w2]^T, then back to tokens (unit weights)
-    dxp = torch.empty(max(A, 1), d, device=dev, dtype=_BF16)
+    # ---- dxperm = dgu . [w1|w2]^T (rows [0, A)); the router's dx contribution goes to
+    # rows [A, A + T) and one unit-weight gather sums both per token
+    dxp = torch.empty(A + T, d, device=dev, dtype=_BF16)
     with _stage("bwd_gemm_dx"):
         _lib.call("kmoe_gemm_grouped", ptr(dgu), ptr(disp.offsets), E, 2 * Fp, A, ptr(bw.w13t), _ru(d, 256), d,
                   ptr(dxp), d, d, s)
-    ones = torch.ones(T, k, device=dev, dtype=torch.float32)
-    dx_e = ops.combine(dxp, disp.slot_row.view(T, k), ones, T)
 
     # ---- router: logit gradient, MLP backward, dx contribution, dW_in
     dl = torch.empty(T, E, device=dev, dtype=torch.float32)
@@ -134,44 +134,58 @@ def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], 
         _lib.call("kmoe_router_mlp_bwd", ptr(dl), ptr(sv.hidden), T, E, ptr(w_out_b), ptr(da), ptr(dw_out),
                   _lib.DTYPE_F32 if wdt == torch.float32 else _lib.DTYPE_BF16, ptr(ws), wsb, s)
         one_seg = torch.tensor([0, T], device=dev, dtype=torch.int32)
-        dx_r = torch.empty(T, d, device=dev, dtype=_BF16)
         _lib.call("kmoe_gemm_grouped", ptr(da), ptr(one_seg), 1, _lib.ROUTER_HIDDEN, T, ptr(bw.w_in_t), _ru(d, 256),
-                  d, ptr(dx_r), d, d, s)
+                  d, ptr(dxp[A:]), d, d, s)
+    src = torch.cat([disp.slot_row.view(T, k), torch.arange(A, A + T, device=dev, dtype=torch.int32)[:, None]], 1)
     dx = torch.empty(T, d, device=dev, dtype=_BF16)
-    _lib.call("kmoe_add_bf16", ptr(dx_e), ptr(dx_r), T * d, ptr(dx), s)
+    with _stage("bwd_gather_dx"):
+        _lib.call("kmoe_combine", ptr(dxp), d, ptr(src), ptr(torch.ones(T, k + 1, device=dev)), k + 1, None, None, T,
+                  ptr(dx), _lib.DTYPE_BF16, s)
     if not need_weights:
         return Grads(dx, None, dw_out, None, None, None)
 
     # ---- weight gradients over transposed row segments
-    with _stage("bwd_wgrad"):
-        kt1 = lib.kmoe_wgrad_k_total(T, 1)
+    kt = lib.kmoe_wgrad_k_total(A, E)
+    dpad = _ru(d, 256)
+    # dW_in = da^T x: a 128 x d output (few tiles) over K = T, split into token
+    # segments of WG_SPLIT rows whose fp32 partial sums are then reduced in order
+    split = max(WG_SPLIT, _ru(-(-T // _lib.MAX_EXPERTS), 64))  # at most MAX_EXPERTS segments
+    nseg = max(1, -(-T // split))
+    segs = torch.clamp(torch.arange(nseg + 1, device=dev, dtype=torch.int32) * split, max=T).to(torch.int32)
+    kt1 = lib.kmoe_wgrad_k_total(T, nseg)
+    with _stage("bwd_transpose"):
         daT = torch.empty(_lib.ROUTER_HIDDEN, kt1, device=dev, dtype=_BF16)
-        _lib.call("kmoe_seg_transpose", ptr(da), _lib.ROUTER_HIDDEN, None, None, ptr(one_seg), 1, _lib.ROUTER_HIDDEN,
+        _lib.call("kmoe_seg_transpose", ptr(da), _lib.ROUTER_HIDDEN, None, None, ptr(segs), nseg, _lib.ROUTER_HIDDEN,
                   _lib.ROUTER_HIDDEN, ptr(daT), kt1, s)
-        dpad = _ru(d, 256)
         xT1 = torch.empty(dpad, kt1, device=dev, dtype=_BF16)
-        _lib.call("kmoe_seg_transpose", ptr(x2d), d, None, None, ptr(one_seg), 1, d, dpad, ptr(xT1), kt1, s)
-        dw_in = torch.empty(_lib.ROUTER_HIDDEN, d, device=dev, dtype=_BF16)
-        _lib.call("kmoe_gemm_wgrad", ptr(daT), ptr(xT1), kt1, ptr(one_seg), 1, _lib.ROUTER_HIDDEN, dpad, ptr(dw_in),
-                  None, d, d, s)
-        del daT, xT1
-
-        kt = lib.kmoe_wgrad_k_total(A, E)
-        dw3 = torch.empty(E, F, d, device=dev, dtype=_BF16)
+        _lib.call("kmoe_seg_transpose", ptr(x2d), d, None, None, ptr(segs), nseg, d, dpad, ptr(xT1), kt1, s)
+    dw_in = torch.empty(_lib.ROUTER_HIDDEN, d, device=dev, dtype=_BF16)
+    with _stage("bwd_wgrad_router"):
+        part = torch.empty(nseg, _lib.ROUTER_HIDDEN, d, device=dev, dtype=torch.float32)
+        _lib.call("kmoe_gemm_wgrad", ptr(daT), ptr(xT1), kt1, ptr(segs), nseg, _lib.ROUTER_HIDDEN, dpad, ptr(part),
+                  None, _lib.DTYPE_F32, d, d, s)
+        _lib.call("kmoe_reduce_f32", ptr(part), nseg, _lib.ROUTER_HIDDEN * d, ptr(dw_in), _lib.DTYPE_BF16, s)
+    del daT, xT1, part
+    with _stage("bwd_transpose"):
         hT = torch.empty(Fp, kt, device=dev, dtype=_BF16)
         _lib.call("kmoe_seg_transpose", ptr(sv.h), Fp, None, None, ptr(disp.offsets), E, Fp, Fp, ptr(hT), kt, s)
         dyT = torch.empty(dpad, kt, device=dev, dtype=_BF16)
         _lib.call("kmoe_seg_transpose", ptr(dyperm), d, None, None, ptr(disp.offsets), E, d, dpad, ptr(dyT), kt, s)
-        _lib.call("kmoe_gemm_wgrad", ptr(hT), ptr(dyT), kt, ptr(disp.offsets), E, F, dpad, ptr(dw3), None, d, d, s)
-        del hT, dyT
-        dw1 = torch.empty(E, d, F, device=dev, dtype=_BF16)
-        dw2 = torch.empty(E, d, F, device=dev, dtype=_BF16)
+    dw3 = torch.empty(E, F, d, device=dev, dtype=_BF16)
+    with _stage("bwd_wgrad_w3"):
+        _lib.call("kmoe_gemm_wgrad", ptr(hT), ptr(dyT), kt, ptr(disp.offsets), E, F, dpad, ptr(dw3), None,
+                  _lib.DTYPE_BF16, d, d, s)
+    del hT, dyT
+    with _stage("bwd_transpose"):
         xT = torch.empty(d, kt, device=dev, dtype=_BF16)
         _lib.call("kmoe_seg_transpose", ptr(x2d), d, ptr(disp.row_token), None, ptr(disp.offsets), E, d, d, ptr(xT),
                   kt, s)
         dguT = torch.empty(2 * Fp, kt, device=dev, dtype=_BF16)
         _lib.call("kmoe_seg_transpose", ptr(dgu), 2 * Fp, None, None, ptr(disp.offsets), E, 2 * Fp, 2 * Fp, ptr(dguT),
                   kt, s)
-        _lib.call("kmoe_gemm_wgrad", ptr(xT), ptr(dguT), kt, ptr(disp.offsets), E, d, 2 * Fp, ptr(dw1), ptr(dw2), F,
-                  F, s)
+    dw1 = torch.empty(E, d, F, device=dev, dtype=_BF16)
+    dw2 = torch.empty(E, d, F, device=dev, dtype=_BF16)
+    with _stage("bwd_wgrad_w13"):
+        _lib.call("kmoe_gemm_wgrad", ptr(xT), ptr(dguT), kt, ptr(disp.offsets), E, d, 2 * Fp, ptr(dw1), ptr(dw2),
+                  _lib.DTYPE_BF16, F, F, s)
     return Grads(dx, dw_in, dw_out, dw1, dw2, dw3)

@@ -182,3 +182,99 @@ def test_backward_deterministic(dev):
         grads.append([xx.grad.clone()] + [p.grad.clone() for p in layer.parameters()])
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+def test_backward_full_size(dev):
+    """Config-2 shape (T=16384, d=2048, E=16, top-2, F=2816): dx on 64 sampled tokens
+    against an fp64 per-token restatement (aux terms with the global counts and T),
+    dW_out against fp64 from the saved router tensors, dW3 / dW1 of the smallest expert
+    on sampled columns / rows against fp64 of the saved h, g/u and the weighted dy
+    rows; a second backward over the same saved forward is bit-identical."""
+    from kmoe import backward as BW
+    wl = synth.WORKLOADS[2]
+    t = synth.make_tensors(wl, "cpu")
+    layer = synth.build_layer(wl, dev, {kk: v.to(dev) for kk, v in t.items()}).train()
+    T, d, E, k, F = wl.T, wl.d, wl.E, wl.k, wl.F
+    x2d = t["x"].reshape(T, d).to(dev)
+    g = torch.Generator().manual_seed(77)
+    dy = torch.randn(T, d, generator=g).to(torch.bfloat16)
+    w_out = layer.router.router[2].weight
+    wlb, wz = layer.load_balance_loss_weight, layer.router_z_loss_weight
+    with torch.no_grad():
+        _, _, sv = layer._train_forward(x2d, T, torch.bfloat16)
+        ga = torch.ones((), device=dev)
+        bw = layer._bwd_weights()
+        g1 = BW.moe_backward(sv, dy.to(dev), ga, w_out, bw, E, F, wlb, wz)
+        g2 = BW.moe_backward(sv, dy.to(dev), ga, w_out, bw, E, F, wlb, wz)
+    torch.cuda.synchronize()
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+    for a in g1:
+        assert torch.isfinite(a.float()).all()
+    cpu = lambda z: z.detach().cpu()
+    idx, counts = cpu(sv.idx), cpu(sv.disp.counts).double()
+    f = counts / (T * k)
+    W = {n: cpu(p).double() for n, p in (("w_in", layer.router.router[0].weight), ("w_out", w_out))}
+    ge = layer.grouped_experts
+
+    # 1) dx on a token sample: the gradient w.r.t. x_S of the loss restricted to S
+    S = torch.randperm(T, generator=g)[:64]
+    xs = cpu(x2d)[S].double().requires_grad_(True)
+    logits = torch.nn.functional.silu(xs @ W["w_in"].T) @ W["w_out"].T
+    p = torch.softmax(logits, -1)
+    ids = idx[S]
+    v = p.gather(1, ids)
+    wsel = v / v.sum(1, keepdim=True)
+    y = torch.zeros_like(xs)
+    for e in torch.unique(ids).tolist():
+        w1, w2, w3 = (cpu(w[e]).double() for w in (ge.w1, ge.w2, ge.w3))
+        rr, jj = torch.nonzero(ids == e, as_tuple=True)
+        h = torch.nn.functional.silu(xs[rr] @ w1) * (xs[rr] @ w2)
+        y = y.index_add(0, rr, wsel[rr, jj, None] * (h @ w3))
+    loss = (y * dy[S].double()).sum()
+    loss = loss + wlb * E * (f * p.sum(0) / T).sum() + wz * (torch.logsumexp(logits, -1) ** 2).sum() / T
+    loss.backward()
+    e_dx = _rel(cpu(g1.dx)[S], xs.grad)
+
+    # 2) dW_out over all tokens from the saved router tensors (fp64)
+    slot_row, slot_w = cpu(sv.disp.slot_row).long(), cpu(sv.disp.slot_w).double()
+    yp = cpu(sv.yperm).double()
+    dyd = dy.double()
+    dw = (dyd.repeat_interleave(k, 0) * yp[slot_row.clamp(min=0)]).sum(1) * (slot_row >= 0)
+    dw = dw.view(T, k)
+    wk = cpu(sv.w).double()
+    dl = torch.zeros(T, E, dtype=torch.float64)
+    dl.scatter_add_(1, idx, wk * (dw - (wk * dw).sum(1, keepdim=True)))
+    lg = cpu(sv.logits).double()
+    pp = torch.softmax(lg, -1)
+    lse = torch.logsumexp(lg, -1, keepdim=True)
+    dl += wlb * E / T * pp * (f - (pp * f).sum(1, keepdim=True)) + wz * 2.0 / T * lse * pp
+    s_act = torch.nn.functional.silu(cpu(sv.hidden).double())
+    e_dwout = _rel(cpu(g1.dw_out), dl.T @ s_act)
+
+    # 3) dW3 / dW1 of the smallest expert on sampled columns / rows
+    offs = cpu(sv.disp.offsets).long()
+    e = int(torch.argmin(offs[1:] - offs[:-1]))
+    lo, hi = int(offs[e]), int(offs[e + 1])
+    wr = torch.zeros(T * k, dtype=torch.float64)
+    keep = slot_row >= 0
+    wr[slot_row[keep]] = slot_w[keep]
+    tok = cpu(sv.disp.row_token).long()[lo:hi]
+    dY = wr[lo:hi, None] * dyd[tok]                      # weighted dy rows of the expert
+    Fp = (F + 127) // 128 * 128
+    h = cpu(sv.h)[lo:hi, :F].double()
+    cols = torch.randperm(d, generator=g)[:16]
+    e_dw3 = _rel(cpu(g1.dw3[e])[:, cols], h.T @ dY[:, cols])
+    gu = cpu(sv.gu)[lo:hi].double()
+    fcol = torch.arange(F)
+    gc = (fcol // 128) * 256 + fcol % 128
+    gg, uu = gu[:, gc], gu[:, gc + 128]
+    dh = dY @ cpu(ge.w3[e]).double().T
+    sg = torch.sigmoid(gg)
+    dg = dh * uu * sg * (1 + gg * (1 - sg))
+    rows_i = torch.randperm(d, generator=g)[:16]
+    xe = cpu(x2d)[tok].double()
+    e_dw1 = _rel(cpu(g1.dw1[e])[rows_i], xe[:, rows_i].T @ dg)
+    errs = {"dx_sample": e_dx, "dw_out": e_dwout, "dw3_e": e_dw3, "dw1_e": e_dw1}
+    print("full-size rel-L2:", {n: f"{v:.2e}" for n, v in errs.items()}, "expert", e, "rows", hi - lo)
+    assert e_dx <= 1e-2 and e_dw3 <= 1e-2 and e_dw1 <= 1e-2 and e_dwout <= 2e-2, errs
