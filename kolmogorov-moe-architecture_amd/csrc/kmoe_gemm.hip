@@ -254,13 +254,18 @@ struct GemmArgs {
   float* Cf;
 };
 
+// Output of a plain (non gate/up) tile: bf16 to C; bf16 with the column tile split
+// between C and C2 (the gate and up halves of a w13-ordered tile); fp32 to Cf.
+// Compile-time, so that the forward kernels carry none of the other epilogues.
+constexpr int OUT_BF16 = 0, OUT_SPLIT = 1, OUT_F32 = 2;
+
 // One output tile: rows [m0, min(m0 + 256, m_end)) of expert e against B rows of
 // full column tile nt (narrow part q when WNB < 4).
 // FP8: A/B bytes are e4m3; a_scale per A row, b_scale per B row (global row index).
 // GATHER: A is the unpermuted activation matrix and permuted row r is its row
 // row_index[row_token[r]] (row_token[r] without row_index): the dispatch gather is
 // fused into the A loads.
-template <bool GATE_UP, bool FP8, bool GATHER, int WNB>
+template <bool GATE_UP, bool FP8, bool GATHER, int WNB, int OUT = OUT_BF16, bool SAVE_GU = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e, int m0, int m_end, int nt,
                                           int q) {
   static_assert(WNB == 4 || WNB == 2 || (WNB == 1 && !GATE_UP), "tile width");
@@ -423,22 +428,22 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   // (VALU, no LDS round trip): for the rows of r = 2p and 2p+1, an even lane packs
   // its own and its right neighbour's value of row 2p, an odd lane its left
   // neighbour's and its own of row 2p+1, so every lane writes 4 bytes, unmasked.
-  if constexpr (!GATE_UP && !FP8) {
-    if (g.Cf != nullptr) {
-      // fp32 out straight from the accumulators: for each (block, r) the 32 lanes of a
-      // half-wave store 32 consecutive columns (128 bytes) of one row
+  static_assert(OUT == OUT_BF16 || (!GATE_UP && !FP8), "split / fp32 outputs are for bf16 plain tiles");
+  static_assert(!SAVE_GU || (GATE_UP && !FP8), "g/u saving is for bf16 gate/up tiles");
+  if constexpr (OUT == OUT_F32) {
+    // fp32 out straight from the accumulators: for each (block, r) the 32 lanes of a
+    // half-wave store 32 consecutive columns (128 bytes) of one row
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int j = 0; j < WNB; ++j)
+      for (int j = 0; j < WNB; ++j)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            const int col = nt * 256 + q * (64 * WNB) + b_lds_row<false, WNB>(wn, j, lr);
-            if (row < m_end && col < g.n_valid) g.Cf[(int64_t)row * g.ldc + col] = acc[mi][j][r];
-          }
-      return;
-    }
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          const int col = nt * 256 + q * (64 * WNB) + b_lds_row<false, WNB>(wn, j, lr);
+          if (row < m_end && col < g.n_valid) g.Cf[(int64_t)row * g.ldc + col] = acc[mi][j][r];
+        }
+    return;
   }
   constexpr int NC = GATE_UP ? 32 * WNB : 64 * WNB;  // output columns of the tile
   constexpr int NJ = GATE_UP ? WNB / 2 : WNB;        // output column blocks per wave
@@ -496,13 +501,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   __syncthreads();
   constexpr int OCPR = NC * 2 / 16;  // 16-byte chunks per output row
   const int col0 = (GATE_UP ? nt * 128 : nt * 256) + q * NC;
-  const bool split_c = !GATE_UP && g.C2 != nullptr;
+  constexpr bool split_c = OUT == OUT_SPLIT;
   for (int c = tid; c < BM * OCPR; c += GEMM_THREADS) {
     const int trow = c / OCPR, ch = c % OCPR;
     const int grow = m0 + trow;
     uint16_t* dst = g.C;
     int gcol = col0 + ch * 8;
-    if (split_c) {
+    if constexpr (split_c) {
       const int cf = q * NC + ch * 8;  // column within the full tile
       dst = cf < 128 ? g.C : g.C2;
       gcol = nt * 128 + (cf & 127);
@@ -514,40 +519,38 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
 
   // training forward: the pre-activation gate and up values of the tile, bf16, in the
   // packed column order (row stride 2*ldc), for the SwiGLU backward
-  if constexpr (GATE_UP && !FP8) {
-    if (g.gu_out != nullptr) {
-      constexpr int NC2 = 64 * WNB;
-      constexpr int OSTR2 = NC2 * 2 + 16;
-      __syncthreads();
-      uint8_t* const wb2 = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR2 + (lr - (odd ? 1 : 0)) * 2;
+  if constexpr (SAVE_GU) {
+    constexpr int NC2 = 64 * WNB;
+    constexpr int OSTR2 = NC2 * 2 + 16;
+    __syncthreads();
+    uint8_t* const wb2 = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR2 + (lr - (odd ? 1 : 0)) * 2;
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) {
+    for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
+      for (int p = 0; p < 8; ++p) {
 #pragma unroll
-          for (int j = 0; j < WNB; ++j) {
-            const float a = acc[mi][j][2 * p], b = acc[mi][j][2 * p + 1];
-            const float a_next = __builtin_bit_cast(
-                float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, a), 0x101, 0xf, 0xf, false));
-            const float b_prev = __builtin_bit_cast(
-                float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, b), 0x111, 0xf, 0xf, false));
-            const float lo = odd ? b_prev : a, hi = odd ? b : a_next;
-            const uint32_t packed = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
-            const int col = b_lds_row<true, WNB>(wn, j, 0);
-            *reinterpret_cast<uint32_t*>(wb2 + (mi * 32 + 8 * (p >> 1) + 2 * (p & 1)) * OSTR2 + col * 2) = packed;
-          }
+        for (int j = 0; j < WNB; ++j) {
+          const float a = acc[mi][j][2 * p], b = acc[mi][j][2 * p + 1];
+          const float a_next = __builtin_bit_cast(
+              float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, a), 0x101, 0xf, 0xf, false));
+          const float b_prev = __builtin_bit_cast(
+              float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, b), 0x111, 0xf, 0xf, false));
+          const float lo = odd ? b_prev : a, hi = odd ? b : a_next;
+          const uint32_t packed = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+          const int col = b_lds_row<true, WNB>(wn, j, 0);
+          *reinterpret_cast<uint32_t*>(wb2 + (mi * 32 + 8 * (p >> 1) + 2 * (p & 1)) * OSTR2 + col * 2) = packed;
         }
       }
-      __syncthreads();
-      constexpr int OCPR2 = NC2 * 2 / 16;
-      for (int c = tid; c < BM * OCPR2; c += GEMM_THREADS) {
-        const int trow = c / OCPR2, ch = c % OCPR2;
-        const int grow = m0 + trow;
-        const int gcol = nt * 256 + b_packed_row<true, WNB>(ch * 8, q);
-        if (grow < m_end)
-          *reinterpret_cast<i32x4_t*>(g.gu_out + (int64_t)grow * 2 * g.ldc + gcol) =
-              *reinterpret_cast<const i32x4_t*>(lds + trow * OSTR2 + ch * 16);
-      }
+    }
+    __syncthreads();
+    constexpr int OCPR2 = NC2 * 2 / 16;
+    for (int c = tid; c < BM * OCPR2; c += GEMM_THREADS) {
+      const int trow = c / OCPR2, ch = c % OCPR2;
+      const int grow = m0 + trow;
+      const int gcol = nt * 256 + b_packed_row<true, WNB>(ch * 8, q);
+      if (grow < m_end)
+        *reinterpret_cast<i32x4_t*>(g.gu_out + (int64_t)grow * 2 * g.ldc + gcol) =
+            *reinterpret_cast<const i32x4_t*>(lds + trow * OSTR2 + ch * 16);
     }
   }
 }
@@ -560,7 +563,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
 // of 1/split of its columns (the full K), which all run at once.  A narrow tile
 // computes every output element with the same MFMA sequence as the full tile, so
 // the results are identical.  split = 1 keeps the tail tiles whole.
-template <bool GATE_UP, bool FP8, bool GATHER>
+template <bool GATE_UP, bool FP8, bool GATHER, bool SAVE_GU = false>
 __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_kernel(
     GemmArgs g, const int32_t* __restrict__ offsets, int E, int n_tiles, int n_cu, int allow_split) {
   static_assert(!(GATHER && FP8), "the fp8 path reads rows quantised by the dispatch");
@@ -592,11 +595,11 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   dense_tile(t, st.n_slots, n_tiles, slot, nt);
   find_slot(st, E, slot, e, m0, m_end);
   if (L < base || split == 1)
-    gemm_tile<GATE_UP, FP8, GATHER, 4>(g, lds, e, m0, m_end, nt, 0);
+    gemm_tile<GATE_UP, FP8, GATHER, 4, OUT_BF16, SAVE_GU>(g, lds, e, m0, m_end, nt, 0);
   else if (split == 2)
-    gemm_tile<GATE_UP, FP8, GATHER, 2>(g, lds, e, m0, m_end, nt, q);
+    gemm_tile<GATE_UP, FP8, GATHER, 2, OUT_BF16, SAVE_GU>(g, lds, e, m0, m_end, nt, q);
   else if constexpr (!GATE_UP)
-    gemm_tile<GATE_UP, FP8, GATHER, 1>(g, lds, e, m0, m_end, nt, q);
+    gemm_tile<GATE_UP, FP8, GATHER, 1, OUT_BF16, SAVE_GU>(g, lds, e, m0, m_end, nt, q);
 }
 
 // ---------------------------------------------------------------- weight gradients
@@ -620,6 +623,7 @@ __device__ __forceinline__ void wgrad_segment(const int32_t* __restrict__ offset
 // number of rows).  Workgroup -> (expert, row tile, column tile); the tile itself is
 // gemm_tile on the expert's K range (At rows are the output rows, Bt rows the output
 // columns, both K-contiguous).  An expert without rows writes a zero tile.
+template <int OUT>
 __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void wgrad_kernel(
     GemmArgs g, const int32_t* __restrict__ offsets, int E, int M, int n_mt, int n_nt, int64_t c_expert_stride) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[GEMM_LDS];
@@ -637,7 +641,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   ge.C2 = g.C2 ? g.C2 + (int64_t)e * c_expert_stride : nullptr;
   ge.Cf = g.Cf ? g.Cf + (int64_t)e * c_expert_stride : nullptr;
   const int m0 = mt * BM;
-  if (kpad == 0 && ge.Cf) {
+  if (kpad == 0 && OUT == OUT_F32) {
     for (int c = threadIdx.x; c < BM * 256; c += GEMM_THREADS) {
       const int grow = m0 + c / 256, gcol = nt * 256 + c % 256;
       if (grow < M && gcol < g.n_valid) ge.Cf[(int64_t)grow * g.ldc + gcol] = 0.0f;
@@ -651,7 +655,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
       const int grow = m0 + trow;
       uint16_t* dst = ge.C;
       int gcol = nt * 256 + ch * 8;
-      if (ge.C2) {
+      if (OUT == OUT_SPLIT) {
         dst = ch < 16 ? ge.C : ge.C2;
         gcol = nt * 128 + (ch & 15) * 8;
       }
@@ -663,7 +667,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   ge.A = g.A + (int64_t)koff * 2;
   ge.B = g.B + (int64_t)koff * 2;
   ge.k_bytes = kpad * 2;
-  gemm_tile<false, false, false, 4>(ge, lds, 0, m0, M, nt, 0);
+  gemm_tile<false, false, false, 4, OUT>(ge, lds, 0, m0, M, nt, 0);
 }
 
 // ---------------------------------------------------------------- weight packing
@@ -821,7 +825,10 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
 #define KMOE_LAUNCH_GEMM(GU, F8, GA)                                                                         \
   hipLaunchKernelGGL((grouped_gemm_kernel<GU, F8, GA>), grid, block, 0, s, g, offsets, E, n_tiles, n_cu, \
                      allow_split)
-  if (row_token)
+  if (row_token && gu_out)
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, false, true, true>), grid, block, 0, s, g, offsets, E, n_tiles,
+                       n_cu, allow_split);
+  else if (row_token)
     KMOE_LAUNCH_GEMM(true, false, true);
   else if (gate_up && !fp8)
     KMOE_LAUNCH_GEMM(true, false, false);
@@ -1123,7 +1130,14 @@ extern "C" int kmoe_gemm_wgrad(const void* at, const void* bt, int64_t k_total, 
   g.n_valid = n_valid;
   const int n_mt = kmoe::ceil_div(M, BM), n_nt = N / BN;
   const int64_t blocks = (int64_t)E * n_mt * n_nt;
-  hipLaunchKernelGGL(wgrad_kernel, dim3((unsigned)blocks), dim3(GEMM_THREADS), 0, kmoe::as_stream(stream), g, offsets,
-                     E, M, n_mt, n_nt, (int64_t)M * ldc);
+  const dim3 grid((unsigned)blocks), block(GEMM_THREADS);
+  hipStream_t s = kmoe::as_stream(stream);
+  const int64_t stride = (int64_t)M * ldc;
+  if (f32)
+    hipLaunchKernelGGL(wgrad_kernel<OUT_F32>, grid, block, 0, s, g, offsets, E, M, n_mt, n_nt, stride);
+  else if (c2)
+    hipLaunchKernelGGL(wgrad_kernel<OUT_SPLIT>, grid, block, 0, s, g, offsets, E, M, n_mt, n_nt, stride);
+  else
+    hipLaunchKernelGGL(wgrad_kernel<OUT_BF16>, grid, block, 0, s, g, offsets, E, M, n_mt, n_nt, stride);
   return kmoe::check_launch("kmoe_gemm_wgrad");
 }
