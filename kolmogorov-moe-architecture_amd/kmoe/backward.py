@@ -84,6 +84,30 @@ def _stage(name):
     return ops._Stage(name)
 
 
+_INDEX_CACHE: dict = {}
+
+
+def _index_tensors(T: int, k: int, dev):
+    """Small constant index tensors of a backward of T tokens (cached per shape and
+    device, so that a step makes no host-to-device copies): the one-segment offsets
+    [0, T], the split-K token segments of the router weight gradient, the unit
+    weights and the router-row column of the dx gather."""
+    key = (T, k, str(dev))
+    hit = _INDEX_CACHE.get(key)
+    if hit is None:
+        split = max(WG_SPLIT, _ru(-(-T // _lib.MAX_EXPERTS), 64))  # at most MAX_EXPERTS segments
+        nseg = max(1, -(-T // split))
+        segs = torch.clamp(torch.arange(nseg + 1, dtype=torch.int64) * split, max=T).to(torch.int32).to(dev)
+        one_seg = torch.tensor([0, T], dtype=torch.int32).to(dev)
+        ones = torch.ones(T, k + 1, device=dev, dtype=torch.float32)
+        extra = torch.arange(T * k, T * k + T, dtype=torch.int32).to(dev)[:, None]
+        hit = (one_seg, segs, nseg, ones, extra)
+        if len(_INDEX_CACHE) > 16:
+            _INDEX_CACHE.clear()
+        _INDEX_CACHE[key] = hit
+    return hit
+
+
 def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], w_out: torch.Tensor,
                  bw: BwdWeights, E: int, F: int, w_lb: float, w_z: float, need_weights: bool = True) -> Grads:
     """All gradients of one token-choice MoE layer forward (bf16 compute)."""
@@ -97,6 +121,7 @@ def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], 
     s = ops._stream(x2d)
     disp = sv.disp
     dy = dy.reshape(T, d).to(_BF16).contiguous()
+    one_seg, segs, nseg, ones, extra = _index_tensors(T, k, dev)
 
     # ---- combine backward: dyperm, dw
     dyperm = torch.empty(max(A, 1), d, device=dev, dtype=_BF16)
@@ -133,14 +158,12 @@ def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], 
         w_out_b = w_out.detach().to(_BF16).contiguous()
         _lib.call("kmoe_router_mlp_bwd", ptr(dl), ptr(sv.hidden), T, E, ptr(w_out_b), ptr(da), ptr(dw_out),
                   _lib.DTYPE_F32 if wdt == torch.float32 else _lib.DTYPE_BF16, ptr(ws), wsb, s)
-        one_seg = torch.tensor([0, T], device=dev, dtype=torch.int32)
         _lib.call("kmoe_gemm_grouped", ptr(da), ptr(one_seg), 1, _lib.ROUTER_HIDDEN, T, ptr(bw.w_in_t), _ru(d, 256),
                   d, ptr(dxp[A:]), d, d, s)
-    src = torch.cat([disp.slot_row.view(T, k), torch.arange(A, A + T, device=dev, dtype=torch.int32)[:, None]], 1)
+    src = torch.cat([disp.slot_row.view(T, k), extra], 1)
     dx = torch.empty(T, d, device=dev, dtype=_BF16)
     with _stage("bwd_gather_dx"):
-        _lib.call("kmoe_combine", ptr(dxp), d, ptr(src), ptr(torch.ones(T, k + 1, device=dev)), k + 1, None, None, T,
-                  ptr(dx), _lib.DTYPE_BF16, s)
+        _lib.call("kmoe_combine", ptr(dxp), d, ptr(src), ptr(ones), k + 1, None, None, T, ptr(dx), _lib.DTYPE_BF16, s)
     if not need_weights:
         return Grads(dx, None, dw_out, None, None, None)
 
@@ -149,9 +172,6 @@ def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], 
     dpad = _ru(d, 256)
     # dW_in = da^T x: a 128 x d output (few tiles) over K = T, split into token
     # segments of WG_SPLIT rows whose fp32 partial sums are then reduced in order
-    split = max(WG_SPLIT, _ru(-(-T // _lib.MAX_EXPERTS), 64))  # at most MAX_EXPERTS segments
-    nseg = max(1, -(-T // split))
-    segs = torch.clamp(torch.arange(nseg + 1, device=dev, dtype=torch.int32) * split, max=T).to(torch.int32)
     kt1 = lib.kmoe_wgrad_k_total(T, nseg)
     with _stage("bwd_transpose"):
         daT = torch.empty(_lib.ROUTER_HIDDEN, kt1, device=dev, dtype=_BF16)
