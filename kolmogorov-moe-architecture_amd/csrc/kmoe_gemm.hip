@@ -631,9 +631,13 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   const int L = blockIdx.x;
   if (L >= n_all) return;
   const int t = (n_all % (NXCD * SB_TILES)) == 0 ? xcd_tile(L) : L;
+  // within an expert, row tiles in groups of 4 walked column tile by column tile (the
+  // forward's dense order): the 32 tiles an XCD takes at a time share 4 At and 8 Bt
+  // K-slices in its L2 (row-major order shared ~2 and ~22: 5x the operand fetch)
   const int per_e = n_mt * n_nt;
   const int e = t / per_e, rem = t - e * per_e;
-  const int mt = rem / n_nt, nt = rem - mt * n_nt;
+  int mt, nt;
+  dense_tile(rem, n_mt, n_nt, mt, nt);
   int koff, kpad;
   wgrad_segment(offsets, E, e, koff, kpad);
   GemmArgs ge = g;
