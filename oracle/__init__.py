@@ -23,5 +23,7 @@ Pinning (how each oracle function is checked independently, tests/test_oracle.py
   f32_to_e4m3        torch.float8_e4m3fn cast (library routine) on saturated inputs,
                      exhaustively over every code and every rounding midpoint
   torch_port vs moe_oracle at small shapes (two independent restatements)
+  moe_loss_tc_routed forward = torch_port.moe_layer_tc at its own routing; its
+                     autograd gradients = finite differences (gradcheck, fp64)
 No function is left unpinned.
 """

@@ -98,6 +98,52 @@ def moe_layer_tc(x3d, w_in, w_out, w1, w2, w3, k, training=True):
     return y.view(B, S, d), aux
 
 
+def moe_loss_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, dy, capacity=0, bias=None, training=True, w_lb=0.01,
+                       w_z=0.001):
+    """Scalar loss sum(y * dy) (+ aux in training) of MoELayer's token-choice forward with
+    the routing fixed to `idx` (T, k): Router.forward's logits / softmax and its top-k
+    values gathered at idx and renormalised (moe.py:423-462), GroupedExperts.forward's
+    stable-argsort / padded-bmm / index_add_ experts (moe.py:213-294), the load-balance
+    and z losses with one-hot counts of idx (moe.py:840-939).  For autograd: at a fixed
+    routing the layer is smooth, so the gradients of this loss are the reference's
+    backward.  capacity > 0 keeps the first `capacity` assignments of each expert in
+    assignment order (the build's drop rule); bias (E,) is added to the logits."""
+    T, d = x2d.shape
+    k = idx.shape[1]
+    E = w1.shape[0]
+    logits = F.linear(F.silu(F.linear(x2d, w_in)), w_out)
+    if bias is not None:
+        logits = logits + bias
+    probs = F.softmax(logits, dim=-1)
+    v = probs.gather(1, idx)
+    w = v / v.sum(dim=-1, keepdim=True)
+    flat_e = idx.reshape(-1)
+    tok = torch.arange(T).unsqueeze(1).expand(-1, k).reshape(-1)
+    order = torch.argsort(flat_e, stable=True)
+    s_tok, s_e, s_w = tok[order], flat_e[order], w.reshape(-1)[order]
+    counts = torch.bincount(flat_e, minlength=E)
+    starts = torch.cumsum(counts, 0) - counts
+    pos = torch.arange(s_tok.numel()) - starts[s_e]
+    if capacity > 0:
+        keep = pos < capacity
+        s_tok, s_e, s_w, pos = s_tok[keep], s_e[keep], s_w[keep], pos[keep]
+    y = x2d.new_zeros(x2d.shape)
+    if s_tok.numel():
+        m = int(pos.max().item()) + 1
+        padded = x2d.new_zeros(E, m, d)
+        padded = padded.index_put((s_e, pos), x2d[s_tok])
+        h = F.silu(torch.bmm(padded, w1)) * torch.bmm(padded, w2)
+        out = torch.bmm(h, w3)
+        y = y.index_add(0, s_tok, out[s_e, pos] * s_w.unsqueeze(1))
+    loss = (y * dy).sum()
+    if training:
+        f = counts.to(x2d.dtype) / (T * k)
+        lb = E * (f * probs.mean(dim=0)).sum()
+        z = (torch.logsumexp(logits, dim=-1) ** 2).mean()
+        loss = loss + w_lb * lb + w_z * z
+    return loss
+
+
 def moe_layer_ec(x3d, w_in, w_out, w1, w2, w3, cf):
     """MoELayer expert-choice forward (moe.py:815-838) without torch.compile."""
     B, S, d = x3d.shape

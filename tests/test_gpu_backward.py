@@ -1,8 +1,9 @@
 """Backward pass of the token-choice MoE layer on the HIP kernels vs autograd of
-an fp64 CPU restatement of the reference forward (moe.py:423-462 router,
-moe.py:213-294 experts + combine, moe.py:840-939 aux losses; SwiGLU ffn.py:17-64),
-fed the kernel's own routing (the selection is pinned bit-exactly by the forward
-tests) and the bf16 values of the inputs and parameters.
+the oracle's fp64 restatement of the reference forward at a fixed routing
+(oracle/torch_port.moe_loss_tc_routed: moe.py:423-462 router, moe.py:213-294
+experts + combine, moe.py:840-939 aux losses; pinned on the CPU by
+tests/test_oracle.py), fed the kernel's own routing (the selection is pinned
+bit-exactly by the forward tests) and the bf16 values of the inputs and parameters.
 
 Tolerance: rel-L2 <= 1e-2 for dx and the expert weight gradients, 2e-2 for the
 router weight gradients (bf16 intermediates: the permuted dy rows, dh, dg/du, the
@@ -14,6 +15,7 @@ import torch
 
 import kmoe  # noqa: F401
 from kmoe import synth
+from oracle import torch_port as P
 from kmoe.config import AdvancedMoEConfig
 from kmoe.moe import MoELayer
 
@@ -25,37 +27,6 @@ def dev():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda:0")
-
-
-def _ref_loss(x, w_in, w_out, w1, w2, w3, idx, dy, E, k, cap, w_lb, w_z, bias, train):
-    """fp64 restatement of the reference forward + the loss sum(y * dy) (+ aux)."""
-    T = x.shape[0]
-    a = x @ w_in.T
-    logits = torch.nn.functional.silu(a) @ w_out.T
-    if bias is not None:
-        logits = logits + bias
-    p = torch.softmax(logits, -1)
-    v = p.gather(1, idx)
-    w = v / v.sum(1, keepdim=True)
-    y = torch.zeros_like(x)
-    flat = idx.reshape(-1)
-    for e in range(E):
-        a_idx = torch.nonzero(flat == e).reshape(-1)  # assignment order = token order
-        if cap > 0:
-            a_idx = a_idx[:cap]
-        if a_idx.numel() == 0:
-            continue
-        t, j = a_idx // k, a_idx % k
-        rows = x[t]
-        h = torch.nn.functional.silu(rows @ w1[e]) * (rows @ w2[e])
-        y = y.index_add(0, t, w[t, j, None] * (h @ w3[e]))
-    loss = (y * dy).sum()
-    if train:
-        counts = torch.bincount(flat, minlength=E).double()
-        lb = E * ((counts / (T * k)) * p.mean(0)).sum()
-        z = (torch.logsumexp(logits, -1) ** 2).mean()
-        loss = loss + w_lb * lb + w_z * z
-    return loss
 
 
 def _rel(a, b):
@@ -102,8 +73,8 @@ def _run(dev, B, S, d, E, k, F, seed, drop_cf=None, train=True, zipf=False, empt
     xr = f64(x.reshape(B * S, d))
     cap = int(np.ceil(drop_cf * B * S * k / E)) if drop_cf is not None else 0
     bias = None if layer.router.logit_bias is None else layer.router.logit_bias.double().cpu()
-    ref = _ref_loss(xr, *params, idx, dy.reshape(B * S, d).double(), E, k, cap,
-                    layer.load_balance_loss_weight, layer.router_z_loss_weight, bias, train)
+    ref = P.moe_loss_tc_routed(xr, *params, idx, dy.reshape(B * S, d).double(), capacity=cap, bias=bias,
+                               training=train, w_lb=layer.load_balance_loss_weight, w_z=layer.router_z_loss_weight)
     ref.backward()
     got = [x.grad.reshape(B * S, d), layer.router.router[0].weight.grad, layer.router.router[2].weight.grad,
            ge.w1.grad, ge.w2.grad, ge.w3.grad]

@@ -382,3 +382,39 @@ def test_golden_fixture_cfg1():
 def test_golden_fixture_e4m3():
     g = np.load(os.path.join(GOLDEN, "e4m3_kat.npz"))
     assert np.array_equal(O.f32_to_e4m3(g["inputs"]), g["codes"])
+
+
+# ---------------------------------------------------------------- backward oracle
+def _tiny_layer(seed, T=6, d=4, E=3, k=2, F_=5, scale=0.5):
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda *s: (torch.randn(*s, generator=g, dtype=torch.float64) * scale).requires_grad_(True)
+    return (mk(T, d), mk(128, d), mk(E, 128), mk(E, d, F_), mk(E, d, F_), mk(E, F_, d),
+            torch.randn(T, d, generator=g, dtype=torch.float64))
+
+
+def test_routed_loss_matches_port_forward():
+    """At the port's own top-k routing, the routed loss equals sum(y * dy) + aux of
+    torch_port.moe_layer_tc (two restatements of moe.py:213-294, 423-462, 840-939)."""
+    x, w_in, w_out, w1, w2, w3, dy = _tiny_layer(1, T=40, d=16, E=5, k=2, F_=12)
+    with torch.no_grad():
+        y, aux = P.moe_layer_tc(x[None], w_in, w_out, w1, w2, w3, 2, training=True)
+        _, idx, _ = P.router_tc(x[None], w_in, w_out, 2)
+        got_y = P.moe_loss_tc_routed(x, w_in, w_out, w1, w2, w3, idx[0], dy, training=False)
+        got = P.moe_loss_tc_routed(x, w_in, w_out, w1, w2, w3, idx[0], dy)
+    assert got_y == (y[0] * dy).sum()  # same ops, same order
+    # the port forms its one-hot counts in float32 (as the reference's .float() does)
+    assert abs(float(got - ((y[0] * dy).sum() + aux))) <= 1e-9
+
+
+@pytest.mark.parametrize("cap,training,bias", [(0, True, False), (3, True, True), (0, False, False)])
+def test_routed_loss_gradcheck(cap, training, bias):
+    """At a fixed routing the layer is smooth: autograd of the routed loss equals
+    central finite differences (fp64) for x and every parameter, with the capacity
+    drop, a logit bias and without the aux losses."""
+    x, w_in, w_out, w1, w2, w3, dy = _tiny_layer(2)
+    with torch.no_grad():
+        logits = F.linear(F.silu(F.linear(x, w_in)), w_out)
+        idx = torch.topk(logits, 2, dim=-1).indices
+    b = torch.tensor([0.3, -0.2, 0.1], dtype=torch.float64) if bias else None
+    fn = lambda *a: P.moe_loss_tc_routed(*a, idx, dy, capacity=cap, bias=b, training=training)
+    assert torch.autograd.gradcheck(fn, (x, w_in, w_out, w1, w2, w3), eps=1e-6, atol=1e-7, rtol=1e-5)
