@@ -278,6 +278,17 @@ int kmoe_seg_transpose(const void* src, int64_t ld_src, const int32_t* row_token
 int kmoe_gemm_wgrad(const void* at, const void* bt, int64_t k_total, const int32_t* offsets, int E, int M, int N,
                     void* c, void* c2, int c_dtype, int64_t ldc, int n_valid, void* stream);
 
+/* Weight gradients read straight from row-major row buffers (no transposes):
+ *   c_e[m, n] = sum over expert e's rows r of a[r, m] * b[r, n]
+ * a (max_rows, lda) and b (max_rows, ldb) bf16, rows of expert e = [offsets[e],
+ * offsets[e+1]); c as kmoe_gemm_wgrad (bf16 with optional c2 split, or f32), n_valid
+ * and ldc multiples of 8.  dW3 = h^T dyperm: a = h (lda F_pad), b = dyperm (ldb d), M = F,
+ * N = round_up(d, 256);  dW1, dW2: a = the permuted x rows (kmoe_dispatch's xperm),
+ * b = dgu (ldb 2*F_pad), M = d, N = 2*F_pad, c = dW1, c2 = dW2.                 */
+int kmoe_gemm_wgrad_rows(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t max_rows,
+                         const int32_t* offsets, int E, int M, int N, void* c, void* c2, int c_dtype, int64_t ldc,
+                         int n_valid, void* stream);
+
 /* out[i] = sum_p partial[p][i] (p = 0 .. n_parts-1 in order, fp32), bf16 or f32 out. */
 int kmoe_reduce_f32(const float* partial, int64_t n_parts, int64_t n, void* out, int out_dtype, void* stream);
 

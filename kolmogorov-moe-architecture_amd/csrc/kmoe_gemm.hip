@@ -674,6 +674,258 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   gemm_tile<false, false, false, 4, OUT>(ge, lds, 0, m0, M, nt, 0);
 }
 
+// ---------------------------------------------------------------- weight gradients, row-major operands
+// C_e[m, n] = sum over expert e's rows r of A[r, m] * B[r, n] with A (rows, lda) and B
+// (rows, ldb) row-major and the rows of expert e = [offsets[e], offsets[e+1]): the
+// weight gradients read straight from the permuted row buffers, no transposes.
+// K advances 64 rows per step.  A stage holds 64 rows x 256 columns (512 B per row) of
+// A and of B, row-major, with the 64-byte segments of row r XOR-ed by
+// f(r) = (r & 3) | ((r >> 1) & 4).  MFMA operands come from ds_read_b64_tr_b16: in each
+// 16-lane group, lane i receives element i mod 4 of the 8-byte chunks addressed by
+// lanes 4p + i/4 (p = 0..3), so lanes 4p + c addressing row k0 + p, columns c0 + 4c
+// give lane i column c0 + i at rows k0 .. k0 + 3: half an operand fragment (the
+// second read takes rows k0 + 4 .. k0 + 7).  The 8 rows of one read fall in 8 distinct
+// segments, two per bank group: the 512 bytes take the minimum two LDS passes.
+// Rows past the expert's end read as zero: each operand's buffer window ends at the
+// expert's last row (raw buffer loads past the window return 0).
+constexpr int TN_KR = 64;                 // K rows per step
+constexpr int TN_ROWB = 512;              // bytes of a 256-column bf16 tile row
+constexpr int TN_TILE = TN_KR * TN_ROWB;  // 32 KiB
+__device__ __forceinline__ int tn_f(int r) { return (r & 3) | ((r >> 1) & 4); }
+// LDS byte offset of 16-byte chunk c (0..31) of stage-tile row r
+__device__ __forceinline__ int tn_chunk(int r, int c) { return r * TN_ROWB + ((((c >> 2) ^ tn_f(r)) << 2) | (c & 3)) * 16; }
+// LDS byte offset of the 8 bytes at column col (a multiple of 4) of stage-tile row r
+__device__ __forceinline__ int tn_elem(int r, int col) { return r * TN_ROWB + (((col >> 5) ^ tn_f(r)) << 6) + ((col & 31) << 1); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_window(const void* base, int64_t bytes) {
+  const int n = bytes < 0 ? 0 : (bytes > 0x7fffffffll ? 0x7fffffff : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+typedef short tr4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ Frag<false> read_frag_tr(const uint8_t* l, int row, int col) {
+  const tr4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (KMOE_LDS tr4_t*)(l + tn_elem(row, col)));
+  const tr4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (KMOE_LDS tr4_t*)(l + tn_elem(row + 4, col)));
+  Frag<false> f;
+  f.v = __builtin_bit_cast(bf16x8_t, (short __attribute__((ext_vector_type(8)))){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1],
+                                                                                 hi[2], hi[3]});
+  return f;
+}
+
+// One 256 x 256 output tile of expert rows [row0, row0 + nrows), output rows [m0, ...),
+// columns [256 nt, ...); g.C / g.C2 / g.Cf already point at the expert's output.
+template <int OUT>
+__device__ __forceinline__ void wgrad_tn_tile(const GemmArgs& g, uint8_t* lds, int64_t row0, int nrows, int m0, int M,
+                                              int nt) {
+  constexpr int NBLK = 16;  // 8 A + 8 B blocks of 1 KiB (2 rows x 512 B) per wave per step
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n0 = nt * 256;
+  const __amdgpu_buffer_rsrc_t arsrc =
+      make_rsrc_window(g.A + row0 * g.lda_bytes + (int64_t)m0 * 2, (int64_t)nrows * g.lda_bytes - (int64_t)m0 * 2);
+  const __amdgpu_buffer_rsrc_t brsrc =
+      make_rsrc_window(g.B + row0 * g.ldb_bytes + (int64_t)n0 * 2, (int64_t)nrows * g.ldb_bytes - (int64_t)n0 * 2);
+  const int nk = (nrows + TN_KR - 1) / TN_KR;
+  auto la_buf = [&](int st) { return lds + st * 2 * TN_TILE; };
+  auto lb_buf = [&](int st) { return lds + st * 2 * TN_TILE + TN_TILE; };
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // block qq < 8: A block 8 wave + qq (tile rows 2b, 2b + 1; lane: row 2b + lane/32,
+  // 16-byte chunk lane % 32); qq >= 8: the B block likewise
+  uint32_t voff[NBLK];
+  int dst[8];
+#pragma unroll
+  for (int qq = 0; qq < 8; ++qq) {
+    const int tr = 2 * (wave * 8 + qq) + (lane >> 5), c = lane & 31;
+    voff[qq] = (uint32_t)tr * (uint32_t)g.lda_bytes + (uint32_t)c * 16u;
+    voff[qq + 8] = (uint32_t)tr * (uint32_t)g.ldb_bytes + (uint32_t)c * 16u;
+    dst[qq] = tn_chunk(tr, c);
+  }
+  i32x4_t stg[NBLK];
+  // The step's row offset goes into the per-lane (VGPR) offset: the buffer range check
+  // covers the VGPR and instruction offsets but not the scalar one, and it is what
+  // turns the rows past the expert's end into zeros.  Offsets and the window are
+  // multiples of 16 bytes, so a 16-byte load is either wholly inside or wholly outside.
+  const uint32_t astep = (uint32_t)TN_KR * (uint32_t)g.lda_bytes, bstep = (uint32_t)TN_KR * (uint32_t)g.ldb_bytes;
+  auto load_block = [&](int qq, int kt) {
+    const uint32_t ks = (uint32_t)(kt < nk ? kt : nk - 1);
+    if (qq < 8)
+      stg[qq] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, voff[qq] + ks * astep, 0, 0);
+    else
+      stg[qq] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, voff[qq] + ks * bstep, 0, 0);
+  };
+  auto write_block = [&](int qq, int st) {
+    uint8_t* base = qq < 8 ? la_buf(st) : lb_buf(st);
+    *reinterpret_cast<i32x4_t*>(base + dst[qq & 7]) = stg[qq];
+  };
+  // operand fragments of K-substep i: lane group g = lane/16 reads rows
+  // 16 i + 8 (g/2) + (lane%16)/4 (+4), columns base + 16 (g%2) + 4 (lane%4)
+  const int grp = lane >> 4, i16 = lane & 15;
+  const int frow = 8 * (grp >> 1) + (i16 >> 2), fcol = 16 * (grp & 1) + 4 * (i16 & 3);
+  Frag<false> fa[2][4], fb[2][4];
+  auto rd = [&](int st, int i, Frag<false> (&a)[4], Frag<false> (&b)[4]) {
+    const uint8_t* la = la_buf(st);
+    const uint8_t* lb = lb_buf(st);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) a[mi] = read_frag_tr(la, 16 * i + frow, wm * 128 + mi * 32 + fcol);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = read_frag_tr(lb, 16 * i + frow, wn * 128 + j * 32 + fcol);
+  };
+  auto mma = [&](const Frag<false> (&a)[4], const Frag<false> (&b)[4]) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mfma<false>(acc[mi][j], a[mi], b[j]);
+  };
+  // the NT tile's pipeline: step kt computes stage kt%2 while the registers hold step
+  // kt+1's data, written into the other stage over the first substeps and reloaded
+  // with step kt+2's; one barrier per step
+  constexpr int RD = 16;  // transpose reads per substep (4 A + 4 B fragments, 2 each)
+  constexpr int C1 = (NBLK * 6 + 8) / 16, C2 = (NBLK * 11 + 8) / 16;
+  for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 0);
+  for (int qq = 0; qq < NBLK; ++qq) write_block(qq, 0);
+  for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 1);
+  wait_lgkmcnt0();
+  barrier_nofence();
+  rd(0, 0, fa[0], fb[0]);
+  auto step = [&](int kt, auto last_tag) {
+    constexpr bool LAST = decltype(last_tag)::value;
+    const int cur = kt & 1, nxt = cur ^ 1;
+    static_for<0, 4>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr int bi = i & 1;
+      constexpr int q0 = i == 0 ? 0 : i == 1 ? C1 : i == 2 ? C2 : NBLK;
+      constexpr int q1 = i == 0 ? C1 : i == 1 ? C2 : NBLK;
+      constexpr int nq = LAST ? 0 : q1 - q0;
+      constexpr bool RDN = i + 1 < 4 || !LAST;
+      if constexpr (i + 1 < 4) {
+        rd(cur, i + 1, fa[bi ^ 1], fb[bi ^ 1]);
+      } else if constexpr (!LAST) {
+        wait_lgkmcnt0();
+        barrier_nofence();
+        rd(nxt, 0, fa[bi ^ 1], fb[bi ^ 1]);
+      }
+      if constexpr (nq > 0) {
+        static_for<q0, q1>([&](auto qc) { write_block(decltype(qc)::value, nxt); });
+        static_for<q0, q1>([&](auto qc) { load_block(decltype(qc)::value, kt + 2); });
+      }
+      mma(fa[bi], fb[bi]);
+      sched_spread<16, (RDN ? RD : 0), nq, nq>();
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  for (int kt = 0; kt + 1 < nk; ++kt) step(kt, std::false_type{});
+  step(nk - 1, std::true_type{});
+
+  // ---- epilogue, straight from the accumulators: acc[mi][j][r] is row
+  // wm*128 + mi*32 + 8(r/4) + 4 lh + r%4, column wn*128 + j*32 + lr of the tile.
+  if constexpr (OUT == OUT_F32) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          const int col = n0 + wn * 128 + j * 32 + lr;
+          if (row < M && col < g.n_valid) g.Cf[(int64_t)row * g.ldc + col] = acc[mi][j][r];
+        }
+  } else {
+    // bf16 through LDS (rows padded by 16 bytes), then 16-byte row stores: pairs are
+    // formed across neighbouring lanes with DPP (an even lane packs its own and its right
+    // neighbour's value of row 2p, an odd lane its left neighbour's and its own of row
+    // 2p+1)
+    constexpr int OSTR = 256 * 2 + 16;
+    const bool odd = lr & 1;
+    __syncthreads();
+    uint8_t* const wbase = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR + (wn * 128 + lr - (odd ? 1 : 0)) * 2;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int p = 0; p < 8; ++p)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = acc[mi][j][2 * p], b = acc[mi][j][2 * p + 1];
+          const float a_next = __builtin_bit_cast(
+              float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, a), 0x101, 0xf, 0xf, false));
+          const float b_prev = __builtin_bit_cast(
+              float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, b), 0x111, 0xf, 0xf, false));
+          const float lo = odd ? b_prev : a, hi = odd ? b : a_next;
+          const uint32_t packed = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+          *reinterpret_cast<uint32_t*>(wbase + (mi * 32 + 8 * (p >> 1) + 2 * (p & 1)) * OSTR + j * 64) = packed;
+        }
+    __syncthreads();
+    for (int c = tid; c < BM * 32; c += GEMM_THREADS) {
+      const int trow = c >> 5, tc = (c & 31) * 8;  // tile row, first column of the 8
+      const int grow = m0 + trow;
+      uint16_t* base = g.C;
+      int gcol = n0 + tc;
+      if constexpr (OUT == OUT_SPLIT) {
+        base = tc < 128 ? g.C : g.C2;
+        gcol = nt * 128 + (tc & 127);
+      }
+      if (grow < M && gcol < g.n_valid)
+        *reinterpret_cast<i32x4_t*>(base + (int64_t)grow * g.ldc + gcol) =
+            *reinterpret_cast<const i32x4_t*>(lds + trow * OSTR + tc * 2);
+    }
+  }
+}
+
+template <int OUT>
+__global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void wgrad_rows_kernel(
+    GemmArgs g, const int32_t* __restrict__ offsets, int E, int M, int n_mt, int n_nt, int64_t c_expert_stride) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * TN_TILE > BM * (256 * 2 + 16) ? 4 * TN_TILE : BM * (256 * 2 + 16)];
+  const int n_all = E * n_mt * n_nt;
+  const int L = blockIdx.x;
+  if (L >= n_all) return;
+  const int t = (n_all % (NXCD * SB_TILES)) == 0 ? xcd_tile(L) : L;
+  const int per_e = n_mt * n_nt;
+  const int e = t / per_e, rem = t - e * per_e;
+  int mt, nt;
+  dense_tile(rem, n_mt, n_nt, mt, nt);
+  const int row0 = __builtin_amdgcn_readfirstlane(offsets[e]);
+  const int nrows = __builtin_amdgcn_readfirstlane(offsets[e + 1]) - row0;
+  GemmArgs ge = g;
+  ge.C = g.C ? g.C + (int64_t)e * c_expert_stride : nullptr;
+  ge.C2 = g.C2 ? g.C2 + (int64_t)e * c_expert_stride : nullptr;
+  ge.Cf = g.Cf ? g.Cf + (int64_t)e * c_expert_stride : nullptr;
+  const int m0 = mt * BM;
+  if (nrows <= 0) {
+    // no rows: a zero gradient tile
+    for (int c = threadIdx.x; c < BM * 128; c += GEMM_THREADS) {
+      const int grow = m0 + c / 128, tc = 2 * (c % 128);
+      if (grow >= M) continue;
+      if constexpr (OUT == OUT_F32) {
+        const int gcol = nt * 256 + tc;
+        if (gcol < g.n_valid) ge.Cf[(int64_t)grow * g.ldc + gcol] = 0.0f;
+        if (gcol + 1 < g.n_valid) ge.Cf[(int64_t)grow * g.ldc + gcol + 1] = 0.0f;
+      } else {
+        uint16_t* base = ge.C;
+        int gcol = nt * 256 + tc;
+        if constexpr (OUT == OUT_SPLIT) {
+          base = tc < 128 ? ge.C : ge.C2;
+          gcol = nt * 128 + (tc & 127);
+        }
+        if (gcol < g.n_valid) *reinterpret_cast<uint32_t*>(base + (int64_t)grow * g.ldc + gcol) = 0u;
+      }
+    }
+    return;
+  }
+  wgrad_tn_tile<OUT>(ge, lds, row0, nrows, m0, M, nt);
+}
+
 // ---------------------------------------------------------------- weight packing
 // out[e][map(c)][r] = in[e][r][c] for in (E, R, Cn) row-major; rows of `out` have
 // length out_ld (>= R, zero padded), out has out_rows rows per expert (zero padded).
@@ -1144,4 +1396,47 @@ extern "C" int kmoe_gemm_wgrad(const void* at, const void* bt, int64_t k_total, 
   else
     hipLaunchKernelGGL(wgrad_kernel<OUT_BF16>, grid, block, 0, s, g, offsets, E, M, n_mt, n_nt, stride);
   return kmoe::check_launch("kmoe_gemm_wgrad");
+}
+
+extern "C" int kmoe_gemm_wgrad_rows(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t max_rows,
+                                    const int32_t* offsets, int E, int M, int N, void* c, void* c2, int c_dtype,
+                                    int64_t ldc, int n_valid, void* stream) {
+  KMOE_REQUIRE(a && b && offsets && c, KMOE_ERR_NULL, "kmoe_gemm_wgrad_rows: null buffer");
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_gemm_wgrad_rows: E=%d out of range", E);
+  KMOE_REQUIRE(M > 0 && N > 0 && N % BN == 0, KMOE_ERR_SHAPE, "kmoe_gemm_wgrad_rows: M=%d, N=%d (N a multiple of %d)",
+               M, N, BN);
+  KMOE_REQUIRE(lda >= M && ldb >= 1 && lda % 8 == 0 && ldb % 8 == 0, KMOE_ERR_SHAPE,
+               "kmoe_gemm_wgrad_rows: lda=%lld, ldb=%lld (multiples of 8, lda >= M)", (long long)lda, (long long)ldb);
+  KMOE_REQUIRE(c_dtype == KMOE_DTYPE_BF16 || (c_dtype == KMOE_DTYPE_F32 && c2 == nullptr), KMOE_ERR_DTYPE,
+               "kmoe_gemm_wgrad_rows: c dtype must be bf16, or f32 without c2");
+  KMOE_REQUIRE(n_valid > 0 && n_valid <= ldc && n_valid % 8 == 0 && ldc % 8 == 0, KMOE_ERR_SHAPE,
+               "kmoe_gemm_wgrad_rows: n_valid=%d, ldc=%lld (multiples of 8, n_valid <= ldc)", n_valid, (long long)ldc);
+  // an expert's row window (at most max_rows + one K-step of rows) must fit the
+  // buffer's 31-bit record count and the 32-bit per-lane offsets
+  KMOE_REQUIRE(max_rows >= 0 && (max_rows + TN_KR) * (lda > ldb ? lda : ldb) * 2 < ((int64_t)1 << 31),
+               KMOE_ERR_SHAPE, "kmoe_gemm_wgrad_rows: %lld rows too large for 32-bit buffer offsets",
+               (long long)max_rows);
+
+  GemmArgs g{};
+  g.A = static_cast<const uint8_t*>(a);
+  g.lda_bytes = lda * 2;
+  g.B = static_cast<const uint8_t*>(b);
+  g.ldb_bytes = ldb * 2;
+  const bool f32 = c_dtype == KMOE_DTYPE_F32;
+  g.C = f32 ? nullptr : static_cast<uint16_t*>(c);
+  g.C2 = static_cast<uint16_t*>(c2);
+  g.Cf = f32 ? static_cast<float*>(c) : nullptr;
+  g.ldc = ldc;
+  g.n_valid = n_valid;
+  const int n_mt = kmoe::ceil_div(M, BM), n_nt = N / BN;
+  const dim3 grid((unsigned)((int64_t)E * n_mt * n_nt)), block(GEMM_THREADS);
+  hipStream_t s = kmoe::as_stream(stream);
+  const int64_t stride = (int64_t)M * ldc;
+  if (f32)
+    hipLaunchKernelGGL(wgrad_rows_kernel<OUT_F32>, grid, block, 0, s, g, offsets, E, M, n_mt, n_nt, stride);
+  else if (c2)
+    hipLaunchKernelGGL(wgrad_rows_kernel<OUT_SPLIT>, grid, block, 0, s, g, offsets, E, M, n_mt, n_nt, stride);
+  else
+    hipLaunchKernelGGL(wgrad_rows_kernel<OUT_BF16>, grid, block, 0, s, g, offsets, E, M, n_mt, n_nt, stride);
+  return kmoe::check_launch("kmoe_gemm_wgrad_rows");
 }

@@ -67,6 +67,8 @@ _SIGNATURES = {
     "kmoe_seg_transpose": (_i32, [_vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _vp]),
     "kmoe_gemm_wgrad": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _i64, _i32, _vp]),
     "kmoe_reduce_f32": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
+    "kmoe_gemm_wgrad_rows": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _i64, _i32,
+                                    _vp]),
     "kmoe_router_dlogits": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _vp, _vp]),
     "kmoe_router_bwd_workspace_bytes": (_sz, [_i64, _i32]),
     "kmoe_router_mlp_bwd": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),

@@ -13,7 +13,7 @@ Data flow (A = routed rows, grouped by expert):
   dgu = swiglu_bwd(dh, g, u)     g, u saved by the forward's gate/up GEMM
   dxp = dgu . [w1|w2]^T          grouped GEMM (packed w13t)
   dx  = sum_j dxp[slot(t,j)] + (da . w_in)[t]   (one unit-weight gather of both)
-  dW3 = h^T dyperm, dW1|dW2 = x^T dgu           per-expert GEMMs over transposed row segments
+  dW3 = h^T dyperm, dW1|dW2 = xperm^T dgu       per-expert GEMMs on the row buffers (LDS transpose reads)
   dlogits = topk-renorm backward(dw) + aux backward;  da, dW_out (router MLP);  dW_in = da^T x
 """
 from __future__ import annotations
@@ -69,6 +69,7 @@ class Saved(NamedTuple):
     h: torch.Tensor          # (A, F_pad) bf16
     gu: torch.Tensor         # (A, 2 F_pad) bf16 pre-activation gate / up
     yperm: torch.Tensor      # (A, d) bf16 expert outputs
+    xperm: torch.Tensor      # (A, d) bf16 permuted input rows (the dispatch's gather)
 
 
 class Grads(NamedTuple):
@@ -168,7 +169,6 @@ def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], 
         return Grads(dx, None, dw_out, None, None, None)
 
     # ---- weight gradients over transposed row segments
-    kt = lib.kmoe_wgrad_k_total(A, E)
     dpad = _ru(d, 256)
     # dW_in = da^T x: a 128 x d output (few tiles) over K = T, split into token
     # segments of WG_SPLIT rows whose fp32 partial sums are then reduced in order
@@ -186,26 +186,14 @@ def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], 
                   None, _lib.DTYPE_F32, d, d, s)
         _lib.call("kmoe_reduce_f32", ptr(part), nseg, _lib.ROUTER_HIDDEN * d, ptr(dw_in), _lib.DTYPE_BF16, s)
     del daT, xT1, part
-    with _stage("bwd_transpose"):
-        hT = torch.empty(Fp, kt, device=dev, dtype=_BF16)
-        _lib.call("kmoe_seg_transpose", ptr(sv.h), Fp, None, None, ptr(disp.offsets), E, Fp, Fp, ptr(hT), kt, s)
-        dyT = torch.empty(dpad, kt, device=dev, dtype=_BF16)
-        _lib.call("kmoe_seg_transpose", ptr(dyperm), d, None, None, ptr(disp.offsets), E, d, dpad, ptr(dyT), kt, s)
+    # expert weight gradients straight from the row buffers (transpose reads in LDS)
     dw3 = torch.empty(E, F, d, device=dev, dtype=_BF16)
     with _stage("bwd_wgrad_w3"):
-        _lib.call("kmoe_gemm_wgrad", ptr(hT), ptr(dyT), kt, ptr(disp.offsets), E, F, dpad, ptr(dw3), None,
-                  _lib.DTYPE_BF16, d, d, s)
-    del hT, dyT
-    with _stage("bwd_transpose"):
-        xT = torch.empty(d, kt, device=dev, dtype=_BF16)
-        _lib.call("kmoe_seg_transpose", ptr(x2d), d, ptr(disp.row_token), None, ptr(disp.offsets), E, d, d, ptr(xT),
-                  kt, s)
-        dguT = torch.empty(2 * Fp, kt, device=dev, dtype=_BF16)
-        _lib.call("kmoe_seg_transpose", ptr(dgu), 2 * Fp, None, None, ptr(disp.offsets), E, 2 * Fp, 2 * Fp, ptr(dguT),
-                  kt, s)
+        _lib.call("kmoe_gemm_wgrad_rows", ptr(sv.h), Fp, ptr(dyperm), d, A, ptr(disp.offsets), E, F, dpad, ptr(dw3),
+                  None, _lib.DTYPE_BF16, d, d, s)
     dw1 = torch.empty(E, d, F, device=dev, dtype=_BF16)
     dw2 = torch.empty(E, d, F, device=dev, dtype=_BF16)
     with _stage("bwd_wgrad_w13"):
-        _lib.call("kmoe_gemm_wgrad", ptr(xT), ptr(dguT), kt, ptr(disp.offsets), E, d, 2 * Fp, ptr(dw1), ptr(dw2),
-                  _lib.DTYPE_BF16, F, F, s)
+        _lib.call("kmoe_gemm_wgrad_rows", ptr(sv.xperm), d, ptr(dgu), 2 * Fp, A, ptr(disp.offsets), E, d, 2 * Fp,
+                  ptr(dw1), ptr(dw2), _lib.DTYPE_BF16, F, F, s)
     return Grads(dx, dw_in, dw_out, dw1, dw2, dw3)

@@ -330,7 +330,8 @@ class MoELayer(nn.Module):
         if not (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
         ge = self.grouped_experts
-        return not (ge.use_fp8 or self.router.balanced_routing)
+        # the weight-gradient stores write rows of 8 bf16 (d_ff_expert a multiple of 8)
+        return not (ge.use_fp8 or self.router.balanced_routing or ge.d_ff % 8)
 
     def _bwd_weights(self) -> _bwd.BwdWeights:
         """Backward packed weights, rebuilt only when a parameter changed."""
@@ -351,7 +352,9 @@ class MoELayer(nn.Module):
         k, E = self.top_k, self.n_experts
         cap = ops.capacity_of(self.capacity_factor, T, k, E) if self.drop_overflow else 0
         pw = ge.packed()
-        disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=False)
+        # the permuted x rows are kept for the weight gradient (the gate/up GEMM still
+        # gathers its own A rows from x)
+        disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=True)
         h, gu = ops.gemm_gate_up_rows(x2d, None, disp.row_token, disp.offsets, pw, T * k, save_gu=True)
         yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T, out_dtype=out_dtype)
@@ -360,7 +363,7 @@ class MoELayer(nn.Module):
         if self.training:
             aux = ops.aux_loss(r.partials, T, E, disp.counts, k, self.load_balance_loss_weight,
                                self.router_z_loss_weight)[0]
-        sv = _bwd.Saved(x2d, r.logits, r.idx, r.w, r.hidden, disp, h, gu, yperm)
+        sv = _bwd.Saved(x2d, r.logits, r.idx, r.w, r.hidden, disp, h, gu, yperm, disp.xperm)
         return y, aux, sv
 
     def _forward_token_choice(self, hidden_states: torch.Tensor) -> torch.Tensor:
