@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-train", action="store_true", help="skip the training-step (backward) pass")
+    ap.add_argument("--no-block", action="store_true",
+                    help="skip the fused FFN-block (RMSNorm + MoE + residual) pass")
     ap.add_argument("--stage-steps", type=int, default=20, help="forwards of the per-stage timing pass")
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
@@ -150,7 +152,9 @@ def run_gpu(args, wl):
     work = stage_bytes_flops(wl, layer, dict(a_kept=a_kept, a_all=a_all, t_in=t_in))
     stage_out = {}
     for name, v in stages.items():
-        us = statistics.mean(v)
+        # median: a one-off host stall (an allocation) inside one event pair of the
+        # pass would otherwise dominate a mean
+        us = statistics.median(v)
         rec = {"us": round(us, 2), "launches_per_step": len(v) // args.stage_steps}
         if name in work:
             kind, amount = work[name]
@@ -165,9 +169,61 @@ def run_gpu(args, wl):
     training = None
     if not (wl.fp8 or wl.mod or wl.routing == "expert_choice") and not args.no_train:
         training = run_training(args, wl, layer, x)
+    block = None
+    if not (wl.fp8 or wl.mod or wl.routing == "expert_choice") and not args.no_block:
+        block = run_block(args, wl, layer, x)
     return dict(elapsed=elapsed, stages=stage_out, a_kept=a_kept, a_all=a_all, t_in=t_in,
                 gemm_us=statistics.mean(gu_timed) if gu_timed else float("nan"), gemm_samples=len(gu_timed),
-                work=work, rows_us=rows_us, training=training)
+                work=work, rows_us=rows_us, training=training, block=block)
+
+
+def run_block(args, wl, layer, x):
+    """The FFN half of the transformer block, out = h + MoE(RMSNorm(h)) (layers.py:142-147,
+    184-187), in inference: fused (norm folded into the router and the gate/up GEMM,
+    residual add in the combine) against the unfused composition (the reference's
+    RMSNorm formula in torch, the same kmoe layer, a torch add).  Timed outside the
+    forward metric's region, K forwards between synchronisations."""
+    import torch
+    from kmoe import ops
+    from kmoe.block import MoEFFNBlock
+
+    blk = MoEFFNBlock(layer.config, 0, ffn=layer)
+    g = torch.Generator().manual_seed(wl.seed + 200)
+    blk.ffn_norm.weight = torch.nn.Parameter((1.0 + 0.1 * torch.randn(wl.d, generator=g)).to(x.device, x.dtype))
+    blk.eval()
+    norm = blk.ffn_norm
+    fns = {"fused": lambda: blk(x), "unfused": lambda: x + layer(norm(x))}
+    steps = max(1, args.steps // 2)
+    ms = {}
+    with torch.no_grad():
+        for name, fn in fns.items():
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            torch.cuda.synchronize()
+            ms[name] = (time.perf_counter() - t0) / steps * 1e3
+        events = []
+        ops.set_stage_timing(events)
+        for _ in range(10):
+            fns["fused"]()
+        torch.cuda.synchronize()
+        ops.set_stage_timing(None)
+    assert blk.last_path == "fused"
+    layer.train()
+    per = {}
+    for name, a, b in events:
+        per.setdefault(name, []).append(a.elapsed_time(b) * 1e3)
+    stages = {name: round(statistics.median(v), 2) for name, v in per.items()}
+    return {"fused_ms": round(ms["fused"], 4), "unfused_ms": round(ms["unfused"], 4),
+            "fused_tokens_per_s": round(wl.T / (ms["fused"] * 1e-3), 1),
+            "unfused_tokens_per_s": round(wl.T / (ms["unfused"] * 1e-3), 1),
+            "saved_us": round((ms["unfused"] - ms["fused"]) * 1e3, 1), "steps": steps,
+            "fused_stages_us": stages,
+            "note": "h + MoE(RMSNorm(h)), eval, bf16 norm weight; unfused = torch RMSNorm (embeddings.py:190-195) "
+                    "+ kmoe layer + torch add"}
 
 
 def run_training(args, wl, layer, x):
@@ -339,6 +395,8 @@ def main():
         out["combine_GBps"] = res["stages"]["combine"].get("GBps")
     if res.get("training"):
         out["training"] = res["training"]
+    if res.get("block"):
+        out["ffn_block"] = res["block"]
     if not args.no_cpu:
         out["cpu_baseline"] = run_cpu_baseline(synth.WORKLOADS[2], args.cpu_tokens)
     else:

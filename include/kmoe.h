@@ -312,6 +312,38 @@ int kmoe_router_mlp_bwd(const float* dlogits, const float* hidden_pre, int64_t T
 size_t kmoe_packed_w_in_t_bytes(int d);
 int kmoe_pack_w_in_t(const void* w_in, int w_dtype, int d, void* out, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Layer-boundary fusions: the FFN half of TransformerBlock.forward
+ * (layers.py:142-147, 184-187), out = h + MoE(RMSNorm(h)), with RMSNorm
+ * (embeddings.py:167-195: y = w_norm * x / sqrt(mean(x^2) + eps)) folded into the
+ * router and the gate/up GEMM, and the residual add folded into the combine.
+ * The caller folds the norm weight into the weights once per parameter version:
+ *   w_in_g[j][i] = w_in[j][i] * w_norm[i];  w13 = kmoe_pack_weights(w1 * w_norm[:,None],
+ *   w2 * w_norm[:,None], w3, ...).  x is then the un-normalised h.           */
+
+/* kmoe_router on RMSNorm(x): w_in_g carries the norm weight; the kernel computes
+ * rscale[t] = 1/sqrt(mean(x[row(t)]^2) + eps) (f32, (T,)) from the x rows it reads and
+ * scales the hidden pre-activation by it (replaces the separate norm pass).   */
+int kmoe_router_rms(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in_g,
+                    const void* w_out, int E, const float* logit_bias, int k, float* logits,
+                    int64_t* topk_idx, float* topk_w, float* partials, float eps, float* rscale, void* stream);
+
+/* kmoe_gemm_gate_up_rows on RMSNorm(x): the gate and up values of permuted row r are
+ * scaled by rscale[row_token[r]] before the SiLU (w13 packed from the norm-folded
+ * w1 / w2).  The normalised rows are never written.                           */
+int kmoe_gemm_gate_up_rows_scaled(const void* x, const int32_t* row_index, int64_t n_x_rows,
+                                  const int32_t* row_token, const int32_t* offsets, int E, int d, int F,
+                                  int64_t max_rows, const void* w13_packed, const float* rscale, void* h,
+                                  void* stream);
+
+/* kmoe_combine plus a residual (y's dtype, (T_out, d)), added in f32 before the one
+ * rounding: y[o] = residual[o] + scale[s] sum_j w[s,j] yperm[src[s,j]]; rows with
+ * out_map[o] < 0 get residual[o].  residual may be NULL (= kmoe_combine).
+ * residual and y must not overlap unless they are the same buffer.            */
+int kmoe_combine_residual(const void* yperm, int d, const int32_t* src_row, const float* src_w, int fan,
+                          const int32_t* out_map, const float* scale, const void* residual, int64_t T_out,
+                          void* y, int y_dtype, void* stream);
+
 
 #ifdef __cplusplus
 }

@@ -6,26 +6,39 @@
 //
 // One wave per output row, 16-byte vector loads of each source row, fp32
 // accumulation in a fixed source order: no atomics, bit-reproducible.
+//
+// With a residual (y's dtype, (T_out, d)): y[o] = residual[o] + the sum above, added
+// in fp32 before the one rounding to y's dtype; rows without a source set
+// (out_map[o] < 0) get residual[o].  This is the residual add of the block's FFN half
+// (hidden_states = residual + ffn_output, layers.py:187) folded into the combine.
 #include "kmoe_common.h"
 
 namespace {
 
 constexpr int CROWS = 4;  // rows (waves) per workgroup
 
-template <bool OUT_F32>
+template <bool OUT_F32, bool RES = false>
 __global__ __launch_bounds__(64 * CROWS) void combine_kernel(const uint16_t* __restrict__ yperm, int d,
                                                              const int32_t* __restrict__ src_row,
                                                              const float* __restrict__ src_w, int fan,
                                                              const int32_t* __restrict__ out_map,
                                                              const float* __restrict__ scale, int64_t T_out,
-                                                             void* __restrict__ y) {
+                                                             void* __restrict__ y,
+                                                             const void* __restrict__ residual) {
   const int lane = threadIdx.x & 63;
   const int64_t o = (int64_t)blockIdx.x * CROWS + (threadIdx.x >> 6);
   if (o >= T_out) return;
   const int64_t s = out_map ? (int64_t)out_map[o] : o;
   const int nvec = d / 8;
   if (s < 0) {
-    if (OUT_F32) {
+    if (RES) {
+      // 16 bytes per vector of 8 bf16, 32 of 8 f32
+      const int nb = OUT_F32 ? 2 * nvec : nvec;
+      const i32x4_t* src = reinterpret_cast<const i32x4_t*>(static_cast<const uint8_t*>(residual) +
+                                                            o * d * (OUT_F32 ? 4 : 2));
+      i32x4_t* dst = reinterpret_cast<i32x4_t*>(static_cast<uint8_t*>(y) + o * d * (OUT_F32 ? 4 : 2));
+      for (int v = lane; v < nb; v += 64) dst[v] = src[v];
+    } else if (OUT_F32) {
       f32x4_t* dst = reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o * d);
       const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
       for (int v = lane; v < nvec; v += 64) {
@@ -102,16 +115,39 @@ __global__ __launch_bounds__(64 * CROWS) void combine_kernel(const uint16_t* __r
     for (int u = 0; u < 4; ++u) {
       const int v = v0 + u * 64 + lane;
       if (v >= nvec) continue;
+      float res[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) res[q] = 0.0f;
+      if constexpr (RES) {
+        if (OUT_F32) {
+          const f32x4_t* rp = reinterpret_cast<const f32x4_t*>(static_cast<const float*>(residual) + o * d) + 2 * v;
+          const f32x4_t r0v = rp[0], r1v = rp[1];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            res[q] = r0v[q];
+            res[4 + q] = r1v[q];
+          }
+        } else {
+          const i32x4_t rv = reinterpret_cast<const i32x4_t*>(static_cast<const uint16_t*>(residual) + o * d)[v];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            res[2 * q] = __uint_as_float(((uint32_t)rv[q]) << 16);
+            res[2 * q + 1] = __uint_as_float(((uint32_t)rv[q]) & 0xffff0000u);
+          }
+        }
+      }
       if (OUT_F32) {
         f32x4_t* dst = reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o * d) + 2 * v;
-        dst[0] = f32x4_t{acc[u][0] * sc, acc[u][1] * sc, acc[u][2] * sc, acc[u][3] * sc};
-        dst[1] = f32x4_t{acc[u][4] * sc, acc[u][5] * sc, acc[u][6] * sc, acc[u][7] * sc};
+        dst[0] = f32x4_t{fmaf(acc[u][0], sc, res[0]), fmaf(acc[u][1], sc, res[1]), fmaf(acc[u][2], sc, res[2]),
+                         fmaf(acc[u][3], sc, res[3])};
+        dst[1] = f32x4_t{fmaf(acc[u][4], sc, res[4]), fmaf(acc[u][5], sc, res[5]), fmaf(acc[u][6], sc, res[6]),
+                         fmaf(acc[u][7], sc, res[7])};
       } else {
         i32x4_t out;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          out[q] = (int)((uint32_t)f32_to_bf16(acc[u][2 * q] * sc) |
-                         ((uint32_t)f32_to_bf16(acc[u][2 * q + 1] * sc) << 16));
+          out[q] = (int)((uint32_t)f32_to_bf16(fmaf(acc[u][2 * q], sc, res[2 * q])) |
+                         ((uint32_t)f32_to_bf16(fmaf(acc[u][2 * q + 1], sc, res[2 * q + 1])) << 16));
         reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(y) + o * d)[v] = out;
       }
     }
@@ -125,12 +161,14 @@ __global__ __launch_bounds__(64 * CROWS) void combine_kernel(const uint16_t* __r
 // results are bit-identical; the straight-line form runs 37.8 -> 33.8 us at config 2
 // (the source loop's ballot / shuffle / bounds bookkeeping delayed the loads).
 constexpr int C2_D = 2048;
+template <bool RES = false>
 __global__ __launch_bounds__(256) void combine2_kernel(const uint16_t* __restrict__ yperm,
                                                        const int32_t* __restrict__ src_row,
                                                        const float* __restrict__ src_w,
                                                        const int32_t* __restrict__ out_map,
                                                        const float* __restrict__ scale, int64_t T_out,
-                                                       uint16_t* __restrict__ y) {
+                                                       uint16_t* __restrict__ y,
+                                                       const uint16_t* __restrict__ residual) {
   constexpr int NV = C2_D / 8 / 64;  // 16-byte vectors per lane
   const int lane = threadIdx.x & 63;
   const int64_t o = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -139,7 +177,9 @@ __global__ __launch_bounds__(256) void combine2_kernel(const uint16_t* __restric
   i32x4_t* dst = reinterpret_cast<i32x4_t*>(y + o * C2_D);
   if (s < 0) {
 #pragma unroll
-    for (int u = 0; u < NV; ++u) dst[u * 64 + lane] = i32x4_t{0, 0, 0, 0};
+    for (int u = 0; u < NV; ++u)
+      dst[u * 64 + lane] =
+          RES ? reinterpret_cast<const i32x4_t*>(residual + o * C2_D)[u * 64 + lane] : i32x4_t{0, 0, 0, 0};
     return;
   }
   int ms = -1;
@@ -151,11 +191,12 @@ __global__ __launch_bounds__(256) void combine2_kernel(const uint16_t* __restric
   const int r0 = __shfl(ms, 0, 64), r1 = __shfl(ms, 1, 64);
   const float w0 = __shfl(mw, 0, 64), w1 = __shfl(mw, 1, 64);
   const float sc = scale ? scale[s] : 1.0f;
-  i32x4_t a[NV], b[NV];
+  i32x4_t a[NV], b[NV], rr[RES ? NV : 1];
 #pragma unroll
   for (int u = 0; u < NV; ++u) {
     a[u] = r0 >= 0 ? reinterpret_cast<const i32x4_t*>(yperm + (int64_t)r0 * C2_D)[u * 64 + lane] : i32x4_t{0, 0, 0, 0};
     b[u] = r1 >= 0 ? reinterpret_cast<const i32x4_t*>(yperm + (int64_t)r1 * C2_D)[u * 64 + lane] : i32x4_t{0, 0, 0, 0};
+    if constexpr (RES) rr[u] = reinterpret_cast<const i32x4_t*>(residual + o * C2_D)[u * 64 + lane];
   }
 #pragma unroll
   for (int u = 0; u < NV; ++u) {
@@ -171,7 +212,12 @@ __global__ __launch_bounds__(256) void combine2_kernel(const uint16_t* __restric
         lo = fmaf(w1, __uint_as_float(((uint32_t)b[u][q]) << 16), lo);
         hi = fmaf(w1, __uint_as_float(((uint32_t)b[u][q]) & 0xffff0000u), hi);
       }
-      out[q] = (int)((uint32_t)f32_to_bf16(lo * sc) | ((uint32_t)f32_to_bf16(hi * sc) << 16));
+      float rlo = 0.0f, rhi = 0.0f;
+      if constexpr (RES) {
+        rlo = __uint_as_float(((uint32_t)rr[u][q]) << 16);
+        rhi = __uint_as_float(((uint32_t)rr[u][q]) & 0xffff0000u);
+      }
+      out[q] = (int)((uint32_t)f32_to_bf16(fmaf(lo, sc, rlo)) | ((uint32_t)f32_to_bf16(fmaf(hi, sc, rhi)) << 16));
     }
     dst[u * 64 + lane] = out;
   }
@@ -179,9 +225,9 @@ __global__ __launch_bounds__(256) void combine2_kernel(const uint16_t* __restric
 
 }  // namespace
 
-extern "C" int kmoe_combine(const void* yperm, int d, const int32_t* src_row, const float* src_w, int fan,
-                            const int32_t* out_map, const float* scale, int64_t T_out, void* y, int y_dtype,
-                            void* stream) {
+extern "C" int kmoe_combine_residual(const void* yperm, int d, const int32_t* src_row, const float* src_w,
+                                     int fan, const int32_t* out_map, const float* scale, const void* residual,
+                                     int64_t T_out, void* y, int y_dtype, void* stream) {
   KMOE_REQUIRE(yperm && src_row && src_w && y, KMOE_ERR_NULL, "kmoe_combine: null buffer");
   KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "kmoe_combine: d=%d must be a positive multiple of 64", d);
   KMOE_REQUIRE(fan >= 1 && fan <= 64, KMOE_ERR_SHAPE, "kmoe_combine: fan=%d not in [1,64]", fan);
@@ -192,14 +238,35 @@ extern "C" int kmoe_combine(const void* yperm, int d, const int32_t* src_row, co
   const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(T_out, CROWS));
   hipStream_t s = kmoe::as_stream(stream);
   const uint16_t* yp = static_cast<const uint16_t*>(yperm);
-  if (y_dtype == KMOE_DTYPE_BF16 && fan == 2 && d == C2_D)
-    hipLaunchKernelGGL(combine2_kernel, grid, dim3(256), 0, s, yp, src_row, src_w, out_map, scale, T_out,
-                       static_cast<uint16_t*>(y));
-  else if (y_dtype == KMOE_DTYPE_BF16)
-    hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(64 * CROWS), 0, s, yp, d, src_row, src_w, fan, out_map,
-                       scale, T_out, y);
-  else
-    hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(64 * CROWS), 0, s, yp, d, src_row, src_w, fan, out_map,
-                       scale, T_out, y);
+  const bool bf = y_dtype == KMOE_DTYPE_BF16;
+  uint16_t* y16 = static_cast<uint16_t*>(y);
+  const uint16_t* r16 = static_cast<const uint16_t*>(residual);
+  if (bf && fan == 2 && d == C2_D) {
+    if (residual)
+      hipLaunchKernelGGL(combine2_kernel<true>, grid, dim3(256), 0, s, yp, src_row, src_w, out_map, scale, T_out,
+                         y16, r16);
+    else
+      hipLaunchKernelGGL(combine2_kernel<false>, grid, dim3(256), 0, s, yp, src_row, src_w, out_map, scale, T_out,
+                         y16, r16);
+  } else {
+#define KMOE_COMBINE(F32_, RES_)                                                                                \
+  hipLaunchKernelGGL((combine_kernel<F32_, RES_>), grid, dim3(64 * CROWS), 0, s, yp, d, src_row, src_w, fan, \
+                     out_map, scale, T_out, y, residual)
+    if (bf && residual)
+      KMOE_COMBINE(false, true);
+    else if (bf)
+      KMOE_COMBINE(false, false);
+    else if (residual)
+      KMOE_COMBINE(true, true);
+    else
+      KMOE_COMBINE(true, false);
+#undef KMOE_COMBINE
+  }
   return kmoe::check_launch("kmoe_combine");
+}
+
+extern "C" int kmoe_combine(const void* yperm, int d, const int32_t* src_row, const float* src_w, int fan,
+                            const int32_t* out_map, const float* scale, int64_t T_out, void* y, int y_dtype,
+                            void* stream) {
+  return kmoe_combine_residual(yperm, d, src_row, src_w, fan, out_map, scale, nullptr, T_out, y, y_dtype, stream);
 }

@@ -265,7 +265,11 @@ constexpr int OUT_BF16 = 0, OUT_SPLIT = 1, OUT_F32 = 2;
 // GATHER: A is the unpermuted activation matrix and permuted row r is its row
 // row_index[row_token[r]] (row_token[r] without row_index): the dispatch gather is
 // fused into the A loads.
-template <bool GATE_UP, bool FP8, bool GATHER, int WNB, int OUT = OUT_BF16, bool SAVE_GU = false>
+// RSCALE (bf16 gathered gate/up tiles): a_scale[row_token[r]] scales row r's gate and
+// up values before the SiLU (the per-token RMSNorm scale of x: the norm weight is
+// folded into the packed w1 / w2 rows, and a per-row scale commutes with the product).
+template <bool GATE_UP, bool FP8, bool GATHER, int WNB, int OUT = OUT_BF16, bool SAVE_GU = false,
+          bool RSCALE = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e, int m0, int m_end, int nt,
                                           int q) {
   static_assert(WNB == 4 || WNB == 2 || (WNB == 1 && !GATE_UP), "tile width");
@@ -303,6 +307,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
     const int row = m0 + tid;
     if (row < m_end) sa_v = g.a_scale[row];
     if (tid < BNT) sb_v = g.b_scale[brow0 + b_packed_row<GATE_UP, WNB>(tid, q)];
+  }
+  static_assert(!RSCALE || (GATE_UP && GATHER && !FP8 && !SAVE_GU), "row scales are for bf16 gathered gate/up tiles");
+  if constexpr (RSCALE) {
+    const int row = m0 + tid;
+    if (row < m_end) sa_v = g.a_scale[g.row_token[row]];
   }
 
   // Tile loads: a stage tile is a set of 1 KiB blocks (8 rows of 128 B); wave w loads
@@ -455,6 +464,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
     sa_l[tid] = sa_v;
     if (tid < BNT) sb_l[tid] = sb_v;
   }
+  if constexpr (RSCALE) sa_l[tid] = sa_v;
   __syncthreads();
   // lane's write address for p = 0 of block (0, 0): even lanes row 4lh col lr,
   // odd lanes row 4lh+1 col lr-1
@@ -467,6 +477,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
         const float sa = sa_l[wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
         gg *= sa * bscale(jo);
         u *= sa * bscale(jo + WNB / 2);
+      }
+      if (RSCALE) {
+        const float sa = sa_l[wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
+        gg *= sa;
+        u *= sa;
       }
       return silu_fast_f32(gg) * u;
     } else {
@@ -563,7 +578,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
 // of 1/split of its columns (the full K), which all run at once.  A narrow tile
 // computes every output element with the same MFMA sequence as the full tile, so
 // the results are identical.  split = 1 keeps the tail tiles whole.
-template <bool GATE_UP, bool FP8, bool GATHER, bool SAVE_GU = false>
+template <bool GATE_UP, bool FP8, bool GATHER, bool SAVE_GU = false, bool RSCALE = false>
 __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void grouped_gemm_kernel(
     GemmArgs g, const int32_t* __restrict__ offsets, int E, int n_tiles, int n_cu, int allow_split) {
   static_assert(!(GATHER && FP8), "the fp8 path reads rows quantised by the dispatch");
@@ -595,11 +610,11 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   dense_tile(t, st.n_slots, n_tiles, slot, nt);
   find_slot(st, E, slot, e, m0, m_end);
   if (L < base || split == 1)
-    gemm_tile<GATE_UP, FP8, GATHER, 4, OUT_BF16, SAVE_GU>(g, lds, e, m0, m_end, nt, 0);
+    gemm_tile<GATE_UP, FP8, GATHER, 4, OUT_BF16, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, 0);
   else if (split == 2)
-    gemm_tile<GATE_UP, FP8, GATHER, 2, OUT_BF16, SAVE_GU>(g, lds, e, m0, m_end, nt, q);
+    gemm_tile<GATE_UP, FP8, GATHER, 2, OUT_BF16, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, q);
   else if constexpr (!GATE_UP)
-    gemm_tile<GATE_UP, FP8, GATHER, 1, OUT_BF16, SAVE_GU>(g, lds, e, m0, m_end, nt, q);
+    gemm_tile<GATE_UP, FP8, GATHER, 1, OUT_BF16, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, q);
 }
 
 // ---------------------------------------------------------------- weight gradients
@@ -1084,6 +1099,9 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
   if (row_token && gu_out)
     hipLaunchKernelGGL((grouped_gemm_kernel<true, false, true, true>), grid, block, 0, s, g, offsets, E, n_tiles,
                        n_cu, allow_split);
+  else if (row_token && a_scale)
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, false, true, false, true>), grid, block, 0, s, g, offsets, E,
+                       n_tiles, n_cu, allow_split);
   else if (row_token)
     KMOE_LAUNCH_GEMM(true, false, true);
   else if (gate_up && !fp8)
@@ -1220,6 +1238,24 @@ extern "C" int kmoe_gemm_gate_up_rows(const void* x, const int32_t* row_index, i
                    2 * (int64_t)Fp, nullptr, h, Fp, Fp, Fp / 128, kmoe::as_stream(stream));
   if (rc) return rc;
   return kmoe::check_launch("kmoe_gemm_gate_up_rows");
+}
+
+extern "C" int kmoe_gemm_gate_up_rows_scaled(const void* x, const int32_t* row_index, int64_t n_x_rows,
+                                             const int32_t* row_token, const int32_t* offsets, int E, int d, int F,
+                                             int64_t max_rows, const void* w13_packed, const float* rscale, void* h,
+                                             void* stream) {
+  int rc = check_gemm_args("kmoe_gemm_gate_up_rows_scaled", x, offsets, E, d, F, max_rows, w13_packed, h,
+                           KMOE_DTYPE_BF16);
+  if (rc) return rc;
+  KMOE_REQUIRE(row_token && rscale, KMOE_ERR_NULL, "kmoe_gemm_gate_up_rows_scaled: null row_token / rscale");
+  KMOE_REQUIRE(n_x_rows >= 1, KMOE_ERR_SHAPE, "kmoe_gemm_gate_up_rows_scaled: n_x_rows=%lld must be >= 1",
+               (long long)n_x_rows);
+  if (max_rows == 0) return KMOE_OK;
+  const int Fp = round_up(F, 128);
+  rc = launch_gemm(true, false, x, rscale, row_token, row_index, n_x_rows, offsets, E, d, max_rows, w13_packed,
+                   2 * (int64_t)Fp, nullptr, h, Fp, Fp, Fp / 128, kmoe::as_stream(stream));
+  if (rc) return rc;
+  return kmoe::check_launch("kmoe_gemm_gate_up_rows_scaled");
 }
 
 extern "C" int kmoe_gemm_down(const void* h, const float* h_scale, int in_dtype, const int32_t* offsets, int E, int d,

@@ -40,7 +40,12 @@ struct RtGeom {
 template <int NE, int RKB>
 constexpr int rt_stages() { return (160 * 1024 - NE * (RT_HID + 4) * 4) / RtGeom<RKB>::STAGE; }
 
-template <int NE, int RKB>
+// RMS: the router input is RMSNorm(x) (embeddings.py:167-195) with the norm weight
+// already folded into w_in's columns; the kernel sums x^2 over the K loop from the
+// x fragments it reads anyway, scales each token's hidden pre-activation by
+// r = 1/sqrt(mean(x^2) + eps) (the scale commutes with the d -> 128 product) and
+// writes r to rscale for the expert GEMM.
+template <int NE, int RKB, bool RMS = false>
 __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __restrict__ x,
                                                             const int32_t* __restrict__ row_index, int64_t T, int d,
                                                             const uint16_t* __restrict__ w_in,
@@ -48,7 +53,8 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
                                                             const float* __restrict__ bias, int k,
                                                             float* __restrict__ logits, int64_t* __restrict__ topk_idx,
                                                             float* __restrict__ topk_w, float* __restrict__ partials,
-                                                            float* __restrict__ hidden_pre) {
+                                                            float* __restrict__ hidden_pre, float eps,
+                                                            float* __restrict__ rscale) {
   using G = RtGeom<RKB>;
   constexpr int RT_STAGES = rt_stages<NE, RKB>();
   constexpr int RT_STAGE = G::STAGE;
@@ -57,6 +63,7 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   constexpr int LGS = NE + 4;      // logits / probabilities row stride (floats), 16-byte aligned rows
   __shared__ __attribute__((aligned(1024))) uint8_t smem[RT_STAGES * RT_STAGE];
   __shared__ __attribute__((aligned(16))) float wo[NE * WOS];  // w_out as fp32
+  __shared__ float rs_l[RMS ? RT_TOK : 1];                     // per-token RMSNorm scale
   // after the K loop smem holds: hs[64][HSTR], lg[64][LGS], pe[64][LGS], lse2[64]
   float* hs = reinterpret_cast<float*>(smem);
   float* lg = hs + RT_TOK * HSTR;  // 64 * 129 floats = 33024 bytes: lg rows stay 16-byte aligned
@@ -121,6 +128,7 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
   const int nk = d * 2 / RKB;
+  float ss = 0.0f;  // RMS: this lane's part of sum(x^2) of token wm*32 + lr
   for (int s = 0; s < RT_STAGES - 1 && s < nk; ++s) issue(s);
   // w_out (needed only by layer 2) is staged while the first K-steps are in flight:
   // loading it before them put its global round trip in front of every x load
@@ -152,6 +160,25 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
       if (i + 1 < NSUB) rdf(i + 1, (i + 1) & 1);
       acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i & 1], b0[i & 1], acc[0], 0, 0, 0);
       acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i & 1], b1[i & 1], acc[1], 0, 0, 0);
+      if constexpr (RMS) {
+        // the two waves of a token half read the same x fragments: one of them sums
+        if (wn == 0) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const float v = (float)a[i & 1][c];
+            ss = fmaf(v, v, ss);
+          }
+        }
+      }
+    }
+  }
+  if constexpr (RMS) {
+    // lanes lr and lr + 32 hold the two K halves (chunk parity) of token wm*32 + lr
+    ss += __shfl_xor(ss, 32, 64);
+    if (wn == 0 && lh == 0) {
+      const float r = 1.0f / sqrtf(ss / (float)d + eps);
+      rs_l[wm * 32 + lr] = r;
+      if (tok0 + wm * 32 + lr < T) rscale[tok0 + wm * 32 + lr] = r;
     }
   }
   __syncthreads();  // stage buffers are reused below
@@ -163,8 +190,9 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int m = wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-      hs[m * HSTR + wn * 64 + j * 32 + lr] = silu_f32(acc[j][r]);
-      if (hidden_pre && tok0 + m < T) hidden_pre[(tok0 + m) * RT_HID + wn * 64 + j * 32 + lr] = acc[j][r];
+      const float pre = RMS ? acc[j][r] * rs_l[m] : acc[j][r];
+      hs[m * HSTR + wn * 64 + j * 32 + lr] = silu_f32(pre);
+      if (hidden_pre && tok0 + m < T) hidden_pre[(tok0 + m) * RT_HID + wn * 64 + j * 32 + lr] = pre;
     }
   __syncthreads();
 
@@ -316,9 +344,10 @@ extern "C" int64_t kmoe_router_partials_len(int64_t T, int E) {
   return kmoe::ceil_div<int64_t>(T, RT_TOK) * (int64_t)(E + 1);
 }
 
-extern "C" int kmoe_router_train(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,
-                                 const void* w_out, int E, const float* logit_bias, int k, float* logits,
-                                 int64_t* topk_idx, float* topk_w, float* partials, float* hidden_pre, void* stream) {
+namespace {
+int router_launch(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in, const void* w_out,
+                  int E, const float* logit_bias, int k, float* logits, int64_t* topk_idx, float* topk_w,
+                  float* partials, float* hidden_pre, float eps, float* rscale, void* stream) {
   KMOE_REQUIRE(x && w_in && w_out && logits, KMOE_ERR_NULL, "kmoe_router: null x/w_in/w_out/logits");
   KMOE_REQUIRE(T >= 0 && T <= (int64_t)1 << 31, KMOE_ERR_SHAPE, "kmoe_router: T=%lld out of range",
                (long long)T);
@@ -335,14 +364,21 @@ extern "C" int kmoe_router_train(const void* x, const int32_t* row_index, int64_
   const uint16_t* wo = static_cast<const uint16_t*>(w_out);
   // wide K-steps (256 bytes of every row, half the barriers) when d allows and at
   // least three stages fit; 128-byte steps otherwise
-#define KMOE_ROUTER_LAUNCH(NE_)                                                                                  \
-  do {                                                                                                           \
-    if (d % 128 == 0 && rt_stages<NE_, 256>() >= 3)                                                              \
-      hipLaunchKernelGGL((router_kernel<NE_, 256>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, wo, E, \
-                         logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre);                                       \
-    else                                                                                                         \
-      hipLaunchKernelGGL((router_kernel<NE_, 128>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, wo, E, \
-                         logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre);                                       \
+#define KMOE_ROUTER_LAUNCH2(NE_, RMS_)                                                                         \
+  do {                                                                                                         \
+    if (d % 128 == 0 && rt_stages<NE_, 256>() >= 3)                                                            \
+      hipLaunchKernelGGL((router_kernel<NE_, 256, RMS_>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, \
+                         wo, E, logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre, eps, rscale);    \
+    else                                                                                                       \
+      hipLaunchKernelGGL((router_kernel<NE_, 128, RMS_>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, \
+                         wo, E, logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre, eps, rscale);    \
+  } while (0)
+#define KMOE_ROUTER_LAUNCH(NE_)             \
+  do {                                      \
+    if (rscale)                             \
+      KMOE_ROUTER_LAUNCH2(NE_, true);       \
+    else                                    \
+      KMOE_ROUTER_LAUNCH2(NE_, false);      \
   } while (0)
   if (E <= 8)
     KMOE_ROUTER_LAUNCH(8);
@@ -353,7 +389,26 @@ extern "C" int kmoe_router_train(const void* x, const int32_t* row_index, int64_
   else
     KMOE_ROUTER_LAUNCH(64);
 #undef KMOE_ROUTER_LAUNCH
+#undef KMOE_ROUTER_LAUNCH2
   return kmoe::check_launch("kmoe_router");
+}
+}  // namespace
+
+extern "C" int kmoe_router_train(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,
+                                 const void* w_out, int E, const float* logit_bias, int k, float* logits,
+                                 int64_t* topk_idx, float* topk_w, float* partials, float* hidden_pre, void* stream) {
+  return router_launch(x, row_index, T, d, w_in, w_out, E, logit_bias, k, logits, topk_idx, topk_w, partials,
+                       hidden_pre, 0.0f, nullptr, stream);
+}
+
+extern "C" int kmoe_router_rms(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in_g,
+                               const void* w_out, int E, const float* logit_bias, int k, float* logits,
+                               int64_t* topk_idx, float* topk_w, float* partials, float eps, float* rscale,
+                               void* stream) {
+  KMOE_REQUIRE(rscale, KMOE_ERR_NULL, "kmoe_router_rms: null rscale");
+  KMOE_REQUIRE(eps >= 0.0f, KMOE_ERR_SHAPE, "kmoe_router_rms: eps must be >= 0");
+  return router_launch(x, row_index, T, d, w_in_g, w_out, E, logit_bias, k, logits, topk_idx, topk_w, partials,
+                       nullptr, eps, rscale, stream);
 }
 
 extern "C" int kmoe_router(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,

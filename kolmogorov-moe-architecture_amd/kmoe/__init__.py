@@ -4,10 +4,11 @@ from ._lib import KmoeError, load as load_library
 from .config import AdvancedMoEConfig, get_5b_config, get_test_config
 from .moe import (ExpertChoiceRouter, GroupedExperts, GroupedExpertsExpertChoice, MoELayer, Router)
 from .mod import MoDMoE, MoDRouter
+from .block import MoEFFNBlock, RMSNorm
 from . import ops, kernels
 
 __all__ = [
     "AdvancedMoEConfig", "get_5b_config", "get_test_config", "MoELayer", "Router", "ExpertChoiceRouter",
     "GroupedExperts", "GroupedExpertsExpertChoice", "MoDRouter", "MoDMoE", "ops", "kernels", "KmoeError",
-    "load_library",
+    "load_library", "MoEFFNBlock", "RMSNorm",
 ]

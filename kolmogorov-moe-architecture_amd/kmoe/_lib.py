@@ -57,6 +57,9 @@ _SIGNATURES = {
     # backward pass
     "kmoe_router_train": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_gemm_gate_up_rows_gu": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp]),
+    "kmoe_router_rms": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _f32, _vp, _vp]),
+    "kmoe_gemm_gate_up_rows_scaled": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp]),
+    "kmoe_combine_residual": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _vp, _i32, _vp]),
     "kmoe_combine_bwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp]),
     "kmoe_packed_w3n_bytes": (_sz, [_i32, _i32, _i32]),
     "kmoe_packed_w13t_bytes": (_sz, [_i32, _i32, _i32]),

@@ -36,8 +36,11 @@ class AdvancedMoEConfig:
     mod_capacity_factor: float = 0.75
     mod_load_balance_loss_weight: float = 0.001
     mod_router_hidden_dim: int = 128
-    # regularisation / dtype (config.py:83-108)
+    # regularisation / normalisation / dtype (config.py:83-108)
     dropout: float = 0.1
+    residual_dropout: float = 0.1
+    norm_type: str = "rmsnorm"
+    norm_eps: float = 1e-5
     dtype: str = "bfloat16"
     device: str = "cuda"
     # ---- build-only fields (ignored by the reference) ----

@@ -77,13 +77,17 @@ class RouterOut(NamedTuple):
     w: Optional[torch.Tensor]     # (T, k) f32
     partials: torch.Tensor        # per-block aux partial sums
     hidden: Optional[torch.Tensor] = None  # (T, 128) f32 pre-activation (training router)
+    rscale: Optional[torch.Tensor] = None  # (T,) f32 RMSNorm scale 1/sqrt(mean(x^2)+eps) (rms router)
 
 
-def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=False) -> RouterOut:
+def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=False,
+           rms_eps=None) -> RouterOut:
     """logits/top-k of the reference Router (moe.py:423-462) on the HIP kernel.
 
     x2d: (rows, d) bf16; w_in: (128, d); w_out: (E, 128); row_index: optional
     int32 (T,) selecting the rows of x2d that are the tokens.
+    rms_eps: route RMSNorm(x) (embeddings.py:167-195) with the norm weight already
+    folded into w_in's columns; the result carries the per-token scale (rscale).
     """
     _need_gpu(x2d, w_in, w_out)
     x2d = _contig(x2d, _BF16)
@@ -104,6 +108,14 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=F
     partials = torch.empty(max(npart, 1), device=dev, dtype=torch.float32)
     bias = _contig(bias, torch.float32)
     hidden = torch.empty(T, _lib.ROUTER_HIDDEN, device=dev, dtype=torch.float32) if save_hidden else None
+    if rms_eps is not None:
+        if save_hidden:
+            raise ValueError("kmoe.router: rms_eps is a forward-only (inference) path")
+        rscale = torch.empty(max(T, 1), device=dev, dtype=torch.float32)
+        with _Stage("router"):
+            _lib.call("kmoe_router_rms", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
+                      ptr(logits), ptr(idx), ptr(w), ptr(partials), float(rms_eps), ptr(rscale), _stream(x2d))
+        return RouterOut(logits, idx, w, partials, None, rscale)
     with _Stage("router"):
         _lib.call("kmoe_router_train", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
                   ptr(logits), ptr(idx), ptr(w), ptr(partials), ptr(hidden), _stream(x2d))
@@ -245,11 +257,14 @@ def gemm_gate_up(xperm, xscale, offsets, pw: PackedWeights, max_rows):
     return h
 
 
-def gemm_gate_up_rows(x2d, row_index, row_token, offsets, pw: PackedWeights, max_rows, save_gu=False):
+def gemm_gate_up_rows(x2d, row_index, row_token, offsets, pw: PackedWeights, max_rows, save_gu=False,
+                      rscale=None):
     """gate_up GEMM whose A rows are x2d[row_index[row_token[r]]] (x2d[row_token[r]]
     without row_index): the dispatch gather fused into the GEMM's loads (bf16).
     save_gu (training) also returns the pre-activation gate/up values (max_rows,
-    2*F_pad) in the packed order: returns (h, gu)."""
+    2*F_pad) in the packed order: returns (h, gu).
+    rscale (T,) f32: row r's gate/up values are scaled by rscale[row_token[r]] (the
+    RMSNorm scale; pw packed from norm-folded w1/w2)."""
     if pw.fp8:
         raise ValueError("kmoe.gemm_gate_up_rows: bf16 weights only (fp8 reads quantised permuted rows)")
     _need_gpu(x2d, row_token, offsets)
@@ -257,6 +272,13 @@ def gemm_gate_up_rows(x2d, row_index, row_token, offsets, pw: PackedWeights, max
     lib = _lib.load()
     Fp = lib.kmoe_padded_ff(pw.F)
     h = torch.empty(max(max_rows, 1), Fp, device=x2d.device, dtype=_BF16)
+    if rscale is not None:
+        if save_gu:
+            raise ValueError("kmoe.gemm_gate_up_rows: rscale is a forward-only (inference) path")
+        with _Stage("gemm_gate_up"):
+            _lib.call("kmoe_gemm_gate_up_rows_scaled", ptr(x2d), ptr(row_index), x2d.shape[0], ptr(row_token),
+                      ptr(offsets), pw.E, pw.d, pw.F, max_rows, ptr(pw.w13), ptr(rscale), ptr(h), _stream(x2d))
+        return h
     if save_gu:
         gu = torch.empty(max(max_rows, 1), 2 * Fp, device=x2d.device, dtype=_BF16)
         with _Stage("gemm_gate_up"):
@@ -295,15 +317,20 @@ def grouped_ffn(xperm, xscale, offsets, pw: PackedWeights, max_rows):
     return gemm_down(h, None, offsets, pw, max_rows)
 
 
-def combine(yperm, src_row, src_w, T_out, out_map=None, scale=None, out_dtype=_BF16):
-    """y[o] = scale[s] * sum_j src_w[s,j] * yperm[src_row[s,j]] (moe.py:285-292, 132-158)."""
+def combine(yperm, src_row, src_w, T_out, out_map=None, scale=None, out_dtype=_BF16, residual=None):
+    """y[o] = scale[s] * sum_j src_w[s,j] * yperm[src_row[s,j]] (moe.py:285-292, 132-158),
+    plus residual[o] ((T_out, d), cast to out_dtype) when given (layers.py:187)."""
     fan = src_row.shape[1]
     d = yperm.shape[1]
     y = torch.empty(T_out, d, device=yperm.device, dtype=out_dtype)
     ydt = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
+    if residual is not None:
+        residual = _contig(residual, out_dtype)
+        if residual.shape != (T_out, d):
+            raise ValueError(f"kmoe.combine: residual shape {tuple(residual.shape)} != {(T_out, d)}")
     with _Stage("combine"):
-        _lib.call("kmoe_combine", ptr(yperm), d, ptr(src_row), ptr(src_w), fan, ptr(out_map), ptr(scale), T_out,
-              ptr(y), ydt, _stream(yperm))
+        _lib.call("kmoe_combine_residual", ptr(yperm), d, ptr(src_row), ptr(src_w), fan, ptr(out_map), ptr(scale),
+                  ptr(residual), T_out, ptr(y), ydt, _stream(yperm))
     return y
 
 

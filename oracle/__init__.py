@@ -25,5 +25,8 @@ Pinning (how each oracle function is checked independently, tests/test_oracle.py
   torch_port vs moe_oracle at small shapes (two independent restatements)
   moe_loss_tc_routed forward = torch_port.moe_layer_tc at its own routing; its
                      autograd gradients = finite differences (gradcheck, fp64)
+  rms_norm           torch.nn.functional.rms_norm (library routine); unit mean square at
+                     weight 1, eps 0; invariance under scaling of x; per-element brute force
+  ffn_block_tc       h + torch_port.moe_layer_tc(F.rms_norm(h)) (independent restatement)
 No function is left unpinned.
 """

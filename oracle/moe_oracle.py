@@ -344,3 +344,23 @@ def moe_forward_tc(x, w_in, w_out, w1, w2, w3, k, capacity=0, logits=None, bias=
     y = combine(yrows, dp["slot_row"].reshape(T, k), w)
     aux = aux_losses(logits, dp["counts"], T, k, E, w_lb, w_z)
     return dict(y=y, logits=np.asarray(logits), idx=idx, w=w, aux=aux, **dp)
+
+
+# ----------------------------------------------------------------------------- block boundary
+def rms_norm(x, weight, eps=1e-5, dtype=np.float64):
+    """RMSNorm.forward (embeddings.py:182-195): weight * x / sqrt(mean(x^2, -1) + eps)."""
+    x = np.asarray(x, dtype=dtype)
+    rms = np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return np.asarray(weight, dtype=dtype) * (x / rms)
+
+
+def ffn_block_tc(h, norm_w, eps, w_in, w_out, w1, w2, w3, k, capacity=0, logits=None, bias=None,
+                 dtype=np.float64):
+    """The FFN half of TransformerBlock.forward (layers.py:142-147, 184-187) without MoD
+    and without residual dropout: out = h + MoELayer(RMSNorm(h)).  `logits` as in
+    moe_forward_tc (routing from the kernel's own fp32 logits)."""
+    xn = rms_norm(h, norm_w, eps, dtype=dtype)
+    r = moe_forward_tc(xn, w_in, w_out, w1, w2, w3, k, capacity=capacity, logits=logits, bias=bias, dtype=dtype)
+    r["y"] = np.asarray(h, dtype=dtype) + r["y"]
+    r["xn"] = xn
+    return r

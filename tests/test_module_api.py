@@ -68,3 +68,25 @@ def test_cpu_input_is_rejected():
     m = MoELayer(AdvancedMoEConfig(d_model=128, n_experts=4, d_ff_expert=256), 0)
     with pytest.raises(ValueError, match="GPU"):
         m(torch.randn(1, 8, 128))
+
+
+def test_ffn_block_keys_and_norm():
+    """MoEFFNBlock: a TransformerBlock's FFN-half keys (layers.py:70-74), the config's norm
+    (embeddings.py:196-212), and the RMSNorm module's formula (embeddings.py:190-195)."""
+    cfg = AdvancedMoEConfig(d_model=256, n_experts=8, d_ff_expert=512)
+    assert (cfg.norm_type, cfg.norm_eps, cfg.residual_dropout) == ("rmsnorm", 1e-5, 0.1)
+    blk = kmoe.MoEFFNBlock(cfg, 0)
+    keys = set(blk.state_dict())
+    assert {"ffn_norm.weight", "ffn.router.router.0.weight", "ffn.router.router.2.weight",
+            "ffn.grouped_experts.w1", "ffn.grouped_experts.w2", "ffn.grouped_experts.w3"} == keys
+    x = torch.randn(3, 5, 256, dtype=torch.float64)
+    blk.ffn_norm.weight.data = torch.rand(256) + 0.5
+    ref = torch.nn.functional.rms_norm(x, (256,), blk.ffn_norm.weight.double(), eps=1e-5)
+    torch.testing.assert_close(blk.ffn_norm(x), ref, rtol=1e-6, atol=1e-7)
+    ln = kmoe.MoEFFNBlock(AdvancedMoEConfig(d_model=256, n_experts=8, d_ff_expert=512, norm_type="layernorm"), 0)
+    assert isinstance(ln.ffn_norm, torch.nn.LayerNorm)
+    # wrapping an existing layer shares its parameters
+    m = MoELayer(cfg, 0)
+    assert kmoe.MoEFFNBlock(cfg, 0, ffn=m).ffn is m
+    with pytest.raises(ValueError):
+        blk.eval()(x.float())  # the fused path refuses CPU tensors

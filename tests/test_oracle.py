@@ -418,3 +418,41 @@ def test_routed_loss_gradcheck(cap, training, bias):
     b = torch.tensor([0.3, -0.2, 0.1], dtype=torch.float64) if bias else None
     fn = lambda *a: P.moe_loss_tc_routed(*a, idx, dy, capacity=cap, bias=b, training=training)
     assert torch.autograd.gradcheck(fn, (x, w_in, w_out, w1, w2, w3), eps=1e-6, atol=1e-7, rtol=1e-5)
+
+
+# ------------------------------------------------------------------ block boundary (RMSNorm + residual)
+def test_rms_norm_pins():
+    g = torch.Generator().manual_seed(60)
+    x = torch.randn(37, 96, generator=g, dtype=torch.float64) * 3.0
+    w = 1.0 + 0.3 * torch.randn(96, generator=g, dtype=torch.float64)
+    got = O.rms_norm(x.numpy(), w.numpy(), 1e-5)
+    # library routine
+    ref = F.rms_norm(x, (96,), w, eps=1e-5).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-14)
+    # weight 1, eps 0: every row has mean square 1; scaling x changes nothing
+    u = O.rms_norm(x.numpy(), np.ones(96), 0.0)
+    np.testing.assert_allclose(np.mean(u * u, axis=1), 1.0, rtol=1e-12)
+    np.testing.assert_allclose(O.rms_norm(7.5 * x.numpy(), np.ones(96), 0.0), u, rtol=1e-12, atol=1e-14)
+    # per-element brute force on a tiny input
+    xs, ws = x[:3, :5].numpy(), w[:5].numpy()
+    bf = np.zeros_like(xs)
+    for i in range(3):
+        ms = sum(float(v) * float(v) for v in xs[i]) / 5
+        for j in range(5):
+            bf[i, j] = ws[j] * xs[i, j] / math.sqrt(ms + 1e-5)
+    np.testing.assert_allclose(O.rms_norm(xs, ws, 1e-5), bf, rtol=1e-13)
+
+
+def test_ffn_block_matches_torch_port():
+    T, d, E, k, Fd = 48, 64, 4, 2, 40
+    g = torch.Generator().manual_seed(61)
+    h = torch.randn(1, T, d, generator=g, dtype=torch.float64)
+    nw = 1.0 + 0.3 * torch.randn(d, generator=g, dtype=torch.float64)
+    w_in = torch.randn(128, d, generator=g, dtype=torch.float64) * 0.1
+    w_out = torch.randn(E, 128, generator=g, dtype=torch.float64) * 0.1
+    w1, w2 = (torch.randn(E, d, Fd, generator=g, dtype=torch.float64) * 0.1 for _ in range(2))
+    w3 = torch.randn(E, Fd, d, generator=g, dtype=torch.float64) * 0.1
+    r = O.ffn_block_tc(h[0].numpy(), nw.numpy(), 1e-5, w_in.numpy(), w_out.numpy(), w1.numpy(), w2.numpy(),
+                       w3.numpy(), k)
+    y, _ = P.moe_layer_tc(F.rms_norm(h, (d,), nw, eps=1e-5), w_in, w_out, w1, w2, w3, k, training=False)
+    np.testing.assert_allclose(r["y"], (h + y)[0].numpy(), rtol=1e-9, atol=1e-12)
