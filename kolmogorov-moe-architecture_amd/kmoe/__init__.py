@@ -5,10 +5,10 @@ from .config import AdvancedMoEConfig, get_5b_config, get_test_config
 from .moe import (ExpertChoiceRouter, GroupedExperts, GroupedExpertsExpertChoice, MoELayer, Router)
 from .mod import MoDMoE, MoDRouter
 from .block import MoEFFNBlock, RMSNorm
-from . import ops, kernels
+from . import ops, kernels, checkpoint
 
 __all__ = [
     "AdvancedMoEConfig", "get_5b_config", "get_test_config", "MoELayer", "Router", "ExpertChoiceRouter",
     "GroupedExperts", "GroupedExpertsExpertChoice", "MoDRouter", "MoDMoE", "ops", "kernels", "KmoeError",
-    "load_library", "MoEFFNBlock", "RMSNorm",
+    "load_library", "MoEFFNBlock", "RMSNorm", "checkpoint",
 ]

@@ -165,9 +165,19 @@ class _PackedExperts(nn.Module):
         self._packed = None
         self.use_fp8 = False
 
+    def _packed_key(self):
+        return tuple((w.data_ptr(), w._version, w.device) for w in (self.w1, self.w2, self.w3)) + (self.use_fp8,)
+
+    def install_packed(self, pw: ops.PackedWeights) -> None:
+        """Use `pw` (packed from exactly the current w1/w2/w3, e.g. read back from disk)
+        until a parameter changes."""
+        if (pw.E, pw.d, pw.F, pw.fp8) != (self.n_experts, self.d_model, self.d_ff, self.use_fp8):
+            raise ValueError("kmoe: packed weights do not match the experts' shapes / fp8 mode")
+        self._packed = (self._packed_key(), pw)
+
     def packed(self) -> ops.PackedWeights:
         """Packed weights, rebuilt only when a parameter changed (version counters)."""
-        key = tuple((w.data_ptr(), w._version, w.device) for w in (self.w1, self.w2, self.w3)) + (self.use_fp8,)
+        key = self._packed_key()
         if self._packed is None or self._packed[0] != key:
             with torch.no_grad():
                 pw = ops.pack_weights(self.w1.detach(), self.w2.detach(), self.w3.detach(), fp8=self.use_fp8)
