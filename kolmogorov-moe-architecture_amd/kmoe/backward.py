@@ -168,24 +168,17 @@ def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], 
     if not need_weights:
         return Grads(dx, None, dw_out, None, None, None)
 
-    # ---- weight gradients over transposed row segments
+    # ---- weight gradients, straight from the row-major buffers (transpose reads in LDS)
     dpad = _ru(d, 256)
     # dW_in = da^T x: a 128 x d output (few tiles) over K = T, split into token
     # segments of WG_SPLIT rows whose fp32 partial sums are then reduced in order
-    kt1 = lib.kmoe_wgrad_k_total(T, nseg)
-    with _stage("bwd_transpose"):
-        daT = torch.empty(_lib.ROUTER_HIDDEN, kt1, device=dev, dtype=_BF16)
-        _lib.call("kmoe_seg_transpose", ptr(da), _lib.ROUTER_HIDDEN, None, None, ptr(segs), nseg, _lib.ROUTER_HIDDEN,
-                  _lib.ROUTER_HIDDEN, ptr(daT), kt1, s)
-        xT1 = torch.empty(dpad, kt1, device=dev, dtype=_BF16)
-        _lib.call("kmoe_seg_transpose", ptr(x2d), d, None, None, ptr(segs), nseg, d, dpad, ptr(xT1), kt1, s)
     dw_in = torch.empty(_lib.ROUTER_HIDDEN, d, device=dev, dtype=_BF16)
     with _stage("bwd_wgrad_router"):
         part = torch.empty(nseg, _lib.ROUTER_HIDDEN, d, device=dev, dtype=torch.float32)
-        _lib.call("kmoe_gemm_wgrad", ptr(daT), ptr(xT1), kt1, ptr(segs), nseg, _lib.ROUTER_HIDDEN, dpad, ptr(part),
-                  None, _lib.DTYPE_F32, d, d, s)
+        _lib.call("kmoe_gemm_wgrad_rows", ptr(da), _lib.ROUTER_HIDDEN, ptr(x2d), d, T, ptr(segs), nseg,
+                  _lib.ROUTER_HIDDEN, dpad, ptr(part), None, _lib.DTYPE_F32, d, d, s)
         _lib.call("kmoe_reduce_f32", ptr(part), nseg, _lib.ROUTER_HIDDEN * d, ptr(dw_in), _lib.DTYPE_BF16, s)
-    del daT, xT1, part
+    del part
     # expert weight gradients straight from the row buffers (transpose reads in LDS)
     dw3 = torch.empty(E, F, d, device=dev, dtype=_BF16)
     with _stage("bwd_wgrad_w3"):
