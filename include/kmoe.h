@@ -289,7 +289,8 @@ int kmoe_gemm_wgrad_rows(const void* a, int64_t lda, const void* b, int64_t ldb,
                          const int32_t* offsets, int E, int M, int N, void* c, void* c2, int c_dtype, int64_t ldc,
                          int n_valid, void* stream);
 
-/* out[i] = sum_p partial[p][i] (p = 0 .. n_parts-1 in order, fp32), bf16 or f32 out. */
+/* out[i] = sum_p partial[p][i] (fp32, in a fixed order: 16 strided partial sums over
+ * p = q, q + 16, ..., then those 16 in order; bit-reproducible), bf16 or f32 out. */
 int kmoe_reduce_f32(const float* partial, int64_t n_parts, int64_t n, void* out, int out_dtype, void* stream);
 
 /* Router logit gradient (f32, (T,E)): the top-k renormalisation's softmax-over-

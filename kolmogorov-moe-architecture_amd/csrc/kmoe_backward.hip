@@ -293,17 +293,32 @@ __global__ __launch_bounds__(256) void router_mlp_bwd_kernel(const float* __rest
   }
 }
 
-// out[i] = sum_b partial[b][i] in block order (fixed, bit-reproducible); bf16 or f32 out.
-__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ partial, int64_t nblk,
-                                                              int64_t n, void* __restrict__ out, bool out_f32) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
+// out[i] = sum_b partial[b][i] (bf16 or f32 out).
+// 64 outputs per workgroup (lane = output, coalesced across the wave), RWAVES waves
+// each summing every RWAVES-th partial in order, then the RWAVES sums in wave order:
+// a fixed order, so the result is bit-reproducible.  (One thread per output summing all
+// partials serially left the 256-partial router reduction latency-bound: 8 workgroups.)
+constexpr int RWAVES = 16;
+__global__ __launch_bounds__(64 * RWAVES) void reduce_partials_kernel(const float* __restrict__ partial, int64_t nblk,
+                                                                      int64_t n, void* __restrict__ out, bool out_f32) {
+  __shared__ float red[RWAVES][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t i = (int64_t)blockIdx.x * 64 + lane;
   float s = 0.0f;
-  for (int64_t b = 0; b < nblk; ++b) s += partial[b * n + i];
+  if (i < n) {
+#pragma unroll 4
+    for (int64_t b = w; b < nblk; b += RWAVES) s += partial[b * n + i];
+  }
+  red[w][lane] = s;
+  __syncthreads();
+  if (w != 0 || i >= n) return;
+  float t = 0.0f;
+#pragma unroll
+  for (int q = 0; q < RWAVES; ++q) t += red[q][lane];
   if (out_f32)
-    static_cast<float*>(out)[i] = s;
+    static_cast<float*>(out)[i] = t;
   else
-    static_cast<uint16_t*>(out)[i] = f32_to_bf16(s);
+    static_cast<uint16_t*>(out)[i] = f32_to_bf16(t);
 }
 
 // w_in (128, d) -> packed rows of w_in^T: (round_up(d, 256), 128 + 64) bf16, row i =
@@ -429,8 +444,8 @@ extern "C" int kmoe_router_mlp_bwd(const float* dlogits, const float* hidden_pre
     KMOE_MB(64);
 #undef KMOE_MB
   const int64_t n = (int64_t)E * RH;
-  hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(n, 256)), dim3(256), 0, s, part,
-                     nblk, n, dw_out, dw_dtype == KMOE_DTYPE_F32);
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(n, 64)), dim3(64 * RWAVES), 0, s,
+                     part, nblk, n, dw_out, dw_dtype == KMOE_DTYPE_F32);
   return kmoe::check_launch("kmoe_router_mlp_bwd");
 }
 
@@ -453,7 +468,7 @@ extern "C" int kmoe_reduce_f32(const float* partial, int64_t n_parts, int64_t n,
   KMOE_REQUIRE(n_parts >= 1 && n >= 0, KMOE_ERR_SHAPE, "kmoe_reduce_f32: bad shape");
   KMOE_REQUIRE(out_dtype == KMOE_DTYPE_BF16 || out_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE, "kmoe_reduce_f32: dtype");
   if (n == 0) return KMOE_OK;
-  hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(n, 256)), dim3(256), 0,
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(n, 64)), dim3(64 * RWAVES), 0,
                      kmoe::as_stream(stream), partial, n_parts, n, out, out_dtype == KMOE_DTYPE_F32);
   return kmoe::check_launch("kmoe_reduce_f32");
 }
