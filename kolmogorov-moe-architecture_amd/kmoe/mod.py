@@ -63,15 +63,19 @@ class MoDMoE(nn.Module):
         self.ffn = MoELayer(config, layer_idx)
         self.aux_loss = 0.0
 
-    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+    def forward(self, hidden_states: torch.Tensor, residual: torch.Tensor = None) -> torch.Tensor:
+        """ffn_output; with `residual` (B, S, d), residual + ffn_output (layers.py:187) from the same
+        combine: unselected tokens get the residual row, selected ones residual + weighted output."""
         B, S, d = hidden_states.shape
         x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
         sel = self.ffn_mod_router.select(x)
         keep = sel.sel_idx.shape[1]
         out_dtype = torch.float32 if hidden_states.dtype == torch.float32 else torch.bfloat16
+        res2d = None if residual is None else residual.reshape(B * S, d)
         y, r, disp = self.ffn.forward_rows(x.reshape(B * S, d), T=B * keep, row_index=sel.token_rows,
                                            T_out=B * S, out_map=sel.out_map, scale=sel.sel_w.reshape(-1),
-                                           out_dtype=out_dtype)
+                                           out_dtype=out_dtype, residual=res2d)
         self.ffn._set_token_choice_aux(r, disp, B * keep)
         self.aux_loss = self.ffn.aux_loss
-        return _forward_only(y.view(B, S, d).to(hidden_states.dtype), hidden_states, *self.parameters())
+        ins = (hidden_states,) if residual is None else (hidden_states, residual)
+        return _forward_only(y.view(B, S, d).to(hidden_states.dtype), *ins, *self.parameters())

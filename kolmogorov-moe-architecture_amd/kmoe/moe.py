@@ -191,8 +191,8 @@ class GroupedExperts(_PackedExperts):
     capacity = 0  # 0 = no capacity limit (the reference's behaviour)
 
     def run(self, x2d, expert_indices, expert_weights, row_index=None, T_out=None, out_map=None, scale=None,
-            out_dtype=torch.bfloat16):
-        """dispatch -> grouped GEMMs -> combine; returns (y, DispatchOut)."""
+            out_dtype=torch.bfloat16, residual=None):
+        """dispatch -> grouped GEMMs -> combine (+ residual, added in the combine); returns (y, DispatchOut)."""
         E = self.n_experts
         pw = self.packed()
         T, k = expert_indices.shape
@@ -207,7 +207,8 @@ class GroupedExperts(_PackedExperts):
             h = ops.gemm_gate_up_rows(x2d, row_index, disp.row_token, disp.offsets, pw, T * k)
             yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k),
-                        T if T_out is None else T_out, out_map=out_map, scale=scale, out_dtype=out_dtype)
+                        T if T_out is None else T_out, out_map=out_map, scale=scale, out_dtype=out_dtype,
+                        residual=residual)
         return y, disp
 
     def forward(self, x: torch.Tensor, expert_indices: torch.Tensor, expert_weights: torch.Tensor) -> torch.Tensor:
@@ -390,7 +391,7 @@ class MoELayer(nn.Module):
         return _forward_only(y.view(B, S, d).to(hidden_states.dtype), hidden_states, *self.parameters())
 
     def forward_rows(self, x2d, T, row_index=None, T_out=None, out_map=None, scale=None,
-                     out_dtype=torch.bfloat16):
+                     out_dtype=torch.bfloat16, residual=None):
         """Token-choice MoE over rows row_index[t] (t < T) of x2d; kernel-level entry
         used by the MoD composition.  Returns (y, RouterOut, DispatchOut)."""
         if x2d.dtype != torch.bfloat16:
@@ -399,7 +400,7 @@ class MoELayer(nn.Module):
         ge = self.grouped_experts
         ge.capacity = ops.capacity_of(self.capacity_factor, T, self.top_k, self.n_experts) if self.drop_overflow else 0
         y, disp = ge.run(x2d, r.idx, r.w, row_index=row_index, T_out=T_out, out_map=out_map, scale=scale,
-                         out_dtype=out_dtype)
+                         out_dtype=out_dtype, residual=residual)
         return y, r, disp
 
     def _set_token_choice_aux(self, r, disp, T):

@@ -264,3 +264,28 @@ def test_ffn_block_training_path(dev):
     assert relL2(npf(blk.ffn_norm.weight.grad), nw64.grad.numpy()) <= 2e-2
     for got, want in zip((ge.w1.grad, ge.w2.grad, ge.w3.grad), params[2:]):
         assert relL2(npf(got), want.grad.numpy()) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mod_moe_residual(dev, dtype):
+    """MoDMoE(h, residual) = residual + MoDMoE(h) (layers.py:175-187) from one combine:
+    unselected tokens are the residual itself, selected ones within one rounding of the sum."""
+    from kmoe import MoDMoE
+    print(f"mod residual {dtype}", flush=True)
+    cfg = AdvancedMoEConfig(d_model=256, n_experts=8, moe_top_k=2, d_ff_expert=352, mod_capacity_factor=0.5)
+    torch.manual_seed(11)
+    m = MoDMoE(cfg).to(dev, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(12)
+    h = torch.randn(2, 300, 256, generator=g).to(dev, dtype)
+    res = torch.randn(2, 300, 256, generator=g).to(dev, dtype)
+    with torch.no_grad():
+        a = m(h)
+        b = m(h, residual=res)
+    torch.cuda.synchronize()
+    sel = (a != 0).any(-1)
+    assert 0.3 < sel.float().mean().item() < 0.7
+    assert torch.equal(b[~sel], res[~sel])
+    want = (res.double() + a.double())[sel]
+    tol = 2.0 ** -22 if dtype == torch.float32 else 2.0 ** -8
+    err = (b[sel].double() - want).abs()
+    assert bool((err <= want.abs() * tol + a.double().abs()[sel] * tol + 1e-30).all())
