@@ -259,30 +259,14 @@ int kmoe_gemm_grouped(const void* a, const int32_t* offsets, int E, int K, int64
 int kmoe_swiglu_bwd(const void* dh, const void* gu, int64_t rows, const int32_t* n_rows_dev, int F, void* dgu,
                     void* stream);
 
-/* Segmented transpose into the weight-gradient operand layout: expert e's rows
- * become columns [koff_e, koff_e + n_e) of dst (dst_rows, k_total), koff_e =
- * sum_{e'<e} round_up(n_e', 64), zero padded.  Row r reads src row
- * row_index[row_token[r]] / row_token[r] / r.  k_total: kmoe_wgrad_k_total.   */
-int64_t kmoe_wgrad_k_total(int64_t n_rows, int E);
-int kmoe_seg_transpose(const void* src, int64_t ld_src, const int32_t* row_token, const int32_t* row_index,
-                       const int32_t* offsets, int E, int cols, int dst_rows, void* dst, int64_t k_total,
-                       void* stream);
-
-/* Weight gradients: c_e[m, n] = sum over expert e's rows r of at[m, r] * bt[n, r]
- * (at (M, k_total), bt (N, k_total) from kmoe_seg_transpose; N a multiple of 256).
- * c: (E, M, ldc) bf16 (c_dtype BF16) or f32 (F32: the raw fp32 sums, e.g. split-K
- * partials over row segments), columns < n_valid.  With c2 (bf16 only; dW1/dW2 split
- * of the packed order): columns of 256-column tile nt go to c (first 128) and c2
- * (last 128) at column nt*128.  dW3 = h^T dyperm: at = h^T, bt = dyperm^T;
- * dW1, dW2 = x^T [dg|du]: at = x^T (gathered), bt = dgu^T, c = dW1, c2 = dW2.   */
-int kmoe_gemm_wgrad(const void* at, const void* bt, int64_t k_total, const int32_t* offsets, int E, int M, int N,
-                    void* c, void* c2, int c_dtype, int64_t ldc, int n_valid, void* stream);
-
 /* Weight gradients read straight from row-major row buffers (no transposes):
  *   c_e[m, n] = sum over expert e's rows r of a[r, m] * b[r, n]
  * a (max_rows, lda) and b (max_rows, ldb) bf16, rows of expert e = [offsets[e],
- * offsets[e+1]); c as kmoe_gemm_wgrad (bf16 with optional c2 split, or f32), n_valid
- * and ldc multiples of 8.  dW3 = h^T dyperm: a = h (lda F_pad), b = dyperm (ldb d), M = F,
+ * offsets[e+1]); rows past an expert's end read as zero.  c: (E, M, ldc) bf16 (c_dtype
+ * BF16) or f32 (F32: the raw fp32 sums, e.g. split-K partials over row segments),
+ * columns < n_valid; with c2 (bf16 only; the dW1/dW2 split of the packed order) the
+ * columns of 256-column tile nt go to c (first 128) and c2 (last 128) at column
+ * nt*128.  N a multiple of 256; n_valid and ldc multiples of 8.  dW3 = h^T dyperm: a = h (lda F_pad), b = dyperm (ldb d), M = F,
  * N = round_up(d, 256);  dW1, dW2: a = the permuted x rows (kmoe_dispatch's xperm),
  * b = dgu (ldb 2*F_pad), M = d, N = 2*F_pad, c = dW1, c2 = dW2.                 */
 int kmoe_gemm_wgrad_rows(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t max_rows,
@@ -304,7 +288,7 @@ int kmoe_router_dlogits(const float* logits, int64_t T, int E, const int64_t* to
 /* Router MLP backward: da = (dl . w_out) * silu'(a) -> (T, 128) bf16 and
  * dw_out = dl^T silu(a) -> (E, 128) (bf16 or f32), reduced in a fixed order.
  * hidden_pre: a from kmoe_router_train.  workspace: kmoe_router_bwd_workspace_bytes.
- * dw_in = da^T x and dx += da . w_in follow with kmoe_gemm_wgrad / kmoe_gemm_grouped
+ * dw_in = da^T x and dx += da . w_in follow with kmoe_gemm_wgrad_rows / kmoe_gemm_grouped
  * (w_in^T packed by kmoe_pack_w_in_t).                                       */
 size_t kmoe_router_bwd_workspace_bytes(int64_t T, int E);
 int kmoe_router_mlp_bwd(const float* dlogits, const float* hidden_pre, int64_t T, int E, const void* w_out,

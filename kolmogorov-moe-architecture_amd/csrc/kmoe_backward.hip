@@ -95,96 +95,6 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t* __restr
   }
 }
 
-// Segmented transpose for the weight gradients: expert e's rows [off_e, off_e + n_e)
-// of src (rows, cols; row r read from src row rt[r], rt = row_index[row_token[r]],
-// row_token[r] or r) become columns [koff_e, koff_e + n_e) of dst (dst_rows, k_total),
-// koff_e = sum_{e' < e} round_up(n_e', 64); columns [n_e, round_up(n_e, 64)) of the
-// segment, columns past the last segment and rows [cols, dst_rows) are zero.
-// One 64 x 64 tile per workgroup, through LDS.
-constexpr int TT = 64;
-__global__ __launch_bounds__(256) void seg_transpose_kernel(const uint16_t* __restrict__ src, int64_t ld_src,
-                                                            const int32_t* __restrict__ row_token,
-                                                            const int32_t* __restrict__ row_index,
-                                                            const int32_t* __restrict__ offsets, int E, int cols,
-                                                            uint16_t* __restrict__ dst, int64_t k_total) {
-  __shared__ uint16_t tile[TT][TT + 2];
-  __shared__ int seg[3];  // first source row of the tile, rows valid in the tile
-  const int tid = threadIdx.x;
-  const int64_t kk0 = (int64_t)blockIdx.x * TT;
-  const int c0 = blockIdx.y * TT;
-  if (tid < 64) {
-    const int lane = tid;
-    int lo = 0, n = 0;
-    if (lane < E) {
-      lo = offsets[lane];
-      n = offsets[lane + 1] - lo;
-    }
-    const int pad = (n + TT - 1) / TT * TT;
-    int incl = pad;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int u = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += u;
-    }
-    const int koff = incl - pad;
-    const bool mine = lane < E && kk0 >= koff && kk0 < koff + pad;
-    const uint64_t m = __ballot(mine);
-    if (lane == 0) {
-      seg[0] = 0;
-      seg[1] = 0;
-    }
-    if (m) {
-      const int e = __builtin_ctzll(m);
-      if (lane == e) {
-        seg[0] = lo + (int)(kk0 - koff);
-        seg[1] = min(TT, n - (int)(kk0 - koff));
-      }
-    }
-  }
-  __syncthreads();
-  const int r0 = seg[0], nvalid = seg[1];
-  // load: 64 source rows x 64 columns = 512 chunks of 8 columns
-  for (int c = tid; c < TT * (TT / 8); c += 256) {
-    const int i = c / (TT / 8), q = c % (TT / 8);
-    i32x4_t v = {0, 0, 0, 0};
-    const int col = c0 + q * 8;
-    if (i < nvalid && col < cols) {
-      int64_t r = r0 + i;
-      if (row_token) r = row_token[r];
-      if (row_index) r = row_index[r];
-      if (col + 8 <= cols) {
-        v = *reinterpret_cast<const i32x4_t*>(src + r * ld_src + col);
-      } else {
-        uint16_t tmp[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) tmp[u] = col + u < cols ? src[r * ld_src + col + u] : (uint16_t)0;
-        v = *reinterpret_cast<const i32x4_t*>(tmp);
-      }
-    }
-    const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
-    uint16_t* tr = &tile[i][q * 8];
-    tr[0] = (uint16_t)w0;
-    tr[1] = (uint16_t)(w0 >> 16);
-    tr[2] = (uint16_t)w1;
-    tr[3] = (uint16_t)(w1 >> 16);
-    tr[4] = (uint16_t)w2;
-    tr[5] = (uint16_t)(w2 >> 16);
-    tr[6] = (uint16_t)w3;
-    tr[7] = (uint16_t)(w3 >> 16);
-  }
-  __syncthreads();
-  // store: 64 destination rows (source columns) x 64 k positions
-  for (int c = tid; c < TT * (TT / 8); c += 256) {
-    const int rr = c / (TT / 8), q = c % (TT / 8);
-    uint32_t w[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      w[u] = (uint32_t)tile[q * 8 + 2 * u][rr] | ((uint32_t)tile[q * 8 + 2 * u + 1][rr] << 16);
-    *reinterpret_cast<i32x4_t*>(dst + (int64_t)(c0 + rr) * k_total + kk0 + q * 8) =
-        i32x4_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-  }
-}
-
 // Router logit gradient, one thread per token (E <= 64):
 //   top-k renormalisation (w_j = p_j / sum_sel p = softmax over the selected logits):
 //     dl[i_j] += w_j (dw_j - sum_l w_l dw_l)
@@ -368,25 +278,6 @@ extern "C" int kmoe_swiglu_bwd(const void* dh, const void* gu, int64_t rows, con
                      static_cast<const uint16_t*>(dh), static_cast<const uint16_t*>(gu), rows, n_rows_dev, Fp,
                      static_cast<uint16_t*>(dgu));
   return kmoe::check_launch("kmoe_swiglu_bwd");
-}
-
-extern "C" int kmoe_seg_transpose(const void* src, int64_t ld_src, const int32_t* row_token, const int32_t* row_index,
-                                  const int32_t* offsets, int E, int cols, int dst_rows, void* dst, int64_t k_total,
-                                  void* stream) {
-  KMOE_REQUIRE(src && offsets && dst, KMOE_ERR_NULL, "kmoe_seg_transpose: null buffer");
-  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_seg_transpose: E=%d", E);
-  KMOE_REQUIRE(cols > 0 && dst_rows >= cols && dst_rows % TT == 0, KMOE_ERR_SHAPE,
-               "kmoe_seg_transpose: cols=%d, dst_rows=%d (a multiple of %d >= cols)", cols, dst_rows, TT);
-  KMOE_REQUIRE(k_total > 0 && k_total % TT == 0, KMOE_ERR_SHAPE, "kmoe_seg_transpose: k_total=%lld",
-               (long long)k_total);
-  KMOE_REQUIRE(ld_src >= cols && ld_src % 8 == 0, KMOE_ERR_SHAPE, "kmoe_seg_transpose: ld_src=%lld",
-               (long long)ld_src);
-  KMOE_REQUIRE(!row_index || row_token, KMOE_ERR_NULL, "kmoe_seg_transpose: row_index needs row_token");
-  const dim3 grid((unsigned)(k_total / TT), (unsigned)(dst_rows / TT));
-  hipLaunchKernelGGL(seg_transpose_kernel, grid, dim3(256), 0, kmoe::as_stream(stream),
-                     static_cast<const uint16_t*>(src), ld_src, row_token, row_index, offsets, E, cols,
-                     static_cast<uint16_t*>(dst), k_total);
-  return kmoe::check_launch("kmoe_seg_transpose");
 }
 
 extern "C" int kmoe_router_dlogits(const float* logits, int64_t T, int E, const int64_t* topk_idx, const float* topk_w,

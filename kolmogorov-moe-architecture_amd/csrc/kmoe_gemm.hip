@@ -242,21 +242,20 @@ struct GemmArgs {
   uint16_t* C;
   int64_t ldc;
   int n_valid;
-  // plain (non gate/up) tiles: when set, output columns [128, 256) of a full tile go
-  // to C2 and columns [0, 128) to C, both at column nt*128 (the gate and up halves
-  // of a w13-ordered tile: the dw1 / dw2 split of the weight gradient)
+  // weight-gradient tiles (OUT_SPLIT): output columns [128, 256) of a tile go to C2
+  // and columns [0, 128) to C, both at column nt*128 (the gate and up halves of a
+  // w13-ordered tile: the dw1 / dw2 split)
   uint16_t* C2;
   // gate/up tiles: when set, the pre-activation gate and up values are also written
   // (bf16) in the packed column order, row stride 2*ldc: the backward's saved g, u
   uint16_t* gu_out;
-  // plain tiles: when set, the fp32 accumulators are stored here (row stride ldc)
-  // instead of bf16 to C (split-K partial sums)
+  // weight-gradient tiles (OUT_F32): the fp32 accumulators are stored here (row
+  // stride ldc) instead of bf16 to C (split-K partial sums)
   float* Cf;
 };
 
-// Output of a plain (non gate/up) tile: bf16 to C; bf16 with the column tile split
+// Output of a weight-gradient tile: bf16 to C; bf16 with the column tile split
 // between C and C2 (the gate and up halves of a w13-ordered tile); fp32 to Cf.
-// Compile-time, so that the forward kernels carry none of the other epilogues.
 constexpr int OUT_BF16 = 0, OUT_SPLIT = 1, OUT_F32 = 2;
 
 // One output tile: rows [m0, min(m0 + 256, m_end)) of expert e against B rows of
@@ -268,8 +267,7 @@ constexpr int OUT_BF16 = 0, OUT_SPLIT = 1, OUT_F32 = 2;
 // RSCALE (bf16 gathered gate/up tiles): a_scale[row_token[r]] scales row r's gate and
 // up values before the SiLU (the per-token RMSNorm scale of x: the norm weight is
 // folded into the packed w1 / w2 rows, and a per-row scale commutes with the product).
-template <bool GATE_UP, bool FP8, bool GATHER, int WNB, int OUT = OUT_BF16, bool SAVE_GU = false,
-          bool RSCALE = false>
+template <bool GATE_UP, bool FP8, bool GATHER, int WNB, bool SAVE_GU = false, bool RSCALE = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e, int m0, int m_end, int nt,
                                           int q) {
   static_assert(WNB == 4 || WNB == 2 || (WNB == 1 && !GATE_UP), "tile width");
@@ -437,23 +435,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   // (VALU, no LDS round trip): for the rows of r = 2p and 2p+1, an even lane packs
   // its own and its right neighbour's value of row 2p, an odd lane its left
   // neighbour's and its own of row 2p+1, so every lane writes 4 bytes, unmasked.
-  static_assert(OUT == OUT_BF16 || (!GATE_UP && !FP8), "split / fp32 outputs are for bf16 plain tiles");
   static_assert(!SAVE_GU || (GATE_UP && !FP8), "g/u saving is for bf16 gate/up tiles");
-  if constexpr (OUT == OUT_F32) {
-    // fp32 out straight from the accumulators: for each (block, r) the 32 lanes of a
-    // half-wave store 32 consecutive columns (128 bytes) of one row
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int j = 0; j < WNB; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-          const int col = nt * 256 + q * (64 * WNB) + b_lds_row<false, WNB>(wn, j, lr);
-          if (row < m_end && col < g.n_valid) g.Cf[(int64_t)row * g.ldc + col] = acc[mi][j][r];
-        }
-    return;
-  }
   constexpr int NC = GATE_UP ? 32 * WNB : 64 * WNB;  // output columns of the tile
   constexpr int NJ = GATE_UP ? WNB / 2 : WNB;        // output column blocks per wave
   constexpr int OSTR = NC * 2 + 16;                  // LDS row stride (bytes)
@@ -516,19 +498,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   __syncthreads();
   constexpr int OCPR = NC * 2 / 16;  // 16-byte chunks per output row
   const int col0 = (GATE_UP ? nt * 128 : nt * 256) + q * NC;
-  constexpr bool split_c = OUT == OUT_SPLIT;
   for (int c = tid; c < BM * OCPR; c += GEMM_THREADS) {
     const int trow = c / OCPR, ch = c % OCPR;
     const int grow = m0 + trow;
-    uint16_t* dst = g.C;
-    int gcol = col0 + ch * 8;
-    if constexpr (split_c) {
-      const int cf = q * NC + ch * 8;  // column within the full tile
-      dst = cf < 128 ? g.C : g.C2;
-      gcol = nt * 128 + (cf & 127);
-    }
+    const int gcol = col0 + ch * 8;
     if (grow < m_end && gcol < g.n_valid)
-      *reinterpret_cast<i32x4_t*>(dst + (int64_t)grow * g.ldc + gcol) =
+      *reinterpret_cast<i32x4_t*>(g.C + (int64_t)grow * g.ldc + gcol) =
           *reinterpret_cast<const i32x4_t*>(lds + trow * OSTR + ch * 16);
   }
 
@@ -610,83 +585,11 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   dense_tile(t, st.n_slots, n_tiles, slot, nt);
   find_slot(st, E, slot, e, m0, m_end);
   if (L < base || split == 1)
-    gemm_tile<GATE_UP, FP8, GATHER, 4, OUT_BF16, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, 0);
+    gemm_tile<GATE_UP, FP8, GATHER, 4, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, 0);
   else if (split == 2)
-    gemm_tile<GATE_UP, FP8, GATHER, 2, OUT_BF16, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, q);
+    gemm_tile<GATE_UP, FP8, GATHER, 2, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, q);
   else if constexpr (!GATE_UP)
-    gemm_tile<GATE_UP, FP8, GATHER, 1, OUT_BF16, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, q);
-}
-
-// ---------------------------------------------------------------- weight gradients
-// Row segments are transposed and padded per expert: expert e's rows occupy columns
-// [koff_e, koff_e + kpad_e) of the K axis, kpad_e = counts[e] rounded up to the
-// K-step (64), zero filled.  koff_e of expert e from the offsets (lane-parallel).
-constexpr int WG_KALIGN = KB / 2;  // bf16 elements per K-step
-__device__ __forceinline__ void wgrad_segment(const int32_t* __restrict__ offsets, int E, int e, int& koff, int& kpad) {
-  const int lane = threadIdx.x & 63;
-  int c = 0;
-  if (lane < E) c = round_up(offsets[lane + 1] - offsets[lane], WG_KALIGN);
-  int pre = lane < e ? c : 0;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) pre += __shfl_xor(pre, o, 64);
-  koff = __builtin_amdgcn_readfirstlane(pre);
-  kpad = __builtin_amdgcn_readlane(c, e);
-}
-
-// C_e[m, n] = sum over expert e's rows r of At[m, r] * Bt[n, r] for every expert (the
-// weight gradients dW = X_e^T dY_e of the grouped GEMMs, contraction over a ragged
-// number of rows).  Workgroup -> (expert, row tile, column tile); the tile itself is
-// gemm_tile on the expert's K range (At rows are the output rows, Bt rows the output
-// columns, both K-contiguous).  An expert without rows writes a zero tile.
-template <int OUT>
-__global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void wgrad_kernel(
-    GemmArgs g, const int32_t* __restrict__ offsets, int E, int M, int n_mt, int n_nt, int64_t c_expert_stride) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[GEMM_LDS];
-  const int n_all = E * n_mt * n_nt;
-  const int L = blockIdx.x;
-  if (L >= n_all) return;
-  const int t = (n_all % (NXCD * SB_TILES)) == 0 ? xcd_tile(L) : L;
-  // within an expert, row tiles in groups of 4 walked column tile by column tile (the
-  // forward's dense order): the 32 tiles an XCD takes at a time share 4 At and 8 Bt
-  // K-slices in its L2 (row-major order shared ~2 and ~22: 5x the operand fetch)
-  const int per_e = n_mt * n_nt;
-  const int e = t / per_e, rem = t - e * per_e;
-  int mt, nt;
-  dense_tile(rem, n_mt, n_nt, mt, nt);
-  int koff, kpad;
-  wgrad_segment(offsets, E, e, koff, kpad);
-  GemmArgs ge = g;
-  ge.C = g.C ? g.C + (int64_t)e * c_expert_stride : nullptr;
-  ge.C2 = g.C2 ? g.C2 + (int64_t)e * c_expert_stride : nullptr;
-  ge.Cf = g.Cf ? g.Cf + (int64_t)e * c_expert_stride : nullptr;
-  const int m0 = mt * BM;
-  if (kpad == 0 && OUT == OUT_F32) {
-    for (int c = threadIdx.x; c < BM * 256; c += GEMM_THREADS) {
-      const int grow = m0 + c / 256, gcol = nt * 256 + c % 256;
-      if (grow < M && gcol < g.n_valid) ge.Cf[(int64_t)grow * g.ldc + gcol] = 0.0f;
-    }
-    return;
-  }
-  if (kpad == 0) {
-    // no rows: a zero gradient tile
-    for (int c = threadIdx.x; c < BM * 32; c += GEMM_THREADS) {
-      const int trow = c / 32, ch = c % 32;
-      const int grow = m0 + trow;
-      uint16_t* dst = ge.C;
-      int gcol = nt * 256 + ch * 8;
-      if (OUT == OUT_SPLIT) {
-        dst = ch < 16 ? ge.C : ge.C2;
-        gcol = nt * 128 + (ch & 15) * 8;
-      }
-      if (grow < M && gcol < g.n_valid)
-        *reinterpret_cast<i32x4_t*>(dst + (int64_t)grow * g.ldc + gcol) = i32x4_t{0, 0, 0, 0};
-    }
-    return;
-  }
-  ge.A = g.A + (int64_t)koff * 2;
-  ge.B = g.B + (int64_t)koff * 2;
-  ge.k_bytes = kpad * 2;
-  gemm_tile<false, false, false, 4, OUT>(ge, lds, 0, m0, M, nt, 0);
+    gemm_tile<GATE_UP, FP8, GATHER, 1, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, q);
 }
 
 // ---------------------------------------------------------------- weight gradients, row-major operands
@@ -1388,50 +1291,6 @@ extern "C" int kmoe_gemm_grouped(const void* a, const int32_t* offsets, int E, i
                              kmoe::as_stream(stream));
   if (rc) return rc;
   return kmoe::check_launch("kmoe_gemm_grouped");
-}
-
-extern "C" int64_t kmoe_wgrad_k_total(int64_t n_rows, int E) {
-  return kmoe::ceil_div<int64_t>(n_rows, WG_KALIGN) * WG_KALIGN + (int64_t)E * WG_KALIGN;
-}
-
-extern "C" int kmoe_gemm_wgrad(const void* at, const void* bt, int64_t k_total, const int32_t* offsets, int E, int M,
-                               int N, void* c, void* c2, int c_dtype, int64_t ldc, int n_valid, void* stream) {
-  KMOE_REQUIRE(at && bt && offsets && c, KMOE_ERR_NULL, "kmoe_gemm_wgrad: null buffer");
-  KMOE_REQUIRE(c_dtype == KMOE_DTYPE_BF16 || (c_dtype == KMOE_DTYPE_F32 && c2 == nullptr), KMOE_ERR_DTYPE,
-               "kmoe_gemm_wgrad: c dtype must be bf16, or f32 without c2");
-  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_gemm_wgrad: E=%d out of range", E);
-  KMOE_REQUIRE(M > 0 && N > 0 && N % BN == 0, KMOE_ERR_SHAPE, "kmoe_gemm_wgrad: M=%d, N=%d (N a multiple of %d)", M,
-               N, BN);
-  KMOE_REQUIRE(k_total > 0 && k_total % WG_KALIGN == 0, KMOE_ERR_SHAPE,
-               "kmoe_gemm_wgrad: k_total=%lld must be a positive multiple of %d", (long long)k_total, WG_KALIGN);
-  KMOE_REQUIRE(n_valid > 0 && n_valid <= ldc, KMOE_ERR_SHAPE, "kmoe_gemm_wgrad: n_valid=%d, ldc=%lld", n_valid,
-               (long long)ldc);
-  KMOE_REQUIRE((int64_t)(BM + 1) * k_total * 2 < ((int64_t)1 << 31), KMOE_ERR_SHAPE,
-               "kmoe_gemm_wgrad: k_total=%lld too large for 32-bit tile offsets", (long long)k_total);
-  GemmArgs g{};
-  g.A = static_cast<const uint8_t*>(at);
-  g.lda_bytes = k_total * 2;
-  g.B = static_cast<const uint8_t*>(bt);
-  g.b_expert_rows = 0;
-  g.ldb_bytes = k_total * 2;
-  const bool f32 = c_dtype == KMOE_DTYPE_F32;
-  g.C = f32 ? nullptr : static_cast<uint16_t*>(c);
-  g.C2 = static_cast<uint16_t*>(c2);
-  g.Cf = f32 ? static_cast<float*>(c) : nullptr;
-  g.ldc = ldc;
-  g.n_valid = n_valid;
-  const int n_mt = kmoe::ceil_div(M, BM), n_nt = N / BN;
-  const int64_t blocks = (int64_t)E * n_mt * n_nt;
-  const dim3 grid((unsigned)blocks), block(GEMM_THREADS);
-  hipStream_t s = kmoe::as_stream(stream);
-  const int64_t stride = (int64_t)M * ldc;
-  if (f32)
-    hipLaunchKernelGGL(wgrad_kernel<OUT_F32>, grid, block, 0, s, g, offsets, E, M, n_mt, n_nt, stride);
-  else if (c2)
-    hipLaunchKernelGGL(wgrad_kernel<OUT_SPLIT>, grid, block, 0, s, g, offsets, E, M, n_mt, n_nt, stride);
-  else
-    hipLaunchKernelGGL(wgrad_kernel<OUT_BF16>, grid, block, 0, s, g, offsets, E, M, n_mt, n_nt, stride);
-  return kmoe::check_launch("kmoe_gemm_wgrad");
 }
 
 extern "C" int kmoe_gemm_wgrad_rows(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t max_rows,

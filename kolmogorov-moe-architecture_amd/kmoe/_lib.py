@@ -66,9 +66,6 @@ _SIGNATURES = {
     "kmoe_pack_weights_bwd": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "kmoe_gemm_grouped": (_i32, [_vp, _vp, _i32, _i32, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp]),
     "kmoe_swiglu_bwd": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _vp]),
-    "kmoe_wgrad_k_total": (_i64, [_i64, _i32]),
-    "kmoe_seg_transpose": (_i32, [_vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _vp]),
-    "kmoe_gemm_wgrad": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _i64, _i32, _vp]),
     "kmoe_reduce_f32": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
     "kmoe_gemm_wgrad_rows": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _i64, _i32,
                                     _vp]),
