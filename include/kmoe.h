@@ -53,6 +53,12 @@ extern "C" {
 
 const char* kmoe_last_error(void);
 int kmoe_abi_version(void);
+/* Version of the packed weight layouts written by kmoe_pack_weights /
+ * kmoe_pack_weights_bwd (row order, padding, scale placement).  It changes whenever
+ * those layouts change, so a packed cache saved by another build can be refused.
+ * No counterpart in the reference (its experts have no derived weight layout).  */
+#define KMOE_PACK_LAYOUT 2
+int kmoe_pack_layout_version(void);
 
 /* ------------------------------------------------------------------------ */
 /* (a) Router — replaces Router.forward (moe.py:423-462) and the logits half of

@@ -46,3 +46,5 @@ int cu_count() {
 extern "C" const char* kmoe_last_error(void) { return g_last_error; }
 
 extern "C" int kmoe_abi_version(void) { return KMOE_ABI_VERSION; }
+
+extern "C" int kmoe_pack_layout_version(void) { return KMOE_PACK_LAYOUT; }

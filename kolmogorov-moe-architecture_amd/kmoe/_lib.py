@@ -31,6 +31,7 @@ _sz = ctypes.c_size_t
 _SIGNATURES = {
     "kmoe_last_error": (ctypes.c_char_p, []),
     "kmoe_abi_version": (_i32, []),
+    "kmoe_pack_layout_version": (_i32, []),
     "kmoe_router_partials_len": (_i64, [_i64, _i32]),
     "kmoe_router": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_aux_loss": (_i32, [_vp, _i64, _i32, _vp, _i32, _f32, _f32, _vp, _vp]),

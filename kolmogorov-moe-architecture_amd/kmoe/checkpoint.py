@@ -11,9 +11,11 @@ state-dict keys the model actually has.
   by torch's safe loader, and the error says so; nothing in a checkpoint is executed.
 * The packed expert weights (and, for fp8, the per-row quantisation scales) are a
   derived cache of w1/w2/w3.  ``save_packed`` writes them with a fingerprint of the
-  source parameters (safetensors); ``load_packed`` installs them after checking the
-  fingerprint against the layer's current parameters, so a large layer (or an fp8 one,
-  quantised once) skips the pack at load time.
+  source parameters and the library's packed-layout version, ABI version and buffer
+  sizes (safetensors); ``load_packed`` installs them only when all of these match the
+  layer's current parameters and the loaded library, so a large layer (or an fp8 one,
+  quantised once) skips the pack at load time and a file from a build with another
+  packed layout is re-packed instead of being read with the wrong strides.
 * ``copy_experts`` is the expert copy of tools/reallocate_experts.py:254-266 with the
   keys ``...grouped_experts.w1/w2/w3`` (the reference tool looks for ``gate_proj`` /
   ``up_proj`` / ``down_proj``, which no MoELayer has, so it copies nothing).
@@ -102,36 +104,76 @@ def _fingerprint(experts) -> str:
     return h.hexdigest()
 
 
+def _layout_meta(E: int, d: int, F: int, fp8: bool) -> Dict[str, str]:
+    """What a packed buffer's layout depends on besides E/d/F/fp8: the library's packed
+    layout version and ABI version, and the byte sizes of the packed buffers."""
+    from . import _lib
+
+    lib = _lib.load()
+    pdt = _lib.DTYPE_FP8_E4M3 if fp8 else _lib.DTYPE_BF16
+    return {"layout": str(lib.kmoe_pack_layout_version()), "abi": str(lib.kmoe_abi_version()),
+            "w13_bytes": str(lib.kmoe_packed_w13_bytes(E, d, F, pdt)),
+            "w3_bytes": str(lib.kmoe_packed_w3_bytes(E, d, F, pdt))}
+
+
 def save_packed(experts, path: str) -> None:
     """Write the experts' packed weights (GroupedExperts / GroupedExpertsExpertChoice,
-    bf16 or fp8 with scales) and the source fingerprint to a safetensors file."""
+    bf16 or fp8 with scales), the source fingerprint and the packed layout's version
+    and sizes to a safetensors file."""
     pw = experts.packed()
     tensors = {"w13": pw.w13, "w3": pw.w3}
     if pw.fp8:
         tensors["s13"], tensors["s3"] = pw.s13, pw.s3
     meta = {"kmoe_packed": "1", "E": str(pw.E), "d": str(pw.d), "F": str(pw.F), "fp8": str(int(pw.fp8)),
-            "fingerprint": _fingerprint(experts)}
+            "fingerprint": _fingerprint(experts), **_layout_meta(pw.E, pw.d, pw.F, pw.fp8)}
     save_file({k: v.detach().contiguous().cpu() for k, v in tensors.items()}, path, metadata=meta)
 
 
-def load_packed(experts, path: str, device: Optional[torch.device] = None) -> bool:
-    """Install packed weights saved by save_packed if they were made from exactly the
-    experts' current parameters (same fingerprint, shapes and fp8 mode); returns whether
-    they were installed (False: the next forward packs as usual)."""
+def packed_file_matches(experts, path: str) -> bool:
+    """Whether the packed-weight file at `path` was made from exactly the experts' current
+    parameters (fingerprint, shapes, fp8 mode) by a library with this build's packed layout
+    (layout and ABI versions, buffer sizes).  Reads the metadata and tensor shapes only."""
     from safetensors import safe_open
 
     with safe_open(path, framework="pt") as f:
         meta = f.metadata() or {}
-    if meta.get("kmoe_packed") != "1":
-        raise ValueError(f"kmoe.load_packed: {path} is not a kmoe packed-weight file")
-    E, d, F = experts.n_experts, experts.d_model, experts.d_ff
-    if (int(meta["E"]), int(meta["d"]), int(meta["F"]), bool(int(meta["fp8"]))) != (E, d, F, experts.use_fp8):
+        if meta.get("kmoe_packed") != "1":
+            raise ValueError(f"kmoe.load_packed: {path} is not a kmoe packed-weight file")
+        shapes = {k: tuple(f.get_slice(k).get_shape()) for k in f.keys()}
+    E, d, F, fp8 = experts.n_experts, experts.d_model, experts.d_ff, experts.use_fp8
+    try:
+        if (int(meta["E"]), int(meta["d"]), int(meta["F"]), bool(int(meta["fp8"]))) != (E, d, F, fp8):
+            return False
+    except (KeyError, ValueError):
         return False
-    if meta.get("fingerprint") != _fingerprint(experts):
+    want = _layout_meta(E, d, F, fp8)
+    if any(meta.get(k) != v for k, v in want.items()):
+        return False
+    # the tensors themselves: byte buffers of the sizes the library packs, and one fp32
+    # scale per packed row for fp8
+    Fp = (F + 127) // 128 * 128
+    dp = (d + 255) // 256 * 256
+    exp_shapes = {"w13": (int(want["w13_bytes"]),), "w3": (int(want["w3_bytes"]),)}
+    if fp8:
+        exp_shapes.update({"s13": (E * 2 * Fp,), "s3": (E * dp,)})
+    if shapes != exp_shapes:
+        return False
+    return meta.get("fingerprint") == _fingerprint(experts)
+
+
+def load_packed(experts, path: str, device: Optional[torch.device] = None) -> bool:
+    """Install packed weights saved by save_packed if they were made from exactly the
+    experts' current parameters by a build with the same packed layout
+    (packed_file_matches); returns whether they were installed (False: the next forward
+    packs as usual)."""
+    if not packed_file_matches(experts, path):
         return False
     dev = device if device is not None else experts.w1.device
     t = load_file(path, device=str(dev))
-    pw = ops.PackedWeights(t["w13"], t["w3"], t.get("s13"), t.get("s3"), E, d, F, experts.use_fp8)
+    if t["w13"].dtype != torch.uint8 or t["w3"].dtype != torch.uint8:
+        return False
+    pw = ops.PackedWeights(t["w13"], t["w3"], t.get("s13"), t.get("s3"), experts.n_experts, experts.d_model,
+                           experts.d_ff, experts.use_fp8)
     experts.install_packed(pw)
     return True
 

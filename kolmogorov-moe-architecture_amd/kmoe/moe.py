@@ -188,21 +188,22 @@ class _PackedExperts(nn.Module):
 class GroupedExperts(_PackedExperts):
     """Token-choice grouped SwiGLU experts (moe.py:161-294)."""
 
-    capacity = 0  # 0 = no capacity limit (the reference's behaviour)
-
     def run(self, x2d, expert_indices, expert_weights, row_index=None, T_out=None, out_map=None, scale=None,
-            out_dtype=torch.bfloat16, residual=None):
-        """dispatch -> grouped GEMMs -> combine (+ residual, added in the combine); returns (y, DispatchOut)."""
+            out_dtype=torch.bfloat16, residual=None, capacity=0):
+        """dispatch -> grouped GEMMs -> combine (+ residual, added in the combine); returns (y, DispatchOut).
+        capacity > 0 drops each expert's assignments past the first `capacity` (MoELayer's
+        drop_overflow rule); 0, the default and what forward() uses, drops nothing (the
+        reference's GroupedExperts never drops)."""
         E = self.n_experts
         pw = self.packed()
         T, k = expert_indices.shape
         if pw.fp8:
-            disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=self.capacity, fp8=True,
+            disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=capacity, fp8=True,
                                 row_index=row_index)
             yperm = ops.grouped_ffn(disp.xperm, disp.xscale, disp.offsets, pw, T * k)
         else:
             # bf16: the gate/up GEMM gathers the token rows itself (no permuted copy of x)
-            disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=self.capacity,
+            disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=capacity,
                                 row_index=row_index, materialize=False)
             h = ops.gemm_gate_up_rows(x2d, row_index, disp.row_token, disp.offsets, pw, T * k)
             yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
@@ -271,6 +272,9 @@ class _MoETrainFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy, daux):
+        if ctx.sv is None:
+            raise RuntimeError("kmoe: backward through the MoE layer can run once per forward; "
+                               "retain_graph=True with a second backward is not supported")
         B, S, d, x_dtype, has_aux = ctx.meta
         layer = ctx.layer
         ge = layer.grouped_experts
@@ -397,10 +401,9 @@ class MoELayer(nn.Module):
         if x2d.dtype != torch.bfloat16:
             x2d = x2d.to(torch.bfloat16)
         r = self.router.route(x2d, row_index=row_index, T=T)
-        ge = self.grouped_experts
-        ge.capacity = ops.capacity_of(self.capacity_factor, T, self.top_k, self.n_experts) if self.drop_overflow else 0
-        y, disp = ge.run(x2d, r.idx, r.w, row_index=row_index, T_out=T_out, out_map=out_map, scale=scale,
-                         out_dtype=out_dtype, residual=residual)
+        cap = ops.capacity_of(self.capacity_factor, T, self.top_k, self.n_experts) if self.drop_overflow else 0
+        y, disp = self.grouped_experts.run(x2d, r.idx, r.w, row_index=row_index, T_out=T_out, out_map=out_map,
+                                           scale=scale, out_dtype=out_dtype, residual=residual, capacity=cap)
         return y, r, disp
 
     def _set_token_choice_aux(self, r, disp, T):

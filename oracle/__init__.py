@@ -22,11 +22,20 @@ Pinning (how each oracle function is checked independently, tests/test_oracle.py
   mod_select         brute-force sort; torch.topk + sort on tie-free rows
   f32_to_e4m3        torch.float8_e4m3fn cast (library routine) on saturated inputs,
                      exhaustively over every code and every rounding midpoint
+  quant_rows         round trip: amax element -> exactly +-448, error <= 2^-4 of the amax
+  bf16_round         torch fp32 -> bfloat16 cast (library routine) on random values,
+                     exact ties, overflow to inf, subnormals, +-0, +-inf; NaN stays NaN
+  quant_weight_cols  torch restatement (per-(expert, output column) amax over K,
+                     float8_e4m3fn cast); per-column brute force (amax element exact,
+                     error <= 2^-4 of the column amax), columns of 1e3x / 1e-3x scale
+  swiglu_rows_fp8    torch fake-quant restatement (bf16 and e4m3 library casts);
+                     fp64 per-token brute force at a tiny shape
+  mod_logits         torch nn.Linear(d, 1, bias=False) in fp64; brute force
   torch_port vs moe_oracle at small shapes (two independent restatements)
   moe_loss_tc_routed forward = torch_port.moe_layer_tc at its own routing; its
                      autograd gradients = finite differences (gradcheck, fp64)
   rms_norm           torch.nn.functional.rms_norm (library routine); unit mean square at
                      weight 1, eps 0; invariance under scaling of x; per-element brute force
   ffn_block_tc       h + torch_port.moe_layer_tc(F.rms_norm(h)) (independent restatement)
-No function is left unpinned.
+Every function above has at least one check that does not restate its own formula.
 """

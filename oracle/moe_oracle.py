@@ -313,10 +313,12 @@ def swiglu_rows_fp8(xq, xs, offsets, w1q, w2q, w3q):
 
 
 def bf16_round(v):
-    """Round fp32 to bf16 (RNE) and back to fp32."""
+    """Round fp32 to bf16 (RNE) and back to fp32; NaN stays a (quiet) NaN with its
+    sign (the kernels' f32_to_bf16 rule)."""
     v = np.asarray(v, dtype=np.float32)
     u = v.view(np.uint32).astype(np.uint64)
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    r = np.where(np.isnan(v), ((u >> 16) | 0x40) << 16, r)
     return r.astype(np.uint32).view(np.float32)
 
 

@@ -72,3 +72,51 @@ def test_copy_experts_uses_real_keys():
     assert out["layers.0.ffn.router.router.0.weight"] is sd["layers.0.ffn.router.router.0.weight"]
     with pytest.raises(KeyError):
         C.copy_experts(sd, [(0, 0, 5, 0)])
+
+
+def _packed_file(tmp_path, ge, name, meta_over=None, drop=(), shape_over=None):
+    """A packed-weight file for `ge` as save_packed writes it (zero buffers of the sizes the
+    library packs), with metadata entries replaced / removed and tensor sizes changed."""
+    from safetensors.torch import save_file
+
+    E, d, F, fp8 = ge.n_experts, ge.d_model, ge.d_ff, ge.use_fp8
+    meta = {"kmoe_packed": "1", "E": str(E), "d": str(d), "F": str(F), "fp8": str(int(fp8)),
+            "fingerprint": C._fingerprint(ge), **C._layout_meta(E, d, F, fp8)}
+    meta.update(meta_over or {})
+    for k in drop:
+        meta.pop(k)
+    sizes = {"w13": int(meta.get("w13_bytes", 0) or C._layout_meta(E, d, F, fp8)["w13_bytes"]),
+             "w3": int(C._layout_meta(E, d, F, fp8)["w3_bytes"])}
+    Fp, dp = (F + 127) // 128 * 128, (d + 255) // 256 * 256
+    if fp8:
+        sizes.update({"s13": E * 2 * Fp, "s3": E * dp})
+    sizes.update(shape_over or {})
+    t = {k: torch.zeros(n, dtype=torch.uint8 if k in ("w13", "w3") else torch.float32) for k, n in sizes.items()}
+    path = str(tmp_path / name)
+    save_file(t, path, metadata=meta)
+    return path
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_packed_file_layout_checks(tmp_path, fp8):
+    """A packed-weight file is accepted only with this library's packed-layout and ABI
+    versions and the buffer sizes it packs; anything else is refused (re-pack)."""
+    cfg = AdvancedMoEConfig(d_model=128, n_experts=4, d_ff_expert=200, moe_fp8=fp8)
+    ge = MoELayer(cfg, 0).grouped_experts
+    assert C.packed_file_matches(ge, _packed_file(tmp_path, ge, "ok.st"))
+    lay = C._layout_meta(4, 128, 200, fp8)
+    bad = [
+        dict(meta_over={"layout": str(int(lay["layout"]) + 1)}),
+        dict(meta_over={"layout": "1"}),  # the layout before the packed-row padding
+        dict(meta_over={"abi": "0"}),
+        dict(drop=("layout",)),
+        dict(meta_over={"w13_bytes": str(int(lay["w13_bytes"]) - 128)}),
+        dict(shape_over={"w3": int(lay["w3_bytes"]) - 4096}),
+        dict(meta_over={"F": "192"}),
+        dict(meta_over={"fingerprint": "0" * 16}),
+    ]
+    if fp8:
+        bad.append(dict(shape_over={"s13": 4 * 2 * 256 - 1}))
+    for i, kw in enumerate(bad):
+        assert not C.packed_file_matches(ge, _packed_file(tmp_path, ge, f"bad{i}.st", **kw)), kw
+        assert not C.load_packed(ge, str(tmp_path / f"bad{i}.st"))

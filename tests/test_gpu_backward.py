@@ -249,3 +249,17 @@ def test_backward_full_size(dev):
     errs = {"dx_sample": e_dx, "dw_out": e_dwout, "dw3_e": e_dw3, "dw1_e": e_dw1}
     print("full-size rel-L2:", {n: f"{v:.2e}" for n, v in errs.items()}, "expert", e, "rows", hi - lo)
     assert e_dx <= 1e-2 and e_dw3 <= 1e-2 and e_dw1 <= 1e-2 and e_dwout <= 2e-2, errs
+
+
+def test_second_backward_raises(dev):
+    """A second backward through the same graph (retain_graph=True) fails with a clear
+    error instead of inside the kernels."""
+    print("second backward", flush=True)
+    cfg = AdvancedMoEConfig(d_model=128, n_experts=4, moe_top_k=2, d_ff_expert=256)
+    layer = MoELayer(cfg, 0).to(dev, torch.bfloat16).train()
+    x = torch.randn(1, 64, 128, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    y = layer(x)
+    loss = y.float().square().sum() + layer.aux_loss
+    loss.backward(retain_graph=True)
+    with pytest.raises(RuntimeError, match="once per forward"):
+        loss.backward()

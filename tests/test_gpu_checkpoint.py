@@ -1,6 +1,8 @@
 """Packed-weight cache on disk (kmoe/checkpoint.py save_packed / load_packed): the packed
 buffers read back are bit-identical to a fresh pack, a layer using them gives a
-bit-identical forward, and a file made from other parameters is not installed."""
+bit-identical forward, and a file made from other parameters is not installed.  The fp8
+pack itself (codes and per-row scales) is checked bit for bit against the oracle."""
+import numpy as np
 import pytest
 import torch
 
@@ -42,3 +44,53 @@ def test_packed_roundtrip(dev, tmp_path, fp8):
         c.load_state_dict(a.state_dict())
         c.grouped_experts.w3[0, 0, 0] += 1.0
     assert not C.load_packed(c.grouped_experts, path)
+
+
+def _unpack_fp8(pw):
+    """Host view of the fp8 packed layout: w13 rows (E, 2*F_pad, d + 128 pad bytes),
+    gate row of f at (f//128)*256 + f%128 and up row at +128; w3 rows (E, d_pad,
+    F_pad + 128) with row n = column n of w3[e]; s13 (E, 2*F_pad), s3 (E, d_pad)."""
+    E, d, F = pw.E, pw.d, pw.F
+    Fp = (F + 127) // 128 * 128
+    dp = (d + 255) // 256 * 256
+    w13 = pw.w13.cpu().numpy().reshape(E, 2 * Fp, d + 128)
+    w3 = pw.w3.cpu().numpy().reshape(E, dp, Fp + 128)
+    s13 = pw.s13.cpu().numpy().reshape(E, 2 * Fp)
+    s3 = pw.s3.cpu().numpy().reshape(E, dp)
+    f = np.arange(F)
+    gate_rows = (f // 128) * 256 + f % 128
+    return (w13[:, gate_rows, :d], s13[:, gate_rows], w13[:, gate_rows + 128, :d], s13[:, gate_rows + 128],
+            w3[:, :d, :F], s3[:, :d], w13, w3)
+
+
+@pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
+def test_packed_fp8_codes_match_oracle(dev, wdtype):
+    """kmoe_pack_weights' fp8 codes and per-row scales equal the oracle's per-output-column
+    quantisation (quant_rows of w[e]^T: scale amax/448, RNE e4m3) bit for bit, and the
+    padding is zero."""
+    from oracle import moe_oracle as O
+    from kmoe import ops
+
+    E, d, F = 3, 192, 200  # F_pad 256: a partial f block; d_pad 256: 64 zero rows in w3
+    g = torch.Generator().manual_seed(11)
+    w1, w2, w3 = (torch.randn(*s, generator=g) * 0.02 for s in [(E, d, F), (E, d, F), (E, F, d)])
+    w1[1, :, 7] *= 300.0  # one column far larger than the rest
+    w2[2, :, 9] = 0.0     # an all-zero column: scale 0, codes 0
+    w1, w2, w3 = (w.to(wdtype) for w in (w1, w2, w3))
+    print(f"packed fp8 codes wdtype={wdtype}", flush=True)
+    pw = ops.pack_weights(w1.to(dev), w2.to(dev), w3.to(dev), fp8=True)
+    torch.cuda.synchronize()
+    c1, s1, c2, s2, c3, s3, w13, w3p = _unpack_fp8(pw)
+    for e in range(E):
+        for codes, scales, w in ((c1, s1, w1), (c2, s2, w2), (c3, s3, w3)):
+            q, s = O.quant_rows(np.ascontiguousarray(w[e].float().numpy().T))
+            assert np.array_equal(codes[e], q), e
+            assert np.array_equal(scales[e].view(np.uint32), s.view(np.uint32)), e
+    assert np.all(s2[2, 9] == 0) and np.all(c2[2, 9] == 0)
+    # padding: the 128 bytes after each row, the f rows past F and the d rows past d
+    assert not w13[:, :, d:].any() and not w3p[:, :, F:].any() and not w3p[:, d:, :].any()
+    Fp = (F + 127) // 128 * 128
+    pad_f = [(f // 128) * 256 + h * 128 + f % 128 for f in range(F, Fp) for h in (0, 1)]
+    assert not w13[:, pad_f, :].any()
+    assert not pw.s13.cpu().numpy().reshape(E, 2 * Fp)[:, pad_f].any()
+    assert not pw.s3.cpu().numpy().reshape(E, -1)[:, d:].any()

@@ -253,3 +253,26 @@ def test_cfg5_fp8_mod(dev, cfg_cache):
     assert relL2(got, y32) <= 1e-1
     skipped = np.setdiff1d(np.arange(B * S), rows)
     assert np.all(f(y).reshape(B * S, d)[skipped] == 0)
+
+
+def test_direct_experts_call_after_drop_layer_drops_nothing(dev):
+    """GroupedExperts.forward (the reference's secondary boundary, moe.py:213-294) never
+    drops, also right after a drop_overflow layer forward on the same module."""
+    from kmoe import AdvancedMoEConfig, MoELayer
+    print("direct experts after drop layer", flush=True)
+    cfg = AdvancedMoEConfig(d_model=128, n_experts=4, moe_top_k=2, d_ff_expert=256, moe_capacity_factor=0.5,
+                            moe_drop_overflow=True)
+    torch.manual_seed(3)
+    layer = MoELayer(cfg, 0).to(dev, torch.bfloat16).eval()
+    x = torch.randn(1, 300, 128, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        layer(x)  # capacity ceil(0.5*300*2/4) = 75 < the routed counts: drops
+        assert int(layer.last_expert_counts.max()) > 75
+        T = 300
+        idx = torch.stack([torch.zeros(T, dtype=torch.int64), torch.ones(T, dtype=torch.int64)], 1).to(dev)
+        w = torch.full((T, 2), 0.5, device=dev)
+        y = layer.grouped_experts(x.view(T, 128), idx, w)
+        ge = layer.grouped_experts
+        W = [f(t) for t in (ge.w1, ge.w2, ge.w3)]
+        ref = token_outputs(f(x.view(T, 128)), f(idx), f(w), np.ones((T, 2), bool), W, list(range(T)))
+    assert relL2(f(y), ref) <= 1e-2  # every token has both of its experts

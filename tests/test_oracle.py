@@ -368,6 +368,155 @@ def test_quant_rows_roundtrip():
         assert O.e4m3_to_f32(q[i, j:j + 1])[0] == np.sign(m[i, j]) * 448.0
 
 
+def test_bf16_round_matches_torch():
+    """bf16_round = torch's fp32 -> bfloat16 cast (round to nearest even) and back."""
+    r = rng(14)
+    v = (r.standard_normal(100000) * np.exp(r.uniform(-80, 80, 100000))).astype(np.float32)
+    # exact ties (low half 0x8000, both parities of the kept bit), their neighbours,
+    # the largest finite values (round to inf), subnormals, +-0, +-inf
+    hi = r.integers(0, 1 << 16, 4000, dtype=np.uint64).astype(np.uint32) << 16
+    ties = hi | np.uint32(0x8000)
+    special = np.array([0x7F7FFFFF, 0x7F7F8000, 0x7F7F7FFF, 0x00008000, 0x00018000, 0x00000001, 0x80000000,
+                        0x00000000, 0x7F800000, 0xFF800000], dtype=np.uint32)
+    bits = np.concatenate([v.view(np.uint32), ties, ties - 1, ties + 1, special])
+    vals = bits.view(np.float32)
+    vals = vals[~np.isnan(vals)]
+    ref = torch.from_numpy(vals.copy()).to(torch.bfloat16).float().numpy()
+    got = O.bf16_round(vals)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # NaN stays NaN (also payloads that only have low mantissa bits), sign kept
+    nans = np.array([0x7FC00000, 0x7F800001, 0xFF800001, 0x7FFFFFFF], dtype=np.uint32).view(np.float32)
+    out = O.bf16_round(nans)
+    assert np.all(np.isnan(out))
+    assert np.array_equal(np.signbit(out), np.signbit(nans))
+
+
+def _torch_quant_cols(w):
+    """Per-expert, per-output-column e4m3 fake-quant of w (E, K, N) in torch: scale =
+    amax over K of column n / 448, q = e4m3(clamp(w * (448 / amax))), dequantised."""
+    t = torch.from_numpy(np.asarray(w, dtype=np.float32))
+    amax = t.abs().amax(dim=1, keepdim=True)                       # (E, 1, N)
+    inv = torch.where(amax > 0, torch.tensor(448.0) / amax, torch.zeros_like(amax))
+    q = (t * inv).clamp(-448, 448).to(torch.float8_e4m3fn).float()
+    return (q * (amax / 448.0)).numpy()
+
+
+def test_quant_weight_cols_matches_torch_and_axis():
+    """quant_weight_cols: one scale per (expert, output column n) = amax over the K
+    (input) axis / 448 (cfg 5: per-expert per-output-row scales of w^T)."""
+    r = rng(15)
+    E, K, N = 3, 40, 24
+    w = r.standard_normal((E, K, N)).astype(np.float32) * 0.02
+    # columns of very different magnitudes and an all-zero column: a scale taken over
+    # the wrong axis (per input row, per expert) would crush the small columns
+    w[:, :, 3] *= 1e3
+    w[:, :, 7] *= 1e-3
+    w[1, :, 5] = 0.0
+    got = O.quant_weight_cols(w)
+    ref = _torch_quant_cols(w)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert np.all(got[1, :, 5] == 0.0)
+    # brute force, element by element: every column's largest |w| maps to exactly
+    # +-amax, and every element is within half an e4m3 step of the scaled value
+    for e in range(E):
+        for n in range(N):
+            col = w[e, :, n].astype(np.float64)
+            amax = np.abs(col).max()
+            if amax == 0:
+                continue
+            j = int(np.argmax(np.abs(col)))
+            assert got[e, j, n] == np.float32(np.sign(col[j]) * np.float32(amax / np.float32(448.0)) * 448.0)
+            err = np.abs(got[e, :, n] - col) / amax
+            assert err.max() <= 2.0 ** -4 * 1.0001  # 3 mantissa bits, relative to the column amax
+    # per-column precision: a small column keeps its own relative precision
+    rel7 = np.abs(got[:, :, 7] - w[:, :, 7]).max() / np.abs(w[:, :, 7]).max()
+    assert rel7 <= 2.0 ** -4
+
+
+def _torch_swiglu_fp8(xq, xs, offsets, w1q, w2q, w3q):
+    """fp32 fake-quant restatement in torch of the cfg 5 expert path: x dequantised from
+    its per-token scales, h = silu(x w1) * (x w2) rounded to bf16 by torch's cast,
+    re-quantised per row with torch's e4m3 cast, y = h' w3."""
+    x = torch.from_numpy(O.e4m3_to_f32(xq)) * torch.from_numpy(np.asarray(xs, np.float32))[:, None]
+    y = torch.zeros(x.shape[0], w3q.shape[2])
+    for e in range(w1q.shape[0]):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi <= lo:
+            continue
+        xe = x[lo:hi]
+        g = xe @ torch.from_numpy(w1q[e])
+        u = xe @ torch.from_numpy(w2q[e])
+        h = (g / (1.0 + torch.exp(-g)) * u).to(torch.bfloat16).float()
+        amax = h.abs().amax(dim=1, keepdim=True)
+        inv = torch.where(amax > 0, torch.tensor(448.0) / amax, torch.zeros_like(amax))
+        hq = (h * inv).clamp(-448, 448).to(torch.float8_e4m3fn).float() * (amax / 448.0)
+        y[lo:hi] = hq @ torch.from_numpy(w3q[e])
+    return y.numpy()
+
+
+def _fp8_case(seed, E=4, d=32, F_=24, T=37):
+    r = rng(seed)
+    x = r.standard_normal((T, d)).astype(np.float32)
+    w1, w2, w3 = (r.standard_normal(s).astype(np.float32) * 0.1 for s in [(E, d, F_), (E, d, F_), (E, F_, d)])
+    cuts = np.sort(r.integers(0, T + 1, E - 1))
+    offsets = np.concatenate([[0], cuts, [T]]).astype(np.int64)
+    offsets[2] = offsets[1]  # an empty expert
+    xq, xs = O.quant_rows(O.bf16_round(x))
+    return x, xq, xs, offsets, O.quant_weight_cols(w1), O.quant_weight_cols(w2), O.quant_weight_cols(w3)
+
+
+def test_swiglu_rows_fp8_matches_torch_restatement():
+    """swiglu_rows_fp8 = the torch fake-quant restatement (library casts for bf16 and
+    e4m3).  The two differ only in fp32 summation order, which flips an e4m3 code of h
+    about once in a million; dropping the bf16 rounding of h moves rel-L2 to ~6e-3,
+    taking h's scales per column instead of per row to ~2e-2."""
+    for seed in (16, 17):
+        _, xq, xs, offsets, w1q, w2q, w3q = _fp8_case(seed)
+        got = O.swiglu_rows_fp8(xq, xs, offsets, w1q, w2q, w3q)
+        ref = _torch_swiglu_fp8(xq, xs, offsets, w1q, w2q, w3q)
+        rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert rel <= 1e-4, rel
+        close = np.abs(got - ref) <= 1e-5 * np.abs(ref).max()
+        assert close.mean() >= 0.999
+
+
+def test_swiglu_rows_fp8_bruteforce_fp64():
+    """Per-token fp64 brute force of the fp8 expert path (tiny shape): dequantised x and
+    weights, h in fp64 -> bf16 -> per-row e4m3 (torch casts), y summed in fp64."""
+    E, d, F_, T = 3, 8, 6, 11
+    x, xq, xs, offsets, w1q, w2q, w3q = _fp8_case(18, E=E, d=d, F_=F_, T=T)
+    got = O.swiglu_rows_fp8(xq, xs, offsets, w1q, w2q, w3q)
+    xd = O.e4m3_to_f32(xq).astype(np.float64) * xs.astype(np.float64)[:, None]
+    for e in range(E):
+        for t in range(int(offsets[e]), int(offsets[e + 1])):
+            h = []
+            for f in range(F_):
+                g = sum(xd[t, i] * float(w1q[e, i, f]) for i in range(d))
+                u = sum(xd[t, i] * float(w2q[e, i, f]) for i in range(d))
+                h.append(g / (1.0 + math.exp(-g)) * u)
+            hb = torch.tensor(h, dtype=torch.float64).float().to(torch.bfloat16).float()
+            amax = float(hb.abs().max())
+            sc = np.float32(amax) / np.float32(448.0)
+            inv = np.float32(448.0) / np.float32(amax)
+            hq = (hb * float(inv)).clamp(-448, 448).to(torch.float8_e4m3fn).float().double() * float(sc)
+            for n in range(d):
+                ref = sum(float(hq[f]) * float(w3q[e, f, n]) for f in range(F_))
+                assert abs(got[t, n] - ref) <= 1e-5 * max(1.0, abs(ref)), (e, t, n, got[t, n], ref)
+
+
+def test_mod_logits_matches_linear():
+    """mod_logits = nn.Linear(d, 1, bias=False) of the MoD router (mod.py:93), fp64."""
+    r = rng(19)
+    B, S, d = 2, 9, 24
+    x = r.standard_normal((B, S, d))
+    lin = nn.Linear(d, 1, bias=False).double()
+    ref = lin(torch.from_numpy(x)).squeeze(-1).detach().numpy()
+    got = O.mod_logits(x, lin.weight.detach().numpy())
+    np.testing.assert_allclose(got, ref, rtol=1e-13, atol=1e-13)
+    # brute force on one token
+    assert abs(got[1, 4] - sum(x[1, 4, i] * float(lin.weight.detach()[0, i]) for i in range(d))) < 1e-12
+
+
 # ------------------------------------------------------------------ golden fixtures
 def test_golden_fixture_cfg1():
     path = os.path.join(GOLDEN, "cfg1_small.npz")
