@@ -109,6 +109,24 @@ int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T, int d, con
                   int xperm_dtype, float* xperm_scale, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/* Allocation-free dispatch.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, semantics and results as
+ * kmoe_dispatch (bit for bit), without the workspace: the per-block histograms and
+ * bases live in a file-scope device array of KMOE_DISPATCH_SCRATCH_BYTES on each GPU
+ * (allocated with the library's code object and held until the process ends; looked
+ * up once per device, on the first call with that device current).  Sizes whose
+ * kmoe_dispatch_workspace_bytes(T, k, E) exceeds it are rejected with
+ * KMOE_ERR_WORKSPACE (4 MiB: T*E up to 2^25 - 8192, e.g. T = 2M tokens at E = 16).
+ * It calls no allocator.  Every call on a GPU shares that GPU's array, so calls that
+ * overlap on one GPU (other streams, other threads) race: serialise them.  Nothing in
+ * the array has to start at zero (a call writes every entry it reads).              */
+#define KMOE_DISPATCH_SCRATCH_BYTES (4u << 20)
+int kmoe_dispatch_noalloc(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
+                          const void* topk_w, int w_dtype, int k, int E, int64_t capacity, int32_t* counts,
+                          int32_t* offsets, int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm,
+                          int xperm_dtype, float* xperm_scale, void* stream);
+
 /* Row gather: out[r] = x[row_token[r]] for r < n_rows (rows with row_token < 0 are
  * zero-filled).  out_dtype BF16 (copy) or FP8_E4M3 (per-row scale to out_scale;
  * d <= 8192).

@@ -12,6 +12,8 @@
 //               each permute block computes its own share of this instead)
 //   3. permute: per-block stable ranks via wave ballots, slot tables, then one
 //               read of each token row and k 16-byte-vector row writes
+#include <mutex>
+
 #include "kmoe_common.h"
 
 namespace {
@@ -325,31 +327,39 @@ extern "C" size_t kmoe_dispatch_workspace_bytes(int64_t T, int k, int E) {
   return (size_t)(2 * nblk * E) * sizeof(int32_t) + 256;
 }
 
-extern "C" int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
-                             const void* topk_w, int w_dtype, int k, int E, int64_t capacity, int32_t* counts,
-                             int32_t* offsets, int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm,
-                             int xperm_dtype, float* xperm_scale, void* workspace, size_t workspace_bytes,
-                             void* stream) {
+namespace {
+
+// Argument checks shared by kmoe_dispatch and kmoe_dispatch_noalloc.
+int check_dispatch_args(const char* who, const void* x, int64_t T, int d, const int64_t* topk_idx,
+                        const void* topk_w, int w_dtype, int k, int E, int32_t* counts, int32_t* offsets,
+                        int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm, int xperm_dtype,
+                        float* xperm_scale) {
   KMOE_REQUIRE(x && topk_idx && topk_w && counts && offsets && row_token && slot_row && slot_w &&
                    (xperm || xperm_dtype == KMOE_DTYPE_BF16),
-               KMOE_ERR_NULL, "kmoe_dispatch: null buffer");
-  KMOE_REQUIRE(T >= 0 && T * (int64_t)k < ((int64_t)1 << 31), KMOE_ERR_SHAPE,
-               "kmoe_dispatch: T*k must fit in int32");
-  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "kmoe_dispatch: d=%d must be a positive multiple of 64", d);
-  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_dispatch: E=%d out of range", E);
-  KMOE_REQUIRE(k >= 1 && k <= 8 && k <= E, KMOE_ERR_SHAPE, "kmoe_dispatch: k=%d not in [1, min(8,E)]", k);
+               KMOE_ERR_NULL, "%s: null buffer", who);
+  KMOE_REQUIRE(T >= 0 && T * (int64_t)k < ((int64_t)1 << 31), KMOE_ERR_SHAPE, "%s: T*k must fit in int32", who);
+  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "%s: d=%d must be a positive multiple of 64", who, d);
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "%s: E=%d out of range", who, E);
+  KMOE_REQUIRE(k >= 1 && k <= 8 && k <= E, KMOE_ERR_SHAPE, "%s: k=%d not in [1, min(8,E)]", who, k);
   KMOE_REQUIRE(w_dtype == KMOE_DTYPE_BF16 || w_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE,
-               "kmoe_dispatch: topk_w dtype must be bf16 or f32");
+               "%s: topk_w dtype must be bf16 or f32", who);
   KMOE_REQUIRE(xperm_dtype == KMOE_DTYPE_BF16 || xperm_dtype == KMOE_DTYPE_FP8_E4M3, KMOE_ERR_DTYPE,
-               "kmoe_dispatch: xperm dtype must be bf16 or fp8_e4m3");
-  KMOE_REQUIRE(xperm_dtype != KMOE_DTYPE_FP8_E4M3 || xperm_scale, KMOE_ERR_NULL,
-               "kmoe_dispatch: fp8 output needs xperm_scale");
+               "%s: xperm dtype must be bf16 or fp8_e4m3", who);
+  KMOE_REQUIRE(xperm_dtype != KMOE_DTYPE_FP8_E4M3 || xperm_scale, KMOE_ERR_NULL, "%s: fp8 output needs xperm_scale",
+               who);
   KMOE_REQUIRE(xperm_dtype != KMOE_DTYPE_FP8_E4M3 || d <= 64 * 8 * ROW_REGS, KMOE_ERR_UNSUPPORTED,
-               "kmoe_dispatch: fp8 rows need d <= %d (d=%d)", 64 * 8 * ROW_REGS, d);
-  const size_t need = kmoe_dispatch_workspace_bytes(T, k, E);
-  KMOE_REQUIRE(workspace && workspace_bytes >= need, KMOE_ERR_WORKSPACE,
-               "kmoe_dispatch: workspace %zu < %zu bytes", workspace_bytes, need);
-  hipStream_t s = kmoe::as_stream(stream);
+               "%s: fp8 rows need d <= %d (d=%d)", who, 64 * 8 * ROW_REGS, d);
+  return KMOE_OK;
+}
+
+// The launches of a dispatch whose per-block histograms and bases live in `workspace`
+// (at least kmoe_dispatch_workspace_bytes(T, k, E) bytes).  Every workspace entry a
+// launch reads is written by an earlier launch of the same call (hist_kernel writes all
+// nblk*E counts, the scan writes all bases), so nothing needs to start at zero.
+int dispatch_launch(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
+                    const void* topk_w, int w_dtype, int k, int E, int64_t capacity, int32_t* counts,
+                    int32_t* offsets, int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm,
+                    int xperm_dtype, float* xperm_scale, void* workspace, hipStream_t s) {
   const int64_t nblk = kmoe::ceil_div<int64_t>(T, DTB);
   int32_t* block_counts = static_cast<int32_t*>(workspace);
   int32_t* block_base = block_counts + nblk * E;
@@ -377,6 +387,73 @@ extern "C" int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T,
     hipLaunchKernelGGL(quant_scatter_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0, s, xp,
                        row_index, T, d, k, slot_row, static_cast<uint8_t*>(xperm), xperm_scale);
   return kmoe::check_launch("kmoe_dispatch");
+}
+
+// ---- allocation-free dispatch: its workspace is this file-scope device array.  Host
+// code never passes `scratch` itself to a kernel (on the host the name is a stand-in,
+// not a device address); it passes the address hipGetSymbolAddress returns for the
+// current device, looked up once per device on the first call there.
+static __device__ __align__(256) uint8_t scratch[KMOE_DISPATCH_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  KMOE_REQUIRE(e == hipSuccess, KMOE_ERR_LAUNCH, "kmoe_dispatch_noalloc: hipGetDevice failed: %s",
+               hipGetErrorString(e));
+  KMOE_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, KMOE_ERR_UNSUPPORTED,
+               "kmoe_dispatch_noalloc: device %d beyond the %d supported", dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    KMOE_REQUIRE(e == hipSuccess && p != nullptr, KMOE_ERR_LAUNCH,
+                 "kmoe_dispatch_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                 hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KMOE_OK;
+}
+
+}  // namespace
+
+extern "C" int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
+                             const void* topk_w, int w_dtype, int k, int E, int64_t capacity, int32_t* counts,
+                             int32_t* offsets, int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm,
+                             int xperm_dtype, float* xperm_scale, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  int rc = check_dispatch_args("kmoe_dispatch", x, T, d, topk_idx, topk_w, w_dtype, k, E, counts, offsets,
+                               row_token, slot_row, slot_w, xperm, xperm_dtype, xperm_scale);
+  if (rc) return rc;
+  const size_t need = kmoe_dispatch_workspace_bytes(T, k, E);
+  KMOE_REQUIRE(workspace && workspace_bytes >= need, KMOE_ERR_WORKSPACE,
+               "kmoe_dispatch: workspace %zu < %zu bytes", workspace_bytes, need);
+  return dispatch_launch(x, row_index, T, d, topk_idx, topk_w, w_dtype, k, E, capacity, counts, offsets, row_token,
+                         slot_row, slot_w, xperm, xperm_dtype, xperm_scale, workspace, kmoe::as_stream(stream));
+}
+
+extern "C" int kmoe_dispatch_noalloc(const void* x, const int32_t* row_index, int64_t T, int d,
+                                     const int64_t* topk_idx, const void* topk_w, int w_dtype, int k, int E,
+                                     int64_t capacity, int32_t* counts, int32_t* offsets, int32_t* row_token,
+                                     int32_t* slot_row, float* slot_w, void* xperm, int xperm_dtype,
+                                     float* xperm_scale, void* stream) {
+  int rc = check_dispatch_args("kmoe_dispatch_noalloc", x, T, d, topk_idx, topk_w, w_dtype, k, E, counts, offsets,
+                               row_token, slot_row, slot_w, xperm, xperm_dtype, xperm_scale);
+  if (rc) return rc;
+  const size_t need = kmoe_dispatch_workspace_bytes(T, k, E);
+  KMOE_REQUIRE(need <= (size_t)KMOE_DISPATCH_SCRATCH_BYTES, KMOE_ERR_WORKSPACE,
+               "kmoe_dispatch_noalloc: T=%lld, E=%d needs %zu bytes of scratch, more than the %zu it has "
+               "(use kmoe_dispatch with a workspace)",
+               (long long)T, E, need, (size_t)KMOE_DISPATCH_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  return dispatch_launch(x, row_index, T, d, topk_idx, topk_w, w_dtype, k, E, capacity, counts, offsets, row_token,
+                         slot_row, slot_w, xperm, xperm_dtype, xperm_scale, ws, kmoe::as_stream(stream));
 }
 
 extern "C" int kmoe_gather_rows(const void* x, const int32_t* row_token, int64_t n_rows, const int32_t* n_rows_dev,

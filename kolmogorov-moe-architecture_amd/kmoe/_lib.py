@@ -38,6 +38,8 @@ _SIGNATURES = {
     "kmoe_dispatch_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "kmoe_dispatch": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp,
                              _vp, _i32, _vp, _vp, _sz, _vp]),
+    "kmoe_dispatch_noalloc": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp,
+                                     _vp, _vp, _i32, _vp, _vp]),
     "kmoe_gather_rows": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp]),
     "kmoe_padded_ff": (_i32, [_i32]),
     "kmoe_packed_w13_bytes": (_sz, [_i32, _i32, _i32, _i32]),

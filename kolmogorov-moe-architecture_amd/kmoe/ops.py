@@ -163,11 +163,14 @@ def capacity_of(cf: float, T: int, k: int, E: int) -> int:
     return int(math.ceil(cf * T * k / E))
 
 
-def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None, materialize=True) -> DispatchOut:
+def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None, materialize=True,
+             no_alloc=False) -> DispatchOut:
     """Stable counting-sort dispatch (moe.py:238-272) + optional capacity drop.
 
     materialize=False (bf16 only) writes the routing tables but not the permuted
-    rows: gemm_gate_up_rows gathers them itself (xperm is then None)."""
+    rows: gemm_gate_up_rows gathers them itself (xperm is then None).
+    no_alloc=True calls kmoe_dispatch_noalloc, whose histograms live in the library's
+    own device scratch (no workspace allocation; calls on one GPU must not overlap)."""
     if not materialize and fp8:
         raise ValueError("kmoe.dispatch: the fp8 path needs the quantised permuted rows (materialize=True)")
     _need_gpu(x2d, idx, w)
@@ -188,9 +191,15 @@ def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None, materialize=
     slot_w = torch.empty(max(A, 1), device=dev, dtype=torch.float32)
     xperm = torch.empty(max(A, 1), d, device=dev, dtype=torch.uint8 if fp8 else _BF16) if materialize else None
     xscale = torch.empty(max(A, 1), device=dev, dtype=torch.float32) if fp8 else None
+    wdt = _lib.DTYPE_F32 if w.dtype == torch.float32 else _lib.DTYPE_BF16
+    if no_alloc:
+        with _Stage("dispatch"):
+            _lib.call("kmoe_dispatch_noalloc", ptr(x2d), ptr(row_index), T, d, ptr(idx), ptr(w), wdt, k, E,
+                      int(capacity), ptr(counts), ptr(offsets), ptr(row_token), ptr(slot_row), ptr(slot_w), ptr(xperm),
+                      _lib.DTYPE_FP8_E4M3 if fp8 else _lib.DTYPE_BF16, ptr(xscale), _stream(x2d))
+        return DispatchOut(counts, offsets, row_token, slot_row, slot_w, xperm, xscale)
     wsb = lib.kmoe_dispatch_workspace_bytes(T, k, E)
     ws = torch.empty(wsb, device=dev, dtype=torch.uint8)
-    wdt = _lib.DTYPE_F32 if w.dtype == torch.float32 else _lib.DTYPE_BF16
     with _Stage("dispatch"):
         _lib.call("kmoe_dispatch", ptr(x2d), ptr(row_index), T, d, ptr(idx), ptr(w), wdt, k, E, int(capacity),
               ptr(counts), ptr(offsets), ptr(row_token), ptr(slot_row), ptr(slot_w), ptr(xperm),

@@ -100,3 +100,23 @@ def test_select_validation(lib):
     assert _err(lib, "kmoe_aux_loss", NULL, 16, 4, NULL, 2, 0.01, 0.001, FAKE, NULL)[0] == -1
     assert _err(lib, "kmoe_balanced_topk", FAKE, 100, 4, 5, FAKE, FAKE, FAKE, 1024, NULL)[0] == -2  # k > E
     assert _err(lib, "kmoe_balanced_topk", FAKE, 100, 4, 2, FAKE, FAKE, FAKE, 4, NULL)[0] == -4  # workspace
+
+
+def test_dispatch_noalloc_validation(lib):
+    """The allocation-free dispatch rejects, before any GPU call, sizes whose histograms do
+    not fit its fixed device scratch, and bad arguments like kmoe_dispatch."""
+    args = [FAKE, NULL, 16, 64, FAKE, FAKE, _lib.DTYPE_F32, 2, 8, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+            _lib.DTYPE_BF16, NULL, NULL]
+    big = list(args)
+    big[2] = 1 << 21  # T = 2M tokens at E = 64: 16 MiB of histograms > 4 MiB
+    big[8] = 64
+    rc, msg = _err(lib, "kmoe_dispatch_noalloc", *big)
+    assert rc == -4 and "scratch" in msg
+    bad = list(args)
+    bad[6] = 7
+    assert _err(lib, "kmoe_dispatch_noalloc", *bad)[0] == -3
+    bad = list(args)
+    bad[0] = NULL
+    assert _err(lib, "kmoe_dispatch_noalloc", *bad)[0] == -1
+    # the largest size that fits is accepted by the size check (T*E = 2^25 - 8192 for k=2)
+    assert lib.kmoe_dispatch_workspace_bytes((1 << 21) - 512, 2, 16) <= 4 << 20
