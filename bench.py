@@ -47,6 +47,9 @@ def parse():
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a plain 512 MiB device copy (the reference for PMC byte-counter scaling)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations' summary (the 'configs' object)")
+    ap.add_argument("--config-steps", type=int, default=20, help="timed forwards per other configuration")
     return ap.parse_args()
 
 
@@ -74,7 +77,9 @@ def stage_bytes_flops(wl, layer, fwd_state):
     }
 
 
-def run_gpu(args, wl):
+def run_gpu(args, wl, light=False):
+    """The forward metric of workload `wl` (timed region, per-stage pass); unless `light`,
+    also the materialising-dispatch, training and FFN-block passes."""
     import torch
     from kmoe import ops, synth
 
@@ -124,7 +129,7 @@ def run_gpu(args, wl):
         # the materialising dispatch (tables + the row copy; what the fp8 path and
         # the C-ABI's xperm output use), outside the timed region, on this routing
         rows_us = None
-        if not wl.fp8 and wl.routing != "expert_choice" and not wl.mod:
+        if not light and not wl.fp8 and wl.routing != "expert_choice" and not wl.mod:
             r0 = moe.router.route(x.reshape(wl.T, wl.d))
             cap = ops.capacity_of(moe.capacity_factor, wl.T, wl.k, wl.E) if moe.drop_overflow else 0
             for _ in range(3):
@@ -167,14 +172,52 @@ def run_gpu(args, wl):
         stage_out[name] = rec
     elapsed = t1 - t0
     training = None
-    if not (wl.fp8 or wl.mod or wl.routing == "expert_choice") and not args.no_train:
+    if not light and not (wl.fp8 or wl.mod or wl.routing == "expert_choice") and not args.no_train:
         training = run_training(args, wl, layer, x)
     block = None
-    if not (wl.fp8 or wl.mod or wl.routing == "expert_choice") and not args.no_block:
+    if not light and not (wl.fp8 or wl.mod or wl.routing == "expert_choice") and not args.no_block:
         block = run_block(args, wl, layer, x)
+    del layer, t, x
+    torch.cuda.empty_cache()
     return dict(elapsed=elapsed, stages=stage_out, a_kept=a_kept, a_all=a_all, t_in=t_in,
                 gemm_us=statistics.mean(gu_timed) if gu_timed else float("nan"), gemm_samples=len(gu_timed),
                 work=work, rows_us=rows_us, training=training, block=block)
+
+
+def config_summary(wl, res, steps):
+    """Tokens/s and roofline fractions of one configuration's forward."""
+    peak = PEAK_FP8 if wl.fp8 else PEAK_BF16
+    st = res["stages"]
+    out = {"workload": wl.name, "dtype": "fp8_e4m3" if wl.fp8 else "bf16", "tokens": wl.T,
+           "tokens_into_moe": res["t_in"], "assignments": res["a_all"], "assignments_kept": res["a_kept"],
+           "steps": steps, "tokens_per_s": round(wl.T * steps / res["elapsed"], 1),
+           "ms_per_step": round(res["elapsed"] / steps * 1e3, 4)}
+    us = res["gemm_us"]
+    if us == us:  # not NaN
+        out["gate_up_frac_peak"] = round(res["work"]["gemm_gate_up"][1] / (us * 1e-6) / peak, 4)
+        out["gate_up_launch_us"] = round(us, 2)
+    g_us = st.get("gemm_gate_up", {}).get("us", 0) + st.get("gemm_down", {}).get("us", 0)
+    if g_us:
+        fl = res["work"]["gemm_gate_up"][1] + res["work"]["gemm_down"][1]
+        out["gemm_TFLOPs"] = round(fl / (g_us * 1e-6) / 1e12, 1)
+        out["gemm_frac_peak"] = round(fl / (g_us * 1e-6) / peak, 4)
+        out["peak_TFLOPs"] = peak / 1e12
+    for name in ("router", "dispatch", "gather", "combine"):
+        if name in st and "GBps" in st[name]:
+            out[name] = {"us": st[name]["us"], "GBps": st[name]["GBps"], "frac_hbm": st[name]["frac_hbm"]}
+    out["stages_us"] = {k: v["us"] for k, v in st.items()}
+    return out
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def run_block(args, wl, layer, x):
@@ -315,6 +358,7 @@ def run_cpu_baseline(wl, tokens):
             times.append(time.perf_counter() - t0)
     med = statistics.median(times[1:])
     return {"value": round(tokens / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{tokens} tokens of the config-2 layer (d={wl.d}, E={wl.E}, top-{wl.k}, F={wl.F}), fp32, "
                       f"oracle/torch_port.py (reference op sequence: padded bmm experts), median of 3 after 1 warm-up",
             "seconds_per_forward": round(med, 3)}
@@ -373,6 +417,9 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(achieved, 1),
                      "peak": peak / 1e12, "unit": "TFLOP/s", "frac": round(achieved * 1e12 / peak, 4),
                      "traffic": traffic.get("bytes_per_launch") if traffic else None,
+                     "traffic_source": (f"profile constant, not measured in this run: profiles/traffic_gemm_gate_up_"
+                                        f"cfg{args.config}.json (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this "
+                                        f"kernel, scaled by a plain-copy calibration)") if traffic else None,
                      "work_per_launch": f"4*d*F*A_kept = {flops_gu:.4g} FLOP",
                      "launch_us": round(us, 2), "launch_samples": res["gemm_samples"]},
         "stages": res["stages"],
@@ -397,6 +444,17 @@ def main():
         out["training"] = res["training"]
     if res.get("block"):
         out["ffn_block"] = res["block"]
+    if not args.no_configs:
+        # the other configurations of BASELINE.json, each with its own timed region
+        import argparse as _ap
+        sub = _ap.Namespace(**vars(args))
+        sub.steps, sub.warmup, sub.stage_steps = args.config_steps, 5, 10
+        out["configs"] = {}
+        for n in (2, 3, 4, 5):
+            if n == args.config:
+                continue
+            wl_n = synth.WORKLOADS[n]
+            out["configs"][f"cfg{n}"] = config_summary(wl_n, run_gpu(sub, wl_n, light=True), sub.steps)
     if not args.no_cpu:
         out["cpu_baseline"] = run_cpu_baseline(synth.WORKLOADS[2], args.cpu_tokens)
     else:
