@@ -109,6 +109,23 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 __device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Direct global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4): the 64 lanes'
+// data lands at consecutive 16-byte slots from `lds` (a wave-uniform LDS address, M0).
+// Issued through inline asm on purpose: the compiler does not see these LDS writes, so it
+// adds no waits of its own for them.  For the builtin form it cannot tell the pipeline
+// stages apart and puts a vmcnt(0) (wait for every load in flight, including the ones
+// just issued for a later stage) in front of the next LDS read, which serialises a
+// multi-stage pipeline.  Callers order these loads with explicit wait_vmcnt<N>() and a
+// barrier before any lane reads the data.  Compiler-generated vmcnt waits for ordinary
+// loads stay correct (vmcnt counts all vector-memory loads in issue order, so extra
+// loads in flight only make them wait longer).
+__device__ __forceinline__ void dma16_to_lds(const void* src, KMOE_LDS void* lds) {
+  const uint32_t la = (uint32_t)(uintptr_t)lds;
+  // s_nop: the wait states gfx9 requires between an SALU write of M0 and an LDS-DMA
+  // instruction reading it (the compiler inserts them for its own instructions only)
+  asm volatile("s_nop 1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(la)));
+}
+
 // Wave-level reductions (64 lanes).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

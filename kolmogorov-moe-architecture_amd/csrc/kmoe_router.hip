@@ -113,11 +113,10 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
     const int kb = (kr < nk_all ? kr : kr - nk_all) * RKB;
 #pragma unroll
     for (int q = 0; q < G::XBLK; ++q)
-      __builtin_amdgcn_global_load_lds(xsrc[q] + kb, (KMOE_LDS void*)(st + (wave * G::XBLK + q) * 1024), 16, 0, 0);
+      dma16_to_lds(xsrc[q] + kb, (KMOE_LDS void*)(st + (wave * G::XBLK + q) * 1024));
 #pragma unroll
     for (int q = 0; q < G::WBLK; ++q)
-      __builtin_amdgcn_global_load_lds(wbase + wsrc[q] + kb,
-                                       (KMOE_LDS void*)(st + G::XT + (wave * G::WBLK + q) * 1024), 16, 0, 0);
+      dma16_to_lds(wbase + wsrc[q] + kb, (KMOE_LDS void*)(st + G::XT + (wave * G::WBLK + q) * 1024));
   };
 
   // ---- layer 1 on MFMA: wave (wm, wn) computes 32 tokens x 64 hidden; the next
