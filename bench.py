@@ -133,12 +133,12 @@ def run_gpu(args, wl, light=False):
             r0 = moe.router.route(x.reshape(wl.T, wl.d))
             cap = ops.capacity_of(moe.capacity_factor, wl.T, wl.k, wl.E) if moe.drop_overflow else 0
             for _ in range(3):
-                ops.dispatch(x.reshape(wl.T, wl.d), r0.idx, r0.w, wl.E, capacity=cap)
+                ops.dispatch(x.reshape(wl.T, wl.d), r0.idx, r0.w, wl.E, capacity=cap, block_counts=r0.block_counts)
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             for _ in range(10):
-                ops.dispatch(x.reshape(wl.T, wl.d), r0.idx, r0.w, wl.E, capacity=cap)
+                ops.dispatch(x.reshape(wl.T, wl.d), r0.idx, r0.w, wl.E, capacity=cap, block_counts=r0.block_counts)
             e1.record()
             torch.cuda.synchronize()
             rows_us = e0.elapsed_time(e1) / 10 * 1e3
@@ -436,7 +436,8 @@ def main():
         b = wl.T * wl.d * 2 + res["a_kept"] * wl.d * 2 + 8.0 * res["a_all"]
         out["dispatch_rows"] = {"us": round(res["rows_us"], 2), "GBps": round(b / (res["rows_us"] * 1e-6) / 1e9, 1),
                                 "frac_hbm": round(b / (res["rows_us"] * 1e-6) / PEAK_HBM, 4),
-                                "note": "materialising dispatch (tables + row copy), timed separately; the bf16 "
+                                "note": "materialising dispatch (tables from the router's block histograms + row "
+                                        "copy), as the training forward runs it, timed separately; the bf16 inference "
                                         "layer gathers rows inside the gate/up GEMM instead"}
     if "combine" in res["stages"]:
         out["combine_GBps"] = res["stages"]["combine"].get("GBps")

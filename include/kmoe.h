@@ -109,6 +109,16 @@ int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T, int d, con
                   int xperm_dtype, float* xperm_scale, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/* kmoe_dispatch with the per-block expert histograms given instead of counted from
+ * topk_idx: block_counts[b*E + e] = number of assignments (t, j) with t in
+ * [64b, 64b + 64) and topk_idx[t*k + j] == e, as kmoe_router_hist writes them.  Same
+ * results as kmoe_dispatch, one launch fewer.  Workspace as kmoe_dispatch.        */
+int kmoe_dispatch_counted(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
+                          const void* topk_w, int w_dtype, int k, int E, int64_t capacity,
+                          const int32_t* block_counts, int32_t* counts, int32_t* offsets, int32_t* row_token,
+                          int32_t* slot_row, float* slot_w, void* xperm, int xperm_dtype, float* xperm_scale,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* Allocation-free dispatch.  No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments, semantics and results as
@@ -329,6 +339,14 @@ int kmoe_pack_w_in_t(const void* w_in, int w_dtype, int d, void* out, void* stre
  * The caller folds the norm weight into the weights once per parameter version:
  *   w_in_g[j][i] = w_in[j][i] * w_norm[i];  w13 = kmoe_pack_weights(w1 * w_norm[:,None],
  *   w2 * w_norm[:,None], w3, ...).  x is then the un-normalised h.           */
+
+/* kmoe_router_train (hidden_pre nullable) that also writes each 64-token block's
+ * per-expert routed counts to block_counts (ceil(T/64) * E int32; k >= 1), the
+ * histograms kmoe_dispatch_counted takes: the router already holds every token's
+ * top-k, so the dispatch need not read topk_idx a second time to count them.      */
+int kmoe_router_hist(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,
+                     const void* w_out, int E, const float* logit_bias, int k, float* logits, int64_t* topk_idx,
+                     float* topk_w, float* partials, float* hidden_pre, int32_t* block_counts, void* stream);
 
 /* kmoe_router on RMSNorm(x): w_in_g carries the norm weight; the kernel computes
  * rscale[t] = 1/sqrt(mean(x[row(t)]^2) + eps) (f32, (T,)) from the x rows it reads and

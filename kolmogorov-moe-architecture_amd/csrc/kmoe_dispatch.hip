@@ -5,13 +5,15 @@
 // config 3 (keep the first `capacity` assignments of each expert in assignment
 // order, drop the rest).
 //
-// Two or three launches, no host sync:
-//   1. hist:    per-block (DTB tokens) expert histograms
+// Launches, no host sync:
+//   1. hist:    per-block (DTB tokens) expert histograms (skipped by
+//               kmoe_dispatch_counted: the router wrote them)
 //   2. scan:    per-expert exclusive scan over blocks -> block bases, counts,
 //               kept counts and expert offsets (up to FUSED_SCAN_MAX_BLOCKS blocks
 //               each permute block computes its own share of this instead)
-//   3. permute: per-block stable ranks via wave ballots, slot tables, then one
-//               read of each token row and k 16-byte-vector row writes
+//   3. permute: per-block stable ranks via wave ballots -> slot tables
+//   4. rows (when asked for): one wave per token reads its row once and writes its
+//               kept permuted rows (bf16 copy, or e4m3 with the per-token scale)
 #include <mutex>
 
 #include "kmoe_common.h"
@@ -78,7 +80,7 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ 
   }
 }
 
-// Tables of a block of DTB tokens, then (xperm != nullptr: the bf16 copy) the rows.
+// Tables of a block of DTB tokens (the rows are copied by scatter_rows_kernel).
 // FUSED_SCAN: the block computes its own per-expert base (sum of the counts of the
 // blocks before it), the totals and the expert offsets from all block counts (block
 // 0 also writes counts and offsets), instead of reading them from the scan kernel:
@@ -90,10 +92,9 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
     const int64_t* __restrict__ idx, const void* __restrict__ wsrc, int w_dtype, int k, int E, int64_t capacity,
     const int32_t* __restrict__ block_counts, int64_t nblk, const int32_t* __restrict__ block_base,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ row_token,
-    int32_t* __restrict__ slot_row, float* __restrict__ slot_w, uint16_t* __restrict__ xperm) {
+    int32_t* __restrict__ slot_row, float* __restrict__ slot_w) {
   __shared__ int wave_cnt[DTHREADS / 64][KMOE_MAX_EXPERTS];
   __shared__ int running[KMOE_MAX_EXPERTS];
-  __shared__ int dest[DTB * 8];  // k <= 8
   __shared__ int base_l[KMOE_MAX_EXPERTS];
   __shared__ int off_l[KMOE_MAX_EXPERTS + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -187,7 +188,6 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
       else
         wv = bf16_to_f32(static_cast<const uint16_t*>(wsrc)[a]);
       slot_w[a] = wv;
-      dest[a - a0] = row;
     }
     __syncthreads();
     if (tid < E) {
@@ -198,35 +198,44 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
     __syncthreads();
   }
 
-  // ---- row gather (bf16 copy): every 16-byte chunk of the block's token rows is
-  // read once and written to the token's k permuted rows; CP_UNR chunks in flight
-  // per thread (64 KiB per block).  Without xperm only the tables are written.
-  if (xperm == nullptr) return;
-  constexpr int CP_UNR = 16;
-  const int ntok = (int)min<int64_t>(DTB, T - t0);
-  const int nvec = d / 8;  // 16-byte vectors per row
-  const int total = ntok * nvec;
-  for (int c0 = tid; c0 < total; c0 += CP_UNR * DTHREADS) {
-    i32x4_t val[CP_UNR];
+}
+
+// bf16 rows of the materialising dispatch: one wave per token reads the token's row
+// once (ROW_REGS 16-byte vectors per lane at a time, all in flight together) and
+// writes it to each of its kept permuted rows (slot_row of its k assignments).  A
+// separate launch of T/4 workgroups keeps far more bytes in flight than a copy inside
+// the table kernel's 64-token blocks.
+__global__ __launch_bounds__(256) void scatter_rows_kernel(const uint16_t* __restrict__ x,
+                                                           const int32_t* __restrict__ row_index, int64_t T, int d,
+                                                           int k, const int32_t* __restrict__ slot_row,
+                                                           uint16_t* __restrict__ xperm) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  int rows[8];
+  bool any = false;
+  for (int j = 0; j < k; ++j) {
+    rows[j] = slot_row[t * k + j];
+    any |= rows[j] >= 0;
+  }
+  if (!any) return;  // every assignment of the token was dropped
+  const int nvec = d / 8;
+  const int64_t xr = row_index ? (int64_t)row_index[t] : t;
+  const i32x4_t* src = reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d);
+  for (int v0 = 0; v0 < nvec; v0 += 64 * ROW_REGS) {
+    i32x4_t r[ROW_REGS];
 #pragma unroll
-    for (int u = 0; u < CP_UNR; ++u) {
-      const int c = c0 + u * DTHREADS;
-      if (c < total) {
-        const int tl = c / nvec, v = c - tl * nvec;
-        const int64_t t = t0 + tl;
-        const int64_t xr = row_index ? (int64_t)row_index[t] : t;
-        val[u] = reinterpret_cast<const i32x4_t*>(x + xr * (int64_t)d)[v];
-      }
+    for (int i = 0; i < ROW_REGS; ++i) {
+      const int v = v0 + lane + 64 * i;
+      if (v < nvec) r[i] = src[v];
     }
+    for (int j = 0; j < k; ++j) {
+      if (rows[j] < 0) continue;
+      i32x4_t* dst = reinterpret_cast<i32x4_t*>(xperm + (int64_t)rows[j] * d);
 #pragma unroll
-    for (int u = 0; u < CP_UNR; ++u) {
-      const int c = c0 + u * DTHREADS;
-      if (c < total) {
-        const int tl = c / nvec, v = c - tl * nvec;
-        for (int j = 0; j < k; ++j) {
-          const int row = dest[tl * k + j];
-          if (row >= 0) reinterpret_cast<i32x4_t*>(xperm + (int64_t)row * d)[v] = val[u];
-        }
+      for (int i = 0; i < ROW_REGS; ++i) {
+        const int v = v0 + lane + 64 * i;
+        if (v < nvec) dst[v] = r[i];
       }
     }
   }
@@ -359,33 +368,40 @@ int check_dispatch_args(const char* who, const void* x, int64_t T, int d, const 
 int dispatch_launch(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
                     const void* topk_w, int w_dtype, int k, int E, int64_t capacity, int32_t* counts,
                     int32_t* offsets, int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm,
-                    int xperm_dtype, float* xperm_scale, void* workspace, hipStream_t s) {
+                    int xperm_dtype, float* xperm_scale, void* workspace, hipStream_t s,
+                    const int32_t* given_counts = nullptr) {
   const int64_t nblk = kmoe::ceil_div<int64_t>(T, DTB);
-  int32_t* block_counts = static_cast<int32_t*>(workspace);
-  int32_t* block_base = block_counts + nblk * E;
+  int32_t* ws_counts = static_cast<int32_t*>(workspace);
+  int32_t* block_base = ws_counts + nblk * E;
+  // the per-block histograms: given (kmoe_router_hist wrote them) or counted here
+  const int32_t* block_counts = given_counts ? given_counts : ws_counts;
   if (T == 0) {
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, (int64_t)0, E, capacity, block_base,
                        counts, offsets);
     return kmoe::check_launch("kmoe_dispatch(scan)");
   }
-  hipLaunchKernelGGL(hist_kernel, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, topk_idx, T, k, E, block_counts);
+  if (!given_counts)
+    hipLaunchKernelGGL(hist_kernel, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, topk_idx, T, k, E, ws_counts);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const bool fp8 = xperm_dtype == KMOE_DTYPE_FP8_E4M3;
-  uint16_t* xo = fp8 ? nullptr : static_cast<uint16_t*>(xperm);
   if (nblk <= FUSED_SCAN_MAX_BLOCKS) {
     hipLaunchKernelGGL(permute_kernel<true>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
                        topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, block_base, counts, offsets,
-                       row_token, slot_row, slot_w, xo);
+                       row_token, slot_row, slot_w);
   } else {
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, nblk, E, capacity, block_base, counts,
                        offsets);
     hipLaunchKernelGGL(permute_kernel<false>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
                        topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, block_base, counts, offsets,
-                       row_token, slot_row, slot_w, xo);
+                       row_token, slot_row, slot_w);
   }
+  const dim3 rows_grid((unsigned)kmoe::ceil_div<int64_t>(T, 4));
   if (fp8)
-    hipLaunchKernelGGL(quant_scatter_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0, s, xp,
-                       row_index, T, d, k, slot_row, static_cast<uint8_t*>(xperm), xperm_scale);
+    hipLaunchKernelGGL(quant_scatter_kernel, rows_grid, dim3(256), 0, s, xp, row_index, T, d, k, slot_row,
+                       static_cast<uint8_t*>(xperm), xperm_scale);
+  else if (xperm)
+    hipLaunchKernelGGL(scatter_rows_kernel, rows_grid, dim3(256), 0, s, xp, row_index, T, d, k, slot_row,
+                       static_cast<uint16_t*>(xperm));
   return kmoe::check_launch("kmoe_dispatch");
 }
 
@@ -434,6 +450,24 @@ extern "C" int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T,
                "kmoe_dispatch: workspace %zu < %zu bytes", workspace_bytes, need);
   return dispatch_launch(x, row_index, T, d, topk_idx, topk_w, w_dtype, k, E, capacity, counts, offsets, row_token,
                          slot_row, slot_w, xperm, xperm_dtype, xperm_scale, workspace, kmoe::as_stream(stream));
+}
+
+extern "C" int kmoe_dispatch_counted(const void* x, const int32_t* row_index, int64_t T, int d,
+                                     const int64_t* topk_idx, const void* topk_w, int w_dtype, int k, int E,
+                                     int64_t capacity, const int32_t* block_counts, int32_t* counts, int32_t* offsets,
+                                     int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm,
+                                     int xperm_dtype, float* xperm_scale, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  int rc = check_dispatch_args("kmoe_dispatch_counted", x, T, d, topk_idx, topk_w, w_dtype, k, E, counts, offsets,
+                               row_token, slot_row, slot_w, xperm, xperm_dtype, xperm_scale);
+  if (rc) return rc;
+  KMOE_REQUIRE(block_counts, KMOE_ERR_NULL, "kmoe_dispatch_counted: null block_counts");
+  const size_t need = kmoe_dispatch_workspace_bytes(T, k, E);
+  KMOE_REQUIRE(workspace && workspace_bytes >= need, KMOE_ERR_WORKSPACE,
+               "kmoe_dispatch_counted: workspace %zu < %zu bytes", workspace_bytes, need);
+  return dispatch_launch(x, row_index, T, d, topk_idx, topk_w, w_dtype, k, E, capacity, counts, offsets, row_token,
+                         slot_row, slot_w, xperm, xperm_dtype, xperm_scale, workspace, kmoe::as_stream(stream),
+                         block_counts);
 }
 
 extern "C" int kmoe_dispatch_noalloc(const void* x, const int32_t* row_index, int64_t T, int d,

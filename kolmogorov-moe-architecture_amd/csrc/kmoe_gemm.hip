@@ -317,7 +317,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   // writes them to LDS.  Lane l of a block covers bytes [16l, 16l+16) of it (tile row
   // 8q + l/8, physical chunk l%8) and so loads the logical chunk that swz() maps
   // there: the LDS write of a block is one contiguous, conflict-free 1 KiB.  A rows
-  // past the expert's last row are clamped to it (their results are never stored).
+  // past the expert's last row read as zeros (their results are never stored).
   const int rsub = lane / CPR, pc = lane % CPR;
   uint32_t a_off[BLK_PER_WAVE], b_off[8];
   const int a_last = m_end - 1 - m0;
@@ -336,11 +336,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
       for (int qa = 0; qa < BLK_PER_WAVE; ++qa) ra[qa] = g.row_index[ra[qa]];
     }
   }
+  // Tile rows past the expert's end load zeros instead: an offset beyond the buffer
+  // window's 2 GiB record count makes the hardware return 0 without a memory access
+  // (the scalar K offset is not range-checked, the per-lane offset is).  Their results
+  // are never stored; zero operands spare the memory traffic and the MFMA power of
+  // real data (the expert GEMMs run power-limited).
+  constexpr uint32_t A_OOB = 0x80000000u;
 #pragma unroll
   for (int qa = 0; qa < BLK_PER_WAVE; ++qa) {
     const int tr = (wave * BLK_PER_WAVE + qa) * RPB + rsub;
     const uint32_t chunk = (uint32_t)(pc ^ ((tr >> 1) & (CPR - 1))) << 4;
-    a_off[qa] = (uint32_t)ra[qa] * (uint32_t)g.lda_bytes + chunk;
+    a_off[qa] = tr > a_last ? A_OOB + chunk : (uint32_t)ra[qa] * (uint32_t)g.lda_bytes + chunk;
   }
 #pragma unroll
   for (int qb = 0; qb < BLK_B; ++qb) {

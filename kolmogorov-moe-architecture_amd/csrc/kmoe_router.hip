@@ -54,7 +54,8 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
                                                             float* __restrict__ logits, int64_t* __restrict__ topk_idx,
                                                             float* __restrict__ topk_w, float* __restrict__ partials,
                                                             float* __restrict__ hidden_pre, float eps,
-                                                            float* __restrict__ rscale) {
+                                                            float* __restrict__ rscale,
+                                                            int32_t* __restrict__ block_counts) {
   using G = RtGeom<RKB>;
   constexpr int RT_STAGES = rt_stages<NE, RKB>();
   constexpr int RT_STAGE = G::STAGE;
@@ -227,6 +228,9 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   const int64_t ntok = T - tok0 < RT_TOK ? T - tok0 : RT_TOK;
   if (tid < RT_TOK) {
     const int64_t t = tok0 + tid;
+    int sel[8];  // this token's experts (k <= 8); -1 past T
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sel[j] = -1;
     float L[NE];
 #pragma unroll
     for (int q = 0; q < NE / 4; ++q) {
@@ -259,7 +263,6 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
       if (k > 0) {
         // k selections over the registers; strict '>' keeps the lower index on ties
         uint64_t taken = 0;
-        int sel[8];
         float sev[8];
         float ssum = 0.0f;
         for (int j = 0; j < k; ++j) {
@@ -288,6 +291,18 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
 #pragma unroll
       for (int q = 0; q < NE / 4; ++q) *reinterpret_cast<f32x4_t*>(P + 4 * q) = f32x4_t{0.f, 0.f, 0.f, 0.f};
       lse2[tid] = 0.0f;
+    }
+    // the block's per-expert routed counts (the dispatch's histogram of these 64
+    // tokens): lane e sums the ballots of expert e over the k picks
+    if (block_counts && k > 0) {
+      int cnt = 0;
+      for (int j = 0; j < k; ++j) {
+        for (int e = 0; e < E; ++e) {
+          const uint64_t m = __ballot(sel[j] == e);
+          if (lane == e) cnt += __popcll(m);
+        }
+      }
+      if (lane < E) block_counts[(int64_t)blockIdx.x * E + lane] = cnt;
     }
   }
   __syncthreads();
@@ -346,7 +361,8 @@ extern "C" int64_t kmoe_router_partials_len(int64_t T, int E) {
 namespace {
 int router_launch(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in, const void* w_out,
                   int E, const float* logit_bias, int k, float* logits, int64_t* topk_idx, float* topk_w,
-                  float* partials, float* hidden_pre, float eps, float* rscale, void* stream) {
+                  float* partials, float* hidden_pre, float eps, float* rscale, int32_t* block_counts,
+                  void* stream) {
   KMOE_REQUIRE(x && w_in && w_out && logits, KMOE_ERR_NULL, "kmoe_router: null x/w_in/w_out/logits");
   KMOE_REQUIRE(T >= 0 && T <= (int64_t)1 << 31, KMOE_ERR_SHAPE, "kmoe_router: T=%lld out of range",
                (long long)T);
@@ -367,10 +383,12 @@ int router_launch(const void* x, const int32_t* row_index, int64_t T, int d, con
   do {                                                                                                         \
     if (d % 128 == 0 && rt_stages<NE_, 256>() >= 3)                                                            \
       hipLaunchKernelGGL((router_kernel<NE_, 256, RMS_>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, \
-                         wo, E, logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre, eps, rscale);    \
+                         wo, E, logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre, eps, rscale,     \
+                         block_counts);                                                                        \
     else                                                                                                       \
       hipLaunchKernelGGL((router_kernel<NE_, 128, RMS_>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, \
-                         wo, E, logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre, eps, rscale);    \
+                         wo, E, logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre, eps, rscale,     \
+                         block_counts);                                                                        \
   } while (0)
 #define KMOE_ROUTER_LAUNCH(NE_)             \
   do {                                      \
@@ -397,7 +415,16 @@ extern "C" int kmoe_router_train(const void* x, const int32_t* row_index, int64_
                                  const void* w_out, int E, const float* logit_bias, int k, float* logits,
                                  int64_t* topk_idx, float* topk_w, float* partials, float* hidden_pre, void* stream) {
   return router_launch(x, row_index, T, d, w_in, w_out, E, logit_bias, k, logits, topk_idx, topk_w, partials,
-                       hidden_pre, 0.0f, nullptr, stream);
+                       hidden_pre, 0.0f, nullptr, nullptr, stream);
+}
+
+extern "C" int kmoe_router_hist(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,
+                                const void* w_out, int E, const float* logit_bias, int k, float* logits,
+                                int64_t* topk_idx, float* topk_w, float* partials, float* hidden_pre,
+                                int32_t* block_counts, void* stream) {
+  KMOE_REQUIRE(block_counts && k >= 1, KMOE_ERR_NULL, "kmoe_router_hist: needs block_counts and k >= 1");
+  return router_launch(x, row_index, T, d, w_in, w_out, E, logit_bias, k, logits, topk_idx, topk_w, partials,
+                       hidden_pre, 0.0f, nullptr, block_counts, stream);
 }
 
 extern "C" int kmoe_router_rms(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in_g,
@@ -407,7 +434,7 @@ extern "C" int kmoe_router_rms(const void* x, const int32_t* row_index, int64_t 
   KMOE_REQUIRE(rscale, KMOE_ERR_NULL, "kmoe_router_rms: null rscale");
   KMOE_REQUIRE(eps >= 0.0f, KMOE_ERR_SHAPE, "kmoe_router_rms: eps must be >= 0");
   return router_launch(x, row_index, T, d, w_in_g, w_out, E, logit_bias, k, logits, topk_idx, topk_w, partials,
-                       nullptr, eps, rscale, stream);
+                       nullptr, eps, rscale, nullptr, stream);
 }
 
 extern "C" int kmoe_router(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,

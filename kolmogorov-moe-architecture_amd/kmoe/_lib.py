@@ -38,6 +38,8 @@ _SIGNATURES = {
     "kmoe_dispatch_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "kmoe_dispatch": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp,
                              _vp, _i32, _vp, _vp, _sz, _vp]),
+    "kmoe_dispatch_counted": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp,
+                                     _vp, _vp, _vp, _i32, _vp, _vp, _sz, _vp]),
     "kmoe_dispatch_noalloc": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp,
                                      _vp, _vp, _i32, _vp, _vp]),
     "kmoe_gather_rows": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp]),
@@ -58,6 +60,7 @@ _SIGNATURES = {
     "kmoe_mod_workspace_bytes": (_sz, [_i32, _i64]),
     "kmoe_mod_select": (_i32, [_vp, _i32, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     # backward pass
+    "kmoe_router_hist": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_router_train": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_gemm_gate_up_rows_gu": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp]),
     "kmoe_router_rms": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _f32, _vp, _vp]),

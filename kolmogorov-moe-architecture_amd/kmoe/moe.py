@@ -189,22 +189,23 @@ class GroupedExperts(_PackedExperts):
     """Token-choice grouped SwiGLU experts (moe.py:161-294)."""
 
     def run(self, x2d, expert_indices, expert_weights, row_index=None, T_out=None, out_map=None, scale=None,
-            out_dtype=torch.bfloat16, residual=None, capacity=0):
+            out_dtype=torch.bfloat16, residual=None, capacity=0, block_counts=None):
         """dispatch -> grouped GEMMs -> combine (+ residual, added in the combine); returns (y, DispatchOut).
         capacity > 0 drops each expert's assignments past the first `capacity` (MoELayer's
         drop_overflow rule); 0, the default and what forward() uses, drops nothing (the
-        reference's GroupedExperts never drops)."""
+        reference's GroupedExperts never drops).  block_counts: the router's per-block
+        histograms of expert_indices (RouterOut.block_counts), if it wrote them."""
         E = self.n_experts
         pw = self.packed()
         T, k = expert_indices.shape
         if pw.fp8:
             disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=capacity, fp8=True,
-                                row_index=row_index)
+                                row_index=row_index, block_counts=block_counts)
             yperm = ops.grouped_ffn(disp.xperm, disp.xscale, disp.offsets, pw, T * k)
         else:
             # bf16: the gate/up GEMM gathers the token rows itself (no permuted copy of x)
             disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=capacity,
-                                row_index=row_index, materialize=False)
+                                row_index=row_index, materialize=False, block_counts=block_counts)
             h = ops.gemm_gate_up_rows(x2d, row_index, disp.row_token, disp.offsets, pw, T * k)
             yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k),
@@ -369,7 +370,7 @@ class MoELayer(nn.Module):
         pw = ge.packed()
         # the permuted x rows are kept for the weight gradient (the gate/up GEMM still
         # gathers its own A rows from x)
-        disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=True)
+        disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=True, block_counts=r.block_counts)
         h, gu = ops.gemm_gate_up_rows(x2d, None, disp.row_token, disp.offsets, pw, T * k, save_gu=True)
         yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T, out_dtype=out_dtype)
@@ -403,7 +404,8 @@ class MoELayer(nn.Module):
         r = self.router.route(x2d, row_index=row_index, T=T)
         cap = ops.capacity_of(self.capacity_factor, T, self.top_k, self.n_experts) if self.drop_overflow else 0
         y, disp = self.grouped_experts.run(x2d, r.idx, r.w, row_index=row_index, T_out=T_out, out_map=out_map,
-                                           scale=scale, out_dtype=out_dtype, residual=residual, capacity=cap)
+                                           scale=scale, out_dtype=out_dtype, residual=residual, capacity=cap,
+                                           block_counts=r.block_counts)
         return y, r, disp
 
     def _set_token_choice_aux(self, r, disp, T):

@@ -78,16 +78,19 @@ class RouterOut(NamedTuple):
     partials: torch.Tensor        # per-block aux partial sums
     hidden: Optional[torch.Tensor] = None  # (T, 128) f32 pre-activation (training router)
     rscale: Optional[torch.Tensor] = None  # (T,) f32 RMSNorm scale 1/sqrt(mean(x^2)+eps) (rms router)
+    block_counts: Optional[torch.Tensor] = None  # (ceil(T/64), E) int32 per-block routed counts
 
 
 def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=False,
-           rms_eps=None) -> RouterOut:
+           rms_eps=None, hist=True) -> RouterOut:
     """logits/top-k of the reference Router (moe.py:423-462) on the HIP kernel.
 
     x2d: (rows, d) bf16; w_in: (128, d); w_out: (E, 128); row_index: optional
     int32 (T,) selecting the rows of x2d that are the tokens.
     rms_eps: route RMSNorm(x) (embeddings.py:167-195) with the norm weight already
     folded into w_in's columns; the result carries the per-token scale (rscale).
+    hist (k > 0, not rms): also return each 64-token block's per-expert routed counts,
+    which dispatch(block_counts=...) takes instead of counting them again.
     """
     _need_gpu(x2d, w_in, w_out)
     x2d = _contig(x2d, _BF16)
@@ -116,6 +119,12 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=F
             _lib.call("kmoe_router_rms", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
                       ptr(logits), ptr(idx), ptr(w), ptr(partials), float(rms_eps), ptr(rscale), _stream(x2d))
         return RouterOut(logits, idx, w, partials, None, rscale)
+    if hist and k > 0 and T > 0:
+        bc = torch.empty(npart // (E + 1), E, device=dev, dtype=torch.int32)
+        with _Stage("router"):
+            _lib.call("kmoe_router_hist", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
+                      ptr(logits), ptr(idx), ptr(w), ptr(partials), ptr(hidden), ptr(bc), _stream(x2d))
+        return RouterOut(logits, idx, w, partials, hidden, None, bc)
     with _Stage("router"):
         _lib.call("kmoe_router_train", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
                   ptr(logits), ptr(idx), ptr(w), ptr(partials), ptr(hidden), _stream(x2d))
@@ -164,13 +173,15 @@ def capacity_of(cf: float, T: int, k: int, E: int) -> int:
 
 
 def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None, materialize=True,
-             no_alloc=False) -> DispatchOut:
+             no_alloc=False, block_counts=None) -> DispatchOut:
     """Stable counting-sort dispatch (moe.py:238-272) + optional capacity drop.
 
     materialize=False (bf16 only) writes the routing tables but not the permuted
     rows: gemm_gate_up_rows gathers them itself (xperm is then None).
     no_alloc=True calls kmoe_dispatch_noalloc, whose histograms live in the library's
-    own device scratch (no workspace allocation; calls on one GPU must not overlap)."""
+    own device scratch (no workspace allocation; calls on one GPU must not overlap).
+    block_counts: the router's per-block histograms of idx (RouterOut.block_counts);
+    kmoe_dispatch_counted then skips counting them."""
     if not materialize and fp8:
         raise ValueError("kmoe.dispatch: the fp8 path needs the quantised permuted rows (materialize=True)")
     _need_gpu(x2d, idx, w)
@@ -200,6 +211,15 @@ def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None, materialize=
         return DispatchOut(counts, offsets, row_token, slot_row, slot_w, xperm, xscale)
     wsb = lib.kmoe_dispatch_workspace_bytes(T, k, E)
     ws = torch.empty(wsb, device=dev, dtype=torch.uint8)
+    if block_counts is not None:
+        if block_counts.dtype != torch.int32 or block_counts.numel() != ((T + 63) // 64) * E:
+            raise ValueError("kmoe.dispatch: block_counts must be int32 (ceil(T/64), E)")
+        with _Stage("dispatch"):
+            _lib.call("kmoe_dispatch_counted", ptr(x2d), ptr(row_index), T, d, ptr(idx), ptr(w), wdt, k, E,
+                      int(capacity), ptr(block_counts), ptr(counts), ptr(offsets), ptr(row_token), ptr(slot_row),
+                      ptr(slot_w), ptr(xperm), _lib.DTYPE_FP8_E4M3 if fp8 else _lib.DTYPE_BF16, ptr(xscale),
+                      ptr(ws), wsb, _stream(x2d))
+        return DispatchOut(counts, offsets, row_token, slot_row, slot_w, xperm, xscale)
     with _Stage("dispatch"):
         _lib.call("kmoe_dispatch", ptr(x2d), ptr(row_index), T, d, ptr(idx), ptr(w), wdt, k, E, int(capacity),
               ptr(counts), ptr(offsets), ptr(row_token), ptr(slot_row), ptr(slot_w), ptr(xperm),

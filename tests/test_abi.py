@@ -120,3 +120,17 @@ def test_dispatch_noalloc_validation(lib):
     assert _err(lib, "kmoe_dispatch_noalloc", *bad)[0] == -1
     # the largest size that fits is accepted by the size check (T*E = 2^25 - 8192 for k=2)
     assert lib.kmoe_dispatch_workspace_bytes((1 << 21) - 512, 2, 16) <= 4 << 20
+
+
+def test_counted_dispatch_and_router_hist_validation(lib):
+    args = [FAKE, NULL, 16, 64, FAKE, FAKE, _lib.DTYPE_F32, 2, 8, 0, NULL, FAKE, FAKE, FAKE, FAKE, FAKE, NULL,
+            _lib.DTYPE_BF16, NULL, FAKE, 1 << 20, NULL]
+    rc, msg = _err(lib, "kmoe_dispatch_counted", *args)
+    assert rc == -1 and "block_counts" in msg
+    good = list(args)
+    good[10] = FAKE
+    good[20] = 8  # workspace too small
+    assert _err(lib, "kmoe_dispatch_counted", *good)[0] == -4
+    rc, msg = _err(lib, "kmoe_router_hist", FAKE, NULL, 16, 64, FAKE, FAKE, 8, NULL, 2, FAKE, FAKE, FAKE, NULL, NULL,
+                   NULL, NULL)
+    assert rc == -1 and "block_counts" in msg

@@ -146,6 +146,73 @@ def test_dispatch_parity(dev, T, k, E, cap, skew):
     assert torch.equal(out.xperm[:A_kept].cpu(), xb.cpu()[torch.from_numpy(ref["row_token"][:A_kept])])
 
 
+@pytest.mark.parametrize("T,d,E,k,rows", [(16384, 2048, 16, 2, False), (1000, 128, 64, 4, False), (33, 64, 5, 1, False),
+                                           (3000, 256, 16, 2, True)])
+def test_router_block_counts(dev, T, d, E, k, rows):
+    """kmoe_router_hist's per-64-token-block expert counts = the bincount of its own top-k
+    ids per block (numpy), also with a row_index (MoD's selected rows) and a ragged last
+    block; its logits and ids are those of kmoe_router."""
+    x, w_in, w_out = gen(300 + E, (T + 100, d), (128, d), (E, 128))
+    xb, wib, wob = bf16(x).to(dev), bf16(w_in * 0.02).to(dev), bf16(w_out * 0.02).to(dev)
+    ri = None
+    if rows:
+        ri = torch.randperm(T + 100, generator=torch.Generator().manual_seed(4))[:T].to(torch.int32).to(dev)
+    r = ops.router(xb, wib, wob, k, row_index=ri, T=T)
+    r0 = ops.router(xb, wib, wob, k, row_index=ri, T=T, hist=False)
+    torch.cuda.synchronize()
+    assert r.block_counts is not None and r0.block_counts is None
+    assert torch.equal(r.idx, r0.idx) and torch.equal(r.logits, r0.logits)
+    idx = r.idx.cpu().numpy()
+    nb = (T + 63) // 64
+    ref = np.zeros((nb, E), np.int64)
+    for b in range(nb):
+        ref[b] = np.bincount(idx[64 * b:64 * b + 64].reshape(-1), minlength=E)
+    assert np.array_equal(r.block_counts.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("T,k,E,cap,fp8,mat", [(16384, 2, 16, 2560, False, True), (16384, 2, 16, 0, False, False),
+                                               (70000, 2, 8, 0, False, True), (777, 3, 7, 50, True, True),
+                                               (5000, 8, 64, 0, False, True)])
+def test_dispatch_counted_matches_dispatch(dev, T, k, E, cap, fp8, mat):
+    """kmoe_dispatch_counted with the router's block histograms gives kmoe_dispatch's
+    results bit for bit (tables, permuted rows, fp8 codes and scales); T = 70000 takes
+    the separate scan kernel."""
+    d = 128
+    x, w_in, w_out = gen(400 + T % 97, (T, d), (128, d), (E, 128))
+    xb, wib, wob = bf16(x).to(dev), bf16(w_in * 0.05).to(dev), bf16(w_out * 0.05).to(dev)
+    r = ops.router(xb, wib, wob, k)
+    a = ops.dispatch(xb, r.idx, r.w, E, capacity=cap, fp8=fp8, materialize=mat)
+    b = ops.dispatch(xb, r.idx, r.w, E, capacity=cap, fp8=fp8, materialize=mat, block_counts=r.block_counts)
+    torch.cuda.synchronize()
+    n = int(a.offsets[-1])
+    for name in ("counts", "offsets", "slot_row", "slot_w"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    assert torch.equal(a.row_token[:n], b.row_token[:n])
+    if mat:
+        assert torch.equal(a.xperm[:n].view(torch.uint8), b.xperm[:n].view(torch.uint8))
+    if fp8:
+        assert torch.equal(a.xscale[:n], b.xscale[:n])
+    ref = O.dispatch(r.idx.cpu().numpy(), E, cap)
+    assert np.array_equal(b.slot_row.cpu().numpy()[: T * k], ref["slot_row"])
+
+
+def test_dispatch_rows_bf16_row_index_wide(dev):
+    """The materialising bf16 dispatch through a row_index with the capacity drop, and a
+    row wider than one register pass (d = 10240: the row copy loops)."""
+    for T, d, E, k, cap in ((3000, 512, 16, 2, 300), (300, 10240, 4, 2, 0)):
+        (x,) = gen(17, (T + 200, d))
+        rows = torch.randperm(T + 200, generator=torch.Generator().manual_seed(3))[:T].to(torch.int32)
+        idx, w = _routing(T, k, E, 18, True)
+        xb = bf16(x).to(dev)
+        out = ops.dispatch(xb, idx.to(dev), w.to(dev), E, capacity=cap, row_index=rows.to(dev))
+        torch.cuda.synchronize()
+        ref = O.dispatch(idx.numpy(), E, cap)
+        n = int(ref["offsets"][-1])
+        assert np.array_equal(out.row_token.cpu().numpy()[:n], ref["row_token"][:n])
+        src = xb.cpu()[rows.long()][torch.from_numpy(ref["row_token"][:n])]
+        assert torch.equal(out.xperm[:n].cpu(), src)
+
+
 def test_dispatch_fp8_and_row_index(dev):
     T, k, E, d = 3000, 2, 16, 512
     (x,) = gen(13, (T + 500, d))
