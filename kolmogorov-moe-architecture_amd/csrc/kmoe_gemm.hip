@@ -926,6 +926,167 @@ __global__ void zero_f32_kernel(float* __restrict__ p, int64_t n) {
     p[i] = 0.0f;
 }
 
+// bf16 pack of one weight matrix per expert, in[e] (R x Cn) row-major -> out rows
+// (out[e][map(c)][r] = in[e][r][c], map as in pack_transpose_kernel), 16 bytes per
+// global access: a 64 x 64 tile is read as 8-element row vectors (bf16 16 B, f32 2 x
+// 16 B), transposed through LDS, and written as 8-element vectors of output rows.
+// Entries of out that no input element maps to (the pad after each row, padding
+// rows) are left alone (pack_pad_kernel zeroes them).
+template <bool IN_F32>
+__global__ __launch_bounds__(256) void pack_t16_kernel(const void* __restrict__ in, int R, int Cn,
+                                                       int64_t in_expert_stride, int half, bool gate_up,
+                                                       uint16_t* __restrict__ out, int64_t out_rows, int out_ld) {
+  __shared__ uint16_t tile[64][72];  // [input col][input row], rows padded to 144 B
+  const int e = blockIdx.z;
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tid = threadIdx.x;
+  // load: thread -> (row r0 + tid/8 + 32 i, cols c0 + 8 (tid%8) .. +8), i = 0, 1
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int rr = tid / 8 + 32 * i, cc = 8 * (tid % 8);
+    const int r = r0 + rr, c = c0 + cc;
+    uint16_t v[8];
+    const int64_t off = (int64_t)e * in_expert_stride + (int64_t)r * Cn + c;
+    if (r < R && c + 8 <= Cn && off % (IN_F32 ? 4 : 8) == 0) {
+      if (IN_F32) {
+        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(static_cast<const float*>(in) + off);
+        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(static_cast<const float*>(in) + off + 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v[q] = f32_to_bf16(a[q]);
+          v[4 + q] = f32_to_bf16(b[q]);
+        }
+      } else {
+        const i32x4_t a = *reinterpret_cast<const i32x4_t*>(static_cast<const uint16_t*>(in) + off);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v[2 * q] = (uint16_t)((uint32_t)a[q] & 0xffffu);
+          v[2 * q + 1] = (uint16_t)((uint32_t)a[q] >> 16);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int cq = c + q;
+        float f = 0.0f;
+        if (r < R && cq < Cn) {
+          const int64_t off = (int64_t)e * in_expert_stride + (int64_t)r * Cn + cq;
+          f = IN_F32 ? static_cast<const float*>(in)[off] : bf16_to_f32(static_cast<const uint16_t*>(in)[off]);
+        }
+        v[q] = f32_to_bf16(f);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) tile[cc + q][rr] = v[q];
+  }
+  __syncthreads();
+  // store: thread -> (output row for input col c0 + tid/8 + 32 i, 8 elements r0 + 8 (tid%8))
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int cc = tid / 8 + 32 * i, rr = 8 * (tid % 8);
+    const int c = c0 + cc, r = r0 + rr;
+    if (c >= Cn || r >= R) continue;
+    const int64_t orow = gate_up ? (int64_t)(c / 128) * 256 + half * 128 + (c % 128) : (int64_t)c;
+    uint16_t* dst = out + ((int64_t)e * out_rows + orow) * out_ld + r;
+    if (r + 8 <= R) {
+      i32x4_t w;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        w[q] = (int)((uint32_t)tile[cc][rr + 2 * q] | ((uint32_t)tile[cc][rr + 2 * q + 1] << 16));
+      *reinterpret_cast<i32x4_t*>(dst) = w;
+    } else {
+      for (int q = 0; r + q < R; ++q) dst[q] = tile[cc][rr + q];
+    }
+  }
+}
+
+// Zeroes what pack_t16_kernel leaves: in every packed row the elements [valid_cols,
+// out_ld), and the whole rows that no input column maps to (is_pad_row), 8 bytes at
+// a time (row strides are multiples of 8 bytes).
+__global__ __launch_bounds__(256) void pack_pad_kernel(uint16_t* __restrict__ out, int64_t n_rows, int out_ld,
+                                                       int valid_cols, int rows_per_expert, int valid_in_cols,
+                                                       bool gate_up) {
+  const int words = out_ld / 4;  // 8-byte words per row
+  const int64_t n = n_rows * words;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / words;
+    const int w = (int)(i - row * words);
+    const int pr = (int)(row % rows_per_expert);
+    // the input column this packed row holds (gate_up: w1 / w2 column f of block f/128)
+    const int c = gate_up ? (pr / 256) * 128 + (pr % 128) : pr;
+    const bool pad_row = c >= valid_in_cols;
+    if (pad_row || 4 * w >= valid_cols) {
+      reinterpret_cast<uint64_t*>(out + row * out_ld)[w] = 0ull;
+    } else if (4 * w + 4 > valid_cols) {
+      // the word that straddles the end of the valid columns: its tail only
+      for (int q = valid_cols - 4 * w; q < 4; ++q) out[row * out_ld + 4 * w + q] = 0;
+    }
+  }
+}
+
+// Backward packed layouts (rows K-contiguous, WPAD bytes after every row, zero padded):
+//   w3n : (E, round_up(F, 256), d)        row f = w3[e][f][:]            (dh = dY . w3^T, K = d)
+//   w13t: (E, round_up(d, 256), 2*F_pad)  row i = w1[e][i][:], w2[e][i][:] interleaved per 128
+//                                          columns like w13's rows        (dX = [dg|du] . w13, K = 2*F_pad)
+// Both are row copies with the columns rearranged (no transpose), 16 bytes per access;
+// rows past F (w3n) or d (w13t) and the pads are written as zeros.
+template <bool IN_F32>
+__global__ __launch_bounds__(256) void pack_rows16_kernel(const void* __restrict__ w1, const void* __restrict__ w2,
+                                                          const void* __restrict__ w3, int d, int F, bool w13t,
+                                                          uint16_t* __restrict__ out, int64_t out_rows, int out_ld,
+                                                          int E) {
+  const int nv = out_ld / 8;  // 16-byte vectors per packed row
+  const int64_t n = (int64_t)E * out_rows * nv;
+  const int Fp = round_up(F, 128);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t grow = i / nv;
+    const int v = (int)(i - grow * nv);
+    const int e = (int)(grow / out_rows);
+    const int64_t row = grow - (int64_t)e * out_rows;
+    const int c = 8 * v;  // first packed column of the vector
+    const void* src = nullptr;
+    int64_t off = 0;
+    int n_ok = 0;  // source elements that exist (the rest are zero)
+    if (w13t) {
+      if (row < d && c < 2 * Fp) {
+        const int half = (c >> 7) & 1, f = (c >> 8) * 128 + (c & 127);
+        src = half ? w2 : w1;
+        off = ((int64_t)e * d + row) * F + f;
+        n_ok = F - f < 8 ? (F - f > 0 ? F - f : 0) : 8;
+      }
+    } else if (row < F && c < d) {
+      src = w3;
+      off = ((int64_t)e * F + row) * d + c;
+      n_ok = d - c < 8 ? d - c : 8;
+    }
+    i32x4_t wv = {0, 0, 0, 0};
+    if (n_ok == 8 && (off % (IN_F32 ? 4 : 8)) == 0) {
+      if (IN_F32) {
+        const float* p = static_cast<const float*>(src) + off;
+        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p);
+        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p + 4);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          wv[q] = (int)((uint32_t)f32_to_bf16(a[2 * q]) | ((uint32_t)f32_to_bf16(a[2 * q + 1]) << 16));
+          wv[2 + q] = (int)((uint32_t)f32_to_bf16(b[2 * q]) | ((uint32_t)f32_to_bf16(b[2 * q + 1]) << 16));
+        }
+      } else {
+        wv = *reinterpret_cast<const i32x4_t*>(static_cast<const uint16_t*>(src) + off);
+      }
+    } else {
+      uint16_t t[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        t[q] = q < n_ok ? (IN_F32 ? f32_to_bf16(static_cast<const float*>(src)[off + q])
+                                  : static_cast<const uint16_t*>(src)[off + q])
+                        : (uint16_t)0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wv[q] = (int)((uint32_t)t[2 * q] | ((uint32_t)t[2 * q + 1] << 16));
+    }
+    *reinterpret_cast<i32x4_t*>(out + grow * out_ld + c) = wv;
+  }
+}
+
 // Per-row fp8 quantisation of a bf16 matrix, one wave per row.
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restrict__ in, int64_t rows,
                                                          const int32_t* __restrict__ n_rows_dev, int cols,
@@ -1053,12 +1214,39 @@ extern "C" int kmoe_pack_weights(const void* w1, const void* w2, const void* w3,
   hipStream_t s = kmoe::as_stream(stream);
   const int Fp = round_up(F, 128), dp = round_up(d, 256);
   const int64_t rows13 = 2 * (int64_t)Fp, rows3 = dp;
-  // zero the padding (whole buffers: simple and only done when weights change)
+  const bool f32 = w_dtype == KMOE_DTYPE_F32;
+  if (!fp8) {
+    // bf16: vectorised transposes, then zeros in the pads and padding rows only
+    const int ld13 = d + WPAD / 2, ld3 = Fp + WPAD / 2;
+    uint16_t* o13 = static_cast<uint16_t*>(w13_packed);
+    uint16_t* o3 = static_cast<uint16_t*>(w3_packed);
+    const dim3 g13((unsigned)kmoe::ceil_div(F, 64), (unsigned)kmoe::ceil_div(d, 64), (unsigned)E);
+    const dim3 g3((unsigned)kmoe::ceil_div(d, 64), (unsigned)kmoe::ceil_div(F, 64), (unsigned)E);
+#define KMOE_PACK16(F32_)                                                                                         \
+  do {                                                                                                            \
+    hipLaunchKernelGGL(pack_t16_kernel<F32_>, g13, dim3(256), 0, s, w1, d, F, (int64_t)d * F, 0, true, o13, rows13, \
+                       ld13);                                                                                     \
+    hipLaunchKernelGGL(pack_t16_kernel<F32_>, g13, dim3(256), 0, s, w2, d, F, (int64_t)d * F, 1, true, o13, rows13, \
+                       ld13);                                                                                     \
+    hipLaunchKernelGGL(pack_t16_kernel<F32_>, g3, dim3(256), 0, s, w3, F, d, (int64_t)d * F, 0, false, o3, rows3,  \
+                       ld3);                                                                                      \
+  } while (0)
+    if (f32)
+      KMOE_PACK16(true);
+    else
+      KMOE_PACK16(false);
+#undef KMOE_PACK16
+    hipLaunchKernelGGL(pack_pad_kernel, dim3(2048), dim3(256), 0, s, o13, (int64_t)E * rows13, ld13, d, (int)rows13, F,
+                       true);
+    hipLaunchKernelGGL(pack_pad_kernel, dim3(2048), dim3(256), 0, s, o3, (int64_t)E * rows3, ld3, F, (int)rows3, d,
+                       false);
+    return kmoe::check_launch("kmoe_pack_weights");
+  }
+  // fp8: zero the padding (whole buffers: simple; the fp8 pack runs once per weight version)
   hipLaunchKernelGGL(zero_kernel, dim3(1024), dim3(256), 0, s, static_cast<uint8_t*>(w13_packed),
                      (int64_t)kmoe_packed_w13_bytes(E, d, F, packed_dtype));
   hipLaunchKernelGGL(zero_kernel, dim3(1024), dim3(256), 0, s, static_cast<uint8_t*>(w3_packed),
                      (int64_t)kmoe_packed_w3_bytes(E, d, F, packed_dtype));
-  const bool f32 = w_dtype == KMOE_DTYPE_F32;
   if (fp8) {
     hipLaunchKernelGGL(zero_f32_kernel, dim3(64), dim3(256), 0, s, w13_scale, (int64_t)E * rows13);
     hipLaunchKernelGGL(zero_f32_kernel, dim3(64), dim3(256), 0, s, w3_scale, (int64_t)E * rows3);
@@ -1221,36 +1409,6 @@ extern "C" int kmoe_gemm_gate_up_rows_gu(const void* x, const int32_t* row_index
   return kmoe::check_launch("kmoe_gemm_gate_up_rows_gu");
 }
 
-namespace {
-// Backward packed layouts (rows K-contiguous, WPAD bytes after every row, zero padded):
-//   w3n : (E, round_up(F, 256), d)        row f = w3[e][f][:]            (dh = dY . w3^T, K = d)
-//   w13t: (E, round_up(d, 256), 2*F_pad)  row i = w1[e][i][:], w2[e][i][:] interleaved per 128
-//                                          columns like w13's rows        (dX = [dg|du] . w13, K = 2*F_pad)
-__global__ __launch_bounds__(256) void pack_rows_kernel(const void* __restrict__ w1, const void* __restrict__ w2,
-                                                        const void* __restrict__ w3, bool in_f32, int E, int d,
-                                                        int F, bool w13t, uint16_t* __restrict__ out,
-                                                        int64_t out_rows, int out_ld) {
-  const int e = blockIdx.z;
-  const int64_t row = blockIdx.y;
-  auto ld = [&](const void* p, int64_t off) {
-    return in_f32 ? f32_to_bf16(static_cast<const float*>(p)[off]) : static_cast<const uint16_t*>(p)[off];
-  };
-  for (int c = blockIdx.x * 256 + threadIdx.x; c < out_ld; c += gridDim.x * 256) {
-    uint16_t v = 0;
-    if (w13t) {
-      const int Fp = round_up(F, 128);
-      if (row < d && c < 2 * Fp) {
-        const int half = (c >> 7) & 1, f = (c >> 8) * 128 + (c & 127);
-        if (f < F) v = ld(half ? w2 : w1, ((int64_t)e * d + row) * F + f);
-      }
-    } else if (row < F && c < d) {
-      v = ld(w3, ((int64_t)e * F + row) * d + c);
-    }
-    out[((int64_t)e * out_rows + row) * out_ld + c] = v;
-  }
-}
-}  // namespace
-
 extern "C" size_t kmoe_packed_w3n_bytes(int E, int d, int F) {
   return (size_t)E * (size_t)round_up(F, 256) * ((size_t)d * 2 + WPAD);
 }
@@ -1272,10 +1430,17 @@ extern "C" int kmoe_pack_weights_bwd(const void* w1, const void* w2, const void*
   const int Fp = round_up(F, 128);
   const int64_t r3 = round_up(F, 256), r13 = round_up(d, 256);
   const int ld3 = d + WPAD / 2, ld13 = 2 * Fp + WPAD / 2;
-  hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)kmoe::ceil_div(ld3, 256), (unsigned)r3, (unsigned)E), dim3(256), 0,
-                     s, w1, w2, w3, f32, E, d, F, false, static_cast<uint16_t*>(w3n_packed), r3, ld3);
-  hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)kmoe::ceil_div(ld13, 256), (unsigned)r13, (unsigned)E), dim3(256),
-                     0, s, w1, w2, w3, f32, E, d, F, true, static_cast<uint16_t*>(w13t_packed), r13, ld13);
+  if (f32) {
+    hipLaunchKernelGGL(pack_rows16_kernel<true>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, false,
+                       static_cast<uint16_t*>(w3n_packed), r3, ld3, E);
+    hipLaunchKernelGGL(pack_rows16_kernel<true>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, true,
+                       static_cast<uint16_t*>(w13t_packed), r13, ld13, E);
+  } else {
+    hipLaunchKernelGGL(pack_rows16_kernel<false>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, false,
+                       static_cast<uint16_t*>(w3n_packed), r3, ld3, E);
+    hipLaunchKernelGGL(pack_rows16_kernel<false>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, true,
+                       static_cast<uint16_t*>(w13t_packed), r13, ld13, E);
+  }
   return kmoe::check_launch("kmoe_pack_weights_bwd");
 }
 

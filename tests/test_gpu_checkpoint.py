@@ -94,3 +94,50 @@ def test_packed_fp8_codes_match_oracle(dev, wdtype):
     assert not w13[:, pad_f, :].any()
     assert not pw.s13.cpu().numpy().reshape(E, 2 * Fp)[:, pad_f].any()
     assert not pw.s3.cpu().numpy().reshape(E, -1)[:, d:].any()
+
+
+def _bf16_bits(t):
+    return t.to(torch.bfloat16).view(torch.int16).numpy()
+
+
+@pytest.mark.parametrize("E,d,F,wdtype", [(3, 192, 200, torch.bfloat16), (2, 128, 13, torch.float32),
+                                          (2, 256, 384, torch.float32), (1, 64, 136, torch.bfloat16)])
+def test_bf16_packs_match_host_layout(dev, E, d, F, wdtype):
+    """kmoe_pack_weights (bf16) and kmoe_pack_weights_bwd against the packed layouts built on
+    the host from w1/w2/w3: every element, the zero pads after each row and the zero
+    padding rows (F and d not multiples of the tile sizes; f32 inputs rounded to bf16)."""
+    from kmoe import backward as BW, ops
+
+    g = torch.Generator().manual_seed(21)
+    w1, w2, w3 = (torch.randn(*s, generator=g).to(wdtype) for s in [(E, d, F), (E, d, F), (E, F, d)])
+    print(f"bf16 packs E={E} d={d} F={F} {wdtype}", flush=True)
+    pw = ops.pack_weights(w1.to(dev), w2.to(dev), w3.to(dev))
+    bw = BW.pack_bwd_weights(w1.to(dev), w2.to(dev), w3.to(dev), torch.zeros(128, d, dtype=wdtype, device=dev))
+    torch.cuda.synchronize()
+    Fp = (F + 127) // 128 * 128
+    dp = (d + 255) // 256 * 256
+    b1, b2, b3 = _bf16_bits(w1), _bf16_bits(w2), _bf16_bits(w3)
+    w13 = np.zeros((E, 2 * Fp, d + 64), np.int16)
+    w3p = np.zeros((E, dp, Fp + 64), np.int16)
+    f = np.arange(F)
+    rows = (f // 128) * 256 + f % 128
+    for e in range(E):
+        w13[e, rows, :d] = b1[e].T
+        w13[e, rows + 128, :d] = b2[e].T
+        w3p[e, :d, :F] = b3[e].T
+    assert np.array_equal(pw.w13.cpu().view(torch.int16).numpy().reshape(w13.shape), w13)
+    assert np.array_equal(pw.w3.cpu().view(torch.int16).numpy().reshape(w3p.shape), w3p)
+    F256 = (F + 255) // 256 * 256
+    w3n = np.zeros((E, F256, d + 64), np.int16)
+    w13t = np.zeros((E, dp, 2 * Fp + 64), np.int16)
+    c = np.arange(2 * Fp)
+    src_f = (c >> 8) * 128 + (c & 127)
+    half = (c >> 7) & 1
+    ok = src_f < F
+    for e in range(E):
+        w3n[e, :F, :d] = b3[e]
+        for i in range(d):
+            w13t[e, i, c[ok & (half == 0)]] = b1[e, i, src_f[ok & (half == 0)]]
+            w13t[e, i, c[ok & (half == 1)]] = b2[e, i, src_f[ok & (half == 1)]]
+    assert np.array_equal(bw.w3n.cpu().view(torch.int16).numpy().reshape(w3n.shape), w3n)
+    assert np.array_equal(bw.w13t.cpu().view(torch.int16).numpy().reshape(w13t.shape), w13t)
