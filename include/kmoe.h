@@ -314,10 +314,20 @@ int kmoe_reduce_f32(const float* partial, int64_t n_parts, int64_t n, void* out,
 /* Router logit gradient (f32, (T,E)): the top-k renormalisation's softmax-over-
  * the-selected backward, dl[i_j] += w_j (dw_j - sum_l w_l dw_l), plus the aux
  * losses scaled by *grad_aux (nullable = 0):
- *   dl += g (w_lb E/T p (f - p.f) + w_z 2/T lse p),  f_e = counts[e] / (T k).   */
+ *   dl += g (w_lb E/T p (f - p.f) + w_z 2/T lse p),  f_e = counts[e] / (T k).
+ * k = 0 (topk_idx / topk_w / dw may be NULL): the aux part alone (the expert-choice
+ * layer's z-loss, with counts NULL and w_lb 0).                                   */
 int kmoe_router_dlogits(const float* logits, int64_t T, int E, const int64_t* topk_idx, const float* topk_w,
                         const float* dw, int k, const int32_t* counts, const float* grad_aux, float w_lb, float w_z,
                         float* dlogits, void* stream);
+
+/* Expert-choice logit gradient added to dlogits (f32, (B*S, E)): the backward of
+ * ExpertChoiceRouter.forward's softmax over each sequence's S tokens and per-expert
+ * normalisation w = p / (sum_sel p + 1e-9) (moe.py:513-528), at the selection held by
+ * the combine tables src_row / src_w (B*S, E) of kmoe_ec_select; dw (B*S, E) is the
+ * gradient of each selected slot's weight (kmoe_combine_bwd over those tables).     */
+int kmoe_ec_dlogits(const float* logits, int B, int S, int E, const int32_t* src_row, const float* src_w,
+                    const float* dw, float* dlogits, void* stream);
 
 /* Router MLP backward: da = (dl . w_out) * silu'(a) -> (T, 128) bf16 and
  * dw_out = dl^T silu(a) -> (E, 128) (bf16 or f32), reduced in a fixed order.

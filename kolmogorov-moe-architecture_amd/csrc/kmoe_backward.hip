@@ -157,6 +157,72 @@ __global__ __launch_bounds__(256) void router_dlogits_kernel(const float* __rest
     if (e < E) dl[t * E + e] = g[e];
 }
 
+// Expert-choice logit gradient (ExpertChoiceRouter.forward, moe.py:513-528): per
+// sequence b and expert e, p_s = softmax over the S tokens of logits[b, :, e]; the C
+// selected tokens (src_row[t, e] >= 0) carry w_s = p_s / (P + 1e-9), P = sum_sel p.
+// With g_s = dL/dw_s (dw[t, e]):  dL/dp_s = (g_s - G) / (P + 1e-9) for selected s (0
+// otherwise), G = sum_sel g w;  dl_s += p_s (dL/dp_s - Q),  Q = sum_sel p dL/dp.  One
+// 1024-thread workgroup per (b, e), fixed-order block reductions (bit-reproducible).
+constexpr int ECD_THREADS = 1024;
+__device__ __forceinline__ float ecd_block_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float tot = 0.0f;
+  for (int w = 0; w < ECD_THREADS / 64; ++w) tot += red[w];
+  return tot;
+}
+__device__ __forceinline__ float ecd_block_max(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float m = -INFINITY;
+  for (int w = 0; w < ECD_THREADS / 64; ++w) m = fmaxf(m, red[w]);
+  return m;
+}
+__global__ __launch_bounds__(ECD_THREADS) void ec_dlogits_kernel(const float* __restrict__ logits, int S, int E,
+                                                                 const int32_t* __restrict__ src_row,
+                                                                 const float* __restrict__ src_w,
+                                                                 const float* __restrict__ dw, float* __restrict__ dl) {
+  __shared__ float red[ECD_THREADS / 64];
+  const int b = blockIdx.x / E, e = blockIdx.x % E;
+  const int64_t t0 = (int64_t)b * S;
+  float mx = -INFINITY;
+  for (int s = threadIdx.x; s < S; s += ECD_THREADS) mx = fmaxf(mx, logits[(t0 + s) * E + e]);
+  mx = ecd_block_max(mx, red);
+  float se = 0.0f, pe = 0.0f, gw = 0.0f;
+  for (int s = threadIdx.x; s < S; s += ECD_THREADS) {
+    const int64_t i = (t0 + s) * E + e;
+    const float ex = __expf(logits[i] - mx);
+    se += ex;
+    if (src_row[i] >= 0) {
+      pe += ex;
+      gw += dw[i] * src_w[i];
+    }
+  }
+  se = ecd_block_sum(se, red);
+  pe = ecd_block_sum(pe, red);
+  const float G = ecd_block_sum(gw, red);
+  const float inv = 1.0f / se;
+  const float invZ = 1.0f / (pe * inv + 1e-9f);
+  float q = 0.0f;
+  for (int s = threadIdx.x; s < S; s += ECD_THREADS) {
+    const int64_t i = (t0 + s) * E + e;
+    if (src_row[i] >= 0) q += __expf(logits[i] - mx) * inv * (dw[i] - G) * invZ;
+  }
+  const float Q = ecd_block_sum(q, red);
+  for (int s = threadIdx.x; s < S; s += ECD_THREADS) {
+    const int64_t i = (t0 + s) * E + e;
+    const float p = __expf(logits[i] - mx) * inv;
+    const float dp = src_row[i] >= 0 ? (dw[i] - G) * invZ : 0.0f;
+    dl[i] += p * (dp - Q);
+  }
+}
+
 // Router MLP backward over a block of 64 tokens (256 threads, 4 per token):
 //   s = silu(a), ds = dl w_out, da = ds * silu'(a)      -> da (T, 128) bf16
 //   partial[b][e][j] = sum_{t in block} dl[t,e] s[t,j]  -> reduced by router_reduce_kernel
@@ -283,8 +349,9 @@ extern "C" int kmoe_swiglu_bwd(const void* dh, const void* gu, int64_t rows, con
 extern "C" int kmoe_router_dlogits(const float* logits, int64_t T, int E, const int64_t* topk_idx, const float* topk_w,
                                    const float* dw, int k, const int32_t* counts, const float* grad_aux, float w_lb,
                                    float w_z, float* dlogits, void* stream) {
-  KMOE_REQUIRE(logits && topk_idx && topk_w && dw && dlogits, KMOE_ERR_NULL, "kmoe_router_dlogits: null buffer");
-  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS && k >= 1 && k <= E, KMOE_ERR_SHAPE, "kmoe_router_dlogits: E=%d k=%d",
+  KMOE_REQUIRE(logits && dlogits && (k == 0 || (topk_idx && topk_w && dw)), KMOE_ERR_NULL,
+               "kmoe_router_dlogits: null buffer");
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS && k >= 0 && k <= E, KMOE_ERR_SHAPE, "kmoe_router_dlogits: E=%d k=%d",
                E, k);
   if (T == 0) return KMOE_OK;
   const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(T, 256));
@@ -302,6 +369,16 @@ extern "C" int kmoe_router_dlogits(const float* logits, int64_t T, int E, const 
     KMOE_DL(64);
 #undef KMOE_DL
   return kmoe::check_launch("kmoe_router_dlogits");
+}
+
+extern "C" int kmoe_ec_dlogits(const float* logits, int B, int S, int E, const int32_t* src_row, const float* src_w,
+                               const float* dw, float* dlogits, void* stream) {
+  KMOE_REQUIRE(logits && src_row && src_w && dw && dlogits, KMOE_ERR_NULL, "kmoe_ec_dlogits: null buffer");
+  KMOE_REQUIRE(B >= 1 && S >= 1 && E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_ec_dlogits: B=%d S=%d E=%d",
+               B, S, E);
+  hipLaunchKernelGGL(ec_dlogits_kernel, dim3((unsigned)(B * E)), dim3(ECD_THREADS), 0, kmoe::as_stream(stream), logits,
+                     S, E, src_row, src_w, dw, dlogits);
+  return kmoe::check_launch("kmoe_ec_dlogits");
 }
 
 extern "C" size_t kmoe_router_bwd_workspace_bytes(int64_t T, int E) {

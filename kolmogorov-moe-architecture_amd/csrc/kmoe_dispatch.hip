@@ -235,7 +235,9 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(const uint16_t* __res
 #pragma unroll
       for (int i = 0; i < ROW_REGS; ++i) {
         const int v = v0 + lane + 64 * i;
-        if (v < nvec) dst[v] = r[i];
+        // non-temporal: the permuted rows are read back only by the backward's weight
+        // gradient, long after this; x itself stays cached for the gate/up GEMM
+        if (v < nvec) __builtin_nontemporal_store(r[i], dst + v);
       }
     }
   }

@@ -1001,27 +1001,22 @@ __global__ __launch_bounds__(256) void pack_t16_kernel(const void* __restrict__ 
 }
 
 // Zeroes what pack_t16_kernel leaves: in every packed row the elements [valid_cols,
-// out_ld), and the whole rows that no input column maps to (is_pad_row), 8 bytes at
-// a time (row strides are multiples of 8 bytes).
+// out_ld), and the whole rows that no input column maps to.  One thread per row; the
+// pad of a row that holds data starts at an 8-byte boundary (valid_cols % 4 == 0) or
+// is first finished element by element.
 __global__ __launch_bounds__(256) void pack_pad_kernel(uint16_t* __restrict__ out, int64_t n_rows, int out_ld,
                                                        int valid_cols, int rows_per_expert, int valid_in_cols,
                                                        bool gate_up) {
-  const int words = out_ld / 4;  // 8-byte words per row
-  const int64_t n = n_rows * words;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t row = i / words;
-    const int w = (int)(i - row * words);
-    const int pr = (int)(row % rows_per_expert);
-    // the input column this packed row holds (gate_up: w1 / w2 column f of block f/128)
-    const int c = gate_up ? (pr / 256) * 128 + (pr % 128) : pr;
-    const bool pad_row = c >= valid_in_cols;
-    if (pad_row || 4 * w >= valid_cols) {
-      reinterpret_cast<uint64_t*>(out + row * out_ld)[w] = 0ull;
-    } else if (4 * w + 4 > valid_cols) {
-      // the word that straddles the end of the valid columns: its tail only
-      for (int q = valid_cols - 4 * w; q < 4; ++q) out[row * out_ld + 4 * w + q] = 0;
-    }
-  }
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= n_rows) return;
+  const int pr = (int)(row % rows_per_expert);
+  // the input column this packed row holds (gate_up: w1 / w2 column f of block f/128)
+  const int c = gate_up ? (pr / 256) * 128 + (pr % 128) : pr;
+  uint16_t* p = out + row * out_ld;
+  int from = c >= valid_in_cols ? 0 : valid_cols;
+  for (; (from & 3) != 0 && from < out_ld; ++from) p[from] = 0;
+  uint64_t* w = reinterpret_cast<uint64_t*>(p);
+  for (int i = from / 4; i < out_ld / 4; ++i) w[i] = 0ull;
 }
 
 // Backward packed layouts (rows K-contiguous, WPAD bytes after every row, zero padded):
@@ -1236,10 +1231,10 @@ extern "C" int kmoe_pack_weights(const void* w1, const void* w2, const void* w3,
     else
       KMOE_PACK16(false);
 #undef KMOE_PACK16
-    hipLaunchKernelGGL(pack_pad_kernel, dim3(2048), dim3(256), 0, s, o13, (int64_t)E * rows13, ld13, d, (int)rows13, F,
-                       true);
-    hipLaunchKernelGGL(pack_pad_kernel, dim3(2048), dim3(256), 0, s, o3, (int64_t)E * rows3, ld3, F, (int)rows3, d,
-                       false);
+    hipLaunchKernelGGL(pack_pad_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(E * rows13, 256)), dim3(256), 0, s, o13,
+                       (int64_t)E * rows13, ld13, d, (int)rows13, F, true);
+    hipLaunchKernelGGL(pack_pad_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(E * rows3, 256)), dim3(256), 0, s, o3,
+                       (int64_t)E * rows3, ld3, F, (int)rows3, d, false);
     return kmoe::check_launch("kmoe_pack_weights");
   }
   // fp8: zero the padding (whole buffers: simple; the fp8 pack runs once per weight version)

@@ -76,6 +76,7 @@ _SIGNATURES = {
     "kmoe_gemm_wgrad_rows": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _i64, _i32,
                                     _vp]),
     "kmoe_router_dlogits": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _vp, _vp]),
+    "kmoe_ec_dlogits": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_router_bwd_workspace_bytes": (_sz, [_i64, _i32]),
     "kmoe_router_mlp_bwd": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
     "kmoe_packed_w_in_t_bytes": (_sz, [_i32]),

@@ -40,21 +40,29 @@ class BwdWeights(NamedTuple):
 
 
 def pack_bwd_weights(w1, w2, w3, w_in) -> BwdWeights:
-    E, d, F = w1.shape
-    dt = w1.dtype
-    if dt not in (torch.float32, _BF16):
-        raise ValueError(f"kmoe backward: unsupported weight dtype {dt}")
-    w1, w2, w3 = (w.detach().contiguous() for w in (w1, w2, w3))
-    w_in = w_in.detach().to(dt).contiguous()
+    """Backward packed layouts of the expert weights (w1/w2/w3, any of them None: skipped
+    together) and of the router's w_in (None: skipped)."""
     lib = _lib.load()
-    wdt = _lib.DTYPE_F32 if dt == torch.float32 else _lib.DTYPE_BF16
-    dev = w1.device
-    w3n = torch.empty(lib.kmoe_packed_w3n_bytes(E, d, F), device=dev, dtype=torch.uint8)
-    w13t = torch.empty(lib.kmoe_packed_w13t_bytes(E, d, F), device=dev, dtype=torch.uint8)
-    wit = torch.empty(lib.kmoe_packed_w_in_t_bytes(d), device=dev, dtype=torch.uint8)
-    s = ops._stream(w1)
-    _lib.call("kmoe_pack_weights_bwd", ptr(w1), ptr(w2), ptr(w3), wdt, E, d, F, ptr(w3n), ptr(w13t), s)
-    _lib.call("kmoe_pack_w_in_t", ptr(w_in), wdt, d, ptr(wit), s)
+    w3n = w13t = wit = None
+    if w1 is not None:
+        E, d, F = w1.shape
+        dt = w1.dtype
+        if dt not in (torch.float32, _BF16):
+            raise ValueError(f"kmoe backward: unsupported weight dtype {dt}")
+        w1, w2, w3 = (w.detach().contiguous() for w in (w1, w2, w3))
+        wdt = _lib.DTYPE_F32 if dt == torch.float32 else _lib.DTYPE_BF16
+        dev = w1.device
+        w3n = torch.empty(lib.kmoe_packed_w3n_bytes(E, d, F), device=dev, dtype=torch.uint8)
+        w13t = torch.empty(lib.kmoe_packed_w13t_bytes(E, d, F), device=dev, dtype=torch.uint8)
+        _lib.call("kmoe_pack_weights_bwd", ptr(w1), ptr(w2), ptr(w3), wdt, E, d, F, ptr(w3n), ptr(w13t),
+                  ops._stream(w1))
+    if w_in is not None:
+        dt = w_in.dtype if w_in.dtype in (torch.float32, _BF16) else torch.float32
+        w_in = w_in.detach().to(dt).contiguous()
+        d = w_in.shape[1]
+        wdt = _lib.DTYPE_F32 if dt == torch.float32 else _lib.DTYPE_BF16
+        wit = torch.empty(lib.kmoe_packed_w_in_t_bytes(d), device=w_in.device, dtype=torch.uint8)
+        _lib.call("kmoe_pack_w_in_t", ptr(w_in), wdt, d, ptr(wit), ops._stream(w_in))
     return BwdWeights(w3n, w13t, wit)
 
 
@@ -109,84 +117,222 @@ def _index_tensors(T: int, k: int, dev):
     return hit
 
 
-def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], w_out: torch.Tensor,
-                 bw: BwdWeights, E: int, F: int, w_lb: float, w_z: float, need_weights: bool = True) -> Grads:
-    """All gradients of one token-choice MoE layer forward (bf16 compute)."""
-    lib = _lib.load()
-    x2d = sv.x2d
-    T, d = x2d.shape
-    k = sv.idx.shape[1]
-    A = T * k
+def _experts_core(dy, yperm, gu, slot_row, slot_w, kk, offsets, A, bw: BwdWeights, E, F, extra_rows=0):
+    """Expert-path backward shared by every layer form: from dy (T, d) through the combine
+    (routing-weight gradients dw (T, kk), dyperm), the down GEMM (dh), the SwiGLU and the
+    gate/up GEMM (dgu, dxp rows [0, A)).  dxp has `extra_rows` more rows after the A
+    expert rows for the caller (the router's dx contribution).  Returns
+    (dxp, dw, dyperm, dgu)."""
+    T, d = dy.shape
     Fp = _ru(F, 128)
-    dev = x2d.device
-    s = ops._stream(x2d)
-    disp = sv.disp
-    dy = dy.reshape(T, d).to(_BF16).contiguous()
-    one_seg, segs, nseg, ones, extra = _index_tensors(T, k, dev)
-
-    # ---- combine backward: dyperm, dw
+    dev = dy.device
+    s = ops._stream(dy)
     dyperm = torch.empty(max(A, 1), d, device=dev, dtype=_BF16)
-    dw = torch.empty(T, k, device=dev, dtype=torch.float32)
+    dw = torch.empty(T, kk, device=dev, dtype=torch.float32)
     with _stage("bwd_combine"):
-        _lib.call("kmoe_combine_bwd", ptr(dy), ptr(sv.yperm), ptr(disp.slot_row), ptr(disp.slot_w), k, d, T,
-                  ptr(dyperm), ptr(dw), s)
-    # ---- dh = dyperm . w3^T (fused nothing: plain grouped GEMM), SwiGLU backward
+        _lib.call("kmoe_combine_bwd", ptr(dy), ptr(yperm), ptr(slot_row), ptr(slot_w), kk, d, T, ptr(dyperm), ptr(dw),
+                  s)
     dh = torch.empty(max(A, 1), Fp, device=dev, dtype=_BF16)
     with _stage("bwd_gemm_dh"):
-        _lib.call("kmoe_gemm_grouped", ptr(dyperm), ptr(disp.offsets), E, d, A, ptr(bw.w3n), _ru(F, 256), Fp,
+        _lib.call("kmoe_gemm_grouped", ptr(dyperm), ptr(offsets), E, d, A, ptr(bw.w3n), _ru(F, 256), Fp,
                   ptr(dh), Fp, Fp, s)
     dgu = torch.empty(max(A, 1), 2 * Fp, device=dev, dtype=_BF16)
     with _stage("bwd_swiglu"):
-        _lib.call("kmoe_swiglu_bwd", ptr(dh), ptr(sv.gu), A, ptr(disp.offsets[E:]), F, ptr(dgu), s)
-    # ---- dxperm = dgu . [w1|w2]^T (rows [0, A)); the router's dx contribution goes to
-    # rows [A, A + T) and one unit-weight gather sums both per token
-    dxp = torch.empty(A + T, d, device=dev, dtype=_BF16)
+        _lib.call("kmoe_swiglu_bwd", ptr(dh), ptr(gu), A, ptr(offsets[E:]), F, ptr(dgu), s)
+    dxp = torch.empty(A + extra_rows, d, device=dev, dtype=_BF16)
     with _stage("bwd_gemm_dx"):
-        _lib.call("kmoe_gemm_grouped", ptr(dgu), ptr(disp.offsets), E, 2 * Fp, A, ptr(bw.w13t), _ru(d, 256), d,
+        _lib.call("kmoe_gemm_grouped", ptr(dgu), ptr(offsets), E, 2 * Fp, A, ptr(bw.w13t), _ru(d, 256), d,
                   ptr(dxp), d, d, s)
+    return dxp, dw, dyperm, dgu
 
-    # ---- router: logit gradient, MLP backward, dx contribution, dW_in
-    dl = torch.empty(T, E, device=dev, dtype=torch.float32)
-    ga = None if grad_aux is None else grad_aux.reshape(1).to(torch.float32).contiguous()
+
+def _expert_weight_grads(h, dyperm, xperm, dgu, offsets, A, E, d, F):
+    """dW3 = h^T dyperm and dW1 | dW2 = xperm^T dgu per expert, straight from the row
+    buffers (transpose reads in LDS)."""
+    Fp = _ru(F, 128)
+    dev = h.device
+    s = ops._stream(h)
+    dpad = _ru(d, 256)
+    dw3 = torch.empty(E, F, d, device=dev, dtype=_BF16)
+    with _stage("bwd_wgrad_w3"):
+        _lib.call("kmoe_gemm_wgrad_rows", ptr(h), Fp, ptr(dyperm), d, A, ptr(offsets), E, F, dpad, ptr(dw3),
+                  None, _lib.DTYPE_BF16, d, d, s)
+    dw1 = torch.empty(E, d, F, device=dev, dtype=_BF16)
+    dw2 = torch.empty(E, d, F, device=dev, dtype=_BF16)
+    with _stage("bwd_wgrad_w13"):
+        _lib.call("kmoe_gemm_wgrad_rows", ptr(xperm), d, ptr(dgu), 2 * Fp, A, ptr(offsets), E, d, 2 * Fp,
+                  ptr(dw1), ptr(dw2), _lib.DTYPE_BF16, F, F, s)
+    return dw1, dw2, dw3
+
+
+def _router_core(x2d, hidden, w_out, bw: BwdWeights, dl, dx_rows, need_weights):
+    """Router MLP backward from the logit gradient dl (T, E): da and dW_out
+    (kmoe_router_mlp_bwd), the dx contribution da . w_in written to dx_rows (T, d) bf16,
+    and dW_in = da^T x (split-K over token segments, reduced in order).  Returns
+    (dw_in or None, dw_out)."""
+    lib = _lib.load()
+    T, d = x2d.shape
+    E = dl.shape[1]
+    dev = x2d.device
+    s = ops._stream(x2d)
+    one_seg, segs, nseg, _, _ = _index_tensors(T, 1, dev)
     with _stage("bwd_router"):
-        _lib.call("kmoe_router_dlogits", ptr(sv.logits), T, E, ptr(sv.idx), ptr(sv.w), ptr(dw), k,
-                  ptr(disp.counts), ptr(ga), float(w_lb), float(w_z), ptr(dl), s)
         da = torch.empty(T, _lib.ROUTER_HIDDEN, device=dev, dtype=_BF16)
         wdt = w_out.dtype
         dw_out = torch.empty(E, _lib.ROUTER_HIDDEN, device=dev, dtype=wdt)
         wsb = lib.kmoe_router_bwd_workspace_bytes(T, E)
         ws = torch.empty(max(wsb, 4), device=dev, dtype=torch.uint8)
         w_out_b = w_out.detach().to(_BF16).contiguous()
-        _lib.call("kmoe_router_mlp_bwd", ptr(dl), ptr(sv.hidden), T, E, ptr(w_out_b), ptr(da), ptr(dw_out),
+        _lib.call("kmoe_router_mlp_bwd", ptr(dl), ptr(hidden), T, E, ptr(w_out_b), ptr(da), ptr(dw_out),
                   _lib.DTYPE_F32 if wdt == torch.float32 else _lib.DTYPE_BF16, ptr(ws), wsb, s)
         _lib.call("kmoe_gemm_grouped", ptr(da), ptr(one_seg), 1, _lib.ROUTER_HIDDEN, T, ptr(bw.w_in_t), _ru(d, 256),
-                  d, ptr(dxp[A:]), d, d, s)
-    src = torch.cat([disp.slot_row.view(T, k), extra], 1)
-    dx = torch.empty(T, d, device=dev, dtype=_BF16)
-    with _stage("bwd_gather_dx"):
-        _lib.call("kmoe_combine", ptr(dxp), d, ptr(src), ptr(ones), k + 1, None, None, T, ptr(dx), _lib.DTYPE_BF16, s)
+                  d, ptr(dx_rows), d, d, s)
     if not need_weights:
-        return Grads(dx, None, dw_out, None, None, None)
-
-    # ---- weight gradients, straight from the row-major buffers (transpose reads in LDS)
-    dpad = _ru(d, 256)
+        return None, dw_out
     # dW_in = da^T x: a 128 x d output (few tiles) over K = T, split into token
     # segments of WG_SPLIT rows whose fp32 partial sums are then reduced in order
     dw_in = torch.empty(_lib.ROUTER_HIDDEN, d, device=dev, dtype=_BF16)
     with _stage("bwd_wgrad_router"):
         part = torch.empty(nseg, _lib.ROUTER_HIDDEN, d, device=dev, dtype=torch.float32)
         _lib.call("kmoe_gemm_wgrad_rows", ptr(da), _lib.ROUTER_HIDDEN, ptr(x2d), d, T, ptr(segs), nseg,
-                  _lib.ROUTER_HIDDEN, dpad, ptr(part), None, _lib.DTYPE_F32, d, d, s)
+                  _lib.ROUTER_HIDDEN, _ru(d, 256), ptr(part), None, _lib.DTYPE_F32, d, d, s)
         _lib.call("kmoe_reduce_f32", ptr(part), nseg, _lib.ROUTER_HIDDEN * d, ptr(dw_in), _lib.DTYPE_BF16, s)
-    del part
-    # expert weight gradients straight from the row buffers (transpose reads in LDS)
-    dw3 = torch.empty(E, F, d, device=dev, dtype=_BF16)
-    with _stage("bwd_wgrad_w3"):
-        _lib.call("kmoe_gemm_wgrad_rows", ptr(sv.h), Fp, ptr(dyperm), d, A, ptr(disp.offsets), E, F, dpad, ptr(dw3),
-                  None, _lib.DTYPE_BF16, d, d, s)
-    dw1 = torch.empty(E, d, F, device=dev, dtype=_BF16)
-    dw2 = torch.empty(E, d, F, device=dev, dtype=_BF16)
-    with _stage("bwd_wgrad_w13"):
-        _lib.call("kmoe_gemm_wgrad_rows", ptr(sv.xperm), d, ptr(dgu), 2 * Fp, A, ptr(disp.offsets), E, d, 2 * Fp,
-                  ptr(dw1), ptr(dw2), _lib.DTYPE_BF16, F, F, s)
+    return dw_in, dw_out
+
+
+def _gather_dx(dxp, src, T, d, residual=None):
+    """dx[t] = (residual[t] +) sum of the token's rows src[t, :] of dxp (unit weights,
+    f32 in a fixed order, one bf16 rounding); rows -1 contribute nothing."""
+    fan = src.shape[1]
+    ones = _ones(T, fan, dxp.device)
+    dx = torch.empty(T, d, device=dxp.device, dtype=_BF16)
+    with _stage("bwd_gather_dx"):
+        if residual is None:
+            _lib.call("kmoe_combine", ptr(dxp), d, ptr(src), ptr(ones), fan, None, None, T, ptr(dx), _lib.DTYPE_BF16,
+                      ops._stream(dxp))
+        else:
+            _lib.call("kmoe_combine_residual", ptr(dxp), d, ptr(src), ptr(ones), fan, None, None, ptr(residual), T,
+                      ptr(dx), _lib.DTYPE_BF16, ops._stream(dxp))
+    return dx
+
+
+_ONES: dict = {}
+
+
+def _ones(T, fan, dev):
+    key = (T, fan, str(dev))
+    t = _ONES.get(key)
+    if t is None:
+        if len(_ONES) > 16:
+            _ONES.clear()
+        t = _ONES[key] = torch.ones(T, fan, device=dev, dtype=torch.float32)
+    return t
+
+
+def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], w_out: torch.Tensor,
+                 bw: BwdWeights, E: int, F: int, w_lb: float, w_z: float, need_weights: bool = True) -> Grads:
+    """All gradients of one token-choice MoE layer forward (bf16 compute)."""
+    x2d = sv.x2d
+    T, d = x2d.shape
+    k = sv.idx.shape[1]
+    A = T * k
+    dev = x2d.device
+    s = ops._stream(x2d)
+    disp = sv.disp
+    dy = dy.reshape(T, d).to(_BF16).contiguous()
+    _, _, _, _, extra = _index_tensors(T, k, dev)
+    # expert path; the router's dx contribution goes to rows [A, A + T) of dxp and one
+    # unit-weight gather sums both per token
+    dxp, dw, dyperm, dgu = _experts_core(dy, sv.yperm, sv.gu, disp.slot_row, disp.slot_w, k, disp.offsets, A, bw,
+                                         E, F, extra_rows=T)
+    # router: logit gradient (top-k renormalisation + aux), MLP backward, dx rows, dW_in
+    dl = torch.empty(T, E, device=dev, dtype=torch.float32)
+    ga = None if grad_aux is None else grad_aux.reshape(1).to(torch.float32).contiguous()
+    with _stage("bwd_router"):
+        _lib.call("kmoe_router_dlogits", ptr(sv.logits), T, E, ptr(sv.idx), ptr(sv.w), ptr(dw), k,
+                  ptr(disp.counts), ptr(ga), float(w_lb), float(w_z), ptr(dl), s)
+    dw_in, dw_out = _router_core(x2d, sv.hidden, w_out, bw, dl, dxp[A:], need_weights)
+    src = torch.cat([disp.slot_row.view(T, k), extra], 1)
+    dx = _gather_dx(dxp, src, T, d)
+    if not need_weights:
+        return Grads(dx, None, dw_out, None, None, None)
+    dw1, dw2, dw3 = _expert_weight_grads(sv.h, dyperm, sv.xperm, dgu, disp.offsets, A, E, d, F)
     return Grads(dx, dw_in, dw_out, dw1, dw2, dw3)
+
+
+class SavedEC(NamedTuple):
+    """What the expert-choice training forward keeps for the backward."""
+    x2d: torch.Tensor        # (B*S, d) bf16 layer input
+    logits: torch.Tensor     # (B*S, E) f32
+    hidden: torch.Tensor     # (B*S, 128) f32 router pre-activation
+    sel: "ops.ECSelectOut"   # selection and combine tables (src_row / src_w (B*S, E))
+    h: torch.Tensor          # (A, F_pad) bf16, A = E*B*C
+    gu: torch.Tensor         # (A, 2 F_pad) bf16
+    yperm: torch.Tensor      # (A, d) bf16
+    xperm: torch.Tensor      # (A, d) bf16 gathered rows
+    B: int
+    S: int
+
+
+def ec_backward(sv: SavedEC, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], w_out: torch.Tensor,
+                bw: BwdWeights, E: int, F: int, w_z: float, need_weights: bool = True) -> Grads:
+    """All gradients of one expert-choice MoE layer forward (moe.py:494-530, 588-673,
+    132-158 and the z-loss of moe.py:833-836)."""
+    x2d = sv.x2d
+    T, d = x2d.shape
+    sel = sv.sel
+    A = sv.h.shape[0]
+    dev = x2d.device
+    s = ops._stream(x2d)
+    dy = dy.reshape(T, d).to(_BF16).contiguous()
+    dxp, dw, dyperm, dgu = _experts_core(dy, sv.yperm, sv.gu, sel.src_row, sel.src_w, E, sel.offsets, A, bw, E, F,
+                                         extra_rows=T)
+    dl = torch.empty(T, E, device=dev, dtype=torch.float32)
+    ga = None if grad_aux is None else grad_aux.reshape(1).to(torch.float32).contiguous()
+    with _stage("bwd_router"):
+        # the z-loss part (zero without an aux gradient), then the selection's part
+        _lib.call("kmoe_router_dlogits", ptr(sv.logits), T, E, None, None, None, 0, None, ptr(ga), 0.0, float(w_z),
+                  ptr(dl), s)
+        _lib.call("kmoe_ec_dlogits", ptr(sv.logits), sv.B, sv.S, E, ptr(sel.src_row), ptr(sel.src_w), ptr(dw),
+                  ptr(dl), s)
+    dw_in, dw_out = _router_core(x2d, sv.hidden, w_out, bw, dl, dxp[A:], need_weights)
+    # dx: the token's expert rows (fan up to E) plus its router row, summed once
+    dx = _gather_dx(dxp, sel.src_row, T, d, residual=dxp[A:])
+    if not need_weights:
+        return Grads(dx, None, dw_out, None, None, None)
+    dw1, dw2, dw3 = _expert_weight_grads(sv.h, dyperm, sv.xperm, dgu, sel.offsets, A, E, d, F)
+    return Grads(dx, dw_in, dw_out, dw1, dw2, dw3)
+
+
+def experts_backward(dy, yperm, gu, h, xperm, slot_row, slot_w, offsets, A, bw: BwdWeights, E, F,
+                     need_weights=True):
+    """Backward of the experts alone (GroupedExperts / GroupedExpertsExpertChoice called
+    directly, moe.py:213-294 / 626-673): returns (dx (T, d), dw (T, kk) gradient of each
+    slot's routing weight, dw1, dw2, dw3)."""
+    T, d = dy.shape
+    kk = slot_row.shape[1]
+    dxp, dw, dyperm, dgu = _experts_core(dy, yperm, gu, slot_row, slot_w, kk, offsets, A, bw, E, F)
+    dx = _gather_dx(dxp, slot_row, T, d)
+    if not need_weights:
+        return dx, dw, None, None, None
+    dw1, dw2, dw3 = _expert_weight_grads(h, dyperm, xperm, dgu, offsets, A, E, d, F)
+    return dx, dw, dw1, dw2, dw3
+
+
+def router_backward(x2d, logits, idx, w, hidden, dw, dlogits_in, w_out, bw: BwdWeights, need_weights=True):
+    """Backward of Router.forward alone (moe.py:423-462): from the gradients of its top-k
+    weights dw (T, k) and of its logits (T, E, nullable) to (dx, dw_in, dw_out)."""
+    T, d = x2d.shape
+    E = logits.shape[1]
+    k = idx.shape[1]
+    dev = x2d.device
+    s = ops._stream(x2d)
+    dl = torch.empty(T, E, device=dev, dtype=torch.float32)
+    with _stage("bwd_router"):
+        _lib.call("kmoe_router_dlogits", ptr(logits), T, E, ptr(idx), ptr(w), ptr(dw), k, None, None, 0.0, 0.0,
+                  ptr(dl), s)
+    if dlogits_in is not None:
+        dl += dlogits_in.reshape(T, E).to(torch.float32)
+    dx = torch.empty(T, d, device=dev, dtype=_BF16)
+    dw_in, dw_out = _router_core(x2d, hidden, w_out, bw, dl, dx, need_weights)
+    return dx, dw_in, dw_out

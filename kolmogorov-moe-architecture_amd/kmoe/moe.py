@@ -11,10 +11,12 @@ return contracts as moe_arch/model/moe.py:
 Numerics: the router accumulates in fp32 and ranks experts by fp32 logit
 (equal logits -> lowest expert index); expert GEMMs run bf16 (or fp8 e4m3)
 MFMA with fp32 accumulation; the combine accumulates in fp32 in a fixed order.
-Backward: the token-choice bf16 layer (MoELayer with top-k routing, optional
-capacity drop) trains through the HIP backward kernels (kmoe.backward); the
-other paths (expert choice, fp8, balanced routing, MoD, GroupedExperts called
-directly) are forward-only and raise in backward.
+Backward (bf16 weights and activations) runs on the HIP backward kernels
+(kmoe.backward) for: the token-choice MoELayer (top-k routing, optional capacity
+drop), the expert-choice MoELayer, and Router / ExpertChoiceRouter /
+GroupedExperts / GroupedExpertsExpertChoice called on their own (the reference's
+distillation code trains them so, distill.py:289-314).  fp8 experts and balanced
+routing are forward-only and raise in backward.
 """
 from __future__ import annotations
 
@@ -68,6 +70,19 @@ class _RouterMLP(nn.Module):
             nn.Linear(ROUTER_HIDDEN, n_experts, bias=False),
         )
         self._bf16_cache = None
+        self._bwd_cache = None
+
+    def _bwd_weights(self):
+        """Backward packed w_in (rebuilt only when it changed)."""
+        w_in = self.router[0].weight
+        key = (w_in.data_ptr(), w_in._version)
+        if self._bwd_cache is None or self._bwd_cache[0] != key:
+            with torch.no_grad():
+                self._bwd_cache = (key, _bwd.pack_bwd_weights(None, None, None, w_in))
+        return self._bwd_cache[1]
+
+    def _trainable(self, x) -> bool:
+        return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
 
     def _kernel_weights(self):
         w_in, w_out = self.router[0].weight, self.router[2].weight
@@ -94,7 +109,7 @@ class Router(_RouterMLP):
         self.logit_bias = None if bias is None else torch.tensor(list(bias), dtype=torch.float32)
 
     def route(self, x2d: torch.Tensor, row_index: Optional[torch.Tensor] = None,
-              T: Optional[int] = None, save_hidden: bool = False) -> ops.RouterOut:
+              T: Optional[int] = None, save_hidden: bool = False, hist: bool = True) -> ops.RouterOut:
         """Kernel-level routing of flattened tokens: fp32 logits, int64 idx, f32 weights.
         With moe_balanced_routing the picks are the capacity-balanced assignment
         (moe.py:443-451) over all the tokens of the call."""
@@ -110,14 +125,24 @@ class Router(_RouterMLP):
             r = ops.router(x2d, w_in, w_out, 0, bias=bias, row_index=row_index, T=T)
             idx, w = ops.balanced_topk(r.logits, self.top_k)
             return ops.RouterOut(r.logits, idx, w, r.partials)
-        return ops.router(x2d, w_in, w_out, self.top_k, bias=bias, row_index=row_index, T=T, save_hidden=save_hidden)
+        return ops.router(x2d, w_in, w_out, self.top_k, bias=bias, row_index=row_index, T=T, save_hidden=save_hidden,
+                          hist=hist)
 
     def forward(self, hidden_states: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         B, S, d = hidden_states.shape
-        r = self.route(hidden_states.reshape(B * S, d))
         dt = hidden_states.dtype
-        return (r.w.view(B, S, self.top_k).to(dt), r.idx.view(B, S, self.top_k),
-                r.logits.view(B, S, self.n_experts).to(dt))
+        if self._trainable(hidden_states) and not self.balanced_routing:
+            w, idx, logits = _RouterFn.apply(hidden_states.reshape(B * S, d), self.router[0].weight,
+                                             self.router[2].weight, self)
+            return (w.view(B, S, self.top_k).to(dt), idx.view(B, S, self.top_k),
+                    logits.view(B, S, self.n_experts).to(dt))
+        r = self.route(hidden_states.reshape(B * S, d), hist=False)
+        out = (r.w.view(B, S, self.top_k).to(dt), r.idx.view(B, S, self.top_k),
+               r.logits.view(B, S, self.n_experts).to(dt))
+        if torch.is_grad_enabled() and self.balanced_routing:
+            return (_forward_only(out[0], hidden_states, *self.parameters()), out[1],
+                    _forward_only(out[2], hidden_states, *self.parameters()))
+        return out
 
 
 class ExpertChoiceRouter(_RouterMLP):
@@ -132,18 +157,22 @@ class ExpertChoiceRouter(_RouterMLP):
     def capacity(self, seq_len: int) -> int:
         return int(math.ceil(seq_len * self.capacity_factor / self.n_experts))  # moe.py:511
 
-    def route(self, hidden_states: torch.Tensor, descending: bool = True):
+    def route(self, hidden_states: torch.Tensor, descending: bool = True, save_hidden: bool = False):
         B, S, d = hidden_states.shape
         C = min(self.capacity(S), S)
         w_in, w_out = self._kernel_weights()
-        r = ops.router(hidden_states.reshape(B * S, d), w_in, w_out, 0)
+        r = ops.router(hidden_states.reshape(B * S, d), w_in, w_out, 0, save_hidden=save_hidden)
         sel = ops.ec_select(r.logits, B, S, self.n_experts, C, descending=descending)
         return r, sel, C
 
     def forward(self, hidden_states: torch.Tensor):
         B, S, _ = hidden_states.shape
-        r, sel, C = self.route(hidden_states)
         dt = hidden_states.dtype
+        if self._trainable(hidden_states):
+            C = min(self.capacity(S), S)
+            w, idx, logits = _ECRouterFn.apply(hidden_states, self.router[0].weight, self.router[2].weight, self)
+            return w.to(dt), idx, logits.to(dt), C
+        r, sel, C = self.route(hidden_states)
         return sel.w.to(dt), sel.idx, r.logits.view(B, S, self.n_experts).to(dt), C
 
 
@@ -174,6 +203,24 @@ class _PackedExperts(nn.Module):
         if (pw.E, pw.d, pw.F, pw.fp8) != (self.n_experts, self.d_model, self.d_ff, self.use_fp8):
             raise ValueError("kmoe: packed weights do not match the experts' shapes / fp8 mode")
         self._packed = (self._packed_key(), pw)
+
+    def bwd_packed(self) -> _bwd.BwdWeights:
+        """Backward packed weights (no router part), rebuilt only when a parameter changed."""
+        key = tuple((w.data_ptr(), w._version) for w in (self.w1, self.w2, self.w3))
+        cache = getattr(self, "_bwd_cache", None)
+        if cache is None or cache[0] != key:
+            with torch.no_grad():
+                cache = (key, _bwd.pack_bwd_weights(self.w1, self.w2, self.w3, None))
+            self._bwd_cache = cache
+        return cache[1]
+
+    def _trainable(self, *inputs) -> bool:
+        """Whether a direct call records a backward through the HIP kernels."""
+        if not torch.is_grad_enabled():
+            return False
+        if not any(isinstance(t, torch.Tensor) and t.requires_grad for t in inputs + tuple(self.parameters())):
+            return False
+        return not (self.use_fp8 or self.d_ff % 8)
 
     def packed(self) -> ops.PackedWeights:
         """Packed weights, rebuilt only when a parameter changed (version counters)."""
@@ -214,6 +261,8 @@ class GroupedExperts(_PackedExperts):
         return y, disp
 
     def forward(self, x: torch.Tensor, expert_indices: torch.Tensor, expert_weights: torch.Tensor) -> torch.Tensor:
+        if self._trainable(x, expert_weights):
+            return _ExpertsFn.apply(x, expert_weights, self.w1, self.w2, self.w3, self, expert_indices)
         out_dtype = torch.float32 if x.dtype == torch.float32 else torch.bfloat16
         y, _ = self.run(x, expert_indices, expert_weights, out_dtype=out_dtype)
         return _forward_only(y.to(x.dtype), x, self.w1, self.w2, self.w3, expert_weights)
@@ -230,10 +279,20 @@ class GroupedExpertsExpertChoice(_PackedExperts):
         return ops.combine(yperm, sel.src_row, sel.src_w, B * S, out_dtype=out_dtype)
 
     def forward(self, x: torch.Tensor, expert_weights: torch.Tensor, token_indices: torch.Tensor) -> torch.Tensor:
+        if self._trainable(x, expert_weights):
+            return _ExpertsECFn.apply(x, expert_weights, self.w1, self.w2, self.w3, self, token_indices)
         B, S, d = x.shape
         _, E, C = token_indices.shape
-        # Tables from caller-provided indices (host-built; the fused path uses ec_select's tables).
-        dev = x.device
+        sel = self.tables(token_indices, expert_weights, S)
+        out_dtype = torch.float32 if x.dtype == torch.float32 else torch.bfloat16
+        y = self.run(x.reshape(B * S, d), sel, B, S, C, out_dtype=out_dtype)
+        return _forward_only(y.view(B, S, d).to(x.dtype), x, self.w1, self.w2, self.w3, expert_weights)
+
+    def tables(self, token_indices: torch.Tensor, expert_weights: torch.Tensor, S: int) -> ops.ECSelectOut:
+        """Expert-major rows (row = e*B*C + b*C + c) and per-token combine tables from
+        caller-provided (B, E, C) token indices and weights (moe.py:649-671)."""
+        B, E, C = token_indices.shape
+        dev = token_indices.device
         b_idx = torch.arange(B, device=dev).view(B, 1, 1)
         e_idx = torch.arange(E, device=dev).view(1, E, 1)
         c_idx = torch.arange(C, device=dev).view(1, 1, C)
@@ -245,12 +304,9 @@ class GroupedExpertsExpertChoice(_PackedExperts):
         src_w = torch.zeros(B * S, E, device=dev, dtype=torch.float32)
         ee = e_idx.expand(B, E, C).reshape(-1)
         src_row[toks, ee] = rows.to(torch.int32)
-        src_w[toks, ee] = expert_weights.reshape(-1).float()
+        src_w[toks, ee] = expert_weights.detach().reshape(-1).float()
         offsets = (torch.arange(E + 1, device=dev, dtype=torch.int32) * (B * C))
-        sel = ops.ECSelectOut(token_indices, expert_weights, row_token, offsets, src_row, src_w)
-        out_dtype = torch.float32 if x.dtype == torch.float32 else torch.bfloat16
-        y = self.run(x.reshape(B * S, d), sel, B, S, C, out_dtype=out_dtype)
-        return _forward_only(y.view(B, S, d).to(x.dtype), x, self.w1, self.w2, self.w3, expert_weights)
+        return ops.ECSelectOut(token_indices, expert_weights, row_token, offsets, src_row, src_w)
 
 
 class _MoETrainFn(torch.autograd.Function):
@@ -273,20 +329,208 @@ class _MoETrainFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy, daux):
-        if ctx.sv is None:
-            raise RuntimeError("kmoe: backward through the MoE layer can run once per forward; "
-                               "retain_graph=True with a second backward is not supported")
+        sv = _once(ctx)
         B, S, d, x_dtype, has_aux = ctx.meta
         layer = ctx.layer
         ge = layer.grouped_experts
         w_in, w_out = layer.router.router[0].weight, layer.router.router[2].weight
         need_w = any(ctx.needs_input_grad[1:6])
-        g = _bwd.moe_backward(ctx.sv, dy, daux if has_aux else None, w_out, layer._bwd_weights(), layer.n_experts,
+        g = _bwd.moe_backward(sv, dy, daux if has_aux else None, w_out, layer._bwd_weights(), layer.n_experts,
                               ge.d_ff, layer.load_balance_loss_weight, layer.router_z_loss_weight, need_weights=need_w)
-        ctx.sv = None
         dx = g.dx.view(B, S, d).to(x_dtype)
         if not need_w:
             return dx, None, None, None, None, None, None
+        return (dx, g.dw_in.to(w_in.dtype), g.dw_out.to(w_out.dtype), g.dw1.to(ge.w1.dtype), g.dw2.to(ge.w2.dtype),
+                g.dw3.to(ge.w3.dtype), None)
+
+
+def _once(ctx):
+    if ctx.sv is None:
+        raise RuntimeError("kmoe: backward through an MoE module can run once per forward; "
+                           "retain_graph=True with a second backward is not supported")
+    sv = ctx.sv
+    ctx.sv = None
+    return sv
+
+
+class _RouterFn(torch.autograd.Function):
+    """Router.forward (moe.py:423-462) with its backward on the HIP kernels: from the
+    gradients of the top-k weights and of the logits to x, w_in and w_out."""
+
+    @staticmethod
+    def forward(ctx, x2d, w_in, w_out, router):
+        r = router.route(x2d.detach().to(torch.bfloat16).contiguous(), save_hidden=True, hist=False)
+        ctx.sv = (x2d, r)
+        ctx.router = router
+        ctx.mark_non_differentiable(r.idx)
+        return r.w, r.idx, r.logits
+
+    @staticmethod
+    def backward(ctx, dw, didx, dlogits):
+        x2d, r = _once(ctx)
+        router = ctx.router
+        xb = x2d.detach().to(torch.bfloat16).contiguous()
+        T = xb.shape[0]
+        dw = torch.zeros(T, router.top_k, device=xb.device) if dw is None else dw.float().contiguous()
+        need_w = any(ctx.needs_input_grad[1:3])
+        dx, dw_in, dw_out = _bwd.router_backward(xb, r.logits, r.idx, r.w, r.hidden, dw, dlogits,
+                                                 router.router[2].weight, router._bwd_weights(), need_weights=need_w)
+        w_in, w_out = router.router[0].weight, router.router[2].weight
+        return (dx.to(x2d.dtype), None if dw_in is None else dw_in.to(w_in.dtype), dw_out.to(w_out.dtype), None)
+
+
+class _ECRouterFn(torch.autograd.Function):
+    """ExpertChoiceRouter.forward (moe.py:494-530) with its backward on the HIP kernels:
+    from the gradients of the (B, E, C) weights and of the logits to x, w_in, w_out."""
+
+    @staticmethod
+    def forward(ctx, x3d, w_in, w_out, router):
+        B, S, d = x3d.shape
+        r, sel, C = router.route(x3d.detach().to(torch.bfloat16).contiguous(), save_hidden=True)
+        ctx.sv = (x3d, r, sel)
+        ctx.router = router
+        ctx.mark_non_differentiable(sel.idx)
+        return sel.w, sel.idx, r.logits.view(B, S, router.n_experts)
+
+    @staticmethod
+    def backward(ctx, dw, didx, dlogits):
+        x3d, r, sel = _once(ctx)
+        router = ctx.router
+        B, S, d = x3d.shape
+        E = router.n_experts
+        xb = x3d.detach().reshape(B * S, d).to(torch.bfloat16).contiguous()
+        # the weights' gradient in the per-token (B*S, E) layout of the combine tables
+        dw_te = torch.zeros(B * S, E, device=xb.device, dtype=torch.float32)
+        if dw is not None:
+            tok = (torch.arange(B, device=xb.device).view(B, 1, 1) * S + sel.idx).reshape(-1)
+            ex = torch.arange(E, device=xb.device).view(1, E, 1).expand_as(sel.idx).reshape(-1)
+            dw_te[tok, ex] = dw.float().reshape(-1)
+        dl = torch.zeros(B * S, E, device=xb.device, dtype=torch.float32)
+        ops.ec_dlogits(r.logits, B, S, E, sel.src_row, sel.src_w, dw_te, dl)
+        if dlogits is not None:
+            dl += dlogits.reshape(B * S, E).float()
+        need_w = any(ctx.needs_input_grad[1:3])
+        dx = torch.empty(B * S, d, device=xb.device, dtype=torch.bfloat16)
+        dw_in, dw_out = _bwd._router_core(xb, r.hidden, router.router[2].weight, router._bwd_weights(), dl, dx,
+                                          need_w)
+        w_in, w_out = router.router[0].weight, router.router[2].weight
+        return (dx.view(B, S, d).to(x3d.dtype), None if dw_in is None else dw_in.to(w_in.dtype),
+                dw_out.to(w_out.dtype), None)
+
+
+class _ExpertsFn(torch.autograd.Function):
+    """GroupedExperts.forward (moe.py:213-294) with its backward on the HIP kernels:
+    gradients of x, of the routing weights and of w1 / w2 / w3."""
+
+    @staticmethod
+    def forward(ctx, x2d, w, w1, w2, w3, experts, idx):
+        T, k = idx.shape
+        E = experts.n_experts
+        xb = x2d.detach().to(torch.bfloat16).contiguous()
+        pw = experts.packed()
+        disp = ops.dispatch(xb, idx, w.detach(), E, materialize=True)
+        h, gu = ops.gemm_gate_up_rows(xb, None, disp.row_token, disp.offsets, pw, T * k, save_gu=True)
+        yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
+        out_dtype = torch.float32 if x2d.dtype == torch.float32 else torch.bfloat16
+        y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T, out_dtype=out_dtype)
+        ctx.sv = (disp, h, gu, yperm)
+        ctx.experts = experts
+        ctx.meta = (x2d.dtype, w.dtype, T, k)
+        return y.to(x2d.dtype)
+
+    @staticmethod
+    def backward(ctx, dy):
+        disp, h, gu, yperm = _once(ctx)
+        ge = ctx.experts
+        x_dtype, w_dtype, T, k = ctx.meta
+        need_w = any(ctx.needs_input_grad[2:5])
+        dy = dy.reshape(T, -1).to(torch.bfloat16).contiguous()
+        dx, dw, dw1, dw2, dw3 = _bwd.experts_backward(dy, yperm, gu, h, disp.xperm, disp.slot_row.view(T, k),
+                                                      disp.slot_w.view(T, k), disp.offsets, T * k, ge.bwd_packed(),
+                                                      ge.n_experts, ge.d_ff, need_weights=need_w)
+        wg = (None, None, None) if dw1 is None else (dw1.to(ge.w1.dtype), dw2.to(ge.w2.dtype), dw3.to(ge.w3.dtype))
+        return (dx.to(x_dtype), dw.to(w_dtype), *wg, None, None)
+
+
+class _ExpertsECFn(torch.autograd.Function):
+    """GroupedExpertsExpertChoice.forward (moe.py:588-673) with its backward on the HIP
+    kernels: gradients of x, of the (B, E, C) weights and of w1 / w2 / w3."""
+
+    @staticmethod
+    def forward(ctx, x3d, w, w1, w2, w3, experts, token_indices):
+        B, S, d = x3d.shape
+        _, E, C = token_indices.shape
+        sel = experts.tables(token_indices, w, S)
+        xb = x3d.detach().reshape(B * S, d).to(torch.bfloat16).contiguous()
+        A = E * B * C
+        pw = experts.packed()
+        xperm, _ = ops.gather_rows(xb, sel.row_token, A)
+        h, gu = ops.gemm_gate_up_rows(xb, None, sel.row_token, sel.offsets, pw, A, save_gu=True)
+        yperm = ops.gemm_down(h, None, sel.offsets, pw, A)
+        out_dtype = torch.float32 if x3d.dtype == torch.float32 else torch.bfloat16
+        y = ops.combine(yperm, sel.src_row, sel.src_w, B * S, out_dtype=out_dtype)
+        ctx.sv = (sel, h, gu, yperm, xperm)
+        ctx.experts = experts
+        ctx.meta = (x3d.dtype, w.dtype, B, S, d)
+        return y.view(B, S, d).to(x3d.dtype)
+
+    @staticmethod
+    def backward(ctx, dy):
+        sel, h, gu, yperm, xperm = _once(ctx)
+        ge = ctx.experts
+        x_dtype, w_dtype, B, S, d = ctx.meta
+        E = ge.n_experts
+        need_w = any(ctx.needs_input_grad[2:5])
+        dy = dy.reshape(B * S, d).to(torch.bfloat16).contiguous()
+        dx, dw_te, dw1, dw2, dw3 = _bwd.experts_backward(dy, yperm, gu, h, xperm, sel.src_row, sel.src_w, sel.offsets,
+                                                         h.shape[0], ge.bwd_packed(), E, ge.d_ff, need_weights=need_w)
+        tok = (torch.arange(B, device=dy.device).view(B, 1, 1) * S + sel.idx).reshape(-1)
+        ex = torch.arange(E, device=dy.device).view(1, E, 1).expand_as(sel.idx).reshape(-1)
+        dw = dw_te[tok, ex].view(sel.idx.shape)
+        wg = (None, None, None) if dw1 is None else (dw1.to(ge.w1.dtype), dw2.to(ge.w2.dtype), dw3.to(ge.w3.dtype))
+        return (dx.view(B, S, d).to(x_dtype), dw.to(w_dtype), *wg, None, None)
+
+
+class _MoEECTrainFn(torch.autograd.Function):
+    """Expert-choice MoE layer (moe.py:494-530, 588-673, 815-838) whose backward runs on
+    the HIP kernels; outputs y and the z-loss (0-dim, 0 in eval)."""
+
+    @staticmethod
+    def forward(ctx, x, w_in, w_out, w1, w2, w3, layer):
+        B, S, d = x.shape
+        T = B * S
+        E = layer.n_experts
+        ge = layer.grouped_experts_ec
+        xb = x.detach().to(torch.bfloat16).contiguous()
+        r, sel, C = layer.router.route(xb, descending=False, save_hidden=True)
+        x2d = xb.reshape(T, d)
+        A = E * B * C
+        pw = ge.packed()
+        xperm, _ = ops.gather_rows(x2d, sel.row_token, A)
+        h, gu = ops.gemm_gate_up_rows(x2d, None, sel.row_token, sel.offsets, pw, A, save_gu=True)
+        yperm = ops.gemm_down(h, None, sel.offsets, pw, A)
+        y = ops.combine(yperm, sel.src_row, sel.src_w, T, out_dtype=layer._out_dtype(x))
+        has_aux = layer.training and layer.router_z_loss_weight > 0
+        aux = (ops.aux_loss(r.partials, T, E, None, 1, 0.0, layer.router_z_loss_weight)[0] if has_aux
+               else torch.zeros((), device=x.device, dtype=torch.float32))
+        ctx.sv = _bwd.SavedEC(x2d, r.logits, r.hidden, sel, h, gu, yperm, xperm, B, S)
+        ctx.layer = layer
+        ctx.meta = (x.dtype, has_aux)
+        return y.view(B, S, d).to(x.dtype), aux
+
+    @staticmethod
+    def backward(ctx, dy, daux):
+        sv = _once(ctx)
+        layer = ctx.layer
+        ge = layer.grouped_experts_ec
+        x_dtype, has_aux = ctx.meta
+        w_in, w_out = layer.router.router[0].weight, layer.router.router[2].weight
+        need_w = any(ctx.needs_input_grad[1:6])
+        g = _bwd.ec_backward(sv, dy, daux if has_aux else None, w_out, layer._bwd_weights(), layer.n_experts,
+                             ge.d_ff, layer.router_z_loss_weight, need_weights=need_w)
+        dx = g.dx.view(sv.B, sv.S, -1).to(x_dtype)
+        if not need_w:
+            return dx, None, g.dw_out.to(w_out.dtype), None, None, None, None
         return (dx, g.dw_in.to(w_in.dtype), g.dw_out.to(w_out.dtype), g.dw1.to(ge.w1.dtype), g.dw2.to(ge.w2.dtype),
                 g.dw3.to(ge.w3.dtype), None)
 
@@ -345,13 +589,13 @@ class MoELayer(nn.Module):
             return False
         if not (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
-        ge = self.grouped_experts
+        ge = self.grouped_experts if self.grouped_experts is not None else self.grouped_experts_ec
         # the weight-gradient stores write rows of 8 bf16 (d_ff_expert a multiple of 8)
-        return not (ge.use_fp8 or self.router.balanced_routing or ge.d_ff % 8)
+        return not (ge.use_fp8 or getattr(self.router, "balanced_routing", False) or ge.d_ff % 8)
 
     def _bwd_weights(self) -> _bwd.BwdWeights:
         """Backward packed weights, rebuilt only when a parameter changed."""
-        ge = self.grouped_experts
+        ge = self.grouped_experts if self.grouped_experts is not None else self.grouped_experts_ec
         w_in = self.router.router[0].weight
         key = tuple((w.data_ptr(), w._version) for w in (ge.w1, ge.w2, ge.w3, w_in))
         cache = getattr(self, "_bwd_cache", None)
@@ -419,6 +663,12 @@ class MoELayer(nn.Module):
 
     def _forward_expert_choice(self, hidden_states: torch.Tensor) -> torch.Tensor:
         B, S, d = hidden_states.shape
+        if self._trainable(hidden_states):
+            ge = self.grouped_experts_ec
+            y, aux = _MoEECTrainFn.apply(hidden_states, self.router.router[0].weight, self.router.router[2].weight,
+                                         ge.w1, ge.w2, ge.w3, self)
+            self.aux_loss = aux if (self.training and self.router_z_loss_weight > 0) else 0.0
+            return y
         x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
         # the layer output does not depend on the order of an expert's C slots: take
         # them in token order (no sort)

@@ -120,7 +120,7 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=F
                       ptr(logits), ptr(idx), ptr(w), ptr(partials), float(rms_eps), ptr(rscale), _stream(x2d))
         return RouterOut(logits, idx, w, partials, None, rscale)
     if hist and k > 0 and T > 0:
-        bc = torch.empty(npart // (E + 1), E, device=dev, dtype=torch.int32)
+        bc = torch.empty((T + 63) // 64, E, device=dev, dtype=torch.int32)
         with _Stage("router"):
             _lib.call("kmoe_router_hist", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
                       ptr(logits), ptr(idx), ptr(w), ptr(partials), ptr(hidden), ptr(bc), _stream(x2d))
@@ -391,6 +391,15 @@ def ec_select(logits, B, S, E, C, descending=True) -> ECSelectOut:
               ptr(row_token), ptr(offsets),
               ptr(src_row), ptr(src_w), None, 0, _stream(logits))
     return ECSelectOut(idx, w, row_token, offsets, src_row, src_w)
+
+
+def ec_dlogits(logits, B, S, E, src_row, src_w, dw, dl):
+    """Adds the expert-choice selection's logit gradient (kmoe_ec_dlogits) to dl (B*S, E)."""
+    _need_gpu(logits, src_row, src_w, dw, dl)
+    with _Stage("bwd_router"):
+        _lib.call("kmoe_ec_dlogits", ptr(_contig(logits, torch.float32)), B, S, E, ptr(src_row), ptr(src_w),
+                  ptr(_contig(dw, torch.float32)), ptr(dl), _stream(logits))
+    return dl
 
 
 class ModSelectOut(NamedTuple):

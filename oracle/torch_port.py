@@ -144,6 +144,29 @@ def moe_loss_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, dy, capacity=0, bias=N
     return loss
 
 
+def grouped_experts_ec_tc(x3d, ew, ti, w1, w2, w3):
+    """GroupedExpertsExpertChoice.forward (moe.py:626-673): gather the selected tokens,
+    bmm SwiGLU with the weights repeated per sequence, weight, scatter_add_ back."""
+    B, S, d = x3d.shape
+    _, E, C = ti.shape
+    gi = ti.unsqueeze(-1).expand(-1, -1, -1, d)
+    xin = torch.gather(x3d.unsqueeze(1).expand(-1, E, -1, -1), 2, gi).reshape(B * E, C, d)
+    W1, W2, W3 = w1.repeat(B, 1, 1), w2.repeat(B, 1, 1), w3.repeat(B, 1, 1)
+    out = torch.bmm(F.silu(torch.bmm(xin, W1)) * torch.bmm(xin, W2), W3).view(B, E, C, d)
+    wout = out * ew.unsqueeze(-1)
+    y = x3d.new_zeros(B, S, d)
+    return y.scatter_add(1, ti.reshape(B, E * C).unsqueeze(-1).expand(-1, -1, d), wout.reshape(B, E * C, d))
+
+
+def ec_weights_routed(logits, ti):
+    """ExpertChoiceRouter.forward's weights at a fixed selection ti (B, E, C): softmax of
+    the logits over each sequence's tokens, gathered at ti, normalised per expert with
+    the + 1e-9 of moe.py:528."""
+    probs = F.softmax(logits.transpose(1, 2), dim=-1)
+    ew = probs.gather(2, ti)
+    return ew / (ew.sum(dim=-1, keepdim=True) + 1e-9)
+
+
 def moe_layer_ec(x3d, w_in, w_out, w1, w2, w3, cf):
     """MoELayer expert-choice forward (moe.py:815-838) without torch.compile."""
     B, S, d = x3d.shape
@@ -153,11 +176,25 @@ def moe_layer_ec(x3d, w_in, w_out, w1, w2, w3, cf):
     probs = F.softmax(logits.transpose(1, 2), dim=-1)
     ew, ti = torch.topk(probs, C, dim=-1)
     ew = ew / (ew.sum(dim=-1, keepdim=True) + 1e-9)
-    gi = ti.unsqueeze(-1).expand(-1, -1, -1, d)
-    xin = torch.gather(x3d.unsqueeze(1).expand(-1, E, -1, -1), 2, gi).reshape(B * E, C, d)
-    W1, W2, W3 = w1.repeat(B, 1, 1), w2.repeat(B, 1, 1), w3.repeat(B, 1, 1)
-    out = torch.bmm(F.silu(torch.bmm(xin, W1)) * torch.bmm(xin, W2), W3).view(B, E, C, d)
-    wout = out * ew.unsqueeze(-1)
-    y = x3d.new_zeros(B, S, d)
-    y.scatter_add_(1, ti.reshape(B, E * C).unsqueeze(-1).expand(-1, -1, d), wout.reshape(B, E * C, d))
-    return y
+    return grouped_experts_ec_tc(x3d, ew, ti, w1, w2, w3)
+
+
+def moe_loss_ec_routed(x3d, w_in, w_out, w1, w2, w3, ti, dy, training=True, w_z=0.001):
+    """Scalar loss sum(y * dy) (+ w_z * z-loss in training, moe.py:833-836) of MoELayer's
+    expert-choice forward with the selection fixed to ti (B, E, C): at a fixed selection
+    the layer is smooth, so the autograd gradients of this loss are the reference's."""
+    logits = F.linear(F.silu(F.linear(x3d, w_in)), w_out)
+    y = grouped_experts_ec_tc(x3d, ec_weights_routed(logits, ti), ti, w1, w2, w3)
+    loss = (y * dy).sum()
+    if training:
+        loss = loss + w_z * (torch.logsumexp(logits, dim=-1) ** 2).mean()
+    return loss
+
+
+def router_loss_routed(x2d, w_in, w_out, idx, gw, gl):
+    """sum(w * gw) + sum(logits * gl) of Router.forward (moe.py:423-462) with the top-k
+    experts fixed to idx: for the gradients of the router alone."""
+    logits = F.linear(F.silu(F.linear(x2d, w_in)), w_out)
+    v = F.softmax(logits, dim=-1).gather(1, idx)
+    w = v / v.sum(dim=-1, keepdim=True)
+    return (w * gw).sum() + (logits * gl).sum()

@@ -605,3 +605,51 @@ def test_ffn_block_matches_torch_port():
                        w3.numpy(), k)
     y, _ = P.moe_layer_tc(F.rms_norm(h, (d,), nw, eps=1e-5), w_in, w_out, w1, w2, w3, k, training=False)
     np.testing.assert_allclose(r["y"], (h + y)[0].numpy(), rtol=1e-9, atol=1e-12)
+
+
+# ---------------------------------------------------------------- expert-choice backward oracle
+def _tiny_ec(seed, B=2, S=10, d=6, E=3, F_=5, scale=0.5):
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda *s: (torch.randn(*s, generator=g, dtype=torch.float64) * scale).requires_grad_(True)
+    return (mk(B, S, d), mk(128, d), mk(E, 128), mk(E, d, F_), mk(E, d, F_), mk(E, F_, d),
+            torch.randn(B, S, d, generator=g, dtype=torch.float64))
+
+
+def test_ec_routed_loss_matches_layer_forward():
+    """At its own top-C selection, moe_loss_ec_routed's output term equals moe_layer_ec's
+    y (two restatements of moe.py:494-530, 626-673), and its z term the closed form."""
+    x, w_in, w_out, w1, w2, w3, dy = _tiny_ec(5, B=2, S=16, d=8, E=4, F_=6)
+    with torch.no_grad():
+        y = P.moe_layer_ec(x, w_in, w_out, w1, w2, w3, 2.0)
+        logits = torch.nn.functional.linear(torch.nn.functional.silu(torch.nn.functional.linear(x, w_in)), w_out)
+        C = int(math.ceil(16 * 2.0 / 4))
+        ti = torch.topk(torch.softmax(logits.transpose(1, 2), -1), C, dim=-1).indices
+        l0 = P.moe_loss_ec_routed(x, w_in, w_out, w1, w2, w3, ti, dy, training=False)
+        l1 = P.moe_loss_ec_routed(x, w_in, w_out, w1, w2, w3, ti, dy, training=True, w_z=0.5)
+        z = (torch.logsumexp(logits, -1) ** 2).mean()
+    assert abs(float(l0) - float((y * dy).sum())) < 1e-10
+    assert abs(float(l1) - float(l0) - 0.5 * float(z)) < 1e-10
+
+
+def test_ec_routed_loss_gradcheck():
+    x, w_in, w_out, w1, w2, w3, dy = _tiny_ec(6)
+    with torch.no_grad():
+        logits = torch.nn.functional.linear(torch.nn.functional.silu(torch.nn.functional.linear(x, w_in)), w_out)
+        ti = torch.topk(torch.softmax(logits.transpose(1, 2), -1), 4, dim=-1).indices
+    f = lambda *a: P.moe_loss_ec_routed(*a, ti, dy, training=True, w_z=0.3)
+    assert torch.autograd.gradcheck(f, (x, w_in, w_out, w1, w2, w3), eps=1e-6, atol=1e-6, rtol=1e-5)
+
+
+def test_router_loss_routed_gradcheck_and_forward():
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(9, 6, generator=g, dtype=torch.float64, requires_grad=True)
+    w_in = (torch.randn(128, 6, generator=g, dtype=torch.float64) * 0.3).requires_grad_(True)
+    w_out = (torch.randn(4, 128, generator=g, dtype=torch.float64) * 0.3).requires_grad_(True)
+    w, idx, logits = P.router_tc(x[None], w_in, w_out, 2)
+    gw, gl = torch.randn(9, 2, generator=g, dtype=torch.float64), torch.randn(9, 4, generator=g, dtype=torch.float64)
+    with torch.no_grad():
+        ref = float((w[0] * gw).sum() + (logits[0] * gl).sum())
+        got = float(P.router_loss_routed(x, w_in, w_out, idx[0], gw, gl))
+    assert abs(ref - got) < 1e-12  # at its own routing: Router.forward's (w, logits)
+    f = lambda *a: P.router_loss_routed(*a, idx[0], gw, gl)
+    assert torch.autograd.gradcheck(f, (x, w_in, w_out), eps=1e-6, atol=1e-6, rtol=1e-5)
