@@ -270,6 +270,16 @@ int kmoe_gemm_gate_up_rows_gu(const void* x, const int32_t* row_index, int64_t n
 int kmoe_combine_bwd(const void* dy, const void* yperm, const int32_t* slot_row, const float* slot_w, int k,
                      int d, int64_t T, void* dyperm, float* dw, void* stream);
 
+/* kmoe_combine_bwd for a combine that wrote token t's output to row row_index[t] of
+ * y, scaled by scale[t] (the MoD composition: the gather of layers.py:160-165, the
+ * weighting by the MoD router weights and the scatter_add_ of layers.py:170-184):
+ *   dyperm[r] = scale[t] w[t,j] dy[row_index[t]],  dw[t,j] = scale[t] (dy[row_index[t]] . yperm[r]),
+ *   dscale[t] = sum_j w[t,j] (dy[row_index[t]] . yperm[r])   (the MoD weight's gradient)
+ * row_index NULL = t, scale NULL = 1, dscale nullable.                         */
+int kmoe_combine_bwd_rows(const void* dy, const void* yperm, const int32_t* slot_row, const float* slot_w, int k,
+                          int d, int64_t T, const int32_t* row_index, const float* scale, void* dyperm, float* dw,
+                          float* dscale, void* stream);
+
 /* Backward packed weight layouts (derived caches, like kmoe_pack_weights):
  *   w3n : (E, round_up(F,256), d)       rows of w3 (E,F,d), K = d contiguous
  *   w13t: (E, round_up(d,256), 2*F_pad) rows i of w1/w2 (E,d,F), gate and up
@@ -328,6 +338,36 @@ int kmoe_router_dlogits(const float* logits, int64_t T, int E, const int64_t* to
  * gradient of each selected slot's weight (kmoe_combine_bwd over those tables).     */
 int kmoe_ec_dlogits(const float* logits, int B, int S, int E, const int32_t* src_row, const float* src_w,
                     const float* dw, float* dlogits, void* stream);
+
+/* Backward of MoDRouter.forward (mod.py:93-112) at its selection: with p = sel_w
+ * (B, keep), the softmax over each sequence's kept logits, and dsel its gradient
+ * (kmoe_combine_bwd_rows' dscale):
+ *   dlog[i] = p_i (dsel_i - sum_l p_l dsel_l)     written at dlog[i * dlog_stride]
+ *   dw_mod  = sum_i dlog[i] x_sel[i]              (logits = x . w_mod; nullable: skipped)
+ * x_sel (B*keep, d) bf16: the kept rows in kmoe_mod_select's order.  Unkept tokens
+ * get no logit gradient (top-k is piecewise constant; the MoD auxiliary BCE loss is
+ * not part of this build).  workspace: kmoe_mod_bwd_workspace_bytes(B*keep, d).  */
+size_t kmoe_mod_bwd_workspace_bytes(int64_t n_rows, int d);
+int kmoe_mod_bwd(const float* sel_w, const float* dsel, int B, int64_t keep, const void* x_sel, int d, float* dlog,
+                 int64_t dlog_stride, void* dw_mod, int dw_dtype, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/* RMSNorm of the block boundary (RMSNorm.forward, embeddings.py:167-195; the
+ * ffn_norm of TransformerBlock.forward, layers.py:142-147) for the training path:
+ *   n[t] = bf16(g * x[t] * r_t),  rrms[t] = r_t = 1/sqrt(mean(x[t]^2) + eps)
+ * x (T, d) bf16 or f32, g (d) bf16 or f32; d a multiple of 8, <= 8192.       */
+int kmoe_rmsnorm(const void* x, int x_dtype, const void* weight, int w_dtype, float eps, int64_t T, int d, void* n,
+                 float* rrms, void* stream);
+/* Its backward from dn (T, d) bf16 (the gradient of n):
+ *   dx[t] = dres[t] + r_t g*dn[t] - (r_t^3 / d) x[t] sum_c g_c dn[t,c] x[t,c]
+ *   dweight = sum_t dn[t] * x[t] r_t  (fixed-order reduction)
+ * dres (nullable; the residual's gradient of out = x + f(n)) and dx in x's dtype,
+ * dweight in dw_dtype.  T = 0 writes dweight = 0 (the row buffers may be NULL).
+ * workspace: kmoe_rmsnorm_bwd_workspace_bytes.                               */
+size_t kmoe_rmsnorm_bwd_workspace_bytes(int64_t T, int d);
+int kmoe_rmsnorm_bwd(const void* dn, const void* x, int x_dtype, const void* weight, int w_dtype, const float* rrms,
+                     const void* dres, int64_t T, int d, void* dx, void* dweight, int dw_dtype, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /* Router MLP backward: da = (dl . w_out) * silu'(a) -> (T, 128) bf16 and
  * dw_out = dl^T silu(a) -> (E, 128) (bf16 or f32), reduced in a fixed order.

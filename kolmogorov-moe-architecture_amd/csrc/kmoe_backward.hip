@@ -11,26 +11,35 @@
 
 namespace {
 
-// dyperm[r] = w[t,j] * dy[t] (bf16) for the kept slot r = slot_row[t,j];
-// dw[t,j] = dy[t] . yperm[r] (fp32, lane-ordered fma then a fixed shuffle tree: the
-// result is bit-reproducible; 0 for a dropped slot).  One wave per token.
+// dyperm[r] = scale[t] * w[t,j] * dy[row(t)] (bf16) for the kept slot r = slot_row[t,j];
+// dw[t,j] = scale[t] * (dy[row(t)] . yperm[r]) and dscale[t] = sum_j w[t,j] (dy[row(t)] .
+// yperm[r]) (fp32, lane-ordered fma then a fixed shuffle tree: bit-reproducible; a
+// dropped slot gives dw 0 and adds nothing).  row(t) = row_index[t] (or t), scale 1 and
+// dscale skipped when NULL.  One wave per token.
 __global__ __launch_bounds__(256) void combine_bwd_kernel(const uint16_t* __restrict__ dy,
                                                           const uint16_t* __restrict__ yperm,
                                                           const int32_t* __restrict__ slot_row,
                                                           const float* __restrict__ slot_w, int k, int d, int64_t T,
-                                                          uint16_t* __restrict__ dyperm, float* __restrict__ dw) {
+                                                          const int32_t* __restrict__ row_index,
+                                                          const float* __restrict__ scale,
+                                                          uint16_t* __restrict__ dyperm, float* __restrict__ dw,
+                                                          float* __restrict__ dscale) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const int nvec = d / 8;
-  const i32x4_t* dyr = reinterpret_cast<const i32x4_t*>(dy + t * d);
+  const int64_t trow = row_index ? (int64_t)row_index[t] : t;
+  const float sc = scale ? scale[t] : 1.0f;
+  const i32x4_t* dyr = reinterpret_cast<const i32x4_t*>(dy + trow * d);
+  float ds = 0.0f;
   for (int j = 0; j < k; ++j) {
     const int r = slot_row[t * k + j];
-    const float w = slot_w[t * k + j];
+    const float wj = slot_w[t * k + j];
     if (r < 0) {
       if (lane == 0) dw[t * k + j] = 0.0f;
       continue;
     }
+    const float w = sc * wj;
     const i32x4_t* yr = reinterpret_cast<const i32x4_t*>(yperm + (int64_t)r * d);
     i32x4_t* out = reinterpret_cast<i32x4_t*>(dyperm + (int64_t)r * d);
     float dot = 0.0f;
@@ -48,8 +57,10 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const uint16_t* __rest
       out[v] = o;
     }
     dot = wave_sum(dot);
-    if (lane == 0) dw[t * k + j] = dot;
+    if (lane == 0) dw[t * k + j] = sc * dot;
+    ds = fmaf(wj, dot, ds);
   }
+  if (dscale && lane == 0) dscale[t] = ds;
 }
 
 // SwiGLU backward on the packed column order (per 128-column block: 128 gate then 128
@@ -297,6 +308,73 @@ __global__ __launch_bounds__(64 * RWAVES) void reduce_partials_kernel(const floa
     static_cast<uint16_t*>(out)[i] = f32_to_bf16(t);
 }
 
+// Mixture-of-Depths router backward.  sel_w = softmax over each sequence's kept
+// logits (mod.py:107-112), so for the gradient dsel of the weights
+//   dlog[i] = p_i (dsel_i - sum_l p_l dsel_l)
+// (one workgroup per sequence; the sum in a fixed order).  dlog is written with a
+// stride, so that it can land in a column of a caller's table.
+constexpr int MODB_THREADS = 1024;
+__global__ __launch_bounds__(MODB_THREADS) void mod_dlog_kernel(const float* __restrict__ sel_w,
+                                                                const float* __restrict__ dsel, int64_t keep,
+                                                                float* __restrict__ dlog, int64_t stride) {
+  __shared__ float red[MODB_THREADS / 64];
+  const int64_t base = (int64_t)blockIdx.x * keep;
+  float s = 0.0f;
+  for (int64_t i = threadIdx.x; i < keep; i += MODB_THREADS) s = fmaf(sel_w[base + i], dsel[base + i], s);
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int q = 0; q < MODB_THREADS / 64; ++q) tot += red[q];
+  for (int64_t i = threadIdx.x; i < keep; i += MODB_THREADS) {
+    const float p = sel_w[base + i];
+    dlog[(base + i) * stride] = p * (dsel[base + i] - tot);
+  }
+}
+
+// partial[seg][c] = sum over the rows t of segment seg of dlog[t] x[t][c]: the MoD
+// router weight's gradient (logits = x . w_mod).  4 waves per workgroup, wave w taking
+// every 4th row of the segment, 512 columns per workgroup (8 per lane); the waves'
+// sums are added in wave order through LDS.
+__global__ __launch_bounds__(256) void mod_wgrad_kernel(const uint16_t* __restrict__ x, int d, int64_t T,
+                                                        const float* __restrict__ dlog, int64_t stride,
+                                                        int64_t seg_rows, float* __restrict__ partial) {
+  __shared__ float red[4][512];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c0 = (int)blockIdx.y * 512 + lane * 8;
+  const int64_t t0 = (int64_t)blockIdx.x * seg_rows;
+  const int64_t t1 = t0 + seg_rows < T ? t0 + seg_rows : T;
+  float acc[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+  if (c0 < d) {
+    for (int64_t t = t0 + w; t < t1; t += 4) {
+      const float gl = dlog[t * stride];
+      const i32x4_t a = *reinterpret_cast<const i32x4_t*>(x + t * d + c0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[2 * q] = fmaf(gl, __uint_as_float(((uint32_t)a[q]) << 16), acc[2 * q]);
+        acc[2 * q + 1] = fmaf(gl, __uint_as_float(((uint32_t)a[q]) & 0xffff0000u), acc[2 * q + 1]);
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) red[w][lane * 8 + q] = acc[q];
+  __syncthreads();
+  for (int c = threadIdx.x; c < 512; c += 256) {
+    const int col = (int)blockIdx.y * 512 + c;
+    if (col < d) partial[(int64_t)blockIdx.x * d + col] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
+  }
+}
+
+int64_t mod_seg_rows(int64_t n) {
+  // at most 256 segments, each a multiple of 4 rows
+  int64_t rows = kmoe::ceil_div<int64_t>(n, 256);
+  rows = kmoe::ceil_div<int64_t>(rows, 4) * 4;
+  return rows < 4 ? 4 : rows;
+}
+
 // w_in (128, d) -> packed rows of w_in^T: (round_up(d, 256), 128 + 64) bf16, row i =
 // w_in[:, i] (the B operand of dx_router = da . w_in), zero padded.
 __global__ __launch_bounds__(256) void pack_w_in_t_kernel(const void* __restrict__ w_in, bool in_f32, int d,
@@ -330,8 +408,23 @@ extern "C" int kmoe_combine_bwd(const void* dy, const void* yperm, const int32_t
   if (T == 0) return KMOE_OK;
   hipLaunchKernelGGL(combine_bwd_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0,
                      kmoe::as_stream(stream), static_cast<const uint16_t*>(dy), static_cast<const uint16_t*>(yperm),
-                     slot_row, slot_w, k, d, T, static_cast<uint16_t*>(dyperm), dw);
+                     slot_row, slot_w, k, d, T, nullptr, nullptr, static_cast<uint16_t*>(dyperm), dw, nullptr);
   return kmoe::check_launch("kmoe_combine_bwd");
+}
+
+extern "C" int kmoe_combine_bwd_rows(const void* dy, const void* yperm, const int32_t* slot_row, const float* slot_w,
+                                     int k, int d, int64_t T, const int32_t* row_index, const float* scale,
+                                     void* dyperm, float* dw, float* dscale, void* stream) {
+  KMOE_REQUIRE(dy && yperm && slot_row && slot_w && dyperm && dw, KMOE_ERR_NULL,
+               "kmoe_combine_bwd_rows: null buffer");
+  KMOE_REQUIRE(k >= 1 && k <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_combine_bwd_rows: k=%d", k);
+  KMOE_REQUIRE(d > 0 && d % 8 == 0, KMOE_ERR_SHAPE, "kmoe_combine_bwd_rows: d=%d must be a multiple of 8", d);
+  KMOE_REQUIRE(T >= 0, KMOE_ERR_SHAPE, "kmoe_combine_bwd_rows: T < 0");
+  if (T == 0) return KMOE_OK;
+  hipLaunchKernelGGL(combine_bwd_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0,
+                     kmoe::as_stream(stream), static_cast<const uint16_t*>(dy), static_cast<const uint16_t*>(yperm),
+                     slot_row, slot_w, k, d, T, row_index, scale, static_cast<uint16_t*>(dyperm), dw, dscale);
+  return kmoe::check_launch("kmoe_combine_bwd_rows");
 }
 
 extern "C" int kmoe_swiglu_bwd(const void* dh, const void* gu, int64_t rows, const int32_t* n_rows_dev, int F,
@@ -439,4 +532,36 @@ extern "C" int kmoe_reduce_f32(const float* partial, int64_t n_parts, int64_t n,
   hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(n, 64)), dim3(64 * RWAVES), 0,
                      kmoe::as_stream(stream), partial, n_parts, n, out, out_dtype == KMOE_DTYPE_F32);
   return kmoe::check_launch("kmoe_reduce_f32");
+}
+
+extern "C" size_t kmoe_mod_bwd_workspace_bytes(int64_t n_rows, int d) {
+  if (n_rows <= 0 || d <= 0) return 0;
+  return (size_t)kmoe::ceil_div<int64_t>(n_rows, mod_seg_rows(n_rows)) * (size_t)d * sizeof(float);
+}
+
+extern "C" int kmoe_mod_bwd(const float* sel_w, const float* dsel, int B, int64_t keep, const void* x_sel, int d,
+                            float* dlog, int64_t dlog_stride, void* dw_mod, int dw_dtype, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  KMOE_REQUIRE(sel_w && dsel && dlog, KMOE_ERR_NULL, "kmoe_mod_bwd: null buffer");
+  KMOE_REQUIRE(B >= 1 && keep >= 1 && dlog_stride >= 1, KMOE_ERR_SHAPE, "kmoe_mod_bwd: bad B/keep/stride");
+  hipStream_t s = kmoe::as_stream(stream);
+  hipLaunchKernelGGL(mod_dlog_kernel, dim3((unsigned)B), dim3(MODB_THREADS), 0, s, sel_w, dsel, keep, dlog,
+                     dlog_stride);
+  int rc = kmoe::check_launch("kmoe_mod_bwd");
+  if (rc != KMOE_OK || !dw_mod) return rc;
+  KMOE_REQUIRE(x_sel, KMOE_ERR_NULL, "kmoe_mod_bwd: null x_sel with a weight gradient");
+  KMOE_REQUIRE(d > 0 && d % 8 == 0, KMOE_ERR_SHAPE, "kmoe_mod_bwd: d=%d must be a multiple of 8", d);
+  KMOE_REQUIRE(dw_dtype == KMOE_DTYPE_BF16 || dw_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE, "kmoe_mod_bwd: dtype");
+  const int64_t n = (int64_t)B * keep;
+  const size_t need = kmoe_mod_bwd_workspace_bytes(n, d);
+  KMOE_REQUIRE(workspace && workspace_bytes >= need, KMOE_ERR_WORKSPACE, "kmoe_mod_bwd: workspace %zu < %zu bytes",
+               workspace_bytes, need);
+  const int64_t seg = mod_seg_rows(n);
+  const int64_t nseg = kmoe::ceil_div<int64_t>(n, seg);
+  float* partial = static_cast<float*>(workspace);
+  hipLaunchKernelGGL(mod_wgrad_kernel, dim3((unsigned)nseg, (unsigned)kmoe::ceil_div(d, 512)), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(x_sel), d, n, dlog, dlog_stride, seg, partial);
+  rc = kmoe::check_launch("kmoe_mod_bwd");
+  if (rc != KMOE_OK) return rc;
+  return kmoe_reduce_f32(partial, nseg, d, dw_mod, dw_dtype, stream);
 }

@@ -117,21 +117,30 @@ def _index_tensors(T: int, k: int, dev):
     return hit
 
 
-def _experts_core(dy, yperm, gu, slot_row, slot_w, kk, offsets, A, bw: BwdWeights, E, F, extra_rows=0):
-    """Expert-path backward shared by every layer form: from dy (T, d) through the combine
+def _experts_core(dy, yperm, gu, slot_row, slot_w, kk, offsets, A, bw: BwdWeights, E, F, extra_rows=0,
+                  row_index=None, scale=None):
+    """Expert-path backward shared by every layer form: from dy through the combine
     (routing-weight gradients dw (T, kk), dyperm), the down GEMM (dh), the SwiGLU and the
     gate/up GEMM (dgu, dxp rows [0, A)).  dxp has `extra_rows` more rows after the A
-    expert rows for the caller (the router's dx contribution).  Returns
-    (dxp, dw, dyperm, dgu)."""
-    T, d = dy.shape
+    expert rows for the caller (the router's dx contribution).  T = slot_row.shape[0];
+    token t's output row is dy[row_index[t]] (or dy[t]), scaled by scale[t] (or 1).
+    Returns (dxp, dw, dyperm, dgu, dscale) (dscale (T,): gradient of the scale, or None)."""
+    T = slot_row.shape[0]
+    d = dy.shape[1]
     Fp = _ru(F, 128)
     dev = dy.device
     s = ops._stream(dy)
     dyperm = torch.empty(max(A, 1), d, device=dev, dtype=_BF16)
     dw = torch.empty(T, kk, device=dev, dtype=torch.float32)
+    dscale = None
     with _stage("bwd_combine"):
-        _lib.call("kmoe_combine_bwd", ptr(dy), ptr(yperm), ptr(slot_row), ptr(slot_w), kk, d, T, ptr(dyperm), ptr(dw),
-                  s)
+        if row_index is None and scale is None:
+            _lib.call("kmoe_combine_bwd", ptr(dy), ptr(yperm), ptr(slot_row), ptr(slot_w), kk, d, T, ptr(dyperm),
+                      ptr(dw), s)
+        else:
+            dscale = torch.empty(T, device=dev, dtype=torch.float32) if scale is not None else None
+            _lib.call("kmoe_combine_bwd_rows", ptr(dy), ptr(yperm), ptr(slot_row), ptr(slot_w), kk, d, T,
+                      ptr(row_index), ptr(scale), ptr(dyperm), ptr(dw), ptr(dscale), s)
     dh = torch.empty(max(A, 1), Fp, device=dev, dtype=_BF16)
     with _stage("bwd_gemm_dh"):
         _lib.call("kmoe_gemm_grouped", ptr(dyperm), ptr(offsets), E, d, A, ptr(bw.w3n), _ru(F, 256), Fp,
@@ -143,7 +152,7 @@ def _experts_core(dy, yperm, gu, slot_row, slot_w, kk, offsets, A, bw: BwdWeight
     with _stage("bwd_gemm_dx"):
         _lib.call("kmoe_gemm_grouped", ptr(dgu), ptr(offsets), E, 2 * Fp, A, ptr(bw.w13t), _ru(d, 256), d,
                   ptr(dxp), d, d, s)
-    return dxp, dw, dyperm, dgu
+    return dxp, dw, dyperm, dgu, dscale
 
 
 def _expert_weight_grads(h, dyperm, xperm, dgu, offsets, A, E, d, F):
@@ -229,9 +238,11 @@ def _ones(T, fan, dev):
     return t
 
 
-def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], w_out: torch.Tensor,
-                 bw: BwdWeights, E: int, F: int, w_lb: float, w_z: float, need_weights: bool = True) -> Grads:
-    """All gradients of one token-choice MoE layer forward (bf16 compute)."""
+def _token_choice_core(sv: Saved, dy, grad_aux, w_out, bw: BwdWeights, E, F, w_lb, w_z, need_weights,
+                       extra_rows=0, row_index=None, scale=None):
+    """Expert path and router of a token-choice layer backward: dxp (A + T + extra_rows, d)
+    holds the expert rows' dx in [0, A) and the router's in [A, A + T); returns
+    (dxp, dscale, dw_in, dw_out, dyperm, dgu)."""
     x2d = sv.x2d
     T, d = x2d.shape
     k = sv.idx.shape[1]
@@ -239,25 +250,103 @@ def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], 
     dev = x2d.device
     s = ops._stream(x2d)
     disp = sv.disp
-    dy = dy.reshape(T, d).to(_BF16).contiguous()
-    _, _, _, _, extra = _index_tensors(T, k, dev)
-    # expert path; the router's dx contribution goes to rows [A, A + T) of dxp and one
-    # unit-weight gather sums both per token
-    dxp, dw, dyperm, dgu = _experts_core(dy, sv.yperm, sv.gu, disp.slot_row, disp.slot_w, k, disp.offsets, A, bw,
-                                         E, F, extra_rows=T)
+    dxp, dw, dyperm, dgu, dscale = _experts_core(dy, sv.yperm, sv.gu, disp.slot_row.view(T, k), disp.slot_w, k,
+                                                 disp.offsets, A, bw, E, F, extra_rows=T + extra_rows,
+                                                 row_index=row_index, scale=scale)
     # router: logit gradient (top-k renormalisation + aux), MLP backward, dx rows, dW_in
     dl = torch.empty(T, E, device=dev, dtype=torch.float32)
     ga = None if grad_aux is None else grad_aux.reshape(1).to(torch.float32).contiguous()
     with _stage("bwd_router"):
         _lib.call("kmoe_router_dlogits", ptr(sv.logits), T, E, ptr(sv.idx), ptr(sv.w), ptr(dw), k,
                   ptr(disp.counts), ptr(ga), float(w_lb), float(w_z), ptr(dl), s)
-    dw_in, dw_out = _router_core(x2d, sv.hidden, w_out, bw, dl, dxp[A:], need_weights)
+    dw_in, dw_out = _router_core(x2d, sv.hidden, w_out, bw, dl, dxp[A:A + T], need_weights)
+    return dxp, dscale, dw_in, dw_out, dyperm, dgu
+
+
+def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], w_out: torch.Tensor,
+                 bw: BwdWeights, E: int, F: int, w_lb: float, w_z: float, need_weights: bool = True) -> Grads:
+    """All gradients of one token-choice MoE layer forward (bf16 compute)."""
+    x2d = sv.x2d
+    T, d = x2d.shape
+    k = sv.idx.shape[1]
+    A = T * k
+    disp = sv.disp
+    dy = dy.reshape(T, d).to(_BF16).contiguous()
+    _, _, _, _, extra = _index_tensors(T, k, x2d.device)
+    # the router's dx contribution goes to rows [A, A + T) of dxp and one unit-weight
+    # gather sums both per token
+    dxp, _, dw_in, dw_out, dyperm, dgu = _token_choice_core(sv, dy, grad_aux, w_out, bw, E, F, w_lb, w_z,
+                                                            need_weights)
     src = torch.cat([disp.slot_row.view(T, k), extra], 1)
     dx = _gather_dx(dxp, src, T, d)
     if not need_weights:
         return Grads(dx, None, dw_out, None, None, None)
     dw1, dw2, dw3 = _expert_weight_grads(sv.h, dyperm, sv.xperm, dgu, disp.offsets, A, E, d, F)
     return Grads(dx, dw_in, dw_out, dw1, dw2, dw3)
+
+
+class ModGrads(NamedTuple):
+    dx: torch.Tensor          # (B*S, d) bf16: gradient of the MoD input (0 on unkept tokens)
+    dw_mod: Optional[torch.Tensor]
+    layer: Grads              # the inner layer's weight gradients (its dx field unused: None)
+
+
+def mod_backward(sv: Saved, sel: "ops.ModSelectOut", B: int, keep: int, dy: torch.Tensor,
+                 grad_aux: Optional[torch.Tensor], w_out, w_mod, bw: BwdWeights, E: int, F: int, w_lb: float,
+                 w_z: float, need_weights: bool = True) -> ModGrads:
+    """All gradients of the MoD composition of layers.py:148-184 (gather the kept rows,
+    MoE, weight by the MoD softmax, scatter) with the layer run on the kept rows sv.x2d
+    (B*keep, d).  dy (B*S, d) is the gradient of the scattered output.
+
+    One pass per stage: the combine backward reads dy at the kept rows and returns the
+    MoD weights' gradient; kmoe_mod_bwd turns it into the kept logits' gradient (written
+    into the dx gather's weight table) and dW_mod; one gather then writes the input
+    gradient of every token, sum of its expert rows, its router row and dlog * w_mod."""
+    x_sel = sv.x2d
+    T, d = x_sel.shape
+    k = sv.idx.shape[1]
+    A = T * k
+    T_out = dy.shape[0]
+    dev = x_sel.device
+    s = ops._stream(x_sel)
+    disp = sv.disp
+    dy = dy.to(_BF16).contiguous()
+    sel_w = sel.sel_w.reshape(-1)
+    dxp, dsel, dw_in, dw_out, dyperm, dgu = _token_choice_core(sv, dy, grad_aux, w_out, bw, E, F, w_lb, w_z,
+                                                               need_weights, extra_rows=1,
+                                                               row_index=sel.token_rows, scale=sel_w)
+    # gather table: the k expert rows and the router row with weight 1, w_mod with dlog
+    src, gw = _mod_tables(T, k, dev)
+    lib = _lib.load()
+    dw_mod = None
+    wsb = 0
+    if need_weights:
+        dw_mod = torch.empty(d, device=dev, dtype=w_mod.dtype if w_mod.dtype in (torch.float32, _BF16) else _BF16)
+        wsb = lib.kmoe_mod_bwd_workspace_bytes(T, d)
+    ws = torch.empty(max(wsb, 4), device=dev, dtype=torch.uint8)
+    with _stage("bwd_mod"):
+        _lib.call("kmoe_mod_bwd", ptr(sel_w), ptr(dsel), B, keep, ptr(x_sel), d, ptr(gw[:, k + 1:]), k + 2,
+                  ptr(dw_mod), _lib.DTYPE_F32 if dw_mod is not None and dw_mod.dtype == torch.float32
+                  else _lib.DTYPE_BF16, ptr(ws), wsb, s)
+        dxp[A + T].copy_(w_mod.detach().reshape(-1))
+    src[:, :k].copy_(disp.slot_row.view(T, k))
+    dx = ops.combine(dxp, src, gw, T_out, out_map=sel.out_map, out_dtype=_BF16)
+    if not need_weights:
+        return ModGrads(dx, None, Grads(None, None, dw_out, None, None, None))
+    dw1, dw2, dw3 = _expert_weight_grads(sv.h, dyperm, sv.xperm, dgu, disp.offsets, A, E, d, F)
+    return ModGrads(dx, dw_mod, Grads(None, dw_in, dw_out, dw1, dw2, dw3))
+
+
+def _mod_tables(T, k, dev):
+    """Fresh (src (T, k+2) int32, weights (T, k+2) f32) of the MoD dx gather: columns
+    k and k+1 of src hold the router row A + t and the w_mod row A + T (A = T k); the
+    weights are 1 except column k+1 (filled by kmoe_mod_bwd)."""
+    A = T * k
+    src = torch.empty(T, k + 2, device=dev, dtype=torch.int32)
+    src[:, k] = torch.arange(A, A + T, device=dev, dtype=torch.int32)
+    src[:, k + 1] = A + T
+    gw = torch.ones(T, k + 2, device=dev, dtype=torch.float32)
+    return src, gw
 
 
 class SavedEC(NamedTuple):
@@ -285,8 +374,8 @@ def ec_backward(sv: SavedEC, dy: torch.Tensor, grad_aux: Optional[torch.Tensor],
     dev = x2d.device
     s = ops._stream(x2d)
     dy = dy.reshape(T, d).to(_BF16).contiguous()
-    dxp, dw, dyperm, dgu = _experts_core(dy, sv.yperm, sv.gu, sel.src_row, sel.src_w, E, sel.offsets, A, bw, E, F,
-                                         extra_rows=T)
+    dxp, dw, dyperm, dgu, _ = _experts_core(dy, sv.yperm, sv.gu, sel.src_row, sel.src_w, E, sel.offsets, A, bw,
+                                            E, F, extra_rows=T)
     dl = torch.empty(T, E, device=dev, dtype=torch.float32)
     ga = None if grad_aux is None else grad_aux.reshape(1).to(torch.float32).contiguous()
     with _stage("bwd_router"):
@@ -311,7 +400,7 @@ def experts_backward(dy, yperm, gu, h, xperm, slot_row, slot_w, offsets, A, bw: 
     slot's routing weight, dw1, dw2, dw3)."""
     T, d = dy.shape
     kk = slot_row.shape[1]
-    dxp, dw, dyperm, dgu = _experts_core(dy, yperm, gu, slot_row, slot_w, kk, offsets, A, bw, E, F)
+    dxp, dw, dyperm, dgu, _ = _experts_core(dy, yperm, gu, slot_row, slot_w, kk, offsets, A, bw, E, F)
     dx = _gather_dx(dxp, slot_row, T, d)
     if not need_weights:
         return dx, dw, None, None, None

@@ -19,18 +19,29 @@ gradients, runs the whole expression on the layer's kernels with no extra pass:
   before the SiLU.  The normalised activations are never written.
 * The residual add happens in the combine (one f32 add before the one rounding).
 
-Other configurations (layernorm, expert choice, fp8, balanced routing, gradients
-wanted, active residual dropout) run the unfused composition: the reference's
-RMSNorm / LayerNorm in torch, the kmoe MoE layer (with its HIP backward where it
-has one) and a torch add.
+With gradients (training) and an RMSNorm, a token-choice bf16 layer and no active
+residual dropout, the block runs _BlockTrainFn: kmoe_rmsnorm writes the normalised
+rows once (the saved activation the weight gradients need; folding the norm weight
+into the expert weights would cost a re-fold of both weight packs every step), the
+layer's training forward (MoD-gated when the block has a MoD router and is in
+training mode, layers.py:148-177) adds the residual in its combine, and the backward
+is the layer's (or the MoD composition's) HIP backward followed by kmoe_rmsnorm_bwd,
+which also adds the residual's gradient.
+
+Other configurations (layernorm, expert choice, fp8, active residual dropout) run
+the unfused composition: the reference's RMSNorm / LayerNorm in torch, the kmoe MoE
+layer (MoD-gated in training mode, with its HIP backward where it has one) and a
+torch add.  The MoD router's auxiliary BCE loss is not part of this build.
 """
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 
+from . import backward as _bwd
 from . import ops
-from .moe import MoELayer
+from .mod import MoDRouter, mod_ffn
+from .moe import MoELayer, _once
 
 
 class RMSNorm(nn.Module):
@@ -67,6 +78,8 @@ class MoEFFNBlock(nn.Module):
         self.ffn_norm = get_norm_layer(config)
         # an existing MoE layer can be wrapped (its parameters are shared, not copied)
         self.ffn = ffn if ffn is not None else MoELayer(config, layer_idx)
+        # the MoD router of the FFN (layers.py:84-88), used in training mode only
+        self.ffn_mod_router = MoDRouter(config) if getattr(config, "mod_enabled", False) else None
         self.residual_dropout = nn.Dropout(getattr(config, "residual_dropout", 0.1))
         self.aux_loss = 0.0
         self._fused_cache = None
@@ -104,14 +117,38 @@ class MoEFFNBlock(nn.Module):
             self._fused_cache = (key, w_in_g, w_out_b, pw)
         return self._fused_cache[1:]
 
+    def _train_fusable(self, h: torch.Tensor) -> bool:
+        """Whether the forward records the fused training backward (_BlockTrainFn)."""
+        ffn = self.ffn
+        if not torch.is_grad_enabled():
+            return False
+        params = tuple(self.parameters())
+        if not (h.requires_grad or any(p.requires_grad for p in params)):
+            return False
+        if not isinstance(self.ffn_norm, RMSNorm) or ffn.routing_type == "expert_choice":
+            return False
+        if not ffn._trainable_experts() or (self.training and self.residual_dropout.p > 0):
+            return False
+        return h.dtype in (torch.bfloat16, torch.float32) and self.ffn_norm.weight.dtype in (torch.bfloat16,
+                                                                                               torch.float32)
+
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
-        if self._fusable(hidden_states):
+        use_mod = self.ffn_mod_router is not None and self.training
+        if self._train_fusable(hidden_states):
+            ffn, ge = self.ffn, self.ffn.grouped_experts
+            w_mod = self.ffn_mod_router.router.weight if use_mod else None
+            out, aux = _BlockTrainFn.apply(hidden_states, self.ffn_norm.weight, w_mod, ffn.router.router[0].weight,
+                                           ffn.router.router[2].weight, ge.w1, ge.w2, ge.w3, self, use_mod)
+            ffn.aux_loss = aux if ffn.training else 0.0
+            self.last_path = "fused_train"
+        elif not use_mod and self._fusable(hidden_states):
             out = self._forward_fused(hidden_states)
             self.last_path = "fused"
         else:
             residual = hidden_states
-            ffn_output = self.residual_dropout(self.ffn(self.ffn_norm(hidden_states)))
-            out = residual + ffn_output
+            xn = self.ffn_norm(hidden_states)
+            ffn_output = mod_ffn(self.ffn, self.ffn_mod_router, xn) if use_mod else self.ffn(xn)
+            out = residual + self.residual_dropout(ffn_output)
             self.last_path = "unfused"
         self.aux_loss = self.ffn.aux_loss if self.training else 0.0
         return out
@@ -139,3 +176,65 @@ class MoEFFNBlock(nn.Module):
                         residual=x2d)
         ffn._set_token_choice_aux(r, disp, T)
         return y.view(B, S, d)
+
+
+class _BlockTrainFn(torch.autograd.Function):
+    """out = h + MoE(RMSNorm(h)) (MoD-gated when use_mod, layers.py:142-187 without
+    residual dropout) with its backward on the HIP kernels.  Outputs (out, aux)."""
+
+    @staticmethod
+    def forward(ctx, h, g, w_mod, w_in, w_out, w1, w2, w3, blk, use_mod):
+        B, S, d = h.shape
+        T = B * S
+        ffn = blk.ffn
+        h2d = h.detach().reshape(T, d).contiguous()
+        n, rrms = ops.rmsnorm(h2d, g, blk.ffn_norm.eps)
+        out_dtype = torch.promote_types(h.dtype, g.dtype)
+        sel = None
+        keep = 0
+        if use_mod:
+            sel = blk.ffn_mod_router.select(n.view(B, S, d))
+            keep = sel.sel_idx.shape[1]
+            x_sel, _ = ops.gather_rows(n, sel.token_rows, B * keep)
+            y, aux, sv = ffn._train_forward(x_sel, B * keep, out_dtype, out_map=sel.out_map,
+                                            scale=sel.sel_w.reshape(-1), residual=h2d, T_out=T)
+        else:
+            y, aux, sv = ffn._train_forward(n, T, out_dtype, residual=h2d)
+        ctx.sv = (sv, sel, h2d, rrms)
+        ctx.blk = blk
+        ctx.meta = (B, S, d, keep, h.dtype, aux is not None, use_mod)
+        aux_t = aux if aux is not None else torch.zeros((), device=h.device, dtype=torch.float32)
+        return y.view(B, S, d), aux_t
+
+    @staticmethod
+    def backward(ctx, dy, daux):
+        sv, sel, h2d, rrms = _once(ctx)
+        blk = ctx.blk
+        B, S, d, keep, h_dtype, has_aux, use_mod = ctx.meta
+        T = B * S
+        ffn, ge = blk.ffn, blk.ffn.grouped_experts
+        w_in, w_out = ffn.router.router[0].weight, ffn.router.router[2].weight
+        g = blk.ffn_norm.weight
+        need_w = any(ctx.needs_input_grad[2:8])
+        dy2 = dy.reshape(T, d)
+        ga = daux if has_aux else None
+        dw_mod = None
+        if use_mod:
+            w_mod = blk.ffn_mod_router.router.weight
+            mg = _bwd.mod_backward(sv, sel, B, keep, dy2, ga, w_out, w_mod, ffn._bwd_weights(), ffn.n_experts,
+                                   ge.d_ff, ffn.load_balance_loss_weight, ffn.router_z_loss_weight,
+                                   need_weights=need_w)
+            dn, lg = mg.dx, mg.layer
+            if need_w:
+                dw_mod = mg.dw_mod.view_as(w_mod).to(w_mod.dtype)
+        else:
+            lg = _bwd.moe_backward(sv, dy2, ga, w_out, ffn._bwd_weights(), ffn.n_experts, ge.d_ff,
+                                   ffn.load_balance_loss_weight, ffn.router_z_loss_weight, need_weights=need_w)
+            dn = lg.dx
+        # the norm's backward, plus the residual's gradient dy
+        dh, dg = ops.rmsnorm_bwd(dn, h2d, g, rrms, dres=dy2)
+        dh = dh.view(B, S, d).to(h_dtype)
+        if not need_w:
+            return dh, dg, None, None, None, None, None, None, None, None
+        return (dh, dg, dw_mod, lg.dw_in.to(w_in.dtype), lg.dw_out.to(w_out.dtype), lg.dw1.to(ge.w1.dtype),
+                lg.dw2.to(ge.w2.dtype), lg.dw3.to(ge.w3.dtype), None, None)

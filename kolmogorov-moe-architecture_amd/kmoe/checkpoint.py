@@ -52,15 +52,14 @@ def layer_state_dict(model_sd: Dict[str, torch.Tensor], layer_idx: int, part: st
                      prefix: str = "layers.") -> Dict[str, torch.Tensor]:
     """Entries of block `layer_idx` for a kmoe module: part="ffn" gives the MoELayer's
     keys (``router.router.0.weight``, ``grouped_experts.w1``, ...), part="block" the
-    MoEFFNBlock's (``ffn_norm.weight`` and ``ffn.*``)."""
+    MoEFFNBlock's (``ffn_norm.weight``, ``ffn.*`` and, with MoD, ``ffn_mod_router.*``)."""
     base = f"{prefix}{layer_idx}."
     if part == "ffn":
         head = base + "ffn."
         out = {k[len(head):]: v for k, v in model_sd.items() if k.startswith(head)}
     elif part == "block":
         out = {k[len(base):]: v for k, v in model_sd.items()
-               if k.startswith(base + "ffn.") or k.startswith(base + "ffn_norm.")}
-        # the block's MoD router (ffn_mod_router.*) is not part of the FFN half
+               if k.startswith((base + "ffn.", base + "ffn_norm.", base + "ffn_mod_router."))}
     else:
         raise ValueError(f"kmoe.layer_state_dict: part must be 'ffn' or 'block', not {part!r}")
     if not out:

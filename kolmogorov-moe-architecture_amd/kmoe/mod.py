@@ -5,8 +5,14 @@ Linear(d,1) and the unused-here ``aux_router`` MLP).  MoDMoE is the FFN half of
 TransformerBlock.forward with MoD in training mode (layers.py:148-185):
 select the top ``int(S*cf)`` tokens per sequence, run the MoE on them, weight
 by the softmax over the kept router logits and scatter back, zeros elsewhere.
-Here the gather is fused into the router/dispatch reads (row indirection) and
-the weighted scatter into the combine, so no (B,k,d) copy is materialised.
+Without gradients the gather is fused into the router/dispatch reads (row
+indirection) and the weighted scatter into the combine, so no (B,k,d) copy is
+materialised.  With gradients (mod_ffn's training function) the kept rows are
+gathered once (they are the saved activation of the router's and the experts'
+weight gradients), the weighted scatter stays in the combine, and the backward
+runs on the HIP kernels: the combine backward reads dy at the kept rows and
+yields the MoD weights' gradient, kmoe_mod_bwd the kept logits' and W_mod's,
+and one gather writes the input gradient of every token.
 The MoD auxiliary BCE loss is out of scope.
 """
 from __future__ import annotations
@@ -16,9 +22,10 @@ from typing import Tuple
 import torch
 import torch.nn as nn
 
+from . import backward as _bwd
 from . import ops
 from .config import AdvancedMoEConfig
-from .moe import MoELayer, _forward_only
+from .moe import MoELayer, _forward_only, _once
 
 
 class MoDRouter(nn.Module):
@@ -54,6 +61,87 @@ class MoDRouter(nn.Module):
         return sel.sel_idx, sel.sel_w.to(dt), sel.logits.to(dt), sel.sel_idx
 
 
+class _MoDTrainFn(torch.autograd.Function):
+    """ffn_output (+ residual) of layers.py:148-187 for a normalised input x, with its
+    backward on the HIP kernels (mod_backward).  Outputs (y, aux)."""
+
+    @staticmethod
+    def forward(ctx, x, residual, w_mod, w_in, w_out, w1, w2, w3, ffn, mod_router):
+        B, S, d = x.shape
+        xb = x.detach().to(torch.bfloat16).contiguous()
+        sel = mod_router.select(xb)
+        keep = sel.sel_idx.shape[1]
+        T = B * keep
+        x_sel, _ = ops.gather_rows(xb.view(B * S, d), sel.token_rows, T)
+        out_dtype = torch.float32 if x.dtype == torch.float32 else torch.bfloat16
+        res2d = None if residual is None else residual.detach().reshape(B * S, d)
+        y, aux, sv = ffn._train_forward(x_sel, T, out_dtype, out_map=sel.out_map, scale=sel.sel_w.reshape(-1),
+                                        residual=res2d, T_out=B * S)
+        ctx.sv = (sv, sel)
+        ctx.mods = (ffn, mod_router)
+        ctx.meta = (B, S, d, keep, x.dtype, None if residual is None else residual.dtype, aux is not None)
+        aux_t = aux if aux is not None else torch.zeros((), device=x.device, dtype=torch.float32)
+        return y.view(B, S, d).to(x.dtype), aux_t
+
+    @staticmethod
+    def backward(ctx, dy, daux):
+        sv, sel = _once(ctx)
+        ffn, mod_router = ctx.mods
+        B, S, d, keep, x_dtype, r_dtype, has_aux = ctx.meta
+        ge = ffn.grouped_experts
+        w_in, w_out = ffn.router.router[0].weight, ffn.router.router[2].weight
+        w_mod = mod_router.router.weight
+        need_w = any(ctx.needs_input_grad[2:8])
+        g = _bwd.mod_backward(sv, sel, B, keep, dy.reshape(B * S, d), daux if has_aux else None, w_out, w_mod,
+                              ffn._bwd_weights(), ffn.n_experts, ge.d_ff, ffn.load_balance_loss_weight,
+                              ffn.router_z_loss_weight, need_weights=need_w)
+        dx = g.dx.view(B, S, d).to(x_dtype)
+        dres = None if r_dtype is None else dy.to(r_dtype)
+        if not need_w:
+            return dx, dres, None, None, None, None, None, None, None, None
+        lg = g.layer
+        return (dx, dres, g.dw_mod.view_as(w_mod).to(w_mod.dtype), lg.dw_in.to(w_in.dtype), lg.dw_out.to(w_out.dtype),
+                lg.dw1.to(ge.w1.dtype), lg.dw2.to(ge.w2.dtype), lg.dw3.to(ge.w3.dtype), None, None)
+
+
+def mod_trainable(ffn: MoELayer, mod_router: MoDRouter, *inputs) -> bool:
+    """Whether the MoD composition records a backward through the HIP kernels."""
+    if not torch.is_grad_enabled():
+        return False
+    params = tuple(ffn.parameters()) + (mod_router.router.weight,)
+    if not any(isinstance(t, torch.Tensor) and t.requires_grad for t in inputs + params):
+        return False
+    return ffn.routing_type != "expert_choice" and ffn._trainable_experts()
+
+
+def mod_ffn(ffn: MoELayer, mod_router: MoDRouter, hidden_states: torch.Tensor,
+            residual: torch.Tensor = None) -> torch.Tensor:
+    """ffn_output of layers.py:148-177 for the normalised input (residual + it with
+    `residual`), setting ffn.aux_loss; trains through the HIP backward when gradients
+    are wanted."""
+    B, S, d = hidden_states.shape
+    if ffn.routing_type == "expert_choice":
+        raise NotImplementedError("kmoe: Mixture-of-Depths around an expert-choice layer is not implemented")
+    if mod_trainable(ffn, mod_router, hidden_states, residual):
+        ge = ffn.grouped_experts
+        y, aux = _MoDTrainFn.apply(hidden_states, residual, mod_router.router.weight, ffn.router.router[0].weight,
+                                   ffn.router.router[2].weight, ge.w1, ge.w2, ge.w3, ffn, mod_router)
+        ffn.aux_loss = aux if ffn.training else 0.0
+        return y
+    x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
+    sel = mod_router.select(x)
+    keep = sel.sel_idx.shape[1]
+    out_dtype = torch.float32 if hidden_states.dtype == torch.float32 else torch.bfloat16
+    res2d = None if residual is None else residual.reshape(B * S, d)
+    y, r, disp = ffn.forward_rows(x.reshape(B * S, d), T=B * keep, row_index=sel.token_rows, T_out=B * S,
+                                  out_map=sel.out_map, scale=sel.sel_w.reshape(-1), out_dtype=out_dtype,
+                                  residual=res2d)
+    ffn._set_token_choice_aux(r, disp, B * keep)
+    ins = (hidden_states,) if residual is None else (hidden_states, residual)
+    return _forward_only(y.view(B, S, d).to(hidden_states.dtype), *ins, *ffn.parameters(),
+                         *mod_router.parameters())
+
+
 class MoDMoE(nn.Module):
     """MoD-gated MoE FFN: ffn_output of layers.py:148-185 for a normalised input."""
 
@@ -66,16 +154,6 @@ class MoDMoE(nn.Module):
     def forward(self, hidden_states: torch.Tensor, residual: torch.Tensor = None) -> torch.Tensor:
         """ffn_output; with `residual` (B, S, d), residual + ffn_output (layers.py:187) from the same
         combine: unselected tokens get the residual row, selected ones residual + weighted output."""
-        B, S, d = hidden_states.shape
-        x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
-        sel = self.ffn_mod_router.select(x)
-        keep = sel.sel_idx.shape[1]
-        out_dtype = torch.float32 if hidden_states.dtype == torch.float32 else torch.bfloat16
-        res2d = None if residual is None else residual.reshape(B * S, d)
-        y, r, disp = self.ffn.forward_rows(x.reshape(B * S, d), T=B * keep, row_index=sel.token_rows,
-                                           T_out=B * S, out_map=sel.out_map, scale=sel.sel_w.reshape(-1),
-                                           out_dtype=out_dtype, residual=res2d)
-        self.ffn._set_token_choice_aux(r, disp, B * keep)
+        y = mod_ffn(self.ffn, self.ffn_mod_router, hidden_states, residual)
         self.aux_loss = self.ffn.aux_loss
-        ins = (hidden_states,) if residual is None else (hidden_states, residual)
-        return _forward_only(y.view(B, S, d).to(hidden_states.dtype), *ins, *self.parameters())
+        return y

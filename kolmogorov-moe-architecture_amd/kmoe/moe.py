@@ -15,8 +15,9 @@ Backward (bf16 weights and activations) runs on the HIP backward kernels
 (kmoe.backward) for: the token-choice MoELayer (top-k routing, optional capacity
 drop), the expert-choice MoELayer, and Router / ExpertChoiceRouter /
 GroupedExperts / GroupedExpertsExpertChoice called on their own (the reference's
-distillation code trains them so, distill.py:289-314).  fp8 experts and balanced
-routing are forward-only and raise in backward.
+distillation code trains them so, distill.py:289-314), balanced routing included (its
+weights' backward is the top-k renormalisation's, without the + 1e-9 of moe.py:411,
+a relative difference below 1e-8).  fp8 experts are forward-only and raise in backward.
 """
 from __future__ import annotations
 
@@ -120,29 +121,23 @@ class Router(_RouterMLP):
                 self.logit_bias = self.logit_bias.to(x2d.device)
             bias = self.logit_bias
         if self.balanced_routing:
-            if save_hidden:
-                raise NotImplementedError("kmoe: backward through balanced routing is not implemented")
-            r = ops.router(x2d, w_in, w_out, 0, bias=bias, row_index=row_index, T=T)
+            r = ops.router(x2d, w_in, w_out, 0, bias=bias, row_index=row_index, T=T, save_hidden=save_hidden)
             idx, w = ops.balanced_topk(r.logits, self.top_k)
-            return ops.RouterOut(r.logits, idx, w, r.partials)
+            return ops.RouterOut(r.logits, idx, w, r.partials, r.hidden)
         return ops.router(x2d, w_in, w_out, self.top_k, bias=bias, row_index=row_index, T=T, save_hidden=save_hidden,
                           hist=hist)
 
     def forward(self, hidden_states: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         B, S, d = hidden_states.shape
         dt = hidden_states.dtype
-        if self._trainable(hidden_states) and not self.balanced_routing:
+        if self._trainable(hidden_states):
             w, idx, logits = _RouterFn.apply(hidden_states.reshape(B * S, d), self.router[0].weight,
                                              self.router[2].weight, self)
             return (w.view(B, S, self.top_k).to(dt), idx.view(B, S, self.top_k),
                     logits.view(B, S, self.n_experts).to(dt))
         r = self.route(hidden_states.reshape(B * S, d), hist=False)
-        out = (r.w.view(B, S, self.top_k).to(dt), r.idx.view(B, S, self.top_k),
-               r.logits.view(B, S, self.n_experts).to(dt))
-        if torch.is_grad_enabled() and self.balanced_routing:
-            return (_forward_only(out[0], hidden_states, *self.parameters()), out[1],
-                    _forward_only(out[2], hidden_states, *self.parameters()))
-        return out
+        return (r.w.view(B, S, self.top_k).to(dt), r.idx.view(B, S, self.top_k),
+                r.logits.view(B, S, self.n_experts).to(dt))
 
 
 class ExpertChoiceRouter(_RouterMLP):
@@ -589,9 +584,13 @@ class MoELayer(nn.Module):
             return False
         if not (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
+        return self._trainable_experts()
+
+    def _trainable_experts(self) -> bool:
+        """Whether the experts have a HIP backward: bf16 weights in the GEMMs (not fp8) and
+        d_ff_expert a multiple of 8 (the weight-gradient stores write rows of 8 bf16)."""
         ge = self.grouped_experts if self.grouped_experts is not None else self.grouped_experts_ec
-        # the weight-gradient stores write rows of 8 bf16 (d_ff_expert a multiple of 8)
-        return not (ge.use_fp8 or getattr(self.router, "balanced_routing", False) or ge.d_ff % 8)
+        return not (ge.use_fp8 or ge.d_ff % 8)
 
     def _bwd_weights(self) -> _bwd.BwdWeights:
         """Backward packed weights, rebuilt only when a parameter changed."""
@@ -605,8 +604,10 @@ class MoELayer(nn.Module):
             self._bwd_cache = cache
         return cache[1]
 
-    def _train_forward(self, x2d, T, out_dtype):
-        """Token-choice forward keeping what the backward needs: (y, aux or None, Saved)."""
+    def _train_forward(self, x2d, T, out_dtype, out_map=None, scale=None, residual=None, T_out=None):
+        """Token-choice forward keeping what the backward needs: (y, aux or None, Saved).
+        out_map / scale / residual / T_out go to the combine (the MoD scatter and the
+        block's residual add): y[o] = residual[o] + scale[t] * MoE(x)[t] for t = out_map[o]."""
         r = self.router.route(x2d, T=T, save_hidden=True)
         ge = self.grouped_experts
         k, E = self.top_k, self.n_experts
@@ -617,7 +618,8 @@ class MoELayer(nn.Module):
         disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=True, block_counts=r.block_counts)
         h, gu = ops.gemm_gate_up_rows(x2d, None, disp.row_token, disp.offsets, pw, T * k, save_gu=True)
         yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
-        y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T, out_dtype=out_dtype)
+        y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T if T_out is None else T_out,
+                        out_map=out_map, scale=scale, out_dtype=out_dtype, residual=residual)
         self.last_expert_counts = disp.counts
         aux = None
         if self.training:

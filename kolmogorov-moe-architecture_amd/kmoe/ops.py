@@ -426,3 +426,50 @@ def mod_select(x3d, w_mod, keep) -> ModSelectOut:
         _lib.call("kmoe_mod_select", ptr(x3d), B, S, d, ptr(w_mod), keep, ptr(logits), ptr(sel_idx), ptr(sel_w),
               ptr(token_rows), ptr(out_map), None, 0, _stream(x3d))
     return ModSelectOut(logits, sel_idx, sel_w, token_rows, out_map)
+
+
+def _fdt(t):
+    if t.dtype == torch.float32:
+        return _lib.DTYPE_F32
+    if t.dtype == _BF16:
+        return _lib.DTYPE_BF16
+    raise ValueError(f"kmoe: unsupported dtype {t.dtype}")
+
+
+def rmsnorm(x2d, weight, eps):
+    """RMSNorm (embeddings.py:167-195) of the rows of x2d (bf16 or f32) with weight (d,):
+    (n (T, d) bf16, rrms (T,) f32 = 1/sqrt(mean(x^2) + eps))."""
+    _need_gpu(x2d, weight)
+    if x2d.dtype not in (torch.float32, _BF16):
+        x2d = x2d.float()
+    x2d = x2d.contiguous()
+    weight = weight.detach()
+    if weight.dtype not in (torch.float32, _BF16):
+        weight = weight.float()
+    weight = weight.contiguous()
+    T, d = x2d.shape
+    n = torch.empty(T, d, device=x2d.device, dtype=_BF16)
+    rrms = torch.empty(T, device=x2d.device, dtype=torch.float32)
+    with _Stage("rmsnorm"):
+        _lib.call("kmoe_rmsnorm", ptr(x2d), _fdt(x2d), ptr(weight), _fdt(weight), float(eps), T, d, ptr(n), ptr(rrms),
+                  _stream(x2d))
+    return n, rrms
+
+
+def rmsnorm_bwd(dn, x2d, weight, rrms, dres=None, dw_dtype=None):
+    """Backward of rmsnorm: (dx in x2d's dtype (+ dres), dweight (d,))."""
+    T, d = x2d.shape
+    dn = _contig(dn, _BF16)
+    weight = weight.detach().contiguous()
+    if dres is not None:
+        dres = _contig(dres, x2d.dtype)
+    dw_dtype = weight.dtype if dw_dtype is None else dw_dtype
+    dx = torch.empty(T, d, device=x2d.device, dtype=x2d.dtype)
+    dwt = torch.empty(d, device=x2d.device, dtype=dw_dtype)
+    lib = _lib.load()
+    wsb = lib.kmoe_rmsnorm_bwd_workspace_bytes(T, d)
+    ws = torch.empty(max(wsb, 4), device=x2d.device, dtype=torch.uint8)
+    with _Stage("bwd_rmsnorm"):
+        _lib.call("kmoe_rmsnorm_bwd", ptr(dn), ptr(x2d), _fdt(x2d), ptr(weight), _fdt(weight), ptr(rrms), ptr(dres), T,
+                  d, ptr(dx), ptr(dwt), _fdt(dwt), ptr(ws), wsb, _stream(x2d))
+    return dx, dwt

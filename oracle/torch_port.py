@@ -108,6 +108,12 @@ def moe_loss_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, dy, capacity=0, bias=N
     routing the layer is smooth, so the gradients of this loss are the reference's
     backward.  capacity > 0 keeps the first `capacity` assignments of each expert in
     assignment order (the build's drop rule); bias (E,) is added to the logits."""
+    y, aux = moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity, bias, training, w_lb, w_z)
+    return (y * dy).sum() + aux
+
+
+def moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity=0, bias=None, training=True, w_lb=0.01, w_z=0.001):
+    """(y, aux) of moe_loss_tc_routed's layer (aux 0 when not training)."""
     T, d = x2d.shape
     k = idx.shape[1]
     E = w1.shape[0]
@@ -135,13 +141,53 @@ def moe_loss_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, dy, capacity=0, bias=N
         h = F.silu(torch.bmm(padded, w1)) * torch.bmm(padded, w2)
         out = torch.bmm(h, w3)
         y = y.index_add(0, s_tok, out[s_e, pos] * s_w.unsqueeze(1))
-    loss = (y * dy).sum()
+    aux = x2d.new_zeros(())
     if training:
         f = counts.to(x2d.dtype) / (T * k)
         lb = E * (f * probs.mean(dim=0)).sum()
         z = (torch.logsumexp(logits, dim=-1) ** 2).mean()
-        loss = loss + w_lb * lb + w_z * z
-    return loss
+        aux = w_lb * lb + w_z * z
+    return y, aux
+
+
+def ffn_half_loss_routed(h3d, w_in, w_out, w1, w2, w3, idx, dy, norm_w=None, eps=1e-5, w_mod=None, sel_idx=None,
+                         residual=None, capacity=0, training=True, w_lb=0.01, w_z=0.001, return_out=False):
+    """Scalar loss sum(out * dy) (+ the MoE aux in training) of the FFN half of
+    TransformerBlock.forward (layers.py:142-187, no residual dropout) at a fixed MoD
+    selection and routing:
+      x = RMSNorm(h) (embeddings.py:182-195) when norm_w is given, else h
+      MoD (w_mod and sel_idx (B, keep) ascending given; layers.py:148-184): router
+        logits x . w_mod (mod.py:93), the kept logits in ascending token order
+        (mod.py:100-109), their softmax (mod.py:112); gather the kept rows
+        (layers.py:160-165), the MoE on them with routing idx (B*keep, k), weight by
+        the softmax (layers.py:175), scatter_add_ into zeros (layers.py:180-184)
+      no MoD: the MoE on all rows with routing idx (B*S, k)
+      out = h + ffn_output with a norm (layers.py:187), else residual + ffn_output
+        (residual optional).
+    At a fixed selection and routing the composition is smooth: autograd of this loss
+    is the reference's backward.  return_out: (loss, out)."""
+    B, S, d = h3d.shape
+    x = h3d
+    if norm_w is not None:
+        rms = torch.sqrt(torch.mean(h3d ** 2, dim=-1, keepdim=True) + eps)
+        x = norm_w * (h3d / rms)
+    if w_mod is not None:
+        keep = sel_idx.shape[1]
+        r = (x @ w_mod.reshape(-1, 1)).squeeze(-1)
+        p = F.softmax(r.gather(1, sel_idx), dim=-1)
+        gidx = sel_idx.unsqueeze(-1).expand(-1, -1, d)
+        xs = torch.gather(x, 1, gidx)
+        y, aux = moe_tc_routed(xs.reshape(B * keep, d), w_in, w_out, w1, w2, w3, idx, capacity, None, training,
+                               w_lb, w_z)
+        ffn_out = torch.zeros_like(x).scatter_add(1, gidx, p.unsqueeze(-1) * y.view(B, keep, d))
+    else:
+        y, aux = moe_tc_routed(x.reshape(B * S, d), w_in, w_out, w1, w2, w3, idx, capacity, None, training, w_lb,
+                               w_z)
+        ffn_out = y.view(B, S, d)
+    base = h3d if norm_w is not None else residual
+    out = ffn_out if base is None else base + ffn_out
+    loss = (out * dy).sum() + aux
+    return (loss, out) if return_out else loss
 
 
 def grouped_experts_ec_tc(x3d, ew, ti, w1, w2, w3):

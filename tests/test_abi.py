@@ -134,3 +134,27 @@ def test_counted_dispatch_and_router_hist_validation(lib):
     rc, msg = _err(lib, "kmoe_router_hist", FAKE, NULL, 16, 64, FAKE, FAKE, 8, NULL, 2, FAKE, FAKE, FAKE, NULL, NULL,
                    NULL, NULL)
     assert rc == -1 and "block_counts" in msg
+
+
+def test_norm_and_mod_backward_validation(lib):
+    """Argument checks of the block / MoD training entry points (no launch on failure)."""
+    BF, F32 = _lib.DTYPE_BF16, _lib.DTYPE_F32
+    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, NULL, F32, 1e-5, 16, 64, FAKE, FAKE, NULL)[0] == -1
+    assert _err(lib, "kmoe_rmsnorm", FAKE, 7, FAKE, F32, 1e-5, 16, 64, FAKE, FAKE, NULL)[0] == -3
+    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, FAKE, F32, 1e-5, 16, 60, FAKE, FAKE, NULL)[0] == -2
+    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, FAKE, F32, 1e-5, 16, 8200, FAKE, FAKE, NULL)[0] == -6
+    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, FAKE, F32, -1.0, 16, 64, FAKE, FAKE, NULL)[0] == -2
+    need = lib.kmoe_rmsnorm_bwd_workspace_bytes(5000, 64)
+    assert need == -(-5000 // 8) * 64 * 4  # 8-row segments (at most 1024 of them)
+    rc, msg = _err(lib, "kmoe_rmsnorm_bwd", FAKE, FAKE, BF, FAKE, F32, FAKE, NULL, 5000, 64, FAKE, FAKE, BF, FAKE,
+                   need - 4, NULL)
+    assert rc == -4 and "workspace" in msg
+    assert _err(lib, "kmoe_rmsnorm_bwd", FAKE, FAKE, BF, FAKE, F32, NULL, NULL, 16, 64, FAKE, FAKE, BF, FAKE, 1 << 20,
+                NULL)[0] == -1
+    assert _err(lib, "kmoe_mod_bwd", NULL, FAKE, 2, 8, FAKE, 64, FAKE, 1, NULL, BF, NULL, 0, NULL)[0] == -1
+    assert _err(lib, "kmoe_mod_bwd", FAKE, FAKE, 0, 8, FAKE, 64, FAKE, 1, NULL, BF, NULL, 0, NULL)[0] == -2
+    assert lib.kmoe_mod_bwd_workspace_bytes(1000, 64) == -(-1000 // 4) * 64 * 4
+    assert _err(lib, "kmoe_combine_bwd_rows", FAKE, FAKE, FAKE, FAKE, 2, 12, 16, NULL, NULL, FAKE, FAKE, NULL,
+                NULL)[0] == -2
+    assert _err(lib, "kmoe_combine_bwd_rows", FAKE, FAKE, NULL, FAKE, 2, 64, 16, NULL, NULL, FAKE, FAKE, NULL,
+                NULL)[0] == -1

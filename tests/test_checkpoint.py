@@ -21,7 +21,7 @@ def _model_sd(cfg, n_layers=3):
         for k, v in blk.state_dict().items():
             sd[f"layers.{i}.{k}"] = v.clone()
         sd[f"layers.{i}.seq_norm.weight"] = torch.ones(cfg.d_model)
-        sd[f"layers.{i}.ffn_mod_router.router.0.weight"] = torch.randn(4, cfg.d_model)
+        sd[f"layers.{i}.seq_layer.q_proj.weight"] = torch.randn(4, cfg.d_model)
     return sd
 
 
@@ -35,6 +35,11 @@ def test_layer_state_dict_loads_strict():
     b.load_state_dict(C.layer_state_dict(sd, 2, part="block"), strict=True)
     assert torch.equal(b.ffn_norm.weight, sd["layers.2.ffn_norm.weight"])
     assert torch.equal(b.ffn.router.router[0].weight, sd["layers.2.ffn.router.router.0.weight"])
+    assert torch.equal(b.ffn_mod_router.router.weight, sd["layers.2.ffn_mod_router.router.weight"])
+    # a block without MoD takes the FFN half alone
+    nomod = AdvancedMoEConfig(d_model=64, n_experts=4, d_ff_expert=96, mod_enabled=False)
+    sd2 = {k: v for k, v in sd.items() if ".ffn_mod_router." not in k}
+    kmoe.MoEFFNBlock(nomod, 2).load_state_dict(C.layer_state_dict(sd2, 2, part="block"), strict=True)
     with pytest.raises(KeyError):
         C.layer_state_dict(sd, 7)
 

@@ -263,3 +263,47 @@ def test_second_backward_raises(dev):
     loss.backward(retain_graph=True)
     with pytest.raises(RuntimeError, match="once per forward"):
         loss.backward()
+
+
+def test_backward_balanced_routing(dev):
+    """Balanced routing (moe.py:353-421) trains through the same kernels: the gradients at
+    the balanced picks match fp64 autograd of the routed restatement."""
+    print("backward balanced routing", flush=True)
+    B, S, d, E, k, F = 2, 256, 256, 8, 2, 512
+    cfg = AdvancedMoEConfig(d_model=d, n_experts=E, moe_top_k=k, d_ff_expert=F, moe_balanced_routing=True)
+    layer = MoELayer(cfg, 0).to(dev, torch.bfloat16).train()
+    g = torch.Generator().manual_seed(17)
+    with torch.no_grad():
+        layer.router.router[0].weight.copy_(torch.randn(128, d, generator=g) * 0.05)
+        w_out = torch.randn(E, 128, generator=g) * 0.05
+        # experts 0 and 1 are every token's top two, each the first choice of about half
+        # the tokens: both fill up in the first round, so the second round moves picks
+        v = torch.randn(128, generator=g) * 0.2
+        w_out[0] += 0.3 + v
+        w_out[1] += 0.3 - v
+        layer.router.router[2].weight.copy_(w_out)
+        for w in (layer.grouped_experts.w1, layer.grouped_experts.w2, layer.grouped_experts.w3):
+            w.copy_(torch.randn(w.shape, generator=g) * 0.05)
+    x = torch.randn(B, S, d, generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
+    dy = torch.randn(B, S, d, generator=g).to(torch.bfloat16)
+    y = layer(x)
+    ((y.float() * dy.to(dev).float()).sum() + layer.aux_loss).backward()
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        r = layer.router.route(x.detach().reshape(B * S, d))
+    idx = r.idx.cpu()
+    f64 = lambda t: t.detach().double().cpu().clone().requires_grad_(True)
+    ge = layer.grouped_experts
+    params = [f64(layer.router.router[0].weight), f64(layer.router.router[2].weight), f64(ge.w1), f64(ge.w2),
+              f64(ge.w3)]
+    xr = f64(x.reshape(B * S, d))
+    ref = P.moe_loss_tc_routed(xr, *params, idx, dy.reshape(B * S, d).double(), training=True,
+                               w_lb=layer.load_balance_loss_weight, w_z=layer.router_z_loss_weight)
+    ref.backward()
+    got = [x.grad.reshape(B * S, d), layer.router.router[0].weight.grad, layer.router.router[2].weight.grad,
+           ge.w1.grad, ge.w2.grad, ge.w3.grad]
+    want = [xr.grad] + [p.grad for p in params]
+    errs = {n: _rel(a, b) for n, a, b in zip(["dx", "dw_in", "dw_out", "dw1", "dw2", "dw3"], got, want)}
+    plain = torch.topk(r.logits, k, dim=1).indices.cpu()
+    assert (plain.sort(1).values != idx.sort(1).values).any(), "the capacity rule must have moved some picks"
+    _check(errs)

@@ -11,13 +11,11 @@ bf16 ulp of the fp64 sum (f32 out: 1e-5 rel)."""
 import numpy as np
 import pytest
 import torch
-import torch.nn.functional as F
 
 from kmoe import ops
 from kmoe.block import MoEFFNBlock
 from kmoe.config import AdvancedMoEConfig
 from oracle import moe_oracle as O
-from oracle import torch_port as P
 
 pytestmark = pytest.mark.gpu
 
@@ -227,43 +225,6 @@ def test_ffn_block_fused_vs_unfused(dev):
     a = npf(out_f.reshape(-1, 256))[same] - hr[same]
     b = npf(out_u.reshape(-1, 256))[same] - hr[same]
     assert relL2(a, b) <= 2e-2
-
-
-def test_ffn_block_training_path(dev):
-    """With gradients the block runs the unfused composition: its backward (torch
-    RMSNorm autograd, the kmoe layer's HIP backward) against fp64 autograd of
-    h + MoE(RMSNorm(h)) at the kernel's routing."""
-    print("ffn_block training", flush=True)
-    d, E, k, Fd = 256, 8, 2, 352
-    blk, g = _block(dev, d, E, k, Fd, 250, torch.float32)
-    blk.ffn.train()
-    blk.train()
-    blk.residual_dropout.p = 0.0
-    h = bf(torch.randn(2, 256, d, generator=g)).to(dev).requires_grad_(True)
-    dy = torch.randn(2, 256, d, generator=g)
-    out = blk(h)
-    assert blk.last_path == "unfused"
-    loss = (out.float() * dy.to(dev)).sum() + blk.aux_loss
-    loss.backward()
-    torch.cuda.synchronize()
-    T = 512
-    with torch.no_grad():
-        xn = blk.ffn_norm(h.detach()).to(torch.bfloat16).reshape(T, d)
-        idx = blk.ffn.router.route(xn).idx.cpu()
-    f64 = lambda t: t.detach().double().cpu().clone().requires_grad_(True)
-    ffn, ge = blk.ffn, blk.ffn.grouped_experts
-    h64, nw64 = f64(h.reshape(T, d)), f64(blk.ffn_norm.weight)
-    params = [f64(ffn.router.router[0].weight), f64(ffn.router.router[2].weight), f64(ge.w1), f64(ge.w2),
-              f64(ge.w3)]
-    dy64 = dy.reshape(T, d).double()
-    ref = P.moe_loss_tc_routed(F.rms_norm(h64, (d,), nw64, eps=blk.ffn_norm.eps), *params, idx, dy64,
-                               training=True, w_lb=ffn.load_balance_loss_weight, w_z=ffn.router_z_loss_weight)
-    ref = ref + (h64 * dy64).sum()
-    ref.backward()
-    assert relL2(npf(h.grad.reshape(T, d)), h64.grad.numpy()) <= 1e-2
-    assert relL2(npf(blk.ffn_norm.weight.grad), nw64.grad.numpy()) <= 2e-2
-    for got, want in zip((ge.w1.grad, ge.w2.grad, ge.w3.grad), params[2:]):
-        assert relL2(npf(got), want.grad.numpy()) <= 2e-2
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

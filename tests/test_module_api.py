@@ -77,8 +77,13 @@ def test_ffn_block_keys_and_norm():
     assert (cfg.norm_type, cfg.norm_eps, cfg.residual_dropout) == ("rmsnorm", 1e-5, 0.1)
     blk = kmoe.MoEFFNBlock(cfg, 0)
     keys = set(blk.state_dict())
-    assert {"ffn_norm.weight", "ffn.router.router.0.weight", "ffn.router.router.2.weight",
-            "ffn.grouped_experts.w1", "ffn.grouped_experts.w2", "ffn.grouped_experts.w3"} == keys
+    ffn_keys = {"ffn_norm.weight", "ffn.router.router.0.weight", "ffn.router.router.2.weight",
+                "ffn.grouped_experts.w1", "ffn.grouped_experts.w2", "ffn.grouped_experts.w3"}
+    # mod_enabled (the reference's default) adds the FFN's MoD router (layers.py:84-88)
+    assert ffn_keys | {"ffn_mod_router.router.weight", "ffn_mod_router.aux_router.0.weight",
+                       "ffn_mod_router.aux_router.2.weight"} == keys
+    nomod = kmoe.MoEFFNBlock(AdvancedMoEConfig(d_model=256, n_experts=8, d_ff_expert=512, mod_enabled=False), 0)
+    assert set(nomod.state_dict()) == ffn_keys and nomod.ffn_mod_router is None
     x = torch.randn(3, 5, 256, dtype=torch.float64)
     blk.ffn_norm.weight.data = torch.rand(256) + 0.5
     ref = torch.nn.functional.rms_norm(x, (256,), blk.ffn_norm.weight.double(), eps=1e-5)

@@ -653,3 +653,65 @@ def test_router_loss_routed_gradcheck_and_forward():
     assert abs(ref - got) < 1e-12  # at its own routing: Router.forward's (w, logits)
     f = lambda *a: P.router_loss_routed(*a, idx[0], gw, gl)
     assert torch.autograd.gradcheck(f, (x, w_in, w_out), eps=1e-6, atol=1e-6, rtol=1e-5)
+
+
+def _tiny_ffn_half(seed=21):
+    g = torch.Generator().manual_seed(seed)
+    B, S, d, E, k, F_ = 2, 10, 8, 4, 2, 6
+    r = lambda *s, sc=1.0: (torch.randn(*s, generator=g, dtype=torch.float64) * sc)
+    return dict(h=r(B, S, d), w_in=r(128, d, sc=0.3), w_out=r(E, 128, sc=0.3), w1=r(E, d, F_, sc=0.4),
+                w2=r(E, d, F_, sc=0.4), w3=r(E, F_, d, sc=0.4), nw=1.0 + 0.2 * r(d), w_mod=r(1, d, sc=0.5),
+                dy=r(B, S, d), k=k, keep=7)
+
+
+@pytest.mark.parametrize("with_norm", [False, True])
+def test_ffn_half_loss_matches_numpy_composition(with_norm):
+    """ffn_half_loss_routed (the torch restatement of layers.py:142-187 with MoD) against
+    the numpy oracle's own pieces: rms_norm, mod_logits / mod_select (argsort-based),
+    moe_forward_tc (routing from its own logits) and an explicit scatter of the weighted
+    rows; the loss is sum(out * dy) + the MoE aux on the kept tokens."""
+    c = _tiny_ffn_half()
+    B, S, d = c["h"].shape
+    k, keep = c["k"], c["keep"]
+    h = c["h"].numpy()
+    x = O.rms_norm(h, c["nw"].numpy(), 1e-5) if with_norm else h
+    r = O.mod_logits(x, c["w_mod"].numpy())
+    sel, sw = O.mod_select(r, keep)
+    rows = np.concatenate([x[b, sel[b]] for b in range(B)])
+    ref = O.moe_forward_tc(rows, c["w_in"].numpy(), c["w_out"].numpy(), c["w1"].numpy(), c["w2"].numpy(),
+                           c["w3"].numpy(), k, dtype=np.float64)
+    out = np.zeros_like(x)
+    for b in range(B):
+        out[b, sel[b]] = sw[b][:, None] * ref["y"][b * keep:(b + 1) * keep]
+    base = h if with_norm else 0.0
+    want = float(((base + out) * c["dy"].numpy()).sum() + ref["aux"][0])
+    got = float(P.ffn_half_loss_routed(c["h"], c["w_in"], c["w_out"], c["w1"], c["w2"], c["w3"],
+                                       torch.from_numpy(ref["idx"]), c["dy"], norm_w=c["nw"] if with_norm else None,
+                                       w_mod=c["w_mod"], sel_idx=torch.from_numpy(sel)))
+    assert abs(got - want) <= 1e-10 * max(1.0, abs(want))
+    # without MoD: h + MoE(RMSNorm(h)) of ffn_block_tc
+    if with_norm:
+        blk = O.ffn_block_tc(h.reshape(-1, d), c["nw"].numpy(), 1e-5, c["w_in"].numpy(), c["w_out"].numpy(),
+                             c["w1"].numpy(), c["w2"].numpy(), c["w3"].numpy(), k)
+        want2 = float((blk["y"] * c["dy"].numpy().reshape(-1, d)).sum() + blk["aux"][0])
+        got2 = float(P.ffn_half_loss_routed(c["h"], c["w_in"], c["w_out"], c["w1"], c["w2"], c["w3"],
+                                            torch.from_numpy(blk["idx"]), c["dy"], norm_w=c["nw"]))
+        assert abs(got2 - want2) <= 1e-10 * max(1.0, abs(want2))
+
+
+def test_ffn_half_loss_gradcheck():
+    """Finite differences of the MoD + norm composition at a fixed selection and routing
+    (the gradients the GPU backward is compared with)."""
+    c = _tiny_ffn_half(22)
+    B, S, d = c["h"].shape
+    x = O.rms_norm(c["h"].numpy(), c["nw"].numpy(), 1e-5)
+    sel, _ = O.mod_select(O.mod_logits(x, c["w_mod"].numpy()), c["keep"])
+    rows = np.concatenate([x[b, sel[b]] for b in range(B)])
+    idx = O.moe_forward_tc(rows, c["w_in"].numpy(), c["w_out"].numpy(), c["w1"].numpy(), c["w2"].numpy(),
+                           c["w3"].numpy(), c["k"], dtype=np.float64)["idx"]
+    ins = [c[n].clone().requires_grad_(True) for n in ("h", "nw", "w_mod", "w_in", "w_out", "w1", "w2", "w3")]
+
+    def f(h, nw, w_mod, w_in, w_out, w1, w2, w3):
+        return P.ffn_half_loss_routed(h, w_in, w_out, w1, w2, w3, torch.from_numpy(idx), c["dy"], norm_w=nw,
+                                      w_mod=w_mod, sel_idx=torch.from_numpy(sel))
+    assert torch.autograd.gradcheck(f, ins, eps=1e-6, atol=1e-5, rtol=1e-4)
