@@ -256,6 +256,7 @@ def run_block(args, wl, layer, x):
         ops.set_stage_timing(None)
     assert blk.last_path == "fused"
     layer.train()
+    training = run_block_training(args, wl, layer, x, blk.ffn_norm.weight)
     per = {}
     for name, a, b in events:
         per.setdefault(name, []).append(a.elapsed_time(b) * 1e3)
@@ -264,9 +265,83 @@ def run_block(args, wl, layer, x):
             "fused_tokens_per_s": round(wl.T / (ms["fused"] * 1e-3), 1),
             "unfused_tokens_per_s": round(wl.T / (ms["unfused"] * 1e-3), 1),
             "saved_us": round((ms["unfused"] - ms["fused"]) * 1e3, 1), "steps": steps,
-            "fused_stages_us": stages,
+            "fused_stages_us": stages, "training": training,
             "note": "h + MoE(RMSNorm(h)), eval, bf16 norm weight; unfused = torch RMSNorm (embeddings.py:190-195) "
                     "+ kmoe layer + torch add"}
+
+
+def run_block_training(args, wl, layer, x, norm_w):
+    """Training steps of the FFN half of the block through autograd (forward, then
+    backward of sum(out * dy) + aux to h and every parameter), in training mode with
+    residual dropout 0: with the MoD router (the reference's default mod_enabled,
+    layers.py:148-185) and without.  Gradients are set to None before each step (as an
+    optimizer's zero_grad does); the parameters do not change, so the packed weights
+    stay cached (with_repack: new parameter versions every step, as after an update)."""
+    import dataclasses
+
+    import torch
+    from kmoe import ops
+    from kmoe.block import MoEFFNBlock
+
+    out = {}
+    g = torch.Generator().manual_seed(wl.seed + 300)
+    dy = torch.randn(wl.B, wl.S, wl.d, generator=g).to(torch.bfloat16).to(x.device)
+    h = x.detach().clone().requires_grad_(True)
+    one = torch.ones((), device=x.device)
+    steps = max(1, args.steps // 5)
+    for mod in (True, False):
+        cfg = dataclasses.replace(layer.config, mod_enabled=mod, residual_dropout=0.0)
+        blk = MoEFFNBlock(cfg, 0, ffn=layer).to(x.device)
+        blk.ffn_norm.weight = torch.nn.Parameter(norm_w.detach().clone())
+        if mod:
+            blk.ffn_mod_router.to(x.device, torch.bfloat16)
+        blk.train()
+        params = [p_ for p_ in blk.parameters()]
+
+        def step(repack=False):
+            for p_ in params:
+                p_.grad = None
+                if repack:
+                    torch.autograd.graph.increment_version(p_)
+            h.grad = None
+            o = blk(h)
+            torch.autograd.backward([o, blk.aux_loss], [dy, one])
+
+        for _ in range(3):
+            step()
+        assert blk.last_path == "fused_train"
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            step(repack=True)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        events = []
+        ops.set_stage_timing(events)
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        ops.set_stage_timing(None)
+        per = {}
+        for name, a, b in events:
+            per[name] = per.get(name, 0.0) + a.elapsed_time(b) * 1e3 / steps
+        key = "mod" if mod else "no_mod"
+        out[key] = {"step_ms": round((t1 - t0) / steps * 1e3, 3),
+                    "tokens_per_s": round(wl.T * steps / (t1 - t0), 1),
+                    "step_ms_with_repack": round((t2 - t1) / steps * 1e3, 3),
+                    "stages_us": {n: round(v, 1) for n, v in per.items()}}
+        if mod:
+            out[key]["kept_tokens"] = wl.B * blk.ffn_mod_router.keep_count(wl.S)
+        layer.zero_grad(set_to_none=True)
+        del blk
+    out["steps"] = steps
+    out["note"] = ("autograd step of out = h + MoE(RMSNorm(h)) (MoD-gated: the kept tokens only, "
+                   "mod_capacity_factor 0.75), loss sum(out * dy) + aux, training mode, residual dropout 0")
+    return out
 
 
 def run_training(args, wl, layer, x):
