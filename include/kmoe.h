@@ -235,6 +235,8 @@ int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int64_t C, int 
  *   sel_idx (B,keep) int64 ascending, sel_w (B,keep) f32 = softmax over the kept r
  *   in ascending-index order; token_rows (B*keep) = b*S + sel_idx; out_map (B*S)
  *   = compact index b*keep + i of a kept token, -1 otherwise.
+ * x = NULL: `logits` already holds r (e.g. from kmoe_rmsnorm's mod_logits) and
+ * only the selection runs (w_mod and d unused).
  * Requires 1 <= keep <= S.  workspace: kmoe_mod_workspace_bytes.            */
 size_t kmoe_mod_workspace_bytes(int B, int64_t S);
 int kmoe_mod_select(const void* x, int B, int64_t S, int d, const void* w_mod, int64_t keep, float* logits,
@@ -355,9 +357,12 @@ int kmoe_mod_bwd(const float* sel_w, const float* dsel, int B, int64_t keep, con
 /* RMSNorm of the block boundary (RMSNorm.forward, embeddings.py:167-195; the
  * ffn_norm of TransformerBlock.forward, layers.py:142-147) for the training path:
  *   n[t] = bf16(g * x[t] * r_t),  rrms[t] = r_t = 1/sqrt(mean(x[t]^2) + eps)
- * x (T, d) bf16 or f32, g (d) bf16 or f32; d a multiple of 8, <= 8192.       */
+ * x (T, d) bf16 or f32, g (d) bf16 or f32; d a multiple of 8, <= 8192.
+ * w_mod (d) bf16 and mod_logits (T) f32, both or neither: also the MoD router
+ * logits of the normalised rows, mod_logits[t] = n[t] . w_mod (mod.py:93), bit-identical
+ * to those kmoe_mod_select computes from n (pass them to it with x = NULL).   */
 int kmoe_rmsnorm(const void* x, int x_dtype, const void* weight, int w_dtype, float eps, int64_t T, int d, void* n,
-                 float* rrms, void* stream);
+                 float* rrms, const void* w_mod, float* mod_logits, void* stream);
 /* Its backward from dn (T, d) bf16 (the gradient of n):
  *   dx[t] = dres[t] + r_t g*dn[t] - (r_t^3 / d) x[t] sum_c g_c dn[t,c] x[t,c]
  *   dweight = sum_t dn[t] * x[t] r_t  (fixed-order reduction)

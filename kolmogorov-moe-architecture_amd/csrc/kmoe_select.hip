@@ -410,17 +410,18 @@ extern "C" int kmoe_mod_select(const void* x, int B, int64_t S, int d, const voi
                                size_t workspace_bytes, void* stream) {
   (void)workspace;
   (void)workspace_bytes;
-  KMOE_REQUIRE(x && w_mod && logits && sel_idx && sel_w && token_rows && out_map, KMOE_ERR_NULL,
+  KMOE_REQUIRE((!x || w_mod) && logits && sel_idx && sel_w && token_rows && out_map, KMOE_ERR_NULL,
                "kmoe_mod_select: null buffer");
   KMOE_REQUIRE(B >= 1, KMOE_ERR_SHAPE, "kmoe_mod_select: B=%d", B);
   KMOE_REQUIRE(S >= 1 && S <= SEL_MAX_S, KMOE_ERR_UNSUPPORTED, "kmoe_mod_select: S=%lld not in [1,%d]", (long long)S,
                SEL_MAX_S);
   KMOE_REQUIRE(keep >= 1 && keep <= S, KMOE_ERR_SHAPE, "kmoe_mod_select: keep=%lld not in [1,S]", (long long)keep);
-  KMOE_REQUIRE(d > 0 && d % 8 == 0, KMOE_ERR_SHAPE, "kmoe_mod_select: d=%d must be a multiple of 8", d);
+  KMOE_REQUIRE(!x || (d > 0 && d % 8 == 0), KMOE_ERR_SHAPE, "kmoe_mod_select: d=%d must be a multiple of 8", d);
   hipStream_t s = kmoe::as_stream(stream);
   const int64_t T = (int64_t)B * S;
-  hipLaunchKernelGGL(mod_logits_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0, s,
-                     static_cast<const uint16_t*>(x), T, d, static_cast<const uint16_t*>(w_mod), logits);
+  if (x)  // else the caller's logits are used as they are
+    hipLaunchKernelGGL(mod_logits_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), T, d, static_cast<const uint16_t*>(w_mod), logits);
   hipLaunchKernelGGL(mod_select_kernel, dim3((unsigned)B), dim3(SEL_THREADS), 0, s, logits, (int)S, (int)keep, sel_idx,
                      sel_w, token_rows, out_map);
   return kmoe::check_launch("kmoe_mod_select");

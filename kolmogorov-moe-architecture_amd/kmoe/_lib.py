@@ -70,7 +70,7 @@ _SIGNATURES = {
     "kmoe_combine_bwd_rows": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_mod_bwd_workspace_bytes": (_sz, [_i64, _i32]),
     "kmoe_mod_bwd": (_i32, [_vp, _vp, _i32, _i64, _vp, _i32, _vp, _i64, _vp, _i32, _vp, _sz, _vp]),
-    "kmoe_rmsnorm": (_i32, [_vp, _i32, _vp, _i32, _f32, _i64, _i32, _vp, _vp, _vp]),
+    "kmoe_rmsnorm": (_i32, [_vp, _i32, _vp, _i32, _f32, _i64, _i32, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_rmsnorm_bwd_workspace_bytes": (_sz, [_i64, _i32]),
     "kmoe_rmsnorm_bwd": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _sz, _vp]),
     "kmoe_packed_w3n_bytes": (_sz, [_i32, _i32, _i32]),

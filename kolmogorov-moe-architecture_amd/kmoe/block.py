@@ -188,12 +188,14 @@ class _BlockTrainFn(torch.autograd.Function):
         T = B * S
         ffn = blk.ffn
         h2d = h.detach().reshape(T, d).contiguous()
-        n, rrms = ops.rmsnorm(h2d, g, blk.ffn_norm.eps)
+        w_mod = blk.ffn_mod_router.router.weight if use_mod else None
+        # the norm kernel also writes the MoD logits of the normalised rows
+        n, rrms, mod_logits = ops.rmsnorm(h2d, g, blk.ffn_norm.eps, w_mod=w_mod)
         out_dtype = torch.promote_types(h.dtype, g.dtype)
         sel = None
         keep = 0
         if use_mod:
-            sel = blk.ffn_mod_router.select(n.view(B, S, d))
+            sel = blk.ffn_mod_router.select(n.view(B, S, d), logits=mod_logits)
             keep = sel.sel_idx.shape[1]
             x_sel, _ = ops.gather_rows(n, sel.token_rows, B * keep)
             y, aux, sv = ffn._train_forward(x_sel, B * keep, out_dtype, out_map=sel.out_map,

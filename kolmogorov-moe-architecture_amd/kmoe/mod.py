@@ -46,10 +46,12 @@ class MoDRouter(nn.Module):
     def keep_count(self, seq_len: int) -> int:
         return max(1, min(seq_len, int(seq_len * self.capacity_factor)))  # mod.py:97
 
-    def select(self, hidden_states: torch.Tensor) -> ops.ModSelectOut:
+    def select(self, hidden_states: torch.Tensor, logits: torch.Tensor = None) -> ops.ModSelectOut:
+        """The selection of mod.py:93-112; `logits` ((B, S) f32) when already computed
+        (the block's RMSNorm kernel writes them)."""
         B, S, _ = hidden_states.shape
         w = self.router.weight.detach()
-        return ops.mod_select(hidden_states, w, self.keep_count(S))
+        return ops.mod_select(hidden_states, w, self.keep_count(S), logits=logits)
 
     def forward(self, hidden_states: torch.Tensor) -> Tuple[torch.Tensor, ...]:
         """(sorted_indices, router_weights, router_logits, topk_indices) as mod.py:122.

@@ -410,21 +410,27 @@ class ModSelectOut(NamedTuple):
     out_map: torch.Tensor     # (B*S,) int32
 
 
-def mod_select(x3d, w_mod, keep) -> ModSelectOut:
-    """Mixture-of-Depths top-keep per sequence (mod.py:67-122)."""
+def mod_select(x3d, w_mod, keep, logits=None) -> ModSelectOut:
+    """Mixture-of-Depths top-keep per sequence (mod.py:67-122).  With `logits` ((B, S)
+    f32, e.g. rmsnorm's mod_logits) the selection runs on them and x3d is not read."""
     _need_gpu(x3d, w_mod)
-    x3d = _contig(x3d, _BF16)
-    w_mod = _contig(w_mod, _BF16).reshape(-1)
     B, S, d = x3d.shape
     dev = x3d.device
-    logits = torch.empty(B, S, device=dev, dtype=torch.float32)
+    stream = _stream(x3d)
+    if logits is not None:
+        logits = _contig(logits, torch.float32).view(B, S)
+        x3d = w_mod = None
+    else:
+        x3d = _contig(x3d, _BF16)
+        w_mod = _contig(w_mod, _BF16).reshape(-1)
+        logits = torch.empty(B, S, device=dev, dtype=torch.float32)
     sel_idx = torch.empty(B, keep, device=dev, dtype=torch.int64)
     sel_w = torch.empty(B, keep, device=dev, dtype=torch.float32)
     token_rows = torch.empty(B * keep, device=dev, dtype=torch.int32)
     out_map = torch.empty(B * S, device=dev, dtype=torch.int32)
     with _Stage("mod_select"):
         _lib.call("kmoe_mod_select", ptr(x3d), B, S, d, ptr(w_mod), keep, ptr(logits), ptr(sel_idx), ptr(sel_w),
-              ptr(token_rows), ptr(out_map), None, 0, _stream(x3d))
+              ptr(token_rows), ptr(out_map), None, 0, stream)
     return ModSelectOut(logits, sel_idx, sel_w, token_rows, out_map)
 
 
@@ -436,9 +442,15 @@ def _fdt(t):
     raise ValueError(f"kmoe: unsupported dtype {t.dtype}")
 
 
-def rmsnorm(x2d, weight, eps):
-    """RMSNorm (embeddings.py:167-195) of the rows of x2d (bf16 or f32) with weight (d,):
-    (n (T, d) bf16, rrms (T,) f32 = 1/sqrt(mean(x^2) + eps))."""
+class NormOut(NamedTuple):
+    n: torch.Tensor                       # (T, d) bf16 normalised rows
+    rrms: torch.Tensor                    # (T,) f32 1/sqrt(mean(x^2) + eps)
+    mod_logits: Optional[torch.Tensor]    # (T,) f32 n . w_mod (with w_mod)
+
+
+def rmsnorm(x2d, weight, eps, w_mod=None) -> NormOut:
+    """RMSNorm (embeddings.py:167-195) of the rows of x2d (bf16 or f32) with weight (d,);
+    with w_mod (d,) also the MoD router logits of the normalised rows (mod.py:93)."""
     _need_gpu(x2d, weight)
     if x2d.dtype not in (torch.float32, _BF16):
         x2d = x2d.float()
@@ -450,10 +462,14 @@ def rmsnorm(x2d, weight, eps):
     T, d = x2d.shape
     n = torch.empty(T, d, device=x2d.device, dtype=_BF16)
     rrms = torch.empty(T, device=x2d.device, dtype=torch.float32)
+    ml = None
+    if w_mod is not None:
+        w_mod = _contig(w_mod.detach(), _BF16).reshape(-1)
+        ml = torch.empty(T, device=x2d.device, dtype=torch.float32)
     with _Stage("rmsnorm"):
         _lib.call("kmoe_rmsnorm", ptr(x2d), _fdt(x2d), ptr(weight), _fdt(weight), float(eps), T, d, ptr(n), ptr(rrms),
-                  _stream(x2d))
-    return n, rrms
+                  ptr(w_mod), ptr(ml), _stream(x2d))
+    return NormOut(n, rrms, ml)
 
 
 def rmsnorm_bwd(dn, x2d, weight, rrms, dres=None, dw_dtype=None):

@@ -139,13 +139,14 @@ def test_counted_dispatch_and_router_hist_validation(lib):
 def test_norm_and_mod_backward_validation(lib):
     """Argument checks of the block / MoD training entry points (no launch on failure)."""
     BF, F32 = _lib.DTYPE_BF16, _lib.DTYPE_F32
-    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, NULL, F32, 1e-5, 16, 64, FAKE, FAKE, NULL)[0] == -1
-    assert _err(lib, "kmoe_rmsnorm", FAKE, 7, FAKE, F32, 1e-5, 16, 64, FAKE, FAKE, NULL)[0] == -3
-    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, FAKE, F32, 1e-5, 16, 60, FAKE, FAKE, NULL)[0] == -2
-    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, FAKE, F32, 1e-5, 16, 8200, FAKE, FAKE, NULL)[0] == -6
-    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, FAKE, F32, -1.0, 16, 64, FAKE, FAKE, NULL)[0] == -2
+    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, NULL, F32, 1e-5, 16, 64, FAKE, FAKE, NULL, NULL, NULL)[0] == -1
+    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, FAKE, F32, 1e-5, 16, 64, FAKE, FAKE, FAKE, NULL, NULL)[0] == -1
+    assert _err(lib, "kmoe_rmsnorm", FAKE, 7, FAKE, F32, 1e-5, 16, 64, FAKE, FAKE, NULL, NULL, NULL)[0] == -3
+    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, FAKE, F32, 1e-5, 16, 60, FAKE, FAKE, NULL, NULL, NULL)[0] == -2
+    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, FAKE, F32, 1e-5, 16, 8200, FAKE, FAKE, NULL, NULL, NULL)[0] == -6
+    assert _err(lib, "kmoe_rmsnorm", FAKE, BF, FAKE, F32, -1.0, 16, 64, FAKE, FAKE, NULL, NULL, NULL)[0] == -2
     need = lib.kmoe_rmsnorm_bwd_workspace_bytes(5000, 64)
-    assert need == -(-5000 // 8) * 64 * 4  # 8-row segments (at most 1024 of them)
+    assert need == -(-5000 // 24) * 64 * 4  # segments of 24 rows (a multiple of 8; at most 256 of them)
     rc, msg = _err(lib, "kmoe_rmsnorm_bwd", FAKE, FAKE, BF, FAKE, F32, FAKE, NULL, 5000, 64, FAKE, FAKE, BF, FAKE,
                    need - 4, NULL)
     assert rc == -4 and "workspace" in msg

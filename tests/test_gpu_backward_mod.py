@@ -122,10 +122,12 @@ def test_block_training_backward(dev, mod, norm_dtype, h_dtype):
     T = B * S
     ffn, ge = blk.ffn, blk.ffn.grouped_experts
     with torch.no_grad():
-        n, _ = ops.rmsnorm(h.detach().reshape(T, d), blk.ffn_norm.weight, blk.ffn_norm.eps)
+        n = ops.rmsnorm(h.detach().reshape(T, d), blk.ffn_norm.weight, blk.ffn_norm.eps).n
         sel = None
         if mod:
             keep = blk.ffn_mod_router.keep_count(S)
+            # the selection from n's own logits kernel: the block took it from the logits
+            # its norm kernel wrote (bit-identical, test_rmsnorm_mod_logits)
             sel = ops.mod_select(n.view(B, S, d), blk.ffn_mod_router.router.weight, keep)
             idx = ffn.router.route(n[sel.token_rows.long()]).idx.cpu()
         else:
@@ -177,7 +179,7 @@ def test_rmsnorm_kernels(dev, T, d, x_dtype, w_dtype):
     dn = torch.randn(T, d, generator=g).to(BF)
     dres = torch.randn(T, d, generator=g).to(x_dtype)
     eps = 1e-5
-    n, rrms = ops.rmsnorm(x.to(dev), w.to(dev), eps)
+    n, rrms, _ = ops.rmsnorm(x.to(dev), w.to(dev), eps)
     dx, dw = ops.rmsnorm_bwd(dn.to(dev), x.to(dev), w.to(dev), rrms, dres=dres.to(dev))
     torch.cuda.synchronize()
     x64, w64 = x.double().requires_grad_(True), w.double().requires_grad_(True)
@@ -261,3 +263,22 @@ def test_combine_bwd_rows_kernel(dev, T, k, d, T_out):
     want[slot_row[kept].long()] = ((scale[:, None] * slot_w).double()[..., None] * dyr[:, None, :])[kept]
     got = dyperm.cpu().double()
     assert bool(((got - want).abs() <= want.abs() * 2.0 ** -8 + 1e-30).all())
+
+
+@pytest.mark.parametrize("B,S,d", [(2, 300, 256), (4, 2048, 2048), (1, 7, 8200 - 8)])
+def test_rmsnorm_mod_logits(dev, B, S, d):
+    """The MoD logits the norm kernel writes equal, bit for bit, those kmoe_mod_select
+    computes from the normalised rows, and so does the selection made from them."""
+    print(f"rmsnorm mod logits B={B} S={S} d={d}", flush=True)
+    g = torch.Generator().manual_seed(S + d)
+    x = torch.randn(B * S, d, generator=g).to(BF).to(dev)
+    w = (1.0 + 0.3 * torch.randn(d, generator=g)).to(dev)
+    w_mod = (torch.randn(1, d, generator=g) * 0.05).to(BF).to(dev)
+    out = ops.rmsnorm(x, w, 1e-5, w_mod=w_mod)
+    keep = max(1, int(S * 0.75))
+    ref = ops.mod_select(out.n.view(B, S, d), w_mod, keep)
+    got = ops.mod_select(out.n.view(B, S, d), w_mod, keep, logits=out.mod_logits)
+    torch.cuda.synchronize()
+    assert torch.equal(out.mod_logits.view(B, S), ref.logits)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
