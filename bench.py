@@ -136,6 +136,10 @@ def run_gpu(args, wl, light=False):
                 ops.dispatch(x.reshape(wl.T, wl.d), r0.idx, r0.w, wl.E, capacity=cap, block_counts=r0.block_counts)
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            # the GPU spins ~1.5 ms first, so that the host has enqueued every launch
+            # before e0 fires: the pair then times the kernels back to back (as inside a
+            # training step, where the host runs ahead), not the host's launch overhead
+            torch.cuda._sleep(3_000_000)
             e0.record()
             for _ in range(10):
                 ops.dispatch(x.reshape(wl.T, wl.d), r0.idx, r0.w, wl.E, capacity=cap, block_counts=r0.block_counts)
@@ -537,7 +541,8 @@ def main():
         b = wl.T * wl.d * 2 + res["a_kept"] * wl.d * 2 + 8.0 * res["a_all"]
         out["dispatch_rows"] = {"us": round(res["rows_us"], 2), "GBps": round(b / (res["rows_us"] * 1e-6) / 1e9, 1),
                                 "frac_hbm": round(b / (res["rows_us"] * 1e-6) / PEAK_HBM, 4),
-                                "note": "materialising dispatch (tables from the router's block histograms + row "
+                                "note": "device time (the host has enqueued the 10 timed calls before the first "
+                                        "event fires); materialising dispatch (tables from the router's block histograms + row "
                                         "copy), as the training forward runs it, timed separately; the bf16 inference "
                                         "layer gathers rows inside the gate/up GEMM instead"}
     if "combine" in res["stages"]:
