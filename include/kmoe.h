@@ -305,6 +305,30 @@ int kmoe_gemm_grouped(const void* a, const int32_t* offsets, int E, int K, int64
 int kmoe_swiglu_bwd(const void* dh, const void* gu, int64_t rows, const int32_t* n_rows_dev, int F, void* dgu,
                     void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Non-gated experts — GroupedExperts with an activation other than swiglu
+ * (moe.py:187-191,281-283): w1 (E, d, F), w2 (E, F, d), y = silu(x . w1) . w2.
+ * Forward: p = kmoe_gemm_grouped(xperm, w1t, K = d, N = F_pad), h = kmoe_silu_rows(p),
+ * yperm = kmoe_gemm_grouped(h, w2t, K = F_pad, N = d).  Backward: dh = dyperm . w2^T
+ * (w2n, K = d), dp = kmoe_silu_bwd(dh, p), dx = dp . w1^T (w1n, K = F_pad), and the
+ * weight gradients with kmoe_gemm_wgrad_rows (dW1 = xperm^T dp, dW2 = h^T dyperm).
+ * Packed layouts (bf16, K-contiguous rows, WPAD bytes after every row, zero padded):
+ *   w1t (E, round_up(F,256), d):      row f = w1[e][:, f]
+ *   w2t (E, round_up(d,256), F_pad):  row n = w2[e][:, n]   (kmoe_packed_w3_bytes, bf16)
+ *   w2n (E, round_up(F,256), d):      row f = w2[e][f][:]   (kmoe_packed_w3n_bytes)
+ *   w1n (E, round_up(d,256), F_pad):  row i = w1[e][i][:]                           */
+size_t kmoe_packed_w1t_bytes(int E, int d, int F);
+size_t kmoe_packed_w1n_bytes(int E, int d, int F);
+int kmoe_pack_weights_plain(const void* w1, const void* w2, int w_dtype, int E, int d, int F, void* w1t_packed,
+                            void* w2t_packed, void* stream);
+int kmoe_pack_weights_plain_bwd(const void* w1, const void* w2, int w_dtype, int E, int d, int F, void* w2n_packed,
+                                void* w1n_packed, void* stream);
+/* h = silu(p) and dp = dh * s * (1 + p (1 - s)), s = sigmoid(p), over (rows, F_pad) bf16
+ * (rows < *n_rows_dev if given).                                               */
+int kmoe_silu_rows(const void* p, int64_t rows, const int32_t* n_rows_dev, int F, void* h, void* stream);
+int kmoe_silu_bwd(const void* dh, const void* p, int64_t rows, const int32_t* n_rows_dev, int F, void* dp,
+                  void* stream);
+
 /* Weight gradients read straight from row-major row buffers (no transposes):
  *   c_e[m, n] = sum over expert e's rows r of a[r, m] * b[r, n]
  * a (max_rows, lda) and b (max_rows, ldb) bf16, rows of expert e = [offsets[e],

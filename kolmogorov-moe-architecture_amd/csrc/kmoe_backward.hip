@@ -106,6 +106,43 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t* __restr
   }
 }
 
+// Non-gated experts (silu(x . w1) . w2, moe.py:187-191,281-283) on rows of F_pad
+// columns, rows < n_rows_dev[0] when given:
+//   forward:  h = silu(p)                            (p: the pre-activation x . w1)
+//   backward: dp = dh * s * (1 + p (1 - s)),  s = sigmoid(p)
+template <bool BWD>
+__global__ __launch_bounds__(256) void silu_rows_kernel(const uint16_t* __restrict__ dh, const uint16_t* __restrict__ p,
+                                                        int64_t rows, const int32_t* __restrict__ n_rows_dev, int Fp,
+                                                        uint16_t* __restrict__ out) {
+  int64_t nr = rows;
+  if (n_rows_dev) nr = min<int64_t>(nr, (int64_t)*n_rows_dev);
+  const int64_t total = nr * (Fp / 8);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const i32x4_t pv = reinterpret_cast<const i32x4_t*>(p)[i];
+    i32x4_t hv = {0, 0, 0, 0};
+    if constexpr (BWD) hv = reinterpret_cast<const i32x4_t*>(dh)[i];
+    i32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int hlf = 0; hlf < 2; ++hlf) {
+        const int sh = hlf * 16;
+        const float g = bf16_to_f32((uint16_t)((uint32_t)pv[q] >> sh));
+        const float sg = 1.0f / (1.0f + __expf(-g));
+        float v;
+        if constexpr (BWD)
+          v = bf16_to_f32((uint16_t)((uint32_t)hv[q] >> sh)) * sg * (1.0f + g * (1.0f - sg));
+        else
+          v = g * sg;
+        w |= (uint32_t)f32_to_bf16(v) << sh;
+      }
+      o[q] = (int)w;
+    }
+    reinterpret_cast<i32x4_t*>(out)[i] = o;
+  }
+}
+
 // Router logit gradient, one thread per token (E <= 64):
 //   top-k renormalisation (w_j = p_j / sum_sel p = softmax over the selected logits):
 //     dl[i_j] += w_j (dw_j - sum_l w_l dw_l)
@@ -437,6 +474,29 @@ extern "C" int kmoe_swiglu_bwd(const void* dh, const void* gu, int64_t rows, con
                      static_cast<const uint16_t*>(dh), static_cast<const uint16_t*>(gu), rows, n_rows_dev, Fp,
                      static_cast<uint16_t*>(dgu));
   return kmoe::check_launch("kmoe_swiglu_bwd");
+}
+
+extern "C" int kmoe_silu_rows(const void* p, int64_t rows, const int32_t* n_rows_dev, int F, void* h, void* stream) {
+  KMOE_REQUIRE(p && h, KMOE_ERR_NULL, "kmoe_silu_rows: null buffer");
+  KMOE_REQUIRE(rows >= 0 && F > 0, KMOE_ERR_SHAPE, "kmoe_silu_rows: bad shape");
+  if (rows == 0) return KMOE_OK;
+  const int Fp = (F + 127) / 128 * 128;
+  hipLaunchKernelGGL(silu_rows_kernel<false>, dim3(grid_for(rows * (Fp / 8), 256)), dim3(256), 0,
+                     kmoe::as_stream(stream), nullptr, static_cast<const uint16_t*>(p), rows, n_rows_dev, Fp,
+                     static_cast<uint16_t*>(h));
+  return kmoe::check_launch("kmoe_silu_rows");
+}
+
+extern "C" int kmoe_silu_bwd(const void* dh, const void* p, int64_t rows, const int32_t* n_rows_dev, int F, void* dp,
+                             void* stream) {
+  KMOE_REQUIRE(dh && p && dp, KMOE_ERR_NULL, "kmoe_silu_bwd: null buffer");
+  KMOE_REQUIRE(rows >= 0 && F > 0, KMOE_ERR_SHAPE, "kmoe_silu_bwd: bad shape");
+  if (rows == 0) return KMOE_OK;
+  const int Fp = (F + 127) / 128 * 128;
+  hipLaunchKernelGGL(silu_rows_kernel<true>, dim3(grid_for(rows * (Fp / 8), 256)), dim3(256), 0,
+                     kmoe::as_stream(stream), static_cast<const uint16_t*>(dh), static_cast<const uint16_t*>(p), rows,
+                     n_rows_dev, Fp, static_cast<uint16_t*>(dp));
+  return kmoe::check_launch("kmoe_silu_bwd");
 }
 
 extern "C" int kmoe_router_dlogits(const float* logits, int64_t T, int E, const int64_t* topk_idx, const float* topk_w,

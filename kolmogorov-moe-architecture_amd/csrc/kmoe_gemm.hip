@@ -1020,14 +1020,16 @@ __global__ __launch_bounds__(256) void pack_pad_kernel(uint16_t* __restrict__ ou
 }
 
 // Backward packed layouts (rows K-contiguous, WPAD bytes after every row, zero padded):
-//   w3n : (E, round_up(F, 256), d)        row f = w3[e][f][:]            (dh = dY . w3^T, K = d)
-//   w13t: (E, round_up(d, 256), 2*F_pad)  row i = w1[e][i][:], w2[e][i][:] interleaved per 128
-//                                          columns like w13's rows        (dX = [dg|du] . w13, K = 2*F_pad)
-// Both are row copies with the columns rearranged (no transpose), 16 bytes per access;
-// rows past F (w3n) or d (w13t) and the pads are written as zeros.
+//   mode ROWS_W3N : (E, round_up(F, 256), d)        row f = w3[e][f][:]      (dh = dY . w3^T, K = d)
+//   mode ROWS_W13T: (E, round_up(d, 256), 2*F_pad)  row i = w1[e][i][:], w2[e][i][:] interleaved per 128
+//                                                    columns like w13's rows  (dX = [dg|du] . w13, K = 2*F_pad)
+//   mode ROWS_W1N : (E, round_up(d, 256), F_pad)    row i = w1[e][i][:]      (non-gated experts: dX = dp . w1^T)
+// All are row copies with the columns rearranged (no transpose), 16 bytes per access;
+// rows past F (w3n) or d (w13t, w1n) and the pads are written as zeros.
+enum { ROWS_W3N = 0, ROWS_W13T = 1, ROWS_W1N = 2 };
 template <bool IN_F32>
 __global__ __launch_bounds__(256) void pack_rows16_kernel(const void* __restrict__ w1, const void* __restrict__ w2,
-                                                          const void* __restrict__ w3, int d, int F, bool w13t,
+                                                          const void* __restrict__ w3, int d, int F, int mode,
                                                           uint16_t* __restrict__ out, int64_t out_rows, int out_ld,
                                                           int E) {
   const int nv = out_ld / 8;  // 16-byte vectors per packed row
@@ -1042,12 +1044,18 @@ __global__ __launch_bounds__(256) void pack_rows16_kernel(const void* __restrict
     const void* src = nullptr;
     int64_t off = 0;
     int n_ok = 0;  // source elements that exist (the rest are zero)
-    if (w13t) {
+    if (mode == ROWS_W13T) {
       if (row < d && c < 2 * Fp) {
         const int half = (c >> 7) & 1, f = (c >> 8) * 128 + (c & 127);
         src = half ? w2 : w1;
         off = ((int64_t)e * d + row) * F + f;
         n_ok = F - f < 8 ? (F - f > 0 ? F - f : 0) : 8;
+      }
+    } else if (mode == ROWS_W1N) {
+      if (row < d && c < Fp) {
+        src = w1;
+        off = ((int64_t)e * d + row) * F + c;
+        n_ok = F - c < 8 ? (F - c > 0 ? F - c : 0) : 8;
       }
     } else if (row < F && c < d) {
       src = w3;
@@ -1426,17 +1434,87 @@ extern "C" int kmoe_pack_weights_bwd(const void* w1, const void* w2, const void*
   const int64_t r3 = round_up(F, 256), r13 = round_up(d, 256);
   const int ld3 = d + WPAD / 2, ld13 = 2 * Fp + WPAD / 2;
   if (f32) {
-    hipLaunchKernelGGL(pack_rows16_kernel<true>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, false,
+    hipLaunchKernelGGL(pack_rows16_kernel<true>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, (int)ROWS_W3N,
                        static_cast<uint16_t*>(w3n_packed), r3, ld3, E);
-    hipLaunchKernelGGL(pack_rows16_kernel<true>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, true,
+    hipLaunchKernelGGL(pack_rows16_kernel<true>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, (int)ROWS_W13T,
                        static_cast<uint16_t*>(w13t_packed), r13, ld13, E);
   } else {
-    hipLaunchKernelGGL(pack_rows16_kernel<false>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, false,
+    hipLaunchKernelGGL(pack_rows16_kernel<false>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, (int)ROWS_W3N,
                        static_cast<uint16_t*>(w3n_packed), r3, ld3, E);
-    hipLaunchKernelGGL(pack_rows16_kernel<false>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, true,
+    hipLaunchKernelGGL(pack_rows16_kernel<false>, dim3(4096), dim3(256), 0, s, w1, w2, w3, d, F, (int)ROWS_W13T,
                        static_cast<uint16_t*>(w13t_packed), r13, ld13, E);
   }
   return kmoe::check_launch("kmoe_pack_weights_bwd");
+}
+
+// ---- non-gated experts (silu(x . w1) . w2, moe.py:187-191,281-283): w1 (E, d, F), w2 (E, F, d)
+extern "C" size_t kmoe_packed_w1t_bytes(int E, int d, int F) {
+  return (size_t)E * (size_t)round_up(F, 256) * ((size_t)d * 2 + WPAD);
+}
+
+extern "C" size_t kmoe_packed_w1n_bytes(int E, int d, int F) {
+  return (size_t)E * (size_t)round_up(d, 256) * ((size_t)round_up(F, 128) * 2 + WPAD);
+}
+
+static int check_plain_pack(const char* who, const void* w1, const void* w2, const void* o1, const void* o2,
+                            int w_dtype, int E, int d, int F) {
+  KMOE_REQUIRE(w1 && w2 && o1 && o2, KMOE_ERR_NULL, "%s: null buffer", who);
+  KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "%s: E=%d out of range", who, E);
+  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "%s: d=%d must be a positive multiple of 64", who, d);
+  KMOE_REQUIRE(F > 0, KMOE_ERR_SHAPE, "%s: F=%d must be > 0", who, F);
+  KMOE_REQUIRE(w_dtype == KMOE_DTYPE_BF16 || w_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE,
+               "%s: weight dtype must be bf16 or f32", who);
+  return KMOE_OK;
+}
+
+extern "C" int kmoe_pack_weights_plain(const void* w1, const void* w2, int w_dtype, int E, int d, int F,
+                                       void* w1t_packed, void* w2t_packed, void* stream) {
+  const int rc = check_plain_pack("kmoe_pack_weights_plain", w1, w2, w1t_packed, w2t_packed, w_dtype, E, d, F);
+  if (rc) return rc;
+  hipStream_t s = kmoe::as_stream(stream);
+  const int Fp = round_up(F, 128);
+  const int64_t r1 = round_up(F, 256), r2 = round_up(d, 256);
+  const int ld1 = d + WPAD / 2, ld2 = Fp + WPAD / 2;
+  uint16_t* o1 = static_cast<uint16_t*>(w1t_packed);
+  uint16_t* o2 = static_cast<uint16_t*>(w2t_packed);
+  // w1t: row f = w1[e][:, f] (K = d); w2t: row n = w2[e][:, n] (K = F_pad), the down pack's layout
+  const dim3 g1((unsigned)kmoe::ceil_div(F, 64), (unsigned)kmoe::ceil_div(d, 64), (unsigned)E);
+  const dim3 g2((unsigned)kmoe::ceil_div(d, 64), (unsigned)kmoe::ceil_div(F, 64), (unsigned)E);
+  if (w_dtype == KMOE_DTYPE_F32) {
+    hipLaunchKernelGGL(pack_t16_kernel<true>, g1, dim3(256), 0, s, w1, d, F, (int64_t)d * F, 0, false, o1, r1, ld1);
+    hipLaunchKernelGGL(pack_t16_kernel<true>, g2, dim3(256), 0, s, w2, F, d, (int64_t)d * F, 0, false, o2, r2, ld2);
+  } else {
+    hipLaunchKernelGGL(pack_t16_kernel<false>, g1, dim3(256), 0, s, w1, d, F, (int64_t)d * F, 0, false, o1, r1, ld1);
+    hipLaunchKernelGGL(pack_t16_kernel<false>, g2, dim3(256), 0, s, w2, F, d, (int64_t)d * F, 0, false, o2, r2, ld2);
+  }
+  hipLaunchKernelGGL(pack_pad_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(E * r1, 256)), dim3(256), 0, s, o1,
+                     (int64_t)E * r1, ld1, d, (int)r1, F, false);
+  hipLaunchKernelGGL(pack_pad_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(E * r2, 256)), dim3(256), 0, s, o2,
+                     (int64_t)E * r2, ld2, F, (int)r2, d, false);
+  return kmoe::check_launch("kmoe_pack_weights_plain");
+}
+
+extern "C" int kmoe_pack_weights_plain_bwd(const void* w1, const void* w2, int w_dtype, int E, int d, int F,
+                                           void* w2n_packed, void* w1n_packed, void* stream) {
+  const int rc = check_plain_pack("kmoe_pack_weights_plain_bwd", w1, w2, w2n_packed, w1n_packed, w_dtype, E, d, F);
+  if (rc) return rc;
+  hipStream_t s = kmoe::as_stream(stream);
+  const int Fp = round_up(F, 128);
+  const int64_t r2 = round_up(F, 256), r1 = round_up(d, 256);
+  const int ld2 = d + WPAD / 2, ld1 = Fp + WPAD / 2;
+  // w2n: row f = w2[e][f][:] (dh = dY . w2^T, K = d), the w3n layout of w2; w1n: row i = w1[e][i][:] (K = F_pad)
+  if (w_dtype == KMOE_DTYPE_F32) {
+    hipLaunchKernelGGL(pack_rows16_kernel<true>, dim3(4096), dim3(256), 0, s, w1, nullptr, w2, d, F, (int)ROWS_W3N,
+                       static_cast<uint16_t*>(w2n_packed), r2, ld2, E);
+    hipLaunchKernelGGL(pack_rows16_kernel<true>, dim3(4096), dim3(256), 0, s, w1, nullptr, w2, d, F, (int)ROWS_W1N,
+                       static_cast<uint16_t*>(w1n_packed), r1, ld1, E);
+  } else {
+    hipLaunchKernelGGL(pack_rows16_kernel<false>, dim3(4096), dim3(256), 0, s, w1, nullptr, w2, d, F, (int)ROWS_W3N,
+                       static_cast<uint16_t*>(w2n_packed), r2, ld2, E);
+    hipLaunchKernelGGL(pack_rows16_kernel<false>, dim3(4096), dim3(256), 0, s, w1, nullptr, w2, d, F, (int)ROWS_W1N,
+                       static_cast<uint16_t*>(w1n_packed), r1, ld1, E);
+  }
+  return kmoe::check_launch("kmoe_pack_weights_plain_bwd");
 }
 
 extern "C" int kmoe_gemm_grouped(const void* a, const int32_t* offsets, int E, int K, int64_t max_rows,

@@ -76,6 +76,12 @@ _SIGNATURES = {
     "kmoe_packed_w3n_bytes": (_sz, [_i32, _i32, _i32]),
     "kmoe_packed_w13t_bytes": (_sz, [_i32, _i32, _i32]),
     "kmoe_pack_weights_bwd": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "kmoe_packed_w1t_bytes": (_sz, [_i32, _i32, _i32]),
+    "kmoe_packed_w1n_bytes": (_sz, [_i32, _i32, _i32]),
+    "kmoe_pack_weights_plain": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "kmoe_pack_weights_plain_bwd": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "kmoe_silu_rows": (_i32, [_vp, _i64, _vp, _i32, _vp, _vp]),
+    "kmoe_silu_bwd": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _vp]),
     "kmoe_gemm_grouped": (_i32, [_vp, _vp, _i32, _i32, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp]),
     "kmoe_swiglu_bwd": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _vp]),
     "kmoe_reduce_f32": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),

@@ -34,16 +34,29 @@ def _ru(a: int, b: int) -> int:
 
 
 class BwdWeights(NamedTuple):
-    w3n: torch.Tensor    # (E, round_up(F,256), d) packed rows of w3
-    w13t: torch.Tensor   # (E, round_up(d,256), 2*F_pad) packed rows of w1|w2
+    w3n: torch.Tensor    # (E, round_up(F,256), d) packed rows of w3 (non-gated: of w2)
+    w13t: torch.Tensor   # (E, round_up(d,256), 2*F_pad) packed rows of w1|w2 (non-gated: rows of w1, F_pad)
     w_in_t: torch.Tensor  # (round_up(d,256), 128) packed rows of w_in^T
+    plain: bool = False  # non-gated experts (silu(x w1) w2)
 
 
 def pack_bwd_weights(w1, w2, w3, w_in) -> BwdWeights:
-    """Backward packed layouts of the expert weights (w1/w2/w3, any of them None: skipped
-    together) and of the router's w_in (None: skipped)."""
+    """Backward packed layouts of the expert weights (w1/w2/w3; w1 None: skipped; w3 None:
+    the non-gated experts' w1 (E,d,F), w2 (E,F,d)) and of the router's w_in (None: skipped)."""
     lib = _lib.load()
     w3n = w13t = wit = None
+    plain = False
+    if w1 is not None and w3 is None:
+        E, d, F = w1.shape
+        dt = w1.dtype if w1.dtype in (torch.float32, _BF16) else torch.float32
+        w1, w2 = (w.detach().to(dt).contiguous() for w in (w1, w2))
+        w3n = torch.empty(lib.kmoe_packed_w3n_bytes(E, d, F), device=w1.device, dtype=torch.uint8)
+        w13t = torch.empty(lib.kmoe_packed_w1n_bytes(E, d, F), device=w1.device, dtype=torch.uint8)
+        _lib.call("kmoe_pack_weights_plain_bwd", ptr(w1), ptr(w2),
+                  _lib.DTYPE_F32 if dt == torch.float32 else _lib.DTYPE_BF16, E, d, F, ptr(w3n), ptr(w13t),
+                  ops._stream(w1))
+        plain = True
+        w1 = None
     if w1 is not None:
         E, d, F = w1.shape
         dt = w1.dtype
@@ -63,7 +76,7 @@ def pack_bwd_weights(w1, w2, w3, w_in) -> BwdWeights:
         wdt = _lib.DTYPE_F32 if dt == torch.float32 else _lib.DTYPE_BF16
         wit = torch.empty(lib.kmoe_packed_w_in_t_bytes(d), device=w_in.device, dtype=torch.uint8)
         _lib.call("kmoe_pack_w_in_t", ptr(w_in), wdt, d, ptr(wit), ops._stream(w_in))
-    return BwdWeights(w3n, w13t, wit)
+    return BwdWeights(w3n, w13t, wit, plain)
 
 
 class Saved(NamedTuple):
@@ -145,19 +158,25 @@ def _experts_core(dy, yperm, gu, slot_row, slot_w, kk, offsets, A, bw: BwdWeight
     with _stage("bwd_gemm_dh"):
         _lib.call("kmoe_gemm_grouped", ptr(dyperm), ptr(offsets), E, d, A, ptr(bw.w3n), _ru(F, 256), Fp,
                   ptr(dh), Fp, Fp, s)
-    dgu = torch.empty(max(A, 1), 2 * Fp, device=dev, dtype=_BF16)
+    # gated: [dg | du] from the saved gate / up values; non-gated: dp from the saved p
+    kk2 = 1 if bw.plain else 2
+    dgu = torch.empty(max(A, 1), kk2 * Fp, device=dev, dtype=_BF16)
     with _stage("bwd_swiglu"):
-        _lib.call("kmoe_swiglu_bwd", ptr(dh), ptr(gu), A, ptr(offsets[E:]), F, ptr(dgu), s)
+        if bw.plain:
+            _lib.call("kmoe_silu_bwd", ptr(dh), ptr(gu), A, ptr(offsets[E:]), F, ptr(dgu), s)
+        else:
+            _lib.call("kmoe_swiglu_bwd", ptr(dh), ptr(gu), A, ptr(offsets[E:]), F, ptr(dgu), s)
     dxp = torch.empty(A + extra_rows, d, device=dev, dtype=_BF16)
     with _stage("bwd_gemm_dx"):
-        _lib.call("kmoe_gemm_grouped", ptr(dgu), ptr(offsets), E, 2 * Fp, A, ptr(bw.w13t), _ru(d, 256), d,
+        _lib.call("kmoe_gemm_grouped", ptr(dgu), ptr(offsets), E, kk2 * Fp, A, ptr(bw.w13t), _ru(d, 256), d,
                   ptr(dxp), d, d, s)
     return dxp, dw, dyperm, dgu, dscale
 
 
-def _expert_weight_grads(h, dyperm, xperm, dgu, offsets, A, E, d, F):
+def _expert_weight_grads(h, dyperm, xperm, dgu, offsets, A, E, d, F, plain=False):
     """dW3 = h^T dyperm and dW1 | dW2 = xperm^T dgu per expert, straight from the row
-    buffers (transpose reads in LDS)."""
+    buffers (transpose reads in LDS).  Non-gated experts: (dW1 = xperm^T dp, dW2 = h^T
+    dyperm, None)."""
     Fp = _ru(F, 128)
     dev = h.device
     s = ops._stream(h)
@@ -166,6 +185,12 @@ def _expert_weight_grads(h, dyperm, xperm, dgu, offsets, A, E, d, F):
     with _stage("bwd_wgrad_w3"):
         _lib.call("kmoe_gemm_wgrad_rows", ptr(h), Fp, ptr(dyperm), d, A, ptr(offsets), E, F, dpad, ptr(dw3),
                   None, _lib.DTYPE_BF16, d, d, s)
+    if plain:
+        dw1 = torch.empty(E, d, F, device=dev, dtype=_BF16)
+        with _stage("bwd_wgrad_w13"):
+            _lib.call("kmoe_gemm_wgrad_rows", ptr(xperm), d, ptr(dgu), Fp, A, ptr(offsets), E, d, _ru(F, 256),
+                      ptr(dw1), None, _lib.DTYPE_BF16, F, F, s)
+        return dw1, dw3, None
     dw1 = torch.empty(E, d, F, device=dev, dtype=_BF16)
     dw2 = torch.empty(E, d, F, device=dev, dtype=_BF16)
     with _stage("bwd_wgrad_w13"):
@@ -281,7 +306,7 @@ def moe_backward(sv: Saved, dy: torch.Tensor, grad_aux: Optional[torch.Tensor], 
     dx = _gather_dx(dxp, src, T, d)
     if not need_weights:
         return Grads(dx, None, dw_out, None, None, None)
-    dw1, dw2, dw3 = _expert_weight_grads(sv.h, dyperm, sv.xperm, dgu, disp.offsets, A, E, d, F)
+    dw1, dw2, dw3 = _expert_weight_grads(sv.h, dyperm, sv.xperm, dgu, disp.offsets, A, E, d, F, bw.plain)
     return Grads(dx, dw_in, dw_out, dw1, dw2, dw3)
 
 
@@ -333,7 +358,7 @@ def mod_backward(sv: Saved, sel: "ops.ModSelectOut", B: int, keep: int, dy: torc
     dx = ops.combine(dxp, src, gw, T_out, out_map=sel.out_map, out_dtype=_BF16)
     if not need_weights:
         return ModGrads(dx, None, Grads(None, None, dw_out, None, None, None))
-    dw1, dw2, dw3 = _expert_weight_grads(sv.h, dyperm, sv.xperm, dgu, disp.offsets, A, E, d, F)
+    dw1, dw2, dw3 = _expert_weight_grads(sv.h, dyperm, sv.xperm, dgu, disp.offsets, A, E, d, F, bw.plain)
     return ModGrads(dx, dw_mod, Grads(None, dw_in, dw_out, dw1, dw2, dw3))
 
 
@@ -389,7 +414,7 @@ def ec_backward(sv: SavedEC, dy: torch.Tensor, grad_aux: Optional[torch.Tensor],
     dx = _gather_dx(dxp, sel.src_row, T, d, residual=dxp[A:])
     if not need_weights:
         return Grads(dx, None, dw_out, None, None, None)
-    dw1, dw2, dw3 = _expert_weight_grads(sv.h, dyperm, sv.xperm, dgu, sel.offsets, A, E, d, F)
+    dw1, dw2, dw3 = _expert_weight_grads(sv.h, dyperm, sv.xperm, dgu, sel.offsets, A, E, d, F, bw.plain)
     return Grads(dx, dw_in, dw_out, dw1, dw2, dw3)
 
 
@@ -404,7 +429,7 @@ def experts_backward(dy, yperm, gu, h, xperm, slot_row, slot_w, offsets, A, bw: 
     dx = _gather_dx(dxp, slot_row, T, d)
     if not need_weights:
         return dx, dw, None, None, None
-    dw1, dw2, dw3 = _expert_weight_grads(h, dyperm, xperm, dgu, offsets, A, E, d, F)
+    dw1, dw2, dw3 = _expert_weight_grads(h, dyperm, xperm, dgu, offsets, A, E, d, F, bw.plain)
     return dx, dw, dw1, dw2, dw3
 
 

@@ -90,7 +90,7 @@ class MoEFFNBlock(nn.Module):
         ffn = self.ffn
         if not isinstance(self.ffn_norm, RMSNorm) or ffn.routing_type == "expert_choice":
             return False
-        if ffn.grouped_experts.use_fp8 or ffn.router.balanced_routing:
+        if ffn.grouped_experts.use_fp8 or ffn.router.balanced_routing or not ffn.grouped_experts.gated:
             return False
         if self.training and self.residual_dropout.p > 0:
             return False
@@ -238,5 +238,5 @@ class _BlockTrainFn(torch.autograd.Function):
         dh = dh.view(B, S, d).to(h_dtype)
         if not need_w:
             return dh, dg, None, None, None, None, None, None, None, None
-        return (dh, dg, dw_mod, lg.dw_in.to(w_in.dtype), lg.dw_out.to(w_out.dtype), lg.dw1.to(ge.w1.dtype),
-                lg.dw2.to(ge.w2.dtype), lg.dw3.to(ge.w3.dtype), None, None)
+        return (dh, dg, dw_mod, lg.dw_in.to(w_in.dtype), lg.dw_out.to(w_out.dtype),
+                *ge.cast_grads(lg.dw1, lg.dw2, lg.dw3), None, None)

@@ -79,6 +79,8 @@ def copy_experts(model_sd: Dict[str, torch.Tensor], moves: Iterable[Tuple[int, i
         for w in _EXPERT_KEYS:
             sk = f"{prefix}{sl}.ffn.grouped_experts.{w}"
             dk = f"{prefix}{dl}.ffn.grouped_experts.{w}"
+            if w == "w3" and sk not in model_sd and dk not in model_sd:
+                continue  # non-gated experts have w1 and w2 only
             if sk not in model_sd or dk not in model_sd:
                 raise KeyError(f"kmoe.copy_experts: missing {sk if sk not in model_sd else dk}")
             src, dst = model_sd[sk], model_sd[dk]
@@ -118,7 +120,9 @@ def _layout_meta(E: int, d: int, F: int, fp8: bool) -> Dict[str, str]:
 def save_packed(experts, path: str) -> None:
     """Write the experts' packed weights (GroupedExperts / GroupedExpertsExpertChoice,
     bf16 or fp8 with scales), the source fingerprint and the packed layout's version
-    and sizes to a safetensors file."""
+    and sizes to a safetensors file.  Gated (swiglu) experts only."""
+    if not getattr(experts, "gated", True):
+        raise ValueError("kmoe: packed-weight files hold gated (swiglu) experts only")
     pw = experts.packed()
     tensors = {"w13": pw.w13, "w3": pw.w3}
     if pw.fp8:
@@ -134,6 +138,8 @@ def packed_file_matches(experts, path: str) -> bool:
     (layout and ABI versions, buffer sizes).  Reads the metadata and tensor shapes only."""
     from safetensors import safe_open
 
+    if not getattr(experts, "gated", True):
+        return False  # packed-weight files hold gated (swiglu) experts only
     with safe_open(path, framework="pt") as f:
         meta = f.metadata() or {}
         if meta.get("kmoe_packed") != "1":

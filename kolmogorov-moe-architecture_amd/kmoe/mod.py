@@ -103,7 +103,7 @@ class _MoDTrainFn(torch.autograd.Function):
             return dx, dres, None, None, None, None, None, None, None, None
         lg = g.layer
         return (dx, dres, g.dw_mod.view_as(w_mod).to(w_mod.dtype), lg.dw_in.to(w_in.dtype), lg.dw_out.to(w_out.dtype),
-                lg.dw1.to(ge.w1.dtype), lg.dw2.to(ge.w2.dtype), lg.dw3.to(ge.w3.dtype), None, None)
+                *ge.cast_grads(lg.dw1, lg.dw2, lg.dw3), None, None)
 
 
 def mod_trainable(ffn: MoELayer, mod_router: MoDRouter, *inputs) -> bool:

@@ -176,32 +176,62 @@ class _PackedExperts(nn.Module):
 
     def __init__(self, n_experts: int, d_model: int, d_ff: int, activation: str = "swiglu"):
         super().__init__()
-        if activation != "swiglu":
-            raise NotImplementedError(f"kmoe: expert activation {activation!r} (only swiglu is implemented)")
         self.n_experts = n_experts
         self.d_model = d_model
         self.d_ff = d_ff
         self.activation = activation
+        # swiglu: (silu(x w1) * (x w2)) w3; any other activation string: silu(x w1) w2, with
+        # w2 (E, F, d) and no w3 (moe.py:180-191, 275-283)
+        self.gated = activation == "swiglu"
         self.w1 = nn.Parameter(torch.empty(n_experts, d_model, d_ff))
-        self.w2 = nn.Parameter(torch.empty(n_experts, d_model, d_ff))
-        self.w3 = nn.Parameter(torch.empty(n_experts, d_ff, d_model))
+        if self.gated:
+            self.w2 = nn.Parameter(torch.empty(n_experts, d_model, d_ff))
+            self.w3 = nn.Parameter(torch.empty(n_experts, d_ff, d_model))
+        else:
+            self.w2 = nn.Parameter(torch.empty(n_experts, d_ff, d_model))
+            self.register_parameter("w3", None)
         _init_expert_weights(self.w1, self.w2, self.w3)
         self._packed = None
         self.use_fp8 = False
 
+    def _weights(self):
+        return tuple(w for w in (self.w1, self.w2, self.w3) if w is not None)
+
     def _packed_key(self):
-        return tuple((w.data_ptr(), w._version, w.device) for w in (self.w1, self.w2, self.w3)) + (self.use_fp8,)
+        return tuple((w.data_ptr(), w._version, w.device) for w in self._weights()) + (self.use_fp8,)
+
+    def cast_grads(self, dw1, dw2, dw3):
+        """The weight gradients in the parameters' dtypes (dw3 None for non-gated experts)."""
+        if dw1 is None:
+            return None, None, None
+        return (dw1.to(self.w1.dtype), dw2.to(self.w2.dtype), None if self.w3 is None else dw3.to(self.w3.dtype))
+
+    def expert_rows(self, x2d, row_token, offsets, A, xperm=None, save=False):
+        """The experts on A routed rows: (yperm (A, d), h, pre-activations or None).  Gated:
+        the gate/up GEMM gathers x2d[row_token[r]] itself (with save, the pre-activation
+        gate/up values for the backward); non-gated: from the permuted rows xperm (the
+        pre-activation x w1 is always returned)."""
+        pw = self.packed()
+        if not self.gated:
+            return ops.plain_ffn(xperm, offsets, pw, A)
+        if save:
+            h, gu = ops.gemm_gate_up_rows(x2d, None, row_token, offsets, pw, A, save_gu=True)
+        else:
+            h, gu = ops.gemm_gate_up_rows(x2d, None, row_token, offsets, pw, A), None
+        return ops.gemm_down(h, None, offsets, pw, A), h, gu
 
     def install_packed(self, pw: ops.PackedWeights) -> None:
         """Use `pw` (packed from exactly the current w1/w2/w3, e.g. read back from disk)
         until a parameter changes."""
+        if not self.gated:
+            raise ValueError("kmoe: packed-weight files hold gated (swiglu) experts only")
         if (pw.E, pw.d, pw.F, pw.fp8) != (self.n_experts, self.d_model, self.d_ff, self.use_fp8):
             raise ValueError("kmoe: packed weights do not match the experts' shapes / fp8 mode")
         self._packed = (self._packed_key(), pw)
 
     def bwd_packed(self) -> _bwd.BwdWeights:
         """Backward packed weights (no router part), rebuilt only when a parameter changed."""
-        key = tuple((w.data_ptr(), w._version) for w in (self.w1, self.w2, self.w3))
+        key = tuple((w.data_ptr(), w._version) for w in self._weights())
         cache = getattr(self, "_bwd_cache", None)
         if cache is None or cache[0] != key:
             with torch.no_grad():
@@ -222,7 +252,12 @@ class _PackedExperts(nn.Module):
         key = self._packed_key()
         if self._packed is None or self._packed[0] != key:
             with torch.no_grad():
-                pw = ops.pack_weights(self.w1.detach(), self.w2.detach(), self.w3.detach(), fp8=self.use_fp8)
+                if not self.gated:
+                    if self.use_fp8:
+                        raise NotImplementedError("kmoe: fp8 non-gated experts are not implemented")
+                    pw = ops.pack_weights_plain(self.w1.detach(), self.w2.detach())
+                else:
+                    pw = ops.pack_weights(self.w1.detach(), self.w2.detach(), self.w3.detach(), fp8=self.use_fp8)
             self._packed = (key, pw)
         return self._packed[1]
 
@@ -244,6 +279,11 @@ class GroupedExperts(_PackedExperts):
             disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=capacity, fp8=True,
                                 row_index=row_index, block_counts=block_counts)
             yperm = ops.grouped_ffn(disp.xperm, disp.xscale, disp.offsets, pw, T * k)
+        elif not self.gated:
+            # non-gated experts run on the permuted rows (materialised by the dispatch)
+            disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=capacity, row_index=row_index,
+                                materialize=True, block_counts=block_counts)
+            yperm = ops.plain_ffn(disp.xperm, disp.offsets, pw, T * k)[0]
         else:
             # bf16: the gate/up GEMM gathers the token rows itself (no permuted copy of x)
             disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=capacity,
@@ -335,8 +375,7 @@ class _MoETrainFn(torch.autograd.Function):
         dx = g.dx.view(B, S, d).to(x_dtype)
         if not need_w:
             return dx, None, None, None, None, None, None
-        return (dx, g.dw_in.to(w_in.dtype), g.dw_out.to(w_out.dtype), g.dw1.to(ge.w1.dtype), g.dw2.to(ge.w2.dtype),
-                g.dw3.to(ge.w3.dtype), None)
+        return (dx, g.dw_in.to(w_in.dtype), g.dw_out.to(w_out.dtype), *ge.cast_grads(g.dw1, g.dw2, g.dw3), None)
 
 
 def _once(ctx):
@@ -422,10 +461,8 @@ class _ExpertsFn(torch.autograd.Function):
         T, k = idx.shape
         E = experts.n_experts
         xb = x2d.detach().to(torch.bfloat16).contiguous()
-        pw = experts.packed()
         disp = ops.dispatch(xb, idx, w.detach(), E, materialize=True)
-        h, gu = ops.gemm_gate_up_rows(xb, None, disp.row_token, disp.offsets, pw, T * k, save_gu=True)
-        yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
+        yperm, h, gu = experts.expert_rows(xb, disp.row_token, disp.offsets, T * k, xperm=disp.xperm, save=True)
         out_dtype = torch.float32 if x2d.dtype == torch.float32 else torch.bfloat16
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T, out_dtype=out_dtype)
         ctx.sv = (disp, h, gu, yperm)
@@ -443,7 +480,7 @@ class _ExpertsFn(torch.autograd.Function):
         dx, dw, dw1, dw2, dw3 = _bwd.experts_backward(dy, yperm, gu, h, disp.xperm, disp.slot_row.view(T, k),
                                                       disp.slot_w.view(T, k), disp.offsets, T * k, ge.bwd_packed(),
                                                       ge.n_experts, ge.d_ff, need_weights=need_w)
-        wg = (None, None, None) if dw1 is None else (dw1.to(ge.w1.dtype), dw2.to(ge.w2.dtype), dw3.to(ge.w3.dtype))
+        wg = ge.cast_grads(dw1, dw2, dw3)
         return (dx.to(x_dtype), dw.to(w_dtype), *wg, None, None)
 
 
@@ -458,10 +495,8 @@ class _ExpertsECFn(torch.autograd.Function):
         sel = experts.tables(token_indices, w, S)
         xb = x3d.detach().reshape(B * S, d).to(torch.bfloat16).contiguous()
         A = E * B * C
-        pw = experts.packed()
         xperm, _ = ops.gather_rows(xb, sel.row_token, A)
-        h, gu = ops.gemm_gate_up_rows(xb, None, sel.row_token, sel.offsets, pw, A, save_gu=True)
-        yperm = ops.gemm_down(h, None, sel.offsets, pw, A)
+        yperm, h, gu = experts.expert_rows(xb, sel.row_token, sel.offsets, A, xperm=xperm, save=True)
         out_dtype = torch.float32 if x3d.dtype == torch.float32 else torch.bfloat16
         y = ops.combine(yperm, sel.src_row, sel.src_w, B * S, out_dtype=out_dtype)
         ctx.sv = (sel, h, gu, yperm, xperm)
@@ -482,7 +517,7 @@ class _ExpertsECFn(torch.autograd.Function):
         tok = (torch.arange(B, device=dy.device).view(B, 1, 1) * S + sel.idx).reshape(-1)
         ex = torch.arange(E, device=dy.device).view(1, E, 1).expand_as(sel.idx).reshape(-1)
         dw = dw_te[tok, ex].view(sel.idx.shape)
-        wg = (None, None, None) if dw1 is None else (dw1.to(ge.w1.dtype), dw2.to(ge.w2.dtype), dw3.to(ge.w3.dtype))
+        wg = ge.cast_grads(dw1, dw2, dw3)
         return (dx.view(B, S, d).to(x_dtype), dw.to(w_dtype), *wg, None, None)
 
 
@@ -500,10 +535,8 @@ class _MoEECTrainFn(torch.autograd.Function):
         r, sel, C = layer.router.route(xb, descending=False, save_hidden=True)
         x2d = xb.reshape(T, d)
         A = E * B * C
-        pw = ge.packed()
         xperm, _ = ops.gather_rows(x2d, sel.row_token, A)
-        h, gu = ops.gemm_gate_up_rows(x2d, None, sel.row_token, sel.offsets, pw, A, save_gu=True)
-        yperm = ops.gemm_down(h, None, sel.offsets, pw, A)
+        yperm, h, gu = ge.expert_rows(x2d, sel.row_token, sel.offsets, A, xperm=xperm, save=True)
         y = ops.combine(yperm, sel.src_row, sel.src_w, T, out_dtype=layer._out_dtype(x))
         has_aux = layer.training and layer.router_z_loss_weight > 0
         aux = (ops.aux_loss(r.partials, T, E, None, 1, 0.0, layer.router_z_loss_weight)[0] if has_aux
@@ -526,8 +559,7 @@ class _MoEECTrainFn(torch.autograd.Function):
         dx = g.dx.view(sv.B, sv.S, -1).to(x_dtype)
         if not need_w:
             return dx, None, g.dw_out.to(w_out.dtype), None, None, None, None
-        return (dx, g.dw_in.to(w_in.dtype), g.dw_out.to(w_out.dtype), g.dw1.to(ge.w1.dtype), g.dw2.to(ge.w2.dtype),
-                g.dw3.to(ge.w3.dtype), None)
+        return (dx, g.dw_in.to(w_in.dtype), g.dw_out.to(w_out.dtype), *ge.cast_grads(g.dw1, g.dw2, g.dw3), None)
 
 
 class MoELayer(nn.Module):
@@ -548,6 +580,8 @@ class MoELayer(nn.Module):
         self.expert_parallel_layer = None
         self.drop_overflow = bool(getattr(config, "moe_drop_overflow", False))
         use_fp8 = bool(getattr(config, "moe_fp8", False))
+        if use_fp8 and getattr(config, "ffn_activation", "swiglu") != "swiglu":
+            raise NotImplementedError("kmoe: fp8 experts are implemented for swiglu only")
         if self.routing_type == "expert_choice":
             self.router = ExpertChoiceRouter(config)
             self.grouped_experts = None
@@ -596,7 +630,7 @@ class MoELayer(nn.Module):
         """Backward packed weights, rebuilt only when a parameter changed."""
         ge = self.grouped_experts if self.grouped_experts is not None else self.grouped_experts_ec
         w_in = self.router.router[0].weight
-        key = tuple((w.data_ptr(), w._version) for w in (ge.w1, ge.w2, ge.w3, w_in))
+        key = tuple((w.data_ptr(), w._version) for w in ge._weights() + (w_in,))
         cache = getattr(self, "_bwd_cache", None)
         if cache is None or cache[0] != key:
             with torch.no_grad():
@@ -612,12 +646,10 @@ class MoELayer(nn.Module):
         ge = self.grouped_experts
         k, E = self.top_k, self.n_experts
         cap = ops.capacity_of(self.capacity_factor, T, k, E) if self.drop_overflow else 0
-        pw = ge.packed()
-        # the permuted x rows are kept for the weight gradient (the gate/up GEMM still
+        # the permuted x rows are kept for the weight gradient (the gated gate/up GEMM still
         # gathers its own A rows from x)
         disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=True, block_counts=r.block_counts)
-        h, gu = ops.gemm_gate_up_rows(x2d, None, disp.row_token, disp.offsets, pw, T * k, save_gu=True)
-        yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
+        yperm, h, gu = ge.expert_rows(x2d, disp.row_token, disp.offsets, T * k, xperm=disp.xperm, save=True)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T if T_out is None else T_out,
                         out_map=out_map, scale=scale, out_dtype=out_dtype, residual=residual)
         self.last_expert_counts = disp.counts

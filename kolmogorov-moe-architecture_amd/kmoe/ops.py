@@ -337,8 +337,62 @@ def quant_rows_fp8(m, n_rows_dev=None):
     return q, s
 
 
+class PlainPacked(NamedTuple):
+    """Packed weights of non-gated experts (silu(x w1) w2): w1t (rows f of w1^T), w2t (rows n of w2^T)."""
+    w1t: torch.Tensor
+    w2t: torch.Tensor
+    E: int
+    d: int
+    F: int
+    fp8: bool = False
+
+
+def pack_weights_plain(w1, w2) -> PlainPacked:
+    """Derived kernel layout of non-gated expert weights w1 (E,d,F), w2 (E,F,d) (moe.py:187-191)."""
+    _need_gpu(w1, w2)
+    E, d, F = w1.shape
+    if w2.shape != (E, F, d):
+        raise ValueError("kmoe.pack_weights_plain: w1 must be (E,d,F) and w2 (E,F,d)")
+    if w1.dtype not in (torch.float32, _BF16):
+        raise ValueError(f"kmoe.pack_weights_plain: unsupported weight dtype {w1.dtype}")
+    dt = w1.dtype
+    w1, w2 = _contig(w1, dt), _contig(w2, dt)
+    lib = _lib.load()
+    dev = w1.device
+    w1t = torch.empty(lib.kmoe_packed_w1t_bytes(E, d, F), device=dev, dtype=torch.uint8)
+    w2t = torch.empty(lib.kmoe_packed_w3_bytes(E, d, F, _lib.DTYPE_BF16), device=dev, dtype=torch.uint8)
+    _lib.call("kmoe_pack_weights_plain", ptr(w1), ptr(w2), _lib.DTYPE_F32 if dt == torch.float32 else _lib.DTYPE_BF16,
+              E, d, F, ptr(w1t), ptr(w2t), _stream(w1))
+    return PlainPacked(w1t, w2t, E, d, F)
+
+
+def plain_ffn(xperm, offsets, pp: PlainPacked, max_rows):
+    """Non-gated experts on the permuted rows (moe.py:281-283): p = x w1, h = silu(p),
+    y = h w2.  Returns (yperm (max_rows, d), h, p) bf16."""
+    E, d, F = pp.E, pp.d, pp.F
+    lib = _lib.load()
+    Fp = lib.kmoe_padded_ff(F)
+    dev = xperm.device
+    s = _stream(xperm)
+    rows = max(max_rows, 1)
+    p = torch.empty(rows, Fp, device=dev, dtype=_BF16)
+    h = torch.empty(rows, Fp, device=dev, dtype=_BF16)
+    y = torch.empty(rows, d, device=dev, dtype=_BF16)
+    with _Stage("gemm_gate_up"):
+        _lib.call("kmoe_gemm_grouped", ptr(xperm), ptr(offsets), E, d, max_rows, ptr(pp.w1t), (F + 255) // 256 * 256,
+                  Fp, ptr(p), Fp, Fp, s)
+    with _Stage("silu"):
+        _lib.call("kmoe_silu_rows", ptr(p), max_rows, ptr(offsets[E:]), F, ptr(h), s)
+    with _Stage("gemm_down"):
+        _lib.call("kmoe_gemm_grouped", ptr(h), ptr(offsets), E, Fp, max_rows, ptr(pp.w2t), (d + 255) // 256 * 256, d,
+                  ptr(y), d, d, s)
+    return y, h, p
+
+
 def grouped_ffn(xperm, xscale, offsets, pw: PackedWeights, max_rows):
     """gate_up -> (fp8: per-row requant of h) -> down.  Returns yperm (max_rows, d) bf16."""
+    if isinstance(pw, PlainPacked):
+        return plain_ffn(xperm, offsets, pw, max_rows)[0]
     h = gemm_gate_up(xperm, xscale, offsets, pw, max_rows)
     if pw.fp8:
         hq, hs = quant_rows_fp8(h, offsets[pw.E:])

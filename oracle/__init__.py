@@ -17,6 +17,7 @@ Pinning (how each oracle function is checked independently, tests/test_oracle.py
                      counts with uniform probabilities; brute-force loops
   dispatch           numpy/torch stable argsort + bincount (library routines); brute force
   swiglu_rows        fp64 per-token brute force
+  plain_rows         fp64 per-token, per-unit loops; torch_port's padded bmm with w3 None
   combine            brute-force per-token sums
   ec_select          brute-force sort on (-logit, index); torch.topk on tie-free columns
   mod_select         brute-force sort; torch.topk + sort on tie-free rows

@@ -134,7 +134,10 @@ def dispatch(idx, E, capacity=0):
 def swiglu_rows(xrows, offsets, w1, w2, w3, dtype=np.float32):
     """Per-expert SwiGLU on expert-contiguous rows:
     y = (silu(x W1[e]) * (x W2[e])) W3[e]  (moe.py:275-279, ffn.py:17-64,
-    kernels/__init__.py:59-102)."""
+    kernels/__init__.py:59-102).  w3 None: the non-gated experts of an activation other
+    than swiglu, y = silu(x W1[e]) W2[e] with W2 (E, F, d) (moe.py:180-191, 281-283)."""
+    if w3 is None:
+        return plain_rows(xrows, offsets, w1, w2, dtype=dtype)
     E = w1.shape[0]
     y = np.zeros((xrows.shape[0], w3.shape[2]), dtype=dtype)
     for e in range(E):
@@ -144,6 +147,18 @@ def swiglu_rows(xrows, offsets, w1, w2, w3, dtype=np.float32):
         xe = xrows[lo:hi].astype(dtype)
         h = silu(xe @ w1[e].astype(dtype)) * (xe @ w2[e].astype(dtype))
         y[lo:hi] = h @ w3[e].astype(dtype)
+    return y
+
+
+def plain_rows(xrows, offsets, w1, w2, dtype=np.float32):
+    """Non-gated experts on expert-contiguous rows: y = silu(x W1[e]) W2[e] (moe.py:281-283)."""
+    E = w1.shape[0]
+    y = np.zeros((xrows.shape[0], w2.shape[2]), dtype=dtype)
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi <= lo:
+            continue
+        y[lo:hi] = silu(xrows[lo:hi].astype(dtype) @ w1[e].astype(dtype)) @ w2[e].astype(dtype)
     return y
 
 

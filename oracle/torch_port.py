@@ -53,6 +53,14 @@ def balanced_topk_tc(probs, k):
     return wts / (wts.sum(dim=-1, keepdim=True) + 1e-9), sel
 
 
+def _expert_bmm(padded, w1, w2, w3):
+    """The experts' batched products (moe.py:275-283): swiglu (silu(x w1) * (x w2)) w3, or,
+    with w3 None, the non-gated silu(x w1) w2."""
+    if w3 is None:
+        return torch.bmm(F.silu(torch.bmm(padded, w1)), w2)
+    return torch.bmm(F.silu(torch.bmm(padded, w1)) * torch.bmm(padded, w2), w3)
+
+
 def grouped_experts_tc(x, idx, w, w1, w2, w3):
     """GroupedExperts.forward's padded-bmm formulation."""
     n_tok, k = idx.shape
@@ -72,8 +80,7 @@ def grouped_experts_tc(x, idx, w, w1, w2, w3):
     pos = torch.arange(s_tok.numel()) - starts[s_e]
     padded = x.new_zeros(E, m, x.shape[1])
     padded[s_e, pos] = rows
-    h = F.silu(torch.bmm(padded, w1)) * torch.bmm(padded, w2)
-    out = torch.bmm(h, w3)
+    out = _expert_bmm(padded, w1, w2, w3)
     contrib = out[s_e, pos] * s_w.unsqueeze(1)
     y = x.new_zeros(x.shape)
     y.index_add_(0, s_tok, contrib)
@@ -138,8 +145,7 @@ def moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity=0, bias=None, trai
         m = int(pos.max().item()) + 1
         padded = x2d.new_zeros(E, m, d)
         padded = padded.index_put((s_e, pos), x2d[s_tok])
-        h = F.silu(torch.bmm(padded, w1)) * torch.bmm(padded, w2)
-        out = torch.bmm(h, w3)
+        out = _expert_bmm(padded, w1, w2, w3)
         y = y.index_add(0, s_tok, out[s_e, pos] * s_w.unsqueeze(1))
     aux = x2d.new_zeros(())
     if training:
@@ -197,8 +203,9 @@ def grouped_experts_ec_tc(x3d, ew, ti, w1, w2, w3):
     _, E, C = ti.shape
     gi = ti.unsqueeze(-1).expand(-1, -1, -1, d)
     xin = torch.gather(x3d.unsqueeze(1).expand(-1, E, -1, -1), 2, gi).reshape(B * E, C, d)
-    W1, W2, W3 = w1.repeat(B, 1, 1), w2.repeat(B, 1, 1), w3.repeat(B, 1, 1)
-    out = torch.bmm(F.silu(torch.bmm(xin, W1)) * torch.bmm(xin, W2), W3).view(B, E, C, d)
+    W1, W2 = w1.repeat(B, 1, 1), w2.repeat(B, 1, 1)
+    W3 = None if w3 is None else w3.repeat(B, 1, 1)
+    out = _expert_bmm(xin, W1, W2, W3).view(B, E, C, d)
     wout = out * ew.unsqueeze(-1)
     y = x3d.new_zeros(B, S, d)
     return y.scatter_add(1, ti.reshape(B, E * C).unsqueeze(-1).expand(-1, -1, d), wout.reshape(B, E * C, d))

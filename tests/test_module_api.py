@@ -61,7 +61,22 @@ def test_unsupported_modes_fail_loudly():
     with pytest.raises(NotImplementedError):
         MoELayer(AdvancedMoEConfig(d_model=128, moe_implementation="expert_parallel"), 0)
     with pytest.raises(NotImplementedError):
-        MoELayer(AdvancedMoEConfig(d_model=128, ffn_activation="gelu"), 0)
+        MoELayer(AdvancedMoEConfig(d_model=128, ffn_activation="gelu", moe_fp8=True), 0)
+
+
+@pytest.mark.parametrize("routing", ["token_choice", "expert_choice"])
+def test_non_gated_expert_keys(routing):
+    """An activation other than swiglu gives the reference's two-matrix experts
+    (moe.py:180-191): w1 (E, d, F), w2 (E, F, d), no w3; silu(x w1) w2 whatever the name."""
+    cfg = AdvancedMoEConfig(d_model=128, n_experts=4, d_ff_expert=96, ffn_activation="gelu", moe_routing=routing)
+    m = MoELayer(cfg, 0)
+    ge = m.grouped_experts if routing == "token_choice" else m.grouped_experts_ec
+    pre = "grouped_experts." if routing == "token_choice" else "grouped_experts_ec."
+    sd = m.state_dict()
+    assert {k for k in sd if k.startswith(pre)} == {pre + "w1", pre + "w2"}
+    assert ge.w1.shape == (4, 128, 96) and ge.w2.shape == (4, 96, 128) and ge.w3 is None and not ge.gated
+    bound = 1.0 / 128 ** 0.5  # per-expert kaiming-uniform bound of w1 (fan_in d), moe.py:194-211
+    assert float(ge.w1.detach().abs().max()) <= bound and float(ge.w2.detach().abs().max()) <= 1.0 / 96 ** 0.5
 
 
 def test_cpu_input_is_rejected():

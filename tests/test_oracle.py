@@ -715,3 +715,55 @@ def test_ffn_half_loss_gradcheck():
         return P.ffn_half_loss_routed(h, w_in, w_out, w1, w2, w3, torch.from_numpy(idx), c["dy"], norm_w=nw,
                                       w_mod=w_mod, sel_idx=torch.from_numpy(sel))
     assert torch.autograd.gradcheck(f, ins, eps=1e-6, atol=1e-5, rtol=1e-4)
+
+
+# ------------------------------------------------------------------ non-gated experts
+def test_plain_rows_bruteforce():
+    """plain_rows (silu(x W1[e]) W2[e], moe.py:281-283) against a per-token, per-unit fp64
+    loop; and the torch port's padded-bmm experts with w3 None against dispatch +
+    plain_rows + combine of the numpy oracle (two restatements)."""
+    rng = np.random.default_rng(41)
+    T, d, E, k, F_ = 13, 6, 3, 2, 5
+    x = rng.standard_normal((T, d))
+    w1 = rng.standard_normal((E, d, F_)) * 0.4
+    w2 = rng.standard_normal((E, F_, d)) * 0.4
+    idx, w = O.topk_select(rng.standard_normal((T, E)), k)
+    dp = O.dispatch(idx, E)
+    rows = x[dp["row_token"][: dp["offsets"][E]]]
+    got = O.plain_rows(rows, dp["offsets"], w1, w2, dtype=np.float64)
+    want = np.zeros_like(got)
+    for e in range(E):
+        for r in range(int(dp["offsets"][e]), int(dp["offsets"][e + 1])):
+            for f in range(F_):
+                a = sum(rows[r, i] * w1[e, i, f] for i in range(d))
+                want[r] += a / (1.0 + math.exp(-a)) * w2[e, f]
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+    assert np.array_equal(O.swiglu_rows(rows, dp["offsets"], w1, w2, None, dtype=np.float64), got)
+    y_np = O.combine(got, dp["slot_row"].reshape(T, k), w)
+    y_t = P.grouped_experts_tc(torch.from_numpy(x), torch.from_numpy(idx), torch.from_numpy(w), torch.from_numpy(w1),
+                               torch.from_numpy(w2), None)
+    assert np.allclose(y_t.numpy(), y_np, rtol=1e-12, atol=1e-12)
+
+
+def test_plain_routed_losses_gradcheck():
+    """The backward references with non-gated experts: token choice at its own routing
+    equals moe_layer_tc's forward, and both routed losses pass finite differences."""
+    g = torch.Generator().manual_seed(43)
+    mk = lambda *s: (torch.randn(*s, generator=g, dtype=torch.float64) * 0.5).requires_grad_(True)
+    x, w_in, w_out, w1, w2 = mk(9, 6), mk(128, 6), mk(4, 128), mk(4, 6, 5), mk(4, 5, 6)
+    dy = torch.randn(9, 6, generator=g, dtype=torch.float64)
+    with torch.no_grad():
+        y, aux = P.moe_layer_tc(x[None], w_in, w_out, w1, w2, None, 2, training=True)
+        _, idx, _ = P.router_tc(x[None], w_in, w_out, 2)
+        got = P.moe_loss_tc_routed(x, w_in, w_out, w1, w2, None, idx[0], dy, training=True)
+    # (aux_tc counts in float32: 1e-8 relative)
+    assert abs(float(got) - float((y[0] * dy).sum() + aux)) < 1e-8 * max(1.0, abs(float(got)))
+    f = lambda *a: P.moe_loss_tc_routed(*a, None, idx[0], dy, training=True)
+    assert torch.autograd.gradcheck(f, (x, w_in, w_out, w1, w2), eps=1e-6, atol=1e-6, rtol=1e-5)
+    xe, wi, wo, e1, e2, _, dye = _tiny_ec(44)
+    e2 = (torch.randn(3, 5, 6, generator=g, dtype=torch.float64) * 0.5).requires_grad_(True)
+    with torch.no_grad():
+        logits = torch.nn.functional.linear(torch.nn.functional.silu(torch.nn.functional.linear(xe, wi)), wo)
+        ti = torch.topk(torch.softmax(logits.transpose(1, 2), -1), 4, dim=-1).indices
+    fe = lambda *a: P.moe_loss_ec_routed(*a, None, ti, dye, training=True, w_z=0.3)
+    assert torch.autograd.gradcheck(fe, (xe, wi, wo, e1, e2), eps=1e-6, atol=1e-6, rtol=1e-5)
