@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other configurations' summary (the 'configs' object)")
     ap.add_argument("--config-steps", type=int, default=20, help="timed forwards per other configuration")
+    ap.add_argument("--no-library-gemm", dest="library_gemm", action="store_false",
+                    help="skip the vendor-library dense GEMM reference (library_gemm)")
     return ap.parse_args()
 
 
@@ -469,6 +471,36 @@ def run_cpu_baseline(wl, tokens):
             "seconds_per_forward": round(med, 3)}
 
 
+def library_gemm_reference(wl, a_kept, gu_us):
+    """The vendor library's dense bf16 GEMM (torch.mm -> hipBLASLt) of the gate/up shape in
+    the same process: (A_kept x d) @ (d x 2F), no grouping and no row gather, K-steps of
+    the same size.  A reference for the grouped kernel's rate on this box (same clock and
+    power limit), not a replacement: the grouped GEMM has 16 ragged expert groups."""
+    import torch
+    g = torch.Generator().manual_seed(wl.seed + 400)
+    a = (torch.randn(a_kept, wl.d, generator=g) * 0.5).to(torch.bfloat16).to("cuda:0")
+    b = (torch.randn(wl.d, 2 * wl.F, generator=g) * 0.02).to(torch.bfloat16).to("cuda:0")
+    for _ in range(3):
+        torch.mm(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = 20
+    e0.record()
+    for _ in range(n):
+        torch.mm(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    lib_us = e0.elapsed_time(e1) / n * 1e3
+    flops = 4.0 * wl.d * wl.F * a_kept
+    del a, b
+    torch.cuda.empty_cache()
+    return {"shape": f"({a_kept} x {wl.d}) @ ({wl.d} x {2 * wl.F}) bf16", "us": round(lib_us, 2),
+            "TFLOPs": round(flops / (lib_us * 1e-6) / 1e12, 1), "frac_peak": round(flops / (lib_us * 1e-6) / PEAK_BF16, 4),
+            "grouped_gate_up_over_library": round(lib_us / gu_us, 4),
+            "note": "torch.mm (hipBLASLt) on the dense gate/up shape, same process, after the timed region; the grouped "
+                    "kernel additionally gathers its A rows and handles 16 ragged expert groups"}
+
+
 def load_traffic(name):
     path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
     if os.path.exists(path):
@@ -551,6 +583,8 @@ def main():
         out["training"] = res["training"]
     if res.get("block"):
         out["ffn_block"] = res["block"]
+    if not wl.fp8 and args.library_gemm:
+        out["library_gemm"] = library_gemm_reference(wl, res["a_kept"], us)
     if not args.no_configs:
         # the other configurations of BASELINE.json, each with its own timed region
         import argparse as _ap
