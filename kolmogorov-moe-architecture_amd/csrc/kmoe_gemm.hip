@@ -894,22 +894,28 @@ __global__ __launch_bounds__(256) void pack_transpose_kernel(const void* __restr
 }
 
 // Column amax of in[e] (R x Cn) -> per packed row amax (turned into amax/448 by
-// finalize_scale_kernel once the rows have been quantised).
+// finalize_scale_kernel once the rows have been quantised).  Workgroup (column block,
+// row block, expert): each thread takes the max over COLS_ROWS rows of its column and
+// merges it with an integer atomicMax on the float's bits (non-negative floats order
+// like their bit patterns; max is order-independent, so the result is deterministic).
+// The scale buffer starts at 0 (zero_f32_kernel).
+constexpr int COLS_ROWS = 64;
 template <bool IN_F32>
 __global__ __launch_bounds__(256) void col_scale_kernel(const void* __restrict__ in, int R, int Cn,
                                                         int64_t in_expert_stride, int half, bool gate_up,
                                                         float* __restrict__ scale, int64_t out_rows) {
-  const int e = blockIdx.y;
+  const int e = blockIdx.z;
   const int c = blockIdx.x * 256 + threadIdx.x;
   if (c >= Cn) return;
+  const int r0 = blockIdx.y * COLS_ROWS, r1 = min(R, r0 + COLS_ROWS);
   float amax = 0.0f;
-  for (int r = 0; r < R; ++r) {
+  for (int r = r0; r < r1; ++r) {
     const int64_t off = (int64_t)e * in_expert_stride + (int64_t)r * Cn + c;
     const float v = IN_F32 ? static_cast<const float*>(in)[off] : bf16_to_f32(static_cast<const uint16_t*>(in)[off]);
     amax = fmaxf(amax, fabsf(v));
   }
   const int64_t orow = gate_up ? (int64_t)(c / 128) * 256 + half * 128 + (c % 128) : (int64_t)c;
-  scale[(int64_t)e * out_rows + orow] = amax;
+  atomicMax(reinterpret_cast<unsigned int*>(scale + (int64_t)e * out_rows + orow), __float_as_uint(amax));
 }
 
 __global__ void finalize_scale_kernel(float* __restrict__ p, int64_t n) {
@@ -1253,7 +1259,8 @@ extern "C" int kmoe_pack_weights(const void* w1, const void* w2, const void* w3,
   if (fp8) {
     hipLaunchKernelGGL(zero_f32_kernel, dim3(64), dim3(256), 0, s, w13_scale, (int64_t)E * rows13);
     hipLaunchKernelGGL(zero_f32_kernel, dim3(64), dim3(256), 0, s, w3_scale, (int64_t)E * rows3);
-    const dim3 g13((unsigned)kmoe::ceil_div(F, 256), (unsigned)E), g3((unsigned)kmoe::ceil_div(d, 256), (unsigned)E);
+    const dim3 g13((unsigned)kmoe::ceil_div(F, 256), (unsigned)kmoe::ceil_div(d, COLS_ROWS), (unsigned)E);
+    const dim3 g3((unsigned)kmoe::ceil_div(d, 256), (unsigned)kmoe::ceil_div(F, COLS_ROWS), (unsigned)E);
     if (f32) {
       hipLaunchKernelGGL(col_scale_kernel<true>, g13, dim3(256), 0, s, w1, d, F, (int64_t)d * F, 0, true, w13_scale, rows13);
       hipLaunchKernelGGL(col_scale_kernel<true>, g13, dim3(256), 0, s, w2, d, F, (int64_t)d * F, 1, true, w13_scale, rows13);
