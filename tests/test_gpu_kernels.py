@@ -453,14 +453,20 @@ def test_ec_select_token_order(dev, B, S, E, C, ties):
     assert np.array_equal(asc.src_w.cpu().numpy()[sel], src_w[sel].astype(np.float32))
 
 
-@pytest.mark.parametrize("B,S,keep,ties", [(4, 2048, 1536, False), (2, 100, 75, True), (1, 7, 1, False)])
+@pytest.mark.parametrize(
+    "B,S,keep,ties",
+    [(4, 2048, 1536, None), (2, 100, 75, "some"), (1, 7, 1, None), (1, 4096, 3000, "some"), (2, 333, 333, None),
+     (2, 1000, 250, "all"), (1, 5000, 1234, "some")],  # S > 4096: the one-workgroup-per-sequence kernel
+)
 def test_mod_select_parity(dev, B, S, keep, ties):
     d = 256
     g = torch.Generator().manual_seed(41)
     x = torch.randn(B, S, d, generator=g)
     wm = torch.randn(1, d, generator=g) * 0.05
-    if ties:
+    if ties == "some":
         x[:, ::3] = x[:, :1]  # repeated rows -> equal router logits
+    elif ties == "all":
+        x[:] = x[:, :1]  # every logit of a sequence equal: the lowest indices are kept
     xb, wb = bf16(x).to(dev), bf16(wm).to(dev)
     out = ops.mod_select(xb, wb, keep)
     r = npf(out.logits)
