@@ -267,7 +267,12 @@ constexpr int OUT_BF16 = 0, OUT_SPLIT = 1, OUT_F32 = 2;
 // RSCALE (bf16 gathered gate/up tiles): a_scale[row_token[r]] scales row r's gate and
 // up values before the SiLU (the per-token RMSNorm scale of x: the norm weight is
 // folded into the packed w1 / w2 rows, and a per-row scale commutes with the product).
-template <bool GATE_UP, bool FP8, bool GATHER, int WNB, bool SAVE_GU = false, bool RSCALE = false>
+// NMA: the row blocks of this wave that hold rows of the expert.  A wave's 128 rows
+// are 4 blocks of 32; a slot's last tile is often partly empty, and its waves then
+// run with NMA < 4 (the first NMA blocks), which skips the other blocks' fragment
+// reads, MFMAs and epilogue (their accumulators stay 0 and are never stored).  The
+// waves of a workgroup may differ in NMA: loads, LDS writes and barriers are the same.
+template <bool GATE_UP, bool FP8, bool GATHER, int WNB, bool SAVE_GU = false, bool RSCALE = false, int NMA = 4>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e, int m0, int m_end, int nt,
                                           int q) {
   static_assert(WNB == 4 || WNB == 2 || (WNB == 1 && !GATE_UP), "tile width");
@@ -276,7 +281,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   constexpr int TBB = BNT * KB;                  // bytes of one B stage tile
   constexpr int BLK_B = BNT * KB / 1024 / 4;     // B load blocks per wave per step
   constexpr int NBLK = BLK_PER_WAVE + BLK_B;     // load blocks per wave per step
-  constexpr int NM = 4 * WNB;                    // MFMAs per substep
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -371,16 +375,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   };
   Frag<FP8> fa[2][4], fb[2][WNB];
   auto rd = [&](int st, int i, Frag<FP8> (&a)[4], Frag<FP8> (&b)[WNB]) {
-    const uint8_t* la = la_buf(st);
-    const uint8_t* lb = lb_buf(st);
+    if constexpr (NMA > 0) {
+      const uint8_t* la = la_buf(st);
+      const uint8_t* lb = lb_buf(st);
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) read_frag<FP8>(la, wm * 128 + mi * 32 + lr, i, lh, a[mi]);
+      for (int mi = 0; mi < NMA; ++mi) read_frag<FP8>(la, wm * 128 + mi * 32 + lr, i, lh, a[mi]);
 #pragma unroll
-    for (int j = 0; j < WNB; ++j) read_frag<FP8>(lb, b_lds_row<GATE_UP, WNB>(wn, j, lr), i, lh, b[j]);
+      for (int j = 0; j < WNB; ++j) read_frag<FP8>(lb, b_lds_row<GATE_UP, WNB>(wn, j, lr), i, lh, b[j]);
+    }
   };
   auto mma = [&](const Frag<FP8> (&a)[4], const Frag<FP8> (&b)[WNB]) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < NMA; ++mi)
 #pragma unroll
       for (int j = 0; j < WNB; ++j) mfma<FP8>(acc[mi][j], a[mi], b[j]);
   };
@@ -395,7 +401,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   // stage kt+1, whose first fragments are read under the last substep's MFMAs.
   // Register dependencies give the vmcnt waits; the scheduling groups interleave the
   // LDS and memory operations with the MFMAs, fragment reads first.
-  constexpr int RD = (FP8 ? 2 : 1) * (4 + WNB);  // LDS reads of a substep's fragments
+  constexpr int RD = NMA > 0 ? (FP8 ? 2 : 1) * (NMA + WNB) : 0;  // LDS reads of a substep's fragments
+  constexpr int NMS = NMA * WNB;                                    // MFMAs per substep
   constexpr int C1 = (NBLK * 6 + 8) / 16, C2 = (NBLK * 11 + 8) / 16;
   for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 0);
   for (int qq = 0; qq < NBLK; ++qq) write_block(qq, 0);
@@ -428,7 +435,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
         static_for<q0, q1>([&](auto qc) { load_block(decltype(qc)::value, kt + 2); });
       }
       mma(fa[bi], fb[bi]);
-      sched_spread<NM, (RDN ? RD : 0), nq, nq>();
+      sched_spread<NMS, (RDN ? RD : 0), nq, nq>();
       __builtin_amdgcn_sched_barrier(0);
     });
   };
@@ -483,6 +490,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   };
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
+    if (mi >= NMA) break;  // rows past the expert's end: never stored
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
       const int r0 = 2 * p, r1 = 2 * p + 1;
@@ -522,6 +530,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
     uint8_t* const wb2 = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR2 + (lr - (odd ? 1 : 0)) * 2;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
+      if (mi >= NMA) break;
 #pragma unroll
       for (int p = 0; p < 8; ++p) {
 #pragma unroll
@@ -590,9 +599,18 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   int slot, nt, e, m0, m_end;
   dense_tile(t, st.n_slots, n_tiles, slot, nt);
   find_slot(st, E, slot, e, m0, m_end);
-  if (L < base || split == 1)
-    gemm_tile<GATE_UP, FP8, GATHER, 4, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, 0);
-  else if (split == 2)
+  if (L < base || split == 1) {
+    // row blocks of this wave holding rows (wave-uniform): 4 (more than 64 rows), 2, 1, 0
+    const int wrows = m_end - m0 - (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >> 1) * 128;
+    if (wrows > 64)
+      gemm_tile<GATE_UP, FP8, GATHER, 4, SAVE_GU, RSCALE, 4>(g, lds, e, m0, m_end, nt, 0);
+    else if (wrows > 32)
+      gemm_tile<GATE_UP, FP8, GATHER, 4, SAVE_GU, RSCALE, 2>(g, lds, e, m0, m_end, nt, 0);
+    else if (wrows > 0)
+      gemm_tile<GATE_UP, FP8, GATHER, 4, SAVE_GU, RSCALE, 1>(g, lds, e, m0, m_end, nt, 0);
+    else
+      gemm_tile<GATE_UP, FP8, GATHER, 4, SAVE_GU, RSCALE, 0>(g, lds, e, m0, m_end, nt, 0);
+  } else if (split == 2)
     gemm_tile<GATE_UP, FP8, GATHER, 2, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, q);
   else if constexpr (!GATE_UP)
     gemm_tile<GATE_UP, FP8, GATHER, 1, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, q);
