@@ -65,7 +65,7 @@ int kmoe_pack_layout_version(void);
  * ExpertChoiceRouter.forward (moe.py:513-514).
  *   logits[t,:] = SiLU(x[row(t)] . w_in^T) . w_out^T  (+ logit_bias), fp32 accumulate
  *   row(t) = row_index ? row_index[t] : t
- * When k > 0 it also selects the top-k experts of each token, ranked by fp32
+ * When k > 0 (k <= min(8, E)) it also selects the top-k experts of each token, ranked by fp32
  * logit (descending; equal logits -> lowest expert index first), and writes the
  * renormalised softmax weights  w_j = p_j / sum_sel p  (moe.py:441,455-460).
  * `partials` (nullable) receives per-block sums for the aux losses; its length in

@@ -103,18 +103,38 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
   const int64_t a1 = min<int64_t>(a0 + (int64_t)DTB * k, T * k);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   if (tid < E) running[tid] = 0;
+  auto load_w = [&](int64_t a) -> float {
+    return w_dtype == KMOE_DTYPE_F32 ? static_cast<const float*>(wsrc)[a]
+                                     : bf16_to_f32(static_cast<const uint16_t*>(wsrc)[a]);
+  };
+  // the first chunk's expert ids and weights are loaded before the scan, so their round
+  // trips overlap the block-count loads
+  bool valid = a0 + tid < a1;
+  int e = valid ? load_expert(idx, a0 + tid, E) : -1;
+  float wv = valid ? load_w(a0 + tid) : 0.0f;
   if constexpr (FUSED_SCAN) {
     // thread (j, e) of an ep x (DTHREADS/ep) grid sums blocks j, j + DTHREADS/ep, ...
     __shared__ int red_pre[DTHREADS], red_tot[DTHREADS];
     int ep = 1;
     while (ep < E) ep <<= 1;
-    const int e = tid & (ep - 1), j = tid / ep, ng = DTHREADS / ep;
+    const int ex = tid & (ep - 1), j = tid / ep, ng = DTHREADS / ep;
     int pre = 0, tot = 0;
-    if (e < E) {
-      for (int64_t b = j; b < nblk; b += ng) {
-        const int v = block_counts[b * E + e];
-        tot += v;
-        if (b < (int64_t)blockIdx.x) pre += v;
+    if (ex < E) {
+      // 16 loads in flight per batch (a loop of dependent round trips took most of the
+      // kernel's time)
+      constexpr int NB = 16;
+      for (int64_t b0 = j; b0 < nblk; b0 += (int64_t)NB * ng) {
+        int v[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+          const int64_t b = b0 + (int64_t)u * ng;
+          v[u] = b < nblk ? block_counts[b * E + ex] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+          tot += v[u];
+          if (b0 + (int64_t)u * ng < (int64_t)blockIdx.x) pre += v[u];
+        }
       }
     }
     red_pre[tid] = pre;
@@ -161,8 +181,6 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
   // ---- ranks, in assignment order (chunks of 256 assignments)
   for (int64_t c0 = a0; c0 < a1; c0 += DTHREADS) {
     const int64_t a = c0 + tid;
-    const bool valid = a < a1;
-    const int e = valid ? load_expert(idx, a, E) : -1;
     int rank_w = 0;
     for (int ee = 0; ee < E; ++ee) {
       const uint64_t m = __ballot(e == ee);
@@ -182,13 +200,12 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
         }
       }
       slot_row[a] = row;
-      float wv;
-      if (w_dtype == KMOE_DTYPE_F32)
-        wv = static_cast<const float*>(wsrc)[a];
-      else
-        wv = bf16_to_f32(static_cast<const uint16_t*>(wsrc)[a]);
       slot_w[a] = wv;
     }
+    // the next chunk's ids and weights
+    valid = a + DTHREADS < a1;
+    e = valid ? load_expert(idx, a + DTHREADS, E) : -1;
+    wv = valid ? load_w(a + DTHREADS) : 0.0f;
     __syncthreads();
     if (tid < E) {
       int s = 0;

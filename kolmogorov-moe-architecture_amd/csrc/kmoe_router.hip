@@ -6,11 +6,12 @@
 // v_mfma_f32_32x32x16_bf16 (each wave: 32 tokens x 64 hidden units) over a K
 // pipeline of as many stages as fit in LDS (K-steps of 128 or 256 bytes per row):
 // x rows and w_in rows go global -> LDS directly (global_load_lds), so all but one
-// stage are in flight while one is computed.  The hidden
-// activations go through LDS (fp32) for the 128 -> E layer, computed on the vector
-// ALUs in fp32; softmax/top-k then run one token per thread with the token's logits
-// in registers, and the logits, aux partials and outputs leave through coalesced,
-// all-thread copies and wave reductions.
+// stage are in flight while one is computed.  The hidden activations go through LDS
+// (fp32) to the 128 -> E layer, which runs in fp32 on v_mfma_f32_16x16x4_f32 (each
+// wave: 16 tokens x all experts); softmax/top-k then run four lanes per token (each
+// with a quarter of the experts' logits in registers, merged by lane shuffles), and
+// the logits, aux partials and outputs leave through coalesced, all-thread copies
+// and wave reductions.
 #include "kmoe_common.h"
 
 namespace {
@@ -18,7 +19,10 @@ namespace {
 constexpr int RT_TOK = 64;        // tokens per workgroup
 constexpr int RT_THREADS = 256;   // 4 waves: 2 (token halves) x 2 (hidden halves)
 constexpr int RT_HID = KMOE_ROUTER_HIDDEN;
-constexpr int HSTR = RT_HID + 1;  // padded LDS row stride (floats) of the hidden tile
+// padded LDS row strides (floats) of the hidden tile and of w_out: 2 mod 32, so the 32
+// lanes (row i, k) of a 16x16x4 MFMA operand read (banks 2i + k) are conflict free
+constexpr int HSTR = RT_HID + 2;
+constexpr int WOS = RT_HID + 2;
 // One K-step covers RKB bytes of every row (RKB = 128 or 256: 64 or 128 bf16).
 template <int RKB>
 struct RtGeom {
@@ -36,9 +40,12 @@ struct RtGeom {
     return row * RKB + ((chunk ^ (RKB == 128 ? ((row >> 1) & 7) : (row & 15))) << 4);
   }
 };
-// K pipeline depth: as many stages as fit beside w_out (NE padded rows of 132 fp32)
+// K pipeline depth: as many stages as fit beside w_out (NE rows, at least 16, of WOS
+// fp32), the block's expert counts and the RMS scales
 template <int NE, int RKB>
-constexpr int rt_stages() { return (160 * 1024 - NE * (RT_HID + 4) * 4) / RtGeom<RKB>::STAGE; }
+constexpr int rt_stages() {
+  return (160 * 1024 - (NE < 16 ? 16 : NE) * WOS * 4 - NE * 4 - RT_TOK * 4) / RtGeom<RKB>::STAGE;
+}
 
 // RMS: the router input is RMSNorm(x) (embeddings.py:167-195) with the norm weight
 // already folded into w_in's columns; the kernel sums x^2 over the K loop from the
@@ -60,14 +67,17 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   constexpr int RT_STAGES = rt_stages<NE, RKB>();
   constexpr int RT_STAGE = G::STAGE;
   static_assert(RT_STAGES >= 2, "K pipeline");
-  constexpr int WOS = RT_HID + 4;  // padded w_out row (floats): the 4 lanes of a token hit distinct banks
-  constexpr int LGS = NE + 4;      // logits / probabilities row stride (floats), 16-byte aligned rows
+  static_assert(RT_STAGES * RT_STAGE >= (RT_TOK * HSTR + 2 * RT_TOK * (NE + 4) + RT_TOK) * 4,
+                "the epilogue's hidden / logit / probability tiles reuse the stages");
+  constexpr int NEP = NE < 16 ? 16 : NE;  // experts padded to whole 16-wide MFMA blocks
+  constexpr int LGS = NE + 4;             // logits / probabilities row stride (floats), 16-byte aligned rows
   __shared__ __attribute__((aligned(1024))) uint8_t smem[RT_STAGES * RT_STAGE];
-  __shared__ __attribute__((aligned(16))) float wo[NE * WOS];  // w_out as fp32
-  __shared__ float rs_l[RMS ? RT_TOK : 1];                     // per-token RMSNorm scale
+  __shared__ __attribute__((aligned(16))) float wo[NEP * WOS];  // w_out as fp32 (rows >= E: 0)
+  __shared__ float rs_l[RMS ? RT_TOK : 1];                      // per-token RMSNorm scale
+  __shared__ int cnt_l[NE];                                     // the block's per-expert routed counts
   // after the K loop smem holds: hs[64][HSTR], lg[64][LGS], pe[64][LGS], lse2[64]
   float* hs = reinterpret_cast<float*>(smem);
-  float* lg = hs + RT_TOK * HSTR;  // 64 * 129 floats = 33024 bytes: lg rows stay 16-byte aligned
+  float* lg = hs + RT_TOK * HSTR;  // 64 * 130 floats = 33280 bytes: lg rows stay 16-byte aligned
   float* pe = lg + RT_TOK * LGS;
   float* lse2 = pe + RT_TOK * LGS;
 
@@ -133,10 +143,11 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   // w_out (needed only by layer 2) is staged while the first K-steps are in flight:
   // loading it before them put its global round trip in front of every x load
   // (2.9 -> 0.6 us before the first K-step)
-  for (int i = tid; i < NE * RT_HID; i += RT_THREADS) {
+  for (int i = tid; i < NEP * RT_HID; i += RT_THREADS) {
     const int e = i / RT_HID, j = i % RT_HID;
     wo[e * WOS + j] = e < E ? bf16_to_f32(w_out[i]) : 0.0f;
   }
+  if (tid < NE) cnt_l[tid] = 0;
   constexpr int NSUB = RKB / 32;  // MFMA K-substeps per K-step
   for (int kt = 0; kt < nk; ++kt) {
     if (kt + RT_STAGES - 2 < nk)
@@ -196,116 +207,121 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
     }
   __syncthreads();
 
-  // ---- layer 2 (fp32 FMA): thread (token t>>2, part t&3) computes experts part+4q
+  // ---- layer 2 on v_mfma_f32_16x16x4_f32 (fp32 operands): wave w computes tokens
+  // [16w, 16w + 16) x every 16-expert block; operand lane l holds row l%16 at k = l/16,
+  // result register r of lane l is (token 4(l/16) + r, expert l%16)
   {
-    const int tl = tid >> 2, part = tid & 3;
-    float l2[NE / 4];
+    constexpr int NEB = NEP / 16;
+    const int i16 = lane & 15, k4 = lane >> 4;
+    f32x4_t l2[NEB];
 #pragma unroll
-    for (int q = 0; q < NE / 4; ++q) l2[q] = 0.0f;
-    const float* hrow = hs + tl * HSTR;
-#pragma unroll 4
-    for (int j = 0; j < RT_HID; j += 4) {
-      const float h0 = hrow[j], h1 = hrow[j + 1], h2 = hrow[j + 2], h3 = hrow[j + 3];
+    for (int eb = 0; eb < NEB; ++eb) l2[eb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const float* ha = hs + (wave * 16 + i16) * HSTR + k4;
+    const float* wb = wo + i16 * WOS + k4;
+#pragma unroll 8
+    for (int st = 0; st < RT_HID / 4; ++st) {
+      const float av = ha[4 * st];
 #pragma unroll
-      for (int q = 0; q < NE / 4; ++q) {
-        const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(&wo[(part + 4 * q) * WOS + j]);
-        l2[q] = fmaf(h0, wv[0], l2[q]);
-        l2[q] = fmaf(h1, wv[1], l2[q]);
-        l2[q] = fmaf(h2, wv[2], l2[q]);
-        l2[q] = fmaf(h3, wv[3], l2[q]);
-      }
+      for (int eb = 0; eb < NEB; ++eb)
+        l2[eb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wb[eb * 16 * WOS + 4 * st], l2[eb], 0, 0, 0);
     }
 #pragma unroll
-    for (int q = 0; q < NE / 4; ++q) {
-      const int e = part + 4 * q;
-      lg[tl * LGS + e] = e < E ? l2[q] + (bias ? bias[e] : 0.0f) : 0.0f;
+    for (int eb = 0; eb < NEB; ++eb) {
+      const int e = eb * 16 + i16;
+      if (e < NE) {
+        const float be = (e < E && bias) ? bias[e] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) lg[(wave * 16 + 4 * k4 + r) * LGS + e] = e < E ? l2[eb][r] + be : 0.0f;
+      }
     }
   }
   __syncthreads();
 
-  // ---- softmax, top-k, outputs: one token per thread (threads 0..63), the token's
-  // logits in registers
+  // ---- softmax, top-k, outputs: four lanes per token (lane part p holds the logits of
+  // experts p + 4q in registers), merged with shuffles inside each group of four
   const int64_t ntok = T - tok0 < RT_TOK ? T - tok0 : RT_TOK;
-  if (tid < RT_TOK) {
-    const int64_t t = tok0 + tid;
-    int sel[8];  // this token's experts (k <= 8); -1 past T
+  {
+    constexpr int NQ = NE / 4;
+    const int tl = tid >> 2, part = tid & 3;
+    const int64_t t = tok0 + tl;
+    float L[NQ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sel[j] = -1;
-    float L[NE];
+    for (int q = 0; q < NQ; ++q) L[q] = lg[tl * LGS + part + 4 * q];
+    float* P = pe + tl * LGS;
+    if (t < T) {  // the same for the four lanes of a token
+      float mx = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < NE / 4; ++q) {
-      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(lg + tid * LGS + 4 * q);
-      L[4 * q] = v[0];
-      L[4 * q + 1] = v[1];
-      L[4 * q + 2] = v[2];
-      L[4 * q + 3] = v[3];
-    }
-    float* P = pe + tid * LGS;
-    if (t < T) {
-      float mx = L[0];
+      for (int q = 0; q < NQ; ++q)
+        if (part + 4 * q < E) mx = fmaxf(mx, L[q]);
+      mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+      float ex[NQ], s = 0.0f;
 #pragma unroll
-      for (int e = 1; e < NE; ++e)
-        if (e < E) mx = fmaxf(mx, L[e]);
-      float s = 0.0f;
-      float ex[NE];
-#pragma unroll
-      for (int e = 0; e < NE; ++e) {
-        ex[e] = e < E ? __expf(L[e] - mx) : 0.0f;
-        s += ex[e];
+      for (int q = 0; q < NQ; ++q) {
+        ex[q] = part + 4 * q < E ? __expf(L[q] - mx) : 0.0f;
+        s += ex[q];
       }
+      s += __shfl_xor(s, 1, 64);
+      s += __shfl_xor(s, 2, 64);
       const float inv_s = 1.0f / s;
-      const float lse = mx + __logf(s);
 #pragma unroll
-      for (int q = 0; q < NE / 4; ++q)
-        *reinterpret_cast<f32x4_t*>(P + 4 * q) =
-            f32x4_t{ex[4 * q] * inv_s, ex[4 * q + 1] * inv_s, ex[4 * q + 2] * inv_s, ex[4 * q + 3] * inv_s};
-      lse2[tid] = lse * lse;
+      for (int q = 0; q < NQ; ++q) P[part + 4 * q] = ex[q] * inv_s;
+      if (part == 0) {
+        const float lse = mx + __logf(s);
+        lse2[tl] = lse * lse;
+      }
       if (k > 0) {
-        // k selections over the registers; strict '>' keeps the lower index on ties
-        uint64_t taken = 0;
+        // k rounds: each lane's best untaken expert (strict '>' over ascending q keeps
+        // the lower index), then the best of the four (higher logit, or the lower index
+        // on equal logits); NaN ranks below every number
+        uint32_t taken = 0;
+        int sel[8];
         float sev[8];
         float ssum = 0.0f;
         for (int j = 0; j < k; ++j) {
           int bi = -1;
-          float bv = 0.0f;
+          float bv = -INFINITY;
 #pragma unroll
-          for (int e = 0; e < NE; ++e) {
-            const bool ok = e < E && !((taken >> e) & 1ull);
-            if (ok && (bi < 0 || L[e] > bv)) {
-              bi = e;
-              bv = L[e];
+          for (int q = 0; q < NQ; ++q) {
+            const float v = L[q] != L[q] ? -INFINITY : L[q];
+            if (part + 4 * q < E && !((taken >> q) & 1u) && (bi < 0 || v > bv)) {
+              bi = part + 4 * q;
+              bv = v;
             }
           }
-          taken |= 1ull << bi;
+#pragma unroll
+          for (int o = 1; o <= 2; o <<= 1) {
+            const int oi = __shfl_xor(bi, o, 64);
+            const float ov = __shfl_xor(bv, o, 64);
+            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+              bi = oi;
+              bv = ov;
+            }
+          }
+          if ((bi & 3) == part) taken |= 1u << (bi >> 2);
           sel[j] = bi;
           sev[j] = __expf(bv - mx);
           ssum += sev[j];
         }
-        const float inv = 1.0f / ssum;
-        for (int j = 0; j < k; ++j) {
-          topk_idx[t * k + j] = sel[j];
-          topk_w[t * k + j] = sev[j] * inv;
+        if (part == 0) {
+          const float inv = 1.0f / ssum;
+          for (int j = 0; j < k; ++j) {
+            topk_idx[t * k + j] = sel[j];
+            topk_w[t * k + j] = sev[j] * inv;
+            // the block's per-expert routed counts (the dispatch's histogram of these
+            // 64 tokens)
+            if (block_counts) atomicAdd(&cnt_l[sel[j]], 1);
+          }
         }
       }
     } else {
 #pragma unroll
-      for (int q = 0; q < NE / 4; ++q) *reinterpret_cast<f32x4_t*>(P + 4 * q) = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      lse2[tid] = 0.0f;
-    }
-    // the block's per-expert routed counts (the dispatch's histogram of these 64
-    // tokens): lane e sums the ballots of expert e over the k picks
-    if (block_counts && k > 0) {
-      int cnt = 0;
-      for (int j = 0; j < k; ++j) {
-        for (int e = 0; e < E; ++e) {
-          const uint64_t m = __ballot(sel[j] == e);
-          if (lane == e) cnt += __popcll(m);
-        }
-      }
-      if (lane < E) block_counts[(int64_t)blockIdx.x * E + lane] = cnt;
+      for (int q = 0; q < NQ; ++q) P[part + 4 * q] = 0.0f;
+      if (part == 0) lse2[tl] = 0.0f;
     }
   }
   __syncthreads();
+  if (block_counts && k > 0 && tid < E) block_counts[(int64_t)blockIdx.x * E + tid] = cnt_l[tid];
 
   // ---- logits out: the block's ntok x E floats are contiguous; coalesced copy
   for (int i = tid; i < ntok * E; i += RT_THREADS) logits[tok0 * E + i] = lg[(i / E) * LGS + i % E];
@@ -369,7 +385,7 @@ int router_launch(const void* x, const int32_t* row_index, int64_t T, int d, con
   KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "kmoe_router: d=%d must be a positive multiple of 64", d);
   KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_router: E=%d not in [1,%d]", E,
                KMOE_MAX_EXPERTS);
-  KMOE_REQUIRE(k >= 0 && k <= E, KMOE_ERR_SHAPE, "kmoe_router: k=%d not in [0,E=%d]", k, E);
+  KMOE_REQUIRE(k >= 0 && k <= E && k <= 8, KMOE_ERR_SHAPE, "kmoe_router: k=%d not in [0, min(8, E=%d)]", k, E);
   KMOE_REQUIRE(k == 0 || (topk_idx && topk_w), KMOE_ERR_NULL, "kmoe_router: k>0 needs topk_idx and topk_w");
   if (T == 0) return KMOE_OK;
   const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(T, RT_TOK));

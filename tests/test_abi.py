@@ -51,6 +51,9 @@ def test_router_validation(lib):
     assert rc == -2 and "E=65" in msg
     rc, msg = _err(lib, "kmoe_router", FAKE, NULL, 16, 64, FAKE, FAKE, 8, NULL, 9, FAKE, FAKE, FAKE, NULL, NULL)
     assert rc == -2 and "k=9" in msg
+    # at most 8 picks per token, however many experts
+    rc, msg = _err(lib, "kmoe_router", FAKE, NULL, 16, 64, FAKE, FAKE, 64, NULL, 9, FAKE, FAKE, FAKE, NULL, NULL)
+    assert rc == -2 and "k=9" in msg
     rc, _ = _err(lib, "kmoe_router", FAKE, NULL, 16, 64, FAKE, FAKE, 8, NULL, 2, FAKE, NULL, FAKE, NULL, NULL)
     assert rc == -1
 
