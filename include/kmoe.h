@@ -221,7 +221,8 @@ int kmoe_balanced_topk(const float* logits, int64_t T, int E, int k, int64_t* id
  * Also writes the dispatch/combine tables: row_token (E*B*C, expert-major rows
  * e*B*C + b*C + c -> token b*S + idx), offsets (E+1) and the per-token combine
  * table src_row/src_w (B*S, E): permuted row of (token, expert) or -1.
- * Requires C <= S.  workspace: kmoe_ec_workspace_bytes.                      */
+ * Requires C <= S.  workspace: kmoe_ec_workspace_bytes (B*S*E floats: the logits
+ * transposed to (B, E, S), so each (sequence, expert) column is read contiguously). */
 size_t kmoe_ec_workspace_bytes(int B, int64_t S, int E);
 int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int64_t C, int order, int64_t* idx, float* w,
                    int32_t* row_token, int32_t* offsets, int32_t* src_row, float* src_w, void* workspace,

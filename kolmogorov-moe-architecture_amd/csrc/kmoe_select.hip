@@ -30,28 +30,6 @@ __device__ __forceinline__ float key_value(uint32_t k) {  // inverse of order_ke
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// Exclusive block scan of one int per thread (1024 threads); returns the exclusive
-// prefix and writes the total to *total.
-__device__ int block_excl_scan(int v, int* s_wave, int* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  int s = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(s, o, 64);
-    if (lane >= o) s += u;
-  }
-  if (lane == 63) s_wave[wave] = s;
-  __syncthreads();
-  int before = 0, tot = 0;
-  for (int w = 0; w < nw; ++w) {
-    if (w < wave) before += s_wave[w];
-    tot += s_wave[w];
-  }
-  __syncthreads();
-  *total = tot;
-  return before + s - v;
-}
-
 __device__ float block_sum(float v, float* s_red) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   v = wave_sum(v);
@@ -120,35 +98,82 @@ __device__ void radix_select_desc(const uint32_t* keys, int n, int C, uint32_t* 
 }
 
 // Index-ordered compaction of the selection; calls emit(i, pos) for each selected
-// index i with its position pos in index order.  Threads own contiguous chunks.
+// index i with its position pos in index order, skip(i) for the others.  Wave w owns
+// the contiguous segment [w*seg, (w+1)*seg) and reads it 64 consecutive keys at a time
+// (conflict-free LDS reads; threads owning contiguous chunks read with a stride of the
+// chunk length, a 32-way bank conflict at 16 keys per thread).  Each wave counts its
+// keys above and equal to thr; one exchange gives every wave its first position and
+// its first rank among the equal keys (of which the lowest `need` indices are taken);
+// positions inside a wave come from ballots.
 template <typename Emit, typename Skip>
 __device__ void compact_selected(const uint32_t* keys, int n, uint32_t thr, int need, int* s_wave, Emit emit,
                                  Skip skip) {
-  const int chunk = (n + (int)blockDim.x - 1) / (int)blockDim.x;
-  const int i0 = min(n, (int)threadIdx.x * chunk), i1 = min(n, i0 + chunk);
-  int n_eq = 0;
-  for (int i = i0; i < i1; ++i) n_eq += keys[i] == thr;
-  int tot;
-  int eq_before = block_excl_scan(n_eq, s_wave, &tot);
-  int n_take = 0;
-  {
-    int eqr = eq_before;
-    for (int i = i0; i < i1; ++i) {
-      const uint32_t k = keys[i];
-      if (k > thr) ++n_take;
-      else if (k == thr) n_take += (eqr++ < need);
-    }
+  __shared__ int s_gt[SEL_THREADS / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int seg = (((n + nw - 1) / nw) + 63) & ~63;
+  const int s0 = min(n, wave * seg), s1 = min(n, s0 + seg);
+  auto mbcnt = [&](uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+  };
+  int gt_w = 0, eq_w = 0;
+  for (int r0 = s0; r0 < s1; r0 += 64) {  // wave-uniform trip count
+    const int i = r0 + lane;
+    const bool v = i < s1;
+    const uint32_t k = v ? keys[i] : 0u;
+    gt_w += (int)__builtin_popcountll(__ballot(v && k > thr));
+    eq_w += (int)__builtin_popcountll(__ballot(v && k == thr));
   }
-  int pos = block_excl_scan(n_take, s_wave, &tot);
-  int eqr = eq_before;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t k = keys[i];
-    bool take = k > thr;
-    if (k == thr) take = (eqr++ < need);
+  if (lane == 0) {
+    s_wave[wave] = eq_w;
+    s_gt[wave] = gt_w;
+  }
+  __syncthreads();
+  int eqr = 0, pos = 0;
+  for (int q = 0; q < wave; ++q) {
+    const int eqq = s_wave[q];
+    pos += s_gt[q] + min(eqq, max(0, need - eqr));
+    eqr += eqq;
+  }
+  __syncthreads();  // callers reuse s_wave
+  for (int r0 = s0; r0 < s1; r0 += 64) {
+    const int i = r0 + lane;
+    const bool v = i < s1;
+    const uint32_t k = v ? keys[i] : 0u;
+    const bool eq = v && k == thr;
+    const uint64_t em = __ballot(eq);
+    const bool take = (v && k > thr) || (eq && eqr + mbcnt(em) < need);
+    const uint64_t tm = __ballot(take);
     if (take)
-      emit(i, pos++);
-    else
+      emit(i, pos + mbcnt(tm));
+    else if (v)
       skip(i);
+    eqr += (int)__builtin_popcountll(em);
+    pos += (int)__builtin_popcountll(tm);
+  }
+}
+
+// Expert-choice preparation: the logits (B*S, E) transposed to lt (B, E, S), so each
+// selection block reads its (sequence, expert) column as contiguous floats (a column
+// read with a stride of E floats touches a cache line per two tokens), and the combine
+// table src_row (B*S, E) filled with -1 in the same coalesced pass (the selection then
+// writes only its C rows per block).  A block moves 64 tokens x E through LDS.
+__global__ __launch_bounds__(256) void ec_prep_kernel(const float* __restrict__ logits, int B, int S, int E,
+                                                      float* __restrict__ lt, int32_t* __restrict__ src_row) {
+  __shared__ float tile[64][KMOE_MAX_EXPERTS + 1];
+  const int64_t T = (int64_t)B * S;
+  const int64_t t0 = (int64_t)blockIdx.x * 64;
+  const int64_t nt = min<int64_t>(64, T - t0);
+  const int64_t n = nt * E;  // the block's logits are contiguous
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    tile[i / E][i % E] = logits[t0 * E + i];
+    src_row[t0 * E + i] = -1;
+  }
+  __syncthreads();
+  const int tl = threadIdx.x & 63;
+  if (tl < nt) {
+    const int64_t t = t0 + tl;
+    const int64_t b = t / S, s = t - b * S;
+    for (int e = threadIdx.x >> 6; e < E; e += 4) lt[(b * E + e) * S + s] = tile[tl][e];
   }
 }
 
@@ -166,15 +191,15 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
   __shared__ int s_wave[SEL_THREADS / 64];
   __shared__ float s_red[SEL_THREADS / 64];
   const int b = blockIdx.x / E, e = blockIdx.x % E;
-  const float* lg = logits + (int64_t)b * S * E + e;
+  const float* lg = logits + ((int64_t)b * E + e) * S;  // the transposed logits (ec_prep_kernel)
 
-  // the sequence's column of logits: all of a thread's (strided) loads in flight at once
+  // the sequence's column of logits: all of a thread's loads in flight at once
   constexpr int PER = SEL_MAX_S / SEL_THREADS;
   float v[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
     const int i = threadIdx.x + u * SEL_THREADS;
-    v[u] = i < S ? lg[(int64_t)i * E] : 0.0f;
+    v[u] = i < S ? lg[i] : 0.0f;
   }
   float mx = -INFINITY;
 #pragma unroll
@@ -206,15 +231,15 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
   while (Cp < C) Cp <<= 1;
   for (int i = threadIdx.x; i < Cp; i += blockDim.x) sorted[i] = 0ull;
   __syncthreads();
-  // selected: into the sort buffer in token order; not selected: no row in the
-  // combine table (the selected ones get theirs with the weights below)
-  int32_t* const src_row_b = src_row + (int64_t)b * S * E + e;
+  // selected: into the sort buffer in token order (the combine table's -1 entries of
+  // the others were written by ec_prep_kernel; the selected ones get their rows with
+  // the weights below)
   compact_selected(
       keys, S, thr, need, s_wave,
       [&](int i, int pos) {
         if (pos < C) sorted[pos] = ((uint64_t)keys[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
       },
-      [&](int i) { src_row_b[(int64_t)i * E] = -1; });
+      [&](int) {});
   __syncthreads();
   // sum of the selected probabilities, over the selection in token order (the same
   // sum whichever output order is asked for)
@@ -377,17 +402,12 @@ __global__ __launch_bounds__(SEL_THREADS) void mod_select_kernel(const float* __
 }  // namespace
 
 extern "C" size_t kmoe_ec_workspace_bytes(int B, int64_t S, int E) {
-  (void)B;
-  (void)S;
-  (void)E;
-  return 0;
+  return B > 0 && S > 0 && E > 0 ? (size_t)B * (size_t)S * (size_t)E * sizeof(float) : 0;
 }
 
 extern "C" int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int64_t C, int order, int64_t* idx,
                               float* w, int32_t* row_token, int32_t* offsets, int32_t* src_row, float* src_w,
                               void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   KMOE_REQUIRE(logits && idx && w && row_token && offsets && src_row && src_w, KMOE_ERR_NULL,
                "kmoe_ec_select: null buffer");
   KMOE_REQUIRE(B >= 1 && E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_ec_select: bad B=%d/E=%d", B, E);
@@ -397,8 +417,14 @@ extern "C" int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int6
                (long long)C, SEL_MAX_C);
   KMOE_REQUIRE((int64_t)E * B * C < ((int64_t)1 << 31), KMOE_ERR_SHAPE, "kmoe_ec_select: E*B*C must fit in int32");
   KMOE_REQUIRE(order == 0 || order == 1, KMOE_ERR_SHAPE, "kmoe_ec_select: order=%d not 0 or 1", order);
+  const size_t need_ws = kmoe_ec_workspace_bytes(B, S, E);
+  KMOE_REQUIRE(workspace && workspace_bytes >= need_ws, KMOE_ERR_WORKSPACE,
+               "kmoe_ec_select: workspace of %zu bytes needed (kmoe_ec_workspace_bytes)", need_ws);
   hipStream_t s = kmoe::as_stream(stream);
-  hipLaunchKernelGGL(ec_select_kernel, dim3((unsigned)(B * E)), dim3(SEL_THREADS), 0, s, logits, B, (int)S, E, (int)C,
+  float* lt = static_cast<float*>(workspace);
+  hipLaunchKernelGGL(ec_prep_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>((int64_t)B * S, 64)), dim3(256), 0, s,
+                     logits, B, (int)S, E, lt, src_row);
+  hipLaunchKernelGGL(ec_select_kernel, dim3((unsigned)(B * E)), dim3(SEL_THREADS), 0, s, lt, B, (int)S, E, (int)C,
                      order, idx, w, row_token, offsets, src_row, src_w);
   return kmoe::check_launch("kmoe_ec_select");
 }

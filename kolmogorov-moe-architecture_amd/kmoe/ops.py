@@ -440,10 +440,11 @@ def ec_select(logits, B, S, E, C, descending=True) -> ECSelectOut:
     offsets = torch.empty(E + 1, device=dev, dtype=torch.int32)
     src_row = torch.empty(B * S, E, device=dev, dtype=torch.int32)
     src_w = torch.empty(B * S, E, device=dev, dtype=torch.float32)
+    ws_bytes = _lib.load().kmoe_ec_workspace_bytes(B, S, E)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)  # the logits transposed per expert
     with _Stage("ec_select"):
         _lib.call("kmoe_ec_select", ptr(logits), B, S, E, C, 1 if descending else 0, ptr(idx), ptr(w),
-              ptr(row_token), ptr(offsets),
-              ptr(src_row), ptr(src_w), None, 0, _stream(logits))
+                  ptr(row_token), ptr(offsets), ptr(src_row), ptr(src_w), ptr(ws), ws_bytes, _stream(logits))
     return ECSelectOut(idx, w, row_token, offsets, src_row, src_w)
 
 

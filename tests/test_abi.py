@@ -98,6 +98,10 @@ def test_select_validation(lib):
                 NULL)[0] == -2
     assert _err(lib, "kmoe_ec_select", FAKE, 1, 100000, 4, 10, 1, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
                 NULL)[0] == -6
+    # the transposed-logits workspace: B*S*E floats, checked before any launch
+    assert lib.kmoe_ec_workspace_bytes(2, 100, 4) == 2 * 100 * 4 * 4
+    assert _err(lib, "kmoe_ec_select", FAKE, 2, 100, 4, 10, 1, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                2 * 100 * 4 * 4 - 1, NULL)[0] == -4
     assert _err(lib, "kmoe_mod_select", FAKE, 2, 100, 64, FAKE, 0, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 0,
                 NULL)[0] == -2
     assert _err(lib, "kmoe_aux_loss", NULL, 16, 4, NULL, 2, 0.01, 0.001, FAKE, NULL)[0] == -1
