@@ -464,33 +464,39 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   // lane's write address for p = 0 of block (0, 0): even lanes row 4lh col lr,
   // odd lanes row 4lh+1 col lr-1
   uint8_t* const wbase = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR + (wn * (NC / 2) + lr - (odd ? 1 : 0)) * 2;
-  auto bscale = [&](int j) { return sb_l[b_lds_row<GATE_UP, WNB>(wn, j, lr)]; };
+  // The scales go to registers first: the B-row scales of the lane's WNB blocks once, the
+  // A-row scales of each row block (16 rows of the lane) before its results.  Read from
+  // LDS per output element, they were re-read after every staging write (the compiler
+  // cannot tell the two LDS areas apart): about 4.5 k more cycles per tile than bf16.
+  float sbr[WNB];
+#pragma unroll
+  for (int j = 0; j < WNB; ++j) sbr[j] = FP8 ? sb_l[b_lds_row<GATE_UP, WNB>(wn, j, lr)] : 1.0f;
+  float sar[16];
   auto result = [&](int mi, int r, int jo) -> float {
     if (GATE_UP) {
       float gg = acc[mi][jo][r], u = acc[mi][jo + WNB / 2][r];
       if (FP8) {
-        const float sa = sa_l[wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
-        gg *= sa * bscale(jo);
-        u *= sa * bscale(jo + WNB / 2);
+        gg *= sar[r] * sbr[jo];
+        u *= sar[r] * sbr[jo + WNB / 2];
       }
       if (RSCALE) {
-        const float sa = sa_l[wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
-        gg *= sa;
-        u *= sa;
+        gg *= sar[r];
+        u *= sar[r];
       }
       return silu_fast_f32(gg) * u;
     } else {
       float v = acc[mi][jo][r];
-      if (FP8) {
-        const float sa = sa_l[wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
-        v *= sa * bscale(jo);
-      }
+      if (FP8) v *= sar[r] * sbr[jo];
       return v;
     }
   };
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
     if (mi >= NMA) break;  // rows past the expert's end: never stored
+    if constexpr (FP8 || RSCALE) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sar[r] = sa_l[wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
+    }
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
       const int r0 = 2 * p, r1 = 2 * p + 1;
