@@ -390,6 +390,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
 #pragma unroll
       for (int j = 0; j < WNB; ++j) mfma<FP8>(acc[mi][j], a[mi], b[j]);
   };
+  // MFMAs [lo, hi) of a substep (linear index mi * WNB + j)
+  auto mma_part = [&](const Frag<FP8> (&a)[4], const Frag<FP8> (&b)[WNB], auto lo_tag, auto hi_tag) {
+    static_for<decltype(lo_tag)::value, decltype(hi_tag)::value>(
+        [&](auto xc) { mfma<FP8>(acc[decltype(xc)::value / WNB][decltype(xc)::value % WNB], a[decltype(xc)::value / WNB], b[decltype(xc)::value % WNB]); });
+  };
 
   // Pipeline.  Step kt computes LDS stage kt%2 while the registers hold step kt+1's
   // tile data.  Those blocks are written into stage (kt+1)%2 (which every wave
@@ -425,6 +430,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
       // next substep's fragments first: they are on the MFMA critical path
       if constexpr (i + 1 < NSUB) {
         rd(cur, i + 1, fa[bi ^ 1], fb[bi ^ 1]);
+      } else if constexpr (!LAST && NMS > 0) {
+        // last substep: most of its MFMAs go out before the wait and the barrier that
+        // publishes the next stage (they read registers only), so the MFMA pipe is busy
+        // while the waves meet; the next stage's first fragment reads then issue two per
+        // MFMA under the remaining NA.  (Barrier first: each step lost the pipe for the
+        // wait on the substeps' LDS writes plus the barrier, 0.6 k cycles per fp8 step.)
+        static_assert(nq == 0, "the block writes of a step are in its earlier substeps");
+        constexpr int NA = (RD + 1) / 2 < NMS ? (RD + 1) / 2 : NMS;
+        mma_part(fa[bi], fb[bi], std::integral_constant<int, 0>{}, std::integral_constant<int, NMS - NA>{});
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkmcnt0();
+        barrier_nofence();
+        rd(nxt, 0, fa[bi ^ 1], fb[bi ^ 1]);
+        mma_part(fa[bi], fb[bi], std::integral_constant<int, NMS - NA>{}, std::integral_constant<int, NMS>{});
+        sched_spread<NA, RD, 0, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+        return;
       } else if constexpr (!LAST) {
         wait_lgkmcnt0();
         barrier_nofence();
