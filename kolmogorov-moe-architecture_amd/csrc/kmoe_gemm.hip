@@ -222,6 +222,20 @@ __device__ __forceinline__ void sched_spread() {
   }
 }
 
+// Scheduling groups for NM MFMAs with NWR LDS block writes and NVM memory loads spread
+// evenly over them (no fragment reads among them).
+template <int NM, int NWR, int NVM, int G = 0>
+__device__ __forceinline__ void sched_even() {
+  if constexpr (G < NM) {
+    constexpr int w = (NWR * (G + 1)) / NM - (NWR * G) / NM;
+    constexpr int v = (NVM * (G + 1)) / NM - (NVM * G) / NM;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
+    if constexpr (w > 0) __builtin_amdgcn_sched_group_barrier(0x200, w, 0);  // DS write
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x020, v, 0);  // VMEM read
+    sched_even<NM, NWR, NVM, G + 1>();
+  }
+}
+
 // Raw buffer resource over [base, base + 4 GiB): loads address it with a 32-bit
 // per-lane offset plus a wave-uniform (SGPR) offset, so advancing K costs no VALU.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
@@ -398,17 +412,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
 
   // Pipeline.  Step kt computes LDS stage kt%2 while the registers hold step kt+1's
   // tile data.  Those blocks are written into stage (kt+1)%2 (which every wave
-  // stopped reading at step kt-1's barrier) over the first substeps, each block
-  // reloaded with step kt+2's data right after its write, so a load has a whole
-  // step to land and the LDS write traffic is spread evenly (bf16: about 6/5/5
-  // sixteenths of the blocks in substeps 0-2; fp8: all in substep 0).  The last
-  // substep waits for this wave's LDS writes and reads, then one barrier publishes
-  // stage kt+1, whose first fragments are read under the last substep's MFMAs.
-  // Register dependencies give the vmcnt waits; the scheduling groups interleave the
-  // LDS and memory operations with the MFMAs, fragment reads first.
+  // stopped reading at step kt-1's barrier) over the substeps, each block reloaded
+  // with step kt+2's data right after its write, so a load has a whole step to land
+  // and the LDS write traffic is spread (bf16: about 6/5/5 sixteenths of the blocks
+  // in substeps 0-2; fp8: half in each substep).  In the last substep, after most of
+  // its MFMAs, the wave waits for its LDS writes and reads, then one barrier publishes
+  // stage kt+1, whose first fragments are read under the last few MFMAs.  Register
+  // dependencies give the vmcnt waits; the scheduling groups interleave the LDS and
+  // memory operations with the MFMAs, fragment reads first.
   constexpr int RD = NMA > 0 ? (FP8 ? 2 : 1) * (NMA + WNB) : 0;  // LDS reads of a substep's fragments
   constexpr int NMS = NMA * WNB;                                    // MFMAs per substep
-  constexpr int C1 = (NBLK * 6 + 8) / 16, C2 = (NBLK * 11 + 8) / 16;
   for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 0);
   for (int qq = 0; qq < NBLK; ++qq) write_block(qq, 0);
   for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 1);
@@ -422,35 +435,43 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
     static_for<0, NSUB>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr int bi = i & 1;
-      // blocks [q0, q1) are written and reloaded in this substep
-      constexpr int q0 = NSUB == 4 ? (i == 0 ? 0 : i == 1 ? C1 : i == 2 ? C2 : NBLK) : (i == 0 ? 0 : NBLK);
-      constexpr int q1 = NSUB == 4 ? (i == 0 ? C1 : i == 1 ? C2 : NBLK) : NBLK;
+      // blocks [q0, q1) are written and reloaded in this substep.  bf16 (4 substeps):
+      // about 6/5/5 sixteenths in substeps 0-2.  fp8 (2 substeps): half in each, the
+      // last substep's before its barrier (all in substep 0 crowded the LDS queue with
+      // that substep's fragment reads: 3% slower).
+      constexpr int C1 = (NBLK * 6 + 8) / 16, C2 = (NBLK * 11 + 8) / 16;
+      constexpr int q0 = NSUB == 4 ? (i == 0 ? 0 : i == 1 ? C1 : i == 2 ? C2 : NBLK) : i * NBLK / NSUB;
+      constexpr int q1 = NSUB == 4 ? (i == 0 ? C1 : i == 1 ? C2 : NBLK) : (i + 1) * NBLK / NSUB;
       constexpr int nq = LAST ? 0 : q1 - q0;
       constexpr bool RDN = i + 1 < NSUB || !LAST;
       // next substep's fragments first: they are on the MFMA critical path
       if constexpr (i + 1 < NSUB) {
         rd(cur, i + 1, fa[bi ^ 1], fb[bi ^ 1]);
-      } else if constexpr (!LAST && NMS > 0) {
-        // last substep: most of its MFMAs go out before the wait and the barrier that
-        // publishes the next stage (they read registers only), so the MFMA pipe is busy
-        // while the waves meet; the next stage's first fragment reads then issue two per
-        // MFMA under the remaining NA.  (Barrier first: each step lost the pipe for the
-        // wait on the substeps' LDS writes plus the barrier, 0.6 k cycles per fp8 step.)
-        static_assert(nq == 0, "the block writes of a step are in its earlier substeps");
+      } else if constexpr (!LAST) {
+        // last substep: its share of the block writes and most of its MFMAs go out before
+        // the wait and the barrier that publish the next stage (the MFMAs read registers
+        // only), so the MFMA pipe is busy while the waves meet; the next stage's first
+        // fragment reads then issue two per MFMA under the remaining NA.  (Barrier first:
+        // each step lost the pipe for the wait on the writes plus the barrier.)
         constexpr int NA = (RD + 1) / 2 < NMS ? (RD + 1) / 2 : NMS;
-        mma_part(fa[bi], fb[bi], std::integral_constant<int, 0>{}, std::integral_constant<int, NMS - NA>{});
+        if constexpr (nq > 0) {
+          static_for<q0, q1>([&](auto qc) { write_block(decltype(qc)::value, nxt); });
+          static_for<q0, q1>([&](auto qc) { load_block(decltype(qc)::value, kt + 2); });
+        }
+        if constexpr (NMS - NA > 0) {
+          mma_part(fa[bi], fb[bi], std::integral_constant<int, 0>{}, std::integral_constant<int, NMS - NA>{});
+          sched_even<NMS - NA, nq, nq>();
+        }
         __builtin_amdgcn_sched_barrier(0);
         wait_lgkmcnt0();
         barrier_nofence();
         rd(nxt, 0, fa[bi ^ 1], fb[bi ^ 1]);
-        mma_part(fa[bi], fb[bi], std::integral_constant<int, NMS - NA>{}, std::integral_constant<int, NMS>{});
-        sched_spread<NA, RD, 0, 0>();
+        if constexpr (NA > 0) {
+          mma_part(fa[bi], fb[bi], std::integral_constant<int, NMS - NA>{}, std::integral_constant<int, NMS>{});
+          sched_spread<NA, RD, 0, 0>();
+        }
         __builtin_amdgcn_sched_barrier(0);
         return;
-      } else if constexpr (!LAST) {
-        wait_lgkmcnt0();
-        barrier_nofence();
-        rd(nxt, 0, fa[bi ^ 1], fb[bi ^ 1]);
       }
       if constexpr (nq > 0) {
         static_for<q0, q1>([&](auto qc) { write_block(decltype(qc)::value, nxt); });
