@@ -281,6 +281,35 @@ constexpr int OUT_BF16 = 0, OUT_SPLIT = 1, OUT_F32 = 2;
 // RSCALE (bf16 gathered gate/up tiles): a_scale[row_token[r]] scales row r's gate and
 // up values before the SiLU (the per-token RMSNorm scale of x: the norm weight is
 // folded into the packed w1 / w2 rows, and a per-row scale commutes with the product).
+// Stores a tile staged in LDS (BM rows of OCPR 16-byte chunks, row stride OSTR bytes)
+// to the rows [m0, m_end) of `out` (row stride ld elements, chunk ch at out + 8 ch;
+// chunks from column col0 + 8 ch >= n_valid are not stored).  A thread always handles
+// the same chunk of every GEMM_THREADS / OCPR-th row, so its addresses advance by a
+// fixed stride; LDS reads go out eight at a time ahead of their stores (one read, wait,
+// store per iteration serialised the loop on the LDS latency).
+template <int OCPR, int OSTR>
+__device__ __forceinline__ void store_staged(const uint8_t* lds, int tid, int m0, int m_end, uint16_t* out,
+                                             int64_t ld, int col0, int n_valid) {
+  constexpr int RPI = GEMM_THREADS / OCPR;  // rows per iteration
+  constexpr int NIT = BM / RPI;             // iterations per thread
+  constexpr int CH = NIT < 8 ? NIT : 8;
+  static_assert(GEMM_THREADS % OCPR == 0 && NIT % CH == 0, "store layout");
+  const int ch = tid % OCPR, tr0 = tid / OCPR;
+  const bool col_ok = col0 + ch * 8 < n_valid;
+  const uint8_t* lp = lds + tr0 * OSTR + ch * 16;
+  uint16_t* gp = out + (int64_t)(m0 + tr0) * ld + ch * 8;
+  const int rows = m_end - m0 - tr0;  // this thread's rows: tr0 + RPI i < m_end - m0
+#pragma unroll
+  for (int h = 0; h < NIT; h += CH) {
+    i32x4_t v[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) v[u] = *reinterpret_cast<const i32x4_t*>(lp + (h + u) * RPI * OSTR);
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+      if (col_ok && (h + u) * RPI < rows) *reinterpret_cast<i32x4_t*>(gp + (int64_t)(h + u) * RPI * ld) = v[u];
+  }
+}
+
 // NMA: the row blocks of this wave that hold rows of the expert.  A wave's 128 rows
 // are 4 blocks of 32; a slot's last tile is often partly empty, and its waves then
 // run with NMA < 4 (the first NMA blocks), which skips the other blocks' fragment
@@ -561,14 +590,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   __syncthreads();
   constexpr int OCPR = NC * 2 / 16;  // 16-byte chunks per output row
   const int col0 = (GATE_UP ? nt * 128 : nt * 256) + q * NC;
-  for (int c = tid; c < BM * OCPR; c += GEMM_THREADS) {
-    const int trow = c / OCPR, ch = c % OCPR;
-    const int grow = m0 + trow;
-    const int gcol = col0 + ch * 8;
-    if (grow < m_end && gcol < g.n_valid)
-      *reinterpret_cast<i32x4_t*>(g.C + (int64_t)grow * g.ldc + gcol) =
-          *reinterpret_cast<const i32x4_t*>(lds + trow * OSTR + ch * 16);
-  }
+  store_staged<OCPR, OSTR>(lds, tid, m0, m_end, g.C + col0, g.ldc, col0, g.n_valid);
 
   // training forward: the pre-activation gate and up values of the tile, bf16, in the
   // packed column order (row stride 2*ldc), for the SwiGLU backward
@@ -598,14 +620,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
     }
     __syncthreads();
     constexpr int OCPR2 = NC2 * 2 / 16;
-    for (int c = tid; c < BM * OCPR2; c += GEMM_THREADS) {
-      const int trow = c / OCPR2, ch = c % OCPR2;
-      const int grow = m0 + trow;
-      const int gcol = nt * 256 + b_packed_row<true, WNB>(ch * 8, q);
-      if (grow < m_end)
-        *reinterpret_cast<i32x4_t*>(g.gu_out + (int64_t)grow * 2 * g.ldc + gcol) =
-            *reinterpret_cast<const i32x4_t*>(lds + trow * OSTR2 + ch * 16);
-    }
+    // chunk ch of a staged row lands at packed column b_packed_row(8 ch): contiguous
+    // within each 8-column chunk, so the per-thread base column is that of its chunk
+    const int ch2 = tid % OCPR2;
+    const int gcol2 = nt * 256 + b_packed_row<true, WNB>(ch2 * 8, q);
+    store_staged<OCPR2, OSTR2>(lds, tid, m0, m_end, g.gu_out + gcol2 - ch2 * 8, 2 * g.ldc, 0, 1 << 30);
   }
 }
 
