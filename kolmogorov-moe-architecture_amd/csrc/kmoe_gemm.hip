@@ -268,19 +268,6 @@ struct GemmArgs {
   float* Cf;
 };
 
-// Output of a weight-gradient tile: bf16 to C; bf16 with the column tile split
-// between C and C2 (the gate and up halves of a w13-ordered tile); fp32 to Cf.
-constexpr int OUT_BF16 = 0, OUT_SPLIT = 1, OUT_F32 = 2;
-
-// One output tile: rows [m0, min(m0 + 256, m_end)) of expert e against B rows of
-// full column tile nt (narrow part q when WNB < 4).
-// FP8: A/B bytes are e4m3; a_scale per A row, b_scale per B row (global row index).
-// GATHER: A is the unpermuted activation matrix and permuted row r is its row
-// row_index[row_token[r]] (row_token[r] without row_index): the dispatch gather is
-// fused into the A loads.
-// RSCALE (bf16 gathered gate/up tiles): a_scale[row_token[r]] scales row r's gate and
-// up values before the SiLU (the per-token RMSNorm scale of x: the norm weight is
-// folded into the packed w1 / w2 rows, and a per-row scale commutes with the product).
 // Stores a tile staged in LDS (BM rows of OCPR 16-byte chunks, row stride OSTR bytes)
 // to the rows [m0, m_end) of `out` (row stride ld elements, chunk ch at out + 8 ch;
 // chunks from column col0 + 8 ch >= n_valid are not stored).  A thread always handles
@@ -310,6 +297,19 @@ __device__ __forceinline__ void store_staged(const uint8_t* lds, int tid, int m0
   }
 }
 
+// Output of a weight-gradient tile: bf16 to C; bf16 with the column tile split
+// between C and C2 (the gate and up halves of a w13-ordered tile); fp32 to Cf.
+constexpr int OUT_BF16 = 0, OUT_SPLIT = 1, OUT_F32 = 2;
+
+// One output tile: rows [m0, min(m0 + 256, m_end)) of expert e against B rows of
+// full column tile nt (narrow part q when WNB < 4).
+// FP8: A/B bytes are e4m3; a_scale per A row, b_scale per B row (global row index).
+// GATHER: A is the unpermuted activation matrix and permuted row r is its row
+// row_index[row_token[r]] (row_token[r] without row_index): the dispatch gather is
+// fused into the A loads.
+// RSCALE (bf16 gathered gate/up tiles): a_scale[row_token[r]] scales row r's gate and
+// up values before the SiLU (the per-token RMSNorm scale of x: the norm weight is
+// folded into the packed w1 / w2 rows, and a per-row scale commutes with the product).
 // NMA: the row blocks of this wave that hold rows of the expert.  A wave's 128 rows
 // are 4 blocks of 32; a slot's last tile is often partly empty, and its waves then
 // run with NMA < 4 (the first NMA blocks), which skips the other blocks' fragment
@@ -431,12 +431,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
 #pragma unroll
     for (int mi = 0; mi < NMA; ++mi)
 #pragma unroll
-      for (int j = 0; j < WNB; ++j) mfma<FP8>(acc[mi][j], a[mi], b[j]);
+      for (int j = 0; j < WNB; ++j) mfma<FP8>(acc[mi][j], b[j], a[mi]);
   };
   // MFMAs [lo, hi) of a substep (linear index mi * WNB + j)
   auto mma_part = [&](const Frag<FP8> (&a)[4], const Frag<FP8> (&b)[WNB], auto lo_tag, auto hi_tag) {
     static_for<decltype(lo_tag)::value, decltype(hi_tag)::value>(
-        [&](auto xc) { mfma<FP8>(acc[decltype(xc)::value / WNB][decltype(xc)::value % WNB], a[decltype(xc)::value / WNB], b[decltype(xc)::value % WNB]); });
+        [&](auto xc) { mfma<FP8>(acc[decltype(xc)::value / WNB][decltype(xc)::value % WNB], b[decltype(xc)::value % WNB], a[decltype(xc)::value / WNB]); });
   };
 
   // Pipeline.  Step kt computes LDS stage kt%2 while the registers hold step kt+1's
@@ -514,17 +514,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   for (int kt = 0; kt + 1 < nk; ++kt) step(kt, std::false_type{});
   step(nk - 1, std::true_type{});
 
-  // ---- epilogue.  acc[mi][j][r] is (row 8*(r/4)+4*lh+r%4, col lr) of block (mi, j).
-  // Results go to an LDS tile (rows padded by 16 bytes) as bf16 pairs, then out with
-  // 16-byte stores along rows.  Pairs are formed across neighbouring lanes with DPP
-  // (VALU, no LDS round trip): for the rows of r = 2p and 2p+1, an even lane packs
-  // its own and its right neighbour's value of row 2p, an odd lane its left
-  // neighbour's and its own of row 2p+1, so every lane writes 4 bytes, unmasked.
+  // ---- epilogue.  The MFMAs take the B fragment as their first operand, so block
+  // (mi, j) accumulates the transposed product: acc[mi][j][4c+t] is A row mi*32 + lr
+  // against B row 8c + 4lh + t of B block j, i.e. output row wm*128 + mi*32 + lr and
+  // four consecutive output columns per c.  A lane packs each such run to 8 bytes of
+  // bf16 in registers and writes it to an LDS tile (rows padded by 16 bytes), which
+  // then goes out with 16-byte stores along rows.
   static_assert(!SAVE_GU || (GATE_UP && !FP8), "g/u saving is for bf16 gate/up tiles");
   constexpr int NC = GATE_UP ? 32 * WNB : 64 * WNB;  // output columns of the tile
   constexpr int NJ = GATE_UP ? WNB / 2 : WNB;        // output column blocks per wave
   constexpr int OSTR = NC * 2 + 16;                  // LDS row stride (bytes)
-  const bool odd = lr & 1;
   float* const sa_l = reinterpret_cast<float*>(lds + SCALE_LDS);
   float* const sb_l = sa_l + BM;
   if constexpr (FP8) {
@@ -533,59 +532,53 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   }
   if constexpr (RSCALE) sa_l[tid] = sa_v;
   __syncthreads();
-  // lane's write address for p = 0 of block (0, 0): even lanes row 4lh col lr,
-  // odd lanes row 4lh+1 col lr-1
-  uint8_t* const wbase = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR + (wn * (NC / 2) + lr - (odd ? 1 : 0)) * 2;
-  // The scales go to registers first: the B-row scales of the lane's WNB blocks once, the
-  // A-row scales of each row block (16 rows of the lane) before its results.  Read from
-  // LDS per output element, they were re-read after every staging write (the compiler
-  // cannot tell the two LDS areas apart): about 4.5 k more cycles per tile than bf16.
-  float sbr[WNB];
+  // The scales go to registers first: the B-row scales of the lane's 16 B rows of each
+  // block once, the A-row scale of each row block before its results.  Read from LDS
+  // per output element, they were re-read after every staging write (the compiler
+  // cannot tell the two LDS areas apart).
+  float sbr[WNB][16];
 #pragma unroll
-  for (int j = 0; j < WNB; ++j) sbr[j] = FP8 ? sb_l[b_lds_row<GATE_UP, WNB>(wn, j, lr)] : 1.0f;
-  float sar[16];
+  for (int j = 0; j < WNB; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      sbr[j][r] = FP8 ? sb_l[b_lds_row<GATE_UP, WNB>(wn, j, 8 * (r >> 2) + 4 * lh + (r & 3))] : 1.0f;
+  float sar = 1.0f;
   auto result = [&](int mi, int r, int jo) -> float {
     if (GATE_UP) {
       float gg = acc[mi][jo][r], u = acc[mi][jo + WNB / 2][r];
       if (FP8) {
-        gg *= sar[r] * sbr[jo];
-        u *= sar[r] * sbr[jo + WNB / 2];
+        gg *= sar * sbr[jo][r];
+        u *= sar * sbr[jo + WNB / 2][r];
       }
       if (RSCALE) {
-        gg *= sar[r];
-        u *= sar[r];
+        gg *= sar;
+        u *= sar;
       }
       return silu_fast_f32(gg) * u;
     } else {
       float v = acc[mi][jo][r];
-      if (FP8) v *= sar[r] * sbr[jo];
+      if (FP8) v *= sar * sbr[jo][r];
       return v;
     }
   };
+  auto pack4 = [](float a, float b, float c, float d) {
+    const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+    const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{c, d}, bf16x2_t));
+    return i32x2_t{(int)lo, (int)hi};
+  };
+  // lane's row of block 0 and its first column (c = 0) of output column block 0
+  uint8_t* const wbase = lds + (wm * 128 + lr) * OSTR + (wn * (NC / 2) + 4 * lh) * 2;
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
     if (mi >= NMA) break;  // rows past the expert's end: never stored
-    if constexpr (FP8 || RSCALE) {
+    if constexpr (FP8 || RSCALE) sar = sa_l[wm * 128 + mi * 32 + lr];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sar[r] = sa_l[wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
-    }
+    for (int jo = 0; jo < NJ; ++jo)
 #pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const int r0 = 2 * p, r1 = 2 * p + 1;
-#pragma unroll
-      for (int jo = 0; jo < NJ; ++jo) {
-        const float a = result(mi, r0, jo), b = result(mi, r1, jo);
-        // row_shl:1 -> value of lane+1, row_shr:1 -> value of lane-1 (within 16 lanes)
-        const float a_next = __builtin_bit_cast(
-            float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, a), 0x101, 0xf, 0xf, false));
-        const float b_prev = __builtin_bit_cast(
-            float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, b), 0x111, 0xf, 0xf, false));
-        const float lo = odd ? b_prev : a, hi = odd ? b : a_next;
-        const uint32_t packed = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
-        // row of r0 is mi*32 + 8*(p/2) + 2*(p%2) (+1 for odd lanes via wbase)
-        *reinterpret_cast<uint32_t*>(wbase + (mi * 32 + 8 * (p >> 1) + 2 * (p & 1)) * OSTR + jo * 64) = packed;
-      }
-    }
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<i32x2_t*>(wbase + mi * 32 * OSTR + (jo * 32 + 8 * c) * 2) =
+            pack4(result(mi, 4 * c, jo), result(mi, 4 * c + 1, jo), result(mi, 4 * c + 2, jo),
+                  result(mi, 4 * c + 3, jo));
   }
   __syncthreads();
   constexpr int OCPR = NC * 2 / 16;  // 16-byte chunks per output row
@@ -598,24 +591,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
     constexpr int NC2 = 64 * WNB;
     constexpr int OSTR2 = NC2 * 2 + 16;
     __syncthreads();
-    uint8_t* const wb2 = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR2 + (lr - (odd ? 1 : 0)) * 2;
+    uint8_t* const wb2 = lds + (wm * 128 + lr) * OSTR2 + 4 * lh * 2;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       if (mi >= NMA) break;
 #pragma unroll
-      for (int p = 0; p < 8; ++p) {
+      for (int j = 0; j < WNB; ++j) {
+        const int col = b_lds_row<true, WNB>(wn, j, 0);
 #pragma unroll
-        for (int j = 0; j < WNB; ++j) {
-          const float a = acc[mi][j][2 * p], b = acc[mi][j][2 * p + 1];
-          const float a_next = __builtin_bit_cast(
-              float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, a), 0x101, 0xf, 0xf, false));
-          const float b_prev = __builtin_bit_cast(
-              float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, b), 0x111, 0xf, 0xf, false));
-          const float lo = odd ? b_prev : a, hi = odd ? b : a_next;
-          const uint32_t packed = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
-          const int col = b_lds_row<true, WNB>(wn, j, 0);
-          *reinterpret_cast<uint32_t*>(wb2 + (mi * 32 + 8 * (p >> 1) + 2 * (p & 1)) * OSTR2 + col * 2) = packed;
-        }
+        for (int c = 0; c < 4; ++c)
+          *reinterpret_cast<i32x2_t*>(wb2 + mi * 32 * OSTR2 + (col + 8 * c) * 2) =
+              pack4(acc[mi][j][4 * c], acc[mi][j][4 * c + 1], acc[mi][j][4 * c + 2], acc[mi][j][4 * c + 3]);
       }
     }
     __syncthreads();
