@@ -167,11 +167,15 @@ __device__ __forceinline__ void mfma(f32x16_t& acc, const Frag<FP8>& a, const Fr
 // B-tile geometry of a tile whose waves hold WNB 32-row B blocks each (WNB = 4: the
 // full 256 B rows; 2 and 1: the narrow tiles of the split tail, a half or a
 // quarter `q` of a full tile's output columns).  LDS B row of block j of wave
-// column wn:  down: 32 WNB wn + 32 j + lr;  gate_up: the first WNB/2 blocks are
-// gate rows and the rest the up rows of the same f columns.
+// column wn:  down: 32 WNB wn + 32 j + lr;  gate_up (WNB >= 2): the first WNB/2
+// blocks are gate rows and the rest the up rows of the same f columns;  gate_up
+// WNB = 1: the wave's one block is 16 gate rows then the 16 up rows of the same f
+// columns (LDS rows 32 wn + lr).
 template <bool GATE_UP, int WNB>
 __device__ __forceinline__ int b_lds_row(int wn, int j, int lr) {
-  if constexpr (GATE_UP) {
+  if constexpr (GATE_UP && WNB == 1) {
+    return wn * 32 + lr;
+  } else if constexpr (GATE_UP) {
     constexpr int H = WNB / 2;
     return (j / H) * (32 * WNB) + wn * (16 * WNB) + (j % H) * 32 + lr;
   } else {
@@ -182,7 +186,10 @@ __device__ __forceinline__ int b_lds_row(int wn, int j, int lr) {
 // gate_up packs 128 gate rows then 128 up rows per full tile.
 template <bool GATE_UP, int WNB>
 __device__ __forceinline__ int b_packed_row(int lrow, int q) {
-  if constexpr (GATE_UP) {
+  if constexpr (GATE_UP && WNB == 1) {
+    const int i = lrow & 31;  // f column 32 q + 16 (lrow / 32) + i % 16; up rows from i = 16
+    return (i >> 4) * 128 + q * 32 + (lrow >> 5) * 16 + (i & 15);
+  } else if constexpr (GATE_UP) {
     constexpr int HR = 32 * WNB;  // gate (or up) rows of the tile
     return (lrow / HR) * 128 + q * HR + lrow % HR;
   } else {
@@ -318,7 +325,7 @@ constexpr int OUT_BF16 = 0, OUT_SPLIT = 1, OUT_F32 = 2;
 template <bool GATE_UP, bool FP8, bool GATHER, int WNB, bool SAVE_GU = false, bool RSCALE = false, int NMA = 4>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e, int m0, int m_end, int nt,
                                           int q) {
-  static_assert(WNB == 4 || WNB == 2 || (WNB == 1 && !GATE_UP), "tile width");
+  static_assert(WNB == 4 || WNB == 2 || WNB == 1, "tile width");
   constexpr int NSUB = FP8 ? KB / 64 : KB / 32;  // MFMA K-substeps per pipeline step
   constexpr int BNT = 64 * WNB;                  // B rows of the tile
   constexpr int TBB = BNT * KB;                  // bytes of one B stage tile
@@ -522,7 +529,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   // then goes out with 16-byte stores along rows.
   static_assert(!SAVE_GU || (GATE_UP && !FP8), "g/u saving is for bf16 gate/up tiles");
   constexpr int NC = GATE_UP ? 32 * WNB : 64 * WNB;  // output columns of the tile
-  constexpr int NJ = GATE_UP ? WNB / 2 : WNB;        // output column blocks per wave
+  // output column blocks per wave, and 4-column runs per block and lane: a gate/up
+  // WNB = 1 block holds its gate values in runs c = 0, 1 and the up values of the same
+  // columns in runs c + 2
+  constexpr bool GU1 = GATE_UP && WNB == 1;
+  constexpr int NJ = GU1 ? 1 : GATE_UP ? WNB / 2 : WNB;
+  constexpr int NCR = GU1 ? 2 : 4;
   constexpr int OSTR = NC * 2 + 16;                  // LDS row stride (bytes)
   float* const sa_l = reinterpret_cast<float*>(lds + SCALE_LDS);
   float* const sb_l = sa_l + BM;
@@ -545,10 +557,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   float sar = 1.0f;
   auto result = [&](int mi, int r, int jo) -> float {
     if (GATE_UP) {
-      float gg = acc[mi][jo][r], u = acc[mi][jo + WNB / 2][r];
+      constexpr int UJ = GU1 ? 0 : WNB / 2, UR = GU1 ? 8 : 0;  // up value: block jo + UJ, run + UR/4
+      float gg = acc[mi][jo][r], u = acc[mi][jo + UJ][r + UR];
       if (FP8) {
         gg *= sar * sbr[jo][r];
-        u *= sar * sbr[jo + WNB / 2][r];
+        u *= sar * sbr[jo + UJ][r + UR];
       }
       if (RSCALE) {
         gg *= sar;
@@ -575,7 +588,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
 #pragma unroll
     for (int jo = 0; jo < NJ; ++jo)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < NCR; ++c)
         *reinterpret_cast<i32x2_t*>(wbase + mi * 32 * OSTR + (jo * 32 + 8 * c) * 2) =
             pack4(result(mi, 4 * c, jo), result(mi, 4 * c + 1, jo), result(mi, 4 * c + 2, jo),
                   result(mi, 4 * c + 3, jo));
@@ -632,7 +645,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
   const int rounds = n_all / n_cu, base = rounds * n_cu, n_rest = n_all - base;
   int split = 1;
   if (allow_split && n_rest > 0) {
-    if (!GATE_UP && 4 * n_rest <= n_cu)
+    if (4 * n_rest <= n_cu)
       split = 4;
     else if (2 * n_rest <= n_cu)
       split = 2;
@@ -666,7 +679,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 1) __attribute__((amdgpu_waves_per_eu
       gemm_tile<GATE_UP, FP8, GATHER, 4, SAVE_GU, RSCALE, 0>(g, lds, e, m0, m_end, nt, 0);
   } else if (split == 2)
     gemm_tile<GATE_UP, FP8, GATHER, 2, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, q);
-  else if constexpr (!GATE_UP)
+  else
     gemm_tile<GATE_UP, FP8, GATHER, 1, SAVE_GU, RSCALE>(g, lds, e, m0, m_end, nt, q);
 }
 

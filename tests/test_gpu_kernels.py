@@ -353,6 +353,71 @@ def test_grouped_swiglu_fp8(dev):
     assert relL2(npf(y[:A]), ref) <= 1e-1
 
 
+@pytest.mark.parametrize("path", ["bf16", "gather", "save_gu", "rscale", "fp8"])
+@pytest.mark.parametrize("rest", [4, 84, 144])
+def test_split_tail_tiles_bit_identical(dev, path, rest):
+    """The last partial round of tiles runs as narrow tiles (a quarter of the columns when
+    at most n_cu/4 tiles are left, a half when at most n_cu/2, whole tiles otherwise).
+    They compute every output element with the same MFMAs as a full tile: the experts
+    of a launch whose tail they fill (`rest` tiles past the last full round: split 4,
+    2, 1) give the same bits as in a launch with an extra expert appended, which has no
+    partial round at all, for the gate/up (plain, gathered, g/u-saving, RMS-scaled,
+    fp8) and the down GEMMs."""
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    d, F = 512, 256  # 2 column tiles per slot in both GEMMs
+    assert rest % 2 == 0 and rest < n_cu
+    slots_a = (n_cu + rest) // 2  # tiles: n_cu + rest
+    slots_b = n_cu                # tiles: 2 n_cu (two full rounds)
+    rng = np.random.default_rng(rest)
+    # slots per expert (7 experts), rows 256 (s - 1) + r with r in [1, 256]
+    sl = np.full(7, slots_a // 7)
+    sl[: slots_a - sl.sum()] += 1
+    counts = [int(256 * (s - 1) + r) for s, r in zip(sl, rng.integers(1, 257, 7))]
+    counts[1] = 256 * (int(sl[1]) - 1) + 256  # a slot of exactly 256 rows
+    counts[2] = 256 * (int(sl[2]) - 1) + 1    # and one of a single row
+    counts_b = counts + [256 * (slots_b - slots_a)]
+    A, Ab = sum(counts), sum(counts_b)
+    w1, w2, w3 = _experts(8, d, F, 40)
+    (x,) = gen(41, (Ab, d))
+    xb = bf16(x).to(dev)
+    fp8 = path == "fp8"
+    pws = [ops.pack_weights(bf16(w1[:E]).to(dev), bf16(w2[:E]).to(dev), bf16(w3[:E]).to(dev), fp8=fp8)
+           for E in (7, 8)]
+    rs = (torch.rand(Ab, generator=torch.Generator().manual_seed(42)) + 0.5).to(dev)
+    outs = []
+    for cnt, pw in zip((counts, counts_b), pws):
+        n = sum(cnt)
+        off = torch.tensor(np.concatenate([[0], np.cumsum(cnt)]), dtype=torch.int32, device=dev)
+        rt = torch.arange(n, dtype=torch.int32, device=dev)
+        xs = xb[:n]
+        gu = None
+        if path == "bf16":
+            h = ops.gemm_gate_up(xs, None, off, pw, n)
+        elif path == "gather":
+            h = ops.gemm_gate_up_rows(xs, None, rt, off, pw, n)
+        elif path == "save_gu":
+            h, gu = ops.gemm_gate_up_rows(xs, None, rt, off, pw, n, save_gu=True)
+        elif path == "rscale":
+            h = ops.gemm_gate_up_rows(xs, None, rt, off, pw, n, rscale=rs[:n].contiguous())
+        if fp8:
+            xq, xsc = ops.gather_rows(xb, rt, n, fp8=True)
+            h = ops.gemm_gate_up(xq, xsc, off, pw, n)
+            y = ops.grouped_ffn(xq, xsc, off, pw, n)
+        else:
+            y = ops.gemm_down(h, None, off, pw, n)
+        outs.append((h, gu, y))
+    torch.cuda.synchronize()
+    (ha, gua, ya), (hb, gub, yb) = outs
+    assert torch.equal(ha[:A].view(torch.int16), hb[:A].view(torch.int16))
+    assert torch.equal(ya[:A].view(torch.int16), yb[:A].view(torch.int16))
+    if gua is not None:
+        assert torch.equal(gua[:A].view(torch.int16), gub[:A].view(torch.int16))
+    if path == "bf16":
+        off = np.concatenate([[0], np.cumsum(counts)])
+        ref = O.swiglu_rows(npf(xb[:A]), off, npf(bf16(w1[:7])), npf(bf16(w2[:7])), npf(bf16(w3[:7])))
+        assert relL2(npf(ya[:A]), ref) <= 1e-2
+
+
 # ------------------------------------------------------------------ combine
 def test_combine_parity(dev):
     T, fan, d, R = 1000, 3, 384, 2500
