@@ -17,8 +17,10 @@
 // are bank-conflict free.  Fragment reads, LDS writes and loads are interleaved
 // with the MFMAs by scheduling groups; fragments are double buffered in registers;
 // one barrier per step, in its last substep.
-// The output tile is staged through LDS (bf16 pairs formed across lanes with DPP)
-// and written with 16-byte row stores.
+// The MFMAs take the B fragment as their first operand, so each lane accumulates
+// runs of four consecutive output columns of one row; the epilogue packs them to
+// 8-byte bf16 runs in registers, stages the tile through LDS and writes it with
+// 16-byte row stores.
 //
 // Ragged groups: every row tile ("slot") of every expert is enumerated from the
 // device-resident offsets; the grid is sized for the worst case
