@@ -8,6 +8,8 @@ Bars (as the per-kernel tests): routing indices and per-expert counts bit-exact 
 kernel's own fp32 logits; router logits within 2e-5 abs / 1e-4 rel of fp64; the layer
 output rel-L2 <= 1e-2 of the fp32 oracle on the same bf16 inputs; the aux loss within
 1e-4 relative."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -19,6 +21,9 @@ from kmoe.moe import MoELayer
 from oracle import moe_oracle as O
 
 pytestmark = pytest.mark.gpu
+
+# KMOE_SWEEP_DRAWS=N runs N draws of each sweep instead of the default 16 / 6 / 6
+_DRAWS = int(os.environ.get("KMOE_SWEEP_DRAWS", "0"))
 
 
 def _draw(i):
@@ -51,7 +56,7 @@ def _layer(dev, T, d, E, k, F, cap, bias, seed):
     return cfg, layer, g
 
 
-@pytest.mark.parametrize("i", range(16))
+@pytest.mark.parametrize("i", range(_DRAWS or 16))
 def test_layer_forward_sweep(dev, i):
     T, d, E, k, F, cap, bias = _draw(i)
     print(f"sweep {i}: T={T} d={d} E={E} k={k} F={F} cap={cap} bias={bias}", flush=True)
@@ -78,7 +83,7 @@ def test_layer_forward_sweep(dev, i):
     assert abs(aux - ref["aux"][0]) <= 1e-4 * abs(ref["aux"][0]) + 1e-7
 
 
-@pytest.mark.parametrize("i", range(6))
+@pytest.mark.parametrize("i", range(_DRAWS or 6))
 def test_ffn_block_sweep(dev, i):
     T, d, E, k, F, cap, bias = _draw(100 + i)
     print(f"block sweep {i}: T={T} d={d} E={E} k={k} F={F} cap={cap} bias={bias}", flush=True)
@@ -106,7 +111,7 @@ def test_ffn_block_sweep(dev, i):
     assert _rel(f(out.reshape(T, d)) - hr, ref["y"] - hr) <= 1e-2
 
 
-@pytest.mark.parametrize("i", range(6))
+@pytest.mark.parametrize("i", range(_DRAWS or 6))
 def test_backward_sweep(dev, i):
     """Gradients of the training path (HIP backward) against fp64 autograd of the oracle's
     restatement of the reference forward at the kernel's routing (as test_gpu_backward.py):
