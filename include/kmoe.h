@@ -119,6 +119,19 @@ int kmoe_dispatch_counted(const void* x, const int32_t* row_index, int64_t T, in
                           int32_t* slot_row, float* slot_w, void* xperm, int xperm_dtype, float* xperm_scale,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* kmoe_dispatch_counted that also writes the aux losses of kmoe_aux_loss (the
+ * dispatch's load-balancing inputs of MoELayer._compute_auxiliary_losses,
+ * moe.py:840-939, with counts = this dispatch's routed counts): aux_out[0..2] as
+ * kmoe_aux_loss's out, bit for bit.  Up to 65536 tokens one more workgroup of the
+ * table launch reduces the router's partials, so a training forward needs no launch
+ * for the losses; beyond, kmoe_aux_loss runs after the dispatch.  T must be > 0. */
+int kmoe_dispatch_counted_aux(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
+                              const void* topk_w, int w_dtype, int k, int E, int64_t capacity,
+                              const int32_t* block_counts, int32_t* counts, int32_t* offsets, int32_t* row_token,
+                              int32_t* slot_row, float* slot_w, void* xperm, int xperm_dtype, float* xperm_scale,
+                              void* workspace, size_t workspace_bytes, const float* partials, float w_lb,
+                              float w_z, float* aux_out, void* stream);
+
 /* Allocation-free dispatch.  No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments, semantics and results as

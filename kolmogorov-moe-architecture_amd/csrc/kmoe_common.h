@@ -133,6 +133,39 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// Auxiliary losses from the router's per-block partial sums (moe.py:840-939): column c
+// of block b is partials[b (E + 1) + c], the block's summed softmax probabilities of
+// expert c (c < E) or its summed lse^2 (c = E).  aux_reduce_cols: wave w of `nw` waves
+// reduces columns w, w + nw, ...; lane l sums blocks l, l + 64, ... in order, then the
+// wave sums its lanes with a fixed shuffle tree, so the result does not depend on the
+// launch (bit-reproducible).  col[] lives in LDS; the caller synchronises before
+// aux_finish reads it.
+__device__ __forceinline__ void aux_reduce_cols(const float* __restrict__ partials, int64_t nblk, int E, int wave,
+                                                int nw, int lane, float* col) {
+  for (int c = wave; c <= E; c += nw) {
+    float s = 0.0f;
+    for (int64_t b = lane; b < nblk; b += 64) s += partials[b * (E + 1) + c];
+    s = wave_sum(s);
+    if (lane == 0) col[c] = s;
+  }
+}
+// out = (w_lb lb + w_z z, lb, z): lb = E sum_e (counts[e] / (T k)) (P_e / T) (0 without
+// counts), z = mean lse^2.  One thread.
+__device__ __forceinline__ void aux_finish(const float* col, const int32_t* counts, int64_t T, int E, int k,
+                                           float w_lb, float w_z, float* __restrict__ out) {
+  const float invT = 1.0f / (float)T;
+  float lb = 0.0f;
+  if (counts) {
+    const float inv_assign = 1.0f / ((float)T * (float)k);
+    for (int e = 0; e < E; ++e) lb += ((float)counts[e] * inv_assign) * (col[e] * invT);
+    lb *= (float)E;
+  }
+  const float z = col[E] * invT;
+  out[0] = w_lb * lb + w_z * z;
+  out[1] = lb;
+  out[2] = z;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

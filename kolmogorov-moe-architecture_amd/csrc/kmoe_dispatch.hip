@@ -85,6 +85,10 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ 
 // blocks before it), the totals and the expert offsets from all block counts (block
 // 0 also writes counts and offsets), instead of reading them from the scan kernel:
 // one launch less, for up to FUSED_SCAN_MAX_BLOCKS blocks.
+// With aux_out (FUSED_SCAN only) the launch has one block more, block nblk: it sums the
+// block counts like the others (the routed count of each expert), then reduces the
+// router's aux partials and writes the auxiliary losses (aux_reduce_cols / aux_finish:
+// the same sums in the same order as kmoe_aux_loss) instead of a launch of its own.
 constexpr int FUSED_SCAN_MAX_BLOCKS = 1024;
 template <bool FUSED_SCAN>
 __global__ __launch_bounds__(DTHREADS) void permute_kernel(
@@ -92,11 +96,15 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
     const int64_t* __restrict__ idx, const void* __restrict__ wsrc, int w_dtype, int k, int E, int64_t capacity,
     const int32_t* __restrict__ block_counts, int64_t nblk, const int32_t* __restrict__ block_base,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ row_token,
-    int32_t* __restrict__ slot_row, float* __restrict__ slot_w) {
+    int32_t* __restrict__ slot_row, float* __restrict__ slot_w, const float* __restrict__ aux_partials,
+    float w_lb, float w_z, float* __restrict__ aux_out) {
   __shared__ int wave_cnt[DTHREADS / 64][KMOE_MAX_EXPERTS];
   __shared__ int running[KMOE_MAX_EXPERTS];
   __shared__ int base_l[KMOE_MAX_EXPERTS];
   __shared__ int off_l[KMOE_MAX_EXPERTS + 1];
+  __shared__ int tot_l[KMOE_MAX_EXPERTS];           // aux block: routed count per expert
+  __shared__ float aux_col[KMOE_MAX_EXPERTS + 1];  // aux block: partial column sums
+  const bool aux_block = FUSED_SCAN && aux_out && (int64_t)blockIdx.x == nblk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = (int64_t)blockIdx.x * DTB;
   const int64_t a0 = t0 * k;
@@ -159,6 +167,7 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
       if (lane < E) {
         base_l[lane] = p;
         off_l[lane] = incl - kept;
+        tot_l[lane] = c;
         if (blockIdx.x == 0) {
           counts[lane] = c;
           offsets[lane] = incl - kept;
@@ -177,6 +186,12 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
     }
   }
   __syncthreads();
+  if (aux_block) {
+    aux_reduce_cols(aux_partials, nblk, E, wave, DTHREADS / 64, lane, aux_col);
+    __syncthreads();
+    if (tid == 0) aux_finish(aux_col, tot_l, T, E, k, w_lb, w_z, aux_out);
+    return;
+  }
 
   // ---- ranks, in assignment order (chunks of 256 assignments)
   for (int64_t c0 = a0; c0 < a1; c0 += DTHREADS) {
@@ -388,7 +403,8 @@ int dispatch_launch(const void* x, const int32_t* row_index, int64_t T, int d, c
                     const void* topk_w, int w_dtype, int k, int E, int64_t capacity, int32_t* counts,
                     int32_t* offsets, int32_t* row_token, int32_t* slot_row, float* slot_w, void* xperm,
                     int xperm_dtype, float* xperm_scale, void* workspace, hipStream_t s,
-                    const int32_t* given_counts = nullptr) {
+                    const int32_t* given_counts = nullptr, const float* aux_partials = nullptr, float w_lb = 0.0f,
+                    float w_z = 0.0f, float* aux_out = nullptr) {
   const int64_t nblk = kmoe::ceil_div<int64_t>(T, DTB);
   int32_t* ws_counts = static_cast<int32_t*>(workspace);
   int32_t* block_base = ws_counts + nblk * E;
@@ -399,20 +415,27 @@ int dispatch_launch(const void* x, const int32_t* row_index, int64_t T, int d, c
                        counts, offsets);
     return kmoe::check_launch("kmoe_dispatch(scan)");
   }
+  // the auxiliary losses ride on the permute launch when it sums the block counts itself
+  const bool aux_fused = aux_out && nblk <= FUSED_SCAN_MAX_BLOCKS;
   if (!given_counts)
     hipLaunchKernelGGL(hist_kernel, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, topk_idx, T, k, E, ws_counts);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const bool fp8 = xperm_dtype == KMOE_DTYPE_FP8_E4M3;
   if (nblk <= FUSED_SCAN_MAX_BLOCKS) {
-    hipLaunchKernelGGL(permute_kernel<true>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
-                       topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, block_base, counts, offsets,
-                       row_token, slot_row, slot_w);
+    hipLaunchKernelGGL(permute_kernel<true>, dim3((unsigned)(nblk + (aux_fused ? 1 : 0))), dim3(DTHREADS), 0, s, xp,
+                       row_index, T, d, topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, block_base,
+                       counts, offsets, row_token, slot_row, slot_w, aux_partials, w_lb, w_z,
+                       aux_fused ? aux_out : nullptr);
   } else {
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, nblk, E, capacity, block_base, counts,
                        offsets);
     hipLaunchKernelGGL(permute_kernel<false>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
                        topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, block_base, counts, offsets,
-                       row_token, slot_row, slot_w);
+                       row_token, slot_row, slot_w, nullptr, 0.0f, 0.0f, nullptr);
+  }
+  if (aux_out && !aux_fused) {
+    const int rc = kmoe_aux_loss(aux_partials, T, E, counts, k, w_lb, w_z, aux_out, s);
+    if (rc) return rc;
   }
   const dim3 rows_grid((unsigned)kmoe::ceil_div<int64_t>(T, 4));
   if (fp8)
@@ -487,6 +510,27 @@ extern "C" int kmoe_dispatch_counted(const void* x, const int32_t* row_index, in
   return dispatch_launch(x, row_index, T, d, topk_idx, topk_w, w_dtype, k, E, capacity, counts, offsets, row_token,
                          slot_row, slot_w, xperm, xperm_dtype, xperm_scale, workspace, kmoe::as_stream(stream),
                          block_counts);
+}
+
+extern "C" int kmoe_dispatch_counted_aux(const void* x, const int32_t* row_index, int64_t T, int d,
+                                         const int64_t* topk_idx, const void* topk_w, int w_dtype, int k, int E,
+                                         int64_t capacity, const int32_t* block_counts, int32_t* counts,
+                                         int32_t* offsets, int32_t* row_token, int32_t* slot_row, float* slot_w,
+                                         void* xperm, int xperm_dtype, float* xperm_scale, void* workspace,
+                                         size_t workspace_bytes, const float* partials, float w_lb, float w_z,
+                                         float* aux_out, void* stream) {
+  int rc = check_dispatch_args("kmoe_dispatch_counted_aux", x, T, d, topk_idx, topk_w, w_dtype, k, E, counts,
+                               offsets, row_token, slot_row, slot_w, xperm, xperm_dtype, xperm_scale);
+  if (rc) return rc;
+  KMOE_REQUIRE(block_counts && partials && aux_out, KMOE_ERR_NULL,
+               "kmoe_dispatch_counted_aux: null block_counts / partials / aux_out");
+  KMOE_REQUIRE(T > 0, KMOE_ERR_SHAPE, "kmoe_dispatch_counted_aux: T must be > 0 (the losses average over tokens)");
+  const size_t need = kmoe_dispatch_workspace_bytes(T, k, E);
+  KMOE_REQUIRE(workspace && workspace_bytes >= need, KMOE_ERR_WORKSPACE,
+               "kmoe_dispatch_counted_aux: workspace %zu < %zu bytes", workspace_bytes, need);
+  return dispatch_launch(x, row_index, T, d, topk_idx, topk_w, w_dtype, k, E, capacity, counts, offsets, row_token,
+                         slot_row, slot_w, xperm, xperm_dtype, xperm_scale, workspace, kmoe::as_stream(stream),
+                         block_counts, partials, w_lb, w_z, aux_out);
 }
 
 extern "C" int kmoe_dispatch_noalloc(const void* x, const int32_t* row_index, int64_t T, int d,

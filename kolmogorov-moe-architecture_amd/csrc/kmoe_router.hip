@@ -338,34 +338,15 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   }
 }
 
-// One workgroup, 4 waves: wave w reduces partial columns w, w+4, ...; lane l sums
-// blocks l, l+64, ... and the wave then sums its lanes with a fixed shuffle tree, so
-// the result is bit-reproducible.
+// One workgroup, 4 waves: the column sums (aux_reduce_cols), then thread 0 forms the
+// losses (aux_finish).
 __global__ __launch_bounds__(256) void aux_loss_kernel(const float* __restrict__ partials, int64_t nblk, int64_t T,
                                                        int E, const int32_t* __restrict__ counts, int k, float w_lb,
                                                        float w_z, float* __restrict__ out) {
   __shared__ float col[KMOE_MAX_EXPERTS + 1];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int c = wave; c <= E; c += 4) {
-    float s = 0.0f;
-    for (int64_t b = lane; b < nblk; b += 64) s += partials[b * (E + 1) + c];
-    s = wave_sum(s);
-    if (lane == 0) col[c] = s;
-  }
+  aux_reduce_cols(partials, nblk, E, threadIdx.x >> 6, 4, threadIdx.x & 63, col);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const float invT = 1.0f / (float)T;
-    float lb = 0.0f;
-    if (counts) {
-      const float inv_assign = 1.0f / ((float)T * (float)k);
-      for (int e = 0; e < E; ++e) lb += ((float)counts[e] * inv_assign) * (col[e] * invT);
-      lb *= (float)E;
-    }
-    const float z = col[E] * invT;
-    out[0] = w_lb * lb + w_z * z;
-    out[1] = lb;
-    out[2] = z;
-  }
+  if (threadIdx.x == 0) aux_finish(col, counts, T, E, k, w_lb, w_z, out);
 }
 
 }  // namespace

@@ -40,6 +40,8 @@ _SIGNATURES = {
                              _vp, _i32, _vp, _vp, _sz, _vp]),
     "kmoe_dispatch_counted": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp,
                                      _vp, _vp, _vp, _i32, _vp, _vp, _sz, _vp]),
+    "kmoe_dispatch_counted_aux": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp,
+                                         _vp, _vp, _vp, _i32, _vp, _vp, _sz, _vp, _f32, _f32, _vp, _vp]),
     "kmoe_dispatch_noalloc": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp,
                                      _vp, _vp, _i32, _vp, _vp]),
     "kmoe_gather_rows": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp]),

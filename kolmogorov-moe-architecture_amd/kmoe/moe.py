@@ -266,28 +266,30 @@ class GroupedExperts(_PackedExperts):
     """Token-choice grouped SwiGLU experts (moe.py:161-294)."""
 
     def run(self, x2d, expert_indices, expert_weights, row_index=None, T_out=None, out_map=None, scale=None,
-            out_dtype=torch.bfloat16, residual=None, capacity=0, block_counts=None):
+            out_dtype=torch.bfloat16, residual=None, capacity=0, block_counts=None, aux=None):
         """dispatch -> grouped GEMMs -> combine (+ residual, added in the combine); returns (y, DispatchOut).
         capacity > 0 drops each expert's assignments past the first `capacity` (MoELayer's
         drop_overflow rule); 0, the default and what forward() uses, drops nothing (the
         reference's GroupedExperts never drops).  block_counts: the router's per-block
-        histograms of expert_indices (RouterOut.block_counts), if it wrote them."""
+        histograms of expert_indices (RouterOut.block_counts), if it wrote them.
+        aux = (partials, w_lb, w_z): the dispatch also computes the aux losses
+        (DispatchOut.aux; needs block_counts)."""
         E = self.n_experts
         pw = self.packed()
         T, k = expert_indices.shape
         if pw.fp8:
             disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=capacity, fp8=True,
-                                row_index=row_index, block_counts=block_counts)
+                                row_index=row_index, block_counts=block_counts, aux=aux)
             yperm = ops.grouped_ffn(disp.xperm, disp.xscale, disp.offsets, pw, T * k)
         elif not self.gated:
             # non-gated experts run on the permuted rows (materialised by the dispatch)
             disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=capacity, row_index=row_index,
-                                materialize=True, block_counts=block_counts)
+                                materialize=True, block_counts=block_counts, aux=aux)
             yperm = ops.plain_ffn(disp.xperm, disp.offsets, pw, T * k)[0]
         else:
             # bf16: the gate/up GEMM gathers the token rows itself (no permuted copy of x)
             disp = ops.dispatch(x2d, expert_indices, expert_weights, E, capacity=capacity,
-                                row_index=row_index, materialize=False, block_counts=block_counts)
+                                row_index=row_index, materialize=False, block_counts=block_counts, aux=aux)
             h = ops.gemm_gate_up_rows(x2d, row_index, disp.row_token, disp.offsets, pw, T * k)
             yperm = ops.gemm_down(h, None, disp.offsets, pw, T * k)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k),
@@ -648,15 +650,18 @@ class MoELayer(nn.Module):
         cap = ops.capacity_of(self.capacity_factor, T, k, E) if self.drop_overflow else 0
         # the permuted x rows are kept for the weight gradient (the gated gate/up GEMM still
         # gathers its own A rows from x)
-        disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=True, block_counts=r.block_counts)
+        aux_in = self._aux_args(r, T)
+        disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=True, block_counts=r.block_counts,
+                            aux=aux_in)
         yperm, h, gu = ge.expert_rows(x2d, disp.row_token, disp.offsets, T * k, xperm=disp.xperm, save=True)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T if T_out is None else T_out,
                         out_map=out_map, scale=scale, out_dtype=out_dtype, residual=residual)
         self.last_expert_counts = disp.counts
         aux = None
         if self.training:
-            aux = ops.aux_loss(r.partials, T, E, disp.counts, k, self.load_balance_loss_weight,
-                               self.router_z_loss_weight)[0]
+            aux = (disp.aux if disp.aux is not None else
+                   ops.aux_loss(r.partials, T, E, disp.counts, k, self.load_balance_loss_weight,
+                                self.router_z_loss_weight))[0]
         sv = _bwd.Saved(x2d, r.logits, r.idx, r.w, r.hidden, disp, h, gu, yperm, disp.xperm)
         return y, aux, sv
 
@@ -683,14 +688,22 @@ class MoELayer(nn.Module):
         cap = ops.capacity_of(self.capacity_factor, T, self.top_k, self.n_experts) if self.drop_overflow else 0
         y, disp = self.grouped_experts.run(x2d, r.idx, r.w, row_index=row_index, T_out=T_out, out_map=out_map,
                                            scale=scale, out_dtype=out_dtype, residual=residual, capacity=cap,
-                                           block_counts=r.block_counts)
+                                           block_counts=r.block_counts, aux=self._aux_args(r, T))
         return y, r, disp
+
+    def _aux_args(self, r, T):
+        """(partials, w_lb, w_z) for a dispatch that computes the aux losses too (training
+        mode, router block histograms present), else None."""
+        if self.training and T > 0 and r.block_counts is not None and r.partials is not None:
+            return (r.partials, self.load_balance_loss_weight, self.router_z_loss_weight)
+        return None
 
     def _set_token_choice_aux(self, r, disp, T):
         self.last_expert_counts = disp.counts
         if self.training:
-            out = ops.aux_loss(r.partials, T, self.n_experts, disp.counts, self.top_k,
-                               self.load_balance_loss_weight, self.router_z_loss_weight)
+            out = disp.aux if disp.aux is not None else ops.aux_loss(
+                r.partials, T, self.n_experts, disp.counts, self.top_k, self.load_balance_loss_weight,
+                self.router_z_loss_weight)
             self.aux_loss = out[0]
         else:
             self.aux_loss = 0.0

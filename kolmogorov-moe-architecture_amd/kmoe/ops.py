@@ -165,6 +165,7 @@ class DispatchOut(NamedTuple):
     slot_w: torch.Tensor     # (T*k,) f32
     xperm: torch.Tensor      # (T*k, d) bf16 or uint8 (fp8 e4m3)
     xscale: Optional[torch.Tensor]  # (T*k,) f32 for fp8
+    aux: Optional[torch.Tensor] = None  # (3,) f32 aux losses, when asked for (aux_loss's output)
 
 
 def capacity_of(cf: float, T: int, k: int, E: int) -> int:
@@ -173,7 +174,7 @@ def capacity_of(cf: float, T: int, k: int, E: int) -> int:
 
 
 def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None, materialize=True,
-             no_alloc=False, block_counts=None) -> DispatchOut:
+             no_alloc=False, block_counts=None, aux=None) -> DispatchOut:
     """Stable counting-sort dispatch (moe.py:238-272) + optional capacity drop.
 
     materialize=False (bf16 only) writes the routing tables but not the permuted
@@ -181,7 +182,10 @@ def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None, materialize=
     no_alloc=True calls kmoe_dispatch_noalloc, whose histograms live in the library's
     own device scratch (no workspace allocation; calls on one GPU must not overlap).
     block_counts: the router's per-block histograms of idx (RouterOut.block_counts);
-    kmoe_dispatch_counted then skips counting them."""
+    kmoe_dispatch_counted then skips counting them.
+    aux = (partials, w_lb, w_z) (with block_counts): the aux losses of aux_loss(partials, T,
+    E, counts, k, w_lb, w_z) come back in DispatchOut.aux, computed inside the dispatch's
+    table launch (kmoe_dispatch_counted_aux) instead of a launch of their own."""
     if not materialize and fp8:
         raise ValueError("kmoe.dispatch: the fp8 path needs the quantised permuted rows (materialize=True)")
     _need_gpu(x2d, idx, w)
@@ -211,9 +215,20 @@ def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None, materialize=
         return DispatchOut(counts, offsets, row_token, slot_row, slot_w, xperm, xscale)
     wsb = lib.kmoe_dispatch_workspace_bytes(T, k, E)
     ws = torch.empty(wsb, device=dev, dtype=torch.uint8)
+    if aux is not None and (block_counts is None or no_alloc or T == 0):
+        raise ValueError("kmoe.dispatch: aux needs block_counts (and T > 0, not no_alloc)")
     if block_counts is not None:
         if block_counts.dtype != torch.int32 or block_counts.numel() != ((T + 63) // 64) * E:
             raise ValueError("kmoe.dispatch: block_counts must be int32 (ceil(T/64), E)")
+        if aux is not None:
+            partials, w_lb, w_z = aux
+            aux_out = torch.empty(3, device=dev, dtype=torch.float32)
+            with _Stage("dispatch"):
+                _lib.call("kmoe_dispatch_counted_aux", ptr(x2d), ptr(row_index), T, d, ptr(idx), ptr(w), wdt, k, E,
+                          int(capacity), ptr(block_counts), ptr(counts), ptr(offsets), ptr(row_token), ptr(slot_row),
+                          ptr(slot_w), ptr(xperm), _lib.DTYPE_FP8_E4M3 if fp8 else _lib.DTYPE_BF16, ptr(xscale),
+                          ptr(ws), wsb, ptr(partials), float(w_lb), float(w_z), ptr(aux_out), _stream(x2d))
+            return DispatchOut(counts, offsets, row_token, slot_row, slot_w, xperm, xscale, aux_out)
         with _Stage("dispatch"):
             _lib.call("kmoe_dispatch_counted", ptr(x2d), ptr(row_index), T, d, ptr(idx), ptr(w), wdt, k, E,
                       int(capacity), ptr(block_counts), ptr(counts), ptr(offsets), ptr(row_token), ptr(slot_row),

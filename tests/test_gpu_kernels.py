@@ -196,6 +196,36 @@ def test_dispatch_counted_matches_dispatch(dev, T, k, E, cap, fp8, mat):
     assert np.array_equal(b.slot_row.cpu().numpy()[: T * k], ref["slot_row"])
 
 
+@pytest.mark.parametrize("T,k,E,cap,fp8,mat", [(16384, 2, 16, 0, False, False), (16384, 2, 16, 2560, False, True),
+                                               (777, 3, 7, 50, True, True), (70000, 2, 8, 0, False, False),
+                                               (65536, 1, 64, 0, False, False)])
+def test_dispatch_counted_aux(dev, T, k, E, cap, fp8, mat):
+    """kmoe_dispatch_counted_aux: the tables, rows and codes of kmoe_dispatch_counted and the
+    aux losses of kmoe_aux_loss, bit for bit (one more workgroup of the table launch up to
+    65536 tokens, the separate launch beyond: T = 70000); the losses against the oracle."""
+    d = 128
+    x, w_in, w_out = gen(500 + T % 89, (T, d), (128, d), (E, 128))
+    xb, wib, wob = bf16(x).to(dev), bf16(w_in * 0.05).to(dev), bf16(w_out * 0.05).to(dev)
+    r = ops.router(xb, wib, wob, k)
+    a = ops.dispatch(xb, r.idx, r.w, E, capacity=cap, fp8=fp8, materialize=mat, block_counts=r.block_counts)
+    b = ops.dispatch(xb, r.idx, r.w, E, capacity=cap, fp8=fp8, materialize=mat, block_counts=r.block_counts,
+                     aux=(r.partials, 0.01, 0.001))
+    ref_aux = ops.aux_loss(r.partials, T, E, a.counts, k, 0.01, 0.001)
+    torch.cuda.synchronize()
+    assert a.aux is None and b.aux is not None
+    n = int(a.offsets[-1])
+    for name in ("counts", "offsets", "slot_row", "slot_w"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    assert torch.equal(a.row_token[:n], b.row_token[:n])
+    if mat:
+        assert torch.equal(a.xperm[:n].view(torch.uint8), b.xperm[:n].view(torch.uint8))
+    if fp8:
+        assert torch.equal(a.xscale[:n], b.xscale[:n])
+    assert torch.equal(b.aux, ref_aux)
+    counts = np.bincount(r.idx.cpu().numpy().reshape(-1), minlength=E)
+    np.testing.assert_allclose(npf(b.aux), O.aux_losses(npf(r.logits), counts, T, k, E), rtol=2e-5)
+
+
 def test_dispatch_rows_bf16_row_index_wide(dev):
     """The materialising bf16 dispatch through a row_index with the capacity drop, and a
     row wider than one register pass (d = 10240: the row copy loops)."""
