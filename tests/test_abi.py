@@ -143,6 +143,23 @@ def test_counted_dispatch_and_router_hist_validation(lib):
     assert rc == -1 and "block_counts" in msg
 
 
+def test_counted_dispatch_aux_validation(lib):
+    # kmoe_dispatch_counted's arguments, then partials, w_lb, w_z, aux_out, stream
+    base = [FAKE, NULL, 16, 64, FAKE, FAKE, _lib.DTYPE_F32, 2, 8, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL,
+            _lib.DTYPE_BF16, NULL, FAKE, 1 << 20]
+    rc, msg = _err(lib, "kmoe_dispatch_counted_aux", *base, NULL, 0.01, 0.001, FAKE, NULL)
+    assert rc == -1 and "partials" in msg
+    rc, msg = _err(lib, "kmoe_dispatch_counted_aux", *base, FAKE, 0.01, 0.001, NULL, NULL)
+    assert rc == -1 and "aux_out" in msg
+    no_t = list(base)
+    no_t[2] = 0
+    rc, msg = _err(lib, "kmoe_dispatch_counted_aux", *no_t, FAKE, 0.01, 0.001, FAKE, NULL)
+    assert rc == -2 and "T must be > 0" in msg
+    small = list(base)
+    small[20] = 8
+    assert _err(lib, "kmoe_dispatch_counted_aux", *small, FAKE, 0.01, 0.001, FAKE, NULL)[0] == -4
+
+
 def test_norm_and_mod_backward_validation(lib):
     """Argument checks of the block / MoD training entry points (no launch on failure)."""
     BF, F32 = _lib.DTYPE_BF16, _lib.DTYPE_F32
