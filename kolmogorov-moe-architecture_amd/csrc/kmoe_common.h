@@ -138,15 +138,42 @@ __device__ __forceinline__ float wave_sum(float v) {
 // expert c (c < E) or its summed lse^2 (c = E).  aux_reduce_cols: wave w of `nw` waves
 // reduces columns w, w + nw, ...; lane l sums blocks l, l + 64, ... in order, then the
 // wave sums its lanes with a fixed shuffle tree, so the result does not depend on the
-// launch (bit-reproducible).  col[] lives in LDS; the caller synchronises before
+// launch (bit-reproducible).  The loads go out 16 at a time (4 columns x 4 blocks), the
+// sums stay in block order.  col[] lives in LDS; the caller synchronises before
 // aux_finish reads it.
 __device__ __forceinline__ void aux_reduce_cols(const float* __restrict__ partials, int64_t nblk, int E, int wave,
                                                 int nw, int lane, float* col) {
-  for (int c = wave; c <= E; c += nw) {
-    float s = 0.0f;
-    for (int64_t b = lane; b < nblk; b += 64) s += partials[b * (E + 1) + c];
-    s = wave_sum(s);
-    if (lane == 0) col[c] = s;
+  for (int c0 = wave; c0 <= E; c0 += 4 * nw) {
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t b = lane;
+    for (; b + 192 < nblk; b += 256) {
+      float v[4][4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int c = c0 + q * nw;
+          v[q][u] = c <= E ? partials[(b + 64 * u) * (E + 1) + c] : 0.0f;
+        }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s[q] += v[q][u];
+    }
+    for (; b < nblk; b += 64)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = c0 + q * nw;
+        if (c <= E) s[q] += partials[b * (E + 1) + c];
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = c0 + q * nw;  // wave-uniform
+      if (c <= E) {
+        const float t = wave_sum(s[q]);
+        if (lane == 0) col[c] = t;
+      }
+    }
   }
 }
 // out = (w_lb lb + w_z z, lb, z): lb = E sum_e (counts[e] / (T k)) (P_e / T) (0 without
