@@ -198,7 +198,8 @@ def test_dispatch_counted_matches_dispatch(dev, T, k, E, cap, fp8, mat):
 
 @pytest.mark.parametrize("T,k,E,cap,fp8,mat", [(16384, 2, 16, 0, False, False), (16384, 2, 16, 2560, False, True),
                                                (777, 3, 7, 50, True, True), (70000, 2, 8, 0, False, False),
-                                               (65536, 1, 64, 0, False, False)])
+                                               (65536, 1, 64, 0, False, False), (1, 1, 4, 0, False, False),
+                                               (63, 8, 64, 3, False, True)])
 def test_dispatch_counted_aux(dev, T, k, E, cap, fp8, mat):
     """kmoe_dispatch_counted_aux: the tables, rows and codes of kmoe_dispatch_counted and the
     aux losses of kmoe_aux_loss, bit for bit (one more workgroup of the table launch up to
