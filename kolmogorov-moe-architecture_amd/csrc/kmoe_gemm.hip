@@ -1183,30 +1183,75 @@ __global__ __launch_bounds__(256) void pack_rows16_kernel(const void* __restrict
   }
 }
 
-// Per-row fp8 quantisation of a bf16 matrix, one wave per row.
+// Per-row fp8 quantisation of a bf16 matrix: each wave takes rows w, w + W, ... (W waves
+// in the grid) and loads its next row into a second register set before it reduces and
+// stores the current one, so a wave's reads and writes overlap (one row per wave, all
+// resident at once, read every row first and wrote them all after).  NV: 16-byte vectors
+// per lane of a row (the register sets are sized for the row, not for the largest one).
+// PREFETCH = false (rows of more than 8 vectors per lane, where two register sets leave one
+// wave per SIMD): one row per wave, no second set.
+template <int NV, bool PREFETCH = true>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restrict__ in, int64_t rows,
                                                          const int32_t* __restrict__ n_rows_dev, int cols,
                                                          uint8_t* __restrict__ out, float* __restrict__ scale) {
+  struct Regs {
+    i32x4_t v[NV];
+  };
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   int64_t nr = rows;
   if (n_rows_dev) nr = min<int64_t>(nr, (int64_t)*n_rows_dev);
-  if (r >= nr) return;
-  const int nvec = cols / 8;  // <= 64 * ROW_REGS (checked on the host)
-  RowRegs rr;
-  const float amax = load_row_amax(reinterpret_cast<const i32x4_t*>(in + r * cols), nvec, lane, rr);
-  const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
-  uint32_t* dst = reinterpret_cast<uint32_t*>(out + r * cols);
+  const int nvec = cols / 8;  // <= 64 * NV (chosen on the host)
+  auto load = [&](int64_t row, Regs& rr) {
+    const i32x4_t* src = reinterpret_cast<const i32x4_t*>(in + row * cols);
 #pragma unroll
-  for (int i = 0; i < ROW_REGS; ++i) {
-    const int v = lane + 64 * i;
-    if (v < nvec) {
-      uint32_t lo, hi;
-      quant_vec_e4m3(rr.v[i], inv, lo, hi);
-      *reinterpret_cast<uint2*>(dst + 2 * v) = make_uint2(lo, hi);
+    for (int i = 0; i < NV; ++i) {
+      const int v = lane + 64 * i;
+      if (v < nvec) rr.v[i] = src[v];
     }
+  };
+  auto finish = [&](int64_t row, const Regs& rr) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i < nvec) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) amax = fmaxf(amax, bf16_pair_absmax((uint32_t)rr.v[i][q]));
+      }
+    amax = wave_max(amax);
+    const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(out + row * cols);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int v = lane + 64 * i;
+      if (v < nvec) {
+        uint32_t lo, hi;
+        quant_vec_e4m3(rr.v[i], inv, lo, hi);
+        *reinterpret_cast<uint2*>(dst + 2 * v) = make_uint2(lo, hi);
+      }
+    }
+    if (lane == 0) scale[row] = amax / 448.0f;
+  };
+  Regs a;
+  if constexpr (!PREFETCH) {
+    if (r < nr) {
+      load(r, a);
+      finish(r, a);
+    }
+    return;
   }
-  if (lane == 0) scale[r] = amax / 448.0f;
+  Regs b;
+  if (r < nr) load(r, a);
+  while (r < nr) {
+    if (r + nw < nr) load(r + nw, b);
+    finish(r, a);
+    r += nw;
+    if (r >= nr) break;
+    if (r + nw < nr) load(r + nw, a);
+    finish(r, b);
+    r += nw;
+  }
 }
 
 int elem_bytes(int dtype) { return dtype == KMOE_DTYPE_FP8_E4M3 ? 1 : 2; }
@@ -1474,8 +1519,24 @@ extern "C" int kmoe_quant_rows_fp8(const void* in, int64_t rows, const int32_t* 
   KMOE_REQUIRE(cols <= 64 * 8 * ROW_REGS, KMOE_ERR_UNSUPPORTED, "kmoe_quant_rows_fp8: cols=%d > %d", cols,
                64 * 8 * ROW_REGS);
   if (rows == 0) return KMOE_OK;
-  hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(rows, 4)), dim3(256), 0,
-                     kmoe::as_stream(stream), static_cast<const uint16_t*>(in), rows, n_rows_dev, cols, out, scale);
+  // up to 8 vectors per lane: as many workgroups per CU as are resident at once (the
+  // kernel's register use for NV = 2, 4, 8: 7, 4, 3 waves per SIMD), each wave looping
+  // over its rows; wider rows: one row per wave
+  const int nv = kmoe::ceil_div(cols / 8, 64);
+  const int per_cu = nv <= 2 ? 6 : nv <= 4 ? 4 : 3;
+  const int64_t all_rows = kmoe::ceil_div<int64_t>(rows, 4);  // one row per wave
+  const int64_t blocks = nv <= 8 ? std::min<int64_t>(all_rows, (int64_t)kmoe::cu_count() * per_cu) : all_rows;
+  hipStream_t s = kmoe::as_stream(stream);
+  const uint16_t* ip = static_cast<const uint16_t*>(in);
+  if (nv <= 2)
+    hipLaunchKernelGGL(quant_rows_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, s, ip, rows, n_rows_dev, cols, out, scale);
+  else if (nv <= 4)
+    hipLaunchKernelGGL(quant_rows_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, ip, rows, n_rows_dev, cols, out, scale);
+  else if (nv <= 8)
+    hipLaunchKernelGGL(quant_rows_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, s, ip, rows, n_rows_dev, cols, out, scale);
+  else
+    hipLaunchKernelGGL((quant_rows_kernel<ROW_REGS, false>), dim3((unsigned)blocks), dim3(256), 0, s, ip, rows,
+                       n_rows_dev, cols, out, scale);
   return kmoe::check_launch("kmoe_quant_rows_fp8");
 }
 

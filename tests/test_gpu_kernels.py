@@ -262,6 +262,25 @@ def test_dispatch_fp8_and_row_index(dev):
     assert np.array_equal(npf(out.slot_w[:A]), npf(bf16(w)).reshape(-1))
 
 
+@pytest.mark.parametrize("rows,cols,bound", [(12288, 2816, 11000), (4096, 1024, None), (300, 8192, 299),
+                                             (5, 64, None), (1000, 512, 0)])
+def test_quant_rows_fp8(dev, rows, cols, bound):
+    """kmoe_quant_rows_fp8 (h before the fp8 down GEMM) against the oracle's per-row e4m3
+    rule, codes and scales bit for bit, for every register-set width (2 to 16 vectors per
+    lane) and a device-side row bound (only the rows below it are quantised); zero rows
+    give scale 0 and zero codes."""
+    g = torch.Generator().manual_seed(rows + cols)
+    m = torch.randn(rows, cols, generator=g) * torch.exp(torch.randn(rows, 1, generator=g) * 3)
+    m[rows // 2] = 0.0
+    mb = bf16(m).to(dev)
+    nb = None if bound is None else torch.tensor([bound], dtype=torch.int32, device=dev)
+    q, sc = ops.quant_rows_fp8(mb, n_rows_dev=nb)
+    n = rows if bound is None else bound
+    qr, sr = O.quant_rows(npf(mb[:n]))
+    assert np.array_equal(q[:n].cpu().numpy(), qr)
+    assert np.array_equal(npf(sc[:n]), sr)
+
+
 def test_gather_rows(dev):
     (x,) = gen(15, (100, 128))
     xb = bf16(x).to(dev)
