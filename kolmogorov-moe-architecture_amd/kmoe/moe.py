@@ -311,8 +311,15 @@ class GroupedExpertsExpertChoice(_PackedExperts):
     def run(self, x2d, sel: ops.ECSelectOut, B, S, C, out_dtype=torch.bfloat16):
         pw = self.packed()
         n_rows = self.n_experts * B * C
-        xperm, xscale = ops.gather_rows(x2d, sel.row_token, n_rows, fp8=pw.fp8)
-        yperm = ops.grouped_ffn(xperm, xscale, sel.offsets, pw, n_rows)
+        if isinstance(pw, ops.PackedWeights) and not pw.fp8:
+            # bf16 SwiGLU: the gate/up GEMM gathers the selected token rows itself (no
+            # permuted copy of x; a -1 entry of row_token reads as a zero row, as gather_rows
+            # writes it)
+            h = ops.gemm_gate_up_rows(x2d, None, sel.row_token, sel.offsets, pw, n_rows)
+            yperm = ops.gemm_down(h, None, sel.offsets, pw, n_rows)
+        else:
+            xperm, xscale = ops.gather_rows(x2d, sel.row_token, n_rows, fp8=pw.fp8)
+            yperm = ops.grouped_ffn(xperm, xscale, sel.offsets, pw, n_rows)
         return ops.combine(yperm, sel.src_row, sel.src_w, B * S, out_dtype=out_dtype)
 
     def forward(self, x: torch.Tensor, expert_weights: torch.Tensor, token_indices: torch.Tensor) -> torch.Tensor:
