@@ -123,7 +123,7 @@ def mod_ffn(ffn: MoELayer, mod_router: MoDRouter, hidden_states: torch.Tensor,
     are wanted."""
     B, S, d = hidden_states.shape
     if ffn.routing_type == "expert_choice":
-        raise NotImplementedError("kmoe: Mixture-of-Depths around an expert-choice layer is not implemented")
+        return _mod_expert_choice(ffn, mod_router, hidden_states, residual)
     if mod_trainable(ffn, mod_router, hidden_states, residual):
         ge = ffn.grouped_experts
         y, aux = _MoDTrainFn.apply(hidden_states, residual, mod_router.router.weight, ffn.router.router[0].weight,
@@ -142,6 +142,32 @@ def mod_ffn(ffn: MoELayer, mod_router: MoDRouter, hidden_states: torch.Tensor,
     ins = (hidden_states,) if residual is None else (hidden_states, residual)
     return _forward_only(y.view(B, S, d).to(hidden_states.dtype), *ins, *ffn.parameters(),
                          *mod_router.parameters())
+
+
+def _mod_expert_choice(ffn: MoELayer, mod_router: MoDRouter, hidden_states: torch.Tensor,
+                       residual: torch.Tensor = None) -> torch.Tensor:
+    """MoD around an expert-choice MoELayer (layers.py:148-187 with moe_routing
+    "expert_choice"): the selection on the MoD kernel, the kept rows (B, keep, d) through
+    the expert-choice layer (its capacity from the kept length, moe.py:494-530; it trains
+    through its own HIP backward and sets ffn.aux_loss), then the rows weighted by the
+    softmax over the kept logits (mod.py:112) and scattered back (layers.py:175-184).
+    The expert-choice combine sums each token's rows from its own fan-in tables, so the
+    gather, the kept logits' softmax and the weighted scatter around it are tensor ops
+    on the GPU, differentiable: autograd takes the gradients of x, the residual and
+    w_mod through them."""
+    B, S, d = hidden_states.shape
+    x = hidden_states
+    sel = mod_router.select(x.detach().to(torch.bfloat16).contiguous())
+    gidx = sel.sel_idx.long().unsqueeze(-1).expand(-1, -1, d)
+    xs = torch.gather(x, 1, gidx)
+    ys = ffn(xs)
+    w_mod = mod_router.router.weight
+    p = torch.softmax((xs.float() @ w_mod.float().t()).squeeze(-1), dim=-1)
+    out = torch.zeros(B, S, d, device=x.device, dtype=torch.float32).scatter_add(1, gidx,
+                                                                                 p.unsqueeze(-1) * ys.float())
+    if residual is not None:
+        out = out + residual.float()
+    return out.to(x.dtype)
 
 
 class MoDMoE(nn.Module):

@@ -179,13 +179,13 @@ def ffn_half_loss_routed(h3d, w_in, w_out, w1, w2, w3, idx, dy, norm_w=None, eps
         x = norm_w * (h3d / rms)
     if w_mod is not None:
         keep = sel_idx.shape[1]
-        r = (x @ w_mod.reshape(-1, 1)).squeeze(-1)
-        p = F.softmax(r.gather(1, sel_idx), dim=-1)
-        gidx = sel_idx.unsqueeze(-1).expand(-1, -1, d)
-        xs = torch.gather(x, 1, gidx)
-        y, aux = moe_tc_routed(xs.reshape(B * keep, d), w_in, w_out, w1, w2, w3, idx, capacity, None, training,
-                               w_lb, w_z)
-        ffn_out = torch.zeros_like(x).scatter_add(1, gidx, p.unsqueeze(-1) * y.view(B, keep, d))
+
+        def moe(xs):
+            y, aux = moe_tc_routed(xs.reshape(B * keep, d), w_in, w_out, w1, w2, w3, idx, capacity, None, training,
+                                   w_lb, w_z)
+            return y.view(B, keep, d), aux
+
+        ffn_out, aux = mod_apply(x, w_mod, sel_idx, moe)
     else:
         y, aux = moe_tc_routed(x.reshape(B * S, d), w_in, w_out, w1, w2, w3, idx, capacity, None, training, w_lb,
                                w_z)
@@ -194,6 +194,19 @@ def ffn_half_loss_routed(h3d, w_in, w_out, w1, w2, w3, idx, dy, norm_w=None, eps
     out = ffn_out if base is None else base + ffn_out
     loss = (out * dy).sum() + aux
     return (loss, out) if return_out else loss
+
+
+def mod_apply(x, w_mod, sel_idx, f):
+    """The MoD composition of layers.py:148-184 around f at a fixed selection sel_idx
+    (B, keep), ascending: the router logits x . w_mod (mod.py:93), the softmax over the
+    kept ones (mod.py:112), f on the gathered rows (B, keep, d) -> (y, aux), the rows
+    weighted by the softmax and scatter_add_-ed into zeros.  Returns (ffn_out, aux)."""
+    d = x.shape[-1]
+    r = (x @ w_mod.reshape(-1, 1)).squeeze(-1)
+    p = F.softmax(r.gather(1, sel_idx), dim=-1)
+    gidx = sel_idx.unsqueeze(-1).expand(-1, -1, d)
+    y, aux = f(torch.gather(x, 1, gidx))
+    return torch.zeros_like(x).scatter_add(1, gidx, p.unsqueeze(-1) * y), aux
 
 
 def grouped_experts_ec_tc(x3d, ew, ti, w1, w2, w3):
@@ -236,12 +249,31 @@ def moe_loss_ec_routed(x3d, w_in, w_out, w1, w2, w3, ti, dy, training=True, w_z=
     """Scalar loss sum(y * dy) (+ w_z * z-loss in training, moe.py:833-836) of MoELayer's
     expert-choice forward with the selection fixed to ti (B, E, C): at a fixed selection
     the layer is smooth, so the autograd gradients of this loss are the reference's."""
+    y, aux = ec_layer_routed(x3d, w_in, w_out, w1, w2, w3, ti, training, w_z)
+    return (y * dy).sum() + aux
+
+
+def ec_layer_routed(x3d, w_in, w_out, w1, w2, w3, ti, training=True, w_z=0.001):
+    """(y, aux) of MoELayer's expert-choice forward (moe.py:815-838) with the selection
+    fixed to ti (B, E, C); aux = w_z * z-loss in training (moe.py:833-836), else 0."""
     logits = F.linear(F.silu(F.linear(x3d, w_in)), w_out)
     y = grouped_experts_ec_tc(x3d, ec_weights_routed(logits, ti), ti, w1, w2, w3)
-    loss = (y * dy).sum()
-    if training:
-        loss = loss + w_z * (torch.logsumexp(logits, dim=-1) ** 2).mean()
-    return loss
+    aux = w_z * (torch.logsumexp(logits, dim=-1) ** 2).mean() if training else 0.0
+    return y, aux
+
+
+def ffn_half_loss_ec_routed(x3d, w_in, w_out, w1, w2, w3, ti, dy, w_mod, sel_idx, residual=None, training=True,
+                            w_z=0.001, return_out=False):
+    """Scalar loss sum(out * dy) (+ the layer's z-loss in training) of the FFN half of
+    TransformerBlock.forward with MoD (layers.py:148-187) around an expert-choice
+    MoELayer: mod_apply with the expert-choice layer on the kept rows (B, keep, d), its
+    selection fixed to ti (B, E, C) over the kept positions; out = residual + ffn_output
+    (residual optional).  return_out: (loss, out)."""
+    ffn_out, aux = mod_apply(x3d, w_mod, sel_idx,
+                             lambda xs: ec_layer_routed(xs, w_in, w_out, w1, w2, w3, ti, training, w_z))
+    out = ffn_out if residual is None else residual + ffn_out
+    loss = (out * dy).sum() + aux
+    return (loss, out) if return_out else loss
 
 
 def router_loss_routed(x2d, w_in, w_out, idx, gw, gl):

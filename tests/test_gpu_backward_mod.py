@@ -93,6 +93,57 @@ def test_mod_moe_backward(dev, B, S, d, E, k, F_, cf, with_res):
     _check(errs)
 
 
+@pytest.mark.parametrize("B,S,d,E,F_,cf,ec_cf,with_res,train", [
+    (2, 256, 256, 8, 352, 0.75, 2.0, False, True),
+    (2, 300, 256, 8, 352, 0.5, 1.0, True, True),
+    (1, 400, 384, 4, 320, 0.75, 2.0, True, False),
+])
+def test_mod_expert_choice(dev, B, S, d, E, F_, cf, ec_cf, with_res, train):
+    """MoD around an expert-choice layer: forward and gradients against fp64 autograd of
+    oracle/torch_port.ffn_half_loss_ec_routed (pinned on the CPU against the numpy
+    oracle's pieces) at the kernels' own MoD selection and expert-choice selection."""
+    print(f"mod ec B={B} S={S} d={d} E={E} cf={cf} ec_cf={ec_cf} res={with_res} train={train}", flush=True)
+    cfg = AdvancedMoEConfig(d_model=d, n_experts=E, d_ff_expert=F_, mod_capacity_factor=cf,
+                            moe_routing="expert_choice", moe_capacity_factor=ec_cf, moe_router_z_loss_weight=0.01)
+    m = MoDMoE(cfg).to(dev, BF).train(train)
+    g = torch.Generator().manual_seed(500 + S)
+    ffn, ge = m.ffn, m.ffn.grouped_experts_ec
+    with torch.no_grad():
+        ffn.router.router[0].weight.copy_(torch.randn(128, d, generator=g) * 0.05)
+        ffn.router.router[2].weight.copy_(torch.randn(E, 128, generator=g) * 0.05)
+        for w in (ge.w1, ge.w2, ge.w3):
+            w.copy_(torch.randn(w.shape, generator=g) * 0.05)
+        m.ffn_mod_router.router.weight.copy_(torch.randn(1, d, generator=g) * 0.08)
+    x = torch.randn(B, S, d, generator=g).to(BF).to(dev).requires_grad_(True)
+    res = torch.randn(B, S, d, generator=g).to(BF).to(dev).requires_grad_(True) if with_res else None
+    dy = torch.randn(B, S, d, generator=g).to(BF)
+    y = m(x, residual=res)
+    loss = (y.float() * dy.to(dev).float()).sum()
+    if train:
+        loss = loss + m.aux_loss
+    loss.backward()
+    torch.cuda.synchronize()
+    keep = m.ffn_mod_router.keep_count(S)
+    with torch.no_grad():
+        sel = ops.mod_select(x.detach(), m.ffn_mod_router.router.weight, keep)
+        xs = x.detach().reshape(B * S, d)[sel.token_rows.long()].view(B, keep, d)
+        ti = ffn.router.route(xs)[1].idx.cpu()
+    names = ["w_mod", "w_in", "w_out", "w1", "w2", "w3"]
+    mods = [m.ffn_mod_router.router.weight, ffn.router.router[0].weight, ffn.router.router[2].weight, ge.w1, ge.w2,
+            ge.w3]
+    p64 = [_f64(t) for t in mods]
+    x64 = _f64(x)
+    r64 = _f64(res) if with_res else None
+    ref, out = P.ffn_half_loss_ec_routed(x64, *p64[1:], ti, dy.double(), w_mod=p64[0], sel_idx=sel.sel_idx.cpu().long(),
+                                         residual=r64, training=train, w_z=0.01, return_out=True)
+    ref.backward()
+    errs = {"y": _rel(y.detach(), out.detach()), "dx": _rel(x.grad, x64.grad)}
+    if with_res:
+        errs["dres"] = _rel(res.grad, r64.grad)
+    errs.update({"d" + n: _rel(t.grad, p.grad) for n, t, p in zip(names, mods, p64)})
+    _check(errs)
+
+
 # ------------------------------------------------------------------ the block in training
 @pytest.mark.parametrize("mod,norm_dtype,h_dtype", [
     (False, torch.float32, BF),

@@ -699,6 +699,42 @@ def test_ffn_half_loss_matches_numpy_composition(with_norm):
         assert abs(got2 - want2) <= 1e-10 * max(1.0, abs(want2))
 
 
+def test_ffn_half_loss_ec_matches_numpy_composition():
+    """ffn_half_loss_ec_routed (MoD around the expert-choice layer, layers.py:148-187)
+    against the numpy oracle's pieces: mod_logits / mod_select, then on the kept rows
+    router_logits, ec_select (capacity from the kept length), ec_tables, swiglu_rows and
+    combine, an explicit scatter of the weighted rows and the z-loss of the kept rows'
+    logits; plus the same with w_z = 0 and no residual."""
+    c = _tiny_ffn_half(23)
+    B, S, d = c["h"].shape
+    keep, E, cf, w_z = c["keep"], c["w_out"].shape[0], 2.0, 0.3
+    h = c["h"].numpy()
+    res = 0.5 * c["dy"].numpy()[:, ::-1].copy()
+    sel, sw = O.mod_select(O.mod_logits(h, c["w_mod"].numpy()), keep)
+    xs = np.concatenate([h[b, sel[b]] for b in range(B)])
+    C = math.ceil(keep * cf / E)
+    lg = O.router_logits(xs, c["w_in"].numpy(), c["w_out"].numpy())
+    idx, w = O.ec_select(lg, B, keep, E, C)
+    row_token, offsets, src_row, src_w = O.ec_tables(idx, w, keep)
+    yrows = O.swiglu_rows(xs[row_token], offsets, c["w1"].numpy(), c["w2"].numpy(), c["w3"].numpy(),
+                          dtype=np.float64)
+    y = O.combine(yrows, src_row, src_w).reshape(B, keep, d)
+    out = np.zeros_like(h)
+    for b in range(B):
+        out[b, sel[b]] = sw[b][:, None] * y[b]
+    m = lg.max(axis=-1)
+    z = np.mean((m + np.log(np.exp(lg - m[:, None]).sum(axis=-1))) ** 2)
+    dy = c["dy"].numpy()
+    args = [c[n] for n in ("h", "w_in", "w_out", "w1", "w2", "w3")] + [torch.from_numpy(idx), c["dy"]]
+    kw = dict(w_mod=c["w_mod"], sel_idx=torch.from_numpy(sel))
+    want = float(((res + out) * dy).sum() + w_z * z)
+    got = float(P.ffn_half_loss_ec_routed(*args, residual=torch.from_numpy(res), w_z=w_z, **kw))
+    assert abs(got - want) <= 1e-10 * max(1.0, abs(want))
+    want0 = float((out * dy).sum())
+    got0 = float(P.ffn_half_loss_ec_routed(*args, training=False, **kw))
+    assert abs(got0 - want0) <= 1e-10 * max(1.0, abs(want0))
+
+
 def test_ffn_half_loss_gradcheck():
     """Finite differences of the MoD + norm composition at a fixed selection and routing
     (the gradients the GPU backward is compared with)."""
