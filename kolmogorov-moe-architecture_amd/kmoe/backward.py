@@ -201,8 +201,8 @@ def _expert_weight_grads(h, dyperm, xperm, dgu, offsets, A, E, d, F, plain=False
 
 def _router_core(x2d, hidden, w_out, bw: BwdWeights, dl, dx_rows, need_weights):
     """Router MLP backward from the logit gradient dl (T, E): da and dW_out
-    (kmoe_router_mlp_bwd), the dx contribution da . w_in written to dx_rows (T, d) bf16,
-    and dW_in = da^T x (split-K over token segments, reduced in order).  Returns
+    (kmoe_router_mlp_bwd), the dx contribution da . w_in written to dx_rows (T, d) bf16
+    (dx_rows None: no input gradient), and dW_in = da^T x (split-K over token segments, reduced in order).  Returns
     (dw_in or None, dw_out)."""
     lib = _lib.load()
     T, d = x2d.shape
@@ -219,8 +219,9 @@ def _router_core(x2d, hidden, w_out, bw: BwdWeights, dl, dx_rows, need_weights):
         w_out_b = w_out.detach().to(_BF16).contiguous()
         _lib.call("kmoe_router_mlp_bwd", ptr(dl), ptr(hidden), T, E, ptr(w_out_b), ptr(da), ptr(dw_out),
                   _lib.DTYPE_F32 if wdt == torch.float32 else _lib.DTYPE_BF16, ptr(ws), wsb, s)
-        _lib.call("kmoe_gemm_grouped", ptr(da), ptr(one_seg), 1, _lib.ROUTER_HIDDEN, T, ptr(bw.w_in_t), _ru(d, 256),
-                  d, ptr(dx_rows), d, d, s)
+        if dx_rows is not None:
+            _lib.call("kmoe_gemm_grouped", ptr(da), ptr(one_seg), 1, _lib.ROUTER_HIDDEN, T, ptr(bw.w_in_t),
+                      _ru(d, 256), d, ptr(dx_rows), d, d, s)
     if not need_weights:
         return None, dw_out
     # dW_in = da^T x: a 128 x d output (few tiles) over K = T, split into token
@@ -232,6 +233,13 @@ def _router_core(x2d, hidden, w_out, bw: BwdWeights, dl, dx_rows, need_weights):
                   _lib.ROUTER_HIDDEN, _ru(d, 256), ptr(part), None, _lib.DTYPE_F32, d, d, s)
         _lib.call("kmoe_reduce_f32", ptr(part), nseg, _lib.ROUTER_HIDDEN * d, ptr(dw_in), _lib.DTYPE_BF16, s)
     return dw_in, dw_out
+
+
+def router_weight_grads(x2d, hidden, w_out, dl):
+    """(dW_in, dW_out) of a router MLP (Linear(d, 128), SiLU, Linear(128, E)) from the
+    logit gradient dl (T, E) f32, for an input that takes no gradient (the MoD
+    auxiliary router's detached input, mod.py:155)."""
+    return _router_core(x2d, hidden, w_out, None, dl, None, True)
 
 
 def _gather_dx(dxp, src, T, d, residual=None):

@@ -137,9 +137,12 @@ class MoEFFNBlock(nn.Module):
         if self._train_fusable(hidden_states):
             ffn, ge = self.ffn, self.ffn.grouped_experts
             w_mod = self.ffn_mod_router.router.weight if use_mod else None
-            out, aux = _BlockTrainFn.apply(hidden_states, self.ffn_norm.weight, w_mod, ffn.router.router[0].weight,
-                                           ffn.router.router[2].weight, ge.w1, ge.w2, ge.w3, self, use_mod)
+            out, aux, n, rows = _BlockTrainFn.apply(hidden_states, self.ffn_norm.weight, w_mod,
+                                                    ffn.router.router[0].weight, ffn.router.router[2].weight, ge.w1,
+                                                    ge.w2, ge.w3, self, use_mod)
             ffn.aux_loss = aux if ffn.training else 0.0
+            if use_mod:
+                self.ffn_mod_router.aux(n, rows)
             self.last_path = "fused_train"
         elif not use_mod and self._fusable(hidden_states):
             out = self._forward_fused(hidden_states)
@@ -151,6 +154,8 @@ class MoEFFNBlock(nn.Module):
             out = residual + self.residual_dropout(ffn_output)
             self.last_path = "unfused"
         self.aux_loss = self.ffn.aux_loss if self.training else 0.0
+        if use_mod:
+            self.aux_loss = self.aux_loss + self.ffn_mod_router.aux_loss
         return out
 
     def _forward_fused(self, h: torch.Tensor) -> torch.Tensor:
@@ -206,10 +211,13 @@ class _BlockTrainFn(torch.autograd.Function):
         ctx.blk = blk
         ctx.meta = (B, S, d, keep, h.dtype, aux is not None, use_mod)
         aux_t = aux if aux is not None else torch.zeros((), device=h.device, dtype=torch.float32)
-        return y.view(B, S, d), aux_t
+        # the normalised rows and the kept rows, for the MoD auxiliary router's loss
+        rows = sel.token_rows if use_mod else torch.zeros(0, device=h.device, dtype=torch.int32)
+        ctx.mark_non_differentiable(n, rows)
+        return y.view(B, S, d), aux_t, n, rows
 
     @staticmethod
-    def backward(ctx, dy, daux):
+    def backward(ctx, dy, daux, dn, drows):
         sv, sel, h2d, rrms = _once(ctx)
         blk = ctx.blk
         B, S, d, keep, h_dtype, has_aux, use_mod = ctx.meta

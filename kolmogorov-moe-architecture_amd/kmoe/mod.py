@@ -13,7 +13,8 @@ weight gradients), the weighted scatter stays in the combine, and the backward
 runs on the HIP kernels: the combine backward reads dy at the kept rows and
 yields the MoD weights' gradient, kmoe_mod_bwd the kept logits' and W_mod's,
 and one gather writes the input gradient of every token.
-The MoD auxiliary BCE loss is out of scope.
+In training the MoD router's auxiliary loss (mod.py:114-171: an MLP on the detached
+input predicting the selection, binary cross-entropy) runs on the router MLP kernels.
 """
 from __future__ import annotations
 
@@ -21,7 +22,9 @@ from typing import Tuple
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
+from . import _lib
 from . import backward as _bwd
 from . import ops
 from .config import AdvancedMoEConfig
@@ -41,7 +44,22 @@ class MoDRouter(nn.Module):
             nn.SiLU(),
             nn.Linear(aux_hidden, 1, bias=False),
         )
+        self.aux_loss_weight = config.mod_load_balance_loss_weight
         self.aux_loss = 0.0
+
+    def aux(self, x2d: torch.Tensor, token_rows: torch.Tensor):
+        """Sets and returns aux_loss for the selection token_rows (the kept rows of the
+        flattened input x2d): in training the auxiliary router's loss (mod.py:114-118,
+        141-171), else 0.0."""
+        if not self.training:
+            self.aux_loss = 0.0
+            return self.aux_loss
+        w_a, w_b = self.aux_router[0].weight, self.aux_router[2].weight
+        if w_a.shape[0] != _lib.ROUTER_HIDDEN:
+            raise NotImplementedError(f"kmoe: the MoD auxiliary router runs on the router kernels, hidden size "
+                                      f"{_lib.ROUTER_HIDDEN} (mod_router_hidden_dim={w_a.shape[0]})")
+        self.aux_loss = _ModAuxFn.apply(x2d.detach(), w_a, w_b, token_rows, float(self.aux_loss_weight))
+        return self.aux_loss
 
     def keep_count(self, seq_len: int) -> int:
         return max(1, min(seq_len, int(seq_len * self.capacity_factor)))  # mod.py:97
@@ -59,8 +77,39 @@ class MoDRouter(nn.Module):
         topk_indices is returned in ascending order (the same set as the reference's
         unsorted top-k)."""
         sel = self.select(hidden_states)
+        B, S, d = hidden_states.shape
+        self.aux(hidden_states.reshape(B * S, d), sel.token_rows)
         dt = hidden_states.dtype
         return sel.sel_idx, sel.sel_w.to(dt), sel.logits.to(dt), sel.sel_idx
+
+
+class _ModAuxFn(torch.autograd.Function):
+    """weight * mean over the B*S tokens of BCE-with-logits(aux_router(x), selected)
+    (mod.py:141-171) with aux_router = Linear(d, 128), SiLU, Linear(128, 1): the router
+    MLP kernel with one output.  x enters detached (mod.py:155), so only the two weights
+    get gradients, from the router MLP backward kernels with dl = weight (sigmoid(l) - t) / T."""
+
+    @staticmethod
+    def forward(ctx, x2d, w_a, w_b, token_rows, weight):
+        T = x2d.shape[0]
+        r = ops.router(x2d, w_a, w_b, 0, save_hidden=True)
+        lg = r.logits.view(T)
+        t = torch.zeros(T, device=x2d.device, dtype=torch.float32)
+        t[token_rows.long()] = 1.0
+        ctx.save_for_backward(x2d, r.hidden, lg, t)
+        ctx.w_b = w_b
+        ctx.weight = weight
+        return weight * (F.softplus(lg) - t * lg).mean()
+
+    @staticmethod
+    def backward(ctx, g):
+        x2d, hidden, lg, t = ctx.saved_tensors
+        T = x2d.shape[0]
+        dl = ((g.float() * (ctx.weight / T)) * (torch.sigmoid(lg) - t)).view(T, 1).contiguous()
+        dw_a, dw_b = _bwd.router_weight_grads(x2d, hidden, ctx.w_b, dl)
+        w_b = ctx.w_b
+        del ctx.w_b
+        return None, dw_a.to(w_b.dtype), dw_b.to(w_b.dtype), None, None
 
 
 class _MoDTrainFn(torch.autograd.Function):
@@ -68,10 +117,8 @@ class _MoDTrainFn(torch.autograd.Function):
     backward on the HIP kernels (mod_backward).  Outputs (y, aux)."""
 
     @staticmethod
-    def forward(ctx, x, residual, w_mod, w_in, w_out, w1, w2, w3, ffn, mod_router):
+    def forward(ctx, x, residual, w_mod, w_in, w_out, w1, w2, w3, ffn, mod_router, xb, sel):
         B, S, d = x.shape
-        xb = x.detach().to(torch.bfloat16).contiguous()
-        sel = mod_router.select(xb)
         keep = sel.sel_idx.shape[1]
         T = B * keep
         x_sel, _ = ops.gather_rows(xb.view(B * S, d), sel.token_rows, T)
@@ -100,10 +147,10 @@ class _MoDTrainFn(torch.autograd.Function):
         dx = g.dx.view(B, S, d).to(x_dtype)
         dres = None if r_dtype is None else dy.to(r_dtype)
         if not need_w:
-            return dx, dres, None, None, None, None, None, None, None, None
+            return dx, dres, None, None, None, None, None, None, None, None, None, None
         lg = g.layer
         return (dx, dres, g.dw_mod.view_as(w_mod).to(w_mod.dtype), lg.dw_in.to(w_in.dtype), lg.dw_out.to(w_out.dtype),
-                *ge.cast_grads(lg.dw1, lg.dw2, lg.dw3), None, None)
+                *ge.cast_grads(lg.dw1, lg.dw2, lg.dw3), None, None, None, None)
 
 
 def mod_trainable(ffn: MoELayer, mod_router: MoDRouter, *inputs) -> bool:
@@ -122,16 +169,17 @@ def mod_ffn(ffn: MoELayer, mod_router: MoDRouter, hidden_states: torch.Tensor,
     `residual`), setting ffn.aux_loss; trains through the HIP backward when gradients
     are wanted."""
     B, S, d = hidden_states.shape
+    x = hidden_states.detach().to(torch.bfloat16).contiguous()
+    sel = mod_router.select(x)
+    mod_router.aux(x.view(B * S, d), sel.token_rows)
     if ffn.routing_type == "expert_choice":
-        return _mod_expert_choice(ffn, mod_router, hidden_states, residual)
+        return _mod_expert_choice(ffn, mod_router, hidden_states, residual, sel)
     if mod_trainable(ffn, mod_router, hidden_states, residual):
         ge = ffn.grouped_experts
         y, aux = _MoDTrainFn.apply(hidden_states, residual, mod_router.router.weight, ffn.router.router[0].weight,
-                                   ffn.router.router[2].weight, ge.w1, ge.w2, ge.w3, ffn, mod_router)
+                                   ffn.router.router[2].weight, ge.w1, ge.w2, ge.w3, ffn, mod_router, x, sel)
         ffn.aux_loss = aux if ffn.training else 0.0
         return y
-    x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
-    sel = mod_router.select(x)
     keep = sel.sel_idx.shape[1]
     out_dtype = torch.float32 if hidden_states.dtype == torch.float32 else torch.bfloat16
     res2d = None if residual is None else residual.reshape(B * S, d)
@@ -145,9 +193,9 @@ def mod_ffn(ffn: MoELayer, mod_router: MoDRouter, hidden_states: torch.Tensor,
 
 
 def _mod_expert_choice(ffn: MoELayer, mod_router: MoDRouter, hidden_states: torch.Tensor,
-                       residual: torch.Tensor = None) -> torch.Tensor:
+                       residual: torch.Tensor, sel: ops.ModSelectOut) -> torch.Tensor:
     """MoD around an expert-choice MoELayer (layers.py:148-187 with moe_routing
-    "expert_choice"): the selection on the MoD kernel, the kept rows (B, keep, d) through
+    "expert_choice"): at the MoD selection sel, the kept rows (B, keep, d) through
     the expert-choice layer (its capacity from the kept length, moe.py:494-530; it trains
     through its own HIP backward and sets ffn.aux_loss), then the rows weighted by the
     softmax over the kept logits (mod.py:112) and scattered back (layers.py:175-184).
@@ -157,7 +205,6 @@ def _mod_expert_choice(ffn: MoELayer, mod_router: MoDRouter, hidden_states: torc
     w_mod through them."""
     B, S, d = hidden_states.shape
     x = hidden_states
-    sel = mod_router.select(x.detach().to(torch.bfloat16).contiguous())
     gidx = sel.sel_idx.long().unsqueeze(-1).expand(-1, -1, d)
     xs = torch.gather(x, 1, gidx)
     ys = ffn(xs)
@@ -183,5 +230,5 @@ class MoDMoE(nn.Module):
         """ffn_output; with `residual` (B, S, d), residual + ffn_output (layers.py:187) from the same
         combine: unselected tokens get the residual row, selected ones residual + weighted output."""
         y = mod_ffn(self.ffn, self.ffn_mod_router, hidden_states, residual)
-        self.aux_loss = self.ffn.aux_loss
+        self.aux_loss = self.ffn.aux_loss + self.ffn_mod_router.aux_loss
         return y

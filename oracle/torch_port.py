@@ -209,6 +209,15 @@ def mod_apply(x, w_mod, sel_idx, f):
     return torch.zeros_like(x).scatter_add(1, gidx, p.unsqueeze(-1) * y), aux
 
 
+def mod_aux_loss(x3d, w_a, w_b, sel_idx, weight=0.001):
+    """The MoD router's auxiliary loss (mod.py:141-171): weight * mean over (B, S) of
+    binary cross-entropy with logits aux_router(x) = Linear(d, h) -> SiLU -> Linear(h, 1)
+    (mod.py:44-50) and targets 1 at the selected positions sel_idx (B, keep), 0 elsewhere."""
+    a = F.linear(F.silu(F.linear(x3d, w_a)), w_b).squeeze(-1)
+    t = torch.zeros_like(a).scatter(1, sel_idx, 1.0)
+    return weight * (F.softplus(a) - t * a).mean()
+
+
 def grouped_experts_ec_tc(x3d, ew, ti, w1, w2, w3):
     """GroupedExpertsExpertChoice.forward (moe.py:626-673): gather the selected tokens,
     bmm SwiGLU with the weights repeated per sequence, weight, scatter_add_ back."""

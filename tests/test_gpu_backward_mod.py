@@ -144,6 +144,46 @@ def test_mod_expert_choice(dev, B, S, d, E, F_, cf, ec_cf, with_res, train):
     _check(errs)
 
 
+@pytest.mark.parametrize("path", ["tc", "ec", "block"])
+def test_mod_aux_router_loss(dev, path):
+    """The MoD router's auxiliary BCE loss (mod.py:141-171) in training: its value and the
+    auxiliary router's weight gradients against fp64 autograd of oracle/torch_port.
+    mod_aux_loss (pinned on the CPU against torch's BCE on the numpy router MLP) at the
+    kernel's selection, fed the bf16 values of the MoD input (the block: the kernel's
+    normalised rows; the input is detached in the reference, so it takes no gradient)."""
+    B, S, d, E, F_ = 2, 256, 256, 8, 352
+    print(f"mod aux path={path}", flush=True)
+    cfg = AdvancedMoEConfig(d_model=d, n_experts=E, d_ff_expert=F_, mod_enabled=True, mod_capacity_factor=0.75,
+                            residual_dropout=0.0, mod_load_balance_loss_weight=0.05,
+                            moe_routing="expert_choice" if path == "ec" else "token_choice")
+    m = (MoEFFNBlock(cfg, 0) if path == "block" else MoDMoE(cfg)).to(dev, BF).train()
+    g = torch.Generator().manual_seed(620 + len(path))
+    with torch.no_grad():
+        for p_ in m.parameters():
+            p_.copy_(torch.randn(p_.shape, generator=g) * 0.05 + (1.0 if p_.dim() == 1 else 0.0))
+    x = torch.randn(B, S, d, generator=g).to(BF).to(dev).requires_grad_(True)
+    y = m(x)
+    if path == "block":
+        assert m.last_path == "fused_train"
+    mr = m.ffn_mod_router
+    aux_mod = mr.aux_loss
+    (y.float().square().mean() + m.aux_loss).backward()
+    torch.cuda.synchronize()
+    keep = mr.keep_count(S)
+    with torch.no_grad():
+        xin = ops.rmsnorm(x.detach().reshape(B * S, d), m.ffn_norm.weight, m.ffn_norm.eps).n if path == "block" \
+            else x.detach()
+        xin = xin.reshape(B, S, d)
+        sel = ops.mod_select(xin, mr.router.weight, keep)
+    w_a, w_b = mr.aux_router[0].weight, mr.aux_router[2].weight
+    a64, b64 = _f64(w_a), _f64(w_b)
+    ref = P.mod_aux_loss(xin.double().cpu(), a64, b64, sel.sel_idx.cpu().long(), 0.05)
+    ref.backward()
+    errs = {"aux": abs(float(aux_mod) - float(ref)) / abs(float(ref)), "dw_a": _rel(w_a.grad, a64.grad),
+            "dw_b": _rel(w_b.grad, b64.grad)}
+    _check(errs, tight=("aux",))
+
+
 # ------------------------------------------------------------------ the block in training
 @pytest.mark.parametrize("mod,norm_dtype,h_dtype", [
     (False, torch.float32, BF),

@@ -735,6 +735,25 @@ def test_ffn_half_loss_ec_matches_numpy_composition():
     assert abs(got0 - want0) <= 1e-10 * max(1.0, abs(want0))
 
 
+def test_mod_aux_loss_matches_library_bce():
+    """mod_aux_loss against torch's binary_cross_entropy_with_logits on the numpy
+    oracle's router MLP (router_logits with one output) and mod_select's kept set."""
+    c = _tiny_ffn_half(24)
+    B, S, d = c["h"].shape
+    g = torch.Generator().manual_seed(7)
+    w_a = torch.randn(128, d, generator=g, dtype=torch.float64) * 0.3
+    w_b = torch.randn(1, 128, generator=g, dtype=torch.float64) * 0.3
+    h = c["h"].numpy()
+    sel, _ = O.mod_select(O.mod_logits(h, c["w_mod"].numpy()), c["keep"])
+    lg = torch.from_numpy(O.router_logits(h.reshape(-1, d), w_a.numpy(), w_b.numpy())).view(B, S)
+    t = torch.zeros(B, S, dtype=torch.float64)
+    for b in range(B):
+        t[b, torch.from_numpy(sel[b])] = 1.0
+    want = 0.25 * float(F.binary_cross_entropy_with_logits(lg, t))
+    got = float(P.mod_aux_loss(c["h"], w_a, w_b, torch.from_numpy(sel), 0.25))
+    assert abs(got - want) <= 1e-12 * max(1.0, abs(want))
+
+
 def test_ffn_half_loss_gradcheck():
     """Finite differences of the MoD + norm composition at a fixed selection and routing
     (the gradients the GPU backward is compared with)."""
