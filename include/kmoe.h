@@ -86,6 +86,15 @@ int kmoe_router(const void* x, const int32_t* row_index, int64_t T, int d, const
 int kmoe_aux_loss(const float* partials, int64_t T, int E, const int32_t* counts, int k, float w_lb,
                   float w_z, float* out, void* stream);
 
+/* MoD router auxiliary loss — replaces MoDRouter._compute_auxiliary_loss's
+ * binary_cross_entropy_with_logits (moe_arch/model/mod.py:141-171) over the auxiliary
+ * router's logits (T) f32 (kmoe_router_train with E = 1, k = 0 on the aux_router MLP):
+ * out[0] = weight / T * (sum_t softplus(logits[t]) - sum_j logits[rows[j]]), the kept
+ * rows rows[0, n_keep) (distinct, each in [0, T)) being the targets equal to 1.
+ * T > 0, 0 <= n_keep <= T. */
+int kmoe_mod_aux_bce(const float* logits, int64_t T, const int32_t* rows, int64_t n_keep, float weight, float* out,
+                     void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* (b) Dispatch — replaces the sort/bincount/gather half of GroupedExperts.forward
  * (moe.py:238-272).  Stable counting sort of the T*k assignments a = t*k + j by

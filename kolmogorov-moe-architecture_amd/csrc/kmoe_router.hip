@@ -441,6 +441,40 @@ extern "C" int kmoe_router(const void* x, const int32_t* row_index, int64_t T, i
                            nullptr, stream);
 }
 
+// MoD auxiliary router loss (mod.py:141-171) from its logits l (T): weight * the mean
+// over t of BCE-with-logits(l_t, y_t), y_t = 1 for the kept rows rows[0, n_keep) and 0
+// elsewhere, i.e. weight / T * (sum_t softplus(l_t) - sum_j l[rows[j]]).  One
+// workgroup; fixed-order sums (per-thread strided, then an LDS tree).
+__global__ __launch_bounds__(1024) void mod_aux_bce_kernel(const float* __restrict__ l, int64_t T,
+                                                           const int32_t* __restrict__ rows, int64_t n_keep,
+                                                           float weight, float* __restrict__ out) {
+  __shared__ float red[1024];
+  const int tid = threadIdx.x;
+  float acc = 0.0f;
+  for (int64_t t = tid; t < T; t += 1024) {
+    const float v = l[t];
+    acc += fmaxf(v, 0.0f) + log1pf(__expf(-fabsf(v)));  // softplus, overflow-free
+  }
+  for (int64_t j = tid; j < n_keep; j += 1024) acc -= l[rows[j]];
+  red[tid] = acc;
+  __syncthreads();
+  for (int s = 512; s > 0; s >>= 1) {
+    if (tid < s) red[tid] += red[tid + s];
+    __syncthreads();
+  }
+  if (tid == 0) out[0] = red[0] * (weight / (float)T);
+}
+
+extern "C" int kmoe_mod_aux_bce(const float* logits, int64_t T, const int32_t* rows, int64_t n_keep, float weight,
+                                float* out, void* stream) {
+  KMOE_REQUIRE(logits && rows && out, KMOE_ERR_NULL, "kmoe_mod_aux_bce: null buffer");
+  KMOE_REQUIRE(T > 0 && n_keep >= 0 && n_keep <= T, KMOE_ERR_SHAPE, "kmoe_mod_aux_bce: T=%lld n_keep=%lld",
+               (long long)T, (long long)n_keep);
+  hipLaunchKernelGGL(mod_aux_bce_kernel, dim3(1), dim3(1024), 0, kmoe::as_stream(stream), logits, T, rows, n_keep,
+                     weight, out);
+  return kmoe::check_launch("kmoe_mod_aux_bce");
+}
+
 extern "C" int kmoe_aux_loss(const float* partials, int64_t T, int E, const int32_t* counts, int k, float w_lb,
                              float w_z, float* out, void* stream) {
   KMOE_REQUIRE(partials && out, KMOE_ERR_NULL, "kmoe_aux_loss: null partials/out");

@@ -22,7 +22,6 @@ from typing import Tuple
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import _lib
 from . import backward as _bwd
@@ -58,7 +57,11 @@ class MoDRouter(nn.Module):
         if w_a.shape[0] != _lib.ROUTER_HIDDEN:
             raise NotImplementedError(f"kmoe: the MoD auxiliary router runs on the router kernels, hidden size "
                                       f"{_lib.ROUTER_HIDDEN} (mod_router_hidden_dim={w_a.shape[0]})")
-        self.aux_loss = _ModAuxFn.apply(x2d.detach(), w_a, w_b, token_rows, float(self.aux_loss_weight))
+        weight = float(self.aux_loss_weight)
+        if torch.is_grad_enabled() and (w_a.requires_grad or w_b.requires_grad):
+            self.aux_loss = _ModAuxFn.apply(x2d.detach(), w_a, w_b, token_rows, weight)
+        else:
+            self.aux_loss = ops.mod_aux_bce(ops.router(x2d.detach(), w_a, w_b, 0).logits, token_rows, weight)
         return self.aux_loss
 
     def keep_count(self, seq_len: int) -> int:
@@ -86,26 +89,26 @@ class MoDRouter(nn.Module):
 class _ModAuxFn(torch.autograd.Function):
     """weight * mean over the B*S tokens of BCE-with-logits(aux_router(x), selected)
     (mod.py:141-171) with aux_router = Linear(d, 128), SiLU, Linear(128, 1): the router
-    MLP kernel with one output.  x enters detached (mod.py:155), so only the two weights
-    get gradients, from the router MLP backward kernels with dl = weight (sigmoid(l) - t) / T."""
+    MLP kernel with one output, then kmoe_mod_aux_bce.  x enters detached (mod.py:155),
+    so only the two weights get gradients, from the router MLP backward kernels with
+    dl = weight (sigmoid(l) - t) / T."""
 
     @staticmethod
     def forward(ctx, x2d, w_a, w_b, token_rows, weight):
         T = x2d.shape[0]
         r = ops.router(x2d, w_a, w_b, 0, save_hidden=True)
-        lg = r.logits.view(T)
-        t = torch.zeros(T, device=x2d.device, dtype=torch.float32)
-        t[token_rows.long()] = 1.0
-        ctx.save_for_backward(x2d, r.hidden, lg, t)
+        ctx.save_for_backward(x2d, r.hidden, r.logits, token_rows)
         ctx.w_b = w_b
         ctx.weight = weight
-        return weight * (F.softplus(lg) - t * lg).mean()
+        return ops.mod_aux_bce(r.logits, token_rows, weight)
 
     @staticmethod
     def backward(ctx, g):
-        x2d, hidden, lg, t = ctx.saved_tensors
+        x2d, hidden, lg, token_rows = ctx.saved_tensors
         T = x2d.shape[0]
-        dl = ((g.float() * (ctx.weight / T)) * (torch.sigmoid(lg) - t)).view(T, 1).contiguous()
+        t = torch.zeros(T, 1, device=x2d.device, dtype=torch.float32)
+        t[token_rows.long()] = 1.0
+        dl = ((g.float() * (ctx.weight / T)) * (torch.sigmoid(lg) - t)).contiguous()
         dw_a, dw_b = _bwd.router_weight_grads(x2d, hidden, ctx.w_b, dl)
         w_b = ctx.w_b
         del ctx.w_b

@@ -157,6 +157,18 @@ def aux_loss(partials, T, E, counts, k, w_lb, w_z):
     return out
 
 
+def mod_aux_bce(logits, rows, weight):
+    """The MoD auxiliary router's loss (mod.py:141-171) from its logits (T,) or (T, 1)
+    f32 and the kept rows (int32): weight * mean BCE-with-logits, targets 1 at rows."""
+    _need_gpu(logits, rows)
+    logits = _contig(logits, torch.float32)
+    rows = _contig(rows, torch.int32)
+    out = torch.empty(1, device=logits.device, dtype=torch.float32)
+    _lib.call("kmoe_mod_aux_bce", ptr(logits), logits.numel(), ptr(rows), rows.numel(), float(weight), ptr(out),
+              _stream(logits))
+    return out[0]
+
+
 class DispatchOut(NamedTuple):
     counts: torch.Tensor     # (E,) int32 routed counts
     offsets: torch.Tensor    # (E+1,) int32 kept-row offsets

@@ -179,6 +179,8 @@ def test_mod_aux_router_loss(dev, path):
     a64, b64 = _f64(w_a), _f64(w_b)
     ref = P.mod_aux_loss(xin.double().cpu(), a64, b64, sel.sel_idx.cpu().long(), 0.05)
     ref.backward()
+    with torch.no_grad():  # the forward-only form: the same kernels, no autograd record
+        assert float(mr.aux(xin.reshape(B * S, d), sel.token_rows)) == float(aux_mod)
     errs = {"aux": abs(float(aux_mod) - float(ref)) / abs(float(ref)), "dw_a": _rel(w_a.grad, a64.grad),
             "dw_b": _rel(w_b.grad, b64.grad)}
     _check(errs, tight=("aux",))
