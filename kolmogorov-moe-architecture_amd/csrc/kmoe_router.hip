@@ -444,25 +444,46 @@ extern "C" int kmoe_router(const void* x, const int32_t* row_index, int64_t T, i
 // MoD auxiliary router loss (mod.py:141-171) from its logits l (T): weight * the mean
 // over t of BCE-with-logits(l_t, y_t), y_t = 1 for the kept rows rows[0, n_keep) and 0
 // elsewhere, i.e. weight / T * (sum_t softplus(l_t) - sum_j l[rows[j]]).  One
-// workgroup; fixed-order sums (per-thread strided, then an LDS tree).
+// workgroup; fixed-order sums (per-thread strided, a wave butterfly, the wave sums in
+// order).  Each thread issues U independent loads per round, and softplus takes the
+// hardware log of 1 + e (e = exp(-|l|); where 1 + e rounds to 1 the dropped log1p(e)
+// is below 6e-8): with single dependent loads and libm's log1pf the one workgroup
+// took 11 us for 8192 logits.
 __global__ __launch_bounds__(1024) void mod_aux_bce_kernel(const float* __restrict__ l, int64_t T,
                                                            const int32_t* __restrict__ rows, int64_t n_keep,
                                                            float weight, float* __restrict__ out) {
-  __shared__ float red[1024];
+  constexpr int U = 8;
+  __shared__ float red[16];
   const int tid = threadIdx.x;
   float acc = 0.0f;
-  for (int64_t t = tid; t < T; t += 1024) {
-    const float v = l[t];
-    acc += fmaxf(v, 0.0f) + log1pf(__expf(-fabsf(v)));  // softplus, overflow-free
+  for (int64_t t0 = tid; t0 < T; t0 += 1024 * U) {
+    float v[U];
+#pragma unroll
+    for (int q = 0; q < U; ++q) v[q] = t0 + 1024 * q < T ? l[t0 + 1024 * q] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < U; ++q)
+      if (t0 + 1024 * q < T) acc += fmaxf(v[q], 0.0f) + __logf(1.0f + __expf(-fabsf(v[q])));  // softplus
   }
-  for (int64_t j = tid; j < n_keep; j += 1024) acc -= l[rows[j]];
-  red[tid] = acc;
+  for (int64_t j0 = tid; j0 < n_keep; j0 += 1024 * U) {
+    int32_t r[U];
+#pragma unroll
+    for (int q = 0; q < U; ++q) r[q] = j0 + 1024 * q < n_keep ? rows[j0 + 1024 * q] : -1;
+    float v[U];
+#pragma unroll
+    for (int q = 0; q < U; ++q) v[q] = r[q] >= 0 ? l[r[q]] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < U; ++q) acc -= v[q];
+  }
+  // wave sums (xor butterfly), then the 16 wave sums in order
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if ((tid & 63) == 0) red[tid >> 6] = acc;
   __syncthreads();
-  for (int s = 512; s > 0; s >>= 1) {
-    if (tid < s) red[tid] += red[tid + s];
-    __syncthreads();
+  if (tid == 0) {
+    float sum = 0.0f;
+    for (int w = 0; w < 16; ++w) sum += red[w];
+    out[0] = sum * (weight / (float)T);
   }
-  if (tid == 0) out[0] = red[0] * (weight / (float)T);
 }
 
 extern "C" int kmoe_mod_aux_bce(const float* logits, int64_t T, const int32_t* rows, int64_t n_keep, float weight,
