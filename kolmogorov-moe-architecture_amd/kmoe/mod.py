@@ -99,6 +99,7 @@ class _ModAuxFn(torch.autograd.Function):
         r = ops.router(x2d, w_a, w_b, 0, save_hidden=True)
         ctx.save_for_backward(x2d, r.hidden, r.logits, token_rows)
         ctx.w_b = w_b
+        ctx.dtypes = (w_a.dtype, w_b.dtype)
         ctx.weight = weight
         return ops.mod_aux_bce(r.logits, token_rows, weight)
 
@@ -110,9 +111,8 @@ class _ModAuxFn(torch.autograd.Function):
         t[token_rows.long()] = 1.0
         dl = ((g.float() * (ctx.weight / T)) * (torch.sigmoid(lg) - t)).contiguous()
         dw_a, dw_b = _bwd.router_weight_grads(x2d, hidden, ctx.w_b, dl)
-        w_b = ctx.w_b
         del ctx.w_b
-        return None, dw_a.to(w_b.dtype), dw_b.to(w_b.dtype), None, None
+        return None, dw_a.to(ctx.dtypes[0]), dw_b.to(ctx.dtypes[1]), None, None
 
 
 class _MoDTrainFn(torch.autograd.Function):
