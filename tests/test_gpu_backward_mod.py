@@ -144,7 +144,7 @@ def test_mod_expert_choice(dev, B, S, d, E, F_, cf, ec_cf, with_res, train):
     _check(errs)
 
 
-@pytest.mark.parametrize("path", ["tc", "ec", "block"])
+@pytest.mark.parametrize("path", ["tc", "ec", "block", "block_ec"])
 def test_mod_aux_router_loss(dev, path):
     """The MoD router's auxiliary BCE loss (mod.py:141-171) in training: its value and the
     auxiliary router's weight gradients against fp64 autograd of oracle/torch_port.
@@ -155,24 +155,29 @@ def test_mod_aux_router_loss(dev, path):
     print(f"mod aux path={path}", flush=True)
     cfg = AdvancedMoEConfig(d_model=d, n_experts=E, d_ff_expert=F_, mod_enabled=True, mod_capacity_factor=0.75,
                             residual_dropout=0.0, mod_load_balance_loss_weight=0.05,
-                            moe_routing="expert_choice" if path == "ec" else "token_choice")
-    m = (MoEFFNBlock(cfg, 0) if path == "block" else MoDMoE(cfg)).to(dev, BF).train()
+                            moe_routing="expert_choice" if path.endswith("ec") else "token_choice")
+    m = (MoEFFNBlock(cfg, 0) if path.startswith("block") else MoDMoE(cfg)).to(dev, BF).train()
     g = torch.Generator().manual_seed(620 + len(path))
     with torch.no_grad():
         for p_ in m.parameters():
             p_.copy_(torch.randn(p_.shape, generator=g) * 0.05 + (1.0 if p_.dim() == 1 else 0.0))
     x = torch.randn(B, S, d, generator=g).to(BF).to(dev).requires_grad_(True)
     y = m(x)
-    if path == "block":
-        assert m.last_path == "fused_train"
+    if path.startswith("block"):
+        # expert choice: the unfused composition (the block's norm module, then MoD around the layer)
+        assert m.last_path == ("unfused" if path == "block_ec" else "fused_train")
     mr = m.ffn_mod_router
     aux_mod = mr.aux_loss
     (y.float().square().mean() + m.aux_loss).backward()
     torch.cuda.synchronize()
     keep = mr.keep_count(S)
     with torch.no_grad():
-        xin = ops.rmsnorm(x.detach().reshape(B * S, d), m.ffn_norm.weight, m.ffn_norm.eps).n if path == "block" \
-            else x.detach()
+        if path == "block":
+            xin = ops.rmsnorm(x.detach().reshape(B * S, d), m.ffn_norm.weight, m.ffn_norm.eps).n
+        elif path == "block_ec":
+            xin = m.ffn_norm(x.detach())
+        else:
+            xin = x.detach()
         xin = xin.reshape(B, S, d)
         sel = ops.mod_select(xin, mr.router.weight, keep)
     w_a, w_b = mr.aux_router[0].weight, mr.aux_router[2].weight
