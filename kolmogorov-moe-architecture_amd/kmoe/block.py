@@ -143,6 +143,7 @@ class MoEFFNBlock(nn.Module):
             ffn.aux_loss = aux if ffn.training else 0.0
             if use_mod:
                 self.ffn_mod_router.aux(n, rows)
+                self.ffn_mod_router.join()
             self.last_path = "fused_train"
         elif not use_mod and self._fusable(hidden_states):
             out = self._forward_fused(hidden_states)
