@@ -6,17 +6,20 @@
 // for the rows r of expert e, [offsets[e], offsets[e+1]).
 //
 // Tiling: a workgroup of 4 waves (one per SIMD) owns a 256-row x 256-B-row tile;
-// waves form 2 (rows) x 2 (B rows) and each computes 128 x 128 as 4x4 blocks of
-// v_mfma_f32_32x32x16_bf16 (fp8: v_mfma_scale_f32_32x32x64_f8f6f4), 256 fp32
-// accumulators per lane.  A 128x128 wave tile reads 0.5 KiB of LDS per MFMA, the
-// least a 4-wave workgroup of this tile allows.  K advances 64 bf16 (128 fp8
-// bytes) per pipeline step through 2 LDS stages of 2 x 32 KiB.  Tile data is
-// loaded into registers with buffer loads (the K offset is a scalar operand) one
-// step ahead and written to the stage not being read, 16-byte chunks XOR-swizzled
-// so that both the 1 KiB block writes and the 16 lanes of each fragment read pass
-// are bank-conflict free.  Fragment reads, LDS writes and loads are interleaved
-// with the MFMAs by scheduling groups; fragments are double buffered in registers;
-// one barrier per step, in its last substep.
+// waves form 2 (rows) x 2 (B rows) and each computes 128 x 128, 256 fp32 accumulators
+// per lane: bf16 as 8x8 blocks of v_mfma_f32_16x16x32_bf16, fp8 as 4x4 blocks of
+// v_mfma_scale_f32_32x32x64_f8f6f4.  (The expert GEMMs run at the chip's power limit,
+// and on random data the 16x16x32 bf16 form sustains a higher clock than 32x32x16:
+// 0.81 against 0.70 of the bf16 peak in an MFMA-only loop; the fp8 16x16x128 form runs
+// at half rate, so fp8 keeps 32x32x64.)  A 128x128 wave tile reads 0.5 KiB of LDS per
+// 32 K-MACs of output, the least a 4-wave workgroup of this tile allows.  K advances 64
+// bf16 (128 fp8 bytes) per pipeline step through 2 LDS stages of 2 x 32 KiB.  Tile
+// data is loaded into registers with buffer loads (the K offset is a scalar operand)
+// one step ahead and written to the stage not being read, 16-byte chunks XOR-swizzled
+// so that both the 1 KiB block writes and every 16-lane fragment read pass are
+// bank-conflict free.  bf16: the K loop is emitted in program order (each MFMA with
+// the LDS or memory instruction assigned to it); fp8: interleaved by scheduling
+// groups, fragments double buffered.  One barrier per step.
 // The MFMAs take the B fragment as their first operand, so each lane accumulates
 // runs of four consecutive output columns of one row; the epilogue packs them to
 // 8-byte bf16 runs in registers, stages the tile through LDS and writes it with
@@ -164,6 +167,19 @@ __device__ __forceinline__ void mfma(f32x16_t& acc, const Frag<FP8>& a, const Fr
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v, b.v, acc, 0, 0, 0);
   else
     acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a.v, b.v, acc, 0, 0, 0, 127, 0, 127);
+}
+
+// bf16 tiles run on v_mfma_f32_16x16x32_bf16: on random data the 32x32x16 form holds the
+// chip at 0.70 of the bf16 peak under its power limit (an MFMA-only loop, all CUs), the
+// 16x16x32 form at 0.81 (it moves half the accumulator bytes per FLOP).  Fragment of
+// K-substep `i` (32 of K: chunks 4i .. 4i+3) for LDS tile rows r0 .. r0+15: lane l reads
+// row r0 + l%16 (`r`), chunk 4i + l/16 (`lq`); a 16-lane pass is 16 consecutive rows of
+// one logical chunk, which the swizzle spreads over all banks.
+__device__ __forceinline__ void read_frag16(const uint8_t* l, int r, int i, int lq, Frag<false>& f) {
+  f.v = *reinterpret_cast<const bf16x8_t*>(l + swz(r, 4 * i + lq));
+}
+__device__ __forceinline__ void mfma16(f32x4_t& acc, const Frag<false>& a, const Frag<false>& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
 }
 
 // B-tile geometry of a tile whose waves hold WNB 32-row B blocks each (WNB = 4: the
@@ -328,7 +344,15 @@ template <bool GATE_UP, bool FP8, bool GATHER, int WNB, bool SAVE_GU = false, bo
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e, int m0, int m_end, int nt,
                                           int q) {
   static_assert(WNB == 4 || WNB == 2 || WNB == 1, "tile width");
-  constexpr int NSUB = FP8 ? KB / 64 : KB / 32;  // MFMA K-substeps per pipeline step
+  // bf16: 16x16x32 MFMAs, 16-row A and B blocks (MA x NBB per wave, NAB of them holding
+  // rows); fp8: 32x32x64, 32-row blocks
+  constexpr bool M16 = !FP8;
+  constexpr int MA = M16 ? 8 : 4;
+  constexpr int NAB = M16 ? 2 * NMA : NMA;
+  constexpr int NBB = M16 ? 2 * WNB : WNB;
+  using Acc = std::conditional_t<M16, f32x4_t, f32x16_t>;
+  constexpr int ACCN = M16 ? 4 : 16;
+  constexpr int NSUB = KB / 64;  // MFMA K-substeps per pipeline step (bf16: 32 of K, fp8: 64)
   constexpr int BNT = 64 * WNB;                  // B rows of the tile
   constexpr int TBB = BNT * KB;                  // bytes of one B stage tile
   constexpr int BLK_B = BNT * KB / 1024 / 4;     // B load blocks per wave per step
@@ -347,13 +371,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   auto la_buf = [&](int st) { return lds + st * (TB + TBB); };
   auto lb_buf = [&](int st) { return lds + st * (TB + TBB) + TB; };
 
-  f32x16_t acc[4][WNB];
+  Acc acc[MA][NBB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MA; ++i)
 #pragma unroll
-    for (int j = 0; j < WNB; ++j)
+    for (int j = 0; j < NBB; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < ACCN; ++r) acc[i][j][r] = 0.0f;
   // fp8 scales of the tile's A rows (thread = row) and B rows (thread = LDS B row),
   // loaded now and put in LDS for the epilogue (rows past the expert's end: 0)
   float sa_v = 0.0f, sb_v = 0.0f;
@@ -425,27 +449,44 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
                                      : lb_buf(st) + (wave * BLK_B + qq - BLK_PER_WAVE) * 1024;
     *reinterpret_cast<i32x4_t*>(dst + lane * 16) = stg[qq];
   };
-  Frag<FP8> fa[2][4], fb[2][WNB];
-  auto rd = [&](int st, int i, Frag<FP8> (&a)[4], Frag<FP8> (&b)[WNB]) {
+  Frag<FP8> fa[2][MA], fb[2][NBB];
+  const int r16 = lane & 15, lq = lane >> 4;
+  auto rd = [&](int st, int i, Frag<FP8> (&a)[MA], Frag<FP8> (&b)[NBB]) {
     if constexpr (NMA > 0) {
       const uint8_t* la = la_buf(st);
       const uint8_t* lb = lb_buf(st);
+      if constexpr (M16) {
 #pragma unroll
-      for (int mi = 0; mi < NMA; ++mi) read_frag<FP8>(la, wm * 128 + mi * 32 + lr, i, lh, a[mi]);
+        for (int j = 0; j < NBB; ++j)
+          read_frag16(lb, b_lds_row<GATE_UP, WNB>(wn, j >> 1, 16 * (j & 1) + r16), i, lq, b[j]);
 #pragma unroll
-      for (int j = 0; j < WNB; ++j) read_frag<FP8>(lb, b_lds_row<GATE_UP, WNB>(wn, j, lr), i, lh, b[j]);
+        for (int mi = 0; mi < NAB; ++mi) read_frag16(la, wm * 128 + mi * 16 + r16, i, lq, a[mi]);
+      } else {
+#pragma unroll
+        for (int mi = 0; mi < NMA; ++mi) read_frag<FP8>(la, wm * 128 + mi * 32 + lr, i, lh, a[mi]);
+#pragma unroll
+        for (int j = 0; j < WNB; ++j) read_frag<FP8>(lb, b_lds_row<GATE_UP, WNB>(wn, j, lr), i, lh, b[j]);
+      }
     }
   };
-  auto mma = [&](const Frag<FP8> (&a)[4], const Frag<FP8> (&b)[WNB]) {
-#pragma unroll
-    for (int mi = 0; mi < NMA; ++mi)
-#pragma unroll
-      for (int j = 0; j < WNB; ++j) mfma<FP8>(acc[mi][j], b[j], a[mi]);
+  auto mma1 = [&](Acc& c, const Frag<FP8>& b, const Frag<FP8>& a) {
+    if constexpr (M16)
+      mfma16(c, b, a);
+    else
+      mfma<FP8>(c, b, a);
   };
-  // MFMAs [lo, hi) of a substep (linear index mi * WNB + j)
-  auto mma_part = [&](const Frag<FP8> (&a)[4], const Frag<FP8> (&b)[WNB], auto lo_tag, auto hi_tag) {
-    static_for<decltype(lo_tag)::value, decltype(hi_tag)::value>(
-        [&](auto xc) { mfma<FP8>(acc[decltype(xc)::value / WNB][decltype(xc)::value % WNB], b[decltype(xc)::value % WNB], a[decltype(xc)::value / WNB]); });
+  auto mma = [&](const Frag<FP8> (&a)[MA], const Frag<FP8> (&b)[NBB]) {
+#pragma unroll
+    for (int mi = 0; mi < NAB; ++mi)
+#pragma unroll
+      for (int j = 0; j < NBB; ++j) mma1(acc[mi][j], b[j], a[mi]);
+  };
+  // MFMAs [lo, hi) of a substep (linear index mi * NBB + j)
+  auto mma_part = [&](const Frag<FP8> (&a)[MA], const Frag<FP8> (&b)[NBB], auto lo_tag, auto hi_tag) {
+    static_for<decltype(lo_tag)::value, decltype(hi_tag)::value>([&](auto xc) {
+      constexpr int x = decltype(xc)::value;
+      mma1(acc[x / NBB][x % NBB], b[x % NBB], a[x / NBB]);
+    });
   };
 
   // Pipeline.  Step kt computes LDS stage kt%2 while the registers hold step kt+1's
@@ -458,16 +499,136 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   // stage kt+1, whose first fragments are read under the last few MFMAs.  Register
   // dependencies give the vmcnt waits; the scheduling groups interleave the LDS and
   // memory operations with the MFMAs, fragment reads first.
-  constexpr int RD = NMA > 0 ? (FP8 ? 2 : 1) * (NMA + WNB) : 0;  // LDS reads of a substep's fragments
-  constexpr int NMS = NMA * WNB;                                    // MFMAs per substep
+  constexpr int RD = NMA > 0 ? (FP8 ? 2 : 1) * (NAB + NBB) : 0;  // LDS reads of a substep's fragments
+  constexpr int NMS = NAB * NBB;                                    // MFMAs per substep
   for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 0);
   for (int qq = 0; qq < NBLK; ++qq) write_block(qq, 0);
   for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 1);
   wait_lgkmcnt0();
   barrier_nofence();
-  rd(0, 0, fa[0], fb[0]);
+  if constexpr (!M16) rd(0, 0, fa[0], fb[0]);
 
+  // bf16 (16x16 blocks): the K loop is emitted in program order, one MFMA at a time,
+  // each followed by the LDS reads, block writes or reloads assigned to it and fenced
+  // with sched_barrier.  (With scheduling groups the scheduler may take the MFMAs out of
+  // order, and the register allocator then stops tying each MFMA's accumulator input to
+  // its output: hundreds of accumulator copies per K-step.)  A 16x16x32 MFMA keeps the
+  // matrix pipe 16 cycles, about what a 1 KiB LDS block write takes to issue, so the
+  // schedule gives each MFMA at most one LDS or memory instruction where it can.
+  // Substep i uses B fragment set fb[i] and the one A set fa[0]; MFMAs go row block by
+  // row block.  Substep 0 reads substep 1's B fragments into fb[1] and each row block's
+  // next A fragment right after that row block's last MFMA (an A ring: no second A set).
+  // Substep 1 meets the other waves at the barrier that publishes stage nxt after MFMA
+  // GB, then reads that stage's substep-0 fragments (B0, A0, B1, ..., each A after its
+  // row block's last MFMA).  The block writes into stage nxt and the reloads of step kt+2
+  // go over substep 0 and the part of substep 1 before the barrier, each reload a few
+  // MFMAs after the write that frees its registers.
+  constexpr bool FULL16 = NMS == 64 && NBB == 8 && NAB == 8 && NBLK == 16;
+  constexpr int NR16 = NMS > 0 ? ((NBB + NAB) < NMS - 1 ? NBB + NAB : NMS - 1) : 0;
+  constexpr int GB = FULL16 ? 31 : NMS - 1 - NR16;  // substep 1: the barrier follows MFMA GB
+  constexpr int H0 = NBLK / 2;                      // block writes in substep 0 (the rest in substep 1)
+  auto rdB16 = [&](int st, int i, int j, Frag<FP8>& b) {
+    if constexpr (M16) read_frag16(lb_buf(st), b_lds_row<GATE_UP, WNB>(wn, j >> 1, 16 * (j & 1) + r16), i, lq, b);
+  };
+  auto rdA16 = [&](int st, int i, int mi) {
+    if constexpr (M16) read_frag16(la_buf(st), wm * 128 + mi * 16 + r16, i, lq, fa[0][mi]);
+  };
+  auto sub16 = [&](int kt, auto i_tag, auto last_tag) {
+    constexpr int i = decltype(i_tag)::value;
+    constexpr bool LAST = decltype(last_tag)::value;
+    const int cur = kt & 1, nxt = cur ^ 1;
+    constexpr int NW = LAST ? 0 : (i == 0 ? H0 : NBLK - H0), QB = i == 0 ? 0 : H0;
+    if constexpr (NMS == 0) {
+      // a wave without rows: only its share of the tile loads and the barrier
+      if constexpr (NW > 0) {
+        static_for<0, NW>([&](auto wc) {
+          write_block(QB + decltype(wc)::value, nxt);
+          load_block(QB + decltype(wc)::value, kt + 2);
+        });
+      }
+      if constexpr (i == 1 && !LAST) {
+        wait_lgkmcnt0();
+        barrier_nofence();
+      }
+      return;
+    }
+    // MFMA after which block write w / its reload go
+    constexpr auto w_at = [](int w) constexpr {
+      if (FULL16) return i == 0 ? 16 + 6 * w : 4 * w;
+      const int span = i == 0 ? NMS - 2 : GB - 2;
+      return span > 0 ? 1 + (w * span) / NW : 0;
+    };
+    constexpr auto l_at = [](int w) constexpr {
+      if (FULL16) return i == 0 ? 18 + 6 * w : 4 * w + 2;
+      const int span = i == 0 ? NMS - 2 : GB - 2;
+      return span > 0 ? 1 + (w * span) / NW : 0;
+    };
+    // substep 0: MFMA after which next-substep read B_j / A_mi goes
+    constexpr auto b0_at = [](int j) constexpr { return FULL16 ? 2 * j : (j < NMS ? j : NMS - 1); };
+    // substep 1: post-barrier read k (0: B0, 1: A0, 2 ..: B1 .. B_{NBB-1}, then A1 ..)
+    constexpr auto post_at = [](int k, int kind, int idx) constexpr {
+      const int e0 = GB + 1 + (FULL16 ? 2 * k + 1 : k);
+      const int e1 = kind == 1 ? idx * NBB + NBB - 1 : 0;
+      const int at = e0 > e1 ? e0 : e1;
+      return at < NMS - 1 ? at : NMS - 1;
+    };
+    static_for<0, NMS>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+      constexpr int mi = g / NBB, j = g % NBB;
+      mma1(acc[mi][j], fb[i][j], fa[0][mi]);
+      __builtin_amdgcn_sched_barrier(0);
+      // block writes, then reloads (substep 1: all before the barrier)
+      static_for<0, NW>([&](auto wc) {
+        constexpr int w = decltype(wc)::value;
+        if constexpr (w_at(w) == g) write_block(QB + w, nxt);
+      });
+      static_for<0, NW>([&](auto wc) {
+        constexpr int w = decltype(wc)::value;
+        if constexpr (l_at(w) == g) load_block(QB + w, kt + 2);
+      });
+      if constexpr (i == 0) {
+        static_for<0, NBB>([&](auto jc) {
+          constexpr int jj = decltype(jc)::value;
+          if constexpr (b0_at(jj) == g) rdB16(cur, 1, jj, fb[1][jj]);
+        });
+        if constexpr (j == NBB - 1) rdA16(cur, 1, mi);
+      } else if constexpr (!LAST) {
+        if constexpr (g == GB) {
+          wait_lgkmcnt0();
+          barrier_nofence();
+        }
+        static_for<0, NBB + NAB>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          constexpr int kind = k == 0 ? 0 : k == 1 ? 1 : k < NBB + 1 ? 0 : 1;
+          constexpr int idx = k == 0 ? 0 : k == 1 ? 0 : k < NBB + 1 ? k - 1 : k - NBB;
+          if constexpr (post_at(k, kind, idx) == g) {
+            if constexpr (kind == 0)
+              rdB16(nxt, 0, idx, fb[0][idx]);
+            else
+              rdA16(nxt, 0, idx);
+          }
+        });
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  auto step16 = [&](int kt, auto last_tag) {
+    sub16(kt, std::integral_constant<int, 0>{}, last_tag);
+    sub16(kt, std::integral_constant<int, 1>{}, last_tag);
+  };
+  if constexpr (M16) {
+    if constexpr (NMA > 0) {
+#pragma unroll
+      for (int j = 0; j < NBB; ++j) rdB16(0, 0, j, fb[0][j]);
+#pragma unroll
+      for (int mi = 0; mi < NAB; ++mi) rdA16(0, 0, mi);
+    }
+  }
   auto step = [&](int kt, auto last_tag) {
+    if constexpr (M16) {
+      step16(kt, last_tag);
+      return;
+    }
     constexpr bool LAST = decltype(last_tag)::value;
     const int cur = kt & 1, nxt = cur ^ 1;
     static_for<0, NSUB>([&](auto ic) {
@@ -581,19 +742,49 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
     const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{c, d}, bf16x2_t));
     return i32x2_t{(int)lo, (int)hi};
   };
-  // lane's row of block 0 and its first column (c = 0) of output column block 0
-  uint8_t* const wbase = lds + (wm * 128 + lr) * OSTR + (wn * (NC / 2) + 4 * lh) * 2;
+  if constexpr (M16) {
+    // 16x16 blocks: acc[mi][j][t] is output row wm*128 + mi*16 + l%16 against B row
+    // 4 (l/16) + t of 16-row B block j: one run of four output columns per block (gate/up:
+    // gate block jo, up block jo + NBB/2, same columns)
+    constexpr int NJ16 = GATE_UP ? NBB / 2 : NBB;
+    uint8_t* const wb16 = lds + (wm * 128 + r16) * OSTR + (wn * (NC / 2) + 4 * lq) * 2;
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-    if (mi >= NMA) break;  // rows past the expert's end: never stored
-    if constexpr (FP8 || RSCALE) sar = sa_l[wm * 128 + mi * 32 + lr];
+    for (int mi = 0; mi < NAB; ++mi) {
+      if constexpr (RSCALE) sar = sa_l[wm * 128 + mi * 16 + r16];
 #pragma unroll
-    for (int jo = 0; jo < NJ; ++jo)
+      for (int jo = 0; jo < NJ16; ++jo) {
+        float v[4];
 #pragma unroll
-      for (int c = 0; c < NCR; ++c)
-        *reinterpret_cast<i32x2_t*>(wbase + mi * 32 * OSTR + (jo * 32 + 8 * c) * 2) =
-            pack4(result(mi, 4 * c, jo), result(mi, 4 * c + 1, jo), result(mi, 4 * c + 2, jo),
-                  result(mi, 4 * c + 3, jo));
+        for (int t = 0; t < 4; ++t) {
+          if constexpr (GATE_UP) {
+            float gg = acc[mi][jo][t], u = acc[mi][jo + NBB / 2][t];
+            if constexpr (RSCALE) {
+              gg *= sar;
+              u *= sar;
+            }
+            v[t] = silu_fast_f32(gg) * u;
+          } else {
+            v[t] = acc[mi][jo][t];
+          }
+        }
+        *reinterpret_cast<i32x2_t*>(wb16 + mi * 16 * OSTR + jo * 32) = pack4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  } else {
+    // lane's row of block 0 and its first column (c = 0) of output column block 0
+    uint8_t* const wbase = lds + (wm * 128 + lr) * OSTR + (wn * (NC / 2) + 4 * lh) * 2;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      if (mi >= NMA) break;  // rows past the expert's end: never stored
+      if constexpr (FP8 || RSCALE) sar = sa_l[wm * 128 + mi * 32 + lr];
+#pragma unroll
+      for (int jo = 0; jo < NJ; ++jo)
+#pragma unroll
+        for (int c = 0; c < NCR; ++c)
+          *reinterpret_cast<i32x2_t*>(wbase + mi * 32 * OSTR + (jo * 32 + 8 * c) * 2) =
+              pack4(result(mi, 4 * c, jo), result(mi, 4 * c + 1, jo), result(mi, 4 * c + 2, jo),
+                    result(mi, 4 * c + 3, jo));
+    }
   }
   __syncthreads();
   constexpr int OCPR = NC * 2 / 16;  // 16-byte chunks per output row
@@ -606,17 +797,29 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
     constexpr int NC2 = 64 * WNB;
     constexpr int OSTR2 = NC2 * 2 + 16;
     __syncthreads();
-    uint8_t* const wb2 = lds + (wm * 128 + lr) * OSTR2 + 4 * lh * 2;
+    if constexpr (M16) {
+      uint8_t* const wb2 = lds + (wm * 128 + r16) * OSTR2 + 4 * lq * 2;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      if (mi >= NMA) break;
+      for (int mi = 0; mi < NAB; ++mi)
 #pragma unroll
-      for (int j = 0; j < WNB; ++j) {
-        const int col = b_lds_row<true, WNB>(wn, j, 0);
+        for (int j = 0; j < NBB; ++j) {
+          const int col = b_lds_row<true, WNB>(wn, j >> 1, 16 * (j & 1));
+          *reinterpret_cast<i32x2_t*>(wb2 + mi * 16 * OSTR2 + col * 2) =
+              pack4(acc[mi][j][0], acc[mi][j][1], acc[mi][j][2], acc[mi][j][3]);
+        }
+    } else {
+      uint8_t* const wb2 = lds + (wm * 128 + lr) * OSTR2 + 4 * lh * 2;
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          *reinterpret_cast<i32x2_t*>(wb2 + mi * 32 * OSTR2 + (col + 8 * c) * 2) =
-              pack4(acc[mi][j][4 * c], acc[mi][j][4 * c + 1], acc[mi][j][4 * c + 2], acc[mi][j][4 * c + 3]);
+      for (int mi = 0; mi < 4; ++mi) {
+        if (mi >= NMA) break;
+#pragma unroll
+        for (int j = 0; j < WNB; ++j) {
+          const int col = b_lds_row<true, WNB>(wn, j, 0);
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            *reinterpret_cast<i32x2_t*>(wb2 + mi * 32 * OSTR2 + (col + 8 * c) * 2) =
+                pack4(acc[mi][j][4 * c], acc[mi][j][4 * c + 1], acc[mi][j][4 * c + 2], acc[mi][j][4 * c + 3]);
+        }
       }
     }
     __syncthreads();
