@@ -31,7 +31,8 @@ which also adds the residual's gradient.
 Other configurations (layernorm, expert choice, fp8, active residual dropout) run
 the unfused composition: the reference's RMSNorm / LayerNorm in torch, the kmoe MoE
 layer (MoD-gated in training mode, with its HIP backward where it has one) and a
-torch add.  The MoD router's auxiliary BCE loss is not part of this build.
+torch add.  In training mode the MoD router's auxiliary BCE loss (mod.py:114-171) is
+added to aux_loss on the fused path as on the unfused one (MoDRouter.aux).
 """
 from __future__ import annotations
 
@@ -143,7 +144,6 @@ class MoEFFNBlock(nn.Module):
             ffn.aux_loss = aux if ffn.training else 0.0
             if use_mod:
                 self.ffn_mod_router.aux(n, rows)
-                self.ffn_mod_router.join()
             self.last_path = "fused_train"
         elif not use_mod and self._fusable(hidden_states):
             out = self._forward_fused(hidden_states)

@@ -61,28 +61,11 @@ class MoDRouter(nn.Module):
         if torch.is_grad_enabled() and (w_a.requires_grad or w_b.requires_grad):
             self.aux_loss = _ModAuxFn.apply(x2d.detach(), w_a, w_b, token_rows, weight)
             return self.aux_loss
-        # forward only: on a side stream (default priority), so that the auxiliary
-        # router's workgroups run beside the MoE router's (the MoE router covers the kept
-        # rows only, 64 per workgroup, and leaves CUs idle); join() orders the main stream
-        # after it
-        main = torch.cuda.current_stream(x2d.device)
-        side = _side_stream(x2d.device)
-        side.wait_stream(main)
-        with torch.cuda.stream(side):
-            out = ops.mod_aux_bce(ops.router(x2d.detach(), w_a, w_b, 0).logits, token_rows, weight)
-        x2d.record_stream(side)
-        token_rows.record_stream(side)
-        out.record_stream(main)
-        self._pending = side
-        self.aux_loss = out
+        # forward only: the same kernels without an autograd record, in order on the
+        # caller's stream
+        self.aux_loss = ops.mod_aux_bce(ops.router(x2d.detach(), w_a, w_b, 0, stage="mod_aux_router").logits,
+                                        token_rows, weight)
         return self.aux_loss
-
-    def join(self):
-        """Orders the current stream after the pending forward-only auxiliary loss."""
-        side = getattr(self, "_pending", None)
-        if side is not None:
-            torch.cuda.current_stream(side.device).wait_stream(side)
-            self._pending = None
 
     def keep_count(self, seq_len: int) -> int:
         return max(1, min(seq_len, int(seq_len * self.capacity_factor)))  # mod.py:97
@@ -102,20 +85,8 @@ class MoDRouter(nn.Module):
         sel = self.select(hidden_states)
         B, S, d = hidden_states.shape
         self.aux(hidden_states.reshape(B * S, d), sel.token_rows)
-        self.join()
         dt = hidden_states.dtype
         return sel.sel_idx, sel.sel_w.to(dt), sel.logits.to(dt), sel.sel_idx
-
-
-_SIDE_STREAMS = {}
-
-
-def _side_stream(device) -> torch.cuda.Stream:
-    """One default-priority side stream per device."""
-    key = torch.device(device).index
-    if key not in _SIDE_STREAMS:
-        _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
-    return _SIDE_STREAMS[key]
 
 
 class _ModAuxFn(torch.autograd.Function):
@@ -128,7 +99,7 @@ class _ModAuxFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x2d, w_a, w_b, token_rows, weight):
         T = x2d.shape[0]
-        r = ops.router(x2d, w_a, w_b, 0, save_hidden=True)
+        r = ops.router(x2d, w_a, w_b, 0, save_hidden=True, stage="mod_aux_router")
         ctx.save_for_backward(x2d, r.hidden, r.logits, token_rows)
         ctx.w_b = w_b
         ctx.dtypes = (w_a.dtype, w_b.dtype)
@@ -203,10 +174,7 @@ def mod_ffn(ffn: MoELayer, mod_router: MoDRouter, hidden_states: torch.Tensor,
     """ffn_output of layers.py:148-177 for the normalised input (residual + it with
     `residual`), setting ffn.aux_loss; trains through the HIP backward when gradients
     are wanted."""
-    try:
-        return _mod_ffn(ffn, mod_router, hidden_states, residual)
-    finally:
-        mod_router.join()
+    return _mod_ffn(ffn, mod_router, hidden_states, residual)
 
 
 def _mod_ffn(ffn: MoELayer, mod_router: MoDRouter, hidden_states: torch.Tensor,

@@ -82,7 +82,7 @@ class RouterOut(NamedTuple):
 
 
 def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=False,
-           rms_eps=None, hist=True) -> RouterOut:
+           rms_eps=None, hist=True, stage="router") -> RouterOut:
     """logits/top-k of the reference Router (moe.py:423-462) on the HIP kernel.
 
     x2d: (rows, d) bf16; w_in: (128, d); w_out: (E, 128); row_index: optional
@@ -91,6 +91,7 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=F
     folded into w_in's columns; the result carries the per-token scale (rscale).
     hist (k > 0, not rms): also return each 64-token block's per-expert routed counts,
     which dispatch(block_counts=...) takes instead of counting them again.
+    stage: the name the per-stage timing records the launch under.
     """
     _need_gpu(x2d, w_in, w_out)
     x2d = _contig(x2d, _BF16)
@@ -115,17 +116,17 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=F
         if save_hidden:
             raise ValueError("kmoe.router: rms_eps is a forward-only (inference) path")
         rscale = torch.empty(max(T, 1), device=dev, dtype=torch.float32)
-        with _Stage("router"):
+        with _Stage(stage):
             _lib.call("kmoe_router_rms", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
                       ptr(logits), ptr(idx), ptr(w), ptr(partials), float(rms_eps), ptr(rscale), _stream(x2d))
         return RouterOut(logits, idx, w, partials, None, rscale)
     if hist and k > 0 and T > 0:
         bc = torch.empty((T + 63) // 64, E, device=dev, dtype=torch.int32)
-        with _Stage("router"):
+        with _Stage(stage):
             _lib.call("kmoe_router_hist", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
                       ptr(logits), ptr(idx), ptr(w), ptr(partials), ptr(hidden), ptr(bc), _stream(x2d))
         return RouterOut(logits, idx, w, partials, hidden, None, bc)
-    with _Stage("router"):
+    with _Stage(stage):
         _lib.call("kmoe_router_train", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
                   ptr(logits), ptr(idx), ptr(w), ptr(partials), ptr(hidden), _stream(x2d))
     return RouterOut(logits, idx, w, partials, hidden)
