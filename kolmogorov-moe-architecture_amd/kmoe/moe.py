@@ -27,6 +27,7 @@ from typing import Optional, Tuple
 import torch
 import torch.nn as nn
 
+from . import _lib
 from . import backward as _bwd
 from . import ops
 from .config import AdvancedMoEConfig
@@ -571,6 +572,28 @@ class _MoEECTrainFn(torch.autograd.Function):
         return (dx, g.dw_in.to(w_in.dtype), g.dw_out.to(w_out.dtype), *ge.cast_grads(g.dw1, g.dw2, g.dw3), None)
 
 
+def check_supported(config: AdvancedMoEConfig) -> None:
+    """Raises ValueError, at construction, for shapes the HIP kernels do not take: more
+    than MAX_EXPERTS experts (dispatch, router and GEMM slot tables hold one expert per
+    wave lane), d_model not a multiple of 64 (the GEMMs' K-steps and the row kernels'
+    16-byte vectors), top-k outside [1, min(8, n_experts)] for token choice (the router
+    keeps its picks in registers).  The reference takes any of these
+    (moe.py:183-185, configs/1b_150m_active.yaml: 164 experts, d_model 1512)."""
+    E, d = int(config.n_experts), int(config.d_model)
+    routing = getattr(config, "moe_routing", "token_choice")
+    problems = []
+    if not 1 <= E <= _lib.MAX_EXPERTS:
+        problems.append(f"n_experts={E} (supported: 1..{_lib.MAX_EXPERTS})")
+    if d <= 0 or d % 64:
+        problems.append(f"d_model={d} (supported: a positive multiple of 64)")
+    if routing != "expert_choice":
+        k = int(config.moe_top_k)
+        if not 1 <= k <= min(8, E):
+            problems.append(f"moe_top_k={k} (supported: 1..min(8, n_experts))")
+    if problems:
+        raise ValueError("kmoe.MoELayer: configuration outside the HIP kernels' range: " + "; ".join(problems))
+
+
 class MoELayer(nn.Module):
     """MoE feed-forward layer (moe.py:676-950) on the HIP kernels."""
 
@@ -591,6 +614,7 @@ class MoELayer(nn.Module):
         use_fp8 = bool(getattr(config, "moe_fp8", False))
         if use_fp8 and getattr(config, "ffn_activation", "swiglu") != "swiglu":
             raise NotImplementedError("kmoe: fp8 experts are implemented for swiglu only")
+        check_supported(config)
         if self.routing_type == "expert_choice":
             self.router = ExpertChoiceRouter(config)
             self.grouped_experts = None

@@ -64,6 +64,22 @@ def test_unsupported_modes_fail_loudly():
         MoELayer(AdvancedMoEConfig(d_model=128, ffn_activation="gelu", moe_fp8=True), 0)
 
 
+@pytest.mark.parametrize("kw, what", [
+    (dict(n_experts=164), "n_experts=164"),            # configs/1b_150m_active.yaml:26
+    (dict(d_model=1512, d_ff=4096, d_ff_expert=512), "d_model=1512"),  # configs/1b_150m_active.yaml:15
+    (dict(n_experts=8, moe_top_k=9), "moe_top_k=9"),
+    (dict(n_experts=4, moe_top_k=5), "moe_top_k=5"),
+    (dict(n_experts=65, moe_routing="expert_choice"), "n_experts=65"),
+])
+def test_out_of_range_configs_fail_at_construction(kw, what):
+    """Shapes the HIP kernels do not take are refused by MoELayer.__init__ with the
+    offending field named, not at the first forward inside the C ABI."""
+    with pytest.raises(ValueError, match=what):
+        MoELayer(AdvancedMoEConfig(**kw), 0)
+    # the limits themselves are accepted
+    MoELayer(AdvancedMoEConfig(d_model=128, d_ff_expert=256, n_experts=64, moe_top_k=8), 0)
+
+
 @pytest.mark.parametrize("routing", ["token_choice", "expert_choice"])
 def test_non_gated_expert_keys(routing):
     """An activation other than swiglu gives the reference's two-matrix experts
