@@ -15,6 +15,7 @@ timed in its own pass after the forward metric's timed region.
 """
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -458,7 +459,9 @@ def run_training(args, wl, layer, x):
 
 
 def run_cpu_baseline(wl, tokens):
-    """The op-for-op torch-CPU port of the reference path on a bounded sample."""
+    """The op-for-op torch-CPU port of the reference path on a bounded sample of
+    `tokens` tokens of workload `wl` (one sequence), fp32 (config 5: fp32 with e4m3
+    fake quantisation): 1 warm-up, median of 3."""
     import torch
     from kmoe import synth
     from oracle import torch_port as P
@@ -467,20 +470,49 @@ def run_cpu_baseline(wl, tokens):
     cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
     torch.set_num_threads(cores)
     wl32 = synth.Workload(wl.name, B=1, S=tokens, d=wl.d, E=wl.E, k=wl.k, F=wl.F, dtype=torch.float32,
-                          seed=wl.seed)
+                          seed=wl.seed, routing=wl.routing, capacity_factor=wl.capacity_factor,
+                          drop_overflow=wl.drop_overflow, zipf_bias=wl.zipf_bias, fp8=wl.fp8, mod=wl.mod,
+                          mod_cf=wl.mod_cf)
     t = synth.make_tensors(wl32, "cpu", tokens=tokens)
-    args = (t["x"], t["w_in"], t["w_out"], t["w1"], t["w2"], t["w3"])
+    x, w_in, w_out, w1, w2, w3 = t["x"], t["w_in"], t["w_out"], t["w1"], t["w2"], t["w3"]
+    if wl.mod:
+        w1q, w2q, w3q = P.fake_quant_expert_weights(w1, w2, w3)  # static weights: quantised once
+        keep = max(1, min(tokens, int(tokens * wl.mod_cf)))
+        fn = lambda: P.moe_layer_fp8_mod(x, t["w_mod"], w_in, w_out, w1q, w2q, w3q, wl.k, keep)
+        what = (f"MoD keep {keep} of {tokens}, token choice top-{wl.k} on the kept rows, e4m3 fake quantisation "
+                f"(float8_e4m3fn casts), oracle/torch_port.py moe_layer_fp8_mod")
+    elif wl.routing == "expert_choice":
+        fn = lambda: P.moe_layer_ec(x, w_in, w_out, w1, w2, w3, wl.capacity_factor)
+        what = (f"expert choice, C = ceil({tokens}*{wl.capacity_factor}/{wl.E}), oracle/torch_port.py moe_layer_ec "
+                f"(reference op sequence: gather, repeated-weight bmm, scatter_add_)")
+    elif wl.drop_overflow or wl.zipf_bias:
+        bias = torch.tensor(synth.zipf_bias(wl.E, wl.seed)) if wl.zipf_bias else None
+        x2d = x.reshape(tokens, wl.d)
+
+        def fn():
+            logits = torch.nn.functional.linear(torch.nn.functional.silu(torch.nn.functional.linear(x2d, w_in)),
+                                                w_out)
+            if bias is not None:
+                logits = logits + bias
+            idx = torch.topk(torch.softmax(logits, dim=-1), wl.k, dim=-1).indices
+            cap = int(math.ceil(tokens * wl.k / wl.E * wl.capacity_factor)) if wl.drop_overflow else 0
+            return P.moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity=cap, bias=bias, training=True)
+        what = (f"Zipf logit bias, capacity factor {wl.capacity_factor} with overflow dropped, "
+                f"oracle/torch_port.py moe_tc_routed (reference op sequence: padded bmm experts)")
+    else:
+        fn = lambda: P.moe_layer_tc(x, w_in, w_out, w1, w2, w3, wl.k, training=True)
+        what = "oracle/torch_port.py moe_layer_tc (reference op sequence: padded bmm experts)"
     times = []
     with torch.no_grad():
         for i in range(4):
             t0 = time.perf_counter()
-            P.moe_layer_tc(*args, wl.k, training=True)
+            fn()
             times.append(time.perf_counter() - t0)
     med = statistics.median(times[1:])
     return {"value": round(tokens / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
             "cpu_model": cpu_model(),
-            "sample": f"{tokens} tokens of the config-2 layer (d={wl.d}, E={wl.E}, top-{wl.k}, F={wl.F}), fp32, "
-                      f"oracle/torch_port.py (reference op sequence: padded bmm experts), median of 3 after 1 warm-up",
+            "sample": f"{tokens} tokens (one sequence) of {wl.name} (d={wl.d}, E={wl.E}, F={wl.F}), fp32, {what}; "
+                      f"median of 3 after 1 warm-up",
             "seconds_per_forward": round(med, 3)}
 
 
@@ -611,7 +643,12 @@ def main():
             wl_n = synth.WORKLOADS[n]
             out["configs"][f"cfg{n}"] = config_summary(wl_n, run_gpu(sub, wl_n, light=True), sub.steps)
     if not args.no_cpu:
-        out["cpu_baseline"] = run_cpu_baseline(synth.WORKLOADS[2], args.cpu_tokens)
+        out["cpu_baseline"] = run_cpu_baseline(synth.WORKLOADS[args.config], args.cpu_tokens)
+        if not args.no_configs:
+            # the other configurations, each on its own bounded sample (the GPU figures
+            # of the 'configs' object are on the full shapes)
+            out["cpu_baselines"] = {f"cfg{n}": run_cpu_baseline(synth.WORKLOADS[n], args.cpu_tokens)
+                                    for n in (2, 3, 4, 5) if n != args.config}
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

@@ -292,3 +292,52 @@ def router_loss_routed(x2d, w_in, w_out, idx, gw, gl):
     v = F.softmax(logits, dim=-1).gather(1, idx)
     w = v / v.sum(dim=-1, keepdim=True)
     return (w * gw).sum() + (logits * gl).sum()
+
+
+def _fake_e4m3_rows(m):
+    """Per-row e4m3 fake quantisation in fp32 (config 5's scheme, cast mechanics as
+    fp8_moe.py:112-125): scale = amax/448, clamp to +-448, float8_e4m3fn cast, back to
+    fp32 times the scale."""
+    amax = m.abs().amax(dim=-1, keepdim=True)
+    inv = torch.where(amax > 0, 448.0 / amax, torch.zeros_like(amax))
+    q = (m * inv).clamp(-448, 448).to(torch.float8_e4m3fn).to(torch.float32)
+    return q * (amax / 448.0)
+
+
+def fake_quant_expert_weights(w1, w2, w3):
+    """Expert weights with per-expert per-output-column e4m3 scales (the columns of w
+    (E, K, N) are the output rows of x @ w), dequantised to fp32."""
+    fq = lambda w: _fake_e4m3_rows(w.transpose(1, 2)).transpose(1, 2).contiguous()
+    return fq(w1), fq(w2), fq(w3)
+
+
+def moe_layer_fp8_mod(x3d, w_mod, w_in, w_out, w1q, w2q, w3q, k, keep):
+    """Config 5 forward: MoD selection of `keep` tokens per sequence (mod.py:93-112:
+    r = x w_mod, top-k over the sequence, indices sorted ascending, softmax over the kept
+    logits), the token-choice MoE on the gathered rows (moe.py:423-462 routing, the
+    padded-bmm experts of moe.py:213-294) with e4m3 fake quantisation (per-token scales
+    of x, per-output-row scales of the weights, pre-quantised in w1q/w2q/w3q, h
+    re-quantised per row before the down product), and the weighted scatter back
+    (layers.py:170-177).  fp32 arithmetic.  Returns the (B, S, d) output."""
+    B, S, d = x3d.shape
+    r = (x3d @ w_mod.reshape(-1, 1)).squeeze(-1)
+    sel = torch.topk(r, keep, dim=-1).indices.sort(dim=-1).values
+    p = F.softmax(r.gather(1, sel), dim=-1)
+    gidx = sel.unsqueeze(-1).expand(-1, -1, d)
+    rows = torch.gather(x3d, 1, gidx).reshape(-1, d)
+    w, idx, _ = router_tc(rows, w_in, w_out, k)
+    T = rows.shape[0]
+    flat_e = idx.reshape(-1)
+    tok = torch.arange(T).unsqueeze(1).expand(-1, k).reshape(-1)
+    order = torch.argsort(flat_e, stable=True)
+    s_tok, s_e, s_w = tok[order], flat_e[order], w.reshape(-1)[order]
+    counts = torch.bincount(flat_e, minlength=w1q.shape[0])
+    starts = torch.cumsum(counts, 0) - counts
+    pos = torch.arange(s_tok.numel()) - starts[s_e]
+    m = int(counts.max().item())
+    xq = _fake_e4m3_rows(rows)
+    padded = rows.new_zeros(w1q.shape[0], m, d).index_put((s_e, pos), xq[s_tok])
+    h = F.silu(torch.bmm(padded, w1q)) * torch.bmm(padded, w2q)
+    out = torch.bmm(_fake_e4m3_rows(h), w3q)
+    y = rows.new_zeros(T, d).index_add(0, s_tok, out[s_e, pos] * s_w.unsqueeze(1))
+    return torch.zeros_like(x3d).scatter_add(1, gidx, p.unsqueeze(-1) * y.view(B, keep, d))
