@@ -317,7 +317,7 @@ def moe_layer_fp8_mod(x3d, w_mod, w_in, w_out, w1q, w2q, w3q, k, keep):
     logits), the token-choice MoE on the gathered rows (moe.py:423-462 routing, the
     padded-bmm experts of moe.py:213-294) with e4m3 fake quantisation (per-token scales
     of x, per-output-row scales of the weights, pre-quantised in w1q/w2q/w3q, h
-    re-quantised per row before the down product), and the weighted scatter back
+    held in bf16 and re-quantised per row before the down product), and the weighted scatter back
     (layers.py:170-177).  fp32 arithmetic.  Returns the (B, S, d) output."""
     B, S, d = x3d.shape
     r = (x3d @ w_mod.reshape(-1, 1)).squeeze(-1)
@@ -338,6 +338,7 @@ def moe_layer_fp8_mod(x3d, w_mod, w_in, w_out, w1q, w2q, w3q, k, keep):
     xq = _fake_e4m3_rows(rows)
     padded = rows.new_zeros(w1q.shape[0], m, d).index_put((s_e, pos), xq[s_tok])
     h = F.silu(torch.bmm(padded, w1q)) * torch.bmm(padded, w2q)
-    out = torch.bmm(_fake_e4m3_rows(h), w3q)
+    # h is held in bf16 (the layer's activation dtype) before its re-quantisation
+    out = torch.bmm(_fake_e4m3_rows(h.to(torch.bfloat16).to(torch.float32)), w3q)
     y = rows.new_zeros(T, d).index_add(0, s_tok, out[s_e, pos] * s_w.unsqueeze(1))
     return torch.zeros_like(x3d).scatter_add(1, gidx, p.unsqueeze(-1) * y.view(B, keep, d))
