@@ -32,6 +32,7 @@ PEAK_BF16 = 2.5e15
 PEAK_FP8 = 5.0e15
 PEAK_HBM = 8.0e12
 EVENT_EVERY = 5  # timed forwards per sampled gate/up event pair
+NEAR_TIE = 2.0 ** -16  # router logit gap counted as a near-tie
 
 
 def parse():
@@ -129,6 +130,21 @@ def run_gpu(args, wl, light=False):
                 a_kept = int(counts.clamp(max=cap).sum())
             else:
                 a_kept = int(counts.sum())
+        # routing conditioning of this input: tokens whose k-th and (k+1)-th largest fp32
+        # logits are within NEAR_TIE of each other (there the top-k choice can flip under
+        # a different fp32 summation order of the router's dot products; exact ties go to
+        # the lower expert index)
+        near = None
+        if wl.routing != "expert_choice":
+            xr = x.reshape(wl.T, wl.d)
+            if wl.mod:
+                xr = xr[layer.ffn_mod_router.select(x).token_rows.long()]
+            lg = moe.router.route(xr).logits  # (with the logit bias, as the kernel routes on)
+            top = torch.topk(lg, wl.k + 1, dim=-1).values
+            gap = top[:, wl.k - 1] - top[:, wl.k]
+            near = {"tokens": int((gap <= NEAR_TIE).sum()), "exact_ties": int((gap == 0).sum()),
+                    "of": int(lg.shape[0]), "threshold": NEAR_TIE,
+                    "note": "tokens whose k-th and (k+1)-th largest router logits differ by at most the threshold"}
         # timed region: K back-to-back forwards; the only extra work on the stream is
         # a HIP event pair around the gate/up GEMM launch (the roofline kernel) on
         # every EVENT_EVERY-th forward (an event pair costs ~6 us of drain per event
@@ -199,7 +215,7 @@ def run_gpu(args, wl, light=False):
         block = run_block(args, wl, layer, x)
     del layer, t, x
     torch.cuda.empty_cache()
-    return dict(elapsed=elapsed, stages=stage_out, a_kept=a_kept, a_all=a_all, t_in=t_in, settle=settle,
+    return dict(elapsed=elapsed, stages=stage_out, a_kept=a_kept, a_all=a_all, t_in=t_in, settle=settle, near_ties=near,
                 gemm_us=statistics.mean(gu_timed) if gu_timed else float("nan"), gemm_samples=len(gu_timed),
                 work=work, rows_us=rows_us, training=training, block=block)
 
@@ -226,6 +242,8 @@ def config_summary(wl, res, steps):
         if name in st and "GBps" in st[name]:
             out[name] = {"us": st[name]["us"], "GBps": st[name]["GBps"], "frac_hbm": st[name]["frac_hbm"]}
     out["stages_us"] = {k: v["us"] for k, v in st.items()}
+    if res.get("near_ties") is not None:
+        out["near_ties"] = {k: v for k, v in res["near_ties"].items() if k != "note"}
     return out
 
 
@@ -625,6 +643,8 @@ def main():
                                         "layer gathers rows inside the gate/up GEMM instead"}
     if "combine" in res["stages"]:
         out["combine_GBps"] = res["stages"]["combine"].get("GBps")
+    if res.get("near_ties") is not None:
+        out["near_ties"] = res["near_ties"]
     if res.get("training"):
         out["training"] = res["training"]
     if res.get("block"):
