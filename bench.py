@@ -311,7 +311,7 @@ def run_block(args, wl, layer, x):
 def run_block_training(args, wl, layer, x, norm_w):
     """Training steps of the FFN half of the block through autograd (forward, then
     backward of sum(out * dy) + aux to h and every parameter), in training mode with
-    residual dropout 0: with the MoD router (the reference's default mod_enabled,
+    the default residual dropout 0.1: with the MoD router (the reference's default mod_enabled,
     layers.py:148-185) and without.  Gradients are set to None before each step (as an
     optimizer's zero_grad does); the parameters do not change, so the packed weights
     stay cached (with_repack: new parameter versions every step, as after an update)."""
@@ -328,7 +328,9 @@ def run_block_training(args, wl, layer, x, norm_w):
     one = torch.ones((), device=x.device)
     steps = max(1, args.steps // 5)
     for mod in (True, False):
-        cfg = dataclasses.replace(layer.config, mod_enabled=mod, residual_dropout=0.0)
+        # the reference's default residual dropout (config.py:87): the fused path applies
+        # its keep mask in the combine
+        cfg = dataclasses.replace(layer.config, mod_enabled=mod, residual_dropout=0.1)
         blk = MoEFFNBlock(cfg, 0, ffn=layer).to(x.device)
         blk.ffn_norm.weight = torch.nn.Parameter(norm_w.detach().clone())
         if mod:
@@ -378,7 +380,8 @@ def run_block_training(args, wl, layer, x, norm_w):
         del blk
     out["steps"] = steps
     out["note"] = ("autograd step of out = h + MoE(RMSNorm(h)) (MoD-gated: the kept tokens only, "
-                   "mod_capacity_factor 0.75), loss sum(out * dy) + aux, training mode, residual dropout 0")
+                   "mod_capacity_factor 0.75), loss sum(out * dy) + aux, training mode, residual dropout 0.1 "
+                   "(a fresh Bernoulli keep mask per step, applied in the combine)")
     return out
 
 

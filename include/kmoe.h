@@ -473,6 +473,16 @@ int kmoe_combine_residual(const void* yperm, int d, const int32_t* src_row, cons
                           const int32_t* out_map, const float* scale, const void* residual, int64_t T_out,
                           void* y, int y_dtype, void* stream);
 
+/* kmoe_combine_residual with the block's residual dropout (replaces residual +
+ * residual_dropout(ffn_output), moe_arch/model/layers.py:187-190, nn.Dropout(p) in
+ * training): y[o] = residual[o] + keep[o] * keep_scale * scale[s] sum_j w[s,j]
+ * yperm[src[s,j]], one rounding.  keep: (T_out, d) bytes, nonzero = kept (the
+ * Bernoulli(1-p) draw); keep_scale = 1/(1-p) >= 1.  residual and keep are required. */
+int kmoe_combine_residual_dropout(const void* yperm, int d, const int32_t* src_row, const float* src_w, int fan,
+                                  const int32_t* out_map, const float* scale, const void* residual,
+                                  const uint8_t* keep, float keep_scale, int64_t T_out, void* y, int y_dtype,
+                                  void* stream);
+
 
 #ifdef __cplusplus
 }

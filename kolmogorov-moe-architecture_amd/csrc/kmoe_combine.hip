@@ -11,20 +11,24 @@
 // in fp32 before the one rounding to y's dtype; rows without a source set
 // (out_map[o] < 0) get residual[o].  This is the residual add of the block's FFN half
 // (hidden_states = residual + ffn_output, layers.py:187) folded into the combine.
+// With a keep mask ((T_out, d) bytes, 0 or 1) the sum is the residual dropout's output:
+// y[o] = residual[o] + keep[o] * keep_scale * (the sum above), keep_scale = 1/(1-p)
+// (layers.py:190, residual + residual_dropout(ffn_output)), still one rounding.
 #include "kmoe_common.h"
 
 namespace {
 
 constexpr int CROWS = 4;  // rows (waves) per workgroup
 
-template <bool OUT_F32, bool RES = false>
+template <bool OUT_F32, bool RES = false, bool MASK = false>
 __global__ __launch_bounds__(64 * CROWS) void combine_kernel(const uint16_t* __restrict__ yperm, int d,
                                                              const int32_t* __restrict__ src_row,
                                                              const float* __restrict__ src_w, int fan,
                                                              const int32_t* __restrict__ out_map,
                                                              const float* __restrict__ scale, int64_t T_out,
                                                              void* __restrict__ y,
-                                                             const void* __restrict__ residual) {
+                                                             const void* __restrict__ residual,
+                                                             const uint8_t* __restrict__ keep, float keep_scale) {
   const int lane = threadIdx.x & 63;
   const int64_t o = (int64_t)blockIdx.x * CROWS + (threadIdx.x >> 6);
   if (o >= T_out) return;
@@ -118,6 +122,15 @@ __global__ __launch_bounds__(64 * CROWS) void combine_kernel(const uint16_t* __r
       float res[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) res[q] = 0.0f;
+      if constexpr (MASK) {
+        // the dropout keep factors of these 8 elements, folded into the accumulators
+        const uint2 kv = reinterpret_cast<const uint2*>(keep + o * d)[v];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const uint32_t byte = ((q < 4 ? kv.x : kv.y) >> (8 * (q & 3))) & 0xffu;
+          acc[u][q] *= byte ? keep_scale : 0.0f;
+        }
+      }
       if constexpr (RES) {
         if (OUT_F32) {
           const f32x4_t* rp = reinterpret_cast<const f32x4_t*>(static_cast<const float*>(residual) + o * d) + 2 * v;
@@ -161,14 +174,15 @@ __global__ __launch_bounds__(64 * CROWS) void combine_kernel(const uint16_t* __r
 // results are bit-identical; the straight-line form runs 37.8 -> 33.8 us at config 2
 // (the source loop's ballot / shuffle / bounds bookkeeping delayed the loads).
 constexpr int C2_D = 2048;
-template <bool RES = false>
+template <bool RES = false, bool MASK = false>
 __global__ __launch_bounds__(256) void combine2_kernel(const uint16_t* __restrict__ yperm,
                                                        const int32_t* __restrict__ src_row,
                                                        const float* __restrict__ src_w,
                                                        const int32_t* __restrict__ out_map,
                                                        const float* __restrict__ scale, int64_t T_out,
                                                        uint16_t* __restrict__ y,
-                                                       const uint16_t* __restrict__ residual) {
+                                                       const uint16_t* __restrict__ residual,
+                                                       const uint8_t* __restrict__ keep, float keep_scale) {
   constexpr int NV = C2_D / 8 / 64;  // 16-byte vectors per lane
   const int lane = threadIdx.x & 63;
   const int64_t o = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -192,11 +206,13 @@ __global__ __launch_bounds__(256) void combine2_kernel(const uint16_t* __restric
   const float w0 = __shfl(mw, 0, 64), w1 = __shfl(mw, 1, 64);
   const float sc = scale ? scale[s] : 1.0f;
   i32x4_t a[NV], b[NV], rr[RES ? NV : 1];
+  uint2 kv[MASK ? NV : 1];
 #pragma unroll
   for (int u = 0; u < NV; ++u) {
     a[u] = r0 >= 0 ? reinterpret_cast<const i32x4_t*>(yperm + (int64_t)r0 * C2_D)[u * 64 + lane] : i32x4_t{0, 0, 0, 0};
     b[u] = r1 >= 0 ? reinterpret_cast<const i32x4_t*>(yperm + (int64_t)r1 * C2_D)[u * 64 + lane] : i32x4_t{0, 0, 0, 0};
     if constexpr (RES) rr[u] = reinterpret_cast<const i32x4_t*>(residual + o * C2_D)[u * 64 + lane];
+    if constexpr (MASK) kv[u] = reinterpret_cast<const uint2*>(keep + o * C2_D)[u * 64 + lane];
   }
 #pragma unroll
   for (int u = 0; u < NV; ++u) {
@@ -217,6 +233,12 @@ __global__ __launch_bounds__(256) void combine2_kernel(const uint16_t* __restric
         rlo = __uint_as_float(((uint32_t)rr[u][q]) << 16);
         rhi = __uint_as_float(((uint32_t)rr[u][q]) & 0xffff0000u);
       }
+      if constexpr (MASK) {
+        // elements 2q and 2q+1 of this vector: bytes 2q, 2q+1 of the 8 keep bytes
+        const uint32_t w32 = q < 2 ? kv[u].x : kv[u].y;
+        lo *= ((w32 >> (16 * (q & 1))) & 0xffu) ? keep_scale : 0.0f;
+        hi *= ((w32 >> (16 * (q & 1) + 8)) & 0xffu) ? keep_scale : 0.0f;
+      }
       out[q] = (int)((uint32_t)f32_to_bf16(fmaf(lo, sc, rlo)) | ((uint32_t)f32_to_bf16(fmaf(hi, sc, rhi)) << 16));
     }
     dst[u * 64 + lane] = out;
@@ -225,15 +247,16 @@ __global__ __launch_bounds__(256) void combine2_kernel(const uint16_t* __restric
 
 }  // namespace
 
-extern "C" int kmoe_combine_residual(const void* yperm, int d, const int32_t* src_row, const float* src_w,
-                                     int fan, const int32_t* out_map, const float* scale, const void* residual,
-                                     int64_t T_out, void* y, int y_dtype, void* stream) {
-  KMOE_REQUIRE(yperm && src_row && src_w && y, KMOE_ERR_NULL, "kmoe_combine: null buffer");
-  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "kmoe_combine: d=%d must be a positive multiple of 64", d);
-  KMOE_REQUIRE(fan >= 1 && fan <= 64, KMOE_ERR_SHAPE, "kmoe_combine: fan=%d not in [1,64]", fan);
-  KMOE_REQUIRE(T_out >= 0, KMOE_ERR_SHAPE, "kmoe_combine: T_out < 0");
+namespace {
+int combine_launch(const char* who, const void* yperm, int d, const int32_t* src_row, const float* src_w, int fan,
+                   const int32_t* out_map, const float* scale, const void* residual, const uint8_t* keep,
+                   float keep_scale, int64_t T_out, void* y, int y_dtype, void* stream) {
+  KMOE_REQUIRE(yperm && src_row && src_w && y, KMOE_ERR_NULL, "%s: null buffer", who);
+  KMOE_REQUIRE(d > 0 && d % 64 == 0, KMOE_ERR_SHAPE, "%s: d=%d must be a positive multiple of 64", who, d);
+  KMOE_REQUIRE(fan >= 1 && fan <= 64, KMOE_ERR_SHAPE, "%s: fan=%d not in [1,64]", who, fan);
+  KMOE_REQUIRE(T_out >= 0, KMOE_ERR_SHAPE, "%s: T_out < 0", who);
   KMOE_REQUIRE(y_dtype == KMOE_DTYPE_BF16 || y_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE,
-               "kmoe_combine: y dtype must be bf16 or f32");
+               "%s: y dtype must be bf16 or f32", who);
   if (T_out == 0) return KMOE_OK;
   const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(T_out, CROWS));
   hipStream_t s = kmoe::as_stream(stream);
@@ -242,27 +265,54 @@ extern "C" int kmoe_combine_residual(const void* yperm, int d, const int32_t* sr
   uint16_t* y16 = static_cast<uint16_t*>(y);
   const uint16_t* r16 = static_cast<const uint16_t*>(residual);
   if (bf && fan == 2 && d == C2_D) {
-    if (residual)
-      hipLaunchKernelGGL(combine2_kernel<true>, grid, dim3(256), 0, s, yp, src_row, src_w, out_map, scale, T_out,
-                         y16, r16);
-    else
-      hipLaunchKernelGGL(combine2_kernel<false>, grid, dim3(256), 0, s, yp, src_row, src_w, out_map, scale, T_out,
-                         y16, r16);
-  } else {
-#define KMOE_COMBINE(F32_, RES_)                                                                                \
-  hipLaunchKernelGGL((combine_kernel<F32_, RES_>), grid, dim3(64 * CROWS), 0, s, yp, d, src_row, src_w, fan, \
-                     out_map, scale, T_out, y, residual)
-    if (bf && residual)
-      KMOE_COMBINE(false, true);
-    else if (bf)
-      KMOE_COMBINE(false, false);
+#define KMOE_COMBINE2(RES_, MASK_)                                                                             \
+  hipLaunchKernelGGL((combine2_kernel<RES_, MASK_>), grid, dim3(256), 0, s, yp, src_row, src_w, out_map, scale, \
+                     T_out, y16, r16, keep, keep_scale)
+    if (keep)
+      KMOE_COMBINE2(true, true);
     else if (residual)
-      KMOE_COMBINE(true, true);
+      KMOE_COMBINE2(true, false);
     else
-      KMOE_COMBINE(true, false);
+      KMOE_COMBINE2(false, false);
+#undef KMOE_COMBINE2
+  } else {
+#define KMOE_COMBINE(F32_, RES_, MASK_)                                                                            \
+  hipLaunchKernelGGL((combine_kernel<F32_, RES_, MASK_>), grid, dim3(64 * CROWS), 0, s, yp, d, src_row, src_w, fan, \
+                     out_map, scale, T_out, y, residual, keep, keep_scale)
+    if (bf && keep)
+      KMOE_COMBINE(false, true, true);
+    else if (bf && residual)
+      KMOE_COMBINE(false, true, false);
+    else if (bf)
+      KMOE_COMBINE(false, false, false);
+    else if (keep)
+      KMOE_COMBINE(true, true, true);
+    else if (residual)
+      KMOE_COMBINE(true, true, false);
+    else
+      KMOE_COMBINE(true, false, false);
 #undef KMOE_COMBINE
   }
-  return kmoe::check_launch("kmoe_combine");
+  return kmoe::check_launch(who);
+}
+}  // namespace
+
+extern "C" int kmoe_combine_residual(const void* yperm, int d, const int32_t* src_row, const float* src_w,
+                                     int fan, const int32_t* out_map, const float* scale, const void* residual,
+                                     int64_t T_out, void* y, int y_dtype, void* stream) {
+  return combine_launch("kmoe_combine", yperm, d, src_row, src_w, fan, out_map, scale, residual, nullptr, 1.0f,
+                        T_out, y, y_dtype, stream);
+}
+
+extern "C" int kmoe_combine_residual_dropout(const void* yperm, int d, const int32_t* src_row, const float* src_w,
+                                             int fan, const int32_t* out_map, const float* scale,
+                                             const void* residual, const uint8_t* keep, float keep_scale,
+                                             int64_t T_out, void* y, int y_dtype, void* stream) {
+  KMOE_REQUIRE(residual && keep, KMOE_ERR_NULL, "kmoe_combine_residual_dropout: null residual / keep mask");
+  KMOE_REQUIRE(keep_scale >= 1.0f, KMOE_ERR_SHAPE,
+               "kmoe_combine_residual_dropout: keep_scale=%g must be 1/(1-p) >= 1", (double)keep_scale);
+  return combine_launch("kmoe_combine_residual_dropout", yperm, d, src_row, src_w, fan, out_map, scale, residual,
+                        keep, keep_scale, T_out, y, y_dtype, stream);
 }
 
 extern "C" int kmoe_combine(const void* yperm, int d, const int32_t* src_row, const float* src_w, int fan,

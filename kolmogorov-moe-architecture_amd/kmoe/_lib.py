@@ -69,6 +69,8 @@ _SIGNATURES = {
     "kmoe_router_rms": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _f32, _vp, _vp]),
     "kmoe_gemm_gate_up_rows_scaled": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp]),
     "kmoe_combine_residual": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _vp, _i32, _vp]),
+    "kmoe_combine_residual_dropout": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _f32, _i64, _vp, _i32,
+                                             _vp]),
     "kmoe_combine_bwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp]),
     "kmoe_combine_bwd_rows": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_mod_bwd_workspace_bytes": (_sz, [_i64, _i32]),

@@ -19,8 +19,8 @@ gradients, runs the whole expression on the layer's kernels with no extra pass:
   before the SiLU.  The normalised activations are never written.
 * The residual add happens in the combine (one f32 add before the one rounding).
 
-With gradients (training) and an RMSNorm, a token-choice bf16 layer and no active
-residual dropout, the block runs _BlockTrainFn: kmoe_rmsnorm writes the normalised
+With gradients (training) and an RMSNorm and a token-choice bf16 layer, the block
+runs _BlockTrainFn: kmoe_rmsnorm writes the normalised
 rows once (the saved activation the weight gradients need; folding the norm weight
 into the expert weights would cost a re-fold of both weight packs every step), the
 layer's training forward (MoD-gated when the block has a MoD router and is in
@@ -28,9 +28,11 @@ training mode, layers.py:148-177) adds the residual in its combine, and the back
 is the layer's (or the MoD composition's) HIP backward followed by kmoe_rmsnorm_bwd,
 which also adds the residual's gradient.
 
-Other configurations (layernorm, expert choice, fp8, active residual dropout) run
-the unfused composition: the reference's RMSNorm / LayerNorm in torch, the kmoe MoE
-layer (MoD-gated in training mode, with its HIP backward where it has one) and a
+With residual dropout active (training, p > 0) the keep mask is one Bernoulli(1-p)
+draw per call (the block's keep_mask_fn) and is applied in the combine, before the
+residual add; its backward scales the MoE's output gradient by the same mask.
+Other configurations (layernorm, expert choice, fp8) run the unfused composition:
+the reference's RMSNorm / LayerNorm in torch, the kmoe MoE layer (MoD-gated in training mode, with its HIP backward where it has one) and a
 torch add.  In training mode the MoD router's auxiliary BCE loss (mod.py:114-171) is
 added to aux_loss on the fused path as on the unfused one (MoDRouter.aux).
 """
@@ -69,6 +71,11 @@ def get_norm_layer(config) -> nn.Module:
     raise ValueError(f"Unknown norm type: {norm_type}")
 
 
+def _bernoulli_keep(shape, device, p):
+    """Keep mask of nn.Dropout(p): True with probability 1-p (torch's generator)."""
+    return torch.empty(shape, device=device, dtype=torch.bool).bernoulli_(1.0 - p)
+
+
 class MoEFFNBlock(nn.Module):
     """out = h + residual_dropout(MoE(ffn_norm(h))): the FFN half of
     TransformerBlock.forward (layers.py:142-147 pre-norm, 184-191 residual and aux)."""
@@ -82,6 +89,9 @@ class MoEFFNBlock(nn.Module):
         # the MoD router of the FFN (layers.py:84-88), used in training mode only
         self.ffn_mod_router = MoDRouter(config) if getattr(config, "mod_enabled", False) else None
         self.residual_dropout = nn.Dropout(getattr(config, "residual_dropout", 0.1))
+        # keep-mask source of the fused paths' residual dropout: (shape, device, p) -> bool
+        # tensor, True where kept (replaceable, e.g. by a test that fixes the mask)
+        self.keep_mask_fn = _bernoulli_keep
         self.aux_loss = 0.0
         self._fused_cache = None
         # which path the last forward took ("fused" or "unfused")
@@ -93,11 +103,18 @@ class MoEFFNBlock(nn.Module):
             return False
         if ffn.grouped_experts.use_fp8 or ffn.router.balanced_routing or not ffn.grouped_experts.gated:
             return False
-        if self.training and self.residual_dropout.p > 0:
-            return False
         if torch.is_grad_enabled() and (h.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
         return torch.promote_types(h.dtype, self.ffn_norm.weight.dtype) in (torch.bfloat16, torch.float32)
+
+    def _dropout_keep(self, T, d, device):
+        """(keep mask or None, 1/(1-p)) of this forward's residual dropout."""
+        p = float(self.residual_dropout.p)
+        if not self.training or p <= 0.0:
+            return None, 1.0
+        if p >= 1.0:
+            return torch.zeros(T, d, device=device, dtype=torch.bool), 1.0
+        return self.keep_mask_fn((T, d), device, p), 1.0 / (1.0 - p)
 
     def _fused_weights(self):
         """Router w_in and packed w1/w2/w3 with the norm weight folded in (cached per version)."""
@@ -128,7 +145,7 @@ class MoEFFNBlock(nn.Module):
             return False
         if not isinstance(self.ffn_norm, RMSNorm) or ffn.routing_type == "expert_choice":
             return False
-        if not ffn._trainable_experts() or (self.training and self.residual_dropout.p > 0):
+        if not ffn._trainable_experts():
             return False
         return h.dtype in (torch.bfloat16, torch.float32) and self.ffn_norm.weight.dtype in (torch.bfloat16,
                                                                                                torch.float32)
@@ -178,15 +195,16 @@ class MoEFFNBlock(nn.Module):
         disp = ops.dispatch(xb, r.idx, r.w, E, capacity=cap, materialize=False)
         hbuf = ops.gemm_gate_up_rows(xb, None, disp.row_token, disp.offsets, pw, T * k, rscale=r.rscale)
         yperm = ops.gemm_down(hbuf, None, disp.offsets, pw, T * k)
+        keep, keep_scale = self._dropout_keep(T, d, h.device)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T, out_dtype=out_dtype,
-                        residual=x2d)
+                        residual=x2d, keep_mask=keep, keep_scale=keep_scale)
         ffn._set_token_choice_aux(r, disp, T)
         return y.view(B, S, d)
 
 
 class _BlockTrainFn(torch.autograd.Function):
-    """out = h + MoE(RMSNorm(h)) (MoD-gated when use_mod, layers.py:142-187 without
-    residual dropout) with its backward on the HIP kernels.  Outputs (out, aux)."""
+    """out = h + residual_dropout(MoE(RMSNorm(h))) (MoD-gated when use_mod,
+    layers.py:142-190) with its backward on the HIP kernels.  Outputs (out, aux)."""
 
     @staticmethod
     def forward(ctx, h, g, w_mod, w_in, w_out, w1, w2, w3, blk, use_mod):
@@ -200,15 +218,17 @@ class _BlockTrainFn(torch.autograd.Function):
         out_dtype = torch.promote_types(h.dtype, g.dtype)
         sel = None
         keep = 0
+        kmask, kscale = blk._dropout_keep(T, d, h.device)
         if use_mod:
             sel = blk.ffn_mod_router.select(n.view(B, S, d), logits=mod_logits)
             keep = sel.sel_idx.shape[1]
             x_sel, _ = ops.gather_rows(n, sel.token_rows, B * keep)
             y, aux, sv = ffn._train_forward(x_sel, B * keep, out_dtype, out_map=sel.out_map,
-                                            scale=sel.sel_w.reshape(-1), residual=h2d, T_out=T)
+                                            scale=sel.sel_w.reshape(-1), residual=h2d, T_out=T, keep_mask=kmask,
+                                            keep_scale=kscale)
         else:
-            y, aux, sv = ffn._train_forward(n, T, out_dtype, residual=h2d)
-        ctx.sv = (sv, sel, h2d, rrms)
+            y, aux, sv = ffn._train_forward(n, T, out_dtype, residual=h2d, keep_mask=kmask, keep_scale=kscale)
+        ctx.sv = (sv, sel, h2d, rrms, kmask, kscale)
         ctx.blk = blk
         ctx.meta = (B, S, d, keep, h.dtype, aux is not None, use_mod)
         aux_t = aux if aux is not None else torch.zeros((), device=h.device, dtype=torch.float32)
@@ -219,7 +239,7 @@ class _BlockTrainFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy, daux, dn, drows):
-        sv, sel, h2d, rrms = _once(ctx)
+        sv, sel, h2d, rrms, kmask, kscale = _once(ctx)
         blk = ctx.blk
         B, S, d, keep, h_dtype, has_aux, use_mod = ctx.meta
         T = B * S
@@ -229,17 +249,20 @@ class _BlockTrainFn(torch.autograd.Function):
         need_w = any(ctx.needs_input_grad[2:8])
         dy2 = dy.reshape(T, d)
         ga = daux if has_aux else None
+        # the MoE output's gradient through the residual dropout; the residual's own
+        # gradient (dres below) is dy
+        dffn = dy2 if kmask is None else (dy2 * kmask.to(dy2.dtype)) * kscale
         dw_mod = None
         if use_mod:
             w_mod = blk.ffn_mod_router.router.weight
-            mg = _bwd.mod_backward(sv, sel, B, keep, dy2, ga, w_out, w_mod, ffn._bwd_weights(), ffn.n_experts,
+            mg = _bwd.mod_backward(sv, sel, B, keep, dffn, ga, w_out, w_mod, ffn._bwd_weights(), ffn.n_experts,
                                    ge.d_ff, ffn.load_balance_loss_weight, ffn.router_z_loss_weight,
                                    need_weights=need_w)
             dn, lg = mg.dx, mg.layer
             if need_w:
                 dw_mod = mg.dw_mod.view_as(w_mod).to(w_mod.dtype)
         else:
-            lg = _bwd.moe_backward(sv, dy2, ga, w_out, ffn._bwd_weights(), ffn.n_experts, ge.d_ff,
+            lg = _bwd.moe_backward(sv, dffn, ga, w_out, ffn._bwd_weights(), ffn.n_experts, ge.d_ff,
                                    ffn.load_balance_loss_weight, ffn.router_z_loss_weight, need_weights=need_w)
             dn = lg.dx
         # the norm's backward, plus the residual's gradient dy

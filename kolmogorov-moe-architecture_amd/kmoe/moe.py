@@ -671,10 +671,12 @@ class MoELayer(nn.Module):
             self._bwd_cache = cache
         return cache[1]
 
-    def _train_forward(self, x2d, T, out_dtype, out_map=None, scale=None, residual=None, T_out=None):
+    def _train_forward(self, x2d, T, out_dtype, out_map=None, scale=None, residual=None, T_out=None,
+                       keep_mask=None, keep_scale=1.0):
         """Token-choice forward keeping what the backward needs: (y, aux or None, Saved).
-        out_map / scale / residual / T_out go to the combine (the MoD scatter and the
-        block's residual add): y[o] = residual[o] + scale[t] * MoE(x)[t] for t = out_map[o]."""
+        out_map / scale / residual / T_out / keep_mask go to the combine (the MoD scatter,
+        the block's residual add and residual dropout): y[o] = residual[o] +
+        keep[o] keep_scale scale[t] MoE(x)[t] for t = out_map[o]."""
         r = self.router.route(x2d, T=T, save_hidden=True)
         ge = self.grouped_experts
         k, E = self.top_k, self.n_experts
@@ -686,7 +688,8 @@ class MoELayer(nn.Module):
                             aux=aux_in)
         yperm, h, gu = ge.expert_rows(x2d, disp.row_token, disp.offsets, T * k, xperm=disp.xperm, save=True)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T if T_out is None else T_out,
-                        out_map=out_map, scale=scale, out_dtype=out_dtype, residual=residual)
+                        out_map=out_map, scale=scale, out_dtype=out_dtype, residual=residual, keep_mask=keep_mask,
+                        keep_scale=keep_scale)
         self.last_expert_counts = disp.counts
         aux = None
         if self.training:

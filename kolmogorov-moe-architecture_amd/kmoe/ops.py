@@ -428,9 +428,12 @@ def grouped_ffn(xperm, xscale, offsets, pw: PackedWeights, max_rows):
     return gemm_down(h, None, offsets, pw, max_rows)
 
 
-def combine(yperm, src_row, src_w, T_out, out_map=None, scale=None, out_dtype=_BF16, residual=None):
+def combine(yperm, src_row, src_w, T_out, out_map=None, scale=None, out_dtype=_BF16, residual=None,
+            keep_mask=None, keep_scale=1.0):
     """y[o] = scale[s] * sum_j src_w[s,j] * yperm[src_row[s,j]] (moe.py:285-292, 132-158),
-    plus residual[o] ((T_out, d), cast to out_dtype) when given (layers.py:187)."""
+    plus residual[o] ((T_out, d), cast to out_dtype) when given (layers.py:187).
+    keep_mask ((T_out, d) bool, with a residual): the residual dropout, the sum times
+    keep_scale = 1/(1-p) where kept and 0 elsewhere (layers.py:190)."""
     fan = src_row.shape[1]
     d = yperm.shape[1]
     y = torch.empty(T_out, d, device=yperm.device, dtype=out_dtype)
@@ -439,6 +442,18 @@ def combine(yperm, src_row, src_w, T_out, out_map=None, scale=None, out_dtype=_B
         residual = _contig(residual, out_dtype)
         if residual.shape != (T_out, d):
             raise ValueError(f"kmoe.combine: residual shape {tuple(residual.shape)} != {(T_out, d)}")
+    if keep_mask is not None:
+        if residual is None:
+            raise ValueError("kmoe.combine: a dropout keep mask needs the residual")
+        if keep_mask.shape != (T_out, d) or keep_mask.dtype not in (torch.bool, torch.uint8):
+            raise ValueError(f"kmoe.combine: keep_mask must be bool/uint8 {(T_out, d)}, got "
+                             f"{keep_mask.dtype} {tuple(keep_mask.shape)}")
+        keep_mask = keep_mask.contiguous()
+        with _Stage("combine"):
+            _lib.call("kmoe_combine_residual_dropout", ptr(yperm), d, ptr(src_row), ptr(src_w), fan, ptr(out_map),
+                      ptr(scale), ptr(residual), ptr(keep_mask), float(keep_scale), T_out, ptr(y), ydt,
+                      _stream(yperm))
+        return y
     with _Stage("combine"):
         _lib.call("kmoe_combine_residual", ptr(yperm), d, ptr(src_row), ptr(src_w), fan, ptr(out_map), ptr(scale),
                   ptr(residual), T_out, ptr(y), ydt, _stream(yperm))

@@ -157,10 +157,12 @@ def moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity=0, bias=None, trai
 
 
 def ffn_half_loss_routed(h3d, w_in, w_out, w1, w2, w3, idx, dy, norm_w=None, eps=1e-5, w_mod=None, sel_idx=None,
-                         residual=None, capacity=0, training=True, w_lb=0.01, w_z=0.001, return_out=False):
+                         residual=None, capacity=0, training=True, w_lb=0.01, w_z=0.001, return_out=False,
+                         drop_keep=None, p_drop=0.0):
     """Scalar loss sum(out * dy) (+ the MoE aux in training) of the FFN half of
-    TransformerBlock.forward (layers.py:142-187, no residual dropout) at a fixed MoD
-    selection and routing:
+    TransformerBlock.forward (layers.py:142-190) at a fixed MoD selection, routing and
+    residual-dropout mask (drop_keep (B, S, d) bool, nn.Dropout's output = input *
+    drop_keep * (1 / (1 - p_drop)); None: no dropout):
       x = RMSNorm(h) (embeddings.py:182-195) when norm_w is given, else h
       MoD (w_mod and sel_idx (B, keep) ascending given; layers.py:148-184): router
         logits x . w_mod (mod.py:93), the kept logits in ascending token order
@@ -168,8 +170,8 @@ def ffn_half_loss_routed(h3d, w_in, w_out, w1, w2, w3, idx, dy, norm_w=None, eps
         (layers.py:160-165), the MoE on them with routing idx (B*keep, k), weight by
         the softmax (layers.py:175), scatter_add_ into zeros (layers.py:180-184)
       no MoD: the MoE on all rows with routing idx (B*S, k)
-      out = h + ffn_output with a norm (layers.py:187), else residual + ffn_output
-        (residual optional).
+      out = h + dropout(ffn_output) with a norm (layers.py:187-190), else
+        residual + dropout(ffn_output) (residual optional).
     At a fixed selection and routing the composition is smooth: autograd of this loss
     is the reference's backward.  return_out: (loss, out)."""
     B, S, d = h3d.shape
@@ -190,6 +192,8 @@ def ffn_half_loss_routed(h3d, w_in, w_out, w1, w2, w3, idx, dy, norm_w=None, eps
         y, aux = moe_tc_routed(x.reshape(B * S, d), w_in, w_out, w1, w2, w3, idx, capacity, None, training, w_lb,
                                w_z)
         ffn_out = y.view(B, S, d)
+    if drop_keep is not None:
+        ffn_out = ffn_out * drop_keep.to(ffn_out.dtype) * (1.0 / (1.0 - p_drop))
     base = h3d if norm_w is not None else residual
     out = ffn_out if base is None else base + ffn_out
     loss = (out * dy).sum() + aux

@@ -91,6 +91,15 @@ def test_gemm_and_combine_validation(lib):
                 NULL)[0] == -3
     assert _err(lib, "kmoe_pack_weights", FAKE, FAKE, FAKE, _lib.DTYPE_BF16, 4, 64, 64, _lib.DTYPE_FP8_E4M3,
                 FAKE, NULL, FAKE, NULL, NULL)[0] == -1
+    # the residual-dropout combine: residual and keep mask required, keep_scale = 1/(1-p) >= 1
+    rc, msg = _err(lib, "kmoe_combine_residual_dropout", FAKE, 64, FAKE, FAKE, 2, NULL, NULL, FAKE, NULL, 1.25, 4,
+                   FAKE, _lib.DTYPE_BF16, NULL)
+    assert rc == -1 and "keep" in msg
+    rc, msg = _err(lib, "kmoe_combine_residual_dropout", FAKE, 64, FAKE, FAKE, 2, NULL, NULL, FAKE, FAKE, 0.5, 4,
+                   FAKE, _lib.DTYPE_BF16, NULL)
+    assert rc == -2 and "keep_scale" in msg
+    assert _err(lib, "kmoe_combine_residual_dropout", FAKE, 60, FAKE, FAKE, 2, NULL, NULL, FAKE, FAKE, 1.25, 4,
+                FAKE, _lib.DTYPE_BF16, NULL)[0] == -2
 
 
 def test_select_validation(lib):

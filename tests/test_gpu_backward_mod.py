@@ -198,19 +198,27 @@ def test_mod_aux_router_loss(dev, path):
 
 
 # ------------------------------------------------------------------ the block in training
-@pytest.mark.parametrize("mod,norm_dtype,h_dtype", [
-    (False, torch.float32, BF),
-    (True, torch.float32, BF),
-    (True, BF, BF),
-    (True, torch.float32, torch.float32),
+@pytest.mark.parametrize("mod,norm_dtype,h_dtype,p_drop", [
+    (False, torch.float32, BF, 0.0),
+    (True, torch.float32, BF, 0.0),
+    (True, BF, BF, 0.0),
+    (True, torch.float32, torch.float32, 0.0),
+    (False, torch.float32, BF, 0.1),   # the reference's default residual_dropout (config.py:87)
+    (True, torch.float32, BF, 0.1),
+    (False, torch.float32, torch.float32, 0.5),
 ])
-def test_block_training_backward(dev, mod, norm_dtype, h_dtype):
+def test_block_training_backward(dev, mod, norm_dtype, h_dtype, p_drop):
     B, S, d, E, k, F_ = 2, 256, 256, 8, 2, 352
-    print(f"block training mod={mod} norm={norm_dtype} h={h_dtype}", flush=True)
+    print(f"block training mod={mod} norm={norm_dtype} h={h_dtype} p={p_drop}", flush=True)
     cfg = AdvancedMoEConfig(d_model=d, n_experts=E, moe_top_k=k, d_ff_expert=F_, mod_enabled=mod,
-                            mod_capacity_factor=0.75, residual_dropout=0.0)
+                            mod_capacity_factor=0.75, residual_dropout=p_drop)
     blk = MoEFFNBlock(cfg, 0).to(dev, BF).train()
     g = torch.Generator().manual_seed(410 + int(mod))
+    drop_keep = None
+    if p_drop > 0:
+        # a fixed keep mask, drawn on the CPU: the fused path applies it in the combine
+        drop_keep = torch.rand(B * S, d, generator=torch.Generator().manual_seed(77)) >= p_drop
+        blk.keep_mask_fn = lambda shape, device, p: drop_keep.to(device)
     _init_ffn(blk.ffn, g, d, E)
     blk.ffn_norm.weight = torch.nn.Parameter((1.0 + 0.3 * torch.randn(d, generator=g)).to(dev, norm_dtype))
     if mod:
@@ -245,7 +253,9 @@ def test_block_training_backward(dev, mod, norm_dtype, h_dtype):
     loss, ref = P.ffn_half_loss_routed(h64, *p64[:5], idx, dy.double(), norm_w=p64[5], eps=blk.ffn_norm.eps,
                                        w_mod=p64[6] if mod else None, sel_idx=None if sel is None else
                                        sel.sel_idx.cpu(), w_lb=ffn.load_balance_loss_weight,
-                                       w_z=ffn.router_z_loss_weight, return_out=True)
+                                       w_z=ffn.router_z_loss_weight, return_out=True,
+                                       drop_keep=None if drop_keep is None else drop_keep.view(B, S, d),
+                                       p_drop=p_drop)
     loss.backward()
     hd = h.detach().double().cpu()
     # an f32 output carries the MoE part exactly; a bf16 one rounds h + MoE part
@@ -256,18 +266,27 @@ def test_block_training_backward(dev, mod, norm_dtype, h_dtype):
     _check(errs)
 
 
-def test_block_dropout_trains_unfused(dev):
-    """Active residual dropout keeps the unfused composition (torch dropout), whose MoE
-    part still trains on the HIP kernels (MoD-gated in training mode)."""
-    print("block dropout", flush=True)
-    cfg = AdvancedMoEConfig(d_model=256, n_experts=8, d_ff_expert=352, residual_dropout=0.1)
+def test_block_dropout_mask_statistics(dev):
+    """Active residual dropout trains on the fused path with a fresh Bernoulli(1-p) mask
+    per call: the dropped elements of out - h are exactly 0, the kept fraction is 1-p,
+    and two calls draw different masks."""
+    print("block dropout mask", flush=True)
+    cfg = AdvancedMoEConfig(d_model=256, n_experts=8, d_ff_expert=352, residual_dropout=0.25, mod_enabled=False)
     blk = MoEFFNBlock(cfg, 0).to(dev, BF).train()
-    h = torch.randn(2, 128, 256, device=dev).to(BF).requires_grad_(True)
-    out = blk(h)
-    assert blk.last_path == "unfused"
-    out.float().sum().backward()
+    blk.ffn_norm.to(torch.float32)
+    # f32 h and norm weight: out is f32, so out - h is the dropped-out MoE part exactly
+    h = torch.randn(2, 512, 256, device=dev).requires_grad_(True)
+    outs = []
+    for _ in range(2):
+        out = blk(h)
+        assert blk.last_path == "fused_train"
+        outs.append((out.float() - h.detach().float()) != 0)
+        out.float().sum().backward()
+    kept = outs[0].float().mean().item()
+    assert abs(kept - 0.75) < 0.01, kept
+    assert (outs[0] != outs[1]).float().mean().item() > 0.2
     assert h.grad is not None and torch.isfinite(h.grad.float()).all()
-    assert blk.ffn.grouped_experts.w1.grad is not None and blk.ffn_mod_router.router.weight.grad is not None
+    assert blk.ffn.grouped_experts.w1.grad is not None
 
 
 # ------------------------------------------------------------------ kernels

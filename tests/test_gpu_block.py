@@ -150,6 +150,47 @@ def test_combine_residual_top2_path(dev):
     assert np.all(np.abs(npf(a) - ref) <= np.abs(ref) * 2.0 ** -8 + mag * 2.0 ** -22)
 
 
+@pytest.mark.parametrize("T,fan,d,out_f32", [(1000, 3, 384, False), (1000, 3, 384, True), (3000, 2, 2048, False)])
+def test_combine_residual_dropout(dev, T, fan, d, out_f32):
+    """kmoe_combine_residual_dropout at a fixed keep mask: residual + keep * (1/(1-p)) *
+    the weighted sum, one rounding; rows without a source set are the residual; with an
+    all-kept mask and keep_scale 1 it equals kmoe_combine_residual bit for bit (the
+    two-source and the generic kernel)."""
+    print(f"combine_residual_dropout T={T} fan={fan} d={d} f32={out_f32}", flush=True)
+    g = torch.Generator().manual_seed(222 + fan)
+    R = 2 * T
+    yperm = bf(torch.randn(R, d, generator=g))
+    src = torch.randint(-1, R, (T, fan), generator=g).to(torch.int32)
+    w = torch.rand(T, fan, generator=g)
+    out_map = torch.randint(-1, T, (T + 50,), generator=g).to(torch.int32)
+    odt = torch.float32 if out_f32 else torch.bfloat16
+    res = (torch.randn(T + 50, d, generator=g) * 2.0).to(odt)
+    p = 0.3
+    keep = torch.rand(T + 50, d, generator=g) >= p
+    args = (yperm.to(dev), src.to(dev), w.to(dev), T + 50)
+    y = ops.combine(*args, out_map=out_map.to(dev), out_dtype=odt, residual=res.to(dev), keep_mask=keep.to(dev),
+                    keep_scale=1.0 / (1.0 - p))
+    torch.cuda.synchronize()
+    comb = O.combine(npf(yperm), src.numpy(), w.numpy(), out_map=out_map.numpy(), T_out=T + 50)
+    ref = npf(res).astype(np.float64) + keep.numpy() * comb / (1.0 - p)
+    got = npf(y)
+    empty = out_map.numpy() < 0
+    assert np.array_equal(got[empty], npf(res)[empty])
+    # dropped elements are the residual exactly
+    assert np.array_equal(got[~keep.numpy()], npf(res)[~keep.numpy()])
+    mag = O.combine(np.abs(npf(yperm)), src.numpy(), w.numpy(), out_map=out_map.numpy(), T_out=T + 50) / (1 - p) \
+        + np.abs(npf(res))
+    tol = (2.0 ** -23 if out_f32 else 2.0 ** -8) * np.abs(ref) + mag * 2.0 ** -21
+    assert np.all(np.abs(got - ref) <= tol)
+    # all kept, scale 1: the plain residual combine's bits
+    a = ops.combine(*args, out_map=out_map.to(dev), out_dtype=odt, residual=res.to(dev),
+                    keep_mask=torch.ones(T + 50, d, dtype=torch.bool, device=dev), keep_scale=1.0)
+    b = ops.combine(*args, out_map=out_map.to(dev), out_dtype=odt, residual=res.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16) if not out_f32 else a.view(torch.int32),
+                       b.view(torch.int16) if not out_f32 else b.view(torch.int32))
+
+
 # ------------------------------------------------------------------ the block
 def _block(dev, d, E, k, Fd, seed, norm_dtype, cap=None):
     cfg = AdvancedMoEConfig(d_model=d, n_experts=E, moe_top_k=k, d_ff_expert=Fd,

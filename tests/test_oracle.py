@@ -858,3 +858,18 @@ def test_fp8_mod_port_matches_numpy_oracle():
     for b in range(B):
         mask[b, sel[b]] = True
     assert np.all(got[~mask] == 0) and np.all(np.abs(got[mask]).sum(-1) > 0)
+
+
+def test_dropout_keep_convention_matches_torch():
+    """ffn_half_loss_routed's residual dropout (ffn_out * keep * (1 / (1 - p)), layers.py:190)
+    against nn.functional.dropout itself: the mask read off torch's output reproduces it
+    exactly; the block's output is residual + that."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(4, 33, 16, generator=g, dtype=torch.float64) + 3.0  # no exact zeros
+    for p in (0.1, 0.5):
+        torch.manual_seed(123)
+        out = F.dropout(x, p=p, training=True)
+        keep = out != 0
+        assert 0 < keep.double().mean().item() < 1
+        assert torch.equal(x * keep.to(x.dtype) * (1.0 / (1.0 - p)), out)
+        # (dividing by 1 - p instead differs in the last bit: the reciprocal is the convention)
