@@ -288,6 +288,32 @@ int kmoe_gemm_gate_up_rows_gu(const void* x, const int32_t* row_index, int64_t n
                               const int32_t* row_token, const int32_t* offsets, int E, int d, int F,
                               int64_t max_rows, const void* w13_packed, void* h, void* gu, void* stream);
 
+/* kmoe_gemm_gate_up on fp8 e4m3 rows (xperm codes with per-row scales, w13 packed
+ * fp8 with per-column scales) that also writes g and u to gu (max_rows, 2*F_pad)
+ * bf16 in the same packed column order, descaled (the values h's SwiGLU took): the
+ * straight-through backward of the fp8 experts, whose gradients flow through the
+ * dequantised operands as autograd of the fake-quantised forward gives them
+ * (fp8_moe.py:179-279 computes its experts in the scaled domain and is
+ * differentiated by autograd).  d % 128 == 0.                                  */
+int kmoe_gemm_gate_up_fp8_gu(const void* xperm, const float* xperm_scale, const int32_t* offsets, int E, int d,
+                             int F, int64_t max_rows, const void* w13_packed, const float* w13_scale, void* h,
+                             void* gu, void* stream);
+
+/* Dequantised fp8 rows for the straight-through backward's weight gradients:
+ * out[r, :] = bf16(e4m3(q[r, :]) * scale[r]) (out (rows, cols) bf16) for rows r <
+ * min(rows, *n_rows_dev) (n_rows_dev nullable).  cols % 8 == 0.  The fake-quantised
+ * x and h of the reference's fp8 experts (fp8_moe.py:225-271) as this build's fp8
+ * GEMMs take them.                                                            */
+int kmoe_dequant_rows_fp8(const uint8_t* q, const float* scale, int64_t rows, const int32_t* n_rows_dev, int cols,
+                          void* out, void* stream);
+
+/* w (E, K, N) (bf16 or f32) fake-quantised per output column of each expert as
+ * kmoe_pack_weights(fp8) quantises it (scale = column amax / 448, e4m3 codes,
+ * saturating, nearest even), dequantised to out (E, K, N) bf16: the weights the
+ * fp8 GEMMs multiplied (fp8_moe.py:171-177, 236-268 scale the whole matrix; this
+ * build scales each column).                                                  */
+int kmoe_fake_quant_e4m3_cols(const void* w, int w_dtype, int E, int K, int N, void* out, void* stream);
+
 /* Combine backward (moe.py:285-292 reversed): for every kept slot r = slot_row[t,j]
  *   dyperm[r] = slot_w[t,j] * dy[t]            (bf16)
  *   dw[t,j]   = dy[t] . yperm[r]               (f32, fixed order; 0 if dropped)

@@ -434,6 +434,69 @@ unsigned grid_for(int64_t n, int per_block) {
   return (unsigned)(b < 65536 ? (b > 0 ? b : 1) : 65536);
 }
 
+// ---------------------------------------------------------------- fp8 straight-through operands
+// The fp8 experts' backward lets the gradients through the e4m3 quantisations unchanged
+// and multiplies by the operands the fp8 GEMMs actually took: the dequantised rows and
+// weights, bf16.
+
+// out[r, :] = bf16(e4m3(q[r, :]) * scale[r]) for rows r < min(rows, *n_rows_dev) (the
+// other rows are not written).  One wave per row at a time, 8 codes per lane and step
+// (an 8-byte load, a 16-byte store).
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __restrict__ q,
+                                                           const float* __restrict__ scale, int64_t rows,
+                                                           const int32_t* __restrict__ n_rows_dev, int cols,
+                                                           uint16_t* __restrict__ out) {
+  int64_t nr = rows;
+  if (n_rows_dev) nr = min<int64_t>(nr, (int64_t)*n_rows_dev);
+  const int lane = threadIdx.x & 63;
+  const int nvec = cols / 8;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < nr; r += (int64_t)gridDim.x * 4) {
+    const float s = scale[r];
+    const uint2* src = reinterpret_cast<const uint2*>(q + r * cols);
+    uint4* dst = reinterpret_cast<uint4*>(out + r * cols);
+    for (int v = lane; v < nvec; v += 64) {
+      const uint2 c = src[v];
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = (i < 2 ? c.x : c.y) >> ((i & 1) * 16);
+        const float a = e4m3_to_f32(w & 0xffu) * s, b = e4m3_to_f32((w >> 8) & 0xffu) * s;
+        o[i] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+      }
+      dst[v] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// out (E, K, N) bf16 = w (E, K, N) fake-quantised per column n of each expert, as the
+// fp8 weight packing quantises it: scale = amax / 448 over the column's K values, code =
+// e4m3(w * (448 / amax)) (saturating, nearest even), out = bf16(code * scale); a zero
+// column stays zero.  Workgroup: 64 columns of one expert, the 4 waves splitting K.
+template <bool F32>
+__global__ __launch_bounds__(256) void fake_quant_cols_kernel(const void* __restrict__ w, int K, int N,
+                                                              uint16_t* __restrict__ out) {
+  __shared__ float red[4][64];
+  const int c = threadIdx.x & 63, kw = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + c;
+  const int64_t base = (int64_t)blockIdx.y * K * N;
+  auto ld = [&](int64_t i) -> float {
+    return F32 ? static_cast<const float*>(w)[i] : bf16_to_f32(static_cast<const uint16_t*>(w)[i]);
+  };
+  float amax = 0.0f;
+  if (n < N)
+    for (int k = kw; k < K; k += 4) amax = fmaxf(amax, fabsf(ld(base + (int64_t)k * N + n)));
+  red[kw][c] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0][c], red[1][c]), fmaxf(red[2][c], red[3][c]));
+  if (n >= N) return;
+  const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+  const float sc = amax / 448.0f;
+  for (int k = kw; k < K; k += 4) {
+    const int64_t i = base + (int64_t)k * N + n;
+    out[i] = f32_to_bf16(e4m3_to_f32(f32_to_e4m3(ld(i) * inv)) * sc);
+  }
+}
+
 }  // namespace
 
 extern "C" int kmoe_combine_bwd(const void* dy, const void* yperm, const int32_t* slot_row, const float* slot_w, int k,
@@ -624,4 +687,35 @@ extern "C" int kmoe_mod_bwd(const float* sel_w, const float* dsel, int B, int64_
   rc = kmoe::check_launch("kmoe_mod_bwd");
   if (rc != KMOE_OK) return rc;
   return kmoe_reduce_f32(partial, nseg, d, dw_mod, dw_dtype, stream);
+}
+
+extern "C" int kmoe_dequant_rows_fp8(const uint8_t* q, const float* scale, int64_t rows, const int32_t* n_rows_dev,
+                                     int cols, void* out, void* stream) {
+  KMOE_REQUIRE(q && scale && out, KMOE_ERR_NULL, "kmoe_dequant_rows_fp8: null buffer");
+  KMOE_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0, KMOE_ERR_SHAPE,
+               "kmoe_dequant_rows_fp8: rows=%lld cols=%d (cols must be a positive multiple of 8)", (long long)rows,
+               cols);
+  if (rows == 0) return KMOE_OK;
+  int64_t blocks = kmoe::ceil_div<int64_t>(rows, 4);
+  const int64_t cap = (int64_t)kmoe::cu_count() * 8;
+  if (blocks > cap) blocks = cap;
+  hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, kmoe::as_stream(stream), q, scale,
+                     rows, n_rows_dev, cols, static_cast<uint16_t*>(out));
+  return kmoe::check_launch("kmoe_dequant_rows_fp8");
+}
+
+extern "C" int kmoe_fake_quant_e4m3_cols(const void* w, int w_dtype, int E, int K, int N, void* out, void* stream) {
+  KMOE_REQUIRE(w && out, KMOE_ERR_NULL, "kmoe_fake_quant_e4m3_cols: null buffer");
+  KMOE_REQUIRE(E >= 1 && E <= 65535 && K >= 1 && N >= 1, KMOE_ERR_SHAPE, "kmoe_fake_quant_e4m3_cols: E=%d K=%d N=%d",
+               E, K, N);
+  KMOE_REQUIRE(w_dtype == KMOE_DTYPE_BF16 || w_dtype == KMOE_DTYPE_F32, KMOE_ERR_DTYPE,
+               "kmoe_fake_quant_e4m3_cols: weights must be bf16 or f32");
+  const dim3 grid((unsigned)kmoe::ceil_div(N, 64), (unsigned)E);
+  hipStream_t s = kmoe::as_stream(stream);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  if (w_dtype == KMOE_DTYPE_F32)
+    hipLaunchKernelGGL(fake_quant_cols_kernel<true>, grid, dim3(256), 0, s, w, K, N, o);
+  else
+    hipLaunchKernelGGL(fake_quant_cols_kernel<false>, grid, dim3(256), 0, s, w, K, N, o);
+  return kmoe::check_launch("kmoe_fake_quant_e4m3_cols");
 }

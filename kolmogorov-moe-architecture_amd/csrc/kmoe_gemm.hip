@@ -690,7 +690,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   // four consecutive output columns per c.  A lane packs each such run to 8 bytes of
   // bf16 in registers and writes it to an LDS tile (rows padded by 16 bytes), which
   // then goes out with 16-byte stores along rows.
-  static_assert(!SAVE_GU || (GATE_UP && !FP8), "g/u saving is for bf16 gate/up tiles");
+  static_assert(!SAVE_GU || GATE_UP, "g/u saving is for gate/up tiles");
+  static_assert(!(SAVE_GU && FP8 && M16), "fp8 tiles use 32x32 blocks");
   constexpr int NC = GATE_UP ? 32 * WNB : 64 * WNB;  // output columns of the tile
   // output column blocks per wave, and 4-column runs per block and lane: a gate/up
   // WNB = 1 block holds its gate values in runs c = 0, 1 and the up values of the same
@@ -792,7 +793,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
   store_staged<OCPR, OSTR>(lds, tid, m0, m_end, g.C + col0, g.ldc, col0, g.n_valid);
 
   // training forward: the pre-activation gate and up values of the tile, bf16, in the
-  // packed column order (row stride 2*ldc), for the SwiGLU backward
+  // packed column order (row stride 2*ldc), for the SwiGLU backward (fp8: descaled by
+  // the row and column scales, the values the SwiGLU of the epilogue took)
   if constexpr (SAVE_GU) {
     constexpr int NC2 = 64 * WNB;
     constexpr int OSTR2 = NC2 * 2 + 16;
@@ -812,13 +814,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
         if (mi >= NMA) break;
+        if constexpr (FP8) sar = sa_l[wm * 128 + mi * 32 + lr];
 #pragma unroll
         for (int j = 0; j < WNB; ++j) {
           const int col = b_lds_row<true, WNB>(wn, j, 0);
+          auto gv = [&](int r) { return FP8 ? acc[mi][j][r] * (sar * sbr[j][r]) : acc[mi][j][r]; };
 #pragma unroll
           for (int c = 0; c < 4; ++c)
             *reinterpret_cast<i32x2_t*>(wb2 + mi * 32 * OSTR2 + (col + 8 * c) * 2) =
-                pack4(acc[mi][j][4 * c], acc[mi][j][4 * c + 1], acc[mi][j][4 * c + 2], acc[mi][j][4 * c + 3]);
+                pack4(gv(4 * c), gv(4 * c + 1), gv(4 * c + 2), gv(4 * c + 3));
         }
       }
     }
@@ -1520,6 +1524,9 @@ int launch_gemm(bool gate_up, bool fp8, const void* A, const float* a_scale, con
     KMOE_LAUNCH_GEMM(true, false, true);
   else if (gate_up && !fp8)
     KMOE_LAUNCH_GEMM(true, false, false);
+  else if (gate_up && gu_out)
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, true, false, true>), grid, block, 0, s, g, offsets, E, n_tiles,
+                       n_cu, allow_split);
   else if (gate_up && fp8)
     KMOE_LAUNCH_GEMM(true, true, false);
   else if (!fp8)
@@ -1768,6 +1775,22 @@ extern "C" int kmoe_gemm_gate_up_rows_gu(const void* x, const int32_t* row_index
                    2 * (int64_t)Fp, nullptr, h, Fp, Fp, Fp / 128, kmoe::as_stream(stream), nullptr, gu);
   if (rc) return rc;
   return kmoe::check_launch("kmoe_gemm_gate_up_rows_gu");
+}
+
+extern "C" int kmoe_gemm_gate_up_fp8_gu(const void* xperm, const float* xperm_scale, const int32_t* offsets, int E,
+                                        int d, int F, int64_t max_rows, const void* w13_packed, const float* w13_scale,
+                                        void* h, void* gu, void* stream) {
+  int rc = check_gemm_args("kmoe_gemm_gate_up_fp8_gu", xperm, offsets, E, d, F, max_rows, w13_packed, h,
+                           KMOE_DTYPE_FP8_E4M3);
+  if (rc) return rc;
+  KMOE_REQUIRE(xperm_scale && w13_scale && gu, KMOE_ERR_NULL, "kmoe_gemm_gate_up_fp8_gu: null scale / gu");
+  KMOE_REQUIRE(d % 128 == 0, KMOE_ERR_SHAPE, "kmoe_gemm_gate_up_fp8_gu: fp8 needs d %% 128 == 0 (d=%d)", d);
+  if (max_rows == 0) return KMOE_OK;
+  const int Fp = round_up(F, 128);
+  rc = launch_gemm(true, true, xperm, xperm_scale, nullptr, nullptr, 0, offsets, E, d, max_rows, w13_packed,
+                   2 * (int64_t)Fp, w13_scale, h, Fp, Fp, Fp / 128, kmoe::as_stream(stream), nullptr, gu);
+  if (rc) return rc;
+  return kmoe::check_launch("kmoe_gemm_gate_up_fp8_gu");
 }
 
 extern "C" size_t kmoe_packed_w3n_bytes(int E, int d, int F) {

@@ -66,6 +66,9 @@ _SIGNATURES = {
     "kmoe_router_hist": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_router_train": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_gemm_gate_up_rows_gu": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp]),
+    "kmoe_gemm_gate_up_fp8_gu": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "kmoe_dequant_rows_fp8": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _vp]),
+    "kmoe_fake_quant_e4m3_cols": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "kmoe_router_rms": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _f32, _vp, _vp]),
     "kmoe_gemm_gate_up_rows_scaled": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp]),
     "kmoe_combine_residual": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _vp, _i32, _vp]),

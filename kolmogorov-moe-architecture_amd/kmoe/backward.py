@@ -87,10 +87,10 @@ class Saved(NamedTuple):
     w: torch.Tensor          # (T, k) f32
     hidden: torch.Tensor     # (T, 128) f32 router pre-activation
     disp: ops.DispatchOut    # routing tables
-    h: torch.Tensor          # (A, F_pad) bf16
+    h: torch.Tensor          # (A, F_pad) bf16 (fp8 experts: dequantised from the down GEMM's e4m3 rows)
     gu: torch.Tensor         # (A, 2 F_pad) bf16 pre-activation gate / up
     yperm: torch.Tensor      # (A, d) bf16 expert outputs
-    xperm: torch.Tensor      # (A, d) bf16 permuted input rows (the dispatch's gather)
+    xperm: torch.Tensor      # (A, d) bf16 permuted input rows (fp8: dequantised e4m3 rows)
 
 
 class Grads(NamedTuple):

@@ -207,19 +207,38 @@ class _PackedExperts(nn.Module):
             return None, None, None
         return (dw1.to(self.w1.dtype), dw2.to(self.w2.dtype), None if self.w3 is None else dw3.to(self.w3.dtype))
 
-    def expert_rows(self, x2d, row_token, offsets, A, xperm=None, save=False):
-        """The experts on A routed rows: (yperm (A, d), h, pre-activations or None).  Gated:
-        the gate/up GEMM gathers x2d[row_token[r]] itself (with save, the pre-activation
-        gate/up values for the backward); non-gated: from the permuted rows xperm (the
-        pre-activation x w1 is always returned)."""
+    def expert_rows(self, x2d, row_token, offsets, A, xperm=None, save=False, xscale=None):
+        """The experts on A routed rows: (yperm (A, d), h, pre-activations or None, the
+        permuted input rows the weight gradient reads).  Gated bf16: the gate/up GEMM
+        gathers x2d[row_token[r]] itself (with save, the pre-activation gate/up values
+        for the backward); non-gated: from the permuted rows xperm (the pre-activation
+        x w1 is always returned); fp8: from the e4m3 rows xperm with row scales xscale,
+        with save h and the input rows dequantised (bf16, the values the fp8 GEMMs
+        took: the straight-through backward's operands) and the descaled gate/up values."""
         pw = self.packed()
+        if self.use_fp8:
+            if not save:
+                return ops.grouped_ffn(xperm, xscale, offsets, pw, A), None, None, None
+            h, gu = ops.gemm_gate_up(xperm, xscale, offsets, pw, A, save_gu=True)
+            n_dev = offsets[self.n_experts:]
+            hq, hs = ops.quant_rows_fp8(h, n_dev)
+            yperm = ops.gemm_down(hq, hs, offsets, pw, A)
+            return yperm, ops.dequant_rows_fp8(hq, hs, n_dev), gu, ops.dequant_rows_fp8(xperm, xscale, n_dev)
         if not self.gated:
-            return ops.plain_ffn(xperm, offsets, pw, A)
+            return (*ops.plain_ffn(xperm, offsets, pw, A), xperm)
         if save:
             h, gu = ops.gemm_gate_up_rows(x2d, None, row_token, offsets, pw, A, save_gu=True)
         else:
             h, gu = ops.gemm_gate_up_rows(x2d, None, row_token, offsets, pw, A), None
-        return ops.gemm_down(h, None, offsets, pw, A), h, gu
+        return ops.gemm_down(h, None, offsets, pw, A), h, gu, xperm
+
+    def bwd_source_weights(self):
+        """The expert weights the backward multiplies by: the parameters, or for fp8
+        experts the fake-quantised ones the fp8 GEMMs used (straight-through: their
+        gradients go to the parameters unchanged)."""
+        if not self.use_fp8:
+            return self.w1, self.w2, self.w3
+        return tuple(ops.fake_quant_cols_e4m3(w) for w in (self.w1, self.w2, self.w3))
 
     def install_packed(self, pw: ops.PackedWeights) -> None:
         """Use `pw` (packed from exactly the current w1/w2/w3, e.g. read back from disk)
@@ -232,11 +251,11 @@ class _PackedExperts(nn.Module):
 
     def bwd_packed(self) -> _bwd.BwdWeights:
         """Backward packed weights (no router part), rebuilt only when a parameter changed."""
-        key = tuple((w.data_ptr(), w._version) for w in self._weights())
+        key = tuple((w.data_ptr(), w._version) for w in self._weights()) + (self.use_fp8,)
         cache = getattr(self, "_bwd_cache", None)
         if cache is None or cache[0] != key:
             with torch.no_grad():
-                cache = (key, _bwd.pack_bwd_weights(self.w1, self.w2, self.w3, None))
+                cache = (key, _bwd.pack_bwd_weights(*self.bwd_source_weights(), None))
             self._bwd_cache = cache
         return cache[1]
 
@@ -246,7 +265,7 @@ class _PackedExperts(nn.Module):
             return False
         if not any(isinstance(t, torch.Tensor) and t.requires_grad for t in inputs + tuple(self.parameters())):
             return False
-        return not (self.use_fp8 or self.d_ff % 8)
+        return not self.d_ff % 8
 
     def packed(self) -> ops.PackedWeights:
         """Packed weights, rebuilt only when a parameter changed (version counters)."""
@@ -471,23 +490,24 @@ class _ExpertsFn(torch.autograd.Function):
         T, k = idx.shape
         E = experts.n_experts
         xb = x2d.detach().to(torch.bfloat16).contiguous()
-        disp = ops.dispatch(xb, idx, w.detach(), E, materialize=True)
-        yperm, h, gu = experts.expert_rows(xb, disp.row_token, disp.offsets, T * k, xperm=disp.xperm, save=True)
+        disp = ops.dispatch(xb, idx, w.detach(), E, materialize=True, fp8=experts.use_fp8)
+        yperm, h, gu, xrows = experts.expert_rows(xb, disp.row_token, disp.offsets, T * k, xperm=disp.xperm,
+                                                  xscale=disp.xscale, save=True)
         out_dtype = torch.float32 if x2d.dtype == torch.float32 else torch.bfloat16
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T, out_dtype=out_dtype)
-        ctx.sv = (disp, h, gu, yperm)
+        ctx.sv = (disp, h, gu, yperm, xrows)
         ctx.experts = experts
         ctx.meta = (x2d.dtype, w.dtype, T, k)
         return y.to(x2d.dtype)
 
     @staticmethod
     def backward(ctx, dy):
-        disp, h, gu, yperm = _once(ctx)
+        disp, h, gu, yperm, xrows = _once(ctx)
         ge = ctx.experts
         x_dtype, w_dtype, T, k = ctx.meta
         need_w = any(ctx.needs_input_grad[2:5])
         dy = dy.reshape(T, -1).to(torch.bfloat16).contiguous()
-        dx, dw, dw1, dw2, dw3 = _bwd.experts_backward(dy, yperm, gu, h, disp.xperm, disp.slot_row.view(T, k),
+        dx, dw, dw1, dw2, dw3 = _bwd.experts_backward(dy, yperm, gu, h, xrows, disp.slot_row.view(T, k),
                                                       disp.slot_w.view(T, k), disp.offsets, T * k, ge.bwd_packed(),
                                                       ge.n_experts, ge.d_ff, need_weights=need_w)
         wg = ge.cast_grads(dw1, dw2, dw3)
@@ -505,8 +525,9 @@ class _ExpertsECFn(torch.autograd.Function):
         sel = experts.tables(token_indices, w, S)
         xb = x3d.detach().reshape(B * S, d).to(torch.bfloat16).contiguous()
         A = E * B * C
-        xperm, _ = ops.gather_rows(xb, sel.row_token, A)
-        yperm, h, gu = experts.expert_rows(xb, sel.row_token, sel.offsets, A, xperm=xperm, save=True)
+        xperm, xscale = ops.gather_rows(xb, sel.row_token, A, fp8=experts.use_fp8)
+        yperm, h, gu, xperm = experts.expert_rows(xb, sel.row_token, sel.offsets, A, xperm=xperm, xscale=xscale,
+                                                  save=True)
         out_dtype = torch.float32 if x3d.dtype == torch.float32 else torch.bfloat16
         y = ops.combine(yperm, sel.src_row, sel.src_w, B * S, out_dtype=out_dtype)
         ctx.sv = (sel, h, gu, yperm, xperm)
@@ -545,8 +566,9 @@ class _MoEECTrainFn(torch.autograd.Function):
         r, sel, C = layer.router.route(xb, descending=False, save_hidden=True)
         x2d = xb.reshape(T, d)
         A = E * B * C
-        xperm, _ = ops.gather_rows(x2d, sel.row_token, A)
-        yperm, h, gu = ge.expert_rows(x2d, sel.row_token, sel.offsets, A, xperm=xperm, save=True)
+        xperm, xscale = ops.gather_rows(x2d, sel.row_token, A, fp8=ge.use_fp8)
+        yperm, h, gu, xperm = ge.expert_rows(x2d, sel.row_token, sel.offsets, A, xperm=xperm, xscale=xscale,
+                                             save=True)
         y = ops.combine(yperm, sel.src_row, sel.src_w, T, out_dtype=layer._out_dtype(x))
         has_aux = layer.training and layer.router_z_loss_weight > 0
         aux = (ops.aux_loss(r.partials, T, E, None, 1, 0.0, layer.router_z_loss_weight)[0] if has_aux
@@ -654,20 +676,22 @@ class MoELayer(nn.Module):
         return self._trainable_experts()
 
     def _trainable_experts(self) -> bool:
-        """Whether the experts have a HIP backward: bf16 weights in the GEMMs (not fp8) and
-        d_ff_expert a multiple of 8 (the weight-gradient stores write rows of 8 bf16)."""
+        """Whether the experts have a HIP backward: d_ff_expert a multiple of 8 (the
+        weight-gradient stores write rows of 8 bf16).  fp8 experts train straight-through:
+        the gradients pass the e4m3 quantisations unchanged and multiply by the
+        dequantised operands the fp8 GEMMs took (bf16 master weights)."""
         ge = self.grouped_experts if self.grouped_experts is not None else self.grouped_experts_ec
-        return not (ge.use_fp8 or ge.d_ff % 8)
+        return not ge.d_ff % 8
 
     def _bwd_weights(self) -> _bwd.BwdWeights:
         """Backward packed weights, rebuilt only when a parameter changed."""
         ge = self.grouped_experts if self.grouped_experts is not None else self.grouped_experts_ec
         w_in = self.router.router[0].weight
-        key = tuple((w.data_ptr(), w._version) for w in ge._weights() + (w_in,))
+        key = tuple((w.data_ptr(), w._version) for w in ge._weights() + (w_in,)) + (ge.use_fp8,)
         cache = getattr(self, "_bwd_cache", None)
         if cache is None or cache[0] != key:
             with torch.no_grad():
-                cache = (key, _bwd.pack_bwd_weights(ge.w1, ge.w2, ge.w3, w_in))
+                cache = (key, _bwd.pack_bwd_weights(*ge.bwd_source_weights(), w_in))
             self._bwd_cache = cache
         return cache[1]
 
@@ -682,11 +706,13 @@ class MoELayer(nn.Module):
         k, E = self.top_k, self.n_experts
         cap = ops.capacity_of(self.capacity_factor, T, k, E) if self.drop_overflow else 0
         # the permuted x rows are kept for the weight gradient (the gated gate/up GEMM still
-        # gathers its own A rows from x)
+        # gathers its own A rows from x; fp8: the rows are the dispatch's e4m3 codes, kept
+        # dequantised)
         aux_in = self._aux_args(r, T)
-        disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=True, block_counts=r.block_counts,
-                            aux=aux_in)
-        yperm, h, gu = ge.expert_rows(x2d, disp.row_token, disp.offsets, T * k, xperm=disp.xperm, save=True)
+        disp = ops.dispatch(x2d, r.idx, r.w, E, capacity=cap, materialize=True, fp8=ge.use_fp8,
+                            block_counts=r.block_counts, aux=aux_in)
+        yperm, h, gu, xrows = ge.expert_rows(x2d, disp.row_token, disp.offsets, T * k, xperm=disp.xperm,
+                                             xscale=disp.xscale, save=True)
         y = ops.combine(yperm, disp.slot_row.view(T, k), disp.slot_w.view(T, k), T if T_out is None else T_out,
                         out_map=out_map, scale=scale, out_dtype=out_dtype, residual=residual, keep_mask=keep_mask,
                         keep_scale=keep_scale)
@@ -696,7 +722,7 @@ class MoELayer(nn.Module):
             aux = (disp.aux if disp.aux is not None else
                    ops.aux_loss(r.partials, T, E, disp.counts, k, self.load_balance_loss_weight,
                                 self.router_z_loss_weight))[0]
-        sv = _bwd.Saved(x2d, r.logits, r.idx, r.w, r.hidden, disp, h, gu, yperm, disp.xperm)
+        sv = _bwd.Saved(x2d, r.logits, r.idx, r.w, r.hidden, disp, h, gu, yperm, xrows)
         return y, aux, sv
 
     def _forward_token_choice(self, hidden_states: torch.Tensor) -> torch.Tensor:

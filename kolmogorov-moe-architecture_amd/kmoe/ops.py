@@ -303,10 +303,21 @@ def pack_weights(w1, w2, w3, fp8=False) -> PackedWeights:
     return PackedWeights(w13p, w3p, s13, s3, E, d, F, fp8)
 
 
-def gemm_gate_up(xperm, xscale, offsets, pw: PackedWeights, max_rows):
+def gemm_gate_up(xperm, xscale, offsets, pw: PackedWeights, max_rows, save_gu=False):
+    """h = SwiGLU gate/up of the permuted rows.  save_gu (fp8 training forward) also
+    returns the descaled pre-activation gate/up values (max_rows, 2*F_pad) bf16 in the
+    packed order: returns (h, gu)."""
     lib = _lib.load()
     Fp = lib.kmoe_padded_ff(pw.F)
     h = torch.empty(max(max_rows, 1), Fp, device=xperm.device, dtype=_BF16)
+    if save_gu:
+        if not pw.fp8:
+            raise ValueError("kmoe.gemm_gate_up: save_gu is for fp8 rows (bf16: gemm_gate_up_rows)")
+        gu = torch.empty(max(max_rows, 1), 2 * Fp, device=xperm.device, dtype=_BF16)
+        with _Stage("gemm_gate_up"):
+            _lib.call("kmoe_gemm_gate_up_fp8_gu", ptr(xperm), ptr(xscale), ptr(offsets), pw.E, pw.d, pw.F, max_rows,
+                      ptr(pw.w13), ptr(pw.s13), ptr(h), ptr(gu), _stream(xperm))
+        return h, gu
     with _Stage("gemm_gate_up"):
         _lib.call("kmoe_gemm_gate_up", ptr(xperm), ptr(xscale),
               _lib.DTYPE_FP8_E4M3 if pw.fp8 else _lib.DTYPE_BF16, ptr(offsets), pw.E, pw.d, pw.F, max_rows,
@@ -363,6 +374,32 @@ def quant_rows_fp8(m, n_rows_dev=None):
     with _Stage("quant_h"):
         _lib.call("kmoe_quant_rows_fp8", ptr(m), rows, ptr(n_rows_dev), cols, ptr(q), ptr(s), _stream(m))
     return q, s
+
+
+def dequant_rows_fp8(q, scale, n_rows_dev=None):
+    """bf16(e4m3(q) * scale[:, None]) of fp8 rows (rows past *n_rows_dev not written):
+    the operand the fp8 GEMM took, for the straight-through backward."""
+    _need_gpu(q, scale)
+    rows, cols = q.shape
+    out = torch.empty(rows, cols, device=q.device, dtype=_BF16)
+    with _Stage("fp8_dequant"):
+        _lib.call("kmoe_dequant_rows_fp8", ptr(q), ptr(scale), rows, ptr(n_rows_dev), cols, ptr(out), _stream(q))
+    return out
+
+
+def fake_quant_cols_e4m3(w):
+    """w (E, K, N) fake-quantised per output column of each expert exactly as the fp8
+    weight packing quantises it, dequantised to bf16 (the weights the fp8 GEMMs
+    multiplied)."""
+    _need_gpu(w)
+    if w.dtype not in (torch.float32, _BF16):
+        raise ValueError(f"kmoe.fake_quant_cols_e4m3: unsupported weight dtype {w.dtype}")
+    w = _contig(w.detach(), w.dtype)
+    E, K, N = w.shape
+    out = torch.empty(E, K, N, device=w.device, dtype=_BF16)
+    _lib.call("kmoe_fake_quant_e4m3_cols", ptr(w), _lib.DTYPE_F32 if w.dtype == torch.float32 else _lib.DTYPE_BF16,
+              E, K, N, ptr(out), _stream(w))
+    return out
 
 
 class PlainPacked(NamedTuple):

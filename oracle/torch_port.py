@@ -61,8 +61,30 @@ def _expert_bmm(padded, w1, w2, w3):
     return torch.bmm(F.silu(torch.bmm(padded, w1)) * torch.bmm(padded, w2), w3)
 
 
-def grouped_experts_tc(x, idx, w, w1, w2, w3):
-    """GroupedExperts.forward's padded-bmm formulation."""
+def ste(fq, t):
+    """Straight-through fake quantisation: the value fq(t), the gradient of t."""
+    return t + (fq(t) - t).detach()
+
+
+def _expert_bmm_fp8_ste(padded, w1, w2, w3, quant_h=True):
+    """_expert_bmm with config 5's e4m3 fake quantisation (per-row scales of the input
+    rows, per-output-column scales of each expert's weights, h rounded to bf16 and
+    re-quantised per row: moe_layer_fp8_mod's scheme), each quantisation
+    straight-through: the gradients multiply by the dequantised operands and pass the
+    quantisers unchanged to the bf16 master values (the reference's fp8 experts,
+    fp8_moe.py:179-279, are differentiated by autograd through their scaled operands)."""
+    fqw = lambda w: _fake_e4m3_rows(w.transpose(1, 2)).transpose(1, 2)
+    xq = ste(_fake_e4m3_rows, padded)
+    w1q, w2q, w3q = ste(fqw, w1), ste(fqw, w2), ste(fqw, w3)
+    h = F.silu(torch.bmm(xq, w1q)) * torch.bmm(xq, w2q)
+    if quant_h:
+        h = ste(lambda t: _fake_e4m3_rows(t.to(torch.bfloat16).to(t.dtype)), h)
+    return torch.bmm(h, w3q)
+
+
+def grouped_experts_tc(x, idx, w, w1, w2, w3, fp8=False):
+    """GroupedExperts.forward's padded-bmm formulation (fp8: the experts fake-quantised
+    straight-through, _expert_bmm_fp8_ste)."""
     n_tok, k = idx.shape
     E = w1.shape[0]
     flat_e = idx.reshape(-1)
@@ -80,7 +102,7 @@ def grouped_experts_tc(x, idx, w, w1, w2, w3):
     pos = torch.arange(s_tok.numel()) - starts[s_e]
     padded = x.new_zeros(E, m, x.shape[1])
     padded[s_e, pos] = rows
-    out = _expert_bmm(padded, w1, w2, w3)
+    out = _expert_bmm_fp8_ste(padded, w1, w2, w3) if fp8 else _expert_bmm(padded, w1, w2, w3)
     contrib = out[s_e, pos] * s_w.unsqueeze(1)
     y = x.new_zeros(x.shape)
     y.index_add_(0, s_tok, contrib)
@@ -106,7 +128,7 @@ def moe_layer_tc(x3d, w_in, w_out, w1, w2, w3, k, training=True):
 
 
 def moe_loss_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, dy, capacity=0, bias=None, training=True, w_lb=0.01,
-                       w_z=0.001):
+                       w_z=0.001, fp8=False):
     """Scalar loss sum(y * dy) (+ aux in training) of MoELayer's token-choice forward with
     the routing fixed to `idx` (T, k): Router.forward's logits / softmax and its top-k
     values gathered at idx and renormalised (moe.py:423-462), GroupedExperts.forward's
@@ -114,12 +136,14 @@ def moe_loss_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, dy, capacity=0, bias=N
     and z losses with one-hot counts of idx (moe.py:840-939).  For autograd: at a fixed
     routing the layer is smooth, so the gradients of this loss are the reference's
     backward.  capacity > 0 keeps the first `capacity` assignments of each expert in
-    assignment order (the build's drop rule); bias (E,) is added to the logits."""
-    y, aux = moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity, bias, training, w_lb, w_z)
+    assignment order (the build's drop rule); bias (E,) is added to the logits.
+    fp8: the experts fake-quantised straight-through (_expert_bmm_fp8_ste)."""
+    y, aux = moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity, bias, training, w_lb, w_z, fp8=fp8)
     return (y * dy).sum() + aux
 
 
-def moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity=0, bias=None, training=True, w_lb=0.01, w_z=0.001):
+def moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity=0, bias=None, training=True, w_lb=0.01, w_z=0.001,
+                  fp8=False):
     """(y, aux) of moe_loss_tc_routed's layer (aux 0 when not training)."""
     T, d = x2d.shape
     k = idx.shape[1]
@@ -145,7 +169,7 @@ def moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity=0, bias=None, trai
         m = int(pos.max().item()) + 1
         padded = x2d.new_zeros(E, m, d)
         padded = padded.index_put((s_e, pos), x2d[s_tok])
-        out = _expert_bmm(padded, w1, w2, w3)
+        out = _expert_bmm_fp8_ste(padded, w1, w2, w3) if fp8 else _expert_bmm(padded, w1, w2, w3)
         y = y.index_add(0, s_tok, out[s_e, pos] * s_w.unsqueeze(1))
     aux = x2d.new_zeros(())
     if training:
@@ -158,7 +182,7 @@ def moe_tc_routed(x2d, w_in, w_out, w1, w2, w3, idx, capacity=0, bias=None, trai
 
 def ffn_half_loss_routed(h3d, w_in, w_out, w1, w2, w3, idx, dy, norm_w=None, eps=1e-5, w_mod=None, sel_idx=None,
                          residual=None, capacity=0, training=True, w_lb=0.01, w_z=0.001, return_out=False,
-                         drop_keep=None, p_drop=0.0):
+                         drop_keep=None, p_drop=0.0, fp8=False):
     """Scalar loss sum(out * dy) (+ the MoE aux in training) of the FFN half of
     TransformerBlock.forward (layers.py:142-190) at a fixed MoD selection, routing and
     residual-dropout mask (drop_keep (B, S, d) bool, nn.Dropout's output = input *
@@ -173,24 +197,29 @@ def ffn_half_loss_routed(h3d, w_in, w_out, w1, w2, w3, idx, dy, norm_w=None, eps
       out = h + dropout(ffn_output) with a norm (layers.py:187-190), else
         residual + dropout(ffn_output) (residual optional).
     At a fixed selection and routing the composition is smooth: autograd of this loss
-    is the reference's backward.  return_out: (loss, out)."""
+    is the reference's backward.  return_out: (loss, out).  fp8: the experts
+    fake-quantised straight-through (_expert_bmm_fp8_ste)."""
     B, S, d = h3d.shape
     x = h3d
     if norm_w is not None:
         rms = torch.sqrt(torch.mean(h3d ** 2, dim=-1, keepdim=True) + eps)
         x = norm_w * (h3d / rms)
+    if fp8:
+        # the layer's activations are bf16 and the e4m3 codes of a row follow from its
+        # bf16 values (rounded straight-through, as every bf16 activation is here)
+        x = ste(lambda t: t.to(torch.bfloat16).to(t.dtype), x)
     if w_mod is not None:
         keep = sel_idx.shape[1]
 
         def moe(xs):
             y, aux = moe_tc_routed(xs.reshape(B * keep, d), w_in, w_out, w1, w2, w3, idx, capacity, None, training,
-                                   w_lb, w_z)
+                                   w_lb, w_z, fp8=fp8)
             return y.view(B, keep, d), aux
 
         ffn_out, aux = mod_apply(x, w_mod, sel_idx, moe)
     else:
         y, aux = moe_tc_routed(x.reshape(B * S, d), w_in, w_out, w1, w2, w3, idx, capacity, None, training, w_lb,
-                               w_z)
+                               w_z, fp8=fp8)
         ffn_out = y.view(B, S, d)
     if drop_keep is not None:
         ffn_out = ffn_out * drop_keep.to(ffn_out.dtype) * (1.0 / (1.0 - p_drop))
@@ -222,16 +251,17 @@ def mod_aux_loss(x3d, w_a, w_b, sel_idx, weight=0.001):
     return weight * (F.softplus(a) - t * a).mean()
 
 
-def grouped_experts_ec_tc(x3d, ew, ti, w1, w2, w3):
+def grouped_experts_ec_tc(x3d, ew, ti, w1, w2, w3, fp8=False):
     """GroupedExpertsExpertChoice.forward (moe.py:626-673): gather the selected tokens,
-    bmm SwiGLU with the weights repeated per sequence, weight, scatter_add_ back."""
+    bmm SwiGLU with the weights repeated per sequence, weight, scatter_add_ back (fp8:
+    the experts fake-quantised straight-through, _expert_bmm_fp8_ste)."""
     B, S, d = x3d.shape
     _, E, C = ti.shape
     gi = ti.unsqueeze(-1).expand(-1, -1, -1, d)
     xin = torch.gather(x3d.unsqueeze(1).expand(-1, E, -1, -1), 2, gi).reshape(B * E, C, d)
     W1, W2 = w1.repeat(B, 1, 1), w2.repeat(B, 1, 1)
     W3 = None if w3 is None else w3.repeat(B, 1, 1)
-    out = _expert_bmm(xin, W1, W2, W3).view(B, E, C, d)
+    out = (_expert_bmm_fp8_ste(xin, W1, W2, W3) if fp8 else _expert_bmm(xin, W1, W2, W3)).view(B, E, C, d)
     wout = out * ew.unsqueeze(-1)
     y = x3d.new_zeros(B, S, d)
     return y.scatter_add(1, ti.reshape(B, E * C).unsqueeze(-1).expand(-1, -1, d), wout.reshape(B, E * C, d))
@@ -258,19 +288,19 @@ def moe_layer_ec(x3d, w_in, w_out, w1, w2, w3, cf):
     return grouped_experts_ec_tc(x3d, ew, ti, w1, w2, w3)
 
 
-def moe_loss_ec_routed(x3d, w_in, w_out, w1, w2, w3, ti, dy, training=True, w_z=0.001):
+def moe_loss_ec_routed(x3d, w_in, w_out, w1, w2, w3, ti, dy, training=True, w_z=0.001, fp8=False):
     """Scalar loss sum(y * dy) (+ w_z * z-loss in training, moe.py:833-836) of MoELayer's
     expert-choice forward with the selection fixed to ti (B, E, C): at a fixed selection
     the layer is smooth, so the autograd gradients of this loss are the reference's."""
-    y, aux = ec_layer_routed(x3d, w_in, w_out, w1, w2, w3, ti, training, w_z)
+    y, aux = ec_layer_routed(x3d, w_in, w_out, w1, w2, w3, ti, training, w_z, fp8=fp8)
     return (y * dy).sum() + aux
 
 
-def ec_layer_routed(x3d, w_in, w_out, w1, w2, w3, ti, training=True, w_z=0.001):
+def ec_layer_routed(x3d, w_in, w_out, w1, w2, w3, ti, training=True, w_z=0.001, fp8=False):
     """(y, aux) of MoELayer's expert-choice forward (moe.py:815-838) with the selection
     fixed to ti (B, E, C); aux = w_z * z-loss in training (moe.py:833-836), else 0."""
     logits = F.linear(F.silu(F.linear(x3d, w_in)), w_out)
-    y = grouped_experts_ec_tc(x3d, ec_weights_routed(logits, ti), ti, w1, w2, w3)
+    y = grouped_experts_ec_tc(x3d, ec_weights_routed(logits, ti), ti, w1, w2, w3, fp8=fp8)
     aux = w_z * (torch.logsumexp(logits, dim=-1) ** 2).mean() if training else 0.0
     return y, aux
 
@@ -343,6 +373,6 @@ def moe_layer_fp8_mod(x3d, w_mod, w_in, w_out, w1q, w2q, w3q, k, keep):
     padded = rows.new_zeros(w1q.shape[0], m, d).index_put((s_e, pos), xq[s_tok])
     h = F.silu(torch.bmm(padded, w1q)) * torch.bmm(padded, w2q)
     # h is held in bf16 (the layer's activation dtype) before its re-quantisation
-    out = torch.bmm(_fake_e4m3_rows(h.to(torch.bfloat16).to(torch.float32)), w3q)
+    out = torch.bmm(_fake_e4m3_rows(h.to(torch.bfloat16).to(h.dtype)), w3q)
     y = rows.new_zeros(T, d).index_add(0, s_tok, out[s_e, pos] * s_w.unsqueeze(1))
     return torch.zeros_like(x3d).scatter_add(1, gidx, p.unsqueeze(-1) * y.view(B, keep, d))

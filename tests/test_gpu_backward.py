@@ -35,10 +35,11 @@ def _rel(a, b):
     return float((a - b).norm() / max(b.norm(), 1e-30))
 
 
-def _run(dev, B, S, d, E, k, F, seed, drop_cf=None, train=True, zipf=False, empty_expert=None, dy_zero=False):
+def _run(dev, B, S, d, E, k, F, seed, drop_cf=None, train=True, zipf=False, empty_expert=None, dy_zero=False,
+         fp8=False):
     cfg = AdvancedMoEConfig(d_model=d, n_experts=E, moe_top_k=k, d_ff_expert=F,
                             moe_capacity_factor=drop_cf or 1.25, moe_drop_overflow=drop_cf is not None,
-                            moe_router_bias=synth.zipf_bias(E, seed).tolist() if zipf else None)
+                            moe_router_bias=synth.zipf_bias(E, seed).tolist() if zipf else None, moe_fp8=fp8)
     layer = MoELayer(cfg, 0).to(dev, torch.bfloat16)
     g = torch.Generator().manual_seed(seed)
     with torch.no_grad():
@@ -74,7 +75,8 @@ def _run(dev, B, S, d, E, k, F, seed, drop_cf=None, train=True, zipf=False, empt
     cap = int(np.ceil(drop_cf * B * S * k / E)) if drop_cf is not None else 0
     bias = None if layer.router.logit_bias is None else layer.router.logit_bias.double().cpu()
     ref = P.moe_loss_tc_routed(xr, *params, idx, dy.reshape(B * S, d).double(), capacity=cap, bias=bias,
-                               training=train, w_lb=layer.load_balance_loss_weight, w_z=layer.router_z_loss_weight)
+                               training=train, w_lb=layer.load_balance_loss_weight, w_z=layer.router_z_loss_weight,
+                               fp8=fp8)
     ref.backward()
     got = [x.grad.reshape(B * S, d), layer.router.router[0].weight.grad, layer.router.router[2].weight.grad,
            ge.w1.grad, ge.w2.grad, ge.w3.grad]
@@ -97,6 +99,19 @@ def _check(errs):
                                          (2, 512, 512, 16, 2, 768)])
 def test_backward_parity(dev, B, S, d, E, k, F):
     errs, _, _ = _run(dev, B, S, d, E, k, F, seed=100 + F)
+    _check(errs)
+
+
+@pytest.mark.parametrize("B,S,d,E,k,F,drop_cf", [(2, 256, 256, 8, 2, 512, None), (1, 640, 384, 4, 2, 320, None),
+                                                 (2, 512, 256, 8, 2, 256, 1.0)])
+def test_backward_fp8_straight_through(dev, B, S, d, E, k, F, drop_cf):
+    """fp8 experts (config 5's e4m3 scheme) train straight-through on bf16 master
+    weights: against fp64 autograd of the fake-quantised restatement
+    (oracle/torch_port._expert_bmm_fp8_ste, pinned by tests/test_oracle.py), whose
+    gradients pass the quantisers unchanged and multiply by the dequantised operands.
+    Same bars as the bf16 backward."""
+    print(f"fp8 straight-through backward B={B} S={S} d={d} E={E} F={F} cf={drop_cf}", flush=True)
+    errs, _, _ = _run(dev, B, S, d, E, k, F, seed=300 + F, drop_cf=drop_cf, fp8=True)
     _check(errs)
 
 

@@ -41,12 +41,15 @@ def _check(errs, loose=()):
         assert e <= (2e-2 if n in loose else 1e-2), (n, e, errs)
 
 
-@pytest.mark.parametrize("B,S,d,E,F,cf,train", [(2, 256, 256, 8, 512, 2.0, True), (1, 512, 384, 4, 320, 1.0, True),
-                                                (2, 192, 256, 16, 256, 2.0, False)])
-def test_ec_layer_backward(dev, B, S, d, E, F, cf, train):
-    print(f"ec layer backward B={B} S={S} d={d} E={E} F={F} cf={cf} train={train}", flush=True)
+@pytest.mark.parametrize("B,S,d,E,F,cf,train,fp8", [(2, 256, 256, 8, 512, 2.0, True, False),
+                                                    (1, 512, 384, 4, 320, 1.0, True, False),
+                                                    (2, 192, 256, 16, 256, 2.0, False, False),
+                                                    (2, 256, 256, 8, 512, 2.0, True, True)])
+def test_ec_layer_backward(dev, B, S, d, E, F, cf, train, fp8):
+    """fp8: the experts straight-through, against the fake-quantised restatement."""
+    print(f"ec layer backward B={B} S={S} d={d} E={E} F={F} cf={cf} train={train} fp8={fp8}", flush=True)
     cfg = AdvancedMoEConfig(d_model=d, n_experts=E, d_ff_expert=F, moe_routing="expert_choice",
-                            moe_capacity_factor=cf, moe_router_z_loss_weight=0.01)
+                            moe_capacity_factor=cf, moe_router_z_loss_weight=0.01, moe_fp8=fp8)
     layer = MoELayer(cfg, 0).to(dev, torch.bfloat16)
     g = torch.Generator().manual_seed(B * S + E)
     _init(layer, g)
@@ -66,7 +69,7 @@ def test_ec_layer_backward(dev, B, S, d, E, F, cf, train):
     mods = [layer.router.router[0].weight, layer.router.router[2].weight, ge.w1, ge.w2, ge.w3]
     params = [f64(p) for p in mods]
     xr = f64(x)
-    ref = P.moe_loss_ec_routed(xr, *params, ti, dy.double(), training=train, w_z=0.01)
+    ref = P.moe_loss_ec_routed(xr, *params, ti, dy.double(), training=train, w_z=0.01, fp8=fp8)
     ref.backward()
     names = ["dx", "dw_in", "dw_out", "dw1", "dw2", "dw3"]
     got = [x.grad] + [p.grad for p in mods]
@@ -74,12 +77,14 @@ def test_ec_layer_backward(dev, B, S, d, E, F, cf, train):
     _check({n: _rel(a, b) for n, a, b in zip(names, got, want)}, loose=("dw_in", "dw_out"))
 
 
-@pytest.mark.parametrize("T,d,E,k,F", [(600, 256, 8, 2, 512), (333, 128, 16, 4, 256)])
-def test_grouped_experts_direct_backward(dev, T, d, E, k, F):
+@pytest.mark.parametrize("T,d,E,k,F,fp8", [(600, 256, 8, 2, 512, False), (333, 128, 16, 4, 256, False),
+                                            (600, 256, 8, 2, 512, True)])
+def test_grouped_experts_direct_backward(dev, T, d, E, k, F, fp8):
     """GroupedExperts.forward(x, idx, w) trained directly: gradients of x, of the routing
-    weights w and of w1 / w2 / w3 (moe.py:213-294)."""
-    print(f"grouped experts direct backward T={T} E={E} k={k}", flush=True)
+    weights w and of w1 / w2 / w3 (moe.py:213-294); fp8: straight-through."""
+    print(f"grouped experts direct backward T={T} E={E} k={k} fp8={fp8}", flush=True)
     ge = GroupedExperts(E, d, F).to(dev, torch.bfloat16)
+    ge.use_fp8 = fp8
     g = torch.Generator().manual_seed(T + E)
     _init(ge, g)
     x = torch.randn(T, d, generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
@@ -91,7 +96,7 @@ def test_grouped_experts_direct_backward(dev, T, d, E, k, F):
     torch.cuda.synchronize()
     params = [f64(ge.w1), f64(ge.w2), f64(ge.w3)]
     xr, wr = f64(x), f64(w)
-    ref = (P.grouped_experts_tc(xr, idx.cpu(), wr, *params) * dy.double()).sum()
+    ref = (P.grouped_experts_tc(xr, idx.cpu(), wr, *params, fp8=fp8) * dy.double()).sum()
     ref.backward()
     names = ["dx", "dw", "dw1", "dw2", "dw3"]
     got = [x.grad, w.grad, ge.w1.grad, ge.w2.grad, ge.w3.grad]

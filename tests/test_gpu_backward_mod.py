@@ -198,20 +198,23 @@ def test_mod_aux_router_loss(dev, path):
 
 
 # ------------------------------------------------------------------ the block in training
-@pytest.mark.parametrize("mod,norm_dtype,h_dtype,p_drop", [
-    (False, torch.float32, BF, 0.0),
-    (True, torch.float32, BF, 0.0),
-    (True, BF, BF, 0.0),
-    (True, torch.float32, torch.float32, 0.0),
-    (False, torch.float32, BF, 0.1),   # the reference's default residual_dropout (config.py:87)
-    (True, torch.float32, BF, 0.1),
-    (False, torch.float32, torch.float32, 0.5),
+@pytest.mark.parametrize("mod,norm_dtype,h_dtype,p_drop,fp8", [
+    (False, torch.float32, BF, 0.0, False),
+    (True, torch.float32, BF, 0.0, False),
+    (True, BF, BF, 0.0, False),
+    (True, torch.float32, torch.float32, 0.0, False),
+    (False, torch.float32, BF, 0.1, False),   # the reference's default residual_dropout (config.py:87)
+    (True, torch.float32, BF, 0.1, False),
+    (False, torch.float32, torch.float32, 0.5, False),
+    # config 5's composition, MoD + fp8 experts, trained straight-through
+    (True, torch.float32, BF, 0.0, True),
+    (True, torch.float32, BF, 0.1, True),
 ])
-def test_block_training_backward(dev, mod, norm_dtype, h_dtype, p_drop):
+def test_block_training_backward(dev, mod, norm_dtype, h_dtype, p_drop, fp8):
     B, S, d, E, k, F_ = 2, 256, 256, 8, 2, 352
-    print(f"block training mod={mod} norm={norm_dtype} h={h_dtype} p={p_drop}", flush=True)
+    print(f"block training mod={mod} norm={norm_dtype} h={h_dtype} p={p_drop} fp8={fp8}", flush=True)
     cfg = AdvancedMoEConfig(d_model=d, n_experts=E, moe_top_k=k, d_ff_expert=F_, mod_enabled=mod,
-                            mod_capacity_factor=0.75, residual_dropout=p_drop)
+                            mod_capacity_factor=0.75, residual_dropout=p_drop, moe_fp8=fp8)
     blk = MoEFFNBlock(cfg, 0).to(dev, BF).train()
     g = torch.Generator().manual_seed(410 + int(mod))
     drop_keep = None
@@ -255,7 +258,7 @@ def test_block_training_backward(dev, mod, norm_dtype, h_dtype, p_drop):
                                        sel.sel_idx.cpu(), w_lb=ffn.load_balance_loss_weight,
                                        w_z=ffn.router_z_loss_weight, return_out=True,
                                        drop_keep=None if drop_keep is None else drop_keep.view(B, S, d),
-                                       p_drop=p_drop)
+                                       p_drop=p_drop, fp8=fp8)
     loss.backward()
     hd = h.detach().double().cpu()
     # an f32 output carries the MoE part exactly; a bf16 one rounds h + MoE part

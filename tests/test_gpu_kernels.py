@@ -403,7 +403,7 @@ def test_grouped_swiglu_fp8(dev):
     assert relL2(npf(y[:A]), ref) <= 1e-1
 
 
-@pytest.mark.parametrize("path", ["bf16", "gather", "save_gu", "rscale", "fp8"])
+@pytest.mark.parametrize("path", ["bf16", "gather", "save_gu", "rscale", "fp8", "fp8_gu"])
 @pytest.mark.parametrize("rest", [4, 84, 144])
 def test_split_tail_tiles_bit_identical(dev, path, rest):
     """The last partial round of tiles runs as narrow tiles (a quarter of the columns when
@@ -412,7 +412,7 @@ def test_split_tail_tiles_bit_identical(dev, path, rest):
     of a launch whose tail they fill (`rest` tiles past the last full round: split 4,
     2, 1) give the same bits as in a launch with an extra expert appended, which has no
     partial round at all, for the gate/up (plain, gathered, g/u-saving, RMS-scaled,
-    fp8) and the down GEMMs."""
+    fp8, fp8 g/u-saving) and the down GEMMs."""
     n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
     d, F = 512, 256  # 2 column tiles per slot in both GEMMs
     assert rest % 2 == 0 and rest < n_cu
@@ -430,7 +430,7 @@ def test_split_tail_tiles_bit_identical(dev, path, rest):
     w1, w2, w3 = _experts(8, d, F, 40)
     (x,) = gen(41, (Ab, d))
     xb = bf16(x).to(dev)
-    fp8 = path == "fp8"
+    fp8 = path.startswith("fp8")
     pws = [ops.pack_weights(bf16(w1[:E]).to(dev), bf16(w2[:E]).to(dev), bf16(w3[:E]).to(dev), fp8=fp8)
            for E in (7, 8)]
     rs = (torch.rand(Ab, generator=torch.Generator().manual_seed(42)) + 0.5).to(dev)
@@ -451,7 +451,10 @@ def test_split_tail_tiles_bit_identical(dev, path, rest):
             h = ops.gemm_gate_up_rows(xs, None, rt, off, pw, n, rscale=rs[:n].contiguous())
         if fp8:
             xq, xsc = ops.gather_rows(xb, rt, n, fp8=True)
-            h = ops.gemm_gate_up(xq, xsc, off, pw, n)
+            if path == "fp8_gu":
+                h, gu = ops.gemm_gate_up(xq, xsc, off, pw, n, save_gu=True)
+            else:
+                h = ops.gemm_gate_up(xq, xsc, off, pw, n)
             y = ops.grouped_ffn(xq, xsc, off, pw, n)
         else:
             y = ops.gemm_down(h, None, off, pw, n)
@@ -466,6 +469,79 @@ def test_split_tail_tiles_bit_identical(dev, path, rest):
         off = np.concatenate([[0], np.cumsum(counts)])
         ref = O.swiglu_rows(npf(xb[:A]), off, npf(bf16(w1[:7])), npf(bf16(w2[:7])), npf(bf16(w3[:7])))
         assert relL2(npf(ya[:A]), ref) <= 1e-2
+
+
+# ------------------------------------------------------------------ fp8 straight-through operands
+def test_gate_up_fp8_gu(dev):
+    """kmoe_gemm_gate_up_fp8_gu: h bit-identical to kmoe_gemm_gate_up's, and the saved
+    descaled gate / up values (packed order: per 128 columns of f, 128 gate then 128 up)
+    against the fp32 products of the oracle's dequantised operands (e4m3 rows times
+    their scales, per-column fake-quantised weights); bf16 rounding of the stored value
+    is the only difference (rel-L2 ~1e-3, bar 4e-3)."""
+    E, d, F = 4, 256, 320
+    counts = [300, 0, 17, 256]
+    A = sum(counts)
+    Fp = 384
+    w1, w2, w3 = _experts(E, d, F, 51)
+    (x,) = gen(52, (A, d))
+    xb = bf16(x).to(dev)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    off = torch.tensor(offsets, dtype=torch.int32, device=dev)
+    pw = ops.pack_weights(bf16(w1).to(dev), bf16(w2).to(dev), bf16(w3).to(dev), fp8=True)
+    xq, xs = ops.gather_rows(xb, torch.arange(A, dtype=torch.int32, device=dev), A, fp8=True)
+    h_plain = ops.gemm_gate_up(xq, xs, off, pw, A)
+    h, gu = ops.gemm_gate_up(xq, xs, off, pw, A, save_gu=True)
+    torch.cuda.synchronize()
+    assert torch.equal(h[:A].view(torch.int16), h_plain[:A].view(torch.int16))
+    g4 = npf(gu[:A]).reshape(A, Fp // 128, 2, 128)
+    g_got, u_got = g4[:, :, 0].reshape(A, Fp)[:, :F], g4[:, :, 1].reshape(A, Fp)[:, :F]
+    qx, sx = O.quant_rows(npf(xb))
+    xd = O.dequant_rows(qx, sx).astype(np.float64)
+    W1q, W2q = O.quant_weight_cols(npf(bf16(w1))), O.quant_weight_cols(npf(bf16(w2)))
+    g_ref = np.zeros((A, F))
+    u_ref = np.zeros((A, F))
+    for e in range(E):
+        r = slice(offsets[e], offsets[e + 1])
+        g_ref[r] = xd[r] @ W1q[e]
+        u_ref[r] = xd[r] @ W2q[e]
+    assert relL2(g_got, g_ref) <= 4e-3 and relL2(u_got, u_ref) <= 4e-3
+
+
+@pytest.mark.parametrize("rows,cols,bound", [(700, 384, None), (700, 384, 513), (64, 2816, 0), (5, 8, None)])
+def test_dequant_rows_fp8(dev, rows, cols, bound):
+    """kmoe_dequant_rows_fp8 against the oracle's dequantisation rounded to bf16, bit for
+    bit, on codes and scales from kmoe_quant_rows_fp8; rows at or past the device-side
+    bound are left as they were."""
+    from kmoe import _lib
+    from kmoe._lib import ptr
+    g = torch.Generator().manual_seed(rows + cols)
+    m = torch.randn(rows, cols, generator=g) * torch.exp(torch.randn(rows, 1, generator=g) * 2)
+    q, sc = ops.quant_rows_fp8(bf16(m).to(dev))
+    nb = None if bound is None else torch.tensor([bound], dtype=torch.int32, device=dev)
+    out = torch.full((rows, cols), 7.0, device=dev, dtype=torch.bfloat16)
+    _lib.call("kmoe_dequant_rows_fp8", ptr(q), ptr(sc), rows, ptr(nb), cols, ptr(out), None)
+    torch.cuda.synchronize()
+    n = rows if bound is None else bound
+    want = torch.from_numpy(O.dequant_rows(q[:n].cpu().numpy(), npf(sc[:n]))).to(torch.bfloat16)
+    assert torch.equal(out[:n].cpu().view(torch.int16), want.view(torch.int16))
+    assert bool((out[n:] == 7.0).all())
+    assert torch.equal(ops.dequant_rows_fp8(q, sc, nb)[:n].view(torch.int16), out[:n].view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fake_quant_cols_e4m3(dev, dtype):
+    """kmoe_fake_quant_e4m3_cols against the oracle's per-output-column weight
+    quantisation (the fp8 packing's), dequantised and rounded to bf16, bit for bit,
+    including a zero column and columns past the last full 64-column block."""
+    E, K, N = 3, 200, 130
+    (w,) = gen(53, (E, K, N), scale=0.05)
+    w[1, :, 7] = 0.0
+    wd = w.to(dtype)
+    got = ops.fake_quant_cols_e4m3(wd.to(dev))
+    torch.cuda.synchronize()
+    want = torch.from_numpy(O.quant_weight_cols(wd.float().numpy())).to(torch.bfloat16)
+    assert torch.equal(got.cpu().view(torch.int16), want.view(torch.int16))
+    assert bool((got[1, :, 7] == 0).all())
 
 
 # ------------------------------------------------------------------ combine

@@ -860,6 +860,74 @@ def test_fp8_mod_port_matches_numpy_oracle():
     assert np.all(got[~mask] == 0) and np.all(np.abs(got[mask]).sum(-1) > 0)
 
 
+def test_fp8_ste_forward_matches_fp8_port():
+    """The straight-through fp8 restatement (ffn_half_loss_routed fp8=True, the GPU
+    training tests' reference) computes the same forward as the pinned config 5 port
+    moe_layer_fp8_mod at the same MoD selection and routing."""
+    g = torch.Generator().manual_seed(22)
+    B, S, d, E, k, F_, keep = 2, 24, 64, 5, 2, 80, 16
+    x = torch.randn(B, S, d, generator=g, dtype=torch.float64).to(torch.bfloat16).to(torch.float64)
+    w_mod = torch.randn(1, d, generator=g, dtype=torch.float64) * 0.05
+    w_in = torch.randn(128, d, generator=g, dtype=torch.float64) * 0.05
+    w_out = torch.randn(E, 128, generator=g, dtype=torch.float64) * 0.05
+    w1, w2 = (torch.randn(E, d, F_, generator=g, dtype=torch.float64) * 0.05 for _ in range(2))
+    w3 = torch.randn(E, F_, d, generator=g, dtype=torch.float64) * 0.05
+    want = P.moe_layer_fp8_mod(x, w_mod, w_in, w_out, *P.fake_quant_expert_weights(w1, w2, w3), k, keep)
+    r = (x @ w_mod.reshape(-1, 1)).squeeze(-1)
+    sel = torch.topk(r, keep, dim=-1).indices.sort(dim=-1).values
+    rows = torch.gather(x, 1, sel.unsqueeze(-1).expand(-1, -1, d)).reshape(-1, d)
+    idx = P.router_tc(rows, w_in, w_out, k)[1]
+    _, got = P.ffn_half_loss_routed(x, w_in, w_out, w1, w2, w3, idx, torch.zeros_like(x), w_mod=w_mod,
+                                    sel_idx=sel, training=False, return_out=True, fp8=True)
+    assert torch.allclose(got, want, rtol=0, atol=1e-12 * float(want.abs().max()))
+    # and it differs from the unquantised layer by the quantisation (a few per cent)
+    _, plain = P.ffn_half_loss_routed(x, w_in, w_out, w1, w2, w3, idx, torch.zeros_like(x), w_mod=w_mod,
+                                      sel_idx=sel, training=False, return_out=True)
+    assert 1e-3 < float((plain - got).norm() / got.norm()) < 0.2
+
+
+def test_fp8_ste_gradients_use_dequantised_operands():
+    """Straight-through gradients of _expert_bmm_fp8_ste: the quantisers pass the gradient
+    unchanged (ste's own gradient is the identity), and with h unquantised the gradients
+    of x, w1, w2, w3 equal those of the plain SwiGLU product evaluated at the
+    fake-quantised operands as leaves (a backward multiplying by the master weights or
+    rows instead would differ by the quantisation, a few per cent).  With h quantised,
+    dw3 is the closed form hq^T dout of each expert with hq = e4m3(bf16(h))."""
+    g = torch.Generator().manual_seed(23)
+    E, m, d, F_ = 3, 7, 32, 48
+    x = torch.randn(E, m, d, generator=g, dtype=torch.float64)
+    ws = [torch.randn(E, d, F_, generator=g, dtype=torch.float64) * 0.1 for _ in range(2)]
+    ws.append(torch.randn(E, F_, d, generator=g, dtype=torch.float64) * 0.1)
+    dout = torch.randn(E, m, d, generator=g, dtype=torch.float64)
+    # ste: value fq(t), gradient of t
+    t = torch.randn(5, 9, generator=g, dtype=torch.float64, requires_grad=True)
+    c = torch.randn(5, 9, generator=g, dtype=torch.float64)
+    q = P.ste(P._fake_e4m3_rows, t)
+    assert torch.equal(q.detach(), P._fake_e4m3_rows(t.detach()))
+    (q * c).sum().backward()
+    assert torch.equal(t.grad, c)
+
+    def grads(fn, leaves):
+        leaves = [v.clone().requires_grad_(True) for v in leaves]
+        (fn(*leaves) * dout).sum().backward()
+        return [v.grad for v in leaves]
+
+    fqw = lambda w: P._fake_e4m3_rows(w.transpose(1, 2)).transpose(1, 2)
+    ste_g = grads(lambda a, b, c_, e: P._expert_bmm_fp8_ste(a, b, c_, e, quant_h=False), [x] + ws)
+    at_q = grads(P._expert_bmm, [P._fake_e4m3_rows(x)] + [fqw(w) for w in ws])
+    master = grads(P._expert_bmm, [x] + ws)
+    for a, b, c_ in zip(ste_g, at_q, master):
+        assert torch.allclose(a, b, rtol=1e-12, atol=1e-12)
+        assert float((c_ - b).norm() / b.norm()) > 1e-3
+    # quantised h: dw3 = hq^T dout per expert
+    xq = P._fake_e4m3_rows(x)
+    h = F.silu(torch.bmm(xq, fqw(ws[0]))) * torch.bmm(xq, fqw(ws[1]))
+    hq = P._fake_e4m3_rows(h.to(torch.bfloat16).to(torch.float64))
+    dw3 = grads(P._expert_bmm_fp8_ste, [x] + ws)[3]
+    for e in range(E):
+        assert torch.allclose(dw3[e], hq[e].T @ dout[e], rtol=1e-12, atol=1e-12)
+
+
 def test_dropout_keep_convention_matches_torch():
     """ffn_half_loss_routed's residual dropout (ffn_out * keep * (1 / (1 - p)), layers.py:190)
     against nn.functional.dropout itself: the mask read off torch's output reproduces it
