@@ -127,6 +127,19 @@ __device__ __forceinline__ void dma16_to_lds(const void* src, KMOE_LDS void* lds
   asm volatile("s_nop 1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(la)));
 }
 
+// Lane l's value from lane l ^ M (M = 1 or 2) of its group of four lanes, in one DPP
+// move (quad_perm [1,0,3,2] / [2,3,0,1]) instead of an LDS-crossbar permute.  Every
+// lane of the quad must be active.
+template <int M>
+__device__ __forceinline__ int quad_xor(int v) {
+  static_assert(M == 1 || M == 2, "lanes of a quad");
+  return __builtin_amdgcn_update_dpp(0, v, M == 1 ? 0xB1 : 0x4E, 0xF, 0xF, false);
+}
+template <int M>
+__device__ __forceinline__ float quad_xor(float v) {
+  return __int_as_float(quad_xor<M>(__float_as_int(v)));
+}
+
 // Wave-level reductions (64 lanes).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

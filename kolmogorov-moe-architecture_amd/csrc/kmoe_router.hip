@@ -9,9 +9,9 @@
 // stage are in flight while one is computed.  The hidden activations go through LDS
 // (fp32) to the 128 -> E layer, which runs in fp32 on v_mfma_f32_16x16x4_f32 (each
 // wave: 16 tokens x all experts); softmax/top-k then run four lanes per token (each
-// with a quarter of the experts' logits in registers, merged by lane shuffles), and
-// the logits, aux partials and outputs leave through coalesced, all-thread copies
-// and wave reductions.
+// with a quarter of the experts' logits in registers, merged by DPP moves inside the
+// quad), the logits leave through a coalesced all-thread copy and each aux partial is
+// one thread's fixed-order column sum.
 #include "kmoe_common.h"
 
 namespace {
@@ -140,12 +140,26 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   const int nk = d * 2 / RKB;
   float ss = 0.0f;  // RMS: this lane's part of sum(x^2) of token wm*32 + lr
   for (int s = 0; s < RT_STAGES - 1 && s < nk; ++s) issue(s);
-  // w_out (needed only by layer 2) is staged while the first K-steps are in flight:
-  // loading it before them put its global round trip in front of every x load
-  // (2.9 -> 0.6 us before the first K-step)
-  for (int i = tid; i < NEP * RT_HID; i += RT_THREADS) {
-    const int e = i / RT_HID, j = i % RT_HID;
-    wo[e * WOS + j] = e < E ? bf16_to_f32(w_out[i]) : 0.0f;
+  // w_out (needed only by layer 2) goes out behind the first K-steps, one 16-byte load
+  // per thread and vector (rows past E read as zero), and reaches LDS after the K loop:
+  // loaded before the K-steps its round trip delayed every x load, and as 2-byte loads
+  // in a loop it cost 8 dependent round trips (~3.5 us) before the first K-step
+  constexpr int WOV = NEP * RT_HID / 8;  // 16-byte vectors of the padded w_out
+  constexpr int WOQ = (WOV + RT_THREADS - 1) / RT_THREADS;
+  const bool wo_vec = (reinterpret_cast<uintptr_t>(w_out) & 15) == 0;
+  i32x4_t wov[WOQ];
+  if (wo_vec) {
+#pragma unroll
+    for (int q = 0; q < WOQ; ++q) {
+      const int v = tid + q * RT_THREADS;
+      wov[q] = (v < WOV && v / (RT_HID / 8) < E) ? reinterpret_cast<const i32x4_t*>(w_out)[v]
+                                                   : i32x4_t{0, 0, 0, 0};
+    }
+  } else {
+    for (int i = tid; i < NEP * RT_HID; i += RT_THREADS) {
+      const int e = i / RT_HID, j = i % RT_HID;
+      wo[e * WOS + j] = e < E ? bf16_to_f32(w_out[i]) : 0.0f;
+    }
   }
   if (tid < NE) cnt_l[tid] = 0;
   constexpr int NSUB = RKB / 32;  // MFMA K-substeps per K-step
@@ -192,6 +206,21 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
       if (tok0 + wm * 32 + lr < T) rscale[tok0 + wm * 32 + lr] = r;
     }
   }
+  if (wo_vec) {
+#pragma unroll
+    for (int q = 0; q < WOQ; ++q) {
+      const int v = tid + q * RT_THREADS;
+      if (v < WOV) {
+        float* dst = wo + (v / (RT_HID / 8)) * WOS + (v % (RT_HID / 8)) * 8;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t pr = (uint32_t)wov[q][c];
+          dst[2 * c] = __uint_as_float(pr << 16);
+          dst[2 * c + 1] = __uint_as_float(pr & 0xffff0000u);
+        }
+      }
+    }
+  }
   __syncthreads();  // stage buffers are reused below
 
   // SiLU, then to LDS: acc[j][r] is hidden wn*64+j*32+lr of token wm*32+8*(r/4)+4*lh+r%4
@@ -202,7 +231,7 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
     for (int r = 0; r < 16; ++r) {
       const int m = wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
       const float pre = RMS ? acc[j][r] * rs_l[m] : acc[j][r];
-      hs[m * HSTR + wn * 64 + j * 32 + lr] = silu_f32(pre);
+      hs[m * HSTR + wn * 64 + j * 32 + lr] = silu_fast_f32(pre);
       if (hidden_pre && tok0 + m < T) hidden_pre[(tok0 + m) * RT_HID + wn * 64 + j * 32 + lr] = pre;
     }
   __syncthreads();
@@ -253,16 +282,16 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
 #pragma unroll
       for (int q = 0; q < NQ; ++q)
         if (part + 4 * q < E) mx = fmaxf(mx, L[q]);
-      mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+      mx = fmaxf(mx, quad_xor<1>(mx));
+      mx = fmaxf(mx, quad_xor<2>(mx));
       float ex[NQ], s = 0.0f;
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         ex[q] = part + 4 * q < E ? __expf(L[q] - mx) : 0.0f;
         s += ex[q];
       }
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
+      s += quad_xor<1>(s);
+      s += quad_xor<2>(s);
       const float inv_s = 1.0f / s;
 #pragma unroll
       for (int q = 0; q < NQ; ++q) P[part + 4 * q] = ex[q] * inv_s;
@@ -289,15 +318,14 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
               bv = v;
             }
           }
-#pragma unroll
-          for (int o = 1; o <= 2; o <<= 1) {
-            const int oi = __shfl_xor(bi, o, 64);
-            const float ov = __shfl_xor(bv, o, 64);
+          auto merge = [&](int oi, float ov) {
             if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
               bi = oi;
               bv = ov;
             }
-          }
+          };
+          merge(quad_xor<1>(bi), quad_xor<1>(bv));
+          merge(quad_xor<2>(bi), quad_xor<2>(bv));
           if ((bi & 3) == part) taken |= 1u << (bi >> 2);
           sel[j] = bi;
           sev[j] = __expf(bv - mx);
@@ -327,14 +355,15 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   for (int i = tid; i < ntok * E; i += RT_THREADS) logits[tok0 * E + i] = lg[(i / E) * LGS + i % E];
 
   // ---- per-block aux partials: column c of the block's 64 tokens (c < E: the
-  // probabilities, c == E: lse^2) summed by one wave with a fixed shuffle tree
-  if (partials) {
-    float* pb = partials + (int64_t)blockIdx.x * (E + 1);
-    for (int c = wave; c <= E; c += RT_THREADS / 64) {
-      const float v = c < E ? pe[lane * LGS + c] : lse2[lane];
-      const float sum = wave_sum(v);
-      if (lane == 0) pb[c] = sum;
-    }
+  // probabilities, c == E: lse^2) summed by thread c in a fixed order (four running
+  // sums over tokens m = 4i + u, then added u = 0..3)
+  if (partials && tid <= E) {
+    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+    for (int m = 0; m < RT_TOK; m += 4)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) sum[u] += tid < E ? pe[(m + u) * LGS + tid] : lse2[m + u];
+    partials[(int64_t)blockIdx.x * (E + 1) + tid] = (sum[0] + sum[1]) + (sum[2] + sum[3]);
   }
 }
 
