@@ -5,7 +5,7 @@
 //                    (moe_arch/model/layers.py:148-185)
 //
 // Selection is an exact radix select over order-preserving uint32 images of the
-// fp32 scores (4 passes of 8 bits, LDS histograms), followed by an index-ordered
+// fp32 scores (passes of 12, 10 and 10 bits, LDS histograms), followed by an index-ordered
 // compaction: every score above the threshold is taken, and of the scores equal
 // to it the lowest indices are taken first.  One 1024-thread workgroup per
 // (sequence, expert); keys live in LDS.
@@ -42,86 +42,124 @@ __device__ float block_sum(float v, float* s_red) {
 }
 
 // Finds the key `thr` of the C-th largest element and how many elements equal to
-// thr must be taken (`need`).  s_hist holds 256 bins per wave of the block.
-__device__ void radix_select_desc(const uint32_t* keys, int n, int C, uint32_t* s_hist, uint32_t* s_bcast,
+// thr must be taken (`need`): an MSD radix select over digits of 12, 10 and 10 bits
+// with one shared histogram (s_hist: RS_BINS bins).  The 12-bit first digit (sign,
+// exponent and three mantissa bits of the score) spreads typical logits over many
+// bins; with an 8-bit first digit (sign and 7 exponent bits) every score in [0.5, 2)
+// shares one bin, and the histogram's LDS atomics from one wave to one address
+// serialise (measured: 9k cycles per pass).  The keys are in registers (key_index;
+// slots at or past n are ignored).  When the chosen bin holds a single key, that key
+// is the threshold and the remaining passes are skipped.
+constexpr int RS_BINS = 4096;
+// Register layout of the keys: lane l of wave w holds key w * 64 PER + 64 u + l in
+// slot u, so each wave owns one contiguous segment of 64 PER keys.
+template <int PER>
+__device__ __forceinline__ int key_index(int u) {
+  return (int)(threadIdx.x >> 6) * (64 * PER) + 64 * u + (int)(threadIdx.x & 63);
+}
+template <int PER>
+__device__ void radix_select_desc(const uint32_t (&kr)[PER], int n, int C, uint32_t* s_hist, uint32_t* s_bcast,
                                   uint32_t& thr, int& need) {
-  __shared__ int s_scan[4];
+  __shared__ __attribute__((aligned(16))) int s_scan[SEL_THREADS / 64];
   uint32_t prefix = 0, pmask = 0;
   int remaining = C;
-  const int nw = blockDim.x >> 6;  // one private 256-bin histogram per wave (no hot-bin contention)
-  uint32_t* wh = s_hist + 256 * (threadIdx.x >> 6);
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = threadIdx.x; i < 256 * nw; i += blockDim.x) s_hist[i] = 0;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int nthr = blockDim.x;
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 20 : pass == 1 ? 10 : 0;
+    const int nb = pass == 0 ? RS_BINS : 1024;
+    for (int i = t; i < nb; i += nthr) s_hist[i] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-      const uint32_t k = keys[i];
-      if ((k & pmask) == prefix) atomicAdd(&wh[(k >> shift) & 255u], 1u);
-    }
-    __syncthreads();
-    // per-digit totals into the first histogram (fixed order: deterministic)
-    for (int dg = threadIdx.x; dg < 256; dg += blockDim.x) {
-      uint32_t tsum = 0;
-      for (int q = 0; q < nw; ++q) tsum += s_hist[256 * q + dg];
-      s_hist[dg] = tsum;
-    }
-    __syncthreads();
-    // bucket choice in parallel: thread t < 256 takes digit 255 - t (descending), an
-    // inclusive scan over t gives the count at or above each digit, and the one
-    // thread whose range crosses `remaining` publishes the digit
-    {
-      const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-      const int h = t < 256 ? (int)s_hist[255 - t] : 0;
-      int incl = h;
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += u;
-      }
-      if (lane == 63 && w < 4) s_scan[w] = incl;
-      __syncthreads();
-      if (t < 256) {
-        for (int q = 0; q < w; ++q) incl += s_scan[q];
-        if (incl >= remaining && incl - h < remaining) {
-          s_bcast[0] = (uint32_t)(255 - t);
-          s_bcast[1] = (uint32_t)(remaining - (incl - h));
+    for (int u = 0; u < PER; ++u)
+      if (key_index<PER>(u) < n && (kr[u] & pmask) == prefix)
+        atomicAdd(&s_hist[(kr[u] >> shift) & (uint32_t)(nb - 1)], 1u);
+    __syncthreads();
+    // bucket choice: thread t owns `per` consecutive digits counted from the top
+    // (digit nb - 1 - (t per + j)); an inclusive scan of the threads' sums gives the
+    // count at or above each range, and the one thread whose range crosses
+    // `remaining` walks its digits and publishes the digit, what is left of
+    // `remaining` inside it and the digit's count
+    const int per = nb > nthr ? nb / nthr : 1;  // 4 or 1
+    int h[RS_BINS / SEL_THREADS];
+    int tsum = 0;
+#pragma unroll
+    for (int j = 0; j < RS_BINS / SEL_THREADS; ++j) {
+      const int r = t * per + j;
+      h[j] = (j < per && r < nb) ? (int)s_hist[nb - 1 - r] : 0;
+      tsum += h[j];
+    }
+    int incl = tsum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += u;
+    }
+    if (lane == 63) s_scan[w] = incl;
+    __syncthreads();
+    // the sums of the waves before this one: the wave totals read as four vectors
+#pragma unroll
+    for (int q4 = 0; q4 < SEL_THREADS / 256; ++q4) {
+      const i32x4_t v = reinterpret_cast<const i32x4_t*>(s_scan)[q4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (4 * q4 + c < w) incl += v[c];
+    }
+    int c = incl - tsum;  // count above this thread's range
+    if (c < remaining && incl >= remaining) {
+#pragma unroll
+      for (int j = 0; j < RS_BINS / SEL_THREADS; ++j) {
+        if (j < per && c + h[j] >= remaining) {
+          s_bcast[0] = (uint32_t)(nb - 1 - (t * per + j));
+          s_bcast[1] = (uint32_t)(remaining - c);
+          s_bcast[2] = (uint32_t)h[j];
+          break;
         }
+        c += h[j];
       }
     }
     __syncthreads();
     prefix |= s_bcast[0] << shift;
-    pmask |= 255u << shift;
+    pmask |= (uint32_t)(nb - 1) << shift;
     remaining = (int)s_bcast[1];
+    const bool single = s_bcast[2] == 1u && pass < 2;
     __syncthreads();
+    if (single) {
+      // the bin's one key (remaining is 1): its owner publishes it
+#pragma unroll
+      for (int u = 0; u < PER; ++u)
+        if (key_index<PER>(u) < n && (kr[u] & pmask) == prefix) s_bcast[3] = kr[u];
+      __syncthreads();
+      prefix = s_bcast[3];
+      __syncthreads();
+      break;
+    }
   }
   thr = prefix;
   need = remaining;
 }
 
-// Index-ordered compaction of the selection; calls emit(i, pos) for each selected
-// index i with its position pos in index order, skip(i) for the others.  Wave w owns
-// the contiguous segment [w*seg, (w+1)*seg) and reads it 64 consecutive keys at a time
-// (conflict-free LDS reads; threads owning contiguous chunks read with a stride of the
-// chunk length, a 32-way bank conflict at 16 keys per thread).  Each wave counts its
-// keys above and equal to thr; one exchange gives every wave its first position and
-// its first rank among the equal keys (of which the lowest `need` indices are taken);
-// positions inside a wave come from ballots.
-template <typename Emit, typename Skip>
-__device__ void compact_selected(const uint32_t* keys, int n, uint32_t thr, int need, int* s_wave, Emit emit,
+// Index-ordered compaction of the selection from the register keys (key_index: each
+// wave owns a contiguous segment and reads it 64 consecutive keys per slot); calls
+// emit(i, pos, key) for each selected index i with its position pos in index order,
+// skip(i) for the others.  Each wave counts its keys above and equal to thr; one
+// exchange gives every wave its first position and its first rank among the equal
+// keys (of which the lowest `need` indices are taken); positions inside a wave come
+// from ballots.
+template <int PER, typename Emit, typename Skip>
+__device__ void compact_selected(const uint32_t (&kr)[PER], int n, uint32_t thr, int need, int* s_wave, Emit emit,
                                  Skip skip) {
   __shared__ int s_gt[SEL_THREADS / 64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int seg = (((n + nw - 1) / nw) + 63) & ~63;
-  const int s0 = min(n, wave * seg), s1 = min(n, s0 + seg);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   auto mbcnt = [&](uint64_t m) {
     return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
   };
   int gt_w = 0, eq_w = 0;
-  for (int r0 = s0; r0 < s1; r0 += 64) {  // wave-uniform trip count
-    const int i = r0 + lane;
-    const bool v = i < s1;
-    const uint32_t k = v ? keys[i] : 0u;
-    gt_w += (int)__builtin_popcountll(__ballot(v && k > thr));
-    eq_w += (int)__builtin_popcountll(__ballot(v && k == thr));
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const bool v = key_index<PER>(u) < n;
+    gt_w += (int)__builtin_popcountll(__ballot(v && kr[u] > thr));
+    eq_w += (int)__builtin_popcountll(__ballot(v && kr[u] == thr));
   }
   if (lane == 0) {
     s_wave[wave] = eq_w;
@@ -135,16 +173,17 @@ __device__ void compact_selected(const uint32_t* keys, int n, uint32_t thr, int 
     eqr += eqq;
   }
   __syncthreads();  // callers reuse s_wave
-  for (int r0 = s0; r0 < s1; r0 += 64) {
-    const int i = r0 + lane;
-    const bool v = i < s1;
-    const uint32_t k = v ? keys[i] : 0u;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = key_index<PER>(u);
+    const bool v = i < n;
+    const uint32_t k = kr[u];
     const bool eq = v && k == thr;
     const uint64_t em = __ballot(eq);
     const bool take = (v && k > thr) || (eq && eqr + mbcnt(em) < need);
     const uint64_t tm = __ballot(take);
     if (take)
-      emit(i, pos + mbcnt(tm));
+      emit(i, pos + mbcnt(tm), k);
     else if (v)
       skip(i);
     eqr += (int)__builtin_popcountll(em);
@@ -177,6 +216,8 @@ __global__ __launch_bounds__(256) void ec_prep_kernel(const float* __restrict__ 
   }
 }
 
+// PER: keys per thread held in registers (S <= PER * SEL_THREADS)
+template <int PER>
 __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __restrict__ logits, int B, int S, int E,
                                                                 int C, int order, int64_t* __restrict__ idx,
                                                                 float* __restrict__ w,
@@ -184,31 +225,27 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
                                                                 int32_t* __restrict__ offsets,
                                                                 int32_t* __restrict__ src_row,
                                                                 float* __restrict__ src_w) {
-  __shared__ uint32_t keys[SEL_MAX_S];
   __shared__ uint64_t sorted[SEL_MAX_C];
-  __shared__ uint32_t hist[256 * (SEL_THREADS / 64)];
-  __shared__ uint32_t bc[2];
+  __shared__ uint32_t hist[RS_BINS];
+  __shared__ uint32_t bc[4];
   __shared__ int s_wave[SEL_THREADS / 64];
   __shared__ float s_red[SEL_THREADS / 64];
   const int b = blockIdx.x / E, e = blockIdx.x % E;
   const float* lg = logits + ((int64_t)b * E + e) * S;  // the transposed logits (ec_prep_kernel)
 
   // the sequence's column of logits: all of a thread's loads in flight at once
-  constexpr int PER = SEL_MAX_S / SEL_THREADS;
   float v[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
-    const int i = threadIdx.x + u * SEL_THREADS;
+    const int i = key_index<PER>(u);
     v[u] = i < S ? lg[i] : 0.0f;
   }
   float mx = -INFINITY;
+  uint32_t kr[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
-    const int i = threadIdx.x + u * SEL_THREADS;
-    if (i < S) {
-      keys[i] = order_key(v[u]);
-      mx = fmaxf(mx, v[u]);
-    }
+    kr[u] = order_key(v[u]);
+    if (key_index<PER>(u) < S) mx = fmaxf(mx, v[u]);
   }
   mx = wave_max(mx);
   if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
@@ -220,12 +257,12 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
   float den = 0.0f;
 #pragma unroll
   for (int u = 0; u < PER; ++u)
-    if (threadIdx.x + u * SEL_THREADS < S) den += __expf(v[u] - mx);
+    if (key_index<PER>(u) < S) den += __expf(v[u] - mx);
   den = block_sum(den, s_red);
 
   uint32_t thr;
   int need;
-  radix_select_desc(keys, S, C, hist, bc, thr, need);
+  radix_select_desc(kr, S, C, hist, bc, thr, need);
 
   int Cp = 1;
   while (Cp < C) Cp <<= 1;
@@ -235,9 +272,9 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
   // the others were written by ec_prep_kernel; the selected ones get their rows with
   // the weights below)
   compact_selected(
-      keys, S, thr, need, s_wave,
-      [&](int i, int pos) {
-        if (pos < C) sorted[pos] = ((uint64_t)keys[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+      kr, S, thr, need, s_wave,
+      [&](int i, int pos, uint32_t k) {
+        if (pos < C) sorted[pos] = ((uint64_t)k << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
       },
       [&](int) {});
   __syncthreads();
@@ -245,8 +282,7 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
   // sum whichever output order is asked for)
   float psel = 0.0f;
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
-    const int s = (int)(0xffffffffu - (uint32_t)(sorted[c] & 0xffffffffu));
-    psel += __expf(key_value(keys[s]) - mx) / den;
+    psel += __expf(key_value((uint32_t)(sorted[c] >> 32)) - mx) / den;
   }
   psel = block_sum(psel, s_red);
   if (order == 1) {
@@ -316,7 +352,7 @@ __global__ __launch_bounds__(SEL_THREADS) void ec_select_kernel(const float* __r
   const int64_t BC = (int64_t)B * C;
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
     const int s = (int)(0xffffffffu - (uint32_t)(sorted[c] & 0xffffffffu));
-    const float p = __expf(key_value(keys[s]) - mx) / den;
+    const float p = __expf(key_value((uint32_t)(sorted[c] >> 32)) - mx) / den;
     const float wv = p * inv;
     const int64_t o = ((int64_t)b * E + e) * C + c;
     idx[o] = s;
@@ -354,49 +390,59 @@ __global__ __launch_bounds__(256) void mod_logits_kernel(const uint16_t* __restr
   if (lane == 0) r[t] = acc;
 }
 
+template <int PER>
 __global__ __launch_bounds__(SEL_THREADS) void mod_select_kernel(const float* __restrict__ r, int S, int keep,
                                                                  int64_t* __restrict__ sel_idx,
                                                                  float* __restrict__ sel_w,
                                                                  int32_t* __restrict__ token_rows,
                                                                  int32_t* __restrict__ out_map) {
-  __shared__ uint32_t keys[SEL_MAX_S];
-  __shared__ uint32_t hist[256 * (SEL_THREADS / 64)];
-  __shared__ uint32_t bc[2];
+  __shared__ float s_p[SEL_MAX_S];  // exp(r - max) of the kept tokens, by output position
+  __shared__ uint32_t hist[RS_BINS];
+  __shared__ uint32_t bc[4];
   __shared__ int s_wave[SEL_THREADS / 64];
   __shared__ float s_red[SEL_THREADS / 64];
+  __shared__ uint32_t s_kmax;
   const int b = blockIdx.x;
   const float* rb = r + (int64_t)b * S;
-  for (int i = threadIdx.x; i < S; i += blockDim.x) keys[i] = order_key(rb[i]);
+  if (threadIdx.x == 0) s_kmax = 0u;
   __syncthreads();
+  uint32_t kr[PER];
+  uint32_t kmax = 0u;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = key_index<PER>(u);
+    kr[u] = i < S ? order_key(rb[i]) : 0u;
+    kmax = kr[u] > kmax ? kr[u] : kmax;
+  }
+  // the largest key (its value is the max over the sequence: fmaxf's result on
+  // non-NaN scores; all NaN: key 0, max -inf)
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t q = (uint32_t)__shfl_xor((int)kmax, o, 64);
+    kmax = q > kmax ? q : kmax;
+  }
+  if ((threadIdx.x & 63) == 0) atomicMax(&s_kmax, kmax);
+  __syncthreads();
+  const float mx = s_kmax == 0u ? -INFINITY : key_value(s_kmax);
   uint32_t thr;
   int need;
-  radix_select_desc(keys, S, keep, hist, bc, thr, need);
-  // max over the kept logits = max over the sequence (the top element is kept)
-  float mx = -INFINITY;
-  for (int i = threadIdx.x; i < S; i += blockDim.x) mx = fmaxf(mx, rb[i]);
-  mx = wave_max(mx);
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  mx = s_red[0];
-  for (int q = 1; q < SEL_THREADS / 64; ++q) mx = fmaxf(mx, s_red[q]);
-  __syncthreads();
-  // pass 1: positions + softmax denominator over the kept tokens (mod.py:112)
+  radix_select_desc(kr, S, keep, hist, bc, thr, need);
+  // positions + softmax denominator over the kept tokens (mod.py:112); a key's value
+  // is its score (-0.0 reads as +0.0: the same exp)
   float den = 0.0f;
-  compact_selected(keys, S, thr, need, s_wave, [&](int i, int pos) {
+  compact_selected(kr, S, thr, need, s_wave, [&](int i, int pos, uint32_t k) {
     if (pos >= keep) return;
     const int64_t o = (int64_t)b * keep + pos;
     sel_idx[o] = i;
     token_rows[o] = (int32_t)((int64_t)b * S + i);
     out_map[(int64_t)b * S + i] = (int32_t)o;
-    den += __expf(rb[i] - mx);
+    const float e = __expf(key_value(k) - mx);
+    s_p[pos] = e;
+    den += e;
   }, [&](int i) { out_map[(int64_t)b * S + i] = -1; });
   den = block_sum(den, s_red);
   const float inv = 1.0f / den;
-  __syncthreads();
-  for (int p = threadIdx.x; p < keep; p += blockDim.x) {
-    const int64_t o = (int64_t)b * keep + p;
-    sel_w[o] = __expf(rb[sel_idx[o]] - mx) * inv;
-  }
+  for (int p = threadIdx.x; p < keep; p += blockDim.x) sel_w[(int64_t)b * keep + p] = s_p[p] * inv;
 }
 
 }  // namespace
@@ -424,8 +470,20 @@ extern "C" int kmoe_ec_select(const float* logits, int B, int64_t S, int E, int6
   float* lt = static_cast<float*>(workspace);
   hipLaunchKernelGGL(ec_prep_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>((int64_t)B * S, 64)), dim3(256), 0, s,
                      logits, B, (int)S, E, lt, src_row);
-  hipLaunchKernelGGL(ec_select_kernel, dim3((unsigned)(B * E)), dim3(SEL_THREADS), 0, s, lt, B, (int)S, E, (int)C,
-                     order, idx, w, row_token, offsets, src_row, src_w);
+#define KMOE_EC_SELECT(P_)                                                                                      \
+  hipLaunchKernelGGL(ec_select_kernel<P_>, dim3((unsigned)(B * E)), dim3(SEL_THREADS), 0, s, lt, B, (int)S, E, (int)C, \
+                     order, idx, w, row_token, offsets, src_row, src_w)
+  if (S <= SEL_THREADS)
+    KMOE_EC_SELECT(1);
+  else if (S <= 2 * SEL_THREADS)
+    KMOE_EC_SELECT(2);
+  else if (S <= 4 * SEL_THREADS)
+    KMOE_EC_SELECT(4);
+  else if (S <= 8 * SEL_THREADS)
+    KMOE_EC_SELECT(8);
+  else
+    KMOE_EC_SELECT(16);
+#undef KMOE_EC_SELECT
   return kmoe::check_launch("kmoe_ec_select");
 }
 
@@ -448,7 +506,19 @@ extern "C" int kmoe_mod_select(const void* x, int B, int64_t S, int d, const voi
   if (x)  // else the caller's logits are used as they are
     hipLaunchKernelGGL(mod_logits_kernel, dim3((unsigned)kmoe::ceil_div<int64_t>(T, 4)), dim3(256), 0, s,
                        static_cast<const uint16_t*>(x), T, d, static_cast<const uint16_t*>(w_mod), logits);
-  hipLaunchKernelGGL(mod_select_kernel, dim3((unsigned)B), dim3(SEL_THREADS), 0, s, logits, (int)S, (int)keep, sel_idx,
-                     sel_w, token_rows, out_map);
+#define KMOE_MOD_SELECT(P_)                                                                                      \
+  hipLaunchKernelGGL(mod_select_kernel<P_>, dim3((unsigned)B), dim3(SEL_THREADS), 0, s, logits, (int)S, (int)keep, \
+                     sel_idx, sel_w, token_rows, out_map)
+  if (S <= SEL_THREADS)
+    KMOE_MOD_SELECT(1);
+  else if (S <= 2 * SEL_THREADS)
+    KMOE_MOD_SELECT(2);
+  else if (S <= 4 * SEL_THREADS)
+    KMOE_MOD_SELECT(4);
+  else if (S <= 8 * SEL_THREADS)
+    KMOE_MOD_SELECT(8);
+  else
+    KMOE_MOD_SELECT(16);
+#undef KMOE_MOD_SELECT
   return kmoe::check_launch("kmoe_mod_select");
 }
