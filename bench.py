@@ -46,8 +46,8 @@ def parse():
     ap.add_argument("--no-block", action="store_true",
                     help="skip the fused FFN-block (RMSNorm + MoE + residual) pass")
     ap.add_argument("--settle-ms", type=float, default=250.0,
-                    help="after the warm-up steps, keep running untimed forwards until this much wall time has "
-                         "passed since the first one, so the timed region starts at the settled clock")
+                    help="after the warm-up steps and the routing statistics, keep running untimed forwards for "
+                         "this much wall time, right up to the timed region, so that it starts at the settled clock")
     ap.add_argument("--stage-steps", type=int, default=20, help="forwards of the per-stage timing pass")
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
@@ -102,19 +102,9 @@ def run_gpu(args, wl, light=False):
         return layer(x)
 
     with torch.no_grad():
-        t_w = time.perf_counter()
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
-        # clock settle: the GPU's clock ramps over the first tens of milliseconds of load
-        # (5 warm-up forwards left the gate/up GEMM ~9% slower than at the settled clock),
-        # so untimed forwards continue until settle_ms of wall time has passed
-        settle = 0
-        while (time.perf_counter() - t_w) * 1e3 < args.settle_ms:
-            for _ in range(10):
-                step()
-            settle += 10
-            torch.cuda.synchronize()
         # routing statistics of this input (outside the timed region)
         moe = layer.ffn if wl.mod else layer
         if wl.routing == "expert_choice":
@@ -145,6 +135,18 @@ def run_gpu(args, wl, light=False):
             near = {"tokens": int((gap <= NEAR_TIE).sum()), "exact_ties": int((gap == 0).sum()),
                     "of": int(lg.shape[0]), "threshold": NEAR_TIE,
                     "note": "tokens whose k-th and (k+1)-th largest router logits differ by at most the threshold"}
+        # clock settle: the GPU's clock ramps over the first tens of milliseconds of load
+        # (5 warm-up forwards left the gate/up GEMM ~9% slower than at the settled clock),
+        # so untimed forwards continue for settle_ms of wall time.  They run
+        # right up to the timed region: an idle gap before it (host-side statistics) let the
+        # clock overshoot, and the first timed forwards then ran ~30% slower
+        settle = 0
+        t_w = time.perf_counter()
+        while (time.perf_counter() - t_w) * 1e3 < args.settle_ms:
+            for _ in range(10):
+                step()
+            settle += 10
+            torch.cuda.synchronize()
         # timed region: K back-to-back forwards; the only extra work on the stream is
         # a HIP event pair around the gate/up GEMM launch (the roofline kernel) on
         # every EVENT_EVERY-th forward (an event pair costs ~6 us of drain per event
