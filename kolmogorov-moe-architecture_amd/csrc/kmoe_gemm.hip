@@ -941,7 +941,6 @@ __device__ __forceinline__ void wgrad_tn_tile(const GemmArgs& g, uint8_t* lds, i
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lr = lane & 31, lh = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
   const int n0 = nt * 256;
   const __amdgpu_buffer_rsrc_t arsrc =
@@ -952,13 +951,12 @@ __device__ __forceinline__ void wgrad_tn_tile(const GemmArgs& g, uint8_t* lds, i
   auto la_buf = [&](int st) { return lds + st * 2 * TN_TILE; };
   auto lb_buf = [&](int st) { return lds + st * 2 * TN_TILE + TN_TILE; };
 
-  f32x16_t acc[4][4];
+  // 8 x 8 blocks of 16 x 16 per wave (v_mfma_f32_16x16x32_bf16, as the forward tiles)
+  f32x4_t acc[8][8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // block qq < 8: A block 8 wave + qq (tile rows 2b, 2b + 1; lane: row 2b + lane/32,
   // 16-byte chunk lane % 32); qq >= 8: the B block likewise
@@ -988,102 +986,121 @@ __device__ __forceinline__ void wgrad_tn_tile(const GemmArgs& g, uint8_t* lds, i
     uint8_t* base = qq < 8 ? la_buf(st) : lb_buf(st);
     *reinterpret_cast<i32x4_t*>(base + dst[qq & 7]) = stg[qq];
   };
-  // operand fragments of K-substep i: lane group g = lane/16 reads rows
-  // 16 i + 8 (g/2) + (lane%16)/4 (+4), columns base + 16 (g%2) + 4 (lane%4)
-  const int grp = lane >> 4, i16 = lane & 15;
-  const int frow = 8 * (grp >> 1) + (i16 >> 2), fcol = 16 * (grp & 1) + 4 * (i16 & 3);
-  Frag<false> fa[2][4], fb[2][4];
-  auto rd = [&](int st, int i, Frag<false> (&a)[4], Frag<false> (&b)[4]) {
-    const uint8_t* la = la_buf(st);
-    const uint8_t* lb = lb_buf(st);
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) a[mi] = read_frag_tr(la, 16 * i + frow, wm * 128 + mi * 32 + fcol);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = read_frag_tr(lb, 16 * i + frow, wn * 128 + j * 32 + fcol);
+  // operand fragments of K-substep i (32 rows of K): lane group kq = lane/16 takes rows
+  // 32 i + 8 kq .. + 7, lane l%16 one column of a 16-column block: two transpose reads
+  // (rows 8 kq + (l%16)/4 and + 4, columns base + 4 (l%4)) give lane l column base + l%16
+  // at eight consecutive rows, the 16x16x32 operand fragment
+  const int kq = lane >> 4, i16 = lane & 15;
+  const int frow = 8 * kq + (i16 >> 2), fcol = 4 * (i16 & 3);
+  Frag<false> fa[8], fb[2][8];
+  auto rdA = [&](int st, int i, int mb) { fa[mb] = read_frag_tr(la_buf(st), 32 * i + frow, wm * 128 + mb * 16 + fcol); };
+  auto rdB = [&](int st, int i, int nb, Frag<false>& b) {
+    b = read_frag_tr(lb_buf(st), 32 * i + frow, wn * 128 + nb * 16 + fcol);
   };
-  auto mma = [&](const Frag<false> (&a)[4], const Frag<false> (&b)[4]) {
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) mfma<false>(acc[mi][j], a[mi], b[j]);
+  // the tile's pipeline: step kt computes stage kt%2 while the registers hold step kt+1's
+  // data, written into the other stage and reloaded with step kt+2's; one barrier per step.
+  // As in the forward tiles, the MFMAs go in program order, one at a time, each followed
+  // by the LDS reads, block writes or reloads assigned to it (sched_barrier fences).  Two
+  // K = 32 substeps per 64-row step; substep i uses B set fb[i] and the A ring fa: substep
+  // 0 reads substep 1's B fragments (MFMAs 0, 2, .., 14) and each A fragment after its row
+  // block's last MFMA; substep 1 meets the other waves at the barrier after MFMA 31, then
+  // reads the next step's substep-0 fragments from stage nxt.  Block writes into stage nxt
+  // and the reloads of step kt+2 go over substep 0 (from MFMA 16) and substep 1 before the
+  // barrier, each reload two MFMAs after the write that frees its registers.
+  constexpr int GB = 31;
+  auto sub = [&](int kt, auto i_tag, auto last_tag) {
+    constexpr int i = decltype(i_tag)::value;
+    constexpr bool LAST = decltype(last_tag)::value;
+    const int cur = kt & 1, nxt = cur ^ 1;
+    constexpr int NW = LAST ? 0 : NBLK / 2, QB = i == 0 ? 0 : NBLK / 2;
+    constexpr auto w_at = [](int w) constexpr { return i == 0 ? 16 + 6 * w : 4 * w; };
+    constexpr auto post_at = [](int k, int kind, int idx) constexpr {
+      const int e0 = GB + 2 + 2 * k;
+      const int e1 = kind == 1 ? idx * 8 + 7 : 0;
+      const int at = e0 > e1 ? e0 : e1;
+      return at < 63 ? at : 63;
+    };
+    static_for<0, 64>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+      constexpr int mb = g / 8, nb = g % 8;
+      // transposed product: lane l holds row m0 + .. + l%16, columns 4 (l/16) .. + 3
+      acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[i][nb].v, fa[mb].v, acc[mb][nb], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, NW>([&](auto wc) {
+        constexpr int w = decltype(wc)::value;
+        if constexpr (w_at(w) == g) write_block(QB + w, nxt);
+      });
+      static_for<0, NW>([&](auto wc) {
+        constexpr int w = decltype(wc)::value;
+        if constexpr (w_at(w) + 2 == g) load_block(QB + w, kt + 2);
+      });
+      if constexpr (i == 0) {
+        if constexpr (g < 16 && g % 2 == 0) rdB(cur, 1, g / 2, fb[1][g / 2]);
+        if constexpr (nb == 7) rdA(cur, 1, mb);
+      } else if constexpr (!LAST) {
+        if constexpr (g == GB) {
+          wait_lgkmcnt0();
+          barrier_nofence();
+        }
+        // post-barrier reads k: 0: B0, 1: A0, 2 .. 8: B1 .. B7, 9 .. 15: A1 .. A7
+        static_for<0, 16>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          constexpr int kind = k == 0 ? 0 : k == 1 ? 1 : k < 9 ? 0 : 1;
+          constexpr int idx = k == 0 ? 0 : k == 1 ? 0 : k < 9 ? k - 1 : k - 8;
+          if constexpr (post_at(k, kind, idx) == g) {
+            if constexpr (kind == 0)
+              rdB(nxt, 0, idx, fb[0][idx]);
+            else
+              rdA(nxt, 0, idx);
+          }
+        });
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
   };
-  // the NT tile's pipeline: step kt computes stage kt%2 while the registers hold step
-  // kt+1's data, written into the other stage over the first substeps and reloaded
-  // with step kt+2's; one barrier per step
-  constexpr int RD = 16;  // transpose reads per substep (4 A + 4 B fragments, 2 each)
-  constexpr int C1 = (NBLK * 6 + 8) / 16, C2 = (NBLK * 11 + 8) / 16;
   for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 0);
   for (int qq = 0; qq < NBLK; ++qq) write_block(qq, 0);
   for (int qq = 0; qq < NBLK; ++qq) load_block(qq, 1);
   wait_lgkmcnt0();
   barrier_nofence();
-  rd(0, 0, fa[0], fb[0]);
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) rdB(0, 0, nb, fb[0][nb]);
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) rdA(0, 0, mb);
   auto step = [&](int kt, auto last_tag) {
-    constexpr bool LAST = decltype(last_tag)::value;
-    const int cur = kt & 1, nxt = cur ^ 1;
-    static_for<0, 4>([&](auto ic) {
-      constexpr int i = decltype(ic)::value;
-      constexpr int bi = i & 1;
-      constexpr int q0 = i == 0 ? 0 : i == 1 ? C1 : i == 2 ? C2 : NBLK;
-      constexpr int q1 = i == 0 ? C1 : i == 1 ? C2 : NBLK;
-      constexpr int nq = LAST ? 0 : q1 - q0;
-      constexpr bool RDN = i + 1 < 4 || !LAST;
-      if constexpr (i + 1 < 4) {
-        rd(cur, i + 1, fa[bi ^ 1], fb[bi ^ 1]);
-      } else if constexpr (!LAST) {
-        wait_lgkmcnt0();
-        barrier_nofence();
-        rd(nxt, 0, fa[bi ^ 1], fb[bi ^ 1]);
-      }
-      if constexpr (nq > 0) {
-        static_for<q0, q1>([&](auto qc) { write_block(decltype(qc)::value, nxt); });
-        static_for<q0, q1>([&](auto qc) { load_block(decltype(qc)::value, kt + 2); });
-      }
-      mma(fa[bi], fb[bi]);
-      sched_spread<16, (RDN ? RD : 0), nq, nq>();
-      __builtin_amdgcn_sched_barrier(0);
-    });
+    sub(kt, std::integral_constant<int, 0>{}, last_tag);
+    sub(kt, std::integral_constant<int, 1>{}, last_tag);
   };
   for (int kt = 0; kt + 1 < nk; ++kt) step(kt, std::false_type{});
   step(nk - 1, std::true_type{});
 
-  // ---- epilogue, straight from the accumulators: acc[mi][j][r] is row
-  // wm*128 + mi*32 + 8(r/4) + 4 lh + r%4, column wn*128 + j*32 + lr of the tile.
+  // ---- epilogue: acc[mb][nb][t] is row wm*128 + mb*16 + l%16, column wn*128 + nb*16 +
+  // 4 (l/16) + t of the tile
   if constexpr (OUT == OUT_F32) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-          const int col = n0 + wn * 128 + j * 32 + lr;
-          if (row < M && col < g.n_valid) g.Cf[(int64_t)row * g.ldc + col] = acc[mi][j][r];
+        for (int t = 0; t < 4; ++t) {
+          const int row = m0 + wm * 128 + mb * 16 + i16;
+          const int col = n0 + wn * 128 + nb * 16 + 4 * kq + t;
+          if (row < M && col < g.n_valid) g.Cf[(int64_t)row * g.ldc + col] = acc[mb][nb][t];
         }
   } else {
-    // bf16 through LDS (rows padded by 16 bytes), then 16-byte row stores: pairs are
-    // formed across neighbouring lanes with DPP (an even lane packs its own and its right
-    // neighbour's value of row 2p, an odd lane its left neighbour's and its own of row
-    // 2p+1)
+    // bf16 through LDS (rows padded by 16 bytes): a lane's four columns as 8 bytes, then
+    // 16-byte row stores
     constexpr int OSTR = 256 * 2 + 16;
-    const bool odd = lr & 1;
     __syncthreads();
-    uint8_t* const wbase = lds + (wm * 128 + 4 * lh + (odd ? 1 : 0)) * OSTR + (wn * 128 + lr - (odd ? 1 : 0)) * 2;
+    uint8_t* const wbase = lds + (wm * 128 + i16) * OSTR + (wn * 128 + 4 * kq) * 2;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-      for (int p = 0; p < 8; ++p)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float a = acc[mi][j][2 * p], b = acc[mi][j][2 * p + 1];
-          const float a_next = __builtin_bit_cast(
-              float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, a), 0x101, 0xf, 0xf, false));
-          const float b_prev = __builtin_bit_cast(
-              float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(uint32_t, b), 0x111, 0xf, 0xf, false));
-          const float lo = odd ? b_prev : a, hi = odd ? b : a_next;
-          const uint32_t packed = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
-          *reinterpret_cast<uint32_t*>(wbase + (mi * 32 + 8 * (p >> 1) + 2 * (p & 1)) * OSTR + j * 64) = packed;
-        }
+      for (int nb = 0; nb < 8; ++nb) {
+        const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{acc[mb][nb][0], acc[mb][nb][1]}, bf16x2_t));
+        const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{acc[mb][nb][2], acc[mb][nb][3]}, bf16x2_t));
+        *reinterpret_cast<i32x2_t*>(wbase + mb * 16 * OSTR + nb * 32) = i32x2_t{(int)lo, (int)hi};
+      }
     __syncthreads();
     for (int c = tid; c < BM * 32; c += GEMM_THREADS) {
       const int trow = c >> 5, tc = (c & 31) * 8;  // tile row, first column of the 8
