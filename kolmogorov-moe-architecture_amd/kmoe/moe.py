@@ -17,7 +17,9 @@ drop), the expert-choice MoELayer, and Router / ExpertChoiceRouter /
 GroupedExperts / GroupedExpertsExpertChoice called on their own (the reference's
 distillation code trains them so, distill.py:289-314), balanced routing included (its
 weights' backward is the top-k renormalisation's, without the + 1e-9 of moe.py:411,
-a relative difference below 1e-8).  fp8 experts are forward-only and raise in backward.
+a relative difference below 1e-8).  fp8 experts train straight-through on their bf16
+master weights: the gradients pass the e4m3 quantisers unchanged and multiply by the
+dequantised operands the fp8 GEMMs took.
 """
 from __future__ import annotations
 
@@ -44,7 +46,7 @@ class _ForwardOnly(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
-        raise NotImplementedError("kmoe: the MoE backward pass is not implemented (forward-only kernels)")
+        raise NotImplementedError("kmoe: no HIP backward for this configuration (d_ff_expert not a multiple of 8)")
 
 
 def _forward_only(y, *inputs):
