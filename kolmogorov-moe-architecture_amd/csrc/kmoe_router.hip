@@ -16,22 +16,23 @@
 
 namespace {
 
-constexpr int RT_TOK = 64;        // tokens per workgroup
-constexpr int RT_THREADS = 256;   // 4 waves: 2 (token halves) x 2 (hidden halves)
+constexpr int RT_TOK = 64;        // tokens per workgroup (the aux partials and block histograms are per 64 tokens)
+constexpr int RT_THREADS = 256;   // 4 waves: 2 (token halves) x 2 (hidden halves); 32-token tiles: 4 hidden quarters
 constexpr int RT_HID = KMOE_ROUTER_HIDDEN;
 // padded LDS row strides (floats) of the hidden tile and of w_out: 2 mod 32, so the 32
 // lanes (row i, k) of a 16x16x4 MFMA operand read (banks 2i + k) are conflict free
 constexpr int HSTR = RT_HID + 2;
 constexpr int WOS = RT_HID + 2;
-// One K-step covers RKB bytes of every row (RKB = 128 or 256: 64 or 128 bf16).
-template <int RKB>
+// One K-step covers RKB bytes of every row (RKB = 128 or 256: 64 or 128 bf16); TOK
+// tokens per workgroup (64, or 32 for the small grids of k = 0 routers, below).
+template <int RKB, int TOK = RT_TOK>
 struct RtGeom {
-  static constexpr int XT = RT_TOK * RKB;      // x tile of one K-step (64 rows)
+  static constexpr int XT = TOK * RKB;         // x tile of one K-step (TOK rows)
   static constexpr int WT = RT_HID * RKB;      // w_in tile of one K-step (128 rows)
   static constexpr int STAGE = XT + WT;
   static constexpr int RPB = 1024 / RKB;       // rows per 1 KiB load block
   static constexpr int CPR = RKB / 16;         // 16-byte chunks per row
-  static constexpr int XBLK = RT_TOK / RPB / 4;  // x load blocks per wave per K-step
+  static constexpr int XBLK = TOK / RPB / 4;   // x load blocks per wave per K-step
   static constexpr int WBLK = RT_HID / RPB / 4;  // w_in load blocks per wave per K-step
   static constexpr int LOADS = XBLK + WBLK;    // direct-to-LDS instructions per wave per K-step
   // Byte offset of 16-byte chunk `chunk` of row `row`: the XOR spreads the 16 lanes
@@ -42,9 +43,9 @@ struct RtGeom {
 };
 // K pipeline depth: as many stages as fit beside w_out (NE rows, at least 16, of WOS
 // fp32), the block's expert counts and the RMS scales
-template <int NE, int RKB>
+template <int NE, int RKB, int TOK = RT_TOK>
 constexpr int rt_stages() {
-  return (160 * 1024 - (NE < 16 ? 16 : NE) * WOS * 4 - NE * 4 - RT_TOK * 4) / RtGeom<RKB>::STAGE;
+  return (160 * 1024 - (NE < 16 ? 16 : NE) * WOS * 4 - NE * 4 - RT_TOK * 4) / RtGeom<RKB, TOK>::STAGE;
 }
 
 // RMS: the router input is RMSNorm(x) (embeddings.py:167-195) with the norm weight
@@ -52,7 +53,10 @@ constexpr int rt_stages() {
 // x fragments it reads anyway, scales each token's hidden pre-activation by
 // r = 1/sqrt(mean(x^2) + eps) (the scale commutes with the d -> 128 product) and
 // writes r to rscale for the expert GEMM.
-template <int NE, int RKB, bool RMS = false>
+// TOK = 32 (k = 0, no aux partials, no block histograms; chosen when 64-token tiles
+// would leave CUs idle): each wave computes all 32 tokens x a quarter of the hidden
+// units, and the epilogue's layer 2 and softmax run on the first 32 token slots.
+template <int NE, int RKB, bool RMS = false, int TOK = RT_TOK>
 __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __restrict__ x,
                                                             const int32_t* __restrict__ row_index, int64_t T, int d,
                                                             const uint16_t* __restrict__ w_in,
@@ -63,8 +67,10 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
                                                             float* __restrict__ hidden_pre, float eps,
                                                             float* __restrict__ rscale,
                                                             int32_t* __restrict__ block_counts) {
-  using G = RtGeom<RKB>;
-  constexpr int RT_STAGES = rt_stages<NE, RKB>();
+  using G = RtGeom<RKB, TOK>;
+  constexpr int RT_STAGES = rt_stages<NE, RKB, TOK>();
+  constexpr int NH = TOK == 64 ? 2 : 1;  // 32-wide hidden blocks per wave
+  static_assert(TOK == 64 || TOK == 32, "token tile");
   constexpr int RT_STAGE = G::STAGE;
   static_assert(RT_STAGES >= 2, "K pipeline");
   static_assert(RT_STAGES * RT_STAGE >= (RT_TOK * HSTR + 2 * RT_TOK * (NE + 4) + RT_TOK) * 4,
@@ -85,8 +91,9 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, lh = lane >> 5;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int64_t tok0 = (int64_t)blockIdx.x * RT_TOK;
+  // wave (wm, wn): tokens wm*32 .. +31, hidden units wn*32*NH .. +32*NH-1
+  const int wm = TOK == 64 ? (wave & 1) : 0, wn = TOK == 64 ? (wave >> 1) : wave;
+  const int64_t tok0 = (int64_t)blockIdx.x * TOK;
 
   // ---- per-lane sources of the direct-to-LDS loads (block q fills tile rows
   // [RPB q, RPB q + RPB), lane l lands at byte 16*l of the block: row RPB q + l/CPR,
@@ -112,12 +119,13 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
     wsrc[q] = (uint32_t)tr * (uint32_t)d * 2u + (uint32_t)chunk_of(tr);
   }
   const uint8_t* wbase = reinterpret_cast<const uint8_t*>(w_in);
-  // Workgroups walk K from different starting steps (blockIdx.x mod the step count):
-  // with every workgroup at the same K offset of 4 KiB-strided rows at once, the
-  // loads concentrate on a few memory channels (measured: 22% slower cold-cache).
-  // The sum order over K then depends on the workgroup, deterministically.
+  // Workgroups walk K from different starting steps (the 64-token block index mod the
+  // step count): with every workgroup at the same K offset of 4 KiB-strided rows at
+  // once, the loads concentrate on a few memory channels (measured: 22% slower
+  // cold-cache).  The sum order over K then depends on the token's 64-token block,
+  // deterministically and the same for both tile sizes.
   const int nk_all = d * 2 / RKB;
-  const int k_rot = (int)(blockIdx.x % (unsigned)nk_all);
+  const int k_rot = (int)((uint64_t)(tok0 / RT_TOK) % (uint64_t)nk_all);
   auto issue = [&](int kt) {
     uint8_t* st = smem + (kt % RT_STAGES) * RT_STAGE;
     const int kr = kt + k_rot;
@@ -130,11 +138,11 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
       dma16_to_lds(wbase + wsrc[q] + kb, (KMOE_LDS void*)(st + G::XT + (wave * G::WBLK + q) * 1024));
   };
 
-  // ---- layer 1 on MFMA: wave (wm, wn) computes 32 tokens x 64 hidden; the next
+  // ---- layer 1 on MFMA: wave (wm, wn) computes 32 tokens x 32*NH hidden; the next
   // substep's fragments are read before the current substep's MFMAs
-  f32x16_t acc[2];
+  f32x16_t acc[NH];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < NH; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
   const int nk = d * 2 / RKB;
@@ -176,15 +184,15 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
     auto rdf = [&](int i, int buf) {
       const int ch = 2 * i + lh;
       a[buf] = *reinterpret_cast<const bf16x8_t*>(xt + G::swz(wm * 32 + lr, ch));
-      b0[buf] = *reinterpret_cast<const bf16x8_t*>(wt + G::swz(wn * 64 + lr, ch));
-      b1[buf] = *reinterpret_cast<const bf16x8_t*>(wt + G::swz(wn * 64 + 32 + lr, ch));
+      b0[buf] = *reinterpret_cast<const bf16x8_t*>(wt + G::swz(wn * 32 * NH + lr, ch));
+      if constexpr (NH == 2) b1[buf] = *reinterpret_cast<const bf16x8_t*>(wt + G::swz(wn * 64 + 32 + lr, ch));
     };
     rdf(0, 0);
 #pragma unroll
     for (int i = 0; i < NSUB; ++i) {
       if (i + 1 < NSUB) rdf(i + 1, (i + 1) & 1);
       acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i & 1], b0[i & 1], acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i & 1], b1[i & 1], acc[1], 0, 0, 0);
+      if constexpr (NH == 2) acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i & 1], b1[i & 1], acc[1], 0, 0, 0);
       if constexpr (RMS) {
         // the two waves of a token half read the same x fragments: one of them sums
         if (wn == 0) {
@@ -223,23 +231,24 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   }
   __syncthreads();  // stage buffers are reused below
 
-  // SiLU, then to LDS: acc[j][r] is hidden wn*64+j*32+lr of token wm*32+8*(r/4)+4*lh+r%4
+  // SiLU, then to LDS: acc[j][r] is hidden wn*32*NH+j*32+lr of token wm*32+8*(r/4)+4*lh+r%4
   // (training: the pre-activation is also kept for the backward)
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < NH; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int m = wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+      const int hcol = wn * 32 * NH + j * 32 + lr;
       const float pre = RMS ? acc[j][r] * rs_l[m] : acc[j][r];
-      hs[m * HSTR + wn * 64 + j * 32 + lr] = silu_fast_f32(pre);
-      if (hidden_pre && tok0 + m < T) hidden_pre[(tok0 + m) * RT_HID + wn * 64 + j * 32 + lr] = pre;
+      hs[m * HSTR + hcol] = silu_fast_f32(pre);
+      if (hidden_pre && tok0 + m < T) hidden_pre[(tok0 + m) * RT_HID + hcol] = pre;
     }
   __syncthreads();
 
   // ---- layer 2 on v_mfma_f32_16x16x4_f32 (fp32 operands): wave w computes tokens
   // [16w, 16w + 16) x every 16-expert block; operand lane l holds row l%16 at k = l/16,
   // result register r of lane l is (token 4(l/16) + r, expert l%16)
-  {
+  if (wave * 16 < TOK) {
     constexpr int NEB = NEP / 16;
     const int i16 = lane & 15, k4 = lane >> 4;
     f32x4_t l2[NEB];
@@ -268,7 +277,7 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
 
   // ---- softmax, top-k, outputs: four lanes per token (lane part p holds the logits of
   // experts p + 4q in registers), merged with shuffles inside each group of four
-  const int64_t ntok = T - tok0 < RT_TOK ? T - tok0 : RT_TOK;
+  const int64_t ntok = T - tok0 < TOK ? T - tok0 : TOK;
   {
     constexpr int NQ = NE / 4;
     const int tl = tid >> 2, part = tid & 3;
@@ -277,7 +286,7 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
 #pragma unroll
     for (int q = 0; q < NQ; ++q) L[q] = lg[tl * LGS + part + 4 * q];
     float* P = pe + tl * LGS;
-    if (t < T) {  // the same for the four lanes of a token
+    if (tl < TOK && t < T) {  // the same for the four lanes of a token
       float mx = -INFINITY;
 #pragma unroll
       for (int q = 0; q < NQ; ++q)
@@ -398,23 +407,34 @@ int router_launch(const void* x, const int32_t* row_index, int64_t T, int d, con
   KMOE_REQUIRE(k >= 0 && k <= E && k <= 8, KMOE_ERR_SHAPE, "kmoe_router: k=%d not in [0, min(8, E=%d)]", k, E);
   KMOE_REQUIRE(k == 0 || (topk_idx && topk_w), KMOE_ERR_NULL, "kmoe_router: k>0 needs topk_idx and topk_w");
   if (T == 0) return KMOE_OK;
-  const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(T, RT_TOK));
+  // 32-token tiles when 64-token tiles would leave CUs idle and nothing per 64-token
+  // block is asked for (no top-k histograms, no aux partials)
+  const bool tok32 = k == 0 && !partials && !block_counts &&
+                     kmoe::ceil_div<int64_t>(T, RT_TOK) < (int64_t)kmoe::cu_count();
+  const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(T, tok32 ? 32 : RT_TOK));
   hipStream_t s = kmoe::as_stream(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wi = static_cast<const uint16_t*>(w_in);
   const uint16_t* wo = static_cast<const uint16_t*>(w_out);
   // wide K-steps (256 bytes of every row, half the barriers) when d allows and at
   // least three stages fit; 128-byte steps otherwise
-#define KMOE_ROUTER_LAUNCH2(NE_, RMS_)                                                                         \
-  do {                                                                                                         \
-    if (d % 128 == 0 && rt_stages<NE_, 256>() >= 3)                                                            \
-      hipLaunchKernelGGL((router_kernel<NE_, 256, RMS_>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, \
-                         wo, E, logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre, eps, rscale,     \
-                         block_counts);                                                                        \
-    else                                                                                                       \
-      hipLaunchKernelGGL((router_kernel<NE_, 128, RMS_>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, wi, \
-                         wo, E, logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre, eps, rscale,     \
-                         block_counts);                                                                        \
+#define KMOE_ROUTER_LAUNCH3(NE_, RKB_, RMS_)                                                                    \
+  do {                                                                                                           \
+    if (tok32)                                                                                                   \
+      hipLaunchKernelGGL((router_kernel<NE_, RKB_, RMS_, 32>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, d, \
+                         wi, wo, E, logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre, eps, rscale,   \
+                         block_counts);                                                                          \
+    else                                                                                                         \
+      hipLaunchKernelGGL((router_kernel<NE_, RKB_, RMS_, RT_TOK>), grid, dim3(RT_THREADS), 0, s, xp, row_index, T, \
+                         d, wi, wo, E, logit_bias, k, logits, topk_idx, topk_w, partials, hidden_pre, eps, rscale, \
+                         block_counts);                                                                          \
+  } while (0)
+#define KMOE_ROUTER_LAUNCH2(NE_, RMS_)                       \
+  do {                                                       \
+    if (d % 128 == 0 && rt_stages<NE_, 256>() >= 3)          \
+      KMOE_ROUTER_LAUNCH3(NE_, 256, RMS_);                   \
+    else                                                     \
+      KMOE_ROUTER_LAUNCH3(NE_, 128, RMS_);                   \
   } while (0)
 #define KMOE_ROUTER_LAUNCH(NE_)             \
   do {                                      \
@@ -433,6 +453,7 @@ int router_launch(const void* x, const int32_t* row_index, int64_t T, int d, con
     KMOE_ROUTER_LAUNCH(64);
 #undef KMOE_ROUTER_LAUNCH
 #undef KMOE_ROUTER_LAUNCH2
+#undef KMOE_ROUTER_LAUNCH3
   return kmoe::check_launch("kmoe_router");
 }
 }  // namespace

@@ -63,7 +63,7 @@ class MoDRouter(nn.Module):
             return self.aux_loss
         # forward only: the same kernels without an autograd record, in order on the
         # caller's stream
-        self.aux_loss = ops.mod_aux_bce(ops.router(x2d.detach(), w_a, w_b, 0, stage="mod_aux_router").logits,
+        self.aux_loss = ops.mod_aux_bce(ops.router(x2d.detach(), w_a, w_b, 0, partials=False, stage="mod_aux_router").logits,
                                         token_rows, weight)
         return self.aux_loss
 
@@ -99,7 +99,7 @@ class _ModAuxFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x2d, w_a, w_b, token_rows, weight):
         T = x2d.shape[0]
-        r = ops.router(x2d, w_a, w_b, 0, save_hidden=True, stage="mod_aux_router")
+        r = ops.router(x2d, w_a, w_b, 0, save_hidden=True, partials=False, stage="mod_aux_router")
         ctx.save_for_backward(x2d, r.hidden, r.logits, token_rows)
         ctx.w_b = w_b
         ctx.dtypes = (w_a.dtype, w_b.dtype)

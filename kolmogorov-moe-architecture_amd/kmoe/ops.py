@@ -75,14 +75,14 @@ class RouterOut(NamedTuple):
     logits: torch.Tensor          # (T, E) f32
     idx: Optional[torch.Tensor]   # (T, k) int64
     w: Optional[torch.Tensor]     # (T, k) f32
-    partials: torch.Tensor        # per-block aux partial sums
+    partials: Optional[torch.Tensor]  # per-block aux partial sums (None: router(partials=False))
     hidden: Optional[torch.Tensor] = None  # (T, 128) f32 pre-activation (training router)
     rscale: Optional[torch.Tensor] = None  # (T,) f32 RMSNorm scale 1/sqrt(mean(x^2)+eps) (rms router)
     block_counts: Optional[torch.Tensor] = None  # (ceil(T/64), E) int32 per-block routed counts
 
 
 def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=False,
-           rms_eps=None, hist=True, stage="router") -> RouterOut:
+           rms_eps=None, hist=True, partials=True, stage="router") -> RouterOut:
     """logits/top-k of the reference Router (moe.py:423-462) on the HIP kernel.
 
     x2d: (rows, d) bf16; w_in: (128, d); w_out: (E, 128); row_index: optional
@@ -91,6 +91,9 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=F
     folded into w_in's columns; the result carries the per-token scale (rscale).
     hist (k > 0, not rms): also return each 64-token block's per-expert routed counts,
     which dispatch(block_counts=...) takes instead of counting them again.
+    partials: write the per-block aux partial sums (aux_loss's input); without them and
+    with k = 0 (a router that only needs its logits, like the MoD auxiliary router) the
+    kernel takes 32-token tiles where 64-token tiles would leave CUs idle.
     stage: the name the per-stage timing records the launch under.
     """
     _need_gpu(x2d, w_in, w_out)
@@ -108,8 +111,10 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=F
     logits = torch.empty(T, E, device=dev, dtype=torch.float32)
     idx = torch.empty(T, k, device=dev, dtype=torch.int64) if k > 0 else None
     w = torch.empty(T, k, device=dev, dtype=torch.float32) if k > 0 else None
-    npart = _lib.load().kmoe_router_partials_len(T, E)
-    partials = torch.empty(max(npart, 1), device=dev, dtype=torch.float32)
+    if partials:
+        partials = torch.empty(max(_lib.load().kmoe_router_partials_len(T, E), 1), device=dev, dtype=torch.float32)
+    else:
+        partials = None
     bias = _contig(bias, torch.float32)
     hidden = torch.empty(T, _lib.ROUTER_HIDDEN, device=dev, dtype=torch.float32) if save_hidden else None
     if rms_eps is not None:

@@ -52,6 +52,21 @@ def test_router_parity(dev, T, d, E, k):
     assert np.mean(np.any(idx64 != idx, axis=1)) < 0.01
 
 
+@pytest.mark.parametrize("T,d,E", [(8192, 2048, 1), (8155, 512, 1), (100, 256, 8), (1000, 128, 64), (33, 64, 5)])
+def test_router_logits_only_tiles(dev, T, d, E):
+    """k = 0 without aux partials takes 32-token tiles on small grids: logits and the
+    saved pre-activation bit-identical to the 64-token kernel (same per-token K order),
+    and within the fp64 bar."""
+    x, w_in, w_out = gen(300 + E, (T, d), (128, d), (E, 128))
+    xb, wib, wob = bf16(x).to(dev), bf16(w_in * 0.02).to(dev), bf16(w_out * 0.1).to(dev)
+    r64 = ops.router(xb, wib, wob, 0, save_hidden=True)
+    r32 = ops.router(xb, wib, wob, 0, save_hidden=True, partials=False)
+    torch.cuda.synchronize()
+    assert r32.partials is None
+    assert torch.equal(r32.logits, r64.logits) and torch.equal(r32.hidden, r64.hidden)
+    np.testing.assert_allclose(npf(r32.logits), O.router_logits(npf(xb), npf(wib), npf(wob)), atol=1e-5, rtol=1e-4)
+
+
 def test_router_ties_lowest_index(dev):
     T, d, E = 256, 128, 8
     x, w_in, w_out = gen(7, (T, d), (128, d), (E, 128))
