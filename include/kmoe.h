@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KMOE_ABI_VERSION 1
+#define KMOE_ABI_VERSION 2
 
 /* status codes */
 #define KMOE_OK 0
@@ -69,10 +69,13 @@ int kmoe_pack_layout_version(void);
  * logit (descending; equal logits -> lowest expert index first), and writes the
  * renormalised softmax weights  w_j = p_j / sum_sel p  (moe.py:441,455-460).
  * `partials` (nullable) receives per-block sums for the aux losses; its length in
- * floats is kmoe_router_partials_len(T, E).
+ * floats is kmoe_router_partials_len(T, E).  A block is kmoe_router_block_tokens(T)
+ * tokens: one workgroup of the kernel (32 when ceil(T/32) workgroups fit the device's
+ * compute units at once, else 64; a function of T and the current device only).
  *   x: (rows, d) bf16;  w_in: (128, d) bf16;  w_out: (E, 128) bf16
  *   logits: (T, E) f32; topk_idx: (T, k) int64; topk_w: (T, k) f32          */
 int64_t kmoe_router_partials_len(int64_t T, int E);
+int kmoe_router_block_tokens(int64_t T);
 int kmoe_router(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,
                 const void* w_out, int E, const float* logit_bias, int k, float* logits,
                 int64_t* topk_idx, float* topk_w, float* partials, void* stream);
@@ -120,8 +123,9 @@ int kmoe_dispatch(const void* x, const int32_t* row_index, int64_t T, int d, con
 
 /* kmoe_dispatch with the per-block expert histograms given instead of counted from
  * topk_idx: block_counts[b*E + e] = number of assignments (t, j) with t in
- * [64b, 64b + 64) and topk_idx[t*k + j] == e, as kmoe_router_hist writes them.  Same
- * results as kmoe_dispatch, one launch fewer.  Workspace as kmoe_dispatch.        */
+ * [Bb, Bb + B) and topk_idx[t*k + j] == e, B = kmoe_router_block_tokens(T), as
+ * kmoe_router_hist writes them.  Same results as kmoe_dispatch, one launch fewer.
+ * Workspace as kmoe_dispatch.                                                     */
 int kmoe_dispatch_counted(const void* x, const int32_t* row_index, int64_t T, int d, const int64_t* topk_idx,
                           const void* topk_w, int w_dtype, int k, int E, int64_t capacity,
                           const int32_t* block_counts, int32_t* counts, int32_t* offsets, int32_t* row_token,
@@ -468,8 +472,9 @@ int kmoe_pack_w_in_t(const void* w_in, int w_dtype, int d, void* out, void* stre
  *   w_in_g[j][i] = w_in[j][i] * w_norm[i];  w13 = kmoe_pack_weights(w1 * w_norm[:,None],
  *   w2 * w_norm[:,None], w3, ...).  x is then the un-normalised h.           */
 
-/* kmoe_router_train (hidden_pre nullable) that also writes each 64-token block's
- * per-expert routed counts to block_counts (ceil(T/64) * E int32; k >= 1), the
+/* kmoe_router_train (hidden_pre nullable) that also writes each block's per-expert
+ * routed counts to block_counts (ceil(T/B) * E int32, B = kmoe_router_block_tokens(T);
+ * k >= 1), the
  * histograms kmoe_dispatch_counted takes: the router already holds every token's
  * top-k, so the dispatch need not read topk_idx a second time to count them.      */
 int kmoe_router_hist(const void* x, const int32_t* row_index, int64_t T, int d, const void* w_in,

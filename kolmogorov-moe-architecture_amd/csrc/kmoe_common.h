@@ -26,6 +26,11 @@ void set_error(const char* fmt, ...);
 int check_launch(const char* what);
 // compute units of the current device (cached per device): the grid of persistent kernels
 int cu_count();
+// Tokens per router workgroup for a call over T tokens (32 when 32-token tiles fit the
+// device in one wave of workgroups, else 64): also the token span of one row of the
+// router's aux partials and block histograms, which the aux-loss and dispatch
+// reductions read.
+int router_block_tokens(int64_t T);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

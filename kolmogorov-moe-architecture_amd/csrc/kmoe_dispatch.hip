@@ -89,15 +89,18 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ 
 // block counts like the others (the routed count of each expert), then reduces the
 // router's aux partials and writes the auxiliary losses (aux_reduce_cols / aux_finish:
 // the same sums in the same order as kmoe_aux_loss) instead of a launch of its own.
+// The histograms may be finer than the DTB-token blocks (FUSED_SCAN only): nhb rows of
+// DTB / hper tokens each (the router's 32-token workgroups give hper = 2), so block b
+// starts after histogram row b * hper; the aux partials have the same nhb rows.
 constexpr int FUSED_SCAN_MAX_BLOCKS = 1024;
 template <bool FUSED_SCAN>
 __global__ __launch_bounds__(DTHREADS) void permute_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, int64_t T, int d,
     const int64_t* __restrict__ idx, const void* __restrict__ wsrc, int w_dtype, int k, int E, int64_t capacity,
-    const int32_t* __restrict__ block_counts, int64_t nblk, const int32_t* __restrict__ block_base,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ row_token,
-    int32_t* __restrict__ slot_row, float* __restrict__ slot_w, const float* __restrict__ aux_partials,
-    float w_lb, float w_z, float* __restrict__ aux_out) {
+    const int32_t* __restrict__ block_counts, int64_t nblk, int64_t nhb, int hper,
+    const int32_t* __restrict__ block_base, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ row_token, int32_t* __restrict__ slot_row, float* __restrict__ slot_w,
+    const float* __restrict__ aux_partials, float w_lb, float w_z, float* __restrict__ aux_out) {
   __shared__ int wave_cnt[DTHREADS / 64][KMOE_MAX_EXPERTS];
   __shared__ int running[KMOE_MAX_EXPERTS];
   __shared__ int base_l[KMOE_MAX_EXPERTS];
@@ -131,17 +134,18 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
       // 16 loads in flight per batch (a loop of dependent round trips took most of the
       // kernel's time)
       constexpr int NB = 16;
-      for (int64_t b0 = j; b0 < nblk; b0 += (int64_t)NB * ng) {
+      const int64_t first = (int64_t)blockIdx.x * hper;  // this block's first histogram row
+      for (int64_t b0 = j; b0 < nhb; b0 += (int64_t)NB * ng) {
         int v[NB];
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
           const int64_t b = b0 + (int64_t)u * ng;
-          v[u] = b < nblk ? block_counts[b * E + ex] : 0;
+          v[u] = b < nhb ? block_counts[b * E + ex] : 0;
         }
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
           tot += v[u];
-          if (b0 + (int64_t)u * ng < (int64_t)blockIdx.x) pre += v[u];
+          if (b0 + (int64_t)u * ng < first) pre += v[u];
         }
       }
     }
@@ -187,7 +191,7 @@ __global__ __launch_bounds__(DTHREADS) void permute_kernel(
   }
   __syncthreads();
   if (aux_block) {
-    aux_reduce_cols(aux_partials, nblk, E, wave, DTHREADS / 64, lane, aux_col);
+    aux_reduce_cols(aux_partials, nhb, E, wave, DTHREADS / 64, lane, aux_col);
     __syncthreads();
     if (tid == 0) aux_finish(aux_col, tot_l, T, E, k, w_lb, w_z, aux_out);
     return;
@@ -408,8 +412,12 @@ int dispatch_launch(const void* x, const int32_t* row_index, int64_t T, int d, c
   const int64_t nblk = kmoe::ceil_div<int64_t>(T, DTB);
   int32_t* ws_counts = static_cast<int32_t*>(workspace);
   int32_t* block_base = ws_counts + nblk * E;
-  // the per-block histograms: given (kmoe_router_hist wrote them) or counted here
+  // the per-block histograms: given (kmoe_router_hist wrote them, one row per router
+  // workgroup of kmoe::router_block_tokens(T) tokens) or counted here per DTB tokens
   const int32_t* block_counts = given_counts ? given_counts : ws_counts;
+  const int hb = given_counts ? kmoe::router_block_tokens(T) : DTB;
+  const int64_t nhb = kmoe::ceil_div<int64_t>(T, hb);
+  const int hper = DTB / hb;
   if (T == 0) {
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, (int64_t)0, E, capacity, block_base,
                        counts, offsets);
@@ -423,15 +431,18 @@ int dispatch_launch(const void* x, const int32_t* row_index, int64_t T, int d, c
   const bool fp8 = xperm_dtype == KMOE_DTYPE_FP8_E4M3;
   if (nblk <= FUSED_SCAN_MAX_BLOCKS) {
     hipLaunchKernelGGL(permute_kernel<true>, dim3((unsigned)(nblk + (aux_fused ? 1 : 0))), dim3(DTHREADS), 0, s, xp,
-                       row_index, T, d, topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, block_base,
-                       counts, offsets, row_token, slot_row, slot_w, aux_partials, w_lb, w_z,
+                       row_index, T, d, topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, nhb, hper,
+                       block_base, counts, offsets, row_token, slot_row, slot_w, aux_partials, w_lb, w_z,
                        aux_fused ? aux_out : nullptr);
   } else {
+    // the scan path reads one histogram row per DTB-token block
+    KMOE_REQUIRE(hper == 1, KMOE_ERR_UNSUPPORTED, "kmoe_dispatch: %d-token histograms over %lld tokens", hb,
+                 (long long)T);
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, nblk, E, capacity, block_base, counts,
                        offsets);
     hipLaunchKernelGGL(permute_kernel<false>, dim3((unsigned)nblk), dim3(DTHREADS), 0, s, xp, row_index, T, d,
-                       topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, block_base, counts, offsets,
-                       row_token, slot_row, slot_w, nullptr, 0.0f, 0.0f, nullptr);
+                       topk_idx, topk_w, w_dtype, k, E, capacity, block_counts, nblk, nblk, 1, block_base, counts,
+                       offsets, row_token, slot_row, slot_w, nullptr, 0.0f, 0.0f, nullptr);
   }
   if (aux_out && !aux_fused) {
     const int rc = kmoe_aux_loss(aux_partials, T, E, counts, k, w_lb, w_z, aux_out, s);

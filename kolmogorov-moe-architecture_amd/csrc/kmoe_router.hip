@@ -16,7 +16,7 @@
 
 namespace {
 
-constexpr int RT_TOK = 64;        // tokens per workgroup (the aux partials and block histograms are per 64 tokens)
+constexpr int RT_TOK = 64;        // tokens per workgroup (32 on small grids: kmoe::router_block_tokens)
 constexpr int RT_THREADS = 256;   // 4 waves: 2 (token halves) x 2 (hidden halves); 32-token tiles: 4 hidden quarters
 constexpr int RT_HID = KMOE_ROUTER_HIDDEN;
 // padded LDS row strides (floats) of the hidden tile and of w_out: 2 mod 32, so the 32
@@ -53,9 +53,9 @@ constexpr int rt_stages() {
 // x fragments it reads anyway, scales each token's hidden pre-activation by
 // r = 1/sqrt(mean(x^2) + eps) (the scale commutes with the d -> 128 product) and
 // writes r to rscale for the expert GEMM.
-// TOK = 32 (k = 0, no aux partials, no block histograms; chosen when 64-token tiles
-// would leave CUs idle): each wave computes all 32 tokens x a quarter of the hidden
-// units, and the epilogue's layer 2 and softmax run on the first 32 token slots.
+// TOK = 32 (when all 32-token workgroups fit the device at once): each wave computes
+// all 32 tokens x a quarter of the hidden units, and the epilogue's layer 2, softmax,
+// top-k and per-block outputs run on the first 32 token slots.
 template <int NE, int RKB, bool RMS = false, int TOK = RT_TOK>
 __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __restrict__ x,
                                                             const int32_t* __restrict__ row_index, int64_t T, int d,
@@ -345,8 +345,8 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
           for (int j = 0; j < k; ++j) {
             topk_idx[t * k + j] = sel[j];
             topk_w[t * k + j] = sev[j] * inv;
-            // the block's per-expert routed counts (the dispatch's histogram of these
-            // 64 tokens)
+            // the block's per-expert routed counts (the dispatch's histogram of the
+            // block's TOK tokens)
             if (block_counts) atomicAdd(&cnt_l[sel[j]], 1);
           }
         }
@@ -363,13 +363,13 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
   // ---- logits out: the block's ntok x E floats are contiguous; coalesced copy
   for (int i = tid; i < ntok * E; i += RT_THREADS) logits[tok0 * E + i] = lg[(i / E) * LGS + i % E];
 
-  // ---- per-block aux partials: column c of the block's 64 tokens (c < E: the
+  // ---- per-block aux partials: column c of the block's TOK tokens (c < E: the
   // probabilities, c == E: lse^2) summed by thread c in a fixed order (four running
   // sums over tokens m = 4i + u, then added u = 0..3)
   if (partials && tid <= E) {
     float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
-    for (int m = 0; m < RT_TOK; m += 4)
+    for (int m = 0; m < TOK; m += 4)
 #pragma unroll
       for (int u = 0; u < 4; ++u) sum[u] += tid < E ? pe[(m + u) * LGS + tid] : lse2[m + u];
     partials[(int64_t)blockIdx.x * (E + 1) + tid] = (sum[0] + sum[1]) + (sum[2] + sum[3]);
@@ -389,8 +389,14 @@ __global__ __launch_bounds__(256) void aux_loss_kernel(const float* __restrict__
 
 }  // namespace
 
+namespace kmoe {
+int router_block_tokens(int64_t T) { return T <= 32 * (int64_t)cu_count() ? 32 : RT_TOK; }
+}  // namespace kmoe
+
+extern "C" int kmoe_router_block_tokens(int64_t T) { return kmoe::router_block_tokens(T < 0 ? 0 : T); }
+
 extern "C" int64_t kmoe_router_partials_len(int64_t T, int E) {
-  return kmoe::ceil_div<int64_t>(T, RT_TOK) * (int64_t)(E + 1);
+  return kmoe::ceil_div<int64_t>(T, kmoe::router_block_tokens(T)) * (int64_t)(E + 1);
 }
 
 namespace {
@@ -407,11 +413,11 @@ int router_launch(const void* x, const int32_t* row_index, int64_t T, int d, con
   KMOE_REQUIRE(k >= 0 && k <= E && k <= 8, KMOE_ERR_SHAPE, "kmoe_router: k=%d not in [0, min(8, E=%d)]", k, E);
   KMOE_REQUIRE(k == 0 || (topk_idx && topk_w), KMOE_ERR_NULL, "kmoe_router: k>0 needs topk_idx and topk_w");
   if (T == 0) return KMOE_OK;
-  // 32-token tiles when 64-token tiles would leave CUs idle and nothing per 64-token
-  // block is asked for (no top-k histograms, no aux partials)
-  const bool tok32 = k == 0 && !partials && !block_counts &&
-                     kmoe::ceil_div<int64_t>(T, RT_TOK) < (int64_t)kmoe::cu_count();
-  const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(T, tok32 ? 32 : RT_TOK));
+  // 32-token tiles when they all fit the device at once (64-token tiles would leave
+  // CUs idle); the aux partials and block histograms are then per 32 tokens
+  const int tok = kmoe::router_block_tokens(T);
+  const bool tok32 = tok == 32;
+  const dim3 grid((unsigned)kmoe::ceil_div<int64_t>(T, tok));
   hipStream_t s = kmoe::as_stream(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wi = static_cast<const uint16_t*>(w_in);
@@ -552,7 +558,7 @@ extern "C" int kmoe_aux_loss(const float* partials, int64_t T, int E, const int3
   KMOE_REQUIRE(T > 0, KMOE_ERR_SHAPE, "kmoe_aux_loss: T must be > 0");
   KMOE_REQUIRE(E >= 1 && E <= KMOE_MAX_EXPERTS, KMOE_ERR_SHAPE, "kmoe_aux_loss: E=%d out of range", E);
   KMOE_REQUIRE(!counts || k >= 1, KMOE_ERR_SHAPE, "kmoe_aux_loss: k must be >= 1 with counts");
-  const int64_t nblk = kmoe::ceil_div<int64_t>(T, RT_TOK);
+  const int64_t nblk = kmoe::ceil_div<int64_t>(T, kmoe::router_block_tokens(T));
   hipLaunchKernelGGL(aux_loss_kernel, dim3(1), dim3(256), 0, kmoe::as_stream(stream), partials, nblk, T, E,
                      counts, k, w_lb, w_z, out);
   return kmoe::check_launch("kmoe_aux_loss");

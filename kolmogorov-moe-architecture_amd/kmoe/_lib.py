@@ -33,6 +33,7 @@ _SIGNATURES = {
     "kmoe_abi_version": (_i32, []),
     "kmoe_pack_layout_version": (_i32, []),
     "kmoe_router_partials_len": (_i64, [_i64, _i32]),
+    "kmoe_router_block_tokens": (_i32, [_i64]),
     "kmoe_router": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "kmoe_aux_loss": (_i32, [_vp, _i64, _i32, _vp, _i32, _f32, _f32, _vp, _vp]),
     "kmoe_mod_aux_bce": (_i32, [_vp, _i64, _vp, _i64, _f32, _vp, _vp]),

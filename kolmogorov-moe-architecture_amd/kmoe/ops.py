@@ -78,7 +78,7 @@ class RouterOut(NamedTuple):
     partials: Optional[torch.Tensor]  # per-block aux partial sums (None: router(partials=False))
     hidden: Optional[torch.Tensor] = None  # (T, 128) f32 pre-activation (training router)
     rscale: Optional[torch.Tensor] = None  # (T,) f32 RMSNorm scale 1/sqrt(mean(x^2)+eps) (rms router)
-    block_counts: Optional[torch.Tensor] = None  # (ceil(T/64), E) int32 per-block routed counts
+    block_counts: Optional[torch.Tensor] = None  # (ceil(T/b), E) int32 per-block routed counts, b = router_block_tokens(T)
 
 
 def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=False,
@@ -89,11 +89,11 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=F
     int32 (T,) selecting the rows of x2d that are the tokens.
     rms_eps: route RMSNorm(x) (embeddings.py:167-195) with the norm weight already
     folded into w_in's columns; the result carries the per-token scale (rscale).
-    hist (k > 0, not rms): also return each 64-token block's per-expert routed counts,
-    which dispatch(block_counts=...) takes instead of counting them again.
-    partials: write the per-block aux partial sums (aux_loss's input); without them and
-    with k = 0 (a router that only needs its logits, like the MoD auxiliary router) the
-    kernel takes 32-token tiles where 64-token tiles would leave CUs idle.
+    hist (k > 0, not rms): also return each router block's per-expert routed counts
+    (blocks of router_block_tokens(T) tokens), which dispatch(block_counts=...) takes
+    instead of counting them again.
+    partials: write the per-block aux partial sums (aux_loss's input); False for a router
+    that only needs its logits (like the MoD auxiliary router).
     stage: the name the per-stage timing records the launch under.
     """
     _need_gpu(x2d, w_in, w_out)
@@ -126,7 +126,7 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=F
                       ptr(logits), ptr(idx), ptr(w), ptr(partials), float(rms_eps), ptr(rscale), _stream(x2d))
         return RouterOut(logits, idx, w, partials, None, rscale)
     if hist and k > 0 and T > 0:
-        bc = torch.empty((T + 63) // 64, E, device=dev, dtype=torch.int32)
+        bc = torch.empty(-(-T // router_block_tokens(T)), E, device=dev, dtype=torch.int32)
         with _Stage(stage):
             _lib.call("kmoe_router_hist", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
                       ptr(logits), ptr(idx), ptr(w), ptr(partials), ptr(hidden), ptr(bc), _stream(x2d))
@@ -135,6 +135,13 @@ def router(x2d, w_in, w_out, k, bias=None, row_index=None, T=None, save_hidden=F
         _lib.call("kmoe_router_train", ptr(x2d), ptr(row_index), T, d, ptr(w_in), ptr(w_out), E, ptr(bias), k,
                   ptr(logits), ptr(idx), ptr(w), ptr(partials), ptr(hidden), _stream(x2d))
     return RouterOut(logits, idx, w, partials, hidden)
+
+
+def router_block_tokens(T: int) -> int:
+    """Tokens per router workgroup for a call over T tokens on the current device (32 when
+    32-token tiles fit the device in one wave of workgroups, else 64): the token span of
+    one row of the router's aux partials and block histograms."""
+    return int(_lib.load().kmoe_router_block_tokens(T))
 
 
 def balanced_topk(logits, k):
@@ -236,8 +243,10 @@ def dispatch(x2d, idx, w, E, capacity=0, fp8=False, row_index=None, materialize=
     if aux is not None and (block_counts is None or no_alloc or T == 0):
         raise ValueError("kmoe.dispatch: aux needs block_counts (and T > 0, not no_alloc)")
     if block_counts is not None:
-        if block_counts.dtype != torch.int32 or block_counts.numel() != ((T + 63) // 64) * E:
-            raise ValueError("kmoe.dispatch: block_counts must be int32 (ceil(T/64), E)")
+        hb = router_block_tokens(T)
+        if block_counts.dtype != torch.int32 or block_counts.numel() != -(-T // hb) * E:
+            raise ValueError(f"kmoe.dispatch: block_counts must be int32 (ceil(T/{hb}), E) "
+                             f"(router_block_tokens)")
         if aux is not None:
             partials, w_lb, w_z = aux
             aux_out = torch.empty(3, device=dev, dtype=torch.float32)

@@ -25,9 +25,13 @@ def test_exports_every_header_symbol(lib):
 
 
 def test_version_and_sizes(lib):
-    assert lib.kmoe_abi_version() == 1
+    assert lib.kmoe_abi_version() == 2
     assert lib.kmoe_padded_ff(2816) == 2816 and lib.kmoe_padded_ff(352) == 384
     assert lib.kmoe_router_partials_len(16384, 16) == 256 * 17
+    # 32-token router blocks when ceil(T/32) workgroups fit the 256 compute units at once
+    assert lib.kmoe_router_block_tokens(16384) == 64 and lib.kmoe_router_block_tokens(8193) == 64
+    assert lib.kmoe_router_block_tokens(8192) == 32 and lib.kmoe_router_block_tokens(1) == 32
+    assert lib.kmoe_router_partials_len(8192, 16) == 256 * 17 and lib.kmoe_router_partials_len(33, 4) == 2 * 5
     # packed rows carry 128 bytes of padding after the K-contiguous data
     assert lib.kmoe_packed_w13_bytes(16, 2048, 2816, _lib.DTYPE_BF16) == 16 * 2 * 2816 * (2048 * 2 + 128)
     assert lib.kmoe_packed_w3_bytes(16, 2048, 2816, _lib.DTYPE_FP8_E4M3) == 16 * 2048 * (2816 + 128)

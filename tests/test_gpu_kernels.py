@@ -164,7 +164,8 @@ def test_dispatch_parity(dev, T, k, E, cap, skew):
 @pytest.mark.parametrize("T,d,E,k,rows", [(16384, 2048, 16, 2, False), (1000, 128, 64, 4, False), (33, 64, 5, 1, False),
                                            (3000, 256, 16, 2, True)])
 def test_router_block_counts(dev, T, d, E, k, rows):
-    """kmoe_router_hist's per-64-token-block expert counts = the bincount of its own top-k
+    """kmoe_router_hist's per-block expert counts (blocks of router_block_tokens(T) tokens:
+    32 when the 32-token workgroups fit the device at once) = the bincount of its own top-k
     ids per block (numpy), also with a row_index (MoD's selected rows) and a ragged last
     block; its logits and ids are those of kmoe_router."""
     x, w_in, w_out = gen(300 + E, (T + 100, d), (128, d), (E, 128))
@@ -178,11 +179,29 @@ def test_router_block_counts(dev, T, d, E, k, rows):
     assert r.block_counts is not None and r0.block_counts is None
     assert torch.equal(r.idx, r0.idx) and torch.equal(r.logits, r0.logits)
     idx = r.idx.cpu().numpy()
-    nb = (T + 63) // 64
+    hb = ops.router_block_tokens(T)
+    assert hb == (32 if T <= 32 * torch.cuda.get_device_properties(dev).multi_processor_count else 64)
+    nb = -(-T // hb)
     ref = np.zeros((nb, E), np.int64)
     for b in range(nb):
-        ref[b] = np.bincount(idx[64 * b:64 * b + 64].reshape(-1), minlength=E)
+        ref[b] = np.bincount(idx[hb * b:hb * b + hb].reshape(-1), minlength=E)
     assert np.array_equal(r.block_counts.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("n,E,k", [(4096, 16, 2), (1000, 64, 4), (8192, 8, 8)])
+def test_router_tiles_bit_identical(dev, n, E, k):
+    """The first n tokens of a 16384-token call (64-token workgroups) and a call over those
+    n tokens alone (32-token workgroups) give the same logits, ids and weights bit for
+    bit: a token's K order depends on its 64-token block only."""
+    T, d = 16384, 512
+    x, w_in, w_out = gen(500 + E, (T, d), (128, d), (E, 128))
+    xb, wib, wob = bf16(x).to(dev), bf16(w_in * 0.02).to(dev), bf16(w_out * 0.05).to(dev)
+    assert ops.router_block_tokens(T) == 64 and ops.router_block_tokens(n) == 32
+    big = ops.router(xb, wib, wob, k, save_hidden=True)
+    small = ops.router(xb[:n].contiguous(), wib, wob, k, save_hidden=True)
+    torch.cuda.synchronize()
+    assert torch.equal(small.logits, big.logits[:n]) and torch.equal(small.hidden, big.hidden[:n])
+    assert torch.equal(small.idx, big.idx[:n]) and torch.equal(small.w, big.w[:n])
 
 
 @pytest.mark.parametrize("T,k,E,cap,fp8,mat", [(16384, 2, 16, 2560, False, True), (16384, 2, 16, 0, False, False),
