@@ -552,16 +552,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint8_t* lds, int e
       }
       return;
     }
-    // MFMA after which block write w / its reload go
+    // MFMA after which block write w / its reload go (w < NW; NW1 keeps the division
+    // defined in the instantiations without block writes)
+    constexpr int NW1 = NW > 0 ? NW : 1;
     constexpr auto w_at = [](int w) constexpr {
       if (FULL16) return i == 0 ? 16 + 6 * w : 4 * w;
       const int span = i == 0 ? NMS - 2 : GB - 2;
-      return span > 0 ? 1 + (w * span) / NW : 0;
+      return span > 0 ? 1 + (w * span) / NW1 : 0;
     };
     constexpr auto l_at = [](int w) constexpr {
       if (FULL16) return i == 0 ? 18 + 6 * w : 4 * w + 2;
       const int span = i == 0 ? NMS - 2 : GB - 2;
-      return span > 0 ? 1 + (w * span) / NW : 0;
+      return span > 0 ? 1 + (w * span) / NW1 : 0;
     };
     // substep 0: MFMA after which next-substep read B_j / A_mi goes
     constexpr auto b0_at = [](int j) constexpr { return FULL16 ? 2 * j : (j < NMS ? j : NMS - 1); };
