@@ -54,9 +54,10 @@ def test_router_parity(dev, T, d, E, k):
 
 @pytest.mark.parametrize("T,d,E", [(8192, 2048, 1), (8155, 512, 1), (100, 256, 8), (1000, 128, 64), (33, 64, 5)])
 def test_router_logits_only_tiles(dev, T, d, E):
-    """k = 0 without aux partials takes 32-token tiles on small grids: logits and the
-    saved pre-activation bit-identical to the 64-token kernel (same per-token K order),
-    and within the fp64 bar."""
+    """k = 0 without aux partials (the MoD auxiliary router's call): no partials buffer,
+    logits and the saved pre-activation bit-identical to the call that writes partials,
+    and within the fp64 bar (32-token tiles at these sizes; test_router_tiles_bit_identical
+    compares the two tile sizes)."""
     x, w_in, w_out = gen(300 + E, (T, d), (128, d), (E, 128))
     xb, wib, wob = bf16(x).to(dev), bf16(w_in * 0.02).to(dev), bf16(w_out * 0.1).to(dev)
     r64 = ops.router(xb, wib, wob, 0, save_hidden=True)
