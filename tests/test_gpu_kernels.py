@@ -234,11 +234,13 @@ def test_dispatch_counted_matches_dispatch(dev, T, k, E, cap, fp8, mat):
 @pytest.mark.parametrize("T,k,E,cap,fp8,mat", [(16384, 2, 16, 0, False, False), (16384, 2, 16, 2560, False, True),
                                                (777, 3, 7, 50, True, True), (70000, 2, 8, 0, False, False),
                                                (65536, 1, 64, 0, False, False), (1, 1, 4, 0, False, False),
-                                               (63, 8, 64, 3, False, True)])
+                                               (63, 8, 64, 3, False, True), (8192, 2, 16, 0, False, False),
+                                               (8193, 2, 16, 1100, True, True)])
 def test_dispatch_counted_aux(dev, T, k, E, cap, fp8, mat):
     """kmoe_dispatch_counted_aux: the tables, rows and codes of kmoe_dispatch_counted and the
     aux losses of kmoe_aux_loss, bit for bit (one more workgroup of the table launch up to
-    65536 tokens, the separate launch beyond: T = 70000); the losses against the oracle."""
+    65536 tokens, the separate launch beyond: T = 70000; router histograms and partials per
+    32 tokens up to 8192 tokens, per 64 from 8193); the losses against the oracle."""
     d = 128
     x, w_in, w_out = gen(500 + T % 89, (T, d), (128, d), (E, 128))
     xb, wib, wob = bf16(x).to(dev), bf16(w_in * 0.05).to(dev), bf16(w_out * 0.05).to(dev)
