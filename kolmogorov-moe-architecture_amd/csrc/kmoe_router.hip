@@ -24,7 +24,7 @@ constexpr int RT_HID = KMOE_ROUTER_HIDDEN;
 constexpr int HSTR = RT_HID + 2;
 constexpr int WOS = RT_HID + 2;
 // One K-step covers RKB bytes of every row (RKB = 128 or 256: 64 or 128 bf16); TOK
-// tokens per workgroup (64, or 32 for the small grids of k = 0 routers, below).
+// tokens per workgroup (64, or 32 on small grids: kmoe::router_block_tokens).
 template <int RKB, int TOK = RT_TOK>
 struct RtGeom {
   static constexpr int XT = TOK * RKB;         // x tile of one K-step (TOK rows)
@@ -194,7 +194,8 @@ __global__ __launch_bounds__(RT_THREADS) void router_kernel(const uint16_t* __re
       acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i & 1], b0[i & 1], acc[0], 0, 0, 0);
       if constexpr (NH == 2) acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i & 1], b1[i & 1], acc[1], 0, 0, 0);
       if constexpr (RMS) {
-        // the two waves of a token half read the same x fragments: one of them sums
+        // the waves of a token half (all four with 32-token tiles) read the same x
+        // fragments: one of them sums
         if (wn == 0) {
 #pragma unroll
           for (int c = 0; c < 8; ++c) {
